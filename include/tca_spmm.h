@@ -1,0 +1,151 @@
+/*
+ * tca_spmm.h -- C ABI of the MI355X (gfx950) TCA-SpMM library, libtcaspmm.so.
+ *
+ * Computes C = A * B where A is an M x K CSR matrix (int32 row offsets and
+ * column indices, zero based, columns ascending within a row), B is a dense
+ * K x N row-major matrix (leading dimension N) and C is a dense M x N
+ * row-major fp32 matrix (leading dimension N).  A and B share one value type
+ * (fp16, bf16 or fp32); products are accumulated in fp32.
+ *
+ * Semantics differ from the reference in one documented way: every row of C
+ * is written (beta = 0), so empty rows of A produce zero rows of C.  The
+ * reference kernel skips empty rows and leaves the caller's C there
+ * (reference src/our_spmm.cu:296-352); its harness zeroes C first
+ * (reference src/test.cu:72), so harness-visible results are identical.
+ *
+ * Every function returns an int status (TCA_OK == 0) and never exits the
+ * process; the reference's CHECK_CUDA printed and called exit()
+ * (reference src/general.cuh:8-16).  tca_last_error() returns a message for
+ * the last failure on the calling thread.
+ */
+#ifndef TCA_SPMM_H
+#define TCA_SPMM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Value types.  TCA_F16 matches the reference's `half` A/B with fp32 C
+ * (reference src/arg_parse.h:39-41, "-d 0"). */
+typedef enum tca_dtype {
+    TCA_F16 = 0,
+    TCA_F32 = 1,
+    TCA_BF16 = 2
+} tca_dtype;
+
+typedef enum tca_status {
+    TCA_OK = 0,
+    TCA_ERR_INVALID = 1,     /* bad argument, shape or CSR structure */
+    TCA_ERR_ALLOC = 2,       /* host or device allocation failed */
+    TCA_ERR_HIP = 3,         /* a HIP runtime call failed */
+    TCA_ERR_UNSUPPORTED = 4, /* valid request this build does not handle */
+    TCA_ERR_IO = 5,          /* file could not be opened or read */
+    TCA_ERR_FORMAT = 6       /* malformed input file */
+} tca_status;
+
+/* Plan flags. */
+#define TCA_PLAN_DEFAULT 0u
+#define TCA_PLAN_NO_MFMA 1u    /* route every row to the wavefront-per-row kernel */
+#define TCA_PLAN_FORCE_MFMA 2u /* route every 16-row window to the MFMA tile kernel (fp16/bf16 only) */
+
+typedef struct tca_spmm_plan tca_spmm_plan;
+
+/* Plan statistics, for the harness's "num_block / blockdim / shm" line
+ * (reference src/our_spmm.cu:552) and for the measurement scripts. */
+typedef struct tca_plan_info {
+    int32_t M, K, N, nnz, dtype;
+    int32_t elems_per_lane;   /* B columns per lane per load (16-byte vectors when possible) */
+    int32_t lanes_per_row;    /* lanes covering one B-row column chunk (power of 2, <= 64) */
+    int32_t col_chunks;       /* column chunks of 64 * elems_per_lane */
+    int32_t n_row_tasks;      /* wavefront tasks of the row kernel */
+    int32_t n_multi_tasks;    /* of which: several short rows per wavefront */
+    int32_t n_seg_tasks;      /* of which: segments of split long rows */
+    int32_t n_long_rows;      /* rows split across wavefronts */
+    int32_t n_windows_mfma;   /* 16-row windows routed to the MFMA tile kernel */
+    int32_t rows_mfma;        /* rows covered by those windows */
+    int64_t nnz_mfma;         /* nonzeros covered by those windows */
+    int64_t cond_cols_mfma;   /* sum over MFMA windows of the padded condensed width */
+    int32_t row_blocks;       /* workgroups of the row kernel */
+    int32_t row_blockdim;     /* threads per workgroup of the row kernel */
+    int32_t mfma_blocks;      /* workgroups of the MFMA kernel */
+    int32_t mfma_blockdim;
+    int32_t mfma_lds_bytes;   /* LDS per MFMA workgroup */
+    int32_t seg_len;          /* nonzeros per long-row segment */
+    int64_t scratch_bytes;    /* device scratch owned by the plan */
+    double plan_ms;           /* host planning time */
+} tca_plan_info;
+
+/* Replaces reference workload_manager (src/our_spmm.cu:353-477) plus the
+ * device uploads of our_spmm_balanced (src/our_spmm.cu:503-525).
+ * rowptr[M+1] and colidx[nnz] are HOST arrays; they are validated (rowptr
+ * monotone from 0 to nnz, 0 <= col < K, columns strictly ascending per row)
+ * and copied to the device.  The plan keeps the structure; values, B and C
+ * are supplied per run.  Requires 1 <= N, M >= 0, K >= 1. */
+int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_t K,
+                         int32_t nnz, int32_t N, int32_t dtype, uint32_t flags,
+                         tca_spmm_plan** plan);
+
+/* Replaces the kernel launch of our_spmm_balanced (src/our_spmm.cu:555,561)
+ * and kernel_our_spmm_balanced (src/our_spmm.cu:296-352).  d_val[nnz],
+ * d_B[K*N] (plan dtype) and d_C[M*N] (fp32) are DEVICE pointers; d_B and d_C
+ * must be aligned to 16 bytes.  Stream-ordered on `stream` (a hipStream_t,
+ * NULL = default stream); does not synchronise.  One plan must not run on two
+ * streams at once: long-row partial sums live in plan-owned scratch. */
+int tca_spmm_run(const tca_spmm_plan* plan, const void* d_val, const void* d_B, float* d_C,
+                 void* stream);
+
+/* Times tca_spmm_run the way our_spmm_balanced does (src/our_spmm.cu:553-576):
+ * `warmup` untimed launches, then `iters` launches between two hipEvents
+ * recorded on `stream`; *avg_ms = elapsed / iters.  Synchronises `stream`. */
+int tca_spmm_time(const tca_spmm_plan* plan, const void* d_val, const void* d_B, float* d_C,
+                  void* stream, int32_t warmup, int32_t iters, float* avg_ms);
+
+int tca_spmm_plan_info(const tca_spmm_plan* plan, tca_plan_info* info);
+
+int tca_spmm_plan_destroy(tca_spmm_plan* plan);
+
+/* Host-pointer driver with the contract of reference our_spmm_balanced
+ * (src/our_spmm.cu:478-594, declared src/our_spmm.cuh:4): allocates device
+ * buffers, copies A, B in, plans, runs 5 warm-ups and n_iter timed launches,
+ * copies C back, frees everything.  *elapsed_ms (if not NULL) receives the
+ * mean ms per launch.  Prints "preprocess %fms taken" and
+ * "num_block: %d blockdim: %d shm: %fKB" like the reference when verbose != 0. */
+int tca_spmm_host(const int32_t* rowptr, const int32_t* colidx, const void* val, int32_t M,
+                  int32_t K, int32_t nnz, const void* B, float* C, int32_t N, int32_t dtype,
+                  int32_t n_iter, int32_t verbose, double* elapsed_ms);
+
+/* ---- condensed row windows (host, exported so tests can pin the indexing) ----
+ * For row window w (rows [w*win, min(M,(w+1)*win))), ucols holds the sorted
+ * union of the window's column indices at [uoff[w], uoff[w+1]), and for each
+ * nonzero j of the window cpos[j] is the position of colidx[j] inside that
+ * union (so ucols[uoff[w] + cpos[j]] == colidx[j]).  Pass ucols == NULL to
+ * get only uoff (sizes).  uoff has n_windows+1 entries. */
+int tca_condense_windows(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_t nnz,
+                         int32_t win, int64_t* uoff, int32_t* ucols, int32_t* cpos);
+
+/* ---- host-only view of the row kernel's task list (no device needed) ----
+ * The wavefront tasks tca_spmm_plan_create builds for this structure, width N
+ * and dtype, with no rows routed to the MFMA kernel.  Call with tasks == NULL
+ * to get the counts, then again with tasks[4*n_tasks], perm[n_perm] and
+ * longrows[4*n_long].  Task int4 {x,y,z,w}: w == 0 row task (x row, [y,z)
+ * nonzeros); w == 1 multi task (x offset into perm, y rows, z longest row);
+ * w & 3 == 2 segment task (x long-row id, [y,z) nonzeros, w >> 2 segment
+ * slot).  longrows entry {row, first segment slot, segments, 0}. */
+int tca_plan_row_tasks(const int32_t* rowptr, int32_t M, int32_t N, int32_t dtype, int32_t* n_tasks,
+                       int32_t* n_perm, int32_t* n_long, int32_t* tasks, int32_t* perm, int32_t* longrows,
+                       int32_t* geometry /* [4]: elems_per_lane, lanes_per_row, col_chunks, seg_len */);
+
+/* ---- library information ---- */
+const char* tca_status_string(int status);
+const char* tca_last_error(void);
+int tca_device_count(int32_t* count);
+int tca_version(void);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* TCA_SPMM_H */

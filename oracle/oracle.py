@@ -1,0 +1,214 @@
+"""CPU oracle for the TCA-SpMM hot path (test infrastructure only).
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
+``bench.py`` may import this module, and only as the checker (or as the timed
+CPU baseline).  The product (``spmm_amd``, the C ABI, the ``./test`` harness)
+never imports or links it.
+
+Each function names the reference lines it restates.  How each is pinned
+(checked against something other than itself):
+
+* ``parse_smtx``       -- the reference fixture's known answers (header, row
+  count, nnz, per-row length buckets) and a second, independent tokeniser.
+* ``dense_to_csr`` / ``csr_to_dense`` -- the fixture round trip
+  (``.smtx -> dense -> CSR`` reproduces the file's arrays), CSR invariants,
+  and the identity ``csr_to_dense(dense_to_csr(D)) == D``.
+* ``condense_windows`` -- reconstruction: scattering every window's
+  condensed tile back through its column union gives the dense window; the
+  union equals the set of nonzero columns; brute force on tiny inputs.
+* ``csr_spmm``         -- exact-arithmetic vectors (bit equality with an fp64
+  closed form), closed forms (identity, permutation, all-ones rows), scipy
+  fixtures and dense brute force.
+* ``compare_mat``      -- hand-built cases for each branch of the verdict.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+_lib = None
+
+
+def build() -> None:
+    """Compile oracle.c into liboracle.so (gcc, see oracle/Makefile)."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+def _load():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        lib = ctypes.CDLL(_LIB_PATH)
+        i32p = ctypes.POINTER(ctypes.c_int32)
+        f32p = ctypes.POINTER(ctypes.c_float)
+        f64p = ctypes.POINTER(ctypes.c_double)
+        lib.oracle_csr_spmm_f32.argtypes = [i32p, i32p, f32p, ctypes.c_int32, ctypes.c_int32,
+                                            f32p, f32p, ctypes.c_int]
+        lib.oracle_csr_spmm_f32.restype = None
+        lib.oracle_csr_spmm_f64.argtypes = [i32p, i32p, f64p, ctypes.c_int32, ctypes.c_int32,
+                                            f64p, f64p, ctypes.c_int]
+        lib.oracle_csr_spmm_f64.restype = None
+        lib.oracle_dense_spmm_f32.argtypes = [f32p, f32p, f32p, ctypes.c_int32, ctypes.c_int32,
+                                              ctypes.c_int32, ctypes.c_int]
+        lib.oracle_dense_spmm_f32.restype = None
+        lib.oracle_compare_mat.argtypes = [f32p, f32p, ctypes.c_int64, ctypes.c_float,
+                                           ctypes.POINTER(ctypes.c_int64),
+                                           ctypes.POINTER(ctypes.c_int64), f32p]
+        lib.oracle_compare_mat.restype = ctypes.c_int
+        _lib = lib
+    return _lib
+
+
+def _ptr(a: np.ndarray, ctype):
+    return a.ctypes.data_as(ctypes.POINTER(ctype))
+
+
+# ---------------------------------------------------------------- .smtx text
+def parse_smtx(text: str):
+    """Restates reference smtx_input_to_Dense's parse (src/file_input.cu:135-193).
+
+    Line 1 is ``rows, cols, nnz`` split on ',' and read with stoi (which skips
+    leading blanks).  Line 2 holds the row offsets split on ' '.  Every
+    remaining line holds column indices split on ' '.  Returns
+    ``(nrow, ncol, nnz, rowptr int32, colidx int32)``.
+    """
+    lines = text.split("\n")
+    head = lines[0].split(",")
+    nrow, ncol, nnz = int(head[0]), int(head[1]), int(head[2])
+    rowptr = [int(t) for t in lines[1].split(" ") if t != ""]
+    cols = []
+    for line in lines[2:]:
+        cols.extend(int(t) for t in line.split(" ") if t != "")
+    return nrow, ncol, nnz, np.asarray(rowptr, np.int32), np.asarray(cols, np.int32)
+
+
+def smtx_to_dense(nrow, ncol, rowptr, colidx, dtype=np.float16):
+    """Dense matrix with 1.0 at every listed entry (src/file_input.cu:182-191)."""
+    d = np.zeros((nrow, ncol), dtype=dtype)
+    for r in range(nrow):
+        for j in range(int(rowptr[r]), int(rowptr[r + 1])):
+            d[r, colidx[j]] = 1.0
+    return d
+
+
+# ------------------------------------------------------------ dense <-> CSR
+def dense_to_csr(dense: np.ndarray):
+    """Restates reference convert_dense_to_csr (src/miscalleneous.cu:29-65).
+
+    Row-major scan keeping entries whose fp32 value compares != 0.0f, so +-0
+    are dropped and columns come out ascending.  Returns
+    ``(rowptr int32[M+1], colidx int32[nnz], values dense.dtype[nnz])``.
+    """
+    m, _ = dense.shape
+    keep = dense.astype(np.float32) != 0.0
+    rows, cols = np.nonzero(keep)  # C order: row-major, columns ascending
+    counts = np.bincount(rows, minlength=m)
+    rowptr = np.zeros(m + 1, np.int32)
+    np.cumsum(counts, out=rowptr[1:])
+    return rowptr, cols.astype(np.int32), dense[rows, cols]
+
+
+def csr_to_dense(rowptr, colidx, values, ncol):
+    """Restates reference convert_csr_to_dense (src/miscalleneous.cu:66-81)."""
+    m = len(rowptr) - 1
+    d = np.zeros((m, ncol), dtype=values.dtype)
+    for r in range(m):
+        s, e = int(rowptr[r]), int(rowptr[r + 1])
+        d[r, colidx[s:e]] = values[s:e]
+    return d
+
+
+# ------------------------------------------------------- condensed windows
+def condense_windows(rowptr, colidx, m: int, win: int):
+    """Condensed-tile indexing of the build (no reference counterpart; the
+    reference kernel gathers B per nonzero, src/our_spmm.cu:44-60).
+
+    For window w (rows [w*win, min(m, (w+1)*win))) the union U_w is the sorted
+    set of its nonzero columns, and each nonzero's condensed position is its
+    index in U_w.  Returns ``(uoff int64[nw+1], ucols int32, cpos int32[nnz])``.
+    """
+    nw = (m + win - 1) // win
+    uoff = np.zeros(nw + 1, np.int64)
+    ucols_parts = []
+    cpos = np.zeros(len(colidx), np.int32)
+    for w in range(nw):
+        s = int(rowptr[w * win])
+        e = int(rowptr[min(m, (w + 1) * win)])
+        seg = np.asarray(colidx[s:e])
+        u = np.unique(seg)
+        ucols_parts.append(u.astype(np.int32))
+        cpos[s:e] = np.searchsorted(u, seg).astype(np.int32)
+        uoff[w + 1] = uoff[w] + len(u)
+    ucols = np.concatenate(ucols_parts) if ucols_parts else np.zeros(0, np.int32)
+    return uoff, ucols, cpos
+
+
+# ------------------------------------------------------------------- SpMM
+def csr_spmm(rowptr, colidx, values, b, threads: int = 0) -> np.ndarray:
+    """fp32 CSR SpMM with reference naive_gemm arithmetic
+    (src/miscalleneous.cu:114-134): per row, k ascending, fp32 multiply then
+    fp32 add.  Inputs of any float dtype are first widened to fp32 exactly."""
+    lib = _load()
+    rowptr = np.ascontiguousarray(rowptr, np.int32)
+    colidx = np.ascontiguousarray(colidx, np.int32)
+    v = np.ascontiguousarray(values, np.float32)
+    bb = np.ascontiguousarray(b, np.float32)
+    m = len(rowptr) - 1
+    n = bb.shape[1]
+    c = np.empty((m, n), np.float32)
+    lib.oracle_csr_spmm_f32(_ptr(rowptr, ctypes.c_int32), _ptr(colidx, ctypes.c_int32),
+                            _ptr(v, ctypes.c_float), m, n, _ptr(bb, ctypes.c_float),
+                            _ptr(c, ctypes.c_float), threads)
+    return c
+
+
+def csr_spmm_f64(rowptr, colidx, values, b, threads: int = 0) -> np.ndarray:
+    """The same product accumulated in fp64 (error measurement only)."""
+    lib = _load()
+    rowptr = np.ascontiguousarray(rowptr, np.int32)
+    colidx = np.ascontiguousarray(colidx, np.int32)
+    v = np.ascontiguousarray(values, np.float64)
+    bb = np.ascontiguousarray(b, np.float64)
+    m = len(rowptr) - 1
+    n = bb.shape[1]
+    c = np.empty((m, n), np.float64)
+    lib.oracle_csr_spmm_f64(_ptr(rowptr, ctypes.c_int32), _ptr(colidx, ctypes.c_int32),
+                            _ptr(v, ctypes.c_double), m, n, _ptr(bb, ctypes.c_double),
+                            _ptr(c, ctypes.c_double), threads)
+    return c
+
+
+def dense_spmm(a, b, threads: int = 0) -> np.ndarray:
+    """Literal reference naive_gemm (src/miscalleneous.cu:114-134) on fp32."""
+    lib = _load()
+    aa = np.ascontiguousarray(a, np.float32)
+    bb = np.ascontiguousarray(b, np.float32)
+    m, k = aa.shape
+    n = bb.shape[1]
+    c = np.empty((m, n), np.float32)
+    lib.oracle_dense_spmm_f32(_ptr(aa, ctypes.c_float), _ptr(bb, ctypes.c_float),
+                              _ptr(c, ctypes.c_float), m, n, k, threads)
+    return c
+
+
+def compare_mat(gold, cmp, tol: float = 1e-3):
+    """Restates reference compare_mat<float> (src/general.cuh:71-123).
+
+    Returns ``(success, fail_count, first_fail, max_rel)``; the scan stops at
+    the 10th failure like the reference."""
+    lib = _load()
+    g = np.ascontiguousarray(gold, np.float32).ravel()
+    c = np.ascontiguousarray(cmp, np.float32).ravel()
+    assert g.size == c.size
+    fc = ctypes.c_int64()
+    ff = ctypes.c_int64()
+    mr = ctypes.c_float()
+    ok = lib.oracle_compare_mat(_ptr(g, ctypes.c_float), _ptr(c, ctypes.c_float), g.size, tol,
+                                ctypes.byref(fc), ctypes.byref(ff), ctypes.byref(mr))
+    return bool(ok), fc.value, ff.value, mr.value

@@ -1,0 +1,316 @@
+"""spmm_amd -- MI355X-native TCA-SpMM (C = A * B, A in CSR, B dense, C fp32).
+
+Python side of the library: numpy-level wrappers of the C ABI in
+``include/tca_spmm.h`` / ``include/tca_host.h`` (readers, generators,
+validation) and :class:`Plan`, which runs the gfx950 kernels on device
+buffers given as raw addresses or torch tensors.
+
+Reference surface mirrored here (YaoLingF/SPMM):
+  * ``CSR`` host struct            -- reference src/general.cuh:125-134
+  * ``.smtx`` reader               -- reference src/file_input.cu:135-193
+  * ``convert_dense_to_csr``       -- reference src/miscalleneous.cu:29-65
+  * ``compare_mat`` verdict        -- reference src/general.cuh:71-123
+  * ``our_spmm_balanced`` driver   -- reference src/our_spmm.cu:478-594
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import _lib
+from ._lib import (TCA_BF16, TCA_F16, TCA_F32, TCA_PLAN_DEFAULT, TCA_PLAN_FORCE_MFMA, TCA_PLAN_NO_MFMA, TcaError,
+                   call, lib, np_ptr)
+
+__all__ = ["CSR", "Plan", "TcaError", "TCA_F16", "TCA_F32", "TCA_BF16", "TCA_PLAN_DEFAULT", "TCA_PLAN_NO_MFMA",
+           "TCA_PLAN_FORCE_MFMA", "read_smtx", "read_smtx_dense", "write_smtx", "read_mtx", "dense_to_csr",
+           "csr_to_dense", "compare_mat", "gen_config", "gen_dense", "gen_bernoulli", "gen_lognormal_rows",
+           "gen_rmat", "gen_zipf_rows", "naive_csr_spmm", "plan_row_tasks", "our_spmm_balanced", "condense_windows", "np_dtype",
+           "to_storage", "from_storage"]
+
+# numpy storage type of each value type (fp16/bf16 are kept as 16-bit patterns)
+_STORAGE = {TCA_F16: np.float16, TCA_F32: np.float32, TCA_BF16: np.uint16}
+
+
+def np_dtype(dtype: int):
+    return _STORAGE[dtype]
+
+
+def to_storage(x: np.ndarray, dtype: int) -> np.ndarray:
+    """fp32 values -> storage array of `dtype` (round to nearest even)."""
+    x = np.ascontiguousarray(x, np.float32)
+    if dtype == TCA_F32:
+        return x.copy()
+    out = np.empty(x.shape, _STORAGE[dtype])
+    lib.tca_convert_array(np_ptr(x), TCA_F32, np_ptr(out), dtype, x.size)
+    return out
+
+
+def from_storage(x: np.ndarray, dtype: int) -> np.ndarray:
+    """storage array of `dtype` -> fp32 values (exact)."""
+    x = np.ascontiguousarray(x)
+    if dtype == TCA_F32:
+        return x.astype(np.float32)
+    out = np.empty(x.shape, np.float32)
+    lib.tca_convert_array(np_ptr(x), dtype, np_ptr(out), TCA_F32, x.size)
+    return out
+
+
+@dataclass
+class CSR:
+    """Host CSR matrix (int32 offsets and indices, values in storage type)."""
+    nrow: int
+    ncol: int
+    rowptr: np.ndarray
+    colidx: np.ndarray
+    values: np.ndarray
+    dtype: int
+
+    @property
+    def nnz(self) -> int:
+        return int(self.rowptr[-1]) if len(self.rowptr) else 0
+
+    def values_f32(self) -> np.ndarray:
+        return from_storage(self.values, self.dtype)
+
+    def as_struct(self) -> _lib.TcaCsr:
+        """A tca_csr view of this matrix (valid while self is alive)."""
+        self.rowptr = np.ascontiguousarray(self.rowptr, np.int32)
+        self.colidx = np.ascontiguousarray(self.colidx, np.int32)
+        self.values = np.ascontiguousarray(self.values, _STORAGE[self.dtype])
+        return _lib.TcaCsr(self.nrow, self.ncol, self.nnz, np_ptr(self.rowptr, ctypes.c_int32),
+                           np_ptr(self.colidx, ctypes.c_int32), self.values.ctypes.data, self.dtype)
+
+    @staticmethod
+    def from_struct(s: _lib.TcaCsr, free: bool = True) -> "CSR":
+        """Copies a library-allocated tca_csr into numpy arrays (and frees it)."""
+        m, nnz = s.nRow, s.nnz
+        rowptr = np.ctypeslib.as_array(s.row_offset, shape=(m + 1,)).copy()
+        colidx = np.ctypeslib.as_array(s.col_idx, shape=(nnz,)).copy() if nnz else np.zeros(0, np.int32)
+        st = _STORAGE[s.dtype]
+        if nnz:
+            buf = (ctypes.c_char * (nnz * np.dtype(st).itemsize)).from_address(s.value)
+            values = np.frombuffer(buf, dtype=st).copy()
+        else:
+            values = np.zeros(0, st)
+        out = CSR(s.nRow, s.nCol, rowptr, colidx, values, s.dtype)
+        if free:
+            lib.tca_csr_free(ctypes.byref(s))
+        return out
+
+    def astype(self, dtype: int) -> "CSR":
+        if dtype == self.dtype:
+            return self
+        return CSR(self.nrow, self.ncol, self.rowptr, self.colidx, to_storage(self.values_f32(), dtype), dtype)
+
+    def validate(self) -> None:
+        call("tca_csr_validate", np_ptr(np.ascontiguousarray(self.rowptr, np.int32), ctypes.c_int32),
+             np_ptr(np.ascontiguousarray(self.colidx, np.int32), ctypes.c_int32), self.nrow, self.ncol, self.nnz)
+
+
+# ------------------------------------------------------------------ I/O
+def read_smtx(path: str, dtype: int = TCA_F16) -> CSR:
+    s = _lib.TcaCsr()
+    call("tca_smtx_read_csr", path.encode(), dtype, ctypes.byref(s))
+    return CSR.from_struct(s)
+
+
+def read_smtx_dense(path: str, dtype: int = TCA_F16) -> np.ndarray:
+    p = ctypes.c_void_p()
+    m, k, nnz = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
+    call("tca_smtx_read_dense", path.encode(), dtype, ctypes.byref(p), ctypes.byref(m), ctypes.byref(k),
+         ctypes.byref(nnz))
+    st = _STORAGE[dtype]
+    n = m.value * k.value
+    buf = (ctypes.c_char * max(n * np.dtype(st).itemsize, 1)).from_address(p.value)
+    out = np.frombuffer(buf, dtype=st, count=n).copy().reshape(m.value, k.value)
+    lib.tca_free(p)
+    return out
+
+
+def write_smtx(path: str, a: CSR) -> None:
+    s = a.as_struct()
+    call("tca_smtx_write", path.encode(), ctypes.byref(s))
+
+
+def read_mtx(path: str, pattern_only: bool = False, zero_based: bool = False, dtype: int = TCA_F16) -> CSR:
+    s = _lib.TcaCsr()
+    call("tca_mtx_read_csr", path.encode(), int(pattern_only), int(zero_based), dtype, ctypes.byref(s))
+    return CSR.from_struct(s)
+
+
+def dense_to_csr(dense: np.ndarray, dtype: int) -> CSR:
+    d = np.ascontiguousarray(dense, _STORAGE[dtype])
+    s = _lib.TcaCsr()
+    call("tca_dense_to_csr", np_ptr(d), d.shape[0], d.shape[1], dtype, ctypes.byref(s))
+    return CSR.from_struct(s)
+
+
+def csr_to_dense(a: CSR) -> np.ndarray:
+    out = np.empty((a.nrow, a.ncol), _STORAGE[a.dtype])
+    s = a.as_struct()
+    call("tca_csr_to_dense", ctypes.byref(s), np_ptr(out))
+    return out
+
+
+def compare_mat(gold: np.ndarray, cmp: np.ndarray, tol: float = 1e-3, floor: float = 1e-6,
+                verbose: bool = False) -> dict:
+    g = np.ascontiguousarray(gold, np.float32).ravel()
+    c = np.ascontiguousarray(cmp, np.float32).ravel()
+    if g.size != c.size:
+        raise ValueError("size mismatch")
+    r = _lib.TcaCompareResult()
+    call("tca_compare_mat", np_ptr(g, ctypes.c_float), np_ptr(c, ctypes.c_float), g.size, tol, floor, int(verbose),
+         ctypes.byref(r))
+    return {"success": bool(r.success), "fail_count": r.fail_count, "first_fail": r.first_fail,
+            "max_rel": r.max_rel, "max_rel_floor": r.max_rel_floor}
+
+
+def naive_csr_spmm(a: CSR, b: np.ndarray, threads: int = 0) -> np.ndarray:
+    bb = np.ascontiguousarray(b, _STORAGE[a.dtype])
+    n = bb.shape[1]
+    c = np.empty((a.nrow, n), np.float32)
+    s = a.as_struct()
+    call("tca_naive_csr_spmm", ctypes.byref(s), np_ptr(bb), np_ptr(c, ctypes.c_float), n, threads)
+    return c
+
+
+def condense_windows(a: CSR, win: int = 16):
+    nw = (a.nrow + win - 1) // win
+    rp = np.ascontiguousarray(a.rowptr, np.int32)
+    ci = np.ascontiguousarray(a.colidx, np.int32)
+    uoff = np.zeros(nw + 1, np.int64)
+    call("tca_condense_windows", np_ptr(rp, ctypes.c_int32), np_ptr(ci, ctypes.c_int32), a.nrow, a.nnz, win,
+         np_ptr(uoff, ctypes.c_int64), None, None)
+    ucols = np.zeros(int(uoff[-1]), np.int32)
+    cpos = np.zeros(a.nnz, np.int32)
+    call("tca_condense_windows", np_ptr(rp, ctypes.c_int32), np_ptr(ci, ctypes.c_int32), a.nrow, a.nnz, win,
+         np_ptr(uoff, ctypes.c_int64), np_ptr(ucols, ctypes.c_int32), np_ptr(cpos, ctypes.c_int32))
+    return uoff, ucols, cpos
+
+
+def plan_row_tasks(a: CSR, n: int, dtype: int = None):
+    """Host-only task list of the row kernel: (tasks int32[T,4], perm, longrows int32[L,4], geometry)."""
+    dtype = a.dtype if dtype is None else dtype
+    rp = np.ascontiguousarray(a.rowptr, np.int32)
+    nt, npm, nl = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
+    geo = np.zeros(4, np.int32)
+    call("tca_plan_row_tasks", np_ptr(rp, ctypes.c_int32), a.nrow, n, dtype, ctypes.byref(nt), ctypes.byref(npm),
+         ctypes.byref(nl), None, None, None, np_ptr(geo, ctypes.c_int32))
+    tasks = np.zeros((nt.value, 4), np.int32)
+    perm = np.zeros(max(npm.value, 1), np.int32)
+    longrows = np.zeros((max(nl.value, 1), 4), np.int32)
+    call("tca_plan_row_tasks", np_ptr(rp, ctypes.c_int32), a.nrow, n, dtype, ctypes.byref(nt), ctypes.byref(npm),
+         ctypes.byref(nl), np_ptr(tasks, ctypes.c_int32), np_ptr(perm, ctypes.c_int32),
+         np_ptr(longrows, ctypes.c_int32), np_ptr(geo, ctypes.c_int32))
+    return tasks, perm[:npm.value], longrows[:nl.value], {"elems_per_lane": int(geo[0]), "lanes_per_row": int(geo[1]),
+                                                          "col_chunks": int(geo[2]), "seg_len": int(geo[3])}
+
+
+# ----------------------------------------------------------- generators
+def gen_dense(rows: int, cols: int, dist: int = 0, seed: int = 1, dtype: int = TCA_F16,
+              sparsity: float = 0.0) -> np.ndarray:
+    """dist 0 = U(-1,1), 1 = N(0,1), 2 = U(0,1), 3 = seeded prepare_cpu_matrix."""
+    out = np.empty((rows, cols), _STORAGE[dtype])
+    call("tca_gen_dense", rows, cols, dist, sparsity, seed, dtype, np_ptr(out))
+    return out
+
+
+def _gen(name, *args):
+    s = _lib.TcaCsr()
+    st = _lib.TcaGenStats()
+    call(name, *args, ctypes.byref(s), ctypes.byref(st))
+    return CSR.from_struct(s), st.as_dict()
+
+
+def gen_bernoulli(m, k, p, sigma=0.02, seed=1, dtype=TCA_F16):
+    return _gen("tca_gen_bernoulli", m, k, p, sigma, seed, dtype)
+
+
+def gen_lognormal_rows(m, k, mean, s=1.0, sigma=0.02, seed=1, dtype=TCA_F16):
+    return _gen("tca_gen_lognormal_rows", m, k, mean, s, sigma, seed, dtype)
+
+
+def gen_rmat(scale, n, samples, a=0.57, b=0.19, c=0.19, symmetric=True, norm=0, seed=1, dtype=TCA_F32):
+    return _gen("tca_gen_rmat", scale, n, samples, a, b, c, int(symmetric), norm, seed, dtype)
+
+
+def gen_zipf_rows(m, k, total, s=1.5, cap=200000, seed=1, dtype=TCA_F16):
+    return _gen("tca_gen_zipf_rows", m, k, total, s, cap, seed, dtype)
+
+
+def gen_config(cfg: int, seed: int = 1, dtype: int = -1):
+    """One of the five BASELINE configurations; returns (A, N, stats)."""
+    s = _lib.TcaCsr()
+    st = _lib.TcaGenStats()
+    n = ctypes.c_int32()
+    call("tca_gen_config", cfg, seed, dtype, ctypes.byref(s), ctypes.byref(n), ctypes.byref(st))
+    return CSR.from_struct(s), n.value, st.as_dict()
+
+
+# ------------------------------------------------------------------ plans
+def _addr(x) -> int:
+    """Device address of a torch tensor or an int."""
+    if isinstance(x, int):
+        return x
+    return int(x.data_ptr())
+
+
+class Plan:
+    """A planned SpMM for one sparsity structure and width N (tca_spmm_plan)."""
+
+    def __init__(self, a: CSR, n: int, flags: int = TCA_PLAN_DEFAULT):
+        self._p = ctypes.c_void_p()
+        rp = np.ascontiguousarray(a.rowptr, np.int32)
+        ci = np.ascontiguousarray(a.colidx, np.int32)
+        call("tca_spmm_plan_create", np_ptr(rp, ctypes.c_int32), np_ptr(ci, ctypes.c_int32), a.nrow, a.ncol, a.nnz,
+             n, a.dtype, flags, ctypes.byref(self._p))
+        self.m, self.k, self.n, self.nnz, self.dtype = a.nrow, a.ncol, n, a.nnz, a.dtype
+
+    def info(self) -> dict:
+        i = _lib.TcaPlanInfo()
+        call("tca_spmm_plan_info", self._p, ctypes.byref(i))
+        return i.as_dict()
+
+    def run(self, val, b, c, stream=None) -> None:
+        """C = A * B on device; val/b/c are torch tensors or device addresses."""
+        call("tca_spmm_run", self._p, _addr(val), _addr(b), _addr(c), _addr(stream) if stream is not None else None)
+
+    def time(self, val, b, c, stream=None, warmup: int = 5, iters: int = 10) -> float:
+        ms = ctypes.c_float()
+        call("tca_spmm_time", self._p, _addr(val), _addr(b), _addr(c),
+             _addr(stream) if stream is not None else None, warmup, iters, ctypes.byref(ms))
+        return ms.value
+
+    def close(self) -> None:
+        if self._p:
+            lib.tca_spmm_plan_destroy(self._p)
+            self._p = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+
+def our_spmm_balanced(a: CSR, b: np.ndarray, n_iter: int = 10, verbose: bool = False):
+    """Host-pointer driver (reference our_spmm_balanced, src/our_spmm.cu:478-594).
+    Returns (C, mean ms per launch)."""
+    bb = np.ascontiguousarray(b, _STORAGE[a.dtype])
+    n = bb.shape[1]
+    c = np.empty((a.nrow, n), np.float32)
+    ms = ctypes.c_double()
+    rp = np.ascontiguousarray(a.rowptr, np.int32)
+    ci = np.ascontiguousarray(a.colidx, np.int32)
+    vals = np.ascontiguousarray(a.values)
+    call("tca_spmm_host", np_ptr(rp, ctypes.c_int32), np_ptr(ci, ctypes.c_int32), np_ptr(vals), a.nrow, a.ncol,
+         a.nnz, np_ptr(bb), np_ptr(c, ctypes.c_float), n, a.dtype, n_iter, int(verbose), ctypes.byref(ms))
+    return c, ms.value

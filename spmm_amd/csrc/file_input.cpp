@@ -1,0 +1,301 @@
+// file_input.cpp -- .smtx and MatrixMarket readers, .smtx writer.
+//
+// The reference parses .smtx with getline + stringstream into a dense M x K
+// half matrix (src/file_input.cu:135-193), which needs 108 GB for the GCN
+// configuration.  This reader streams the file through a fixed buffer and
+// builds the CSR directly; its output equals the reference's
+// .smtx -> dense -> convert_dense_to_csr pipeline (columns ascending and
+// unique per row, value 1.0), and it rejects input the reference would
+// mis-read silently (token counts, offsets, column range).
+#include <algorithm>
+#include <cstdlib>
+#include <vector>
+
+#include "common.hpp"
+
+using namespace tca;
+
+namespace {
+
+class Reader {
+  public:
+    explicit Reader(FILE* f) : f_(f), buf_(1 << 22) {}
+    // Next byte or -1 at end of file.
+    int get() {
+        if (pos_ == len_) {
+            len_ = std::fread(buf_.data(), 1, buf_.size(), f_);
+            pos_ = 0;
+            if (len_ == 0) return -1;
+        }
+        return static_cast<unsigned char>(buf_[pos_++]);
+    }
+    int peek() {
+        const int c = get();
+        if (c >= 0) pos_--;
+        return c;
+    }
+    // Reads an optionally signed decimal integer, skipping the separators in
+    // `seps`.  Stops at '\n' (returned in *stop) or EOF.  Returns true when a
+    // number was read.
+    bool next_int(const char* seps, int64_t* v, int* stop) {
+        int c;
+        for (;;) {
+            c = get();
+            if (c < 0 || c == '\n') { *stop = c; return false; }
+            if (c == '\r' || std::strchr(seps, c)) continue;
+            break;
+        }
+        bool neg = false;
+        if (c == '-' || c == '+') { neg = c == '-'; c = get(); }
+        if (c < '0' || c > '9') { *stop = -2; return false; }  // not a number
+        int64_t x = 0;
+        while (c >= '0' && c <= '9') {
+            x = x * 10 + (c - '0');
+            if (x > (int64_t(1) << 40)) { *stop = -2; return false; }
+            c = get();
+        }
+        if (c >= 0) pos_--;  // leave the terminator for the next call
+        *v = neg ? -x : x;
+        *stop = 0;
+        return true;
+    }
+    // Skips to just after the next '\n'.
+    void skip_line() {
+        int c;
+        while ((c = get()) >= 0 && c != '\n') {}
+    }
+
+  private:
+    FILE* f_;
+    std::vector<char> buf_;
+    size_t pos_ = 0, len_ = 0;
+};
+
+struct SmtxRaw {
+    int32_t nrow = 0, ncol = 0, nnz = 0;
+    std::vector<int32_t> rowptr, colidx;
+};
+
+// Parses the three parts of a .smtx file (reference src/file_input.cu:141-180)
+// and checks counts and ranges; column order inside a row is left as read.
+int parse_smtx(const char* path, SmtxRaw* raw) {
+    FILE* f = std::fopen(path, "rb");
+    if (!f) return fail(TCA_ERR_IO, "cannot open '%s'", path);
+    Reader rd(f);
+    int64_t h[3];
+    int stop = 0;
+    for (int i = 0; i < 3; i++) {
+        if (!rd.next_int(" \t,", &h[i], &stop)) {
+            std::fclose(f);
+            return fail(TCA_ERR_FORMAT, "%s: header must be 'rows, cols, nnz'", path);
+        }
+    }
+    int64_t extra;
+    if (rd.next_int(" \t,", &extra, &stop)) {
+        std::fclose(f);
+        return fail(TCA_ERR_FORMAT, "%s: header has more than 3 numbers", path);
+    }
+    if (stop == -2) { std::fclose(f); return fail(TCA_ERR_FORMAT, "%s: bad header token", path); }
+    if (h[0] < 0 || h[1] < 0 || h[2] < 0 || h[0] > INT32_MAX - 1 || h[1] > INT32_MAX || h[2] > INT32_MAX) {
+        std::fclose(f);
+        return fail(TCA_ERR_FORMAT, "%s: header values out of range", path);
+    }
+    raw->nrow = static_cast<int32_t>(h[0]);
+    raw->ncol = static_cast<int32_t>(h[1]);
+    raw->nnz = static_cast<int32_t>(h[2]);
+    // Line 2: nrow + 1 row offsets.
+    raw->rowptr.resize(static_cast<size_t>(raw->nrow) + 1);
+    int64_t v;
+    size_t n = 0;
+    while (rd.next_int(" \t", &v, &stop)) {
+        if (n > static_cast<size_t>(raw->nrow)) {
+            std::fclose(f);
+            return fail(TCA_ERR_FORMAT, "%s: more than rows+1 = %d row offsets", path, raw->nrow + 1);
+        }
+        raw->rowptr[n++] = static_cast<int32_t>(v);
+    }
+    if (stop == -2 || n != static_cast<size_t>(raw->nrow) + 1) {
+        std::fclose(f);
+        return fail(TCA_ERR_FORMAT, "%s: expected %d row offsets on line 2, read %zu", path, raw->nrow + 1, n);
+    }
+    if (raw->rowptr[0] != 0 || raw->rowptr[raw->nrow] != raw->nnz) {
+        std::fclose(f);
+        return fail(TCA_ERR_FORMAT, "%s: row offsets must run from 0 to nnz = %d", path, raw->nnz);
+    }
+    for (int32_t r = 0; r < raw->nrow; r++)
+        if (raw->rowptr[r + 1] < raw->rowptr[r]) {
+            std::fclose(f);
+            return fail(TCA_ERR_FORMAT, "%s: row offsets decrease at row %d", path, r);
+        }
+    // Remaining lines: nnz column indices.
+    raw->colidx.resize(std::max<int32_t>(raw->nnz, 0));
+    n = 0;
+    for (;;) {
+        if (rd.next_int(" \t", &v, &stop)) {
+            if (n >= static_cast<size_t>(raw->nnz)) {
+                std::fclose(f);
+                return fail(TCA_ERR_FORMAT, "%s: more than nnz = %d column indices", path, raw->nnz);
+            }
+            if (v < 0 || v >= raw->ncol) {
+                std::fclose(f);
+                return fail(TCA_ERR_FORMAT, "%s: column index %lld out of [0, %d)", path, (long long)v, raw->ncol);
+            }
+            raw->colidx[n++] = static_cast<int32_t>(v);
+            continue;
+        }
+        if (stop == -2) { std::fclose(f); return fail(TCA_ERR_FORMAT, "%s: bad column token", path); }
+        if (stop < 0) break;  // EOF
+    }
+    std::fclose(f);
+    if (n != static_cast<size_t>(raw->nnz))
+        return fail(TCA_ERR_FORMAT, "%s: expected %d column indices, read %zu", path, raw->nnz, n);
+    return TCA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int tca_smtx_read_csr(const char* path, int32_t dtype, tca_csr* out) {
+    if (!path || !out || !dtype_ok(dtype)) return fail(TCA_ERR_INVALID, "tca_smtx_read_csr: bad argument");
+    SmtxRaw raw;
+    int st = parse_smtx(path, &raw);
+    if (st) return st;
+    // Sort and de-duplicate each row, as .smtx -> dense -> CSR would
+    // (reference src/file_input.cu:182-191 then src/miscalleneous.cu:29-65).
+    std::vector<int32_t> rp(static_cast<size_t>(raw.nrow) + 1, 0);
+    int32_t w = 0;
+    for (int32_t r = 0; r < raw.nrow; r++) {
+        int32_t* b = raw.colidx.data() + raw.rowptr[r];
+        int32_t* e = raw.colidx.data() + raw.rowptr[r + 1];
+        if (!std::is_sorted(b, e)) std::sort(b, e);
+        for (int32_t* p = b; p < e; p++)
+            if (p == b || *p != p[-1]) raw.colidx[w++] = *p;
+        rp[r + 1] = w;
+    }
+    out->nRow = raw.nrow;
+    out->nCol = raw.ncol;
+    out->nnz = w;
+    out->dtype = dtype;
+    out->row_offset = static_cast<int32_t*>(std::malloc(sizeof(int32_t) * rp.size()));
+    out->col_idx = static_cast<int32_t*>(std::malloc(sizeof(int32_t) * std::max(w, 1)));
+    out->value = std::malloc(dtype_size(dtype) * std::max(w, 1));
+    if (!out->row_offset || !out->col_idx || !out->value) {
+        tca_csr_free(out);
+        return fail(TCA_ERR_ALLOC, "tca_smtx_read_csr: allocation failed");
+    }
+    std::memcpy(out->row_offset, rp.data(), sizeof(int32_t) * rp.size());
+    std::memcpy(out->col_idx, raw.colidx.data(), sizeof(int32_t) * w);
+    for (int32_t j = 0; j < w; j++) store_from_f32(out->value, dtype, j, 1.0f);
+    return TCA_OK;
+}
+
+int tca_smtx_read_dense(const char* path, int32_t dtype, void** dense, int32_t* nRow, int32_t* nCol,
+                        int32_t* nnz) {
+    if (!path || !dense || !nRow || !nCol || !nnz || !dtype_ok(dtype))
+        return fail(TCA_ERR_INVALID, "tca_smtx_read_dense: bad argument");
+    SmtxRaw raw;
+    int st = parse_smtx(path, &raw);
+    if (st) return st;
+    const size_t es = dtype_size(dtype);
+    const size_t total = static_cast<size_t>(raw.nrow) * raw.ncol;
+    void* d = std::calloc(std::max<size_t>(total, 1), es);
+    if (!d) return fail(TCA_ERR_ALLOC, "tca_smtx_read_dense: %zu elements", total);
+    // 1.0 at every listed (row, col) (reference src/file_input.cu:182-191).
+    for (int32_t r = 0; r < raw.nrow; r++)
+        for (int32_t j = raw.rowptr[r]; j < raw.rowptr[r + 1]; j++)
+            store_from_f32(d, dtype, static_cast<int64_t>(r) * raw.ncol + raw.colidx[j], 1.0f);
+    *dense = d;
+    *nRow = raw.nrow;
+    *nCol = raw.ncol;
+    *nnz = raw.nnz;
+    return TCA_OK;
+}
+
+int tca_smtx_write(const char* path, const tca_csr* a) {
+    if (!path || !a) return fail(TCA_ERR_INVALID, "tca_smtx_write: bad argument");
+    FILE* f = std::fopen(path, "wb");
+    if (!f) return fail(TCA_ERR_IO, "cannot create '%s'", path);
+    std::vector<char> buf(1 << 22);
+    std::setvbuf(f, buf.data(), _IOFBF, buf.size());
+    std::fprintf(f, "%d, %d, %d\n", a->nRow, a->nCol, a->nnz);
+    char tmp[16];
+    for (int32_t r = 0; r <= a->nRow; r++) {
+        const int k = std::snprintf(tmp, sizeof tmp, "%d ", a->row_offset[r]);
+        std::fwrite(tmp, 1, k, f);
+    }
+    std::fputc('\n', f);
+    for (int32_t j = 0; j < a->nnz; j++) {
+        const int k = std::snprintf(tmp, sizeof tmp, "%d ", a->col_idx[j]);
+        std::fwrite(tmp, 1, k, f);
+    }
+    std::fputc('\n', f);
+    const bool ok = std::ferror(f) == 0;
+    if (std::fclose(f) != 0 || !ok) return fail(TCA_ERR_IO, "write to '%s' failed", path);
+    return TCA_OK;
+}
+
+int tca_mtx_read_csr(const char* path, int32_t pattern_only, int32_t zero_based, int32_t dtype, tca_csr* out) {
+    if (!path || !out || !dtype_ok(dtype)) return fail(TCA_ERR_INVALID, "tca_mtx_read_csr: bad argument");
+    FILE* f = std::fopen(path, "rb");
+    if (!f) return fail(TCA_ERR_IO, "cannot open '%s'", path);
+    // Skip '%' comment lines, then "rows cols nnz" (reference src/file_input.cu:64-76).
+    std::vector<char> line(1 << 16);
+    int64_t rows = -1, cols = -1, meta = -1;
+    while (std::fgets(line.data(), static_cast<int>(line.size()), f)) {
+        if (line[0] == '%') continue;
+        long long a, b, c;
+        if (std::sscanf(line.data(), "%lld %lld %lld", &a, &b, &c) != 3) {
+            std::fclose(f);
+            return fail(TCA_ERR_FORMAT, "%s: bad size line", path);
+        }
+        rows = a; cols = b; meta = c;
+        break;
+    }
+    if (rows < 0 || cols < 0 || meta < 0 || rows > INT32_MAX - 1 || cols > INT32_MAX || meta > INT32_MAX) {
+        std::fclose(f);
+        return fail(TCA_ERR_FORMAT, "%s: missing or out-of-range size line", path);
+    }
+    tca_coo coo{};
+    coo.nRow = static_cast<int32_t>(rows);
+    coo.nCol = static_cast<int32_t>(cols);
+    coo.dtype = dtype;
+    std::vector<int32_t> ri, ci;
+    std::vector<float> vv;
+    ri.reserve(meta);
+    ci.reserve(meta);
+    vv.reserve(meta);
+    while (std::fgets(line.data(), static_cast<int>(line.size()), f)) {
+        if (line[0] == '%' || line[0] == '\n' || line[0] == '\r') continue;
+        long long r, c;
+        double v = pattern_only ? 1.0 : 0.0;  // reference: v = 0 when a value is missing
+        const int got = std::sscanf(line.data(), "%lld %lld %lf", &r, &c, &v);
+        if (got < 2) { std::fclose(f); return fail(TCA_ERR_FORMAT, "%s: bad entry line", path); }
+        if (pattern_only) v = 1.0;
+        if (!zero_based) { r--; c--; }
+        if (r < 0 || r >= rows || c < 0 || c >= cols) {
+            std::fclose(f);
+            return fail(TCA_ERR_FORMAT, "%s: entry (%lld, %lld) out of range", path, r, c);
+        }
+        ri.push_back(static_cast<int32_t>(r));
+        ci.push_back(static_cast<int32_t>(c));
+        vv.push_back(static_cast<float>(v));
+    }
+    std::fclose(f);
+    if (static_cast<int64_t>(ri.size()) != meta)  // reference asserts the count (src/file_input.cu:114)
+        return fail(TCA_ERR_FORMAT, "%s: header says %lld entries, read %zu", path, (long long)meta, ri.size());
+    coo.nnz = static_cast<int32_t>(ri.size());
+    coo.row_idx = ri.data();
+    coo.col_idx = ci.data();
+    std::vector<uint16_t> v16;
+    if (dtype == TCA_F32) {
+        coo.value = vv.data();
+    } else {
+        v16.resize(vv.size());
+        tca_convert_array(vv.data(), TCA_F32, v16.data(), dtype, static_cast<int64_t>(vv.size()));
+        coo.value = v16.data();
+    }
+    return tca_coo_to_csr(&coo, out);
+}
+
+}  // extern "C"

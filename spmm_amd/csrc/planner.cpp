@@ -1,0 +1,168 @@
+// planner.cpp -- host planning of the row kernel's wavefront task list and
+// the condensed-window indexing.
+#include "planner.hpp"
+
+#include <algorithm>
+#include <numeric>
+
+#include <omp.h>
+
+#include "common.hpp"
+
+namespace tca {
+
+namespace {
+constexpr int kUnroll = 8;  // loads in flight per lane in the row kernel
+
+int32_t next_pow2(int64_t x) {
+    int32_t p = 1;
+    while (p < x) p <<= 1;
+    return p;
+}
+int32_t ilog2(int32_t x) {
+    int32_t l = 0;
+    while ((1 << l) < x) l++;
+    return l;
+}
+}  // namespace
+
+void plan_geometry(int32_t N, int32_t es, RowPlan* p) {
+    int32_t e = 16 / es;
+    while (e > 1 && N % e != 0) e >>= 1;
+    p->elems_per_lane = e;
+    const int64_t lanes = (static_cast<int64_t>(N) + e - 1) / e;
+    if (lanes >= 64) {
+        p->log_lanes = 6;
+        p->col_chunks = static_cast<int32_t>((lanes + 63) / 64);
+    } else {
+        p->log_lanes = ilog2(next_pow2(lanes));
+        p->col_chunks = 1;
+    }
+}
+
+void plan_rows(const int32_t* rowptr, int32_t M, int32_t N, int32_t es, const std::vector<uint8_t>& skip,
+               RowPlan* p) {
+    plan_geometry(N, es, p);
+    const int32_t slots = 64 >> p->log_lanes;
+    const int64_t nnz = rowptr[M];
+    // Segment length: about 1/16384 of the nonzeros (16384 ~ two resident
+    // wavefronts per SIMD on 256 CUs x 4 SIMDs x 8 waves), a power of two
+    // in [512, 8192], and never fewer than 8 loads per slot.
+    p->seg_len = std::min<int64_t>(8192, std::max<int64_t>(512, next_pow2(std::max<int64_t>(nnz / 16384, 1))));
+    p->seg_len = std::max(p->seg_len, slots * kUnroll);
+    // Short rows share a wavefront, one slot each, when slots > 1.
+    p->multi_max = slots > 1 ? 2 * slots : -1;
+
+    std::vector<int32_t> rows;
+    rows.reserve(M);
+    for (int32_t r = 0; r < M; r++)
+        if (skip.empty() || !skip[r]) rows.push_back(r);
+    auto len = [&](int32_t r) { return rowptr[r + 1] - rowptr[r]; };
+    // Longest first; row id breaks ties so the plan is deterministic.
+    std::stable_sort(rows.begin(), rows.end(), [&](int32_t a, int32_t b) { return len(a) > len(b); });
+
+    p->tasks.clear();
+    p->perm.clear();
+    p->longrows.clear();
+    int32_t seg_global = 0;
+    size_t i = 0;
+    // Long rows: equal segments of at most seg_len nonzeros.
+    for (; i < rows.size() && len(rows[i]) > p->seg_len; i++) {
+        const int32_t r = rows[i];
+        const int32_t L = len(r);
+        const int32_t nseg = (L + p->seg_len - 1) / p->seg_len;
+        const int32_t lid = static_cast<int32_t>(p->longrows.size());
+        p->longrows.push_back({r, seg_global, nseg, 0});
+        for (int32_t s = 0; s < nseg; s++) {
+            const int32_t b = rowptr[r] + static_cast<int32_t>(static_cast<int64_t>(L) * s / nseg);
+            const int32_t e = rowptr[r] + static_cast<int32_t>(static_cast<int64_t>(L) * (s + 1) / nseg);
+            p->tasks.push_back({lid, b, e, kTaskSeg | ((seg_global + s) << 2)});
+        }
+        seg_global += nseg;
+    }
+    p->n_seg = static_cast<int32_t>(p->tasks.size());
+    // Medium rows: one wavefront each.
+    for (; i < rows.size() && len(rows[i]) > p->multi_max; i++) {
+        const int32_t r = rows[i];
+        p->tasks.push_back({r, rowptr[r], rowptr[r + 1], kTaskRow});
+    }
+    p->n_rowtasks = static_cast<int32_t>(p->tasks.size()) - p->n_seg;
+    // Short rows: groups of `slots` rows of similar length.
+    const size_t first_multi = p->tasks.size();
+    for (; i < rows.size(); i += slots) {
+        const int32_t cnt = static_cast<int32_t>(std::min<size_t>(slots, rows.size() - i));
+        p->tasks.push_back({static_cast<int32_t>(p->perm.size()), cnt, len(rows[i]), kTaskMulti});
+        for (int32_t k = 0; k < cnt; k++) p->perm.push_back(rows[i + k]);
+    }
+    p->n_multi = static_cast<int32_t>(p->tasks.size() - first_multi);
+}
+
+void condense(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_t win, std::vector<int64_t>* uoff,
+              std::vector<int32_t>* ucols, std::vector<int32_t>* cpos) {
+    const int32_t nw = (M + win - 1) / win;
+    uoff->assign(static_cast<size_t>(nw) + 1, 0);
+    std::vector<std::vector<int32_t>> u(nw);
+#pragma omp parallel for schedule(dynamic, 16)
+    for (int32_t w = 0; w < nw; w++) {
+        const int32_t s = rowptr[static_cast<int64_t>(w) * win];
+        const int32_t e = rowptr[std::min<int64_t>(M, static_cast<int64_t>(w + 1) * win)];
+        std::vector<int32_t>& uw = u[w];
+        uw.assign(colidx + s, colidx + e);
+        std::sort(uw.begin(), uw.end());
+        uw.erase(std::unique(uw.begin(), uw.end()), uw.end());
+        if (cpos)
+            for (int32_t j = s; j < e; j++)
+                (*cpos)[j] = static_cast<int32_t>(std::lower_bound(uw.begin(), uw.end(), colidx[j]) - uw.begin());
+    }
+    for (int32_t w = 0; w < nw; w++) (*uoff)[w + 1] = (*uoff)[w] + static_cast<int64_t>(u[w].size());
+    if (ucols) {
+        ucols->resize((*uoff)[nw]);
+        for (int32_t w = 0; w < nw; w++) std::copy(u[w].begin(), u[w].end(), ucols->begin() + (*uoff)[w]);
+    }
+}
+
+}  // namespace tca
+
+extern "C" int tca_condense_windows(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_t nnz,
+                                    int32_t win, int64_t* uoff, int32_t* ucols, int32_t* cpos) {
+    using namespace tca;
+    if (!rowptr || (nnz > 0 && !colidx) || M < 0 || win < 1 || !uoff)
+        return fail(TCA_ERR_INVALID, "tca_condense_windows: bad argument");
+    if (rowptr[M] != nnz) return fail(TCA_ERR_INVALID, "tca_condense_windows: rowptr[M] != nnz");
+    std::vector<int64_t> off;
+    std::vector<int32_t> uc, cp;
+    if (cpos) cp.resize(nnz);
+    condense(rowptr, colidx, M, win, &off, ucols ? &uc : nullptr, cpos ? &cp : nullptr);
+    std::copy(off.begin(), off.end(), uoff);
+    if (ucols) std::copy(uc.begin(), uc.end(), ucols);
+    if (cpos) std::copy(cp.begin(), cp.end(), cpos);
+    return TCA_OK;
+}
+
+extern "C" int tca_plan_row_tasks(const int32_t* rowptr, int32_t M, int32_t N, int32_t dtype, int32_t* n_tasks,
+                                  int32_t* n_perm, int32_t* n_long, int32_t* tasks, int32_t* perm, int32_t* longrows,
+                                  int32_t* geometry) {
+    using namespace tca;
+    if (!rowptr || M < 0 || N < 1 || !dtype_ok(dtype) || !n_tasks || !n_perm || !n_long)
+        return fail(TCA_ERR_INVALID, "tca_plan_row_tasks: bad argument");
+    RowPlan p;
+    plan_rows(rowptr, M, N, static_cast<int32_t>(dtype_size(dtype)), {}, &p);
+    if (tasks) {
+        if (*n_tasks < static_cast<int32_t>(p.tasks.size()) || *n_perm < static_cast<int32_t>(p.perm.size()) ||
+            *n_long < static_cast<int32_t>(p.longrows.size()) || !perm || !longrows)
+            return fail(TCA_ERR_INVALID, "tca_plan_row_tasks: output buffers too small");
+        if (!p.tasks.empty()) std::copy(&p.tasks[0].x, &p.tasks[0].x + 4 * p.tasks.size(), tasks);
+        std::copy(p.perm.begin(), p.perm.end(), perm);
+        if (!p.longrows.empty()) std::copy(&p.longrows[0].x, &p.longrows[0].x + 4 * p.longrows.size(), longrows);
+    }
+    *n_tasks = static_cast<int32_t>(p.tasks.size());
+    *n_perm = static_cast<int32_t>(p.perm.size());
+    *n_long = static_cast<int32_t>(p.longrows.size());
+    if (geometry) {
+        geometry[0] = p.elems_per_lane;
+        geometry[1] = 1 << p.log_lanes;
+        geometry[2] = p.col_chunks;
+        geometry[3] = p.seg_len;
+    }
+    return TCA_OK;
+}

@@ -1,0 +1,295 @@
+// tca_spmm.hip -- plan / run / time entry points of libtcaspmm.so and the
+// host-pointer driver with the reference our_spmm_balanced contract.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cstdio>
+#include <cstdlib>
+#include <vector>
+
+#include "common.hpp"
+#include "planner.hpp"
+#include "row_kernel.hpp"
+
+using namespace tca;
+
+#define TCA_HIP_TRY(expr)                                                                               \
+    do {                                                                                                \
+        hipError_t e_ = (expr);                                                                         \
+        if (e_ != hipSuccess)                                                                           \
+            return fail(TCA_ERR_HIP, "%s failed: %s (%s:%d)", #expr, hipGetErrorString(e_), __FILE__, __LINE__); \
+    } while (0)
+
+struct tca_spmm_plan {
+    int32_t M = 0, K = 0, N = 0, nnz = 0, dtype = 0;
+    uint32_t flags = 0;
+    int device = 0;
+    RowPlan rows;
+    int32_t ntasks = 0;
+    int* d_rowptr = nullptr;
+    int* d_colidx = nullptr;
+    int4* d_tasks = nullptr;
+    int* d_perm = nullptr;
+    int4* d_longrows = nullptr;
+    float* d_partials = nullptr;
+    int* d_tickets = nullptr;
+    tca_plan_info info{};
+};
+
+namespace {
+
+template <typename T>
+int dev_upload(T** dst, const void* src, size_t count) {
+    *dst = nullptr;
+    if (count == 0) return TCA_OK;
+    hipError_t e = hipMalloc(reinterpret_cast<void**>(dst), sizeof(T) * count);
+    if (e != hipSuccess) {
+        *dst = nullptr;
+        return fail(TCA_ERR_ALLOC, "hipMalloc(%zu bytes): %s", sizeof(T) * count, hipGetErrorString(e));
+    }
+    if (src) {
+        e = hipMemcpy(*dst, src, sizeof(T) * count, hipMemcpyHostToDevice);
+        if (e != hipSuccess) return fail(TCA_ERR_HIP, "hipMemcpy H2D: %s", hipGetErrorString(e));
+    }
+    return TCA_OK;
+}
+
+void free_plan_device(tca_spmm_plan* p) {
+    (void)hipFree(p->d_rowptr);
+    (void)hipFree(p->d_colidx);
+    (void)hipFree(p->d_tasks);
+    (void)hipFree(p->d_perm);
+    (void)hipFree(p->d_longrows);
+    (void)hipFree(p->d_partials);
+    (void)hipFree(p->d_tickets);
+}
+
+template <typename T, int E>
+void launch_rows_t(const tca_spmm_plan* p, const void* val, const void* B, float* C, hipStream_t s) {
+    const dim3 grid((p->ntasks + kRowWaves - 1) / kRowWaves, p->rows.col_chunks);
+    hipLaunchKernelGGL((row_kernel<T, E>), grid, dim3(64 * kRowWaves), 0, s, p->d_tasks, p->ntasks, p->d_rowptr,
+                       p->d_colidx, static_cast<const T*>(val), static_cast<const T*>(B), C, p->N,
+                       p->rows.log_lanes, p->d_perm, p->d_longrows, p->d_partials, p->d_tickets);
+}
+
+template <typename T>
+int launch_rows_e(const tca_spmm_plan* p, const void* val, const void* B, float* C, hipStream_t s) {
+    switch (p->rows.elems_per_lane) {
+        case 1: launch_rows_t<T, 1>(p, val, B, C, s); return TCA_OK;
+        case 2: launch_rows_t<T, 2>(p, val, B, C, s); return TCA_OK;
+        case 4: launch_rows_t<T, 4>(p, val, B, C, s); return TCA_OK;
+        case 8:
+            if constexpr (sizeof(T) == 2) {
+                launch_rows_t<T, 8>(p, val, B, C, s);
+                return TCA_OK;
+            }
+            [[fallthrough]];
+        default: return fail(TCA_ERR_INVALID, "bad lane geometry");
+    }
+}
+
+int launch_rows(const tca_spmm_plan* p, const void* val, const void* B, float* C, hipStream_t s) {
+    if (p->ntasks == 0) return TCA_OK;
+    switch (p->dtype) {
+        case TCA_F16: return launch_rows_e<_Float16>(p, val, B, C, s);
+        case TCA_BF16: return launch_rows_e<bf16_t>(p, val, B, C, s);
+        default: return launch_rows_e<float>(p, val, B, C, s);
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+int tca_version(void) { return 100; }
+
+int tca_device_count(int32_t* count) {
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess) {
+        *count = 0;
+        return fail(TCA_ERR_HIP, "hipGetDeviceCount: %s", hipGetErrorString(e));
+    }
+    *count = n;
+    return TCA_OK;
+}
+
+int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_t K, int32_t nnz,
+                         int32_t N, int32_t dtype, uint32_t flags, tca_spmm_plan** plan) {
+    if (!plan) return fail(TCA_ERR_INVALID, "plan is NULL");
+    *plan = nullptr;
+    if (M < 0 || K < 1 || N < 1 || nnz < 0) return fail(TCA_ERR_INVALID, "bad shape M=%d K=%d N=%d nnz=%d", M, K, N, nnz);
+    if (!dtype_ok(dtype)) return fail(TCA_ERR_INVALID, "unknown dtype %d", dtype);
+    if (static_cast<int64_t>(N) * static_cast<int64_t>(dtype_size(dtype)) > (int64_t(1) << 30))
+        return fail(TCA_ERR_UNSUPPORTED, "N = %d too wide", N);
+    int st = tca_csr_validate(rowptr, colidx, M, K, nnz);
+    if (st) return st;
+    const auto t0 = std::chrono::steady_clock::now();
+    tca_spmm_plan* p = new (std::nothrow) tca_spmm_plan();
+    if (!p) return fail(TCA_ERR_ALLOC, "plan allocation failed");
+    p->M = M;
+    p->K = K;
+    p->N = N;
+    p->nnz = nnz;
+    p->dtype = dtype;
+    p->flags = flags;
+    if (hipGetDevice(&p->device) != hipSuccess) {
+        delete p;
+        return fail(TCA_ERR_HIP, "no HIP device");
+    }
+    plan_rows(rowptr, M, N, static_cast<int32_t>(dtype_size(dtype)), {}, &p->rows);
+    p->ntasks = static_cast<int32_t>(p->rows.tasks.size());
+    const size_t n_seg_total =
+        p->rows.longrows.empty() ? 0 : static_cast<size_t>(p->rows.longrows.back().y + p->rows.longrows.back().z);
+    const auto t1 = std::chrono::steady_clock::now();
+
+    auto bail = [&](int s) {
+        free_plan_device(p);
+        delete p;
+        return s;
+    };
+    if ((st = dev_upload(&p->d_rowptr, rowptr, static_cast<size_t>(M) + 1))) return bail(st);
+    if ((st = dev_upload(&p->d_colidx, colidx, static_cast<size_t>(nnz)))) return bail(st);
+    if ((st = dev_upload(&p->d_tasks, p->rows.tasks.data(), p->rows.tasks.size()))) return bail(st);
+    if ((st = dev_upload(&p->d_perm, p->rows.perm.data(), p->rows.perm.size()))) return bail(st);
+    if ((st = dev_upload(&p->d_longrows, p->rows.longrows.data(), p->rows.longrows.size()))) return bail(st);
+    if ((st = dev_upload(&p->d_partials, nullptr, n_seg_total * N))) return bail(st);
+    const size_t n_tickets = p->rows.longrows.size() * p->rows.col_chunks;
+    if ((st = dev_upload(&p->d_tickets, nullptr, n_tickets))) return bail(st);
+    if (n_tickets && hipMemset(p->d_tickets, 0, sizeof(int) * n_tickets) != hipSuccess)
+        return bail(fail(TCA_ERR_HIP, "hipMemset of tickets failed"));
+    if (hipDeviceSynchronize() != hipSuccess) return bail(fail(TCA_ERR_HIP, "hipDeviceSynchronize failed"));
+
+    tca_plan_info& in = p->info;
+    in.M = M;
+    in.K = K;
+    in.N = N;
+    in.nnz = nnz;
+    in.dtype = dtype;
+    in.elems_per_lane = p->rows.elems_per_lane;
+    in.lanes_per_row = 1 << p->rows.log_lanes;
+    in.col_chunks = p->rows.col_chunks;
+    in.n_row_tasks = p->ntasks;
+    in.n_multi_tasks = p->rows.n_multi;
+    in.n_seg_tasks = p->rows.n_seg;
+    in.n_long_rows = static_cast<int32_t>(p->rows.longrows.size());
+    in.row_blocks = (p->ntasks + kRowWaves - 1) / kRowWaves;
+    in.row_blockdim = 64 * kRowWaves;
+    in.seg_len = p->rows.seg_len;
+    in.scratch_bytes = static_cast<int64_t>(n_seg_total * N * sizeof(float) + n_tickets * sizeof(int));
+    in.plan_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
+    *plan = p;
+    return TCA_OK;
+}
+
+int tca_spmm_plan_info(const tca_spmm_plan* plan, tca_plan_info* info) {
+    if (!plan || !info) return fail(TCA_ERR_INVALID, "NULL argument");
+    *info = plan->info;
+    return TCA_OK;
+}
+
+int tca_spmm_plan_destroy(tca_spmm_plan* plan) {
+    if (!plan) return TCA_OK;
+    free_plan_device(plan);
+    delete plan;
+    return TCA_OK;
+}
+
+int tca_spmm_run(const tca_spmm_plan* p, const void* d_val, const void* d_B, float* d_C, void* stream) {
+    if (!p) return fail(TCA_ERR_INVALID, "plan is NULL");
+    if (p->M == 0) return TCA_OK;
+    if ((p->nnz > 0 && (!d_val || !d_B)) || !d_C) return fail(TCA_ERR_INVALID, "NULL device pointer");
+    const size_t vb = static_cast<size_t>(p->rows.elems_per_lane) * dtype_size(p->dtype);
+    if (reinterpret_cast<uintptr_t>(d_B) % vb != 0)
+        return fail(TCA_ERR_INVALID, "B must be aligned to %zu bytes", vb);
+    if (reinterpret_cast<uintptr_t>(d_C) % 16 != 0) return fail(TCA_ERR_INVALID, "C must be aligned to 16 bytes");
+    if (reinterpret_cast<uintptr_t>(d_val) % dtype_size(p->dtype) != 0)
+        return fail(TCA_ERR_INVALID, "values misaligned");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    int st = launch_rows(p, d_val, d_B, d_C, s);
+    if (st) return st;
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(TCA_ERR_HIP, "kernel launch: %s", hipGetErrorString(e));
+    return TCA_OK;
+}
+
+int tca_spmm_time(const tca_spmm_plan* p, const void* d_val, const void* d_B, float* d_C, void* stream,
+                  int32_t warmup, int32_t iters, float* avg_ms) {
+    if (!p || !avg_ms || iters < 1 || warmup < 0) return fail(TCA_ERR_INVALID, "tca_spmm_time: bad argument");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    for (int i = 0; i < warmup; i++) {
+        int st = tca_spmm_run(p, d_val, d_B, d_C, stream);
+        if (st) return st;
+    }
+    hipEvent_t e0, e1;
+    TCA_HIP_TRY(hipEventCreate(&e0));
+    TCA_HIP_TRY(hipEventCreate(&e1));
+    TCA_HIP_TRY(hipEventRecord(e0, s));
+    for (int i = 0; i < iters; i++) {
+        int st = tca_spmm_run(p, d_val, d_B, d_C, stream);
+        if (st) {
+            (void)hipEventDestroy(e0);
+            (void)hipEventDestroy(e1);
+            return st;
+        }
+    }
+    TCA_HIP_TRY(hipEventRecord(e1, s));
+    TCA_HIP_TRY(hipEventSynchronize(e1));
+    float ms = 0.f;
+    TCA_HIP_TRY(hipEventElapsedTime(&ms, e0, e1));
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    *avg_ms = ms / static_cast<float>(iters);
+    return TCA_OK;
+}
+
+int tca_spmm_host(const int32_t* rowptr, const int32_t* colidx, const void* val, int32_t M, int32_t K, int32_t nnz,
+                  const void* B, float* C, int32_t N, int32_t dtype, int32_t n_iter, int32_t verbose,
+                  double* elapsed_ms) {
+    if (!rowptr || (nnz > 0 && (!colidx || !val)) || !B || !C || n_iter < 1)
+        return fail(TCA_ERR_INVALID, "tca_spmm_host: bad argument");
+    if (!dtype_ok(dtype)) return fail(TCA_ERR_INVALID, "unknown dtype %d", dtype);
+    const size_t es = dtype_size(dtype);
+    void *dval = nullptr, *dB = nullptr;
+    float* dC = nullptr;
+    tca_spmm_plan* plan = nullptr;
+    int st = TCA_OK;
+    auto cleanup = [&](int s) {
+        (void)hipFree(dval);
+        (void)hipFree(dB);
+        (void)hipFree(dC);
+        tca_spmm_plan_destroy(plan);
+        return s;
+    };
+    // Device copies of the operands (reference src/our_spmm.cu:503-525; C is
+    // not copied in: every row of C is written).
+    if (hipMalloc(&dval, es * std::max(nnz, 1)) != hipSuccess ||
+        hipMalloc(&dB, es * static_cast<size_t>(K) * N) != hipSuccess ||
+        hipMalloc(reinterpret_cast<void**>(&dC), sizeof(float) * std::max<size_t>(static_cast<size_t>(M) * N, 1)) !=
+            hipSuccess)
+        return cleanup(fail(TCA_ERR_ALLOC, "tca_spmm_host: device allocation failed"));
+    if ((nnz > 0 && hipMemcpy(dval, val, es * nnz, hipMemcpyHostToDevice) != hipSuccess) ||
+        hipMemcpy(dB, B, es * static_cast<size_t>(K) * N, hipMemcpyHostToDevice) != hipSuccess)
+        return cleanup(fail(TCA_ERR_HIP, "tca_spmm_host: H2D copy failed"));
+    const auto t0 = std::chrono::steady_clock::now();
+    st = tca_spmm_plan_create(rowptr, colidx, M, K, nnz, N, dtype, TCA_PLAN_DEFAULT, &plan);
+    const auto t1 = std::chrono::steady_clock::now();
+    if (st) return cleanup(st);
+    if (verbose) {
+        // Same two lines as reference our_spmm_balanced (src/our_spmm.cu:549,552),
+        // describing this build's plan: the row kernel's grid, block and LDS.
+        std::printf("preprocess %fms taken\n", std::chrono::duration<float, std::milli>(t1 - t0).count());
+        std::printf("num_block: %d blockdim: %d shm: %fKB\n", plan->info.row_blocks, plan->info.row_blockdim,
+                    plan->info.mfma_lds_bytes / 1024.0f);
+    }
+    float ms = 0.f;
+    st = tca_spmm_time(plan, dval, dB, dC, nullptr, 5, n_iter, &ms);
+    if (st) return cleanup(st);
+    if (hipMemcpy(C, dC, sizeof(float) * static_cast<size_t>(M) * N, hipMemcpyDeviceToHost) != hipSuccess)
+        return cleanup(fail(TCA_ERR_HIP, "tca_spmm_host: D2H copy failed"));
+    if (elapsed_ms) *elapsed_ms = ms;
+    return cleanup(TCA_OK);
+}
+
+}  // extern "C"

@@ -1,0 +1,72 @@
+"""The C-ABI library loads and exports every function include/*.h declares
+(no compute call needs a GPU here)."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from conftest import ROOT
+
+import spmm_amd._lib as L
+
+
+def _declared():
+    names = set()
+    inc = os.path.join(ROOT, "include")
+    for fn in sorted(os.listdir(inc)):
+        if not fn.endswith(".h"):
+            continue
+        text = open(os.path.join(inc, fn)).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        text = re.sub(r"//[^\n]*", "", text)
+        for m in re.finditer(r"\b(tca_\w+)\s*\(", text):
+            names.add(m.group(1))
+    return names
+
+
+def test_every_declared_symbol_is_exported():
+    declared = _declared()
+    assert len(declared) > 30
+    lib = ctypes.CDLL(L.LIB_PATH)
+    missing = [n for n in sorted(declared) if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_binding_covers_declarations():
+    assert _declared() == set(L.SIGNATURES), _declared() ^ set(L.SIGNATURES)
+
+
+def test_exports_are_c_linkage():
+    out = subprocess.run(["nm", "-D", "--defined-only", L.LIB_PATH], capture_output=True, text=True, check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if line.strip()}
+    for n in _declared():
+        assert n in exported, n  # unmangled
+
+
+def test_status_strings_and_errors_without_gpu():
+    assert L.lib.tca_status_string(0) == b"ok"
+    assert L.lib.tca_status_string(6) == b"malformed input"
+    assert L.lib.tca_version() >= 100
+    # argument errors are reported, never exit the process
+    p = ctypes.c_void_p()
+    st = L.lib.tca_spmm_plan_create(None, None, 4, 4, 0, 8, 0, 0, ctypes.byref(p))
+    assert st == 1 and b"rowptr" in L.lib.tca_last_error()
+    st = L.lib.tca_spmm_run(None, None, None, None, None)
+    assert st == 1
+
+
+def test_rejects_invalid_csr_before_touching_device():
+    import numpy as np
+    rp = np.array([0, 2, 1, 3], np.int32)  # decreasing offsets
+    ci = np.array([0, 1, 2], np.int32)
+    p = ctypes.c_void_p()
+    st = L.lib.tca_spmm_plan_create(L.np_ptr(rp, ctypes.c_int32), L.np_ptr(ci, ctypes.c_int32), 3, 4, 3, 8, 0, 0,
+                                    ctypes.byref(p))
+    assert st == 1 and b"decreases" in L.lib.tca_last_error()
+    rp = np.array([0, 2, 3, 3], np.int32)
+    ci = np.array([1, 1, 2], np.int32)  # not strictly ascending
+    st = L.lib.tca_spmm_plan_create(L.np_ptr(rp, ctypes.c_int32), L.np_ptr(ci, ctypes.c_int32), 3, 4, 3, 8, 0, 0,
+                                    ctypes.byref(p))
+    assert st == 1 and b"ascending" in L.lib.tca_last_error()

@@ -1,0 +1,223 @@
+"""GPU parity: the gfx950 kernels (through the C ABI) against the CPU oracle
+and the committed golden fixtures.
+
+Bars: bit-exact where the arithmetic is exact (values in {+-1,+-1/2,+-2},
+B in {k/256}, rows short enough that every partial sum is exact in fp32 in
+any order), and the reference verdict (compare_mat, tol 1e-3) plus a max
+relative error <= 1e-3 with an absolute floor elsewhere (fp32 accumulation
+in a different order than the oracle's)."""
+import os
+
+import numpy as np
+import pytest
+
+from conftest import GOLDEN, exact_dense, exact_values
+from oracle import oracle
+
+import spmm_amd as S
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3       # max relative error <= 1e-3
+FLOOR = 1e-2     # |gold| floor of the relative-error report (outputs are O(0.1..10))
+
+
+def _dev(torch, arr):
+    a = np.ascontiguousarray(arr)
+    if a.dtype == np.uint16:
+        a = a.view(np.int16)
+    return torch.from_numpy(a).to("cuda:0")
+
+
+def run_gpu(torch, a: S.CSR, b: np.ndarray, flags=S.TCA_PLAN_DEFAULT, plan=None, out=None):
+    n = b.shape[1]
+    own = plan is None
+    if own:
+        plan = S.Plan(a, n, flags)
+    val = _dev(torch, a.values) if a.nnz else torch.zeros(1, device="cuda:0")
+    bd = _dev(torch, b)
+    c = out if out is not None else torch.full((a.nrow, n), float("nan"), dtype=torch.float32, device="cuda:0")
+    plan.run(val, bd, c)
+    torch.cuda.synchronize()
+    res = c.cpu().numpy()
+    if own:
+        plan.close()
+    return res
+
+
+def oracle_c(a: S.CSR, b: np.ndarray):
+    return oracle.csr_spmm(a.rowptr, a.colidx, a.values_f32(), S.from_storage(b, a.dtype))
+
+
+def assert_close(gold, got, what=""):
+    v = S.compare_mat(gold, got, TOL, FLOOR)
+    assert v["success"], (what, v)
+    assert v["max_rel_floor"] <= TOL, (what, v)
+    assert np.all(np.isfinite(got)), what
+
+
+def make_csr(rng, lens, k, dtype, values="exact"):
+    lens = np.asarray(lens, np.int64)
+    rowptr = np.zeros(len(lens) + 1, np.int32)
+    np.cumsum(lens, out=rowptr[1:])
+    colidx = np.concatenate([np.sort(rng.choice(k, size=int(l), replace=False)) for l in lens]
+                            + [np.zeros(0, np.int64)]).astype(np.int32)
+    nnz = int(rowptr[-1])
+    v = exact_values(rng, nnz) if values == "exact" else (rng.standard_normal(nnz) * 0.02).astype(np.float32)
+    v[v == 0] = 0.5
+    return S.CSR(len(lens), k, rowptr, colidx, S.to_storage(v, dtype), dtype)
+
+
+# ------------------------------------------------------------ golden
+def test_golden_scipy_fixtures(torch_cuda):
+    data = np.load(os.path.join(GOLDEN, "scipy_spmm.npz"))
+    names = sorted({k.split("__")[0] for k in data.files})
+    for nm in names:
+        rp, ci, v, b, c = (data[f"{nm}__{x}"] for x in ("rowptr", "colidx", "values", "b", "c"))
+        dtype = S.TCA_F32 if v.dtype == np.float32 else S.TCA_F16
+        a = S.CSR(len(rp) - 1, b.shape[0], rp, ci, v, dtype)
+        got = run_gpu(torch_cuda, a, b)
+        print(nm, a.nrow, b.shape, flush=True)
+        assert_close(c.astype(np.float32), got, nm)
+        assert_close(oracle_c(a, b), got, nm)
+
+
+def test_fixture_smtx_reference_flow(torch_cuda):
+    """The reference harness flow: .smtx -> CSR (1.0 values), N = 256, seeded B."""
+    a = S.read_smtx(os.path.join(GOLDEN, "body_decoder_layer_2_ffn_conv1.smtx"))
+    for n in (64, 128, 256, 512):
+        b = S.gen_dense(a.ncol, n, 3, seed=n, dtype=S.TCA_F16, sparsity=0.1)
+        got = run_gpu(torch_cuda, a, b)
+        assert_close(oracle_c(a, b), got, f"fixture N={n}")
+        empty = np.diff(a.rowptr) == 0
+        assert np.all(got[empty] == 0.0)
+
+
+# ------------------------------------------------------- exact vectors
+SHAPES_N = [1, 2, 3, 8, 12, 16, 24, 64, 96, 100, 128, 200, 256, 512, 520, 1000, 1024]
+
+
+@pytest.mark.parametrize("dtype", [S.TCA_F16, S.TCA_BF16, S.TCA_F32])
+def test_exact_bit_equal_all_widths(torch_cuda, dtype):
+    rng = np.random.default_rng(11 + dtype)
+    k = 3000
+    # empty rows, 1..8 (multi), medium, and long rows (split into segments)
+    lens = np.concatenate([np.zeros(9, np.int64), rng.integers(1, 9, 60), rng.integers(9, 300, 40),
+                           [600, 1500, 2999, 2500]])
+    rng.shuffle(lens)
+    a = make_csr(rng, lens, k, dtype)
+    for n in SHAPES_N:
+        b = S.to_storage(exact_dense(rng, (k, n)), dtype)
+        got = run_gpu(torch_cuda, a, b)
+        want = oracle_c(a, b)
+        assert np.array_equal(got, want), (dtype, n, np.abs(got - want).max())
+
+
+def test_exact_long_rows_many_segments(torch_cuda):
+    """Rows far above the segment length; every output element exact."""
+    rng = np.random.default_rng(21)
+    k = 16000
+    lens = [15000, 9000, 12000, 0, 3, 16000 - 1]
+    a = make_csr(rng, lens, k, S.TCA_F16)
+    info = None
+    for n in (64, 256, 512):
+        b = S.to_storage(exact_dense(rng, (k, n)), S.TCA_F16)
+        with S.Plan(a, n) as p:
+            info = p.info()
+            got = run_gpu(torch_cuda, a, b, plan=p)
+        assert info["n_long_rows"] >= 4
+        assert np.array_equal(got, oracle_c(a, b)), n
+
+
+def test_plan_reuse_and_determinism(torch_cuda):
+    """One plan, several B: tickets reset between launches; identical bits on repeat."""
+    rng = np.random.default_rng(31)
+    a, _ = S.gen_zipf_rows(4000, 20000, 300000, s=1.5, cap=50000, seed=3)
+    n = 64
+    with S.Plan(a, n) as p:
+        assert p.info()["n_long_rows"] > 0
+        outs = []
+        for seed in (1, 2, 1):
+            b = S.gen_dense(a.ncol, n, 0, seed=seed, dtype=S.TCA_F16)
+            got = run_gpu(torch_cuda, a, b, plan=p)
+            assert_close(oracle_c(a, b), got, f"seed {seed}")
+            outs.append(got)
+        assert np.array_equal(outs[0], outs[2])
+        assert not np.array_equal(outs[0], outs[1])
+
+
+def test_empty_and_degenerate(torch_cuda):
+    rng = np.random.default_rng(41)
+    # no nonzeros at all: C must be all zeros
+    a = S.CSR(5, 7, np.zeros(6, np.int32), np.zeros(0, np.int32), np.zeros(0, np.float16), S.TCA_F16)
+    got = run_gpu(torch_cuda, a, S.to_storage(np.ones((7, 16)), S.TCA_F16))
+    assert np.array_equal(got, np.zeros((5, 16), np.float32))
+    # a single dense row
+    a = make_csr(rng, [300], 300, S.TCA_F32)
+    b = S.to_storage(exact_dense(rng, (300, 33)), S.TCA_F32)
+    assert np.array_equal(run_gpu(torch_cuda, a, b), oracle_c(a, b))
+    # one column matrix
+    a = make_csr(rng, [1, 0, 1], 1, S.TCA_F16)
+    b = S.to_storage(np.array([[0.75]]), S.TCA_F16)
+    assert np.array_equal(run_gpu(torch_cuda, a, b), oracle_c(a, b))
+
+
+def test_misaligned_b_is_rejected(torch_cuda):
+    torch = torch_cuda
+    rng = np.random.default_rng(51)
+    a = make_csr(rng, [3, 4], 10, S.TCA_F16)
+    with S.Plan(a, 64) as p:
+        buf = torch.zeros(10 * 64 + 1, dtype=torch.float16, device="cuda:0")
+        c = torch.zeros((2, 64), dtype=torch.float32, device="cuda:0")
+        val = _dev(torch, a.values)
+        with pytest.raises(S.TcaError):
+            p.run(val, buf.data_ptr() + 2, c)
+
+
+def test_nondefault_stream(torch_cuda):
+    torch = torch_cuda
+    rng = np.random.default_rng(61)
+    a = make_csr(rng, rng.integers(0, 50, 500), 800, S.TCA_F16)
+    b = S.to_storage(exact_dense(rng, (800, 128)), S.TCA_F16)
+    s = torch.cuda.Stream()
+    with S.Plan(a, 128) as p:
+        val, bd = _dev(torch, a.values), _dev(torch, b)
+        c = torch.empty((a.nrow, 128), dtype=torch.float32, device="cuda:0")
+        torch.cuda.synchronize()
+        p.run(val, bd, c, stream=s.cuda_stream)
+        s.synchronize()
+        assert np.array_equal(c.cpu().numpy(), oracle_c(a, b))
+
+
+def test_host_driver_our_spmm_balanced(torch_cuda):
+    a = S.read_smtx(os.path.join(GOLDEN, "body_decoder_layer_2_ffn_conv1.smtx"))
+    b = S.gen_dense(a.ncol, 256, 3, seed=7, dtype=S.TCA_F16, sparsity=0.1)
+    c, ms = S.our_spmm_balanced(a, b, n_iter=10)
+    assert ms > 0
+    assert_close(oracle_c(a, b), c, "host driver")
+
+
+# ------------------------------------------------------------- configs
+@pytest.mark.parametrize("cfg", [0, 1])
+def test_config_full_size_small(torch_cuda, cfg):
+    a, n, st = S.gen_config(cfg, seed=1)
+    dist = 0
+    b = S.gen_dense(a.ncol, n, dist, seed=100 + cfg, dtype=a.dtype)
+    print(f"config {cfg}: M={a.nrow} K={a.ncol} N={n} nnz={a.nnz}", flush=True)
+    got = run_gpu(torch_cuda, a, b)
+    assert_close(oracle_c(a, b), got, f"config {cfg}")
+
+
+@pytest.mark.parametrize("cfg", [2, 3, 4])
+def test_config_full_size_large(torch_cuda, cfg):
+    a, n, st = S.gen_config(cfg, seed=1)
+    dist = 1 if cfg in (2, 3) else 0
+    b = S.gen_dense(a.ncol, n, dist, seed=100 + cfg, dtype=a.dtype)
+    print(f"config {cfg}: M={a.nrow} K={a.ncol} N={n} nnz={a.nnz}", flush=True)
+    got = run_gpu(torch_cuda, a, b)
+    gold = oracle_c(a, b)
+    assert_close(gold, got, f"config {cfg}")
+    # size-independent check: checksum of row sums through the fp64 oracle
+    row_sum_gold = oracle.csr_spmm_f64(a.rowptr, a.colidx, a.values_f32().astype(np.float64),
+                                       S.from_storage(b, a.dtype).astype(np.float64).sum(1, keepdims=True))
+    np.testing.assert_allclose(got.astype(np.float64).sum(1), row_sum_gold[:, 0], rtol=1e-3, atol=1e-2)

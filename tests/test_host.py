@@ -1,0 +1,267 @@
+"""CPU tests of the product's host library (readers, conversion, verdict,
+generators, planner) against the oracle and the reference fixture."""
+import os
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+
+from conftest import FIXTURE_SMTX, ROOT
+from oracle import oracle
+
+import spmm_amd as S
+
+
+# ------------------------------------------------------------- readers
+def test_smtx_reader_matches_oracle(fixture_text):
+    nrow, ncol, nnz, rowptr, colidx = oracle.parse_smtx(fixture_text)
+    a = S.read_smtx(FIXTURE_SMTX)
+    assert (a.nrow, a.ncol, a.nnz) == (nrow, ncol, nnz)
+    assert np.array_equal(a.rowptr, rowptr) and np.array_equal(a.colidx, colidx)
+    assert a.values.dtype == np.float16 and np.all(a.values == 1.0)
+    a.validate()
+
+
+def test_smtx_dense_reader_matches_reference_semantics(fixture_text):
+    nrow, ncol, nnz, rowptr, colidx = oracle.parse_smtx(fixture_text)
+    d = S.read_smtx_dense(FIXTURE_SMTX)
+    assert np.array_equal(d, oracle.smtx_to_dense(nrow, ncol, rowptr, colidx))
+    # .smtx -> dense -> CSR equals the direct reader
+    a = S.dense_to_csr(d, S.TCA_F16)
+    b = S.read_smtx(FIXTURE_SMTX)
+    assert np.array_equal(a.rowptr, b.rowptr) and np.array_equal(a.colidx, b.colidx)
+
+
+def test_smtx_write_round_trip_is_byte_identical(tmp_path):
+    a = S.read_smtx(FIXTURE_SMTX)
+    out = tmp_path / "w.smtx"
+    S.write_smtx(str(out), a)
+    with open(FIXTURE_SMTX, "rb") as f1, open(out, "rb") as f2:
+        assert f1.read() == f2.read()
+
+
+def test_smtx_reader_sorts_and_dedupes_like_dense_path(tmp_path):
+    p = tmp_path / "u.smtx"
+    p.write_text("3, 5, 6\n0 3 3 6 \n4 1 1 0 2 4\n")
+    a = S.read_smtx(str(p))
+    assert a.rowptr.tolist() == [0, 2, 2, 5] and a.colidx.tolist() == [1, 4, 0, 2, 4]
+    d = S.read_smtx_dense(str(p))
+    b = S.dense_to_csr(d, S.TCA_F16)
+    assert np.array_equal(a.rowptr, b.rowptr) and np.array_equal(a.colidx, b.colidx)
+
+
+@pytest.mark.parametrize("text", [
+    "2, 3\n0 1 1\n0\n",                 # short header
+    "2, 3, 1\n0 1\n0\n",                # too few row offsets
+    "2, 3, 1\n0 1 1 1\n0\n",            # too many row offsets
+    "2, 3, 1\n1 1 1\n0\n",              # rowptr[0] != 0
+    "2, 3, 2\n0 2 1\n0 1\n",            # decreasing / not ending at nnz
+    "2, 3, 1\n0 1 1\n3\n",              # column out of range
+    "2, 3, 2\n0 1 2\n0\n",              # too few column indices
+    "2, 3, 1\n0 1 1\n0 1\n",            # too many column indices
+    "2, 3, 1\n0 x 1\n0\n",              # bad token
+])
+def test_smtx_reader_rejects_malformed(tmp_path, text):
+    p = tmp_path / "bad.smtx"
+    p.write_text(text)
+    with pytest.raises(S.TcaError) as e:
+        S.read_smtx(str(p))
+    assert e.value.status == 6  # TCA_ERR_FORMAT
+
+
+def test_missing_file_is_io_error():
+    with pytest.raises(S.TcaError) as e:
+        S.read_smtx("/nonexistent/file.smtx")
+    assert e.value.status == 5
+
+
+def test_mtx_reader(tmp_path):
+    p = tmp_path / "m.mtx"
+    p.write_text("%%MatrixMarket matrix coordinate real general\n% c\n3 4 4\n3 4 2.5\n1 2 1.0\n1 1 -1\n2 3 4\n")
+    a = S.read_mtx(str(p), pattern_only=False, zero_based=False, dtype=S.TCA_F32)
+    assert a.rowptr.tolist() == [0, 2, 3, 4]
+    assert a.colidx.tolist() == [0, 1, 2, 3]
+    assert a.values.tolist() == [-1.0, 1.0, 4.0, 2.5]
+    b = S.read_mtx(str(p), pattern_only=True, zero_based=False, dtype=S.TCA_F16)
+    assert np.all(b.values == 1.0)
+    p.write_text("3 4 2\n0 0\n0 0\n")
+    with pytest.raises(S.TcaError):
+        S.read_mtx(str(p), pattern_only=True, zero_based=True)  # duplicate entry
+    p.write_text("3 4 3\n1 1\n")
+    with pytest.raises(S.TcaError):
+        S.read_mtx(str(p), pattern_only=True)  # count mismatch (reference asserts)
+
+
+# ---------------------------------------------------------- conversions
+def test_f16_conversion_matches_numpy():
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    f = S.from_storage(h.view(np.float16), S.TCA_F16)
+    ref = h.view(np.float16).astype(np.float32)
+    same = (f.view(np.uint32) == ref.view(np.uint32)) | (np.isnan(f) & np.isnan(ref))
+    assert same.all()
+    rng = np.random.default_rng(0)
+    x = np.concatenate([
+        rng.standard_normal(200000).astype(np.float32) * 10.0 ** rng.integers(-9, 6, 200000),
+        np.array([65504, 65519.99, 65520, 1e6, -1e6, 2 ** -24, 2 ** -25, 2 ** -25 * 1.0001, 6.0e-8, 0.0, -0.0,
+                  np.inf, -np.inf], np.float32),
+        (np.arange(-70000, 70000, 0.5, dtype=np.float32)),
+    ]).astype(np.float32)
+    got = S.to_storage(x, S.TCA_F16)
+    assert np.array_equal(got.view(np.uint16), x.astype(np.float16).view(np.uint16))
+
+
+def _bf16_ref(x):
+    u = x.view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    nan = np.isnan(x)
+    r[nan] = ((u[nan] >> 16) | 0x40).astype(np.uint16)
+    return r
+
+
+def test_bf16_conversion():
+    rng = np.random.default_rng(1)
+    x = (rng.standard_normal(100000) * 10.0 ** rng.integers(-30, 30, 100000)).astype(np.float32)
+    x = np.concatenate([x, np.array([np.nan, np.inf, -np.inf, 0.0, -0.0, 3.4e38], np.float32)])
+    got = S.to_storage(x, S.TCA_BF16)
+    assert np.array_equal(got, _bf16_ref(x))
+    back = S.from_storage(got, S.TCA_BF16)
+    assert np.array_equal(back.view(np.uint32), got.astype(np.uint32) << 16)
+
+
+def test_dense_to_csr_and_back_match_oracle():
+    rng = np.random.default_rng(2)
+    d = rng.standard_normal((60, 45)).astype(np.float16)
+    d[rng.random(d.shape) < 0.85] = 0
+    d[3, 4] = -0.0
+    a = S.dense_to_csr(d, S.TCA_F16)
+    rp, ci, v = oracle.dense_to_csr(d)
+    assert np.array_equal(a.rowptr, rp) and np.array_equal(a.colidx, ci) and np.array_equal(a.values, v)
+    assert np.array_equal(S.csr_to_dense(a), np.where(d == 0, np.float16(0), d))
+
+
+# -------------------------------------------------------------- verdict
+def test_compare_mat_matches_oracle():
+    rng = np.random.default_rng(3)
+    for _ in range(50):
+        g = rng.standard_normal(200).astype(np.float32)
+        c = g + rng.standard_normal(200).astype(np.float32) * 10.0 ** rng.integers(-6, 0)
+        c[rng.random(200) < 0.05] = 0
+        g[rng.random(200) < 0.05] = 0
+        ours = S.compare_mat(g, c, 1e-3)
+        ok, fc, ff, mr = oracle.compare_mat(g, c, 1e-3)
+        assert (ours["success"], ours["fail_count"], ours["first_fail"]) == (ok, fc, ff)
+        assert ours["max_rel"] == pytest.approx(mr, nan_ok=True)
+
+
+def test_naive_csr_spmm_bit_equal_to_oracle():
+    rng = np.random.default_rng(4)
+    a, _ = S.gen_bernoulli(100, 80, 0.2, seed=9, dtype=S.TCA_F16)
+    b = S.gen_dense(80, 48, 0, seed=3, dtype=S.TCA_F16)
+    got = S.naive_csr_spmm(a, b)
+    want = oracle.csr_spmm(a.rowptr, a.colidx, a.values_f32(), b.astype(np.float32))
+    assert np.array_equal(got, want)
+
+
+# ----------------------------------------------------------- generators
+def test_generators_deterministic_and_valid():
+    a1, st1 = S.gen_bernoulli(256, 128, 0.1, seed=5)
+    a2, _ = S.gen_bernoulli(256, 128, 0.1, seed=5)
+    a3, _ = S.gen_bernoulli(256, 128, 0.1, seed=6)
+    assert np.array_equal(a1.colidx, a2.colidx) and np.array_equal(a1.values, a2.values)
+    assert not np.array_equal(a1.rowptr, a3.rowptr)
+    a1.validate()
+    p = a1.nnz / (256 * 128)
+    assert abs(p - 0.1) < 0.01
+    v = a1.values_f32()
+    assert abs(v.std() - 0.02) < 0.002 and np.all(v != 0)
+
+
+def test_generators_independent_of_thread_count():
+    code = ("import sys; sys.path.insert(0, %r); import spmm_amd as S, hashlib;"
+            "a,_=S.gen_lognormal_rows(512, 1024, 60, seed=3); r,_=S.gen_rmat(12, 3000, 40000, seed=3);"
+            "z,_=S.gen_zipf_rows(2000, 5000, 40000, cap=3000, seed=3);"
+            "print(hashlib.sha1(a.colidx.tobytes()+a.values.tobytes()+r.colidx.tobytes()+r.values.tobytes()"
+            "+z.colidx.tobytes()+z.rowptr.tobytes()).hexdigest())") % ROOT
+    outs = []
+    for t in ("1", "3", "8"):
+        env = dict(os.environ, OMP_NUM_THREADS=t)
+        outs.append(subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True,
+                                   check=True).stdout.strip())
+    assert len(set(outs)) == 1, outs
+
+
+def test_lognormal_rows_stats():
+    a, st = S.gen_lognormal_rows(4096, 4096, 205.0, 1.0, seed=1)
+    a.validate()
+    lens = np.diff(a.rowptr)
+    assert 190 < lens.mean() < 215
+    # log-lengths ~ N(ln 205 - 0.5, 1)
+    ll = np.log(lens[lens > 0])
+    assert abs(ll.mean() - (np.log(205) - 0.5)) < 0.06 and abs(ll.std() - 1.0) < 0.06
+
+
+def test_rmat_small_structure():
+    a, st = S.gen_rmat(10, 1000, 20000, norm=0, seed=2)
+    a.validate()
+    d = S.csr_to_dense(a.astype(S.TCA_F32)).astype(np.float64)
+    assert np.allclose(d, d.T)  # symmetric values D^-1/2 (A+I) D^-1/2
+    assert np.all(np.diag(d) > 0)  # self-loops
+    deg = np.diff(a.rowptr).astype(np.float64)
+    r = 5
+    cols = a.colidx[a.rowptr[r]:a.rowptr[r + 1]]
+    np.testing.assert_allclose(d[r, cols], 1.0 / np.sqrt(deg[r] * deg[cols]), rtol=1e-6)
+    m, _ = S.gen_rmat(10, 1000, 20000, norm=1, seed=2)
+    lens = np.diff(m.rowptr)
+    for r in np.nonzero(lens)[0][:20]:
+        assert np.allclose(m.values[m.rowptr[r]:m.rowptr[r + 1]], 1.0 / lens[r])
+
+
+def test_zipf_rows_total_and_cap():
+    z, st = S.gen_zipf_rows(20000, 20000, 400000, s=1.5, cap=15000, seed=4)
+    z.validate()
+    lens = np.diff(z.rowptr)
+    assert z.nnz == 400000 and lens.max() <= 15000 and st["max_row"] == lens.max()
+
+
+# -------------------------------------------------------------- planner
+@pytest.mark.parametrize("n,dtype", [(256, S.TCA_F16), (512, S.TCA_F16), (64, S.TCA_F16), (128, S.TCA_F32),
+                                     (7, S.TCA_F32), (100, S.TCA_BF16), (1000, S.TCA_F16)])
+def test_plan_covers_every_row_once(n, dtype):
+    rng = np.random.default_rng(n)
+    lens = np.concatenate([rng.integers(0, 40, 3000), [0, 0, 5000, 20000, 1, 2, 3]])
+    rowptr = np.zeros(len(lens) + 1, np.int32)
+    np.cumsum(lens, out=rowptr[1:])
+    a = S.CSR(len(lens), 1, rowptr, np.zeros(rowptr[-1], np.int32), np.zeros(rowptr[-1], np.float32), S.TCA_F32)
+    tasks, perm, longrows, geo = S.plan_row_tasks(a, n, dtype)
+    e, g = geo["elems_per_lane"], geo["lanes_per_row"]
+    es = 4 if dtype == S.TCA_F32 else 2
+    assert e * es <= 16 and n % e == 0 and g in (1, 2, 4, 8, 16, 32, 64)
+    assert geo["col_chunks"] * 64 * e >= n and g * e >= min(n, 64 * e)
+    covered = np.zeros(len(lens), np.int64)
+    seg_nnz = {}
+    for x, y, z, w in tasks:
+        if w == 0:
+            assert (y, z) == (rowptr[x], rowptr[x + 1])
+            covered[x] += 1
+        elif w == 1:
+            assert 1 <= y <= 64 // g
+            rows = perm[x:x + y]
+            assert z == lens[rows].max()
+            covered[rows] += 1
+        else:
+            assert w & 3 == 2
+            row, first, nseg, _ = longrows[x]
+            assert first <= (w >> 2) < first + nseg
+            seg_nnz.setdefault(row, []).append((y, z))
+    for row, segs in seg_nnz.items():
+        segs.sort()
+        assert segs[0][0] == rowptr[row] and segs[-1][1] == rowptr[row + 1]
+        assert all(segs[i][1] == segs[i + 1][0] for i in range(len(segs) - 1))
+        assert max(z - y for y, z in segs) <= geo["seg_len"]
+        covered[row] += 1
+    assert np.all(covered == 1)
+    # longest first
+    work = [z - y if w != 1 else z for x, y, z, w in tasks]
+    kinds = [w & 3 for *_, w in tasks]
+    assert kinds == sorted(kinds, key=lambda k: {2: 0, 0: 1, 1: 2}[k])
