@@ -59,7 +59,7 @@ typedef struct tca_plan_info {
     int32_t M, K, N, nnz, dtype;
     int32_t elems_per_lane;   /* B columns per lane per load (16-byte vectors when possible) */
     int32_t lanes_per_row;    /* lanes covering one B-row column chunk (power of 2, <= 64) */
-    int32_t col_chunks;       /* column chunks of 64 * elems_per_lane */
+    int32_t col_chunks;       /* column chunks of C (one per XCD slice of B when possible) */
     int32_t n_row_tasks;      /* wavefront tasks of the row kernel */
     int32_t n_multi_tasks;    /* of which: several short rows per wavefront */
     int32_t n_seg_tasks;      /* of which: segments of split long rows */
@@ -76,6 +76,10 @@ typedef struct tca_plan_info {
     int32_t seg_len;          /* nonzeros per long-row segment */
     int64_t scratch_bytes;    /* device scratch owned by the plan */
     double plan_ms;           /* host planning time */
+    int32_t n_wide_tasks;     /* row-kernel tasks that are quarters of workgroup-shared rows */
+    int32_t chunk_lanes;      /* lanes holding data in one column chunk */
+    int32_t row_len;          /* rows up to this length take one wavefront */
+    int32_t wide_len;         /* rows up to this length take one workgroup; longer rows are segmented */
 } tca_plan_info;
 
 /* Replaces reference workload_manager (src/our_spmm.cu:353-477) plus the
@@ -133,10 +137,15 @@ int tca_condense_windows(const int32_t* rowptr, const int32_t* colidx, int32_t M
  * longrows[4*n_long].  Task int4 {x,y,z,w}: w == 0 row task (x row, [y,z)
  * nonzeros); w == 1 multi task (x offset into perm, y rows, z longest row);
  * w & 3 == 2 segment task (x long-row id, [y,z) nonzeros, w >> 2 segment
- * slot).  longrows entry {row, first segment slot, segments, 0}. */
+ * slot); w & 3 == 3 quarter of a wide row (x row, [y,z) nonzeros, w >> 2
+ * quarter), four consecutive 4-aligned tasks per wide row.  longrows entry
+ * {row, first segment slot, segments, 0}.  Every task runs once per column
+ * chunk.  geometry[8] receives elems_per_lane, lanes per slot, column chunks,
+ * segment length, lanes per chunk, row-task length limit, wide-row length
+ * limit and the multi-task length limit. */
 int tca_plan_row_tasks(const int32_t* rowptr, int32_t M, int32_t N, int32_t dtype, int32_t* n_tasks,
                        int32_t* n_perm, int32_t* n_long, int32_t* tasks, int32_t* perm, int32_t* longrows,
-                       int32_t* geometry /* [4]: elems_per_lane, lanes_per_row, col_chunks, seg_len */);
+                       int32_t* geometry);
 
 /* ---- library information ---- */
 const char* tca_status_string(int status);

@@ -195,7 +195,7 @@ def plan_row_tasks(a: CSR, n: int, dtype: int = None):
     dtype = a.dtype if dtype is None else dtype
     rp = np.ascontiguousarray(a.rowptr, np.int32)
     nt, npm, nl = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
-    geo = np.zeros(4, np.int32)
+    geo = np.zeros(8, np.int32)
     call("tca_plan_row_tasks", np_ptr(rp, ctypes.c_int32), a.nrow, n, dtype, ctypes.byref(nt), ctypes.byref(npm),
          ctypes.byref(nl), None, None, None, np_ptr(geo, ctypes.c_int32))
     tasks = np.zeros((nt.value, 4), np.int32)
@@ -204,8 +204,9 @@ def plan_row_tasks(a: CSR, n: int, dtype: int = None):
     call("tca_plan_row_tasks", np_ptr(rp, ctypes.c_int32), a.nrow, n, dtype, ctypes.byref(nt), ctypes.byref(npm),
          ctypes.byref(nl), np_ptr(tasks, ctypes.c_int32), np_ptr(perm, ctypes.c_int32),
          np_ptr(longrows, ctypes.c_int32), np_ptr(geo, ctypes.c_int32))
-    return tasks, perm[:npm.value], longrows[:nl.value], {"elems_per_lane": int(geo[0]), "lanes_per_row": int(geo[1]),
-                                                          "col_chunks": int(geo[2]), "seg_len": int(geo[3])}
+    keys = ("elems_per_lane", "lanes_per_row", "col_chunks", "seg_len", "chunk_lanes", "row_len", "wide_len",
+            "multi_max")
+    return tasks, perm[:npm.value], longrows[:nl.value], {k: int(v) for k, v in zip(keys, geo)}
 
 
 # ----------------------------------------------------------- generators

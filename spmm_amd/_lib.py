@@ -45,7 +45,8 @@ class TcaPlanInfo(ctypes.Structure):
                 ("n_row_tasks", i32), ("n_multi_tasks", i32), ("n_seg_tasks", i32), ("n_long_rows", i32),
                 ("n_windows_mfma", i32), ("rows_mfma", i32), ("nnz_mfma", i64), ("cond_cols_mfma", i64),
                 ("row_blocks", i32), ("row_blockdim", i32), ("mfma_blocks", i32), ("mfma_blockdim", i32),
-                ("mfma_lds_bytes", i32), ("seg_len", i32), ("scratch_bytes", i64), ("plan_ms", ctypes.c_double)]
+                ("mfma_lds_bytes", i32), ("seg_len", i32), ("scratch_bytes", i64), ("plan_ms", ctypes.c_double),
+                ("n_wide_tasks", i32), ("chunk_lanes", i32), ("row_len", i32), ("wide_len", i32)]
 
     def as_dict(self):
         return {name: getattr(self, name) for name, _ in self._fields_}
@@ -124,11 +125,35 @@ class TcaError(RuntimeError):
         self.status = status
 
 
+def _preload_torch_hip_runtime() -> None:
+    """Makes this process use PyTorch's HIP runtime when PyTorch is installed.
+
+    PyTorch-ROCm ships its own libamdhip64.so (SONAME libamdhip64.so.7) and its
+    libraries NEED it by the unversioned name from their own directory.  If
+    libtcaspmm.so were loaded first, its NEEDED libamdhip64.so.7 would resolve
+    to /opt/rocm/lib and a later `import torch` would load a second HIP
+    runtime into the process; device pointers and streams from torch would
+    then be foreign to this library.  Loading torch's copy first (by path,
+    without importing torch) makes both resolve to one runtime.
+    Set TCA_HIP_RUNTIME=system to skip this.
+    """
+    if os.environ.get("TCA_HIP_RUNTIME", "") == "system":
+        return
+    import importlib.util
+    spec = importlib.util.find_spec("torch")
+    if spec is None or not spec.submodule_search_locations:
+        return
+    path = os.path.join(list(spec.submodule_search_locations)[0], "lib", "libamdhip64.so")
+    if os.path.exists(path):
+        ctypes.CDLL(path, mode=ctypes.RTLD_GLOBAL)
+
+
 def _load() -> ctypes.CDLL:
     if not os.path.exists(LIB_PATH):
         raise ImportError(
             f"libtcaspmm.so not found at {LIB_PATH}; build it first (python -c 'import __graft_entry__ as g; g.build()' "
             "or make -C spmm_amd). There is no CPU fallback.")
+    _preload_torch_hip_runtime()
     lib = ctypes.CDLL(LIB_PATH)
     for name, (res, args) in SIGNATURES.items():
         fn = getattr(lib, name)

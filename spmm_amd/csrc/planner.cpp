@@ -26,30 +26,38 @@ int32_t ilog2(int32_t x) {
 }
 }  // namespace
 
-void plan_geometry(int32_t N, int32_t es, RowPlan* p) {
+void plan_geometry(int32_t N, int32_t es, int32_t slices, RowPlan* p) {
     int32_t e = 16 / es;
     while (e > 1 && N % e != 0) e >>= 1;
     p->elems_per_lane = e;
-    const int64_t lanes = (static_cast<int64_t>(N) + e - 1) / e;
-    if (lanes >= 64) {
-        p->log_lanes = 6;
-        p->col_chunks = static_cast<int32_t>((lanes + 63) / 64);
+    const int64_t lanes = N / e;  // 16-byte (or narrower) vectors across one B row
+    int64_t nch = 1;
+    if (slices > 0) {
+        nch = slices;
     } else {
-        p->log_lanes = ilog2(next_pow2(lanes));
-        p->col_chunks = 1;
+        // Up to 8 chunks (one per XCD), each at least one 128-byte L2 line wide.
+        while (nch < 8 && lanes % (2 * nch) == 0 && (lanes / (2 * nch)) * e * es >= 128) nch *= 2;
     }
+    while ((lanes + nch - 1) / nch > 64) nch *= 2;  // at most 64 lanes per chunk
+    p->col_chunks = static_cast<int32_t>(nch);
+    p->chunk_lanes = static_cast<int32_t>((lanes + nch - 1) / nch);
+    p->log_lanes = ilog2(next_pow2(p->chunk_lanes));
 }
 
 void plan_rows(const int32_t* rowptr, int32_t M, int32_t N, int32_t es, const std::vector<uint8_t>& skip,
-               RowPlan* p) {
-    plan_geometry(N, es, p);
+               int32_t slices, RowPlan* p) {
+    plan_geometry(N, es, slices, p);
     const int32_t slots = 64 >> p->log_lanes;
     const int64_t nnz = rowptr[M];
-    // Segment length: about 1/16384 of the nonzeros (16384 ~ two resident
-    // wavefronts per SIMD on 256 CUs x 4 SIMDs x 8 waves), a power of two
-    // in [512, 8192], and never fewer than 8 loads per slot.
-    p->seg_len = std::min<int64_t>(8192, std::max<int64_t>(512, next_pow2(std::max<int64_t>(nnz / 16384, 1))));
-    p->seg_len = std::max(p->seg_len, slots * kUnroll);
+    // Work per wavefront task: about nnz / 16384 nonzeros (two resident
+    // wavefronts on each of 256 CUs x 4 SIMDs x 8 slots when the matrix is
+    // small, so long rows do not leave a latency tail), a power of two
+    // between 2 and 32 rounds of slots * kUnroll loads.
+    const int64_t round = static_cast<int64_t>(slots) * kUnroll;
+    const int64_t target = std::min<int64_t>(32 * round, std::max<int64_t>(2 * round, next_pow2(std::max<int64_t>(nnz / 16384, 1))));
+    p->row_len = static_cast<int32_t>(target);
+    p->wide_len = static_cast<int32_t>(4 * target);
+    p->seg_len = static_cast<int32_t>(target);
     // Short rows share a wavefront, one slot each, when slots > 1.
     p->multi_max = slots > 1 ? 2 * slots : -1;
 
@@ -64,11 +72,23 @@ void plan_rows(const int32_t* rowptr, int32_t M, int32_t N, int32_t es, const st
     p->tasks.clear();
     p->perm.clear();
     p->longrows.clear();
-    int32_t seg_global = 0;
     size_t i = 0;
-    // Long rows: equal segments of at most seg_len nonzeros.
-    for (; i < rows.size() && len(rows[i]) > p->seg_len; i++) {
+    while (i < rows.size() && len(rows[i]) > p->wide_len) i++;
+    const size_t n_long = i;
+    // Wide rows: four quarters, one per wavefront of a workgroup (4-aligned).
+    for (; i < rows.size() && len(rows[i]) > p->row_len; i++) {
         const int32_t r = rows[i];
+        const int64_t L = len(r);
+        for (int32_t q = 0; q < 4; q++)
+            p->tasks.push_back({r, rowptr[r] + static_cast<int32_t>(L * q / 4),
+                                rowptr[r] + static_cast<int32_t>(L * (q + 1) / 4), kTaskWide | (q << 2)});
+    }
+    p->n_wide = static_cast<int32_t>(p->tasks.size());
+    const size_t first_row = i;
+    // Long rows: equal segments of at most seg_len nonzeros, summed by a second kernel.
+    int32_t seg_global = 0;
+    for (size_t k = 0; k < n_long; k++) {
+        const int32_t r = rows[k];
         const int32_t L = len(r);
         const int32_t nseg = (L + p->seg_len - 1) / p->seg_len;
         const int32_t lid = static_cast<int32_t>(p->longrows.size());
@@ -80,13 +100,13 @@ void plan_rows(const int32_t* rowptr, int32_t M, int32_t N, int32_t es, const st
         }
         seg_global += nseg;
     }
-    p->n_seg = static_cast<int32_t>(p->tasks.size());
+    p->n_seg = static_cast<int32_t>(p->tasks.size()) - p->n_wide;
     // Medium rows: one wavefront each.
-    for (; i < rows.size() && len(rows[i]) > p->multi_max; i++) {
+    for (i = first_row; i < rows.size() && len(rows[i]) > p->multi_max; i++) {
         const int32_t r = rows[i];
         p->tasks.push_back({r, rowptr[r], rowptr[r + 1], kTaskRow});
     }
-    p->n_rowtasks = static_cast<int32_t>(p->tasks.size()) - p->n_seg;
+    p->n_rowtasks = static_cast<int32_t>(p->tasks.size()) - p->n_seg - p->n_wide;
     // Short rows: groups of `slots` rows of similar length.
     const size_t first_multi = p->tasks.size();
     for (; i < rows.size(); i += slots) {
@@ -146,7 +166,7 @@ extern "C" int tca_plan_row_tasks(const int32_t* rowptr, int32_t M, int32_t N, i
     if (!rowptr || M < 0 || N < 1 || !dtype_ok(dtype) || !n_tasks || !n_perm || !n_long)
         return fail(TCA_ERR_INVALID, "tca_plan_row_tasks: bad argument");
     RowPlan p;
-    plan_rows(rowptr, M, N, static_cast<int32_t>(dtype_size(dtype)), {}, &p);
+    plan_rows(rowptr, M, N, static_cast<int32_t>(dtype_size(dtype)), {}, 0, &p);
     if (tasks) {
         if (*n_tasks < static_cast<int32_t>(p.tasks.size()) || *n_perm < static_cast<int32_t>(p.perm.size()) ||
             *n_long < static_cast<int32_t>(p.longrows.size()) || !perm || !longrows)
@@ -163,6 +183,10 @@ extern "C" int tca_plan_row_tasks(const int32_t* rowptr, int32_t M, int32_t N, i
         geometry[1] = 1 << p.log_lanes;
         geometry[2] = p.col_chunks;
         geometry[3] = p.seg_len;
+        geometry[4] = p.chunk_lanes;
+        geometry[5] = p.row_len;
+        geometry[6] = p.wide_len;
+        geometry[7] = p.multi_max;
     }
     return TCA_OK;
 }

@@ -1,4 +1,4 @@
-// row_kernel.hpp -- the wavefront-per-row SpMM kernel for gfx950 (VALU path).
+// row_kernel.hpp -- the wavefront-per-row SpMM kernels for gfx950 (VALU path).
 //
 // One 64-lane wavefront per task.  The lanes form S = 64 / G slots of G
 // lanes; the G lanes of a slot cover one chunk of a B row with 16-byte loads
@@ -9,10 +9,14 @@
 //            xor shuffles (identical order on every run) and written once.
 //   multi -- each slot walks its own short row (rows grouped by length).
 //   seg   -- like row over one segment of a long row; the segment's partial
-//            row goes to plan scratch and the last segment to finish (atomic
-//            ticket) adds all segments in segment order and writes C.
+//            row goes to plan scratch and seg_finalize_kernel, launched next
+//            on the same stream, adds the segments in segment order.
 // Every row of C is written exactly once, so results do not depend on the
 // schedule, and C needs no zeroing.
+//
+// All operand loads are raw buffer loads: a masked lane uses an offset past
+// the buffer's size, which the hardware returns as zeros without a fault, so
+// the loads carry no branches and all eight stay in flight.
 //
 // Functionally replaces reference multirow_per_tb / multitb_per_row
 // (src/our_spmm.cu:24-295), which stage B through shared memory and use one
@@ -42,15 +46,50 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kRowWaves = 4;   // wavefronts per workgroup (independent tasks)
 constexpr int kRowUnroll = 8;  // B loads in flight per lane
+constexpr uint32_t kOob = 0xfffffff0u;  // buffer offset past any buffer this library builds
 
-// Stores E consecutive fp32 values (16-byte stores when E >= 4).
+// Raw buffer resource over `bytes` bytes at `base` (gfx9 word 3: 32-bit data format).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
+}
+
+// E elements of T at byte offset `off` of buffer r (zeros when off is out of range).
+template <typename T, int E>
+__device__ __forceinline__ Pack<T, E> load_pack(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    using P = Pack<T, E>;
+    constexpr int bytes = E * static_cast<int>(sizeof(T));
+    if constexpr (bytes == 16) {
+        return __builtin_bit_cast(P, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+    } else if constexpr (bytes == 8) {
+        return __builtin_bit_cast(P, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
+    } else if constexpr (bytes == 4) {
+        return __builtin_bit_cast(P, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+    } else {
+        return __builtin_bit_cast(P, __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0));
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ float load_val(__amdgpu_buffer_rsrc_t r, uint32_t idx, bool ok) {
+    const uint32_t off = ok ? idx * static_cast<uint32_t>(sizeof(T)) : kOob;
+    if constexpr (sizeof(T) == 4) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+    } else {
+        return to_f32(__builtin_bit_cast(T, __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0)));
+    }
+}
+
+__device__ __forceinline__ int load_idx(__amdgpu_buffer_rsrc_t r, uint32_t idx, bool ok) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, ok ? idx * 4u : kOob, 0, 0);
+}
+
+// Stores E consecutive fp32 values (16-byte stores when E >= 4), streaming.
 template <int E>
 __device__ __forceinline__ void store_row(float* dst, const float (&v)[E]) {
     if constexpr (E >= 4) {
 #pragma unroll
         for (int i = 0; i < E; i += 4)
-            __builtin_nontemporal_store(f32x4{v[i], v[i + 1], v[i + 2], v[i + 3]},
-                                        reinterpret_cast<f32x4*>(dst + i));
+            __builtin_nontemporal_store(f32x4{v[i], v[i + 1], v[i + 2], v[i + 3]}, reinterpret_cast<f32x4*>(dst + i));
     } else if constexpr (E == 2) {
         __builtin_nontemporal_store(f32x2{v[0], v[1]}, reinterpret_cast<f32x2*>(dst));
     } else {
@@ -64,22 +103,38 @@ __device__ __forceinline__ void fma_pack(float (&acc)[E], float a, const Pack<T,
     for (int e = 0; e < E; e++) acc[e] = __builtin_fmaf(a, to_f32(b.v[e]), acc[e]);
 }
 
+struct RowArgs {
+    const int4* tasks;
+    int ntasks;
+    const int* rowptr;
+    const int* perm;
+    float* partials;
+    float* C;
+    int N;
+    int logG;         // log2 of lanes per slot
+    int chunk_lanes;  // lanes per slot that hold data
+    int col_chunks;   // blockIdx.x = task group * col_chunks + chunk
+    const void* colidx;  // buffer bases and sizes in bytes
+    const void* val;
+    const void* B;
+    uint32_t colidx_bytes, val_bytes, B_bytes;
+};
+
 // Slots split the nonzeros [beg, end) of one row; lane (slot, g) accumulates
-// columns [col, col + E).  Column indices and values are fetched 64 at a time
-// with one coalesced load and handed to the slots with ds_bpermute (or
+// columns [col, col + E).  Column indices and values are fetched 64 at a
+// time with one coalesced load and handed to the slots with ds_bpermute (or
 // v_readlane when one slot spans the whole wavefront).
 template <typename T, int E, bool kOneSlot>
-__device__ __forceinline__ void accumulate_span(float (&acc)[E], int beg, int end, const int* __restrict__ colidx,
-                                                const T* __restrict__ val, const T* __restrict__ B, int N, int col,
-                                                bool colok, int lane, int slot, int logS) {
+__device__ __forceinline__ void accumulate_span(float (&acc)[E], int beg, int end, const RowArgs& a,
+                                                __amdgpu_buffer_rsrc_t rcol, __amdgpu_buffer_rsrc_t rval,
+                                                __amdgpu_buffer_rsrc_t rB, int col, bool colok, int lane, int slot,
+                                                int logS) {
+    const uint32_t rowbytes = static_cast<uint32_t>(a.N) * sizeof(T);
+    const uint32_t colbytes = static_cast<uint32_t>(col) * sizeof(T);
     for (int base = beg; base < end; base += 64) {
         const int n = min(64, end - base);
-        int myc = 0;
-        float mya = 0.f;
-        if (lane < n) {
-            myc = __builtin_nontemporal_load(colidx + base + lane);
-            mya = to_f32(val[base + lane]);
-        }
+        const int myc = load_idx(rcol, base + lane, lane < n);
+        const float mya = load_val<T>(rval, base + lane, lane < n);
         const int rounds = (n + (1 << logS) - 1) >> logS;
         for (int r = 0; r < rounds; r += kRowUnroll) {
             Pack<T, E> bv[kRowUnroll];
@@ -87,25 +142,19 @@ __device__ __forceinline__ void accumulate_span(float (&acc)[E], int beg, int en
 #pragma unroll
             for (int u = 0; u < kRowUnroll; u++) {
                 int c;
-                float a;
                 bool ok;
                 if constexpr (kOneSlot) {
                     const int idx = r + u;  // wave-uniform
                     c = __builtin_amdgcn_readlane(myc, idx & 63);
-                    a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mya), idx & 63));
+                    av[u] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mya), idx & 63));
                     ok = idx < n && colok;
                 } else {
                     const int idx = ((r + u) << logS) + slot;
                     c = __shfl(myc, idx & 63);
-                    a = __shfl(mya, idx & 63);
+                    av[u] = __shfl(mya, idx & 63);
                     ok = idx < n && colok;
                 }
-                av[u] = ok ? a : 0.f;
-                if (ok)
-                    bv[u] = *reinterpret_cast<const Pack<T, E>*>(B + static_cast<size_t>(c) * N + col);
-                else
-#pragma unroll
-                    for (int e = 0; e < E; e++) bv[u].v[e] = T{};
+                bv[u] = load_pack<T, E>(rB, ok ? static_cast<uint32_t>(c) * rowbytes + colbytes : kOob);
             }
 #pragma unroll
             for (int u = 0; u < kRowUnroll; u++) fma_pack<T, E>(acc, av[u], bv[u]);
@@ -114,20 +163,25 @@ __device__ __forceinline__ void accumulate_span(float (&acc)[E], int beg, int en
 }
 
 template <typename T, int E>
-__global__ __launch_bounds__(256) void row_kernel(const int4* __restrict__ tasks, int ntasks,
-                                                  const int* __restrict__ rowptr, const int* __restrict__ colidx,
-                                                  const T* __restrict__ val, const T* __restrict__ B,
-                                                  float* __restrict__ C, int N, int logG,
-                                                  const int* __restrict__ perm, const int4* __restrict__ longrows,
-                                                  float* __restrict__ partials, int* __restrict__ tickets) {
+__global__ __launch_bounds__(256) void row_kernel(RowArgs a) {
+    __shared__ float red[kRowWaves][64 * E];  // wide rows: one partial row chunk per wavefront
     const int lane = threadIdx.x & 63;
-    const int tid = blockIdx.x * kRowWaves + (threadIdx.x >> 6);
-    if (tid >= ntasks) return;
-    const int logS = 6 - logG;
-    const int slot = lane >> logG;
-    const int col = blockIdx.y * (64 * E) + (lane & ((1 << logG) - 1)) * E;
-    const bool colok = col < N;
-    const int4 t = tasks[tid];
+    const int wave = threadIdx.x >> 6;
+    // Consecutive workgroups take consecutive column chunks: the hardware
+    // deals workgroups to the 8 XCDs round robin, so with 8 (or 4, 2) chunks
+    // every XCD reads one fixed slice of B and keeps it in its own L2.
+    const int chunk = blockIdx.x % a.col_chunks;
+    const int tid = (blockIdx.x / a.col_chunks) * kRowWaves + wave;
+    if (tid >= a.ntasks) return;
+    const __amdgpu_buffer_rsrc_t rcol = make_rsrc(a.colidx, a.colidx_bytes);
+    const __amdgpu_buffer_rsrc_t rval = make_rsrc(a.val, a.val_bytes);
+    const __amdgpu_buffer_rsrc_t rB = make_rsrc(a.B, a.B_bytes);
+    const int logS = 6 - a.logG;
+    const int slot = lane >> a.logG;
+    const int g = lane & ((1 << a.logG) - 1);
+    const int col = (chunk * a.chunk_lanes + g) * E;
+    const bool colok = g < a.chunk_lanes && col < a.N;
+    const int4 t = a.tasks[tid];
     float acc[E];
 #pragma unroll
     for (int e = 0; e < E; e++) acc[e] = 0.f;
@@ -135,75 +189,92 @@ __global__ __launch_bounds__(256) void row_kernel(const int4* __restrict__ tasks
     if (t.w == 1) {  // multi: slot s walks row perm[t.x + s]
         int row = -1, beg = 0, len = 0;
         if (slot < t.y) {
-            row = perm[t.x + slot];
-            beg = rowptr[row];
-            len = rowptr[row + 1] - beg;
+            row = a.perm[t.x + slot];
+            beg = a.rowptr[row];
+            len = a.rowptr[row + 1] - beg;
         }
+        const uint32_t rowbytes = static_cast<uint32_t>(a.N) * sizeof(T);
+        const uint32_t colbytes = static_cast<uint32_t>(col) * sizeof(T);
         for (int j = 0; j < t.z; j += kRowUnroll) {
             Pack<T, E> bv[kRowUnroll];
             float av[kRowUnroll];
+            int c[kRowUnroll];
 #pragma unroll
             for (int u = 0; u < kRowUnroll; u++) {
-                const bool ok = j + u < len && colok;
-                av[u] = 0.f;
-#pragma unroll
-                for (int e = 0; e < E; e++) bv[u].v[e] = T{};
-                if (ok) {
-                    const int c = colidx[beg + j + u];
-                    av[u] = to_f32(val[beg + j + u]);
-                    bv[u] = *reinterpret_cast<const Pack<T, E>*>(B + static_cast<size_t>(c) * N + col);
-                }
+                c[u] = load_idx(rcol, beg + j + u, j + u < len);
+                av[u] = load_val<T>(rval, beg + j + u, j + u < len);
             }
+#pragma unroll
+            for (int u = 0; u < kRowUnroll; u++)
+                bv[u] = load_pack<T, E>(rB, j + u < len && colok ? static_cast<uint32_t>(c[u]) * rowbytes + colbytes
+                                                                 : kOob);
 #pragma unroll
             for (int u = 0; u < kRowUnroll; u++) fma_pack<T, E>(acc, av[u], bv[u]);
         }
-        if (row >= 0 && colok) store_row<E>(C + static_cast<size_t>(row) * N + col, acc);
+        if (row >= 0 && colok) store_row<E>(a.C + static_cast<size_t>(row) * a.N + col, acc);
         return;
     }
 
     // row / seg: all slots on one span
-    if (logG == 6)
-        accumulate_span<T, E, true>(acc, t.y, t.z, colidx, val, B, N, col, colok, lane, slot, logS);
+    if (a.logG == 6)
+        accumulate_span<T, E, true>(acc, t.y, t.z, a, rcol, rval, rB, col, colok, lane, slot, logS);
     else
-        accumulate_span<T, E, false>(acc, t.y, t.z, colidx, val, B, N, col, colok, lane, slot, logS);
-    for (int off = 1 << logG; off < 64; off <<= 1)
+        accumulate_span<T, E, false>(acc, t.y, t.z, a, rcol, rval, rB, col, colok, lane, slot, logS);
+    for (int off = 1 << a.logG; off < 64; off <<= 1)
 #pragma unroll
         for (int e = 0; e < E; e++) acc[e] += __shfl_xor(acc[e], off);
-
-    if (t.w == 0) {
-        if (slot == 0 && colok) store_row<E>(C + static_cast<size_t>(t.x) * N + col, acc);
+    if ((t.w & 3) == 3) {
+        // wide row: the four quarters meet in LDS and wavefront 0 adds them in
+        // quarter order.  Every wavefront of this workgroup holds a quarter of
+        // the same row (the plan places wide groups 4-aligned), so all four
+        // reach the barrier.
+        if (slot == 0)
+#pragma unroll
+            for (int e = 0; e < E; e++) red[wave][g * E + e] = acc[e];
+        __syncthreads();
+        if (wave != 0 || slot != 0 || !colok) return;
+#pragma unroll
+        for (int e = 0; e < E; e++)
+            acc[e] = ((red[0][g * E + e] + red[1][g * E + e]) + red[2][g * E + e]) + red[3][g * E + e];
+        store_row<E>(a.C + static_cast<size_t>(t.x) * a.N + col, acc);
         return;
     }
+    if (slot != 0 || !colok) return;
+    if (t.w == 0)
+        store_row<E>(a.C + static_cast<size_t>(t.x) * a.N + col, acc);
+    else  // seg: partial row of segment slot t.w >> 2
+        store_row<E>(a.partials + static_cast<size_t>(t.w >> 2) * a.N + col, acc);
+}
 
-    // seg: publish this segment, take a ticket; the last one sums in order.
-    const int seg = t.w >> 2;
-    const int4 lr = longrows[t.x];  // {row, first segment, segments, 0}
-    if (slot == 0 && colok) {
-        float* dst = partials + static_cast<size_t>(seg) * N + col;
+// C[row, :] = sum over the row's segments, in segment order.  One wavefront
+// per (long row, chunk of 256 columns).
+__global__ __launch_bounds__(64) void seg_finalize_kernel(const int4* __restrict__ longrows,
+                                                          const float* __restrict__ partials, float* __restrict__ C,
+                                                          int N) {
+    const int4 lr = longrows[blockIdx.x];  // {row, first segment, segments, 0}
+    const int col = (blockIdx.y * 64 + threadIdx.x) * 4;
+    if (col >= N) return;
+    if ((N & 3) == 0) {  // rows 16-byte aligned
+        f32x4 s = {0.f, 0.f, 0.f, 0.f};
+        const f32x4* src = reinterpret_cast<const f32x4*>(partials + static_cast<size_t>(lr.y) * N + col);
+        const size_t stride = static_cast<size_t>(N) / 4;
+        int k = 0;
+        for (; k + 8 <= lr.z; k += 8) {  // eight loads in flight, added in segment order
+            f32x4 v[8];
 #pragma unroll
-        for (int e = 0; e < E; e++) dst[e] = acc[e];
-    }
-    __threadfence();
-    int* ticket = tickets + static_cast<size_t>(t.x) * gridDim.y + blockIdx.y;
-    int prev = 0;
-    if (lane == 0) prev = atomicAdd(ticket, 1);
-    prev = __shfl(prev, 0);
-    if (prev != lr.z - 1) return;
-    __threadfence();
-    // Slot s adds segments s, s + S, ...; then the slots are combined as above.
+            for (int u = 0; u < 8; u++) v[u] = src[(k + u) * stride];
 #pragma unroll
-    for (int e = 0; e < E; e++) acc[e] = 0.f;
-    if (colok)
-        for (int s = slot; s < lr.z; s += (1 << logS)) {
-            const float* src = partials + static_cast<size_t>(lr.y + s) * N + col;
-#pragma unroll
-            for (int e = 0; e < E; e++) acc[e] += src[e];
+            for (int u = 0; u < 8; u++) s += v[u];
         }
-    for (int off = 1 << logG; off < 64; off <<= 1)
-#pragma unroll
-        for (int e = 0; e < E; e++) acc[e] += __shfl_xor(acc[e], off);
-    if (slot == 0 && colok) store_row<E>(C + static_cast<size_t>(lr.x) * N + col, acc);
-    if (lane == 0) *ticket = 0;  // ready for the next launch
+        for (; k < lr.z; k++) s += src[k * stride];
+        *reinterpret_cast<f32x4*>(C + static_cast<size_t>(lr.x) * N + col) = s;
+    } else {
+        for (int c = col; c < N; c++) {
+            float s = 0.f;
+            for (int k = 0; k < lr.z; k++) s += partials[static_cast<size_t>(lr.y + k) * N + c];
+            C[static_cast<size_t>(lr.x) * N + c] = s;
+        }
+    }
 }
 
 }  // namespace tca

@@ -33,7 +33,6 @@ struct tca_spmm_plan {
     int* d_perm = nullptr;
     int4* d_longrows = nullptr;
     float* d_partials = nullptr;
-    int* d_tickets = nullptr;
     tca_plan_info info{};
 };
 
@@ -62,15 +61,34 @@ void free_plan_device(tca_spmm_plan* p) {
     (void)hipFree(p->d_perm);
     (void)hipFree(p->d_longrows);
     (void)hipFree(p->d_partials);
-    (void)hipFree(p->d_tickets);
 }
 
 template <typename T, int E>
 void launch_rows_t(const tca_spmm_plan* p, const void* val, const void* B, float* C, hipStream_t s) {
-    const dim3 grid((p->ntasks + kRowWaves - 1) / kRowWaves, p->rows.col_chunks);
-    hipLaunchKernelGGL((row_kernel<T, E>), grid, dim3(64 * kRowWaves), 0, s, p->d_tasks, p->ntasks, p->d_rowptr,
-                       p->d_colidx, static_cast<const T*>(val), static_cast<const T*>(B), C, p->N,
-                       p->rows.log_lanes, p->d_perm, p->d_longrows, p->d_partials, p->d_tickets);
+    RowArgs a;
+    a.tasks = p->d_tasks;
+    a.ntasks = p->ntasks;
+    a.rowptr = p->d_rowptr;
+    a.perm = p->d_perm;
+    a.partials = p->d_partials;
+    a.C = C;
+    a.N = p->N;
+    a.logG = p->rows.log_lanes;
+    a.chunk_lanes = p->rows.chunk_lanes;
+    a.col_chunks = p->rows.col_chunks;
+    a.colidx = p->d_colidx;
+    a.val = val;
+    a.B = B;
+    // Byte sizes of the buffer ranges (checked < 2^32 - 16 at plan time).
+    a.colidx_bytes = static_cast<uint32_t>(static_cast<uint64_t>(p->nnz) * 4);
+    a.val_bytes = static_cast<uint32_t>(static_cast<uint64_t>(p->nnz) * sizeof(T));
+    a.B_bytes = static_cast<uint32_t>(static_cast<uint64_t>(p->K) * p->N * sizeof(T));
+    const dim3 grid(((p->ntasks + kRowWaves - 1) / kRowWaves) * p->rows.col_chunks);
+    hipLaunchKernelGGL((row_kernel<T, E>), grid, dim3(64 * kRowWaves), 0, s, a);
+    if (!p->rows.longrows.empty()) {
+        const dim3 fgrid(static_cast<unsigned>(p->rows.longrows.size()), (p->N + 255) / 256);
+        hipLaunchKernelGGL(seg_finalize_kernel, fgrid, dim3(64), 0, s, p->d_longrows, p->d_partials, C, p->N);
+    }
 }
 
 template <typename T>
@@ -121,8 +139,12 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
     *plan = nullptr;
     if (M < 0 || K < 1 || N < 1 || nnz < 0) return fail(TCA_ERR_INVALID, "bad shape M=%d K=%d N=%d nnz=%d", M, K, N, nnz);
     if (!dtype_ok(dtype)) return fail(TCA_ERR_INVALID, "unknown dtype %d", dtype);
-    if (static_cast<int64_t>(N) * static_cast<int64_t>(dtype_size(dtype)) > (int64_t(1) << 30))
-        return fail(TCA_ERR_UNSUPPORTED, "N = %d too wide", N);
+    // The kernels address B, values and column indices through 32-bit buffer
+    // offsets, with 0xfffffff0 reserved as the out-of-range marker.
+    const uint64_t b_bytes = static_cast<uint64_t>(K) * static_cast<uint64_t>(N) * dtype_size(dtype);
+    if (b_bytes >= 0xfffffff0ull || static_cast<uint64_t>(nnz) * 4 >= 0xfffffff0ull)
+        return fail(TCA_ERR_UNSUPPORTED, "B (%llu bytes) or the nonzeros exceed the 4 GiB buffer range",
+                    (unsigned long long)b_bytes);
     int st = tca_csr_validate(rowptr, colidx, M, K, nnz);
     if (st) return st;
     const auto t0 = std::chrono::steady_clock::now();
@@ -138,7 +160,9 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
         delete p;
         return fail(TCA_ERR_HIP, "no HIP device");
     }
-    plan_rows(rowptr, M, N, static_cast<int32_t>(dtype_size(dtype)), {}, &p->rows);
+    // TCA_SLICES (tuning only) forces the number of column chunks.
+    const char* sl = std::getenv("TCA_SLICES");
+    plan_rows(rowptr, M, N, static_cast<int32_t>(dtype_size(dtype)), {}, sl ? std::atoi(sl) : 0, &p->rows);
     p->ntasks = static_cast<int32_t>(p->rows.tasks.size());
     const size_t n_seg_total =
         p->rows.longrows.empty() ? 0 : static_cast<size_t>(p->rows.longrows.back().y + p->rows.longrows.back().z);
@@ -155,10 +179,6 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
     if ((st = dev_upload(&p->d_perm, p->rows.perm.data(), p->rows.perm.size()))) return bail(st);
     if ((st = dev_upload(&p->d_longrows, p->rows.longrows.data(), p->rows.longrows.size()))) return bail(st);
     if ((st = dev_upload(&p->d_partials, nullptr, n_seg_total * N))) return bail(st);
-    const size_t n_tickets = p->rows.longrows.size() * p->rows.col_chunks;
-    if ((st = dev_upload(&p->d_tickets, nullptr, n_tickets))) return bail(st);
-    if (n_tickets && hipMemset(p->d_tickets, 0, sizeof(int) * n_tickets) != hipSuccess)
-        return bail(fail(TCA_ERR_HIP, "hipMemset of tickets failed"));
     if (hipDeviceSynchronize() != hipSuccess) return bail(fail(TCA_ERR_HIP, "hipDeviceSynchronize failed"));
 
     tca_plan_info& in = p->info;
@@ -174,10 +194,14 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
     in.n_multi_tasks = p->rows.n_multi;
     in.n_seg_tasks = p->rows.n_seg;
     in.n_long_rows = static_cast<int32_t>(p->rows.longrows.size());
-    in.row_blocks = (p->ntasks + kRowWaves - 1) / kRowWaves;
+    in.n_wide_tasks = p->rows.n_wide;
+    in.chunk_lanes = p->rows.chunk_lanes;
+    in.row_len = p->rows.row_len;
+    in.wide_len = p->rows.wide_len;
+    in.row_blocks = ((p->ntasks + kRowWaves - 1) / kRowWaves) * p->rows.col_chunks;
     in.row_blockdim = 64 * kRowWaves;
     in.seg_len = p->rows.seg_len;
-    in.scratch_bytes = static_cast<int64_t>(n_seg_total * N * sizeof(float) + n_tickets * sizeof(int));
+    in.scratch_bytes = static_cast<int64_t>(n_seg_total * N * sizeof(float));
     in.plan_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
     *plan = p;
     return TCA_OK;

@@ -1,11 +1,16 @@
 """GPU parity: the gfx950 kernels (through the C ABI) against the CPU oracle
 and the committed golden fixtures.
 
-Bars: bit-exact where the arithmetic is exact (values in {+-1,+-1/2,+-2},
-B in {k/256}, rows short enough that every partial sum is exact in fp32 in
-any order), and the reference verdict (compare_mat, tol 1e-3) plus a max
-relative error <= 1e-3 with an absolute floor elsewhere (fp32 accumulation
-in a different order than the oracle's)."""
+Bars:
+* bit-exact where the arithmetic is exact (values in {+-1,+-1/2,+-2}, B in
+  {k/256}, rows short enough that every partial sum is exact in fp32 in any
+  order): GPU == fp32 oracle bit for bit;
+* elsewhere (fp32 accumulation in another order than the oracle's), against
+  the fp64-accumulated oracle G: the reference verdict compare_mat(G, C,
+  1e-3) must pass, and the relative error |C - G| / max(|G|, 1e-3 * S) must
+  be <= 1e-3 for every element, where S = sum_j |a_j * b_j| of that element
+  (the floor makes outputs that cancel to ~0 compare on the scale of their
+  terms; any wrong or missing term of ordinary size still fails it)."""
 import os
 
 import numpy as np
@@ -50,10 +55,29 @@ def oracle_c(a: S.CSR, b: np.ndarray):
 
 
 def assert_close(gold, got, what=""):
+    """Small-row cases: reference verdict and relative error with an absolute floor."""
     v = S.compare_mat(gold, got, TOL, FLOOR)
     assert v["success"], (what, v)
     assert v["max_rel_floor"] <= TOL, (what, v)
     assert np.all(np.isfinite(got)), what
+
+
+def assert_parity(a: S.CSR, b: np.ndarray, got: np.ndarray, what=""):
+    """GPU result against the fp64-accumulated oracle (see module docstring)."""
+    vals = a.values_f32().astype(np.float64)
+    bf = S.from_storage(b, a.dtype).astype(np.float64)
+    g64 = oracle.csr_spmm_f64(a.rowptr, a.colidx, vals, bf)
+    s64 = oracle.csr_spmm_f64(a.rowptr, a.colidx, np.abs(vals), np.abs(bf))
+    assert np.all(np.isfinite(got)), what
+    v = S.compare_mat(g64.astype(np.float32), got, TOL)
+    assert v["success"], (what, v)
+    zero = s64 == 0
+    assert np.all(got[zero] == 0.0), what
+    rel = np.abs(got.astype(np.float64) - g64)[~zero] / np.maximum(np.abs(g64), 1e-3 * s64)[~zero]
+    worst = float(rel.max()) if rel.size else 0.0
+    print(f"{what}: max rel err {worst:.3e} (bar {TOL})", flush=True)
+    assert worst <= TOL, (what, worst)
+    return worst
 
 
 def make_csr(rng, lens, k, dtype, values="exact"):
@@ -79,7 +103,7 @@ def test_golden_scipy_fixtures(torch_cuda):
         got = run_gpu(torch_cuda, a, b)
         print(nm, a.nrow, b.shape, flush=True)
         assert_close(c.astype(np.float32), got, nm)
-        assert_close(oracle_c(a, b), got, nm)
+        assert_parity(a, b, got, nm)
 
 
 def test_fixture_smtx_reference_flow(torch_cuda):
@@ -88,7 +112,7 @@ def test_fixture_smtx_reference_flow(torch_cuda):
     for n in (64, 128, 256, 512):
         b = S.gen_dense(a.ncol, n, 3, seed=n, dtype=S.TCA_F16, sparsity=0.1)
         got = run_gpu(torch_cuda, a, b)
-        assert_close(oracle_c(a, b), got, f"fixture N={n}")
+        assert_parity(a, b, got, f"fixture N={n}")
         empty = np.diff(a.rowptr) == 0
         assert np.all(got[empty] == 0.0)
 
@@ -140,7 +164,7 @@ def test_plan_reuse_and_determinism(torch_cuda):
         for seed in (1, 2, 1):
             b = S.gen_dense(a.ncol, n, 0, seed=seed, dtype=S.TCA_F16)
             got = run_gpu(torch_cuda, a, b, plan=p)
-            assert_close(oracle_c(a, b), got, f"seed {seed}")
+            assert_parity(a, b, got, f"seed {seed}")
             outs.append(got)
         assert np.array_equal(outs[0], outs[2])
         assert not np.array_equal(outs[0], outs[1])
@@ -194,7 +218,7 @@ def test_host_driver_our_spmm_balanced(torch_cuda):
     b = S.gen_dense(a.ncol, 256, 3, seed=7, dtype=S.TCA_F16, sparsity=0.1)
     c, ms = S.our_spmm_balanced(a, b, n_iter=10)
     assert ms > 0
-    assert_close(oracle_c(a, b), c, "host driver")
+    assert_parity(a, b, c, "host driver")
 
 
 # ------------------------------------------------------------- configs
@@ -205,7 +229,8 @@ def test_config_full_size_small(torch_cuda, cfg):
     b = S.gen_dense(a.ncol, n, dist, seed=100 + cfg, dtype=a.dtype)
     print(f"config {cfg}: M={a.nrow} K={a.ncol} N={n} nnz={a.nnz}", flush=True)
     got = run_gpu(torch_cuda, a, b)
-    assert_close(oracle_c(a, b), got, f"config {cfg}")
+    assert_close(oracle_c(a, b), got, f"config {cfg} vs fp32 oracle")
+    assert_parity(a, b, got, f"config {cfg}")
 
 
 @pytest.mark.parametrize("cfg", [2, 3, 4])
@@ -215,9 +240,11 @@ def test_config_full_size_large(torch_cuda, cfg):
     b = S.gen_dense(a.ncol, n, dist, seed=100 + cfg, dtype=a.dtype)
     print(f"config {cfg}: M={a.nrow} K={a.ncol} N={n} nnz={a.nnz}", flush=True)
     got = run_gpu(torch_cuda, a, b)
-    gold = oracle_c(a, b)
-    assert_close(gold, got, f"config {cfg}")
-    # size-independent check: checksum of row sums through the fp64 oracle
+    assert_parity(a, b, got, f"config {cfg}")
+    # size-independent check: row sums of C equal A times the row sums of B
     row_sum_gold = oracle.csr_spmm_f64(a.rowptr, a.colidx, a.values_f32().astype(np.float64),
                                        S.from_storage(b, a.dtype).astype(np.float64).sum(1, keepdims=True))
-    np.testing.assert_allclose(got.astype(np.float64).sum(1), row_sum_gold[:, 0], rtol=1e-3, atol=1e-2)
+    s_abs = oracle.csr_spmm_f64(a.rowptr, a.colidx, np.abs(a.values_f32().astype(np.float64)),
+                                np.abs(S.from_storage(b, a.dtype).astype(np.float64)).sum(1, keepdims=True))
+    err = np.abs(got.astype(np.float64).sum(1) - row_sum_gold[:, 0])
+    assert np.all(err <= 1e-3 * np.maximum(np.abs(row_sum_gold[:, 0]), 1e-3 * s_abs[:, 0]) + 1e-30)

@@ -234,34 +234,42 @@ def test_plan_covers_every_row_once(n, dtype):
     np.cumsum(lens, out=rowptr[1:])
     a = S.CSR(len(lens), 1, rowptr, np.zeros(rowptr[-1], np.int32), np.zeros(rowptr[-1], np.float32), S.TCA_F32)
     tasks, perm, longrows, geo = S.plan_row_tasks(a, n, dtype)
-    e, g = geo["elems_per_lane"], geo["lanes_per_row"]
+    e, g, cl, nch = geo["elems_per_lane"], geo["lanes_per_row"], geo["chunk_lanes"], geo["col_chunks"]
     es = 4 if dtype == S.TCA_F32 else 2
     assert e * es <= 16 and n % e == 0 and g in (1, 2, 4, 8, 16, 32, 64)
-    assert geo["col_chunks"] * 64 * e >= n and g * e >= min(n, 64 * e)
+    assert cl <= g < 2 * cl and nch * cl * e >= n and (nch - 1) * cl * e < n
+    if nch > 1:
+        assert cl * e * es >= 128 or nch * cl > 64 * (nch // 2)  # chunks span whole L2 lines
     covered = np.zeros(len(lens), np.int64)
-    seg_nnz = {}
-    for x, y, z, w in tasks:
+    parts = {}
+    for i, (x, y, z, w) in enumerate(tasks):
         if w == 0:
-            assert (y, z) == (rowptr[x], rowptr[x + 1])
+            assert (y, z) == (rowptr[x], rowptr[x + 1]) and z - y <= geo["row_len"]
             covered[x] += 1
         elif w == 1:
             assert 1 <= y <= 64 // g
             rows = perm[x:x + y]
-            assert z == lens[rows].max()
+            assert z == lens[rows].max() and z <= geo["multi_max"]
             covered[rows] += 1
-        else:
-            assert w & 3 == 2
+        elif w & 3 == 2:
             row, first, nseg, _ = longrows[x]
             assert first <= (w >> 2) < first + nseg
-            seg_nnz.setdefault(row, []).append((y, z))
-    for row, segs in seg_nnz.items():
+            assert lens[row] > geo["wide_len"]
+            parts.setdefault(("seg", row), []).append((y, z))
+        else:
+            assert w & 3 == 3 and i % 4 == (w >> 2)  # quarters are 4-aligned, in order
+            assert geo["row_len"] < lens[x] <= geo["wide_len"]
+            parts.setdefault(("wide", x), []).append((y, z))
+    for (kind, row), segs in parts.items():
         segs.sort()
         assert segs[0][0] == rowptr[row] and segs[-1][1] == rowptr[row + 1]
         assert all(segs[i][1] == segs[i + 1][0] for i in range(len(segs) - 1))
-        assert max(z - y for y, z in segs) <= geo["seg_len"]
+        if kind == "seg":
+            assert max(z - y for y, z in segs) <= geo["seg_len"]
+        else:
+            assert len(segs) == 4
         covered[row] += 1
     assert np.all(covered == 1)
-    # longest first
-    work = [z - y if w != 1 else z for x, y, z, w in tasks]
+    # wide groups first, then segments, rows and multi groups
     kinds = [w & 3 for *_, w in tasks]
-    assert kinds == sorted(kinds, key=lambda k: {2: 0, 0: 1, 1: 2}[k])
+    assert kinds == sorted(kinds, key=lambda k: {3: 0, 2: 1, 0: 2, 1: 3}[k])
