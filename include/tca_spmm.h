@@ -49,7 +49,7 @@ typedef enum tca_status {
 /* Plan flags. */
 #define TCA_PLAN_DEFAULT 0u
 #define TCA_PLAN_NO_MFMA 1u    /* route every row to the wavefront-per-row kernel */
-#define TCA_PLAN_FORCE_MFMA 2u /* route every 16-row window to the MFMA tile kernel (fp16/bf16 only) */
+#define TCA_PLAN_FORCE_MFMA 2u /* route every eligible 64-row window to the MFMA tile kernel (fp16/bf16, N % 8 == 0) */
 
 typedef struct tca_spmm_plan tca_spmm_plan;
 
@@ -146,6 +146,20 @@ int tca_condense_windows(const int32_t* rowptr, const int32_t* colidx, int32_t M
 int tca_plan_row_tasks(const int32_t* rowptr, int32_t M, int32_t N, int32_t dtype, int32_t* n_tasks,
                        int32_t* n_perm, int32_t* n_long, int32_t* tasks, int32_t* perm, int32_t* longrows,
                        int32_t* geometry);
+
+/* ---- host-only view of the MFMA window plan (no device needed) ----
+ * The 64-row windows tca_spmm_plan_create routes to the MFMA tile kernel for
+ * this structure, width N, dtype and flags.  Call with windows == NULL to get
+ * the counts, then with windows[4*n_windows], ucols[32*n_steps],
+ * eoff[n_steps+1] and entries[n_entries].  windows[i] = {first row, steps,
+ * first global step, first nonzero}; global step g gathers B rows
+ * ucols[32g .. 32g+31] (-1 = padding) and holds entries eoff[g] ..
+ * eoff[g+1]-1, each packing the row within the window (bits 0-5), the
+ * column within the step (bits 6-10) and the nonzero index minus the
+ * window's first nonzero (bits 11-31). */
+int tca_plan_mfma_windows(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_t N, int32_t dtype,
+                          uint32_t flags, int32_t* n_windows, int32_t* n_steps, int64_t* n_entries,
+                          int32_t* windows, int32_t* ucols, int32_t* eoff, uint32_t* entries);
 
 /* ---- library information ---- */
 const char* tca_status_string(int status);

@@ -26,7 +26,7 @@ from ._lib import (TCA_BF16, TCA_F16, TCA_F32, TCA_PLAN_DEFAULT, TCA_PLAN_FORCE_
 __all__ = ["CSR", "Plan", "TcaError", "TCA_F16", "TCA_F32", "TCA_BF16", "TCA_PLAN_DEFAULT", "TCA_PLAN_NO_MFMA",
            "TCA_PLAN_FORCE_MFMA", "read_smtx", "read_smtx_dense", "write_smtx", "read_mtx", "dense_to_csr",
            "csr_to_dense", "compare_mat", "gen_config", "gen_dense", "gen_bernoulli", "gen_lognormal_rows",
-           "gen_rmat", "gen_zipf_rows", "naive_csr_spmm", "plan_row_tasks", "our_spmm_balanced", "condense_windows", "np_dtype",
+           "gen_rmat", "gen_zipf_rows", "naive_csr_spmm", "plan_row_tasks", "plan_mfma_windows", "our_spmm_balanced", "condense_windows", "np_dtype",
            "to_storage", "from_storage"]
 
 # numpy storage type of each value type (fp16/bf16 are kept as 16-bit patterns)
@@ -207,6 +207,24 @@ def plan_row_tasks(a: CSR, n: int, dtype: int = None):
     keys = ("elems_per_lane", "lanes_per_row", "col_chunks", "seg_len", "chunk_lanes", "row_len", "wide_len",
             "multi_max")
     return tasks, perm[:npm.value], longrows[:nl.value], {k: int(v) for k, v in zip(keys, geo)}
+
+
+def plan_mfma_windows(a: CSR, n: int, dtype: int = None, flags: int = TCA_PLAN_DEFAULT):
+    """Host-only MFMA window plan: (windows int32[W,4], ucols int32[S*32], eoff int32[S+1], entries uint32)."""
+    dtype = a.dtype if dtype is None else dtype
+    rp = np.ascontiguousarray(a.rowptr, np.int32)
+    ci = np.ascontiguousarray(a.colidx, np.int32)
+    nw, ns, ne = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int64()
+    call("tca_plan_mfma_windows", np_ptr(rp, ctypes.c_int32), np_ptr(ci, ctypes.c_int32), a.nrow, n, dtype, flags,
+         ctypes.byref(nw), ctypes.byref(ns), ctypes.byref(ne), None, None, None, None)
+    windows = np.zeros((max(nw.value, 1), 4), np.int32)
+    ucols = np.zeros(max(ns.value * 32, 1), np.int32)
+    eoff = np.zeros(ns.value + 1, np.int32)
+    entries = np.zeros(max(ne.value, 1), np.uint32)
+    call("tca_plan_mfma_windows", np_ptr(rp, ctypes.c_int32), np_ptr(ci, ctypes.c_int32), a.nrow, n, dtype, flags,
+         ctypes.byref(nw), ctypes.byref(ns), ctypes.byref(ne), np_ptr(windows, ctypes.c_int32),
+         np_ptr(ucols, ctypes.c_int32), np_ptr(eoff, ctypes.c_int32), np_ptr(entries, ctypes.c_uint32))
+    return windows[:nw.value], ucols[:ns.value * 32], eoff, entries[:ne.value]
 
 
 # ----------------------------------------------------------- generators

@@ -77,6 +77,8 @@ SIGNATURES = {
                             ctypes.POINTER(ctypes.c_double)]),
     "tca_condense_windows": (i32, [i32p, i32p, i32, i32, i32, i64p, i32p, i32p]),
     "tca_plan_row_tasks": (i32, [i32p, i32, i32, i32, i32p, i32p, i32p, i32p, i32p, i32p, i32p]),
+    "tca_plan_mfma_windows": (i32, [i32p, i32p, i32, i32, i32, u32, i32p, i32p, i64p, i32p, i32p, i32p,
+                                    ctypes.POINTER(ctypes.c_uint32)]),
     "tca_status_string": (ctypes.c_char_p, [i32]),
     "tca_last_error": (ctypes.c_char_p, []),
     "tca_device_count": (i32, [i32p]),

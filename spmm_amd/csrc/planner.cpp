@@ -3,6 +3,7 @@
 #include "planner.hpp"
 
 #include <algorithm>
+#include <cstdlib>
 #include <numeric>
 
 #include <omp.h>
@@ -54,12 +55,18 @@ void plan_rows(const int32_t* rowptr, int32_t M, int32_t N, int32_t es, const st
     // small, so long rows do not leave a latency tail), a power of two
     // between 2 and 32 rounds of slots * kUnroll loads.
     const int64_t round = static_cast<int64_t>(slots) * kUnroll;
-    const int64_t target = std::min<int64_t>(32 * round, std::max<int64_t>(2 * round, next_pow2(std::max<int64_t>(nnz / 16384, 1))));
+    int64_t target = std::min<int64_t>(32 * round, std::max<int64_t>(2 * round, next_pow2(std::max<int64_t>(nnz / 16384, 1))));
+    // Tuning overrides (not part of the interface): TCA_TARGET sets the
+    // per-task length, TCA_WIDE=0 disables workgroup-shared rows,
+    // TCA_MULTI sets the multi-task row-length limit.
+    if (const char* s = std::getenv("TCA_TARGET")) target = std::max<int64_t>(round, std::atoll(s));
     p->row_len = static_cast<int32_t>(target);
-    p->wide_len = static_cast<int32_t>(4 * target);
+    const char* w = std::getenv("TCA_WIDE");
+    p->wide_len = static_cast<int32_t>((w && std::atoi(w) == 0) ? target : 4 * target);
     p->seg_len = static_cast<int32_t>(target);
     // Short rows share a wavefront, one slot each, when slots > 1.
     p->multi_max = slots > 1 ? 2 * slots : -1;
+    if (const char* s = std::getenv("TCA_MULTI")) p->multi_max = slots > 1 ? std::atoi(s) : -1;
 
     std::vector<int32_t> rows;
     rows.reserve(M);
@@ -141,6 +148,65 @@ void condense(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_t w
     }
 }
 
+void plan_mfma(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_t N, int32_t dtype, bool force,
+               bool disable, double min_density, MfmaPlan* p) {
+    constexpr int32_t kWin = 64, kStep = 32, kMaxStep = 1024;
+    *p = MfmaPlan();
+    p->row_mfma.assign(M, 0);
+    if (disable || dtype == TCA_F32 || N % 8 != 0 || M == 0) return;
+    std::vector<int64_t> uoff;
+    std::vector<int32_t> ucols, cpos(rowptr[M]);
+    condense(rowptr, colidx, M, kWin, &uoff, &ucols, &cpos);
+    const int32_t nw = (M + kWin - 1) / kWin;
+    std::vector<uint8_t> take(nw, 0);
+#pragma omp parallel for schedule(dynamic, 16)
+    for (int32_t w = 0; w < nw; w++) {
+        const int32_t r0 = w * kWin, r1 = std::min(M, r0 + kWin);
+        const int64_t nz = rowptr[r1] - rowptr[r0];
+        const int64_t ucount = uoff[w + 1] - uoff[w];
+        if (nz == 0 || nz >= (int64_t(1) << 21)) continue;
+        const int64_t steps = (ucount + kStep - 1) / kStep;
+        // nonzeros per step must fit 4 per thread of the 256-thread workgroup
+        std::vector<int32_t> per(steps, 0);
+        for (int32_t j = rowptr[r0]; j < rowptr[r1]; j++) per[cpos[j] / kStep]++;
+        if (*std::max_element(per.begin(), per.end()) > kMaxStep) continue;
+        const double density = static_cast<double>(nz) / (static_cast<double>(r1 - r0) * steps * kStep);
+        if (force || density >= min_density) take[w] = 1;
+    }
+    for (int32_t w = 0; w < nw; w++) {
+        if (!take[w]) continue;
+        const int32_t r0 = w * kWin, r1 = std::min(M, r0 + kWin);
+        const int32_t ucount = static_cast<int32_t>(uoff[w + 1] - uoff[w]);
+        const int32_t steps = (ucount + kStep - 1) / kStep;
+        const int32_t gstep = static_cast<int32_t>(p->eoff.size());
+        p->windows.push_back({r0, steps, gstep, rowptr[r0]});
+        for (int32_t s = 0; s < steps * kStep; s++)
+            p->ucols.push_back(s < ucount ? ucols[uoff[w] + s] : -1);
+        // entries bucketed by step; rows in order and columns ascending inside
+        // a row, so each bucket lists (row, column) in row-major order
+        std::vector<int32_t> cnt(steps + 1, 0);
+        for (int32_t j = rowptr[r0]; j < rowptr[r1]; j++) cnt[cpos[j] / kStep + 1]++;
+        for (int32_t s = 0; s < steps; s++) cnt[s + 1] += cnt[s];
+        const size_t ebase = p->entries.size();
+        for (int32_t s = 0; s < steps; s++) p->eoff.push_back(static_cast<int32_t>(ebase + cnt[s]));
+        p->entries.resize(ebase + cnt[steps]);
+        std::vector<int32_t> fill(cnt.begin(), cnt.end() - 1);
+        for (int32_t r = r0; r < r1; r++)
+            for (int32_t j = rowptr[r]; j < rowptr[r + 1]; j++) {
+                const int32_t s = cpos[j] / kStep;
+                p->entries[ebase + fill[s]++] = static_cast<uint32_t>(r - r0) |
+                                                (static_cast<uint32_t>(cpos[j] % kStep) << 6) |
+                                                (static_cast<uint32_t>(j - rowptr[r0]) << 11);
+            }
+        for (int32_t r = r0; r < r1; r++) p->row_mfma[r] = 1;
+        p->nnz += rowptr[r1] - rowptr[r0];
+        p->cond_cols += static_cast<int64_t>(steps) * kStep;
+        p->rows += r1 - r0;
+    }
+    p->eoff.push_back(static_cast<int32_t>(p->entries.size()));
+    (void)kMaxStep;
+}
+
 }  // namespace tca
 
 extern "C" int tca_condense_windows(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_t nnz,
@@ -188,5 +254,32 @@ extern "C" int tca_plan_row_tasks(const int32_t* rowptr, int32_t M, int32_t N, i
         geometry[6] = p.wide_len;
         geometry[7] = p.multi_max;
     }
+    return TCA_OK;
+}
+
+extern "C" int tca_plan_mfma_windows(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_t N,
+                                     int32_t dtype, uint32_t flags, int32_t* n_windows, int32_t* n_steps,
+                                     int64_t* n_entries, int32_t* windows, int32_t* ucols, int32_t* eoff,
+                                     uint32_t* entries) {
+    using namespace tca;
+    if (!rowptr || M < 0 || N < 1 || !dtype_ok(dtype) || !n_windows || !n_steps || !n_entries)
+        return fail(TCA_ERR_INVALID, "tca_plan_mfma_windows: bad argument");
+    MfmaPlan p;
+    const char* md = std::getenv("TCA_MFMA_MIN_DENSITY");
+    plan_mfma(rowptr, colidx, M, N, dtype, (flags & TCA_PLAN_FORCE_MFMA) != 0, (flags & TCA_PLAN_NO_MFMA) != 0,
+              md ? std::atof(md) : kMfmaMinDensity, &p);
+    const int32_t steps = static_cast<int32_t>(p.eoff.size()) - 1;
+    if (windows) {
+        if (*n_windows < static_cast<int32_t>(p.windows.size()) || *n_steps < steps ||
+            *n_entries < static_cast<int64_t>(p.entries.size()) || !ucols || !eoff || !entries)
+            return fail(TCA_ERR_INVALID, "tca_plan_mfma_windows: output buffers too small");
+        if (!p.windows.empty()) std::copy(&p.windows[0].x, &p.windows[0].x + 4 * p.windows.size(), windows);
+        std::copy(p.ucols.begin(), p.ucols.end(), ucols);
+        std::copy(p.eoff.begin(), p.eoff.end(), eoff);
+        std::copy(p.entries.begin(), p.entries.end(), entries);
+    }
+    *n_windows = static_cast<int32_t>(p.windows.size());
+    *n_steps = steps;
+    *n_entries = static_cast<int64_t>(p.entries.size());
     return TCA_OK;
 }

@@ -43,6 +43,37 @@ struct RowPlan {
     int32_t n_multi = 0, n_seg = 0, n_rowtasks = 0, n_wide = 0;
 };
 
+// Row windows routed to the MFMA tile kernel (64 rows each).  For window i:
+// windows[i] = {first row, steps, first global step, first nonzero}; step s
+// of the window has B rows ucols[(first global step + s) * 32 + 0..31]
+// (-1 = padding past the column union) and nonzeros
+// entries[eoff[g] .. eoff[g + 1]) with g its global step; an entry packs the
+// row within the window (6 bits), the column within the step (5 bits, bit 6)
+// and the nonzero index minus the window's first nonzero (bit 11 up).
+// Default routing threshold: windows whose condensed tiles are at least this
+// dense run on the MFMA tile kernel.  Measured crossover on MI355X (4096 x
+// 4096 Bernoulli, fp16, N = 512): the tile kernel is 3.1x slower than the
+// row kernel at density 0.05, equal near 0.2 and 1.9x faster at 0.4.
+constexpr double kMfmaMinDensity = 0.25;
+
+struct MfmaPlan {
+    std::vector<Int4> windows;
+    std::vector<int32_t> ucols;
+    std::vector<int32_t> eoff;
+    std::vector<uint32_t> entries;
+    std::vector<uint8_t> row_mfma;  // per row: covered by an MFMA window
+    int64_t nnz = 0;                // nonzeros in MFMA windows
+    int64_t cond_cols = 0;          // padded condensed columns, summed over windows
+    int32_t rows = 0;
+};
+
+// Windows whose condensed tile density nnz / (rows * padded |U|) is at least
+// min_density (all eligible windows with force, none with disable).  Only for
+// fp16 / bf16 and N % 8 == 0; a window qualifies only while its nonzeros
+// fit the entry encoding (< 2^21) and no step holds more than 1024 of them.
+void plan_mfma(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_t N, int32_t dtype, bool force,
+               bool disable, double min_density, MfmaPlan* p);
+
 // Lane geometry for width N and value size `es` bytes: the widest vector
 // (<= 16 bytes) whose element count divides N, and the column chunks: up to
 // 8 chunks of at least 128 bytes (one L2 line of B per chunk row), at most

@@ -11,6 +11,7 @@
 #include "common.hpp"
 #include "planner.hpp"
 #include "row_kernel.hpp"
+#include "mfma_kernel.hpp"
 
 using namespace tca;
 
@@ -21,11 +22,20 @@ using namespace tca;
             return fail(TCA_ERR_HIP, "%s failed: %s (%s:%d)", #expr, hipGetErrorString(e_), __FILE__, __LINE__); \
     } while (0)
 
+// Column chunks per XCD are used when B is larger than this.
+constexpr uint64_t kSliceBytes = 8ull << 20;
+
 struct tca_spmm_plan {
     int32_t M = 0, K = 0, N = 0, nnz = 0, dtype = 0;
     uint32_t flags = 0;
     int device = 0;
     RowPlan rows;
+    MfmaPlan mfma;
+    int32_t mfma_col_blocks = 0;
+    int4* d_windows = nullptr;
+    int* d_ucols = nullptr;
+    int* d_eoff = nullptr;
+    uint32_t* d_entries = nullptr;
     int32_t ntasks = 0;
     int* d_rowptr = nullptr;
     int* d_colidx = nullptr;
@@ -61,6 +71,10 @@ void free_plan_device(tca_spmm_plan* p) {
     (void)hipFree(p->d_perm);
     (void)hipFree(p->d_longrows);
     (void)hipFree(p->d_partials);
+    (void)hipFree(p->d_windows);
+    (void)hipFree(p->d_ucols);
+    (void)hipFree(p->d_eoff);
+    (void)hipFree(p->d_entries);
 }
 
 template <typename T, int E>
@@ -105,6 +119,29 @@ int launch_rows_e(const tca_spmm_plan* p, const void* val, const void* B, float*
             [[fallthrough]];
         default: return fail(TCA_ERR_INVALID, "bad lane geometry");
     }
+}
+
+int launch_mfma(const tca_spmm_plan* p, const void* val, const void* B, float* C, hipStream_t s) {
+    if (p->mfma.windows.empty()) return TCA_OK;
+    MfmaArgs a;
+    a.windows = p->d_windows;
+    a.ucols = p->d_ucols;
+    a.eoff = p->d_eoff;
+    a.entries = p->d_entries;
+    a.val = val;
+    a.B = B;
+    a.C = C;
+    a.M = p->M;
+    a.N = p->N;
+    a.col_blocks = p->mfma_col_blocks;
+    a.val_bytes = static_cast<uint32_t>(static_cast<uint64_t>(p->nnz) * 2);
+    a.B_bytes = static_cast<uint32_t>(static_cast<uint64_t>(p->K) * p->N * 2);
+    const dim3 grid(static_cast<unsigned>(p->mfma.windows.size()) * p->mfma_col_blocks);
+    if (p->dtype == TCA_BF16)
+        hipLaunchKernelGGL(mfma_tile_kernel<true>, grid, dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL(mfma_tile_kernel<false>, grid, dim3(256), 0, s, a);
+    return TCA_OK;
 }
 
 int launch_rows(const tca_spmm_plan* p, const void* val, const void* B, float* C, hipStream_t s) {
@@ -160,9 +197,17 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
         delete p;
         return fail(TCA_ERR_HIP, "no HIP device");
     }
-    // TCA_SLICES (tuning only) forces the number of column chunks.
+    // Dense-enough 64-row windows go to the MFMA tile kernel (fp16 / bf16).
+    // TCA_MFMA_MIN_DENSITY (tuning only) overrides the routing threshold.
+    const char* md = std::getenv("TCA_MFMA_MIN_DENSITY");
+    plan_mfma(rowptr, colidx, M, N, dtype, (flags & TCA_PLAN_FORCE_MFMA) != 0, (flags & TCA_PLAN_NO_MFMA) != 0,
+              md ? std::atof(md) : kMfmaMinDensity, &p->mfma);
+    p->mfma_col_blocks = (N + kTileCols - 1) / kTileCols;
+    // Column chunks per XCD only pay when B overflows the L2s; TCA_SLICES
+    // (tuning only) forces the number of chunks.
     const char* sl = std::getenv("TCA_SLICES");
-    plan_rows(rowptr, M, N, static_cast<int32_t>(dtype_size(dtype)), {}, sl ? std::atoi(sl) : 0, &p->rows);
+    const int32_t slices = sl ? std::atoi(sl) : (b_bytes > kSliceBytes ? 0 : 1);
+    plan_rows(rowptr, M, N, static_cast<int32_t>(dtype_size(dtype)), p->mfma.row_mfma, slices, &p->rows);
     p->ntasks = static_cast<int32_t>(p->rows.tasks.size());
     const size_t n_seg_total =
         p->rows.longrows.empty() ? 0 : static_cast<size_t>(p->rows.longrows.back().y + p->rows.longrows.back().z);
@@ -179,6 +224,11 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
     if ((st = dev_upload(&p->d_perm, p->rows.perm.data(), p->rows.perm.size()))) return bail(st);
     if ((st = dev_upload(&p->d_longrows, p->rows.longrows.data(), p->rows.longrows.size()))) return bail(st);
     if ((st = dev_upload(&p->d_partials, nullptr, n_seg_total * N))) return bail(st);
+    if ((st = dev_upload(&p->d_windows, p->mfma.windows.data(), p->mfma.windows.size()))) return bail(st);
+    if ((st = dev_upload(&p->d_ucols, p->mfma.ucols.data(), p->mfma.ucols.size()))) return bail(st);
+    if ((st = dev_upload(&p->d_eoff, p->mfma.eoff.data(), p->mfma.windows.empty() ? 0 : p->mfma.eoff.size())))
+        return bail(st);
+    if ((st = dev_upload(&p->d_entries, p->mfma.entries.data(), p->mfma.entries.size()))) return bail(st);
     if (hipDeviceSynchronize() != hipSuccess) return bail(fail(TCA_ERR_HIP, "hipDeviceSynchronize failed"));
 
     tca_plan_info& in = p->info;
@@ -201,6 +251,13 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
     in.row_blocks = ((p->ntasks + kRowWaves - 1) / kRowWaves) * p->rows.col_chunks;
     in.row_blockdim = 64 * kRowWaves;
     in.seg_len = p->rows.seg_len;
+    in.n_windows_mfma = static_cast<int32_t>(p->mfma.windows.size());
+    in.rows_mfma = p->mfma.rows;
+    in.nnz_mfma = p->mfma.nnz;
+    in.cond_cols_mfma = p->mfma.cond_cols;
+    in.mfma_blocks = in.n_windows_mfma * p->mfma_col_blocks;
+    in.mfma_blockdim = 256;
+    in.mfma_lds_bytes = static_cast<int32_t>(3 * (kWinRows * kAStride + kStepK * kBStride) * sizeof(uint16_t));
     in.scratch_bytes = static_cast<int64_t>(n_seg_total * N * sizeof(float));
     in.plan_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
     *plan = p;
@@ -231,7 +288,9 @@ int tca_spmm_run(const tca_spmm_plan* p, const void* d_val, const void* d_B, flo
     if (reinterpret_cast<uintptr_t>(d_val) % dtype_size(p->dtype) != 0)
         return fail(TCA_ERR_INVALID, "values misaligned");
     hipStream_t s = static_cast<hipStream_t>(stream);
-    int st = launch_rows(p, d_val, d_B, d_C, s);
+    int st = launch_mfma(p, d_val, d_B, d_C, s);
+    if (st) return st;
+    st = launch_rows(p, d_val, d_B, d_C, s);
     if (st) return st;
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(TCA_ERR_HIP, "kernel launch: %s", hipGetErrorString(e));

@@ -137,6 +137,41 @@ def test_exact_bit_equal_all_widths(torch_cuda, dtype):
         assert np.array_equal(got, want), (dtype, n, np.abs(got - want).max())
 
 
+@pytest.mark.parametrize("dtype", [S.TCA_F16, S.TCA_BF16])
+def test_mfma_exact_bit_equal(torch_cuda, dtype):
+    """Condensed-tile MFMA path (forced on every eligible window) is bit-equal
+    to the oracle on exact-arithmetic inputs, for partial windows, partial
+    column blocks and empty rows."""
+    rng = np.random.default_rng(71 + dtype)
+    for m, k, p in [(64, 256, 0.1), (130, 700, 0.05), (200, 64, 0.45), (17, 40, 0.3), (96, 5000, 0.004)]:
+        lens = rng.binomial(k, p, m)
+        lens[rng.random(m) < 0.1] = 0
+        a = make_csr(rng, lens, k, dtype)
+        for n in (8, 16, 64, 128, 136, 256, 512):
+            b = S.to_storage(exact_dense(rng, (k, n)), dtype)
+            with S.Plan(a, n, S.TCA_PLAN_FORCE_MFMA) as pl:
+                info = pl.info()
+                got = run_gpu(torch_cuda, a, b, plan=pl)
+            assert info["n_windows_mfma"] > 0, (m, k, n)
+            want = oracle_c(a, b)
+            assert np.array_equal(got, want), (m, k, p, n, np.abs(got - want).max())
+
+
+def test_mfma_and_row_paths_agree(torch_cuda):
+    rng = np.random.default_rng(81)
+    a, _ = S.gen_bernoulli(300, 900, 0.05, seed=5, dtype=S.TCA_F16)
+    a = S.CSR(a.nrow, a.ncol, a.rowptr, a.colidx, S.to_storage(exact_values(rng, a.nnz), S.TCA_F16), S.TCA_F16)
+    b = S.to_storage(exact_dense(rng, (900, 256)), S.TCA_F16)
+    outs = {}
+    for flags in (S.TCA_PLAN_NO_MFMA, S.TCA_PLAN_FORCE_MFMA, S.TCA_PLAN_DEFAULT):
+        with S.Plan(a, 256, flags) as pl:
+            nwin = pl.info()["n_windows_mfma"]
+            outs[flags] = run_gpu(torch_cuda, a, b, plan=pl)
+        assert (nwin > 0) == (flags != S.TCA_PLAN_NO_MFMA)
+    assert np.array_equal(outs[S.TCA_PLAN_NO_MFMA], outs[S.TCA_PLAN_FORCE_MFMA])
+    assert np.array_equal(outs[S.TCA_PLAN_DEFAULT], oracle_c(a, b))
+
+
 def test_exact_long_rows_many_segments(torch_cuda):
     """Rows far above the segment length; every output element exact."""
     rng = np.random.default_rng(21)
@@ -146,7 +181,7 @@ def test_exact_long_rows_many_segments(torch_cuda):
     info = None
     for n in (64, 256, 512):
         b = S.to_storage(exact_dense(rng, (k, n)), S.TCA_F16)
-        with S.Plan(a, n) as p:
+        with S.Plan(a, n, S.TCA_PLAN_NO_MFMA) as p:  # the segment path of the row kernel
             info = p.info()
             got = run_gpu(torch_cuda, a, b, plan=p)
         assert info["n_long_rows"] >= 4
@@ -228,9 +263,15 @@ def test_config_full_size_small(torch_cuda, cfg):
     dist = 0
     b = S.gen_dense(a.ncol, n, dist, seed=100 + cfg, dtype=a.dtype)
     print(f"config {cfg}: M={a.nrow} K={a.ncol} N={n} nnz={a.nnz}", flush=True)
-    got = run_gpu(torch_cuda, a, b)
+    with S.Plan(a, n) as pl:
+        info = pl.info()
+        got = run_gpu(torch_cuda, a, b, plan=pl)
+    assert info["n_windows_mfma"] > 0  # pruned-weight configs take the MFMA tile path
     assert_close(oracle_c(a, b), got, f"config {cfg} vs fp32 oracle")
     assert_parity(a, b, got, f"config {cfg}")
+    with S.Plan(a, n, S.TCA_PLAN_NO_MFMA) as pl:
+        got_rows = run_gpu(torch_cuda, a, b, plan=pl)
+    assert_parity(a, b, got_rows, f"config {cfg} row kernel only")
 
 
 @pytest.mark.parametrize("cfg", [2, 3, 4])

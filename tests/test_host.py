@@ -224,6 +224,48 @@ def test_zipf_rows_total_and_cap():
     assert z.nnz == 400000 and lens.max() <= 15000 and st["max_row"] == lens.max()
 
 
+# --------------------------------------------------- condensed windows
+@pytest.mark.parametrize("m,k,p,win", [(130, 300, 0.05, 64), (64, 64, 0.5, 16), (37, 1000, 0.01, 4), (20, 20, 0.0, 16)])
+def test_condense_windows_bit_exact_with_oracle(m, k, p, win):
+    a, _ = S.gen_bernoulli(m, k, p, seed=m + k, dtype=S.TCA_F16)
+    uoff, ucols, cpos = S.condense_windows(a, win)
+    ou, oc, op = oracle.condense_windows(a.rowptr, a.colidx, m, win)
+    assert np.array_equal(uoff, ou) and np.array_equal(ucols, oc) and np.array_equal(cpos, op)
+
+
+@pytest.mark.parametrize("m,k,n,p,flags", [(200, 700, 128, 0.06, S.TCA_PLAN_DEFAULT),
+                                           (130, 300, 64, 0.02, S.TCA_PLAN_FORCE_MFMA),
+                                           (64, 2048, 256, 0.3, S.TCA_PLAN_DEFAULT)])
+def test_mfma_window_plan_decodes_to_the_csr(m, k, n, p, flags):
+    """Every MFMA window's steps, B-row lists and entries reproduce the CSR
+    exactly, with the oracle's condensed positions."""
+    a, _ = S.gen_bernoulli(m, k, p, seed=7, dtype=S.TCA_F16)
+    windows, ucols, eoff, entries = S.plan_mfma_windows(a, n, flags=flags)
+    assert len(windows) > 0
+    uo, uc, cp = oracle.condense_windows(a.rowptr, a.colidx, m, 64)
+    for row0, steps, gstep, nz0 in windows:
+        w = row0 // 64
+        assert row0 % 64 == 0 and nz0 == a.rowptr[row0]
+        u = uc[uo[w]:uo[w + 1]]
+        assert steps == (len(u) + 31) // 32
+        cols = ucols[gstep * 32:(gstep + steps) * 32]
+        assert np.array_equal(cols[:len(u)], u) and np.all(cols[len(u):] == -1)
+        seen = []
+        for s in range(steps):
+            for e in entries[eoff[gstep + s]:eoff[gstep + s + 1]]:
+                r, kk, rel = int(e) & 63, (int(e) >> 6) & 31, int(e) >> 11
+                j = nz0 + rel
+                assert a.rowptr[row0 + r] <= j < a.rowptr[row0 + r + 1]
+                assert cp[j] == 32 * s + kk and cols[32 * s + kk] == a.colidx[j]
+                seen.append(j)
+        r1 = min(m, row0 + 64)
+        assert sorted(seen) == list(range(a.rowptr[row0], a.rowptr[r1]))
+    none = S.plan_mfma_windows(a, n, flags=S.TCA_PLAN_NO_MFMA)[0]
+    assert len(none) == 0
+    assert len(S.plan_mfma_windows(a.astype(S.TCA_F32), n, flags=S.TCA_PLAN_FORCE_MFMA)[0]) == 0  # fp32: no MFMA
+    assert len(S.plan_mfma_windows(a, 100, flags=S.TCA_PLAN_FORCE_MFMA)[0]) == 0  # N % 8 != 0
+
+
 # -------------------------------------------------------------- planner
 @pytest.mark.parametrize("n,dtype", [(256, S.TCA_F16), (512, S.TCA_F16), (64, S.TCA_F16), (128, S.TCA_F32),
                                      (7, S.TCA_F32), (100, S.TCA_BF16), (1000, S.TCA_F16)])
