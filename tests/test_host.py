@@ -233,7 +233,7 @@ def test_condense_windows_bit_exact_with_oracle(m, k, p, win):
     assert np.array_equal(uoff, ou) and np.array_equal(ucols, oc) and np.array_equal(cpos, op)
 
 
-@pytest.mark.parametrize("m,k,n,p,flags", [(200, 700, 128, 0.06, S.TCA_PLAN_DEFAULT),
+@pytest.mark.parametrize("m,k,n,p,flags", [(200, 700, 128, 0.06, S.TCA_PLAN_FORCE_MFMA),
                                            (130, 300, 64, 0.02, S.TCA_PLAN_FORCE_MFMA),
                                            (64, 2048, 256, 0.3, S.TCA_PLAN_DEFAULT)])
 def test_mfma_window_plan_decodes_to_the_csr(m, k, n, p, flags):
