@@ -161,6 +161,11 @@ int tca_plan_mfma_windows(const int32_t* rowptr, const int32_t* colidx, int32_t 
                           uint32_t flags, int32_t* n_windows, int32_t* n_steps, int64_t* n_entries,
                           int32_t* windows, int32_t* ucols, int32_t* eoff, uint32_t* entries);
 
+/* Launches a trivial kernel on the current device and synchronises
+ * (reference warm_up_gpu_kernel, src/miscalleneous.cu:158-164, launched
+ * <<<1,32>>> ten times by src/test.cu:50-52). */
+int tca_warm_up(void);
+
 /* ---- library information ---- */
 const char* tca_status_string(int status);
 const char* tca_last_error(void);

@@ -82,6 +82,7 @@ SIGNATURES = {
     "tca_status_string": (ctypes.c_char_p, [i32]),
     "tca_last_error": (ctypes.c_char_p, []),
     "tca_device_count": (i32, [i32p]),
+    "tca_warm_up": (i32, []),
     "tca_version": (i32, []),
     # tca_host.h
     "tca_csr_free": (None, [ctypes.POINTER(TcaCsr)]),

@@ -20,6 +20,11 @@ namespace tca {
 int fail(int status, const char* fmt, ...);
 void clear_error();
 
+// .smtx readers over an open stream (`name` only labels error messages).
+int smtx_read_csr_file(FILE* f, const char* name, int32_t dtype, tca_csr* out);
+int smtx_read_dense_file(FILE* f, const char* name, int32_t dtype, void** dense, int32_t* nRow, int32_t* nCol,
+                         int32_t* nnz);
+
 inline size_t dtype_size(int32_t dtype) { return dtype == TCA_F32 ? 4 : 2; }
 inline bool dtype_ok(int32_t dtype) { return dtype == TCA_F16 || dtype == TCA_F32 || dtype == TCA_BF16; }
 

@@ -78,26 +78,22 @@ struct SmtxRaw {
 
 // Parses the three parts of a .smtx file (reference src/file_input.cu:141-180)
 // and checks counts and ranges; column order inside a row is left as read.
-int parse_smtx(const char* path, SmtxRaw* raw) {
-    FILE* f = std::fopen(path, "rb");
-    if (!f) return fail(TCA_ERR_IO, "cannot open '%s'", path);
+// `path` only names the source in messages; the caller owns `f`.
+int parse_smtx_stream(FILE* f, const char* path, SmtxRaw* raw) {
     Reader rd(f);
     int64_t h[3];
     int stop = 0;
     for (int i = 0; i < 3; i++) {
         if (!rd.next_int(" \t,", &h[i], &stop)) {
-            std::fclose(f);
             return fail(TCA_ERR_FORMAT, "%s: header must be 'rows, cols, nnz'", path);
         }
     }
     int64_t extra;
     if (rd.next_int(" \t,", &extra, &stop)) {
-        std::fclose(f);
         return fail(TCA_ERR_FORMAT, "%s: header has more than 3 numbers", path);
     }
-    if (stop == -2) { std::fclose(f); return fail(TCA_ERR_FORMAT, "%s: bad header token", path); }
+    if (stop == -2) { return fail(TCA_ERR_FORMAT, "%s: bad header token", path); }
     if (h[0] < 0 || h[1] < 0 || h[2] < 0 || h[0] > INT32_MAX - 1 || h[1] > INT32_MAX || h[2] > INT32_MAX) {
-        std::fclose(f);
         return fail(TCA_ERR_FORMAT, "%s: header values out of range", path);
     }
     raw->nrow = static_cast<int32_t>(h[0]);
@@ -109,22 +105,18 @@ int parse_smtx(const char* path, SmtxRaw* raw) {
     size_t n = 0;
     while (rd.next_int(" \t", &v, &stop)) {
         if (n > static_cast<size_t>(raw->nrow)) {
-            std::fclose(f);
             return fail(TCA_ERR_FORMAT, "%s: more than rows+1 = %d row offsets", path, raw->nrow + 1);
         }
         raw->rowptr[n++] = static_cast<int32_t>(v);
     }
     if (stop == -2 || n != static_cast<size_t>(raw->nrow) + 1) {
-        std::fclose(f);
         return fail(TCA_ERR_FORMAT, "%s: expected %d row offsets on line 2, read %zu", path, raw->nrow + 1, n);
     }
     if (raw->rowptr[0] != 0 || raw->rowptr[raw->nrow] != raw->nnz) {
-        std::fclose(f);
         return fail(TCA_ERR_FORMAT, "%s: row offsets must run from 0 to nnz = %d", path, raw->nnz);
     }
     for (int32_t r = 0; r < raw->nrow; r++)
         if (raw->rowptr[r + 1] < raw->rowptr[r]) {
-            std::fclose(f);
             return fail(TCA_ERR_FORMAT, "%s: row offsets decrease at row %d", path, r);
         }
     // Remaining lines: nnz column indices.
@@ -133,33 +125,35 @@ int parse_smtx(const char* path, SmtxRaw* raw) {
     for (;;) {
         if (rd.next_int(" \t", &v, &stop)) {
             if (n >= static_cast<size_t>(raw->nnz)) {
-                std::fclose(f);
-                return fail(TCA_ERR_FORMAT, "%s: more than nnz = %d column indices", path, raw->nnz);
+                    return fail(TCA_ERR_FORMAT, "%s: more than nnz = %d column indices", path, raw->nnz);
             }
             if (v < 0 || v >= raw->ncol) {
-                std::fclose(f);
-                return fail(TCA_ERR_FORMAT, "%s: column index %lld out of [0, %d)", path, (long long)v, raw->ncol);
+                    return fail(TCA_ERR_FORMAT, "%s: column index %lld out of [0, %d)", path, (long long)v, raw->ncol);
             }
             raw->colidx[n++] = static_cast<int32_t>(v);
             continue;
         }
-        if (stop == -2) { std::fclose(f); return fail(TCA_ERR_FORMAT, "%s: bad column token", path); }
+        if (stop == -2) { return fail(TCA_ERR_FORMAT, "%s: bad column token", path); }
         if (stop < 0) break;  // EOF
     }
-    std::fclose(f);
     if (n != static_cast<size_t>(raw->nnz))
         return fail(TCA_ERR_FORMAT, "%s: expected %d column indices, read %zu", path, raw->nnz, n);
     return TCA_OK;
 }
 
+
 }  // namespace
 
 extern "C" {
 
-int tca_smtx_read_csr(const char* path, int32_t dtype, tca_csr* out) {
-    if (!path || !out || !dtype_ok(dtype)) return fail(TCA_ERR_INVALID, "tca_smtx_read_csr: bad argument");
+}  // extern "C"
+
+namespace tca {
+
+int smtx_read_csr_file(FILE* f, const char* path, int32_t dtype, tca_csr* out) {
+    if (!f || !out || !dtype_ok(dtype)) return fail(TCA_ERR_INVALID, "smtx_read_csr_file: bad argument");
     SmtxRaw raw;
-    int st = parse_smtx(path, &raw);
+    int st = parse_smtx_stream(f, path, &raw);
     if (st) return st;
     // Sort and de-duplicate each row, as .smtx -> dense -> CSR would
     // (reference src/file_input.cu:182-191 then src/miscalleneous.cu:29-65).
@@ -190,12 +184,12 @@ int tca_smtx_read_csr(const char* path, int32_t dtype, tca_csr* out) {
     return TCA_OK;
 }
 
-int tca_smtx_read_dense(const char* path, int32_t dtype, void** dense, int32_t* nRow, int32_t* nCol,
-                        int32_t* nnz) {
-    if (!path || !dense || !nRow || !nCol || !nnz || !dtype_ok(dtype))
-        return fail(TCA_ERR_INVALID, "tca_smtx_read_dense: bad argument");
+int smtx_read_dense_file(FILE* f, const char* path, int32_t dtype, void** dense, int32_t* nRow, int32_t* nCol,
+                         int32_t* nnz) {
+    if (!f || !dense || !nRow || !nCol || !nnz || !dtype_ok(dtype))
+        return fail(TCA_ERR_INVALID, "smtx_read_dense_file: bad argument");
     SmtxRaw raw;
-    int st = parse_smtx(path, &raw);
+    int st = parse_smtx_stream(f, path, &raw);
     if (st) return st;
     const size_t es = dtype_size(dtype);
     const size_t total = static_cast<size_t>(raw.nrow) * raw.ncol;
@@ -210,6 +204,30 @@ int tca_smtx_read_dense(const char* path, int32_t dtype, void** dense, int32_t* 
     *nCol = raw.ncol;
     *nnz = raw.nnz;
     return TCA_OK;
+}
+
+}  // namespace tca
+
+extern "C" {
+
+int tca_smtx_read_csr(const char* path, int32_t dtype, tca_csr* out) {
+    if (!path || !out || !dtype_ok(dtype)) return fail(TCA_ERR_INVALID, "tca_smtx_read_csr: bad argument");
+    FILE* f = std::fopen(path, "rb");
+    if (!f) return fail(TCA_ERR_IO, "cannot open '%s'", path);
+    const int st = smtx_read_csr_file(f, path, dtype, out);
+    std::fclose(f);
+    return st;
+}
+
+int tca_smtx_read_dense(const char* path, int32_t dtype, void** dense, int32_t* nRow, int32_t* nCol,
+                        int32_t* nnz) {
+    if (!path || !dense || !nRow || !nCol || !nnz || !dtype_ok(dtype))
+        return fail(TCA_ERR_INVALID, "tca_smtx_read_dense: bad argument");
+    FILE* f = std::fopen(path, "rb");
+    if (!f) return fail(TCA_ERR_IO, "cannot open '%s'", path);
+    const int st = smtx_read_dense_file(f, path, dtype, dense, nRow, nCol, nnz);
+    std::fclose(f);
+    return st;
 }
 
 int tca_smtx_write(const char* path, const tca_csr* a) {

@@ -48,6 +48,8 @@ struct tca_spmm_plan {
 
 namespace {
 
+__global__ void warm_up_kernel() {}
+
 template <typename T>
 int dev_upload(T** dst, const void* src, size_t count) {
     *dst = nullptr;
@@ -158,6 +160,13 @@ int launch_rows(const tca_spmm_plan* p, const void* val, const void* B, float* C
 extern "C" {
 
 int tca_version(void) { return 100; }
+
+int tca_warm_up(void) {
+    hipLaunchKernelGGL(warm_up_kernel, dim3(1), dim3(64), 0, nullptr);
+    TCA_HIP_TRY(hipGetLastError());
+    TCA_HIP_TRY(hipDeviceSynchronize());
+    return TCA_OK;
+}
 
 int tca_device_count(int32_t* count) {
     int n = 0;

@@ -263,15 +263,16 @@ def test_config_full_size_small(torch_cuda, cfg):
     dist = 0
     b = S.gen_dense(a.ncol, n, dist, seed=100 + cfg, dtype=a.dtype)
     print(f"config {cfg}: M={a.nrow} K={a.ncol} N={n} nnz={a.nnz}", flush=True)
-    with S.Plan(a, n) as pl:
-        info = pl.info()
-        got = run_gpu(torch_cuda, a, b, plan=pl)
-    assert info["n_windows_mfma"] > 0  # pruned-weight configs take the MFMA tile path
+    got = run_gpu(torch_cuda, a, b)
     assert_close(oracle_c(a, b), got, f"config {cfg} vs fp32 oracle")
     assert_parity(a, b, got, f"config {cfg}")
-    with S.Plan(a, n, S.TCA_PLAN_NO_MFMA) as pl:
-        got_rows = run_gpu(torch_cuda, a, b, plan=pl)
-    assert_parity(a, b, got_rows, f"config {cfg} row kernel only")
+    # both kernels on the whole matrix
+    for flags, what in ((S.TCA_PLAN_NO_MFMA, "row kernel only"), (S.TCA_PLAN_FORCE_MFMA, "MFMA tiles only")):
+        with S.Plan(a, n, flags) as pl:
+            info = pl.info()
+            got_k = run_gpu(torch_cuda, a, b, plan=pl)
+        assert (info["rows_mfma"] == a.nrow) == (flags == S.TCA_PLAN_FORCE_MFMA)
+        assert_parity(a, b, got_k, f"config {cfg} {what}")
 
 
 @pytest.mark.parametrize("cfg", [2, 3, 4])
