@@ -131,8 +131,8 @@ int tca_condense_windows(const int32_t* rowptr, const int32_t* colidx, int32_t M
                          int32_t win, int64_t* uoff, int32_t* ucols, int32_t* cpos);
 
 /* ---- host-only view of the row kernel's task list (no device needed) ----
- * The wavefront tasks tca_spmm_plan_create builds for this structure, width N
- * and dtype, with no rows routed to the MFMA kernel.  Call with tasks == NULL
+ * The wavefront tasks tca_spmm_plan_create builds for this structure, shape
+ * (M x K, width N) and dtype, with no rows routed to the MFMA kernel.  Call with tasks == NULL
  * to get the counts, then again with tasks[4*n_tasks], perm[n_perm] and
  * longrows[4*n_long].  Task int4 {x,y,z,w}: w == 0 row task (x row, [y,z)
  * nonzeros); w == 1 multi task (x offset into perm, y rows, z longest row);
@@ -143,7 +143,7 @@ int tca_condense_windows(const int32_t* rowptr, const int32_t* colidx, int32_t M
  * chunk.  geometry[8] receives elems_per_lane, lanes per slot, column chunks,
  * segment length, lanes per chunk, row-task length limit, wide-row length
  * limit and the multi-task length limit. */
-int tca_plan_row_tasks(const int32_t* rowptr, int32_t M, int32_t N, int32_t dtype, int32_t* n_tasks,
+int tca_plan_row_tasks(const int32_t* rowptr, int32_t M, int32_t K, int32_t N, int32_t dtype, int32_t* n_tasks,
                        int32_t* n_perm, int32_t* n_long, int32_t* tasks, int32_t* perm, int32_t* longrows,
                        int32_t* geometry);
 

@@ -196,12 +196,12 @@ def plan_row_tasks(a: CSR, n: int, dtype: int = None):
     rp = np.ascontiguousarray(a.rowptr, np.int32)
     nt, npm, nl = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
     geo = np.zeros(8, np.int32)
-    call("tca_plan_row_tasks", np_ptr(rp, ctypes.c_int32), a.nrow, n, dtype, ctypes.byref(nt), ctypes.byref(npm),
+    call("tca_plan_row_tasks", np_ptr(rp, ctypes.c_int32), a.nrow, a.ncol, n, dtype, ctypes.byref(nt), ctypes.byref(npm),
          ctypes.byref(nl), None, None, None, np_ptr(geo, ctypes.c_int32))
     tasks = np.zeros((nt.value, 4), np.int32)
     perm = np.zeros(max(npm.value, 1), np.int32)
     longrows = np.zeros((max(nl.value, 1), 4), np.int32)
-    call("tca_plan_row_tasks", np_ptr(rp, ctypes.c_int32), a.nrow, n, dtype, ctypes.byref(nt), ctypes.byref(npm),
+    call("tca_plan_row_tasks", np_ptr(rp, ctypes.c_int32), a.nrow, a.ncol, n, dtype, ctypes.byref(nt), ctypes.byref(npm),
          ctypes.byref(nl), np_ptr(tasks, ctypes.c_int32), np_ptr(perm, ctypes.c_int32),
          np_ptr(longrows, ctypes.c_int32), np_ptr(geo, ctypes.c_int32))
     keys = ("elems_per_lane", "lanes_per_row", "col_chunks", "seg_len", "chunk_lanes", "row_len", "wide_len",

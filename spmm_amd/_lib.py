@@ -76,7 +76,7 @@ SIGNATURES = {
     "tca_spmm_host": (i32, [i32p, i32p, vp, i32, i32, i32, vp, f32p, i32, i32, i32, i32,
                             ctypes.POINTER(ctypes.c_double)]),
     "tca_condense_windows": (i32, [i32p, i32p, i32, i32, i32, i64p, i32p, i32p]),
-    "tca_plan_row_tasks": (i32, [i32p, i32, i32, i32, i32p, i32p, i32p, i32p, i32p, i32p, i32p]),
+    "tca_plan_row_tasks": (i32, [i32p, i32, i32, i32, i32, i32p, i32p, i32p, i32p, i32p, i32p, i32p]),
     "tca_plan_mfma_windows": (i32, [i32p, i32p, i32, i32, i32, u32, i32p, i32p, i64p, i32p, i32p, i32p,
                                     ctypes.POINTER(ctypes.c_uint32)]),
     "tca_status_string": (ctypes.c_char_p, [i32]),

@@ -27,6 +27,12 @@ int32_t ilog2(int32_t x) {
 }
 }  // namespace
 
+int32_t default_slices(int32_t K, int32_t N, int32_t dtype) {
+    if (const char* sl = std::getenv("TCA_SLICES")) return std::atoi(sl);
+    const uint64_t b_bytes = static_cast<uint64_t>(K) * static_cast<uint64_t>(N) * dtype_size(dtype);
+    return b_bytes > (8ull << 20) ? 0 : 1;
+}
+
 void plan_geometry(int32_t N, int32_t es, int32_t slices, RowPlan* p) {
     int32_t e = 16 / es;
     while (e > 1 && N % e != 0) e >>= 1;
@@ -51,11 +57,14 @@ void plan_rows(const int32_t* rowptr, int32_t M, int32_t N, int32_t es, const st
     const int32_t slots = 64 >> p->log_lanes;
     const int64_t nnz = rowptr[M];
     // Work per wavefront task: about nnz / 16384 nonzeros (two resident
-    // wavefronts on each of 256 CUs x 4 SIMDs x 8 slots when the matrix is
-    // small, so long rows do not leave a latency tail), a power of two
-    // between 2 and 32 rounds of slots * kUnroll loads.
+    // wavefronts on each of 256 CUs x 4 SIMDs x 8 slots, so long rows do
+    // not leave a latency tail), a power of two of at least 256 nonzeros and
+    // 2 rounds of slots * kUnroll loads, at most 32 rounds.  (Shorter tasks
+    // cost more in partial sums than they gain in balance: on MI355X the
+    // 4096 x 4096 config-1 matrix runs 44 us at 256 and 47 us at 64.)
     const int64_t round = static_cast<int64_t>(slots) * kUnroll;
-    int64_t target = std::min<int64_t>(32 * round, std::max<int64_t>(2 * round, next_pow2(std::max<int64_t>(nnz / 16384, 1))));
+    int64_t target = next_pow2(std::max<int64_t>(nnz / 16384, 1));
+    target = std::min<int64_t>(std::max<int64_t>(32 * round, 256), std::max<int64_t>({2 * round, 256, target}));
     // Tuning overrides (not part of the interface): TCA_TARGET sets the
     // per-task length, TCA_WIDE=0 disables workgroup-shared rows,
     // TCA_MULTI sets the multi-task row-length limit.
@@ -225,14 +234,14 @@ extern "C" int tca_condense_windows(const int32_t* rowptr, const int32_t* colidx
     return TCA_OK;
 }
 
-extern "C" int tca_plan_row_tasks(const int32_t* rowptr, int32_t M, int32_t N, int32_t dtype, int32_t* n_tasks,
+extern "C" int tca_plan_row_tasks(const int32_t* rowptr, int32_t M, int32_t K, int32_t N, int32_t dtype, int32_t* n_tasks,
                                   int32_t* n_perm, int32_t* n_long, int32_t* tasks, int32_t* perm, int32_t* longrows,
                                   int32_t* geometry) {
     using namespace tca;
-    if (!rowptr || M < 0 || N < 1 || !dtype_ok(dtype) || !n_tasks || !n_perm || !n_long)
+    if (!rowptr || M < 0 || K < 1 || N < 1 || !dtype_ok(dtype) || !n_tasks || !n_perm || !n_long)
         return fail(TCA_ERR_INVALID, "tca_plan_row_tasks: bad argument");
     RowPlan p;
-    plan_rows(rowptr, M, N, static_cast<int32_t>(dtype_size(dtype)), {}, 0, &p);
+    plan_rows(rowptr, M, N, static_cast<int32_t>(dtype_size(dtype)), {}, default_slices(K, N, dtype), &p);
     if (tasks) {
         if (*n_tasks < static_cast<int32_t>(p.tasks.size()) || *n_perm < static_cast<int32_t>(p.perm.size()) ||
             *n_long < static_cast<int32_t>(p.longrows.size()) || !perm || !longrows)

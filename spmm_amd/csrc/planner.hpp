@@ -74,6 +74,11 @@ struct MfmaPlan {
 void plan_mfma(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_t N, int32_t dtype, bool force,
                bool disable, double min_density, MfmaPlan* p);
 
+// Column chunks per XCD pay only when B overflows the L2s: 0 (automatic
+// chunking) when B is larger than 8 MiB, else 1.  TCA_SLICES (tuning only)
+// forces the number of chunks.
+int32_t default_slices(int32_t K, int32_t N, int32_t dtype);
+
 // Lane geometry for width N and value size `es` bytes: the widest vector
 // (<= 16 bytes) whose element count divides N, and the column chunks: up to
 // 8 chunks of at least 128 bytes (one L2 line of B per chunk row), at most

@@ -22,9 +22,6 @@ using namespace tca;
             return fail(TCA_ERR_HIP, "%s failed: %s (%s:%d)", #expr, hipGetErrorString(e_), __FILE__, __LINE__); \
     } while (0)
 
-// Column chunks per XCD are used when B is larger than this.
-constexpr uint64_t kSliceBytes = 8ull << 20;
-
 struct tca_spmm_plan {
     int32_t M = 0, K = 0, N = 0, nnz = 0, dtype = 0;
     uint32_t flags = 0;
@@ -212,11 +209,8 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
     plan_mfma(rowptr, colidx, M, N, dtype, (flags & TCA_PLAN_FORCE_MFMA) != 0, (flags & TCA_PLAN_NO_MFMA) != 0,
               md ? std::atof(md) : kMfmaMinDensity, &p->mfma);
     p->mfma_col_blocks = (N + kTileCols - 1) / kTileCols;
-    // Column chunks per XCD only pay when B overflows the L2s; TCA_SLICES
-    // (tuning only) forces the number of chunks.
-    const char* sl = std::getenv("TCA_SLICES");
-    const int32_t slices = sl ? std::atoi(sl) : (b_bytes > kSliceBytes ? 0 : 1);
-    plan_rows(rowptr, M, N, static_cast<int32_t>(dtype_size(dtype)), p->mfma.row_mfma, slices, &p->rows);
+    plan_rows(rowptr, M, N, static_cast<int32_t>(dtype_size(dtype)), p->mfma.row_mfma, default_slices(K, N, dtype),
+              &p->rows);
     p->ntasks = static_cast<int32_t>(p->rows.tasks.size());
     const size_t n_seg_total =
         p->rows.longrows.empty() ? 0 : static_cast<size_t>(p->rows.longrows.back().y + p->rows.longrows.back().z);

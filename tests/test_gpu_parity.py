@@ -167,7 +167,8 @@ def test_mfma_and_row_paths_agree(torch_cuda):
         with S.Plan(a, 256, flags) as pl:
             nwin = pl.info()["n_windows_mfma"]
             outs[flags] = run_gpu(torch_cuda, a, b, plan=pl)
-        assert (nwin > 0) == (flags != S.TCA_PLAN_NO_MFMA)
+        if flags != S.TCA_PLAN_DEFAULT:
+            assert (nwin > 0) == (flags == S.TCA_PLAN_FORCE_MFMA)
     assert np.array_equal(outs[S.TCA_PLAN_NO_MFMA], outs[S.TCA_PLAN_FORCE_MFMA])
     assert np.array_equal(outs[S.TCA_PLAN_DEFAULT], oracle_c(a, b))
 
