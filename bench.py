@@ -41,6 +41,12 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline time budget")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--flags", type=int, default=0, help="plan flags (1 = no MFMA, 2 = force MFMA)")
+    ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
+                    help="before timing, run one device-to-device copy of MIB MiB (a known-size kernel to "
+                         "scale rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
+    ap.add_argument("--traffic-kib", type=float, nargs=2, default=None, metavar=("FETCH", "WRITE"),
+                    help="measured FETCH_SIZE and WRITE_SIZE of the dominant kernel per launch, already scaled "
+                         "by the copy calibration (KiB); reported as roofline.traffic in bytes")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
@@ -73,6 +79,12 @@ def main():
     info = plan.info()
     log("plan:", json.dumps(info))
     stream = torch.cuda.current_stream()
+    if args.calib_copy > 0:
+        src = torch.empty(args.calib_copy << 18, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     torch.cuda.synchronize()
 
     # Timed region: W warm-up steps, then K steps between hipEvents recorded on
@@ -135,7 +147,9 @@ def main():
         "config": {"workload": WORKLOADS[args.config], "M": m, "K": k, "N": n, "nnz": nnz,
                    "bytes_alg": bytes_alg, "hbm_gbs": round(achieved, 2), "plan_ms": round(info["plan_ms"], 3)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": None},
+                     "frac": round(achieved / HBM_PEAK_GBS, 5),
+                     "traffic": (int(round((args.traffic_kib[0] + args.traffic_kib[1]) * 1024))
+                                 if args.traffic_kib else None)},
         "cpu_baseline": cpu,
     }
     plan.close()
