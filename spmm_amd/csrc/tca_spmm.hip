@@ -29,6 +29,7 @@ struct tca_spmm_plan {
     RowPlan rows;
     MfmaPlan mfma;
     int32_t mfma_col_blocks = 0;
+    int32_t mfma_slots = 1;  // entries per thread and step in the MFMA kernel (1, 2 or 4)
     int4* d_windows = nullptr;
     int* d_ucols = nullptr;
     int* d_eoff = nullptr;
@@ -135,12 +136,28 @@ int launch_mfma(const tca_spmm_plan* p, const void* val, const void* B, float* C
     a.col_blocks = p->mfma_col_blocks;
     a.val_bytes = static_cast<uint32_t>(static_cast<uint64_t>(p->nnz) * 2);
     a.B_bytes = static_cast<uint32_t>(static_cast<uint64_t>(p->K) * p->N * 2);
+    // The device entry array ends with one kNoEntry sentinel.
+    a.sentinel = static_cast<int>(p->mfma.entries.size());
+    a.entries_bytes = static_cast<uint32_t>((p->mfma.entries.size() + 1) * 4);
+    a.ucols_bytes = static_cast<uint32_t>(p->mfma.ucols.size() * 4);
+    a.eoff_bytes = static_cast<uint32_t>(p->mfma.eoff.size() * 4);
     const dim3 grid(static_cast<unsigned>(p->mfma.windows.size()) * p->mfma_col_blocks);
-    if (p->dtype == TCA_BF16)
-        hipLaunchKernelGGL(mfma_tile_kernel<true>, grid, dim3(256), 0, s, a);
-    else
-        hipLaunchKernelGGL(mfma_tile_kernel<false>, grid, dim3(256), 0, s, a);
-    return TCA_OK;
+    const bool bf = p->dtype == TCA_BF16;
+    switch (p->mfma_slots) {
+        case 1:
+            if (bf) hipLaunchKernelGGL((mfma_tile_kernel<true, 1>), grid, dim3(kMfmaThreads), 0, s, a);
+            else hipLaunchKernelGGL((mfma_tile_kernel<false, 1>), grid, dim3(kMfmaThreads), 0, s, a);
+            return TCA_OK;
+        case 2:
+            if (bf) hipLaunchKernelGGL((mfma_tile_kernel<true, 2>), grid, dim3(kMfmaThreads), 0, s, a);
+            else hipLaunchKernelGGL((mfma_tile_kernel<false, 2>), grid, dim3(kMfmaThreads), 0, s, a);
+            return TCA_OK;
+        case 4:
+            if (bf) hipLaunchKernelGGL((mfma_tile_kernel<true, 4>), grid, dim3(kMfmaThreads), 0, s, a);
+            else hipLaunchKernelGGL((mfma_tile_kernel<false, 4>), grid, dim3(kMfmaThreads), 0, s, a);
+            return TCA_OK;
+        default: return fail(TCA_ERR_INVALID, "bad MFMA slot count %d", p->mfma_slots);
+    }
 }
 
 int launch_rows(const tca_spmm_plan* p, const void* val, const void* B, float* C, hipStream_t s) {
@@ -209,6 +226,11 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
     plan_mfma(rowptr, colidx, M, N, dtype, (flags & TCA_PLAN_FORCE_MFMA) != 0, (flags & TCA_PLAN_NO_MFMA) != 0,
               md ? std::atof(md) : kMfmaMinDensity, &p->mfma);
     p->mfma_col_blocks = (N + kTileCols - 1) / kTileCols;
+    {
+        int32_t most = 0;
+        for (size_t i = 0; i + 1 < p->mfma.eoff.size(); i++) most = std::max(most, p->mfma.eoff[i + 1] - p->mfma.eoff[i]);
+        p->mfma_slots = most <= 256 ? 1 : most <= 512 ? 2 : 4;
+    }
     plan_rows(rowptr, M, N, static_cast<int32_t>(dtype_size(dtype)), p->mfma.row_mfma, default_slices(K, N, dtype),
               &p->rows);
     p->ntasks = static_cast<int32_t>(p->rows.tasks.size());
@@ -231,7 +253,11 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
     if ((st = dev_upload(&p->d_ucols, p->mfma.ucols.data(), p->mfma.ucols.size()))) return bail(st);
     if ((st = dev_upload(&p->d_eoff, p->mfma.eoff.data(), p->mfma.windows.empty() ? 0 : p->mfma.eoff.size())))
         return bail(st);
-    if ((st = dev_upload(&p->d_entries, p->mfma.entries.data(), p->mfma.entries.size()))) return bail(st);
+    if (!p->mfma.windows.empty()) {
+        std::vector<uint32_t> ent(p->mfma.entries);
+        ent.push_back(kNoEntry);
+        if ((st = dev_upload(&p->d_entries, ent.data(), ent.size()))) return bail(st);
+    }
     if (hipDeviceSynchronize() != hipSuccess) return bail(fail(TCA_ERR_HIP, "hipDeviceSynchronize failed"));
 
     tca_plan_info& in = p->info;
@@ -259,8 +285,12 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
     in.nnz_mfma = p->mfma.nnz;
     in.cond_cols_mfma = p->mfma.cond_cols;
     in.mfma_blocks = in.n_windows_mfma * p->mfma_col_blocks;
-    in.mfma_blockdim = 256;
-    in.mfma_lds_bytes = static_cast<int32_t>(3 * (kWinRows * kAStride + kStepK * kBStride) * sizeof(uint16_t));
+    in.mfma_blockdim = kMfmaThreads;
+    {
+        const int depth = p->mfma_slots >= 4 ? MfmaDepth<4>::kDepth : MfmaDepth<1>::kDepth;
+        in.mfma_lds_bytes = static_cast<int32_t>(2 * (3 * (kATile + 256) + 2 * kStepK * kBRow) * sizeof(uint16_t) +
+                                                 2 * (2 * depth * kStepK + 2 * depth + 1) * sizeof(int));
+    }
     in.scratch_bytes = static_cast<int64_t>(n_seg_total * N * sizeof(float));
     in.plan_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
     *plan = p;
