@@ -58,6 +58,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "row_kernel.hpp"
 
 namespace tca {
@@ -70,7 +72,7 @@ constexpr int kATile = kWinRows * kStepK;  // halves of one A tile (fragment ord
 constexpr int kBRow = kTileCols;           // halves per B-tile row in LDS (256 bytes)
 
 // A-tile cell of (row, step column): row block, 8-column group, row, column.
-__device__ __forceinline__ int a_cell(int r, int k) {
+__host__ __device__ inline int a_cell(int r, int k) {
     return (r >> 4) * 512 + (k >> 3) * 128 + (r & 15) * 8 + (k & 7);
 }
 // Piece permutation of B-tile row r (even, so a 32-byte pair of pieces stays together).
@@ -84,17 +86,18 @@ typedef int i32x4v __attribute__((ext_vector_type(4)));
 typedef int i32x2v __attribute__((ext_vector_type(2)));
 
 struct MfmaArgs {
-    const int4* windows;     // {first row, steps, first global step, first nonzero}
-    const int* ucols;        // [global step][32] B row per condensed column, -1 = padding
+    const int4* windows;     // {first row, steps, first global step, first nonzero (unused here)}
+    const uint32_t* ucols;   // [global step][32] byte offset of the B row of each condensed column
+                             // (row * N * 2), 0xffffffff = padding
     const int* eoff;         // [global step + 1] entry range of each step
-    const uint32_t* entries; // row (6 bits) | step column << 6 | (nonzero - first nonzero) << 11
-    const void* val;
+    const uint32_t* packed;  // per entry: a_cell(row, step column) | value bits << 16
+                             // (written each run by mfma_pack_kernel), then one kNoEntry sentinel
     const void* B;
     float* C;
     int M, N;
     int col_blocks;          // blockIdx.x = window * col_blocks + column block
-    uint32_t val_bytes, B_bytes, entries_bytes, ucols_bytes, eoff_bytes;
-    int sentinel;            // index of an entry equal to kNoEntry, loaded for empty slots
+    uint32_t B_bytes, packed_bytes, ucols_bytes, eoff_bytes;
+    int sentinel;            // index of the kNoEntry entry, loaded for empty slots
 };
 
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
@@ -103,70 +106,110 @@ typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 // producer's register staging must leave room for two wavefronts per SIMD.
 template <int kSlots>
 struct MfmaDepth {
-    static constexpr int kDepth = kSlots == 1 ? 16 : 8;  // unroll, meta chunk, entry lookahead (pairs)
-    static constexpr int kDataDepth = kDepth / 2;        // B and value lookahead (pairs)
+    static constexpr int kSteps = kSlots == 4 ? 2 : 4;  // steps per iteration (one barrier each)
+    static constexpr int kDepth = 8;      // unroll and meta chunk (iterations)
+    static constexpr int kDataDepth = 4;  // entry and B lookahead (iterations)
 };
 
 constexpr int kMfmaThreads = 512;  // 4 consumer + 4 producer wavefronts
 
+// Per run: pair each MFMA entry's A-tile cell with its value, in step order,
+// so the tile kernel loads one coalesced word per nonzero (the values are
+// read once here instead of once per column block).  The MFMA windows'
+// nonzeros are walked in CSR order: runs of consecutive windows form
+// segments {first nonzero, count, first walk index}, so every load is
+// coalesced and independent of other loads; only the stores scatter.
+__global__ __launch_bounds__(256) void mfma_pack_kernel(const int4* __restrict__ segs, int nsegs,
+                                                        const int* __restrict__ dst, const uint16_t* __restrict__ cell,
+                                                        int n, const uint16_t* __restrict__ val,
+                                                        uint32_t* __restrict__ packed) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    int lo = 0, hi = nsegs - 1;  // last segment with first walk index <= i
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (segs[mid].z <= i) lo = mid;
+        else hi = mid - 1;
+    }
+    const int4 sg = segs[lo];
+    packed[dst[i]] = static_cast<uint32_t>(cell[i]) | (static_cast<uint32_t>(val[sg.x + (i - sg.z)]) << 16);
+}
+
+// Static LDS of mfma_tile_kernel<*, kSlots> in bytes.
+template <int kSlots>
+constexpr int mfma_lds_bytes() {
+    constexpr int KS = MfmaDepth<kSlots>::kSteps, R = MfmaDepth<kSlots>::kDepth;
+    return KS * 3 * (kATile + 256) * 2 + KS * 2 * kStepK * kBRow * 2 + 2 * kStepK * (R * KS + 4) * 4 + 2 * (R * KS + 4) * 4;
+}
+
 template <bool kBf16, int kSlots>
 __global__ __launch_bounds__(kMfmaThreads) void mfma_tile_kernel(MfmaArgs a) {
+    constexpr int KS = MfmaDepth<kSlots>::kSteps;
     constexpr int R = MfmaDepth<kSlots>::kDepth;
     constexpr int D = MfmaDepth<kSlots>::kDataDepth;
-    static_assert(R <= 16 && R % 4 == 0 && D >= 3 && D < R && R % D == 0, "pipeline shape");
-    constexpr int kAElems = kATile + 256;  // A tile + one dummy cell per producer thread
+    static_assert(D >= 2 && D < R && R % D == 0, "pipeline shape");
+    constexpr int kAElems = kATile + 256;         // A tile + one dummy cell per producer thread
     constexpr int kBElems = kStepK * kBRow;
-    constexpr int kMI = R / 4;             // meta B-row indices per producer thread
-    __shared__ __attribute__((aligned(16))) uint16_t As[2][3][kAElems];  // [step parity][ring]
-    __shared__ __attribute__((aligned(16))) uint16_t Bs[2][2][kBElems];  // [step parity][ring]
-    __shared__ __attribute__((aligned(16))) int metaU[2][2 * R * kStepK];
-    __shared__ int metaE[2][2 * R + 1];
+    constexpr int kChunkU = R * KS * kStepK;      // B row offsets per meta chunk
+    static_assert(kChunkU % 256 == 0, "meta chunk split over the producers");
+    constexpr int kMI = kChunkU / 256;            // ... per producer thread
+    __shared__ __attribute__((aligned(16))) uint16_t As[KS][3][kAElems];  // [step in iteration][ring]
+    __shared__ __attribute__((aligned(16))) uint16_t Bs[KS][2][kBElems];  // [step in iteration][ring]
+    // Meta chunks are stored B-row-major ([row][step of the chunk], rows padded
+    // by 4) so that one iteration's KS row offsets of a producer are one read.
+    constexpr int kMetaRow = R * KS + 4;
+    __shared__ __attribute__((aligned(16))) uint32_t metaU[2][kStepK * kMetaRow];
+    __shared__ __attribute__((aligned(16))) int metaE[2][R * KS + 4];
 
     const int t = threadIdx.x;
     const int cb = blockIdx.x % a.col_blocks;
     const int4 win = a.windows[blockIdx.x / a.col_blocks];
-    const int row0 = win.x, nsteps = win.y, sbase = win.z, nzbase = win.w;
+    const int row0 = win.x, nsteps = win.y, sbase = win.z;
     __builtin_assume(nsteps >= 1);
     const int c0 = cb * kTileCols;
-    const int npairs = (nsteps + 1) / 2;
-    // Block blk = iterations [(blk - 1)R, blk R); iteration i computes pair i.
-    // Block 0 (the pipeline fill) is peeled off the loop so the loop is entered
-    // with the same loads in flight as at its back edge.  Blocks run whole
-    // (iterations past the last step only move zeros), so the loop has a
-    // single exit and both roles pass the same barriers.
-    const int nblocks = (npairs + R - 1) / R + 1;
+    const int niters = (nsteps + KS - 1) / KS;
+    // Block blk = iterations [(blk - 1)R, blk R); iteration i computes steps
+    // [KS i, KS i + KS).  Block 0 (the pipeline fill; only its last D iterations
+    // run) is peeled off the loop so the loop is entered with the same loads in
+    // flight as at its back edge.
+    // Blocks run whole (iterations past the last step only move zeros), so the
+    // loop has a single exit and both roles pass the same barriers.
+    const int nblocks = (niters + R - 1) / R + 1;
 
-    // Meta chunk c = pairs [cR, cR + R) = steps [2cR, 2cR + 2R): producer p
-    // holds B row indices kMI p .. kMI p + kMI - 1 of the chunk and, for
-    // p <= 2R, entry offset p.  Buffer loads: lanes past the window read
-    // zeros without a branch.
+    // Meta chunk c = iterations [cR, cR + R) = steps [KS cR, KS cR + KS R):
+    // producer p holds B row offsets kMI p .. kMI p + kMI - 1 of the chunk and,
+    // for p <= KS R, entry offset p.  Buffer loads: lanes past the window read
+    // zeros without a branch (a zero row offset is never used: see ucol below).
     const int p = t - 256;  // producer thread index (valid for t >= 256)
     const __amdgpu_buffer_rsrc_t rU = make_rsrc(a.ucols, a.ucols_bytes);
     const __amdgpu_buffer_rsrc_t rE = make_rsrc(a.eoff, a.eoff_bytes);
-    auto load_meta = [&](int c, int (&mu)[kMI], int& me) {
-        const int s0 = 2 * c * R;
+    auto load_meta = [&](int c, uint32_t (&mu)[kMI], int& me) {
+        const int s0 = KS * c * R;
 #pragma unroll
         for (int q = 0; q < kMI; q++) {
             const int idx = kMI * p + q;
             const uint32_t uo = static_cast<uint32_t>((sbase + s0) * kStepK + idx) * 4u;
-            mu[q] = static_cast<int>(
-                __builtin_amdgcn_raw_buffer_load_b32(rU, s0 + idx / kStepK < nsteps ? uo : kOob, 0, 0));
+            mu[q] = __builtin_amdgcn_raw_buffer_load_b32(rU, s0 + idx / kStepK < nsteps ? uo : kOob, 0, 0);
         }
         const uint32_t eo = static_cast<uint32_t>(sbase + s0 + p) * 4u;
         me = static_cast<int>(
-            __builtin_amdgcn_raw_buffer_load_b32(rE, (p <= 2 * R && s0 + p <= nsteps) ? eo : kOob, 0, 0));
+            __builtin_amdgcn_raw_buffer_load_b32(rE, (p <= KS * R && s0 + p <= nsteps) ? eo : kOob, 0, 0));
     };
-    auto store_meta = [&](int buf, const int (&mu)[kMI], int me) {
+    auto store_meta = [&](int buf, const uint32_t (&mu)[kMI], int me) {
 #pragma unroll
-        for (int q = 0; q < kMI; q++) metaU[buf][kMI * p + q] = mu[q];
-        if (p <= 2 * R) metaE[buf][p] = me;
+        for (int q = 0; q < kMI; q++) {
+            const int idx = kMI * p + q;  // chunk index: step idx / 32, B-tile row idx % 32
+            metaU[buf][(idx % kStepK) * kMetaRow + idx / kStepK] = mu[q];
+        }
+        if (p <= KS * R) metaE[buf][p] = me;
     };
 
     // Clear the A tiles; chunk 0 of the meta goes to LDS before the loop.
-    for (int i = t * 8; i < 2 * 3 * kAElems; i += kMfmaThreads * 8)
+    for (int i = t * 8; i < KS * 3 * kAElems; i += kMfmaThreads * 8)
         *reinterpret_cast<i32x4v*>(&As[0][0][0] + i) = i32x4v{0, 0, 0, 0};
     if (t >= 256) {
-        int mu[kMI], me;
+        uint32_t mu[kMI];
+        int me;
         load_meta(0, mu, me);
         store_meta(0, mu, me);
     }
@@ -181,7 +224,6 @@ __global__ __launch_bounds__(kMfmaThreads) void mfma_tile_kernel(MfmaArgs a) {
         for (int b = 0; b < 4; b++)
 #pragma unroll
             for (int c = 0; c < 2; c++) acc[b][c] = f32x4{0.f, 0.f, 0.f, 0.f};
-        i32x4v af[2][2][4], bfr[2][2][2];  // [iteration parity][step parity]
         // A: lane (i, h) = (lane % 16, lane / 16) holds row 16b + i, columns
         // 8h .. 8h+7 -- in fragment order that is the lane's own 16 bytes.
         // B: the transposing read of a 16-lane group h delivers rows 8h .. 8h+3
@@ -192,55 +234,63 @@ __global__ __launch_bounds__(kMfmaThreads) void mfma_tile_kernel(MfmaArgs a) {
         const int bpc = 4 * wave + ((li & 3) >> 1);   // 16-byte piece of column block 0
         const int b_off0 = br * kBRow + 8 * (bpc ^ bswz(br)) + 4 * (li & 1);
         const int b_off1 = br * kBRow + 8 * ((bpc + 2) ^ bswz(br)) + 4 * (li & 1);
-        auto run_block = [&](const int blk) {
+        auto run_block = [&](const int blk, auto first) {
 #pragma unroll
             for (int u = 0; u < R; u++) {
+                if constexpr (decltype(first)::value)
+                    if (u < R - D) continue;  // the fill needs only D iterations
                 const int i = (blk - 1) * R + u;
-                // MFMAs of steps 2i, 2i+1 on the fragments read last iteration.
-                // Steps past the window have zero tiles and add exact zeros.
+                // Steps KS i .. KS i + KS - 1 in order (tiles written last
+                // iteration); steps past the window have zero tiles and add
+                // exact zeros, so only the pipeline fill skips them.
                 if (i >= 0) {
+                    const int ar = (i + 3 * R) % 3;
+                    // Fragments of step sp + 1 are read while the MFMAs of step sp
+                    // run (two register sets); scheduling barriers keep the
+                    // compiler from sinking the reads below the MFMAs.
+                    i32x4v af[2][4], bfr[2][2];
+                    auto read_frags = [&](int sp, int set) {
+                        const uint16_t* Ab = &As[sp][ar][8 * lane];
 #pragma unroll
-                    for (int sp = 0; sp < 2; sp++)
+                        for (int b = 0; b < 4; b++) af[set][b] = *reinterpret_cast<const i32x4v*>(Ab + 512 * b);
+#pragma unroll
+                        for (int c = 0; c < 2; c++) {
+                            const uint16_t* Bp = &Bs[sp][i & 1][c == 0 ? b_off0 : b_off1];
+                            const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(Bp));
+                            const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(Bp + 4 * kBRow));
+                            bfr[set][c] = i32x4v{__builtin_bit_cast(int, __builtin_shufflevector(lo, lo, 0, 1)),
+                                                 __builtin_bit_cast(int, __builtin_shufflevector(lo, lo, 2, 3)),
+                                                 __builtin_bit_cast(int, __builtin_shufflevector(hi, hi, 0, 1)),
+                                                 __builtin_bit_cast(int, __builtin_shufflevector(hi, hi, 2, 3))};
+                        }
+                    };
+                    read_frags(0, 0);
+#pragma unroll
+                    for (int sp = 0; sp < KS; sp++) {
+                        if (sp + 1 < KS) read_frags(sp + 1, (sp + 1) & 1);
+                        __builtin_amdgcn_sched_barrier(0);
+                        const int set = sp & 1;
 #pragma unroll
                         for (int b = 0; b < 4; b++)
 #pragma unroll
                             for (int c = 0; c < 2; c++) {
                                 if constexpr (kBf16)
                                     acc[b][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                                        __builtin_bit_cast(bf16x8, af[u & 1][sp][b]),
-                                        __builtin_bit_cast(bf16x8, bfr[u & 1][sp][c]), acc[b][c], 0, 0, 0);
+                                        __builtin_bit_cast(bf16x8, af[set][b]), __builtin_bit_cast(bf16x8, bfr[set][c]),
+                                        acc[b][c], 0, 0, 0);
                                 else
                                     acc[b][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                                        __builtin_bit_cast(f16x8, af[u & 1][sp][b]),
-                                        __builtin_bit_cast(f16x8, bfr[u & 1][sp][c]), acc[b][c], 0, 0, 0);
+                                        __builtin_bit_cast(f16x8, af[set][b]), __builtin_bit_cast(f16x8, bfr[set][c]),
+                                        acc[b][c], 0, 0, 0);
                             }
-                }
-                // Fragments of pair i + 1 (written by the producers last iteration).
-                if (i + 1 >= 0) {
-                    const int nx = (u + 1) & 1;
-                    const int ar = (i + 1 + 3 * R) % 3;
-#pragma unroll
-                    for (int sp = 0; sp < 2; sp++) {
-                        const uint16_t* Ab = &As[sp][ar][8 * lane];
-#pragma unroll
-                        for (int b = 0; b < 4; b++) af[nx][sp][b] = *reinterpret_cast<const i32x4v*>(Ab + 512 * b);
-#pragma unroll
-                        for (int c = 0; c < 2; c++) {
-                            const uint16_t* Bp = &Bs[sp][(i + 1) & 1][c == 0 ? b_off0 : b_off1];
-                            const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(Bp));
-                            const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(Bp + 4 * kBRow));
-                            bfr[nx][sp][c] = i32x4v{__builtin_bit_cast(int, __builtin_shufflevector(lo, lo, 0, 1)),
-                                                    __builtin_bit_cast(int, __builtin_shufflevector(lo, lo, 2, 3)),
-                                                    __builtin_bit_cast(int, __builtin_shufflevector(hi, hi, 0, 1)),
-                                                    __builtin_bit_cast(int, __builtin_shufflevector(hi, hi, 2, 3))};
-                        }
+                        __builtin_amdgcn_sched_barrier(0);
                     }
                 }
                 __syncthreads();
             }
         };
-        run_block(0);
-        for (int blk = 1; blk < nblocks; blk++) run_block(blk);
+        run_block(0, std::true_type{});
+        for (int blk = 1; blk < nblocks; blk++) run_block(blk, std::false_type{});
         // Lane (i, h) holds rows 4h .. 4h+3 of row block b, column i of column block c.
 #pragma unroll
         for (int c = 0; c < 2; c++) {
@@ -257,109 +307,105 @@ __global__ __launch_bounds__(kMfmaThreads) void mfma_tile_kernel(MfmaArgs a) {
     } else {
         // ================= producer: loads and LDS staging =================
         const __amdgpu_buffer_rsrc_t rB = make_rsrc(a.B, a.B_bytes);
-        const __amdgpu_buffer_rsrc_t rval = make_rsrc(a.val, a.val_bytes);
-        const __amdgpu_buffer_rsrc_t rent = make_rsrc(a.entries, a.entries_bytes);
-        const uint32_t rowbytes = static_cast<uint32_t>(a.N) * 2u;
+        const __amdgpu_buffer_rsrc_t rent = make_rsrc(a.packed, a.packed_bytes);
         // B staging role: row p / 8 of a step, 16-byte pieces p % 8 and p % 8 + 8
         // (columns c0 + 8q and c0 + 64 + 8q).
         const int brow = p >> 3;
         const int bq = p & 7;
-        const bool bok0 = c0 + 8 * bq < a.N;
-        const bool bok1 = c0 + 64 + 8 * bq < a.N;
-        const uint32_t bcol = static_cast<uint32_t>(c0 + 8 * bq) * 2u;
+        const uint32_t bcol0 = c0 + 8 * bq < a.N ? static_cast<uint32_t>(c0 + 8 * bq) * 2u : kOob;
+        const uint32_t bcol1 = c0 + 64 + 8 * bq < a.N ? static_cast<uint32_t>(c0 + 64 + 8 * bq) * 2u : kOob;
         const int bw0 = brow * kBRow + 8 * (bq ^ bswz(brow));
         const int bw1 = brow * kBRow + 8 * ((bq + 8) ^ bswz(brow));
         // Every stage runs unconditionally (slots of steps outside the window
         // hold zeros / kNoEntry), so no load's register is conditionally consumed.
-        i32x4v breg[2][D][2];          // [step parity][pair % D]: B pieces
-        uint32_t ereg[2][R][kSlots];   // [step parity][pair % R]: entries
-        uint16_t vreg[2][D][kSlots];   // [step parity][pair % D]: values
+        i32x4v breg[KS][D][2];          // [step in iteration][iteration % D]: B pieces
+        uint32_t ereg[KS][D][kSlots];   // [step in iteration][iteration % D]: packed entries
 #pragma unroll
-        for (int sp = 0; sp < 2; sp++) {
+        for (int sp = 0; sp < KS; sp++)
 #pragma unroll
             for (int u = 0; u < D; u++) {
                 breg[sp][u][0] = breg[sp][u][1] = i32x4v{0, 0, 0, 0};
 #pragma unroll
-                for (int k = 0; k < kSlots; k++) vreg[sp][u][k] = 0;
-            }
-#pragma unroll
-            for (int u = 0; u < R; u++)
-#pragma unroll
                 for (int k = 0; k < kSlots; k++) ereg[sp][u][k] = kNoEntry;
-        }
-        // A cells scattered for pairs i and i + 1; an empty slot uses this
-        // thread's own dummy cell past the tile, which no MFMA reads.
+            }
+        // A cells scattered for the previous and current iteration; an empty
+        // slot uses this thread's own dummy cell past the tile, never read.
         const int pad = kATile + p;
-        int pos_prev[2][kSlots], pos_cur[2][kSlots];
+        int pos_prev[KS][kSlots], pos_cur[KS][kSlots];
 #pragma unroll
-        for (int sp = 0; sp < 2; sp++)
+        for (int sp = 0; sp < KS; sp++)
 #pragma unroll
             for (int k = 0; k < kSlots; k++) pos_prev[sp][k] = pos_cur[sp][k] = pad;
-        int mu_next[kMI], me_next;
+        uint32_t mu_next[kMI];
+        int me_next;
+        // Meta of the B / entry stage of iteration (blk, u): pairs of iteration
+        // (blk - 1)R + u + D, in chunk blk - 1 or blk (both in LDS during block blk).
+        using VecKS = int __attribute__((ext_vector_type(KS)));
+        VecKS ev_n, uv_n;
+        int el_n;
+        auto read_meta = [&](int blk, int u) {
+            const int pq = (u + D) % R;
+            const int mb = (u + D < R) ? ((blk - 1) & 1) : (blk & 1);
+            ev_n = *reinterpret_cast<const VecKS*>(&metaE[mb][KS * pq]);
+            el_n = metaE[mb][KS * pq + KS];
+            uv_n = *reinterpret_cast<const VecKS*>(&metaU[mb][brow * kMetaRow + KS * pq]);
+        };
+        read_meta(0, R - D);
 
-        auto run_block = [&](const int blk) {
+        auto run_block = [&](const int blk, auto first) {
             load_meta(blk + 1, mu_next, me_next);
 #pragma unroll
             for (int u = 0; u < R; u++) {
+                if constexpr (decltype(first)::value)
+                    if (u < R - D) continue;  // the fill needs only D iterations
                 const int i = (blk - 1) * R + u;
-                // ---- entries of pair i + R (meta chunk blk, position u)
-#pragma unroll
-                for (int sp = 0; sp < 2; sp++) {
-                    const int eb = metaE[blk & 1][2 * u + sp];
-                    const int ee = metaE[blk & 1][2 * u + sp + 1];
-#pragma unroll
-                    for (int k = 0; k < kSlots; k++) {
-                        const int e = eb + p + 256 * k;
-                        ereg[sp][u][k] = __builtin_amdgcn_raw_buffer_load_b32(
-                            rent, static_cast<uint32_t>(e < ee ? e : a.sentinel) * 4u, 0, 0);
-                    }
-                }
-                // ---- B pieces of pair i + D (meta chunk blk - 1 or blk)
-#pragma unroll
-                for (int sp = 0; sp < 2; sp++) {
-                    const int pq = (u + D) % R;  // position in its chunk
-                    const int mb = (u + D < R) ? ((blk - 1) & 1) : (blk & 1);
-                    const int j = 2 * (i + D) + sp;  // step
-                    const int ucol = (j >= 0 && j < nsteps) ? metaU[mb][(2 * pq + sp) * kStepK + brow] : -1;
-                    const uint32_t boff = ucol >= 0 ? static_cast<uint32_t>(ucol) * rowbytes + bcol : kOob;
-                    breg[sp][u % D][0] =
-                        __builtin_amdgcn_raw_buffer_load_b128(rB, (ucol >= 0 && bok0) ? boff : kOob, 0, 0);
-                    breg[sp][u % D][1] =
-                        __builtin_amdgcn_raw_buffer_load_b128(rB, (ucol >= 0 && bok1) ? boff + 128u : kOob, 0, 0);
-                }
-                // ---- values of pair i + D (its entries were issued R - D iterations ago)
-#pragma unroll
-                for (int sp = 0; sp < 2; sp++) {
-                    const int se = (u + D) % R;
-#pragma unroll
-                    for (int k = 0; k < kSlots; k++) {
-                        const uint32_t e = ereg[sp][se][k];
-                        const uint32_t off =
-                            e != kNoEntry ? (static_cast<uint32_t>(nzbase) + (e >> 11)) * 2u : kOob;
-                        vreg[sp][u % D][k] =
-                            __builtin_bit_cast(uint16_t, __builtin_amdgcn_raw_buffer_load_b16(rval, off, 0, 0));
-                    }
-                }
-                // ---- pair i + 2 to LDS (B ring i&1, A ring (i+2)%3); clear pair i's A cells
+                // ---- packed entries and B pieces of iteration i + D (meta chunk blk - 1 or
+                // blk).  The iteration's KS entry ranges and KS B row offsets were read
+                // from LDS during the previous iteration; the reads for the next
+                // iteration are issued now and complete under this one.
                 {
-                    const int a_wr = (i + 2 + 3 * R) % 3;
-                    const int a_cl = (i + 3 * R) % 3;
-                    const int sb = (u + 2) % D;
-                    const int se = (u + 2) % R;
+                    const VecKS ev = ev_n, uv = uv_n;
+                    const int e_last = el_n;
+                    if (u + 1 < R) read_meta(blk, u + 1);
+                    else read_meta(blk + 1, 0);
 #pragma unroll
-                    for (int sp = 0; sp < 2; sp++) {
-                        uint16_t* bs = &Bs[sp][i & 1][0];
+                    for (int sp = 0; sp < KS; sp++) {
+                        const int j = KS * (i + D) + sp;  // step
+                        const bool in = j >= 0 && j < nsteps;
+                        const int eb = in ? ev[sp] : 0;
+                        const int ee = in ? (sp + 1 < KS ? ev[(sp + 1) % KS] : e_last) : 0;
+#pragma unroll
+                        for (int k = 0; k < kSlots; k++) {
+                            const int e = eb + p + 256 * k;
+                            ereg[sp][u % D][k] = __builtin_amdgcn_raw_buffer_load_b32(
+                                rent, static_cast<uint32_t>(e < ee ? e : a.sentinel) * 4u, 0, 0);
+                        }
+                        // B row byte offset; 0xffffffff = padding column, or a step
+                        // outside the window (chunk -1 of the pipeline fill included).
+                        const uint32_t uo = in ? static_cast<uint32_t>(uv[sp]) : kNoEntry;
+                        breg[sp][u % D][0] =
+                            __builtin_amdgcn_raw_buffer_load_b128(rB, uo != kNoEntry ? uo + bcol0 : kOob, 0, 0);
+                        breg[sp][u % D][1] =
+                            __builtin_amdgcn_raw_buffer_load_b128(rB, uo != kNoEntry ? uo + bcol1 : kOob, 0, 0);
+                    }
+                }
+                // ---- iteration i + 1 to LDS (B ring (i+1)&1, A ring (i+1)%3); clear iteration i-1's A cells
+                {
+                    const int a_wr = (i + 1 + 3 * R) % 3;
+                    const int a_cl = (i + 2 + 3 * R) % 3;
+                    const int sb = (u + 1) % D;
+#pragma unroll
+                    for (int sp = 0; sp < KS; sp++) {
+                        uint16_t* bs = &Bs[sp][(i + 1) & 1][0];
                         *reinterpret_cast<i32x4v*>(bs + bw0) = breg[sp][sb][0];
                         *reinterpret_cast<i32x4v*>(bs + bw1) = breg[sp][sb][1];
 #pragma unroll
                         for (int k = 0; k < kSlots; k++) {
                             As[sp][a_cl][pos_prev[sp][k]] = 0;
-                            // An empty slot's value loaded as zero (out-of-range offset).
-                            const uint32_t e = ereg[sp][se][k];
-                            const int cell = a_cell(static_cast<int>(e & 63u), static_cast<int>((e >> 6) & 31u));
-                            const int m = -static_cast<int>(e != kNoEntry);
-                            const int pos = (cell & m) | (pad & ~m);
-                            As[sp][a_wr][pos] = vreg[sp][sb][k];
+                            const uint32_t e = ereg[sp][sb][k];
+                            const bool ok = e != kNoEntry;
+                            const int pos = ok ? static_cast<int>(e & 0xffffu) : pad;
+                            As[sp][a_wr][pos] = ok ? static_cast<uint16_t>(e >> 16) : uint16_t(0);
                             pos_prev[sp][k] = pos_cur[sp][k];
                             pos_cur[sp][k] = pos;
                         }
@@ -370,8 +416,8 @@ __global__ __launch_bounds__(kMfmaThreads) void mfma_tile_kernel(MfmaArgs a) {
                 __syncthreads();
             }
         };
-        run_block(0);
-        for (int blk = 1; blk < nblocks; blk++) run_block(blk);
+        run_block(0, std::true_type{});
+        for (int blk = 1; blk < nblocks; blk++) run_block(blk, std::false_type{});
     }
 }
 

@@ -167,7 +167,7 @@ void plan_mfma(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_t 
     std::vector<int32_t> ucols, cpos(rowptr[M]);
     condense(rowptr, colidx, M, kWin, &uoff, &ucols, &cpos);
     const int32_t nw = (M + kWin - 1) / kWin;
-    std::vector<uint8_t> take(nw, 0);
+    std::vector<uint8_t> take(nw, 0), ok(nw, 0);  // routed / structurally able
 #pragma omp parallel for schedule(dynamic, 16)
     for (int32_t w = 0; w < nw; w++) {
         const int32_t r0 = w * kWin, r1 = std::min(M, r0 + kWin);
@@ -180,7 +180,31 @@ void plan_mfma(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_t 
         for (int32_t j = rowptr[r0]; j < rowptr[r1]; j++) per[cpos[j] / kStep]++;
         if (*std::max_element(per.begin(), per.end()) > kMaxStep) continue;
         const double density = static_cast<double>(nz) / (static_cast<double>(r1 - r0) * steps * kStep);
+        ok[w] = 1;
         if (force || density >= min_density) take[w] = 1;
+    }
+    if (!force) {
+        // Cost model over the eligible set (see planner.hpp).
+        int64_t n_take = 0, nz_take = 0, max_steps = 0;
+        for (int32_t w = 0; w < nw; w++) {
+            if (!take[w]) continue;
+            const int32_t r0 = w * kWin, r1 = std::min(M, r0 + kWin);
+            n_take++;
+            nz_take += rowptr[r1] - rowptr[r0];
+            max_steps = std::max<int64_t>(max_steps, (uoff[w + 1] - uoff[w] + kStep - 1) / kStep);
+        }
+        const int64_t wgs = n_take * ((N + 127) / 128);
+        const int64_t rounds = (wgs + 255) / 256;
+        const double t_tile = kMfmaFixedUs + static_cast<double>(rounds) * ((max_steps + 3) / 4 + 4) * kMfmaIterUs;
+        const double t_row = static_cast<double>(nz_take) * N * 2.0 / kRowGatherBytesPerUs;
+        if (n_take > 0 && t_tile >= t_row) {
+            std::fill(take.begin(), take.end(), 0);
+        } else if (n_take > 0 && static_cast<double>(nz_take) >= 0.95 * rowptr[M]) {
+            // Nearly everything goes to the tile kernel: take the remaining
+            // qualifying windows too rather than launch the row kernel for a
+            // few rows (the launch alone costs more than their tiles).
+            std::copy(ok.begin(), ok.end(), take.begin());
+        }
     }
     for (int32_t w = 0; w < nw; w++) {
         if (!take[w]) continue;

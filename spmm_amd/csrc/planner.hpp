@@ -50,11 +50,23 @@ struct RowPlan {
 // entries[eoff[g] .. eoff[g + 1]) with g its global step; an entry packs the
 // row within the window (6 bits), the column within the step (5 bits, bit 6)
 // and the nonzero index minus the window's first nonzero (bit 11 up).
-// Default routing threshold: windows whose condensed tiles are at least this
-// dense run on the MFMA tile kernel.  Measured crossover on MI355X (4096 x
-// 4096 Bernoulli, fp16, N = 512): the tile kernel is 3.1x slower than the
-// row kernel at density 0.05, equal near 0.2 and 1.9x faster at 0.4.
-constexpr double kMfmaMinDensity = 0.25;
+// Routing.  A window is eligible for the MFMA tile kernel when its condensed
+// tile density nnz / (rows * padded |U|) is at least kMfmaMinDensity.  The
+// eligible windows then go to the tile kernel as a set when a cost model
+// predicts it beats the row kernel on them:
+//   tile kernel  ~ kMfmaFixedUs + rounds * (max steps / 4 + 4) * kMfmaIterUs
+//                  (rounds = ceil(workgroups / 256): one workgroup per CU;
+//                   4 steps per iteration plus a 4-iteration pipeline fill),
+//   row kernel   ~ eligible nnz * N * value size / kRowGatherBytesPerUs
+//                  (B-row gathers through L2).
+// Constants measured on MI355X (fp16, 4096-row lognormal and Bernoulli
+// matrices, N = 256 / 512): an iteration of 4 steps takes ~0.95 us per
+// workgroup; the row kernel sustains ~20 TB/s of gathered B rows; density
+// below ~0.04 never paid.
+constexpr double kMfmaMinDensity = 0.04;
+constexpr double kMfmaFixedUs = 3.0;
+constexpr double kMfmaIterUs = 0.95;
+constexpr double kRowGatherBytesPerUs = 20.0e6;
 
 struct MfmaPlan {
     std::vector<Int4> windows;
@@ -67,10 +79,10 @@ struct MfmaPlan {
     int32_t rows = 0;
 };
 
-// Windows whose condensed tile density nnz / (rows * padded |U|) is at least
-// min_density (all eligible windows with force, none with disable).  Only for
-// fp16 / bf16 and N % 8 == 0; a window qualifies only while its nonzeros
-// fit the entry encoding (< 2^21) and no step holds more than 1024 of them.
+// Windows routed by the rule above (min_density replaces kMfmaMinDensity; with
+// force every qualifying window, with disable none).  Only for fp16 / bf16 and
+// N % 8 == 0; a window qualifies only while its nonzeros fit the entry
+// encoding (< 2^21) and no step holds more than 1024 of them.
 void plan_mfma(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_t N, int32_t dtype, bool force,
                bool disable, double min_density, MfmaPlan* p);
 

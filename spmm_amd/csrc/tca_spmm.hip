@@ -31,9 +31,13 @@ struct tca_spmm_plan {
     int32_t mfma_col_blocks = 0;
     int32_t mfma_slots = 1;  // entries per thread and step in the MFMA kernel (1, 2 or 4)
     int4* d_windows = nullptr;
-    int* d_ucols = nullptr;
+    uint32_t* d_ucols = nullptr;
     int* d_eoff = nullptr;
-    uint32_t* d_entries = nullptr;
+    int4* d_pk_seg = nullptr;       // runs of consecutive MFMA windows: {first nonzero, count, first walk index, 0}
+    int32_t n_pk_seg = 0;
+    int* d_pk_dst = nullptr;        // MFMA nonzeros in CSR order: entry (step-order) position
+    uint16_t* d_pk_cell = nullptr;  // ... its A-tile cell
+    uint32_t* d_packed = nullptr;   // cell | value << 16 per entry (rewritten each run) + sentinel
     int32_t ntasks = 0;
     int* d_rowptr = nullptr;
     int* d_colidx = nullptr;
@@ -74,7 +78,10 @@ void free_plan_device(tca_spmm_plan* p) {
     (void)hipFree(p->d_windows);
     (void)hipFree(p->d_ucols);
     (void)hipFree(p->d_eoff);
-    (void)hipFree(p->d_entries);
+    (void)hipFree(p->d_pk_seg);
+    (void)hipFree(p->d_pk_dst);
+    (void)hipFree(p->d_pk_cell);
+    (void)hipFree(p->d_packed);
 }
 
 template <typename T, int E>
@@ -127,18 +134,20 @@ int launch_mfma(const tca_spmm_plan* p, const void* val, const void* B, float* C
     a.windows = p->d_windows;
     a.ucols = p->d_ucols;
     a.eoff = p->d_eoff;
-    a.entries = p->d_entries;
-    a.val = val;
+    a.packed = p->d_packed;
     a.B = B;
     a.C = C;
     a.M = p->M;
     a.N = p->N;
     a.col_blocks = p->mfma_col_blocks;
-    a.val_bytes = static_cast<uint32_t>(static_cast<uint64_t>(p->nnz) * 2);
     a.B_bytes = static_cast<uint32_t>(static_cast<uint64_t>(p->K) * p->N * 2);
-    // The device entry array ends with one kNoEntry sentinel.
-    a.sentinel = static_cast<int>(p->mfma.entries.size());
-    a.entries_bytes = static_cast<uint32_t>((p->mfma.entries.size() + 1) * 4);
+    // The packed entry array ends with one kNoEntry sentinel (set at plan time).
+    const int n_ent = static_cast<int>(p->mfma.entries.size());
+    a.sentinel = n_ent;
+    a.packed_bytes = static_cast<uint32_t>((static_cast<uint64_t>(n_ent) + 1) * 4);
+    if (n_ent > 0)
+        hipLaunchKernelGGL(mfma_pack_kernel, dim3((n_ent + 255) / 256), dim3(256), 0, s, p->d_pk_seg, p->n_pk_seg,
+                           p->d_pk_dst, p->d_pk_cell, n_ent, static_cast<const uint16_t*>(val), p->d_packed);
     a.ucols_bytes = static_cast<uint32_t>(p->mfma.ucols.size() * 4);
     a.eoff_bytes = static_cast<uint32_t>(p->mfma.eoff.size() * 4);
     const dim3 grid(static_cast<unsigned>(p->mfma.windows.size()) * p->mfma_col_blocks);
@@ -250,13 +259,42 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
     if ((st = dev_upload(&p->d_longrows, p->rows.longrows.data(), p->rows.longrows.size()))) return bail(st);
     if ((st = dev_upload(&p->d_partials, nullptr, n_seg_total * N))) return bail(st);
     if ((st = dev_upload(&p->d_windows, p->mfma.windows.data(), p->mfma.windows.size()))) return bail(st);
-    if ((st = dev_upload(&p->d_ucols, p->mfma.ucols.data(), p->mfma.ucols.size()))) return bail(st);
-    if ((st = dev_upload(&p->d_eoff, p->mfma.eoff.data(), p->mfma.windows.empty() ? 0 : p->mfma.eoff.size())))
-        return bail(st);
     if (!p->mfma.windows.empty()) {
-        std::vector<uint32_t> ent(p->mfma.entries);
-        ent.push_back(kNoEntry);
-        if ((st = dev_upload(&p->d_entries, ent.data(), ent.size()))) return bail(st);
+        // Device forms: B row byte offsets (padding 0xffffffff); per entry its
+        // fragment-order A-tile cell and nonzero index (the pack kernel pairs
+        // them with the run's values), and the packed array's kNoEntry sentinel.
+        std::vector<uint32_t> uoff(p->mfma.ucols.size());
+        for (size_t i = 0; i < uoff.size(); i++)
+            uoff[i] = p->mfma.ucols[i] < 0 ? kNoEntry
+                                            : static_cast<uint32_t>(p->mfma.ucols[i]) * static_cast<uint32_t>(N) * 2u;
+        if ((st = dev_upload(&p->d_ucols, uoff.data(), uoff.size()))) return bail(st);
+        if ((st = dev_upload(&p->d_eoff, p->mfma.eoff.data(), p->mfma.eoff.size()))) return bail(st);
+        const size_t ne = p->mfma.entries.size();
+        std::vector<int> dst(ne);
+        std::vector<uint16_t> cell(ne);
+        std::vector<uint32_t> packed(ne + 1, 0u);
+        std::vector<int4> segs;
+        for (size_t w = 0, e = 0, base = 0; w < p->mfma.windows.size(); w++) {
+            // The window's entries, indexed by their offset in its CSR range.
+            const Int4 win = p->mfma.windows[w];
+            const size_t e_end = static_cast<size_t>(p->mfma.eoff[win.z + win.y]);
+            const size_t cnt = e_end - e;
+            if (!segs.empty() && segs.back().x + segs.back().y == win.w) segs.back().y += static_cast<int>(cnt);
+            else segs.push_back(int4{win.w, static_cast<int>(cnt), static_cast<int>(base), 0});
+            for (; e < e_end; e++) {
+                const uint32_t en = p->mfma.entries[e];
+                const size_t k = base + (en >> 11);
+                dst[k] = static_cast<int>(e);
+                cell[k] = static_cast<uint16_t>(a_cell(static_cast<int>(en & 63u), static_cast<int>((en >> 6) & 31u)));
+            }
+            base += cnt;
+        }
+        packed[ne] = kNoEntry;
+        p->n_pk_seg = static_cast<int32_t>(segs.size());
+        if ((st = dev_upload(&p->d_pk_seg, segs.data(), segs.size()))) return bail(st);
+        if ((st = dev_upload(&p->d_pk_dst, dst.data(), ne))) return bail(st);
+        if ((st = dev_upload(&p->d_pk_cell, cell.data(), ne))) return bail(st);
+        if ((st = dev_upload(&p->d_packed, packed.data(), ne + 1))) return bail(st);
     }
     if (hipDeviceSynchronize() != hipSuccess) return bail(fail(TCA_ERR_HIP, "hipDeviceSynchronize failed"));
 
@@ -286,11 +324,7 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
     in.cond_cols_mfma = p->mfma.cond_cols;
     in.mfma_blocks = in.n_windows_mfma * p->mfma_col_blocks;
     in.mfma_blockdim = kMfmaThreads;
-    {
-        const int depth = p->mfma_slots >= 4 ? MfmaDepth<4>::kDepth : MfmaDepth<1>::kDepth;
-        in.mfma_lds_bytes = static_cast<int32_t>(2 * (3 * (kATile + 256) + 2 * kStepK * kBRow) * sizeof(uint16_t) +
-                                                 2 * (2 * depth * kStepK + 2 * depth + 1) * sizeof(int));
-    }
+    in.mfma_lds_bytes = p->mfma_slots == 1 ? mfma_lds_bytes<1>() : p->mfma_slots == 2 ? mfma_lds_bytes<2>() : mfma_lds_bytes<4>();
     in.scratch_bytes = static_cast<int64_t>(n_seg_total * N * sizeof(float));
     in.plan_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
     *plan = p;

@@ -141,9 +141,12 @@ def test_exact_bit_equal_all_widths(torch_cuda, dtype):
 def test_mfma_exact_bit_equal(torch_cuda, dtype):
     """Condensed-tile MFMA path (forced on every eligible window) is bit-equal
     to the oracle on exact-arithmetic inputs, for partial windows, partial
-    column blocks and empty rows."""
+    column blocks and empty rows.  The cases cover one, two and four entry
+    slots per thread (up to 256, 512 and 1024 nonzeros in a step) and windows
+    whose steps span several pipeline blocks."""
     rng = np.random.default_rng(71 + dtype)
-    for m, k, p in [(64, 256, 0.1), (130, 700, 0.05), (200, 64, 0.45), (17, 40, 0.3), (96, 5000, 0.004)]:
+    for m, k, p in [(64, 256, 0.1), (130, 700, 0.05), (200, 64, 0.45), (17, 40, 0.3), (96, 5000, 0.004),
+                    (128, 2048, 0.2), (64, 1500, 0.4)]:
         lens = rng.binomial(k, p, m)
         lens[rng.random(m) < 0.1] = 0
         a = make_csr(rng, lens, k, dtype)

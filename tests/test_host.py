@@ -235,7 +235,7 @@ def test_condense_windows_bit_exact_with_oracle(m, k, p, win):
 
 @pytest.mark.parametrize("m,k,n,p,flags", [(200, 700, 128, 0.06, S.TCA_PLAN_FORCE_MFMA),
                                            (130, 300, 64, 0.02, S.TCA_PLAN_FORCE_MFMA),
-                                           (64, 2048, 256, 0.3, S.TCA_PLAN_DEFAULT)])
+                                           (64, 2048, 256, 0.3, S.TCA_PLAN_FORCE_MFMA)])
 def test_mfma_window_plan_decodes_to_the_csr(m, k, n, p, flags):
     """Every MFMA window's steps, B-row lists and entries reproduce the CSR
     exactly, with the oracle's condensed positions."""
@@ -264,6 +264,22 @@ def test_mfma_window_plan_decodes_to_the_csr(m, k, n, p, flags):
     assert len(none) == 0
     assert len(S.plan_mfma_windows(a.astype(S.TCA_F32), n, flags=S.TCA_PLAN_FORCE_MFMA)[0]) == 0  # fp32: no MFMA
     assert len(S.plan_mfma_windows(a, 100, flags=S.TCA_PLAN_FORCE_MFMA)[0]) == 0  # N % 8 != 0
+
+
+def test_mfma_default_routing_follows_the_cost_model():
+    """Default routing: the lognormal 4096 x 4096 layer (config 1) goes to the
+    tile kernel, the small 2048 x 512 Bernoulli layer (config 0) stays on the
+    row kernel (too few steps and workgroups to amortise the pipeline fill),
+    and a very sparse matrix (density below 0.04) stays on the row kernel."""
+    a1, n1, _ = S.gen_config(1, seed=1)
+    w1 = S.plan_mfma_windows(a1, n1)[0]
+    assert len(w1) == (a1.nrow + 63) // 64
+    a0, n0, _ = S.gen_config(0, seed=1)
+    assert len(S.plan_mfma_windows(a0, n0)[0]) == 0
+    sparse, _ = S.gen_lognormal_rows(4096, 4096, 50, seed=5)
+    assert len(S.plan_mfma_windows(sparse, 512)[0]) == 0
+    # the density floor is overridable for tuning, the cost model still applies
+    assert len(S.plan_mfma_windows(a0, n0, flags=S.TCA_PLAN_FORCE_MFMA)[0]) == (a0.nrow + 63) // 64
 
 
 # -------------------------------------------------------------- planner
