@@ -27,6 +27,20 @@ WORKLOADS = {
 }
 
 
+# Dominant kernel of each phase (tca_spmm_time_phases order).
+PHASE_KERNELS = {"pack": "mfma_pack_kernel", "tiles": "mfma_tile_kernel", "rows": "row_kernel",
+                 "segments": "seg_finalize_kernel"}
+
+# HBM bytes per launch of the dominant kernel, measured with rocprofv3 --pmc
+# FETCH_SIZE and WRITE_SIZE (KiB per dispatch, already scaled by the copy
+# calibration: FETCH x 2.00, WRITE x 1.00), keyed by (config, phase, flags).
+# Source: the profiles/ summaries named in each entry.
+MEASURED_TRAFFIC_KIB = {
+    # profiles/mfma_tile_kernel_config1.md
+    (1, "tiles", 0): (12768.8 * 2.0, 10785.3),
+}
+
+
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
@@ -95,13 +109,31 @@ def main():
     wall_ms = (time.perf_counter() - wall0) * 1e3
     if not torch.isfinite(c).all().item():
         sys.exit("non-finite output")
+    # Per-kernel durations (hipEvents between the kernels on the launch stream)
+    # for the roofline of the dominant kernel.
+    phases = plan.time_phases(val, bd, c, stream=stream.cuda_stream, warmup=1, iters=args.steps)
+    torch.cuda.synchronize()
+    dominant = max(phases, key=phases.get)
+    log("phases (ms):", json.dumps(phases))
 
     s_a = 4 if a.dtype == S.TCA_F32 else 2
     m, k, nnz = a.nrow, a.ncol, a.nnz
     flops = 2.0 * nnz * n
     bytes_alg = 4 * (m + 1) + nnz * (4 + s_a) + k * n * s_a + m * n * 4
     gflops = flops / (ms_per_step * 1e-3) / 1e9
-    achieved = bytes_alg / (ms_per_step * 1e-3) / 1e9
+    hbm_gbs = bytes_alg / (ms_per_step * 1e-3) / 1e9
+    # Algorithmic bytes of the dominant kernel: the SpMM restricted to the rows
+    # it computes (each kernel must read its rows' indices and values, B once
+    # and write its rows of C once).
+    if dominant == "tiles":
+        rows_k, nnz_k = info["rows_mfma"], info["nnz_mfma"]
+    else:
+        rows_k, nnz_k = m - info["rows_mfma"], nnz - info["nnz_mfma"]
+    bytes_dom = 4 * (rows_k + 1) + nnz_k * (4 + s_a) + k * n * s_a + rows_k * n * 4
+    dom_ms = phases[dominant]
+    achieved = bytes_dom / (dom_ms * 1e-3) / 1e9
+    kib = args.traffic_kib or MEASURED_TRAFFIC_KIB.get((args.config, dominant, args.flags))
+    traffic = int(round((kib[0] + kib[1]) * 1024)) if kib else None
     log(f"kernel avg {ms_per_step * 1e3:.2f} us/step, wall {wall_ms:.2f} ms for {args.warmup}+{args.steps} steps")
 
     cpu = None
@@ -145,11 +177,14 @@ def main():
         "dtype": "f32" if a.dtype == S.TCA_F32 else ("f16" if a.dtype == S.TCA_F16 else "bf16") + "->f32acc",
         "data": "synthetic (seeded generators, seed %d)" % args.seed,
         "config": {"workload": WORKLOADS[args.config], "M": m, "K": k, "N": n, "nnz": nnz,
-                   "bytes_alg": bytes_alg, "hbm_gbs": round(achieved, 2), "plan_ms": round(info["plan_ms"], 3)},
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 5),
-                     "traffic": (int(round((args.traffic_kib[0] + args.traffic_kib[1]) * 1024))
-                                 if args.traffic_kib else None)},
+                   "bytes_alg": bytes_alg, "hbm_gbs_whole_step": round(hbm_gbs, 2),
+                   "plan_ms": round(info["plan_ms"], 3),
+                   "phases_us": {kk: round(v * 1e3, 3) for kk, v in phases.items()},
+                   "mfma_windows": info["n_windows_mfma"], "rows_mfma": info["rows_mfma"]},
+        "roofline": {"bound": "hbm", "kernel": PHASE_KERNELS[dominant], "bytes_alg": bytes_dom,
+                     "kernel_us": round(dom_ms * 1e3, 3),
+                     "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": traffic},
         "cpu_baseline": cpu,
     }
     plan.close()

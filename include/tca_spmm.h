@@ -107,6 +107,21 @@ int tca_spmm_run(const tca_spmm_plan* plan, const void* d_val, const void* d_B, 
 int tca_spmm_time(const tca_spmm_plan* plan, const void* d_val, const void* d_B, float* d_C,
                   void* stream, int32_t warmup, int32_t iters, float* avg_ms);
 
+/* Phases of one run, in stream order: value pack for the MFMA tiles, MFMA
+ * tile kernel, row kernel, long-row segment sums. */
+#define TCA_PHASES 4
+enum { TCA_PHASE_PACK = 0, TCA_PHASE_TILES = 1, TCA_PHASE_ROWS = 2, TCA_PHASE_SEGMENTS = 3 };
+
+/* Per-phase timing: `warmup` + 1 full runs, then each phase the plan uses is
+ * launched alone `iters` times back to back between two hipEvents on
+ * `stream` (every phase is idempotent once a full run has produced its
+ * inputs): phase_ms[k] = mean milliseconds of one launch of phase k, 0 for a
+ * phase the plan does not use.  No counterpart in the reference, which times
+ * whole runs only (src/our_spmm.cu:553-576); this is the per-kernel figure a
+ * roofline needs. */
+int tca_spmm_time_phases(const tca_spmm_plan* plan, const void* d_val, const void* d_B, float* d_C, void* stream,
+                         int32_t warmup, int32_t iters, float* phase_ms);
+
 int tca_spmm_plan_info(const tca_spmm_plan* plan, tca_plan_info* info);
 
 int tca_spmm_plan_destroy(tca_spmm_plan* plan);

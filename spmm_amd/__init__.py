@@ -302,6 +302,17 @@ class Plan:
              _addr(stream) if stream is not None else None, warmup, iters, ctypes.byref(ms))
         return ms.value
 
+    PHASES = ("pack", "tiles", "rows", "segments")
+
+    def time_phases(self, val, b, c, stream=None, warmup: int = 5, iters: int = 10) -> dict:
+        """Mean milliseconds of one launch of each phase (MFMA value pack, MFMA
+        tiles, row kernel, long-row segment sums): each phase launched alone
+        `iters` times back to back between hipEvents on the run's stream."""
+        ms = (ctypes.c_float * 4)()
+        call("tca_spmm_time_phases", self._p, _addr(val), _addr(b), _addr(c),
+             _addr(stream) if stream is not None else None, warmup, iters, ms)
+        return {k: float(ms[i]) for i, k in enumerate(self.PHASES)}
+
     def close(self) -> None:
         if self._p:
             lib.tca_spmm_plan_destroy(self._p)

@@ -71,6 +71,7 @@ SIGNATURES = {
     "tca_spmm_plan_create": (i32, [i32p, i32p, i32, i32, i32, i32, i32, u32, ctypes.POINTER(vp)]),
     "tca_spmm_run": (i32, [vp, vp, vp, vp, vp]),
     "tca_spmm_time": (i32, [vp, vp, vp, vp, vp, i32, i32, f32p]),
+    "tca_spmm_time_phases": (i32, [vp, vp, vp, vp, vp, i32, i32, f32p]),
     "tca_spmm_plan_info": (i32, [vp, ctypes.POINTER(TcaPlanInfo)]),
     "tca_spmm_plan_destroy": (i32, [vp]),
     "tca_spmm_host": (i32, [i32p, i32p, vp, i32, i32, i32, vp, f32p, i32, i32, i32, i32,

@@ -106,10 +106,13 @@ void launch_rows_t(const tca_spmm_plan* p, const void* val, const void* B, float
     a.B_bytes = static_cast<uint32_t>(static_cast<uint64_t>(p->K) * p->N * sizeof(T));
     const dim3 grid(((p->ntasks + kRowWaves - 1) / kRowWaves) * p->rows.col_chunks);
     hipLaunchKernelGGL((row_kernel<T, E>), grid, dim3(64 * kRowWaves), 0, s, a);
-    if (!p->rows.longrows.empty()) {
-        const dim3 fgrid(static_cast<unsigned>(p->rows.longrows.size()), (p->N + 255) / 256);
-        hipLaunchKernelGGL(seg_finalize_kernel, fgrid, dim3(64), 0, s, p->d_longrows, p->d_partials, C, p->N);
-    }
+}
+
+// Adds the segments of long rows (after the row kernel, same stream).
+void launch_finalize(const tca_spmm_plan* p, float* C, hipStream_t s) {
+    if (p->rows.longrows.empty()) return;
+    const dim3 fgrid(static_cast<unsigned>(p->rows.longrows.size()), (p->N + 255) / 256);
+    hipLaunchKernelGGL(seg_finalize_kernel, fgrid, dim3(64), 0, s, p->d_longrows, p->d_partials, C, p->N);
 }
 
 template <typename T>
@@ -128,7 +131,15 @@ int launch_rows_e(const tca_spmm_plan* p, const void* val, const void* B, float*
     }
 }
 
-int launch_mfma(const tca_spmm_plan* p, const void* val, const void* B, float* C, hipStream_t s) {
+// Pairs the MFMA entries with this run's values (before the tile kernel).
+void launch_pack(const tca_spmm_plan* p, const void* val, hipStream_t s) {
+    const int n_ent = static_cast<int>(p->mfma.entries.size());
+    if (p->mfma.windows.empty() || n_ent == 0) return;
+    hipLaunchKernelGGL(mfma_pack_kernel, dim3((n_ent + 255) / 256), dim3(256), 0, s, p->d_pk_seg, p->n_pk_seg,
+                       p->d_pk_dst, p->d_pk_cell, n_ent, static_cast<const uint16_t*>(val), p->d_packed);
+}
+
+int launch_mfma(const tca_spmm_plan* p, const void* B, float* C, hipStream_t s) {
     if (p->mfma.windows.empty()) return TCA_OK;
     MfmaArgs a;
     a.windows = p->d_windows;
@@ -145,9 +156,6 @@ int launch_mfma(const tca_spmm_plan* p, const void* val, const void* B, float* C
     const int n_ent = static_cast<int>(p->mfma.entries.size());
     a.sentinel = n_ent;
     a.packed_bytes = static_cast<uint32_t>((static_cast<uint64_t>(n_ent) + 1) * 4);
-    if (n_ent > 0)
-        hipLaunchKernelGGL(mfma_pack_kernel, dim3((n_ent + 255) / 256), dim3(256), 0, s, p->d_pk_seg, p->n_pk_seg,
-                           p->d_pk_dst, p->d_pk_cell, n_ent, static_cast<const uint16_t*>(val), p->d_packed);
     a.ucols_bytes = static_cast<uint32_t>(p->mfma.ucols.size() * 4);
     a.eoff_bytes = static_cast<uint32_t>(p->mfma.eoff.size() * 4);
     const dim3 grid(static_cast<unsigned>(p->mfma.windows.size()) * p->mfma_col_blocks);
@@ -176,6 +184,17 @@ int launch_rows(const tca_spmm_plan* p, const void* val, const void* B, float* C
         case TCA_BF16: return launch_rows_e<bf16_t>(p, val, B, C, s);
         default: return launch_rows_e<float>(p, val, B, C, s);
     }
+}
+
+// One SpMM in stream order: pack, tile kernel, row kernel, segment sums.
+int run_phases(const tca_spmm_plan* p, const void* val, const void* B, float* C, hipStream_t s) {
+    launch_pack(p, val, s);
+    int st = launch_mfma(p, B, C, s);
+    if (st) return st;
+    st = launch_rows(p, val, B, C, s);
+    if (st) return st;
+    launch_finalize(p, C, s);
+    return TCA_OK;
 }
 
 }  // namespace
@@ -355,9 +374,7 @@ int tca_spmm_run(const tca_spmm_plan* p, const void* d_val, const void* d_B, flo
     if (reinterpret_cast<uintptr_t>(d_val) % dtype_size(p->dtype) != 0)
         return fail(TCA_ERR_INVALID, "values misaligned");
     hipStream_t s = static_cast<hipStream_t>(stream);
-    int st = launch_mfma(p, d_val, d_B, d_C, s);
-    if (st) return st;
-    st = launch_rows(p, d_val, d_B, d_C, s);
+    const int st = run_phases(p, d_val, d_B, d_C, s);
     if (st) return st;
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(TCA_ERR_HIP, "kernel launch: %s", hipGetErrorString(e));
@@ -392,6 +409,54 @@ int tca_spmm_time(const tca_spmm_plan* p, const void* d_val, const void* d_B, fl
     (void)hipEventDestroy(e1);
     *avg_ms = ms / static_cast<float>(iters);
     return TCA_OK;
+}
+
+int tca_spmm_time_phases(const tca_spmm_plan* p, const void* d_val, const void* d_B, float* d_C, void* stream,
+                         int32_t warmup, int32_t iters, float* phase_ms) {
+    if (!p || !phase_ms || iters < 1 || warmup < 0) return fail(TCA_ERR_INVALID, "tca_spmm_time_phases: bad argument");
+    for (int k = 0; k < TCA_PHASES; k++) phase_ms[k] = 0.f;
+    // Full runs first: every phase's inputs (packed entries, segment partial
+    // sums) then exist, and each phase is idempotent, so a phase can be timed
+    // alone as `iters` back-to-back launches between two events.
+    for (int i = 0; i < warmup + 1; i++) {
+        int st = tca_spmm_run(p, d_val, d_B, d_C, stream);
+        if (st) return st;
+    }
+    if (p->M == 0) return TCA_OK;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    TCA_HIP_TRY(hipEventCreate(&e0));
+    if (hipEventCreate(&e1) != hipSuccess) {
+        (void)hipEventDestroy(e0);
+        return fail(TCA_ERR_HIP, "hipEventCreate failed");
+    }
+    int st = TCA_OK;
+    const bool used[TCA_PHASES] = {!p->mfma.windows.empty() && !p->mfma.entries.empty(), !p->mfma.windows.empty(),
+                                   p->ntasks > 0, !p->rows.longrows.empty()};
+    for (int k = 0; k < TCA_PHASES && st == TCA_OK; k++) {
+        if (!used[k]) continue;
+        (void)hipEventRecord(e0, s);
+        for (int i = 0; i < iters && st == TCA_OK; i++) {
+            switch (k) {
+                case TCA_PHASE_PACK: launch_pack(p, d_val, s); break;
+                case TCA_PHASE_TILES: st = launch_mfma(p, d_B, d_C, s); break;
+                case TCA_PHASE_ROWS: st = launch_rows(p, d_val, d_B, d_C, s); break;
+                default: launch_finalize(p, d_C, s); break;
+            }
+        }
+        (void)hipEventRecord(e1, s);
+        float ms = 0.f;
+        if (st == TCA_OK && (hipEventSynchronize(e1) != hipSuccess || hipEventElapsedTime(&ms, e0, e1) != hipSuccess))
+            st = fail(TCA_ERR_HIP, "event timing failed");
+        phase_ms[k] = ms / static_cast<float>(iters);
+    }
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    if (st == TCA_OK) {
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return fail(TCA_ERR_HIP, "kernel launch: %s", hipGetErrorString(e));
+    }
+    return st;
 }
 
 int tca_spmm_host(const int32_t* rowptr, const int32_t* colidx, const void* val, int32_t M, int32_t K, int32_t nnz,

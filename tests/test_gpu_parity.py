@@ -294,3 +294,23 @@ def test_config_full_size_large(torch_cuda, cfg):
                                 np.abs(S.from_storage(b, a.dtype).astype(np.float64)).sum(1, keepdims=True))
     err = np.abs(got.astype(np.float64).sum(1) - row_sum_gold[:, 0])
     assert np.all(err <= 1e-3 * np.maximum(np.abs(row_sum_gold[:, 0]), 1e-3 * s_abs[:, 0]) + 1e-30)
+
+
+def test_phase_timing_reports_the_kernels_a_plan_uses(torch_cuda):
+    """tca_spmm_time_phases: a phase the plan does not use reads 0, the used
+    ones are positive, and the run afterwards is still exact."""
+    torch = torch_cuda
+    rng = np.random.default_rng(97)
+    a, _ = S.gen_bernoulli(256, 512, 0.2, seed=9, dtype=S.TCA_F16)
+    a = S.CSR(a.nrow, a.ncol, a.rowptr, a.colidx, S.to_storage(exact_values(rng, a.nnz), S.TCA_F16), S.TCA_F16)
+    b = S.to_storage(exact_dense(rng, (512, 256)), S.TCA_F16)
+    dev = torch.device("cuda:0")
+    val = torch.from_numpy(a.values.view(np.int16)).to(dev)
+    bd = torch.from_numpy(b.view(np.int16)).to(dev)
+    for flags, used in ((S.TCA_PLAN_FORCE_MFMA, {"pack", "tiles"}), (S.TCA_PLAN_NO_MFMA, {"rows"})):
+        c = torch.zeros((a.nrow, 256), dtype=torch.float32, device=dev)
+        with S.Plan(a, 256, flags) as pl:
+            ph = pl.time_phases(val, bd, c, warmup=1, iters=3)
+        torch.cuda.synchronize()
+        assert {k for k, v in ph.items() if v > 0} == used, (flags, ph)
+        assert np.array_equal(c.cpu().numpy(), oracle_c(a, b))
