@@ -2,7 +2,7 @@
 
 A "step" is one SpMM C = A * B over one batch of synthetic input, with A, B
 and C resident in HBM before the timed region starts.  Default workload:
-BASELINE config 1 (4096 x 4096 pruned linear layer, lognormal row lengths
+Benchmark configuration 1 (4096 x 4096 pruned linear layer, lognormal row lengths
 with mean 205, fp16 values, B 4096 x 512 fp16, fp32 C).  Prints ONE JSON line.
 
     python bench.py [--steps K] [--warmup W] [--config 0..4] [--gpus 1]

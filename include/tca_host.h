@@ -149,7 +149,7 @@ int tca_gen_dense(int64_t rows, int64_t cols, int32_t dist, float sparsity, uint
                   int32_t dtype, void* out);
 
 /* Each of the M*K entries kept independently with probability p; values
- * N(0, sigma). (2048 x 512, p = 0.1, sigma = 0.02.) */
+ * N(0, sigma). (Benchmark configuration 0: 2048 x 512, p = 0.1, sigma = 0.02.) */
 int tca_gen_bernoulli(int32_t M, int32_t K, double p, double sigma, uint64_t seed,
                       int32_t dtype, tca_csr* out, tca_gen_stats* st);
 
@@ -177,7 +177,7 @@ int tca_gen_rmat(int32_t scale, int32_t n, int64_t samples, double a, double b, 
 int tca_gen_zipf_rows(int32_t M, int32_t K, int64_t total_nnz, double s, int32_t cap,
                       uint64_t seed, int32_t dtype, tca_csr* out, tca_gen_stats* st);
 
-/* The five BASELINE configurations (index 0..4) at full size with their GPU
+/* The five benchmark configurations (index 0..4) at full size with their GPU
  * value types (config 0: fp16 by default like the reference harness types).
  * dtype < 0 selects the config's own type.  *N receives the dense width. */
 int tca_gen_config(int32_t cfg, uint64_t seed, int32_t dtype, tca_csr* out, int32_t* N,

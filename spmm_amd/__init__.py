@@ -260,7 +260,7 @@ def gen_zipf_rows(m, k, total, s=1.5, cap=200000, seed=1, dtype=TCA_F16):
 
 
 def gen_config(cfg: int, seed: int = 1, dtype: int = -1):
-    """One of the five BASELINE configurations; returns (A, N, stats)."""
+    """One of the five benchmark configurations; returns (A, N, stats)."""
     s = _lib.TcaCsr()
     st = _lib.TcaGenStats()
     n = ctypes.c_int32()

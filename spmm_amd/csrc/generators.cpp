@@ -1,5 +1,5 @@
 // generators.cpp -- seeded, thread-count-independent input generators for the
-// five BASELINE configurations (and smaller members of the same families).
+// five benchmark configurations (and smaller members of the same families).
 //
 // The reference draws its inputs from std::random_device (unseeded) with 20
 // OpenMP threads all writing every element (src/general.cuh:140-174), so its

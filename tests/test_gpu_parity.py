@@ -23,7 +23,7 @@ import spmm_amd as S
 
 pytestmark = pytest.mark.gpu
 
-TOL = 1e-3       # max relative error <= 1e-3
+TOL = 1e-3       # target: max relative error <= 1e-3 (the reference verdict tolerance)
 FLOOR = 1e-2     # |gold| floor of the relative-error report (outputs are O(0.1..10))
 
 
