@@ -93,6 +93,15 @@ int tca_csr_to_dense(const tca_csr* a, void* dense);
 int tca_csr_to_coo(const tca_csr* a, tca_coo* out);
 /* Sorts by (row, col); rejects duplicates and out-of-range indices. */
 int tca_coo_to_csr(const tca_coo* a, tca_csr* out);
+
+/* Structure of the transpose: A (M x K, CSR) -> A^T (K x M, CSR), columns of
+ * each row of A^T ascending; perm[t] = the nonzero of A stored at position t
+ * of A^T (values of A^T = values of A gathered through perm).  rowptr_t has
+ * K + 1 entries, colidx_t and perm nnz.  No counterpart in the reference
+ * (it never transposes); the backward pass of the PyTorch op multiplies by
+ * A^T. */
+int tca_csr_transpose(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_t K, int32_t nnz,
+                      int32_t* rowptr_t, int32_t* colidx_t, int32_t* perm);
 /* Value conversion of a CSR (same structure, new dtype, RNE rounding). */
 int tca_csr_convert(const tca_csr* a, int32_t dtype, tca_csr* out);
 

@@ -122,6 +122,20 @@ enum { TCA_PHASE_PACK = 0, TCA_PHASE_TILES = 1, TCA_PHASE_ROWS = 2, TCA_PHASE_SE
 int tca_spmm_time_phases(const tca_spmm_plan* plan, const void* d_val, const void* d_B, float* d_C, void* stream,
                          int32_t warmup, int32_t iters, float* phase_ms);
 
+/* Backward-pass kernels of the PyTorch op (no counterpart in the reference,
+ * which has no backward pass).
+ *
+ * tca_sddmm: d_out[j] = sum_n d_G[row(j) * N + n] * d_B[col(j) * N + n] for
+ * every nonzero j of the plan's A (fp32 G of shape M x N, B K x N in the
+ * plan's dtype, fp32 out[nnz]): the gradient of C = A * B with respect to
+ * A's values.  Deterministic (fixed reduction order).
+ *
+ * tca_gather_values: d_out[i] = (float)d_val[d_perm[i]] for i < n (A's
+ * values in the order of its transpose, see tca_csr_transpose). */
+int tca_sddmm(const tca_spmm_plan* plan, const float* d_G, const void* d_B, float* d_out, void* stream);
+int tca_gather_values(const int32_t* d_perm, int32_t n, const void* d_val, int32_t dtype, float* d_out,
+                      void* stream);
+
 int tca_spmm_plan_info(const tca_spmm_plan* plan, tca_plan_info* info);
 
 int tca_spmm_plan_destroy(tca_spmm_plan* plan);

@@ -72,6 +72,8 @@ SIGNATURES = {
     "tca_spmm_run": (i32, [vp, vp, vp, vp, vp]),
     "tca_spmm_time": (i32, [vp, vp, vp, vp, vp, i32, i32, f32p]),
     "tca_spmm_time_phases": (i32, [vp, vp, vp, vp, vp, i32, i32, f32p]),
+    "tca_sddmm": (i32, [vp, vp, vp, vp, vp]),
+    "tca_gather_values": (i32, [vp, i32, vp, i32, vp, vp]),
     "tca_spmm_plan_info": (i32, [vp, ctypes.POINTER(TcaPlanInfo)]),
     "tca_spmm_plan_destroy": (i32, [vp]),
     "tca_spmm_host": (i32, [i32p, i32p, vp, i32, i32, i32, vp, f32p, i32, i32, i32, i32,
@@ -98,6 +100,7 @@ SIGNATURES = {
     "tca_csr_to_dense": (i32, [ctypes.POINTER(TcaCsr), vp]),
     "tca_csr_to_coo": (i32, [ctypes.POINTER(TcaCsr), ctypes.POINTER(TcaCoo)]),
     "tca_coo_to_csr": (i32, [ctypes.POINTER(TcaCoo), ctypes.POINTER(TcaCsr)]),
+    "tca_csr_transpose": (i32, [i32p, i32p, i32, i32, i32, i32p, i32p, i32p]),
     "tca_csr_convert": (i32, [ctypes.POINTER(TcaCsr), i32, ctypes.POINTER(TcaCsr)]),
     "tca_f32_to_f16": (ctypes.c_uint16, [ctypes.c_float]),
     "tca_f16_to_f32": (ctypes.c_float, [ctypes.c_uint16]),

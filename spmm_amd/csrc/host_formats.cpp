@@ -228,6 +228,30 @@ int tca_coo_to_csr(const tca_coo* a, tca_csr* out) {
     return TCA_OK;
 }
 
+int tca_csr_transpose(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_t K, int32_t nnz,
+                      int32_t* rowptr_t, int32_t* colidx_t, int32_t* perm) {
+    if (!rowptr || (nnz > 0 && (!colidx || !colidx_t || !perm)) || !rowptr_t || M < 0 || K < 0 || nnz < 0)
+        return fail(TCA_ERR_INVALID, "tca_csr_transpose: bad argument");
+    if (rowptr[M] != nnz) return fail(TCA_ERR_INVALID, "tca_csr_transpose: rowptr[M] != nnz");
+    // Counting sort by column; rows are visited in order, so each row of the
+    // transpose lists its columns (A's rows) ascending.
+    std::fill(rowptr_t, rowptr_t + static_cast<size_t>(K) + 1, 0);
+    for (int32_t j = 0; j < nnz; j++) {
+        const int32_t c = colidx[j];
+        if (c < 0 || c >= K) return fail(TCA_ERR_INVALID, "tca_csr_transpose: column %d out of range", c);
+        rowptr_t[c + 1]++;
+    }
+    for (int32_t c = 0; c < K; c++) rowptr_t[c + 1] += rowptr_t[c];
+    std::vector<int32_t> fill(rowptr_t, rowptr_t + K);
+    for (int32_t r = 0; r < M; r++)
+        for (int32_t j = rowptr[r]; j < rowptr[r + 1]; j++) {
+            const int32_t t = fill[colidx[j]]++;
+            colidx_t[t] = r;
+            perm[t] = j;
+        }
+    return TCA_OK;
+}
+
 int tca_csr_convert(const tca_csr* a, int32_t dtype, tca_csr* out) {
     if (!a || !out || !dtype_ok(dtype) || !dtype_ok(a->dtype)) return fail(TCA_ERR_INVALID, "tca_csr_convert: bad argument");
     int st = alloc_csr(out, a->nRow, a->nCol, a->nnz, dtype);

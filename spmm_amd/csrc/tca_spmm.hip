@@ -12,6 +12,7 @@
 #include "planner.hpp"
 #include "row_kernel.hpp"
 #include "mfma_kernel.hpp"
+#include "sddmm_kernel.hpp"
 
 using namespace tca;
 
@@ -408,6 +409,54 @@ int tca_spmm_time(const tca_spmm_plan* p, const void* d_val, const void* d_B, fl
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);
     *avg_ms = ms / static_cast<float>(iters);
+    return TCA_OK;
+}
+
+int tca_sddmm(const tca_spmm_plan* p, const float* d_G, const void* d_B, float* d_out, void* stream) {
+    if (!p) return fail(TCA_ERR_INVALID, "plan is NULL");
+    if (p->M == 0 || p->nnz == 0) return TCA_OK;
+    if (!d_G || !d_B || !d_out) return fail(TCA_ERR_INVALID, "NULL device pointer");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const dim3 grid((p->M + kSddmmRowsPerBlock - 1) / kSddmmRowsPerBlock), block(64 * kSddmmRowsPerBlock);
+    switch (p->dtype) {
+        case TCA_F16:
+            hipLaunchKernelGGL(sddmm_kernel<_Float16>, grid, block, 0, s, p->d_rowptr, p->d_colidx, p->M, p->N, d_G,
+                               static_cast<const _Float16*>(d_B), d_out);
+            break;
+        case TCA_BF16:
+            hipLaunchKernelGGL(sddmm_kernel<bf16_t>, grid, block, 0, s, p->d_rowptr, p->d_colidx, p->M, p->N, d_G,
+                               static_cast<const bf16_t*>(d_B), d_out);
+            break;
+        default:
+            hipLaunchKernelGGL(sddmm_kernel<float>, grid, block, 0, s, p->d_rowptr, p->d_colidx, p->M, p->N, d_G,
+                               static_cast<const float*>(d_B), d_out);
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(TCA_ERR_HIP, "kernel launch: %s", hipGetErrorString(e));
+    return TCA_OK;
+}
+
+int tca_gather_values(const int32_t* d_perm, int32_t n, const void* d_val, int32_t dtype, float* d_out, void* stream) {
+    if (n < 0 || !dtype_ok(dtype)) return fail(TCA_ERR_INVALID, "tca_gather_values: bad argument");
+    if (n == 0) return TCA_OK;
+    if (!d_perm || !d_val || !d_out) return fail(TCA_ERR_INVALID, "NULL device pointer");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const dim3 grid((n + 255) / 256);
+    switch (dtype) {
+        case TCA_F16:
+            hipLaunchKernelGGL(gather_values_kernel<_Float16>, grid, dim3(256), 0, s, d_perm, n,
+                               static_cast<const _Float16*>(d_val), d_out);
+            break;
+        case TCA_BF16:
+            hipLaunchKernelGGL(gather_values_kernel<bf16_t>, grid, dim3(256), 0, s, d_perm, n,
+                               static_cast<const bf16_t*>(d_val), d_out);
+            break;
+        default:
+            hipLaunchKernelGGL(gather_values_kernel<float>, grid, dim3(256), 0, s, d_perm, n,
+                               static_cast<const float*>(d_val), d_out);
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(TCA_ERR_HIP, "kernel launch: %s", hipGetErrorString(e));
     return TCA_OK;
 }
 

@@ -282,6 +282,26 @@ def test_mfma_default_routing_follows_the_cost_model():
     assert len(S.plan_mfma_windows(a0, n0, flags=S.TCA_PLAN_FORCE_MFMA)[0]) == (a0.nrow + 63) // 64
 
 
+@pytest.mark.parametrize("m,k,p", [(50, 70, 0.1), (1, 1, 1.0), (300, 20, 0.3), (20, 300, 0.05), (5, 5, 0.0)])
+def test_csr_transpose_matches_the_dense_transpose(m, k, p):
+    """tca_csr_transpose: the transpose's structure and the value permutation
+    reproduce the dense transpose exactly, with ascending columns per row."""
+    import ctypes
+    a, _ = S.gen_bernoulli(m, k, p, seed=m * 7 + k, dtype=S.TCA_F32)
+    rpt = np.zeros(k + 1, np.int32)
+    cit = np.zeros(max(a.nnz, 1), np.int32)
+    perm = np.zeros(max(a.nnz, 1), np.int32)
+    rp = np.ascontiguousarray(a.rowptr, np.int32)
+    ci = np.ascontiguousarray(a.colidx, np.int32)
+    S.call("tca_csr_transpose", S.np_ptr(rp, ctypes.c_int32), S.np_ptr(ci, ctypes.c_int32), m, k, a.nnz,
+           S.np_ptr(rpt, ctypes.c_int32), S.np_ptr(cit, ctypes.c_int32), S.np_ptr(perm, ctypes.c_int32))
+    at = S.CSR(k, m, rpt, cit[:a.nnz], a.values[perm[:a.nnz]], S.TCA_F32)
+    assert np.array_equal(S.csr_to_dense(at), S.csr_to_dense(a).T)
+    for r in range(k):
+        assert np.all(np.diff(at.colidx[at.rowptr[r]:at.rowptr[r + 1]]) > 0)
+    assert np.array_equal(np.sort(perm[:a.nnz]), np.arange(a.nnz))
+
+
 # -------------------------------------------------------------- planner
 @pytest.mark.parametrize("n,dtype", [(256, S.TCA_F16), (512, S.TCA_F16), (64, S.TCA_F16), (128, S.TCA_F32),
                                      (7, S.TCA_F32), (100, S.TCA_BF16), (1000, S.TCA_F16)])
