@@ -115,6 +115,21 @@ def main():
     torch.cuda.synchronize()
     dominant = max(phases, key=phases.get)
     log("phases (ms):", json.dumps(phases))
+    # Cold-cache SpMM: L2s and MALL flushed by writing a 512 MiB buffer
+    # before each timed run (median of 5), and the empty-kernel launch floor.
+    flush = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+    cold = []
+    for _ in range(5):
+        flush.fill_(1)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        plan.run(val, bd, c, stream=stream.cuda_stream)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        cold.append(e0.elapsed_time(e1))
+    del flush
+    cold_ms = float(np.median(cold))
+    floor_ms = S.launch_floor(stream=stream.cuda_stream, iters=100)
 
     s_a = 4 if a.dtype == S.TCA_F32 else 2
     m, k, nnz = a.nrow, a.ncol, a.nnz
@@ -180,6 +195,7 @@ def main():
                    "bytes_alg": bytes_alg, "hbm_gbs_whole_step": round(hbm_gbs, 2),
                    "plan_ms": round(info["plan_ms"], 3),
                    "phases_us": {kk: round(v * 1e3, 3) for kk, v in phases.items()},
+                   "cold_cache_us": round(cold_ms * 1e3, 3), "launch_floor_us": round(floor_ms * 1e3, 3),
                    "mfma_windows": info["n_windows_mfma"], "rows_mfma": info["rows_mfma"]},
         "roofline": {"bound": "hbm", "kernel": PHASE_KERNELS[dominant], "bytes_alg": bytes_dom,
                      "kernel_us": round(dom_ms * 1e3, 3),

@@ -76,6 +76,21 @@ int tca_smtx_read_dense(const char* path, int32_t dtype, void** dense, int32_t* 
  * the reference fixture. */
 int tca_smtx_write(const char* path, const tca_csr* a);
 
+/* ---- binary CSR cache and values sidecar (no counterpart in the reference) ----
+ * Binary CSR: magic "TCACSR01", int32 nRow, nCol, int64 nnz, int32 dtype,
+ * int32 0, then rowptr int32[nRow+1], colidx int32[nnz], values (dtype)[nnz],
+ * all little endian.  The reader checks the magic, that the header matches
+ * the file size exactly and the CSR invariants (tca_csr_validate): a cache
+ * that loads a large graph without re-parsing text.
+ * Values file: magic "TCAVAL01", int64 nnz, int32 dtype, int32 0, then the
+ * values.  tca_smtx_read_csr_values reads a .smtx pattern and attaches the
+ * values (converted to `dtype`; the counts must agree), since the .smtx
+ * format itself has none (reference src/file_input.cu:189 sets 1.0). */
+int tca_csr_write_binary(const char* path, const tca_csr* a);
+int tca_csr_read_binary(const char* path, tca_csr* out);
+int tca_values_write(const char* path, const void* values, int64_t nnz, int32_t dtype);
+int tca_smtx_read_csr_values(const char* smtx_path, const char* values_path, int32_t dtype, tca_csr* out);
+
 /* ---- MatrixMarket coordinate files (reference src/file_input.cu:8-134) ----
  * '%' lines are skipped, then "rows cols nnz", then one "r c [v]" per line.
  * pattern_only: values are 1.0; zero_based == 0: indices are one based.

@@ -195,6 +195,11 @@ int tca_plan_mfma_windows(const int32_t* rowptr, const int32_t* colidx, int32_t 
  * <<<1,32>>> ten times by src/test.cu:50-52). */
 int tca_warm_up(void);
 
+/* Launch floor: mean milliseconds per launch of an empty one-wavefront kernel,
+ * `iters` launches back to back on `stream` between two hipEvents (the time
+ * below which no SpMM launch can go).  No counterpart in the reference. */
+int tca_launch_floor(void* stream, int32_t iters, float* avg_ms);
+
 /* ---- library information ---- */
 const char* tca_status_string(int status);
 const char* tca_last_error(void);

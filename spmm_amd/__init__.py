@@ -24,7 +24,8 @@ from ._lib import (TCA_BF16, TCA_F16, TCA_F32, TCA_PLAN_DEFAULT, TCA_PLAN_FORCE_
                    call, lib, np_ptr)
 
 __all__ = ["CSR", "Plan", "TcaError", "TCA_F16", "TCA_F32", "TCA_BF16", "TCA_PLAN_DEFAULT", "TCA_PLAN_NO_MFMA",
-           "TCA_PLAN_FORCE_MFMA", "read_smtx", "read_smtx_dense", "write_smtx", "read_mtx", "dense_to_csr",
+           "TCA_PLAN_FORCE_MFMA", "read_smtx", "read_smtx_dense", "write_smtx", "read_mtx", "write_values", "write_csr_binary",
+           "read_csr_binary", "launch_floor", "dense_to_csr",
            "csr_to_dense", "compare_mat", "gen_config", "gen_dense", "gen_bernoulli", "gen_lognormal_rows",
            "gen_rmat", "gen_zipf_rows", "naive_csr_spmm", "plan_row_tasks", "plan_mfma_windows", "our_spmm_balanced", "condense_windows", "np_dtype",
            "to_storage", "from_storage"]
@@ -110,9 +111,30 @@ class CSR:
 
 
 # ------------------------------------------------------------------ I/O
-def read_smtx(path: str, dtype: int = TCA_F16) -> CSR:
+def read_smtx(path: str, dtype: int = TCA_F16, values_path: str = None) -> CSR:
+    """.smtx pattern (values 1.0), or with values from a values file."""
     s = _lib.TcaCsr()
-    call("tca_smtx_read_csr", path.encode(), dtype, ctypes.byref(s))
+    if values_path is None:
+        call("tca_smtx_read_csr", path.encode(), dtype, ctypes.byref(s))
+    else:
+        call("tca_smtx_read_csr_values", path.encode(), values_path.encode(), dtype, ctypes.byref(s))
+    return CSR.from_struct(s)
+
+
+def write_values(path: str, a: CSR) -> None:
+    """A's values as a values file (the sidecar of a .smtx pattern)."""
+    v = np.ascontiguousarray(a.values, _STORAGE[a.dtype])
+    call("tca_values_write", path.encode(), v.ctypes.data, a.nnz, a.dtype)
+
+
+def write_csr_binary(path: str, a: CSR) -> None:
+    s = a.as_struct()
+    call("tca_csr_write_binary", path.encode(), ctypes.byref(s))
+
+
+def read_csr_binary(path: str) -> CSR:
+    s = _lib.TcaCsr()
+    call("tca_csr_read_binary", path.encode(), ctypes.byref(s))
     return CSR.from_struct(s)
 
 
@@ -274,6 +296,13 @@ def _addr(x) -> int:
     if isinstance(x, int):
         return x
     return int(x.data_ptr())
+
+
+def launch_floor(stream=None, iters: int = 100) -> float:
+    """Mean milliseconds per launch of an empty kernel (tca_launch_floor)."""
+    ms = ctypes.c_float()
+    call("tca_launch_floor", _addr(stream) if stream is not None else None, iters, ctypes.byref(ms))
+    return ms.value
 
 
 class Plan:

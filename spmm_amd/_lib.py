@@ -73,6 +73,7 @@ SIGNATURES = {
     "tca_spmm_time": (i32, [vp, vp, vp, vp, vp, i32, i32, f32p]),
     "tca_spmm_time_phases": (i32, [vp, vp, vp, vp, vp, i32, i32, f32p]),
     "tca_sddmm": (i32, [vp, vp, vp, vp, vp]),
+    "tca_launch_floor": (i32, [vp, i32, f32p]),
     "tca_gather_values": (i32, [vp, i32, vp, i32, vp, vp]),
     "tca_spmm_plan_info": (i32, [vp, ctypes.POINTER(TcaPlanInfo)]),
     "tca_spmm_plan_destroy": (i32, [vp]),
@@ -96,6 +97,10 @@ SIGNATURES = {
     "tca_smtx_read_dense": (i32, [ctypes.c_char_p, i32, ctypes.POINTER(vp), i32p, i32p, i32p]),
     "tca_smtx_write": (i32, [ctypes.c_char_p, ctypes.POINTER(TcaCsr)]),
     "tca_mtx_read_csr": (i32, [ctypes.c_char_p, i32, i32, i32, ctypes.POINTER(TcaCsr)]),
+    "tca_csr_write_binary": (i32, [ctypes.c_char_p, ctypes.POINTER(TcaCsr)]),
+    "tca_csr_read_binary": (i32, [ctypes.c_char_p, ctypes.POINTER(TcaCsr)]),
+    "tca_values_write": (i32, [ctypes.c_char_p, vp, i64, i32]),
+    "tca_smtx_read_csr_values": (i32, [ctypes.c_char_p, ctypes.c_char_p, i32, ctypes.POINTER(TcaCsr)]),
     "tca_dense_to_csr": (i32, [vp, i32, i32, i32, ctypes.POINTER(TcaCsr)]),
     "tca_csr_to_dense": (i32, [ctypes.POINTER(TcaCsr), vp]),
     "tca_csr_to_coo": (i32, [ctypes.POINTER(TcaCsr), ctypes.POINTER(TcaCoo)]),

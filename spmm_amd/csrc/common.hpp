@@ -25,6 +25,9 @@ int smtx_read_csr_file(FILE* f, const char* name, int32_t dtype, tca_csr* out);
 int smtx_read_dense_file(FILE* f, const char* name, int32_t dtype, void** dense, int32_t* nRow, int32_t* nCol,
                          int32_t* nnz);
 
+// Allocates the arrays of a host CSR (malloc; tca_csr_free releases them).
+int csr_alloc(tca_csr* out, int32_t nRow, int32_t nCol, int64_t nnz, int32_t dtype);
+
 inline size_t dtype_size(int32_t dtype) { return dtype == TCA_F32 ? 4 : 2; }
 inline bool dtype_ok(int32_t dtype) { return dtype == TCA_F16 || dtype == TCA_F32 || dtype == TCA_BF16; }
 

@@ -253,6 +253,126 @@ int tca_smtx_write(const char* path, const tca_csr* a) {
     return TCA_OK;
 }
 
+// ---- binary CSR cache and values sidecar (no reference counterpart) ----
+// Little-endian: 8-byte magic, then the fields below, then the arrays.
+namespace {
+constexpr char kCsrMagic[8] = {'T', 'C', 'A', 'C', 'S', 'R', '0', '1'};
+constexpr char kValMagic[8] = {'T', 'C', 'A', 'V', 'A', 'L', '0', '1'};
+
+struct CsrHeader {
+    int32_t nRow, nCol;
+    int64_t nnz;
+    int32_t dtype, reserved;
+};
+struct ValHeader {
+    int64_t nnz;
+    int32_t dtype, reserved;
+};
+
+bool write_all(FILE* f, const void* p, size_t n) { return n == 0 || std::fwrite(p, 1, n, f) == n; }
+bool read_all(FILE* f, void* p, size_t n) { return n == 0 || std::fread(p, 1, n, f) == n; }
+
+// Size of an open file (restores the position to the start).
+int64_t file_size(FILE* f) {
+    if (std::fseek(f, 0, SEEK_END) != 0) return -1;
+    const long n = std::ftell(f);
+    std::rewind(f);
+    return n;
+}
+}  // namespace
+
+int tca_csr_write_binary(const char* path, const tca_csr* a) {
+    if (!path || !a || !dtype_ok(a->dtype) || a->nRow < 0 || a->nCol < 0 || a->nnz < 0)
+        return fail(TCA_ERR_INVALID, "tca_csr_write_binary: bad argument");
+    FILE* f = std::fopen(path, "wb");
+    if (!f) return fail(TCA_ERR_IO, "cannot create '%s'", path);
+    const CsrHeader h{a->nRow, a->nCol, a->nnz, a->dtype, 0};
+    bool ok = write_all(f, kCsrMagic, 8) && write_all(f, &h, sizeof h) &&
+              write_all(f, a->row_offset, sizeof(int32_t) * (static_cast<size_t>(a->nRow) + 1)) &&
+              write_all(f, a->col_idx, sizeof(int32_t) * static_cast<size_t>(a->nnz)) &&
+              write_all(f, a->value, dtype_size(a->dtype) * static_cast<size_t>(a->nnz));
+    ok = std::fclose(f) == 0 && ok;
+    return ok ? TCA_OK : fail(TCA_ERR_IO, "write to '%s' failed", path);
+}
+
+int tca_csr_read_binary(const char* path, tca_csr* out) {
+    if (!path || !out) return fail(TCA_ERR_INVALID, "tca_csr_read_binary: bad argument");
+    FILE* f = std::fopen(path, "rb");
+    if (!f) return fail(TCA_ERR_IO, "cannot open '%s'", path);
+    const int64_t size = file_size(f);
+    char magic[8];
+    CsrHeader h{};
+    if (!read_all(f, magic, 8) || std::memcmp(magic, kCsrMagic, 8) != 0 || !read_all(f, &h, sizeof h)) {
+        std::fclose(f);
+        return fail(TCA_ERR_FORMAT, "'%s' is not a binary CSR file", path);
+    }
+    if (h.nRow < 0 || h.nCol < 0 || h.nnz < 0 || h.nnz > INT32_MAX || !dtype_ok(h.dtype) ||
+        size != static_cast<int64_t>(8 + sizeof h + 4 * (static_cast<int64_t>(h.nRow) + 1) + 4 * h.nnz +
+                                     static_cast<int64_t>(dtype_size(h.dtype)) * h.nnz)) {
+        std::fclose(f);
+        return fail(TCA_ERR_FORMAT, "'%s': header (%d x %d, nnz %lld, dtype %d) does not match the file size %lld",
+                    path, h.nRow, h.nCol, (long long)h.nnz, h.dtype, (long long)size);
+    }
+    int st = csr_alloc(out, h.nRow, h.nCol, h.nnz, h.dtype);
+    if (st) {
+        std::fclose(f);
+        return st;
+    }
+    const bool ok = read_all(f, out->row_offset, sizeof(int32_t) * (static_cast<size_t>(h.nRow) + 1)) &&
+                    read_all(f, out->col_idx, sizeof(int32_t) * static_cast<size_t>(h.nnz)) &&
+                    read_all(f, out->value, dtype_size(h.dtype) * static_cast<size_t>(h.nnz));
+    std::fclose(f);
+    if (!ok) {
+        tca_csr_free(out);
+        return fail(TCA_ERR_IO, "read of '%s' failed", path);
+    }
+    st = tca_csr_validate(out->row_offset, out->col_idx, out->nRow, out->nCol, out->nnz);
+    if (st) tca_csr_free(out);
+    return st;
+}
+
+int tca_values_write(const char* path, const void* values, int64_t nnz, int32_t dtype) {
+    if (!path || (nnz > 0 && !values) || nnz < 0 || !dtype_ok(dtype))
+        return fail(TCA_ERR_INVALID, "tca_values_write: bad argument");
+    FILE* f = std::fopen(path, "wb");
+    if (!f) return fail(TCA_ERR_IO, "cannot create '%s'", path);
+    const ValHeader h{nnz, dtype, 0};
+    bool ok = write_all(f, kValMagic, 8) && write_all(f, &h, sizeof h) &&
+              write_all(f, values, dtype_size(dtype) * static_cast<size_t>(nnz));
+    ok = std::fclose(f) == 0 && ok;
+    return ok ? TCA_OK : fail(TCA_ERR_IO, "write to '%s' failed", path);
+}
+
+int tca_smtx_read_csr_values(const char* smtx_path, const char* values_path, int32_t dtype, tca_csr* out) {
+    if (!smtx_path || !values_path || !out || !dtype_ok(dtype))
+        return fail(TCA_ERR_INVALID, "tca_smtx_read_csr_values: bad argument");
+    FILE* f = std::fopen(values_path, "rb");
+    if (!f) return fail(TCA_ERR_IO, "cannot open '%s'", values_path);
+    const int64_t size = file_size(f);
+    char magic[8];
+    ValHeader h{};
+    if (!read_all(f, magic, 8) || std::memcmp(magic, kValMagic, 8) != 0 || !read_all(f, &h, sizeof h) ||
+        h.nnz < 0 || !dtype_ok(h.dtype) ||
+        size != static_cast<int64_t>(8 + sizeof h + static_cast<int64_t>(dtype_size(h.dtype)) * h.nnz)) {
+        std::fclose(f);
+        return fail(TCA_ERR_FORMAT, "'%s' is not a values file of its stated size", values_path);
+    }
+    std::vector<char> vals(dtype_size(h.dtype) * static_cast<size_t>(h.nnz) + 1);
+    const bool ok = read_all(f, vals.data(), dtype_size(h.dtype) * static_cast<size_t>(h.nnz));
+    std::fclose(f);
+    if (!ok) return fail(TCA_ERR_IO, "read of '%s' failed", values_path);
+    int st = tca_smtx_read_csr(smtx_path, dtype, out);
+    if (st) return st;
+    if (out->nnz != h.nnz) {
+        const int32_t got = out->nnz;
+        tca_csr_free(out);
+        return fail(TCA_ERR_FORMAT, "'%s' holds %lld values, '%s' has %d nonzeros", values_path, (long long)h.nnz,
+                    smtx_path, got);
+    }
+    tca_convert_array(vals.data(), h.dtype, out->value, dtype, h.nnz);
+    return TCA_OK;
+}
+
 int tca_mtx_read_csr(const char* path, int32_t pattern_only, int32_t zero_based, int32_t dtype, tca_csr* out) {
     if (!path || !out || !dtype_ok(dtype)) return fail(TCA_ERR_INVALID, "tca_mtx_read_csr: bad argument");
     FILE* f = std::fopen(path, "rb");

@@ -341,3 +341,7 @@ int tca_naive_csr_spmm(const tca_csr* a, const void* B, float* C, int32_t N, int
 }
 
 }  // extern "C"
+
+int tca::csr_alloc(tca_csr* out, int32_t nRow, int32_t nCol, int64_t nnz, int32_t dtype) {
+    return alloc_csr(out, nRow, nCol, nnz, dtype);
+}

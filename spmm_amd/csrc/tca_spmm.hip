@@ -211,6 +211,25 @@ int tca_warm_up(void) {
     return TCA_OK;
 }
 
+int tca_launch_floor(void* stream, int32_t iters, float* avg_ms) {
+    if (iters < 1 || !avg_ms) return fail(TCA_ERR_INVALID, "tca_launch_floor: bad argument");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(warm_up_kernel, dim3(1), dim3(64), 0, s);
+    hipEvent_t e0, e1;
+    TCA_HIP_TRY(hipEventCreate(&e0));
+    TCA_HIP_TRY(hipEventCreate(&e1));
+    (void)hipEventRecord(e0, s);
+    for (int i = 0; i < iters; i++) hipLaunchKernelGGL(warm_up_kernel, dim3(1), dim3(64), 0, s);
+    (void)hipEventRecord(e1, s);
+    float ms = 0.f;
+    const bool ok = hipEventSynchronize(e1) == hipSuccess && hipEventElapsedTime(&ms, e0, e1) == hipSuccess;
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    if (!ok) return fail(TCA_ERR_HIP, "event timing failed");
+    *avg_ms = ms / static_cast<float>(iters);
+    return TCA_OK;
+}
+
 int tca_device_count(int32_t* count) {
     int n = 0;
     hipError_t e = hipGetDeviceCount(&n);

@@ -302,6 +302,47 @@ def test_csr_transpose_matches_the_dense_transpose(m, k, p):
     assert np.array_equal(np.sort(perm[:a.nnz]), np.arange(a.nnz))
 
 
+@pytest.mark.parametrize("dtype", [S.TCA_F16, S.TCA_F32, S.TCA_BF16])
+def test_binary_csr_cache_and_values_sidecar_round_trip(tmp_path, dtype):
+    a, _ = S.gen_lognormal_rows(300, 500, 30, seed=3, dtype=dtype)
+    p = str(tmp_path / "a.tcsr")
+    S.write_csr_binary(p, a)
+    b = S.read_csr_binary(p)
+    assert (b.nrow, b.ncol, b.dtype) == (a.nrow, a.ncol, a.dtype)
+    assert np.array_equal(b.rowptr, a.rowptr) and np.array_equal(b.colidx, a.colidx)
+    assert np.array_equal(b.values.view(np.uint8), a.values.view(np.uint8))
+    # .smtx pattern + values sidecar reproduce the matrix; values convert to the requested dtype
+    sm, sv = str(tmp_path / "a.smtx"), str(tmp_path / "a.values")
+    S.write_smtx(sm, a)
+    S.write_values(sv, a)
+    c = S.read_smtx(sm, dtype, values_path=sv)
+    assert np.array_equal(c.colidx, a.colidx) and np.array_equal(c.values.view(np.uint8), a.values.view(np.uint8))
+    c32 = S.read_smtx(sm, S.TCA_F32, values_path=sv)
+    assert np.array_equal(c32.values, a.values_f32())
+
+
+def test_binary_files_reject_damage(tmp_path):
+    a, _ = S.gen_bernoulli(40, 30, 0.2, seed=2, dtype=S.TCA_F32)
+    p = tmp_path / "a.tcsr"
+    S.write_csr_binary(str(p), a)
+    raw = p.read_bytes()
+    (tmp_path / "short.tcsr").write_bytes(raw[:-4])                       # truncated
+    (tmp_path / "magic.tcsr").write_bytes(b"X" + raw[1:])                 # wrong magic
+    bad = bytearray(raw)
+    off = 8 + 24 + 4 * 41                                                 # first column index
+    bad[off:off + 4] = (10 ** 6).to_bytes(4, "little")                    # column out of range
+    (tmp_path / "col.tcsr").write_bytes(bytes(bad))
+    for name in ("short", "magic", "col"):
+        with pytest.raises(S.TcaError):
+            S.read_csr_binary(str(tmp_path / f"{name}.tcsr"))
+    sm, sv = str(tmp_path / "a.smtx"), str(tmp_path / "b.values")
+    S.write_smtx(sm, a)
+    other, _ = S.gen_bernoulli(40, 30, 0.5, seed=9, dtype=S.TCA_F32)
+    S.write_values(sv, other)                                             # nnz mismatch
+    with pytest.raises(S.TcaError):
+        S.read_smtx(sm, S.TCA_F32, values_path=sv)
+
+
 # -------------------------------------------------------------- planner
 @pytest.mark.parametrize("n,dtype", [(256, S.TCA_F16), (512, S.TCA_F16), (64, S.TCA_F16), (128, S.TCA_F32),
                                      (7, S.TCA_F32), (100, S.TCA_BF16), (1000, S.TCA_F16)])
