@@ -98,6 +98,7 @@ struct MfmaArgs {
     int col_blocks;          // blockIdx.x = window * col_blocks + column block
     uint32_t B_bytes, packed_bytes, ucols_bytes, eoff_bytes;
     int sentinel;            // index of the kNoEntry entry, loaded for empty slots
+    const void* zeros;       // 16 zero bytes (source of padding B pieces, LDS-DMA kernel)
 };
 
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;

@@ -158,9 +158,11 @@ void condense(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_t w
 }
 
 void plan_mfma(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_t N, int32_t dtype, bool force,
-               bool disable, double min_density, MfmaPlan* p) {
-    constexpr int32_t kWin = 64, kStep = 32, kMaxStep = 1024;
+               bool disable, double min_density, const MfmaShape& shape, MfmaPlan* p) {
+    constexpr int32_t kStep = 32;
+    const int32_t kWin = shape.win_rows, kMaxStep = shape.max_step_entries;
     *p = MfmaPlan();
+    p->win_rows = kWin;
     p->row_mfma.assign(M, 0);
     if (disable || dtype == TCA_F32 || N % 8 != 0 || M == 0) return;
     std::vector<int64_t> uoff;
@@ -173,9 +175,9 @@ void plan_mfma(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_t 
         const int32_t r0 = w * kWin, r1 = std::min(M, r0 + kWin);
         const int64_t nz = rowptr[r1] - rowptr[r0];
         const int64_t ucount = uoff[w + 1] - uoff[w];
-        if (nz == 0 || nz >= (int64_t(1) << 21)) continue;
+        if (nz == 0 || nz >= (int64_t(1) << 20)) continue;
         const int64_t steps = (ucount + kStep - 1) / kStep;
-        // nonzeros per step must fit 4 per thread of the 256-thread workgroup
+        // nonzeros per step must fit the kernel's entry slots
         std::vector<int32_t> per(steps, 0);
         for (int32_t j = rowptr[r0]; j < rowptr[r1]; j++) per[cpos[j] / kStep]++;
         if (*std::max_element(per.begin(), per.end()) > kMaxStep) continue;
@@ -193,9 +195,10 @@ void plan_mfma(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_t 
             nz_take += rowptr[r1] - rowptr[r0];
             max_steps = std::max<int64_t>(max_steps, (uoff[w + 1] - uoff[w] + kStep - 1) / kStep);
         }
-        const int64_t wgs = n_take * ((N + 127) / 128);
+        const int64_t wgs = n_take * ((N + shape.tile_cols - 1) / shape.tile_cols);
         const int64_t rounds = (wgs + 255) / 256;
-        const double t_tile = kMfmaFixedUs + static_cast<double>(rounds) * ((max_steps + 3) / 4 + 4) * kMfmaIterUs;
+        const double t_tile =
+            shape.fixed_us + static_cast<double>(rounds) * ((max_steps + 3) / 4 + shape.fill_iters) * shape.iter_us;
         const double t_row = static_cast<double>(nz_take) * N * 2.0 / kRowGatherBytesPerUs;
         if (n_take > 0 && t_tile >= t_row) {
             std::fill(take.begin(), take.end(), 0);
@@ -228,8 +231,8 @@ void plan_mfma(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_t 
             for (int32_t j = rowptr[r]; j < rowptr[r + 1]; j++) {
                 const int32_t s = cpos[j] / kStep;
                 p->entries[ebase + fill[s]++] = static_cast<uint32_t>(r - r0) |
-                                                (static_cast<uint32_t>(cpos[j] % kStep) << 6) |
-                                                (static_cast<uint32_t>(j - rowptr[r0]) << 11);
+                                                (static_cast<uint32_t>(cpos[j] % kStep) << 7) |
+                                                (static_cast<uint32_t>(j - rowptr[r0]) << 12);
             }
         for (int32_t r = r0; r < r1; r++) p->row_mfma[r] = 1;
         p->nnz += rowptr[r1] - rowptr[r0];
@@ -237,7 +240,6 @@ void plan_mfma(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_t 
         p->rows += r1 - r0;
     }
     p->eoff.push_back(static_cast<int32_t>(p->entries.size()));
-    (void)kMaxStep;
 }
 
 }  // namespace tca
@@ -300,7 +302,7 @@ extern "C" int tca_plan_mfma_windows(const int32_t* rowptr, const int32_t* colid
     MfmaPlan p;
     const char* md = std::getenv("TCA_MFMA_MIN_DENSITY");
     plan_mfma(rowptr, colidx, M, N, dtype, (flags & TCA_PLAN_FORCE_MFMA) != 0, (flags & TCA_PLAN_NO_MFMA) != 0,
-              md ? std::atof(md) : kMfmaMinDensity, &p);
+              md ? std::atof(md) : kMfmaMinDensity, mfma_shape(flags), &p);
     const int32_t steps = static_cast<int32_t>(p.eoff.size()) - 1;
     if (windows) {
         if (*n_windows < static_cast<int32_t>(p.windows.size()) || *n_steps < steps ||

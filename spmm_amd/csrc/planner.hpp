@@ -13,6 +13,8 @@
 #include <cstdint>
 #include <vector>
 
+#include "../../include/tca_spmm.h"
+
 namespace tca {
 
 // Task kinds of the row kernel (int4 {x, y, z, w}).
@@ -43,32 +45,47 @@ struct RowPlan {
     int32_t n_multi = 0, n_seg = 0, n_rowtasks = 0, n_wide = 0;
 };
 
-// Row windows routed to the MFMA tile kernel (64 rows each).  For window i:
+// Row windows routed to an MFMA tile kernel (64 rows each for the
+// register-staged kernel, 128 for the LDS-DMA kernel).  For window i:
 // windows[i] = {first row, steps, first global step, first nonzero}; step s
 // of the window has B rows ucols[(first global step + s) * 32 + 0..31]
 // (-1 = padding past the column union) and nonzeros
 // entries[eoff[g] .. eoff[g + 1]) with g its global step; an entry packs the
-// row within the window (6 bits), the column within the step (5 bits, bit 6)
-// and the nonzero index minus the window's first nonzero (bit 11 up).
+// row within the window (7 bits), the column within the step (5 bits, bit 7)
+// and the nonzero index minus the window's first nonzero (bit 12 up).
 // Routing.  A window is eligible for the MFMA tile kernel when its condensed
-// tile density nnz / (rows * padded |U|) is at least kMfmaMinDensity.  The
-// eligible windows then go to the tile kernel as a set when a cost model
-// predicts it beats the row kernel on them:
-//   tile kernel  ~ kMfmaFixedUs + rounds * (max steps / 4 + 4) * kMfmaIterUs
+// tile density nnz / (rows * padded |U|) is at least kMfmaMinDensity and no
+// step holds more nonzeros than the kernel's entry slots.  The eligible
+// windows then go to the tile kernel as a set when a cost model predicts it
+// beats the row kernel on them:
+//   tile kernel  ~ fixed_us + rounds * (max steps / 4 + fill_iters) * iter_us
 //                  (rounds = ceil(workgroups / 256): one workgroup per CU;
-//                   4 steps per iteration plus a 4-iteration pipeline fill),
+//                   4 steps per iteration plus the pipeline fill),
 //   row kernel   ~ eligible nnz * N * value size / kRowGatherBytesPerUs
 //                  (B-row gathers through L2).
 // Constants measured on MI355X (fp16, 4096-row lognormal and Bernoulli
-// matrices, N = 256 / 512): an iteration of 4 steps takes ~0.95 us per
-// workgroup; the row kernel sustains ~20 TB/s of gathered B rows; density
-// below ~0.04 never paid.
+// matrices, N = 256 / 512); the row kernel sustains ~20 TB/s of gathered B
+// rows; density below ~0.04 never paid.
 constexpr double kMfmaMinDensity = 0.04;
-constexpr double kMfmaFixedUs = 3.0;
-constexpr double kMfmaIterUs = 0.95;
 constexpr double kRowGatherBytesPerUs = 20.0e6;
 
+struct MfmaShape {
+    int32_t win_rows;          // rows per window
+    int32_t tile_cols;         // C columns per workgroup
+    int32_t max_step_entries;  // nonzeros a step may hold (entry slots of the kernel)
+    double fixed_us, iter_us;  // cost model: launch + prologue, one 4-step iteration
+    int32_t fill_iters;        // pipeline fill, in iterations
+};
+// Register-staged kernel: 64 x 128 tiles, up to 1024 nonzeros per step, a
+// 4-step iteration ~0.95 us.  LDS-DMA kernel: 128 x 64 tiles, up to 512.
+constexpr MfmaShape kMfmaRegsShape = {64, 128, 1024, 3.0, 0.95, 4};
+constexpr MfmaShape kMfmaDmaShape = {128, 64, 512, 3.0, 0.95, 3};
+inline const MfmaShape& mfma_shape(uint32_t flags) {
+    return (flags & TCA_PLAN_MFMA_DMA) ? kMfmaDmaShape : kMfmaRegsShape;
+}
+
 struct MfmaPlan {
+    int32_t win_rows = 64;
     std::vector<Int4> windows;
     std::vector<int32_t> ucols;
     std::vector<int32_t> eoff;
@@ -82,9 +99,9 @@ struct MfmaPlan {
 // Windows routed by the rule above (min_density replaces kMfmaMinDensity; with
 // force every qualifying window, with disable none).  Only for fp16 / bf16 and
 // N % 8 == 0; a window qualifies only while its nonzeros fit the entry
-// encoding (< 2^21) and no step holds more than 1024 of them.
+// encoding (< 2^20) and no step holds more than shape.max_step_entries.
 void plan_mfma(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_t N, int32_t dtype, bool force,
-               bool disable, double min_density, MfmaPlan* p);
+               bool disable, double min_density, const MfmaShape& shape, MfmaPlan* p);
 
 // Column chunks per XCD pay only when B overflows the L2s: 0 (automatic
 // chunking) when B is larger than 8 MiB, else 1.  TCA_SLICES (tuning only)

@@ -12,6 +12,7 @@
 #include "planner.hpp"
 #include "row_kernel.hpp"
 #include "mfma_kernel.hpp"
+#include "mfma_dma_kernel.hpp"
 #include "sddmm_kernel.hpp"
 
 using namespace tca;
@@ -31,6 +32,9 @@ struct tca_spmm_plan {
     MfmaPlan mfma;
     int32_t mfma_col_blocks = 0;
     int32_t mfma_slots = 1;  // entries per thread and step in the MFMA kernel (1, 2 or 4)
+    bool mfma_dma = false;   // LDS-DMA tile kernel instead of the register-staged one
+    size_t mfma_zeros_at = 0;  // word offset of 16 zero bytes in d_packed (LDS-DMA kernel)
+    size_t n_packed = 0;       // words of d_packed
     int4* d_windows = nullptr;
     uint32_t* d_ucols = nullptr;
     int* d_eoff = nullptr;
@@ -156,11 +160,25 @@ int launch_mfma(const tca_spmm_plan* p, const void* B, float* C, hipStream_t s) 
     // The packed entry array ends with one kNoEntry sentinel (set at plan time).
     const int n_ent = static_cast<int>(p->mfma.entries.size());
     a.sentinel = n_ent;
-    a.packed_bytes = static_cast<uint32_t>((static_cast<uint64_t>(n_ent) + 1) * 4);
+    a.zeros = p->d_packed + p->mfma_zeros_at;
+    a.packed_bytes = static_cast<uint32_t>(p->n_packed * 4);
     a.ucols_bytes = static_cast<uint32_t>(p->mfma.ucols.size() * 4);
     a.eoff_bytes = static_cast<uint32_t>(p->mfma.eoff.size() * 4);
     const dim3 grid(static_cast<unsigned>(p->mfma.windows.size()) * p->mfma_col_blocks);
     const bool bf = p->dtype == TCA_BF16;
+    if (p->mfma_dma && p->mfma_slots <= 2) {
+        switch (p->mfma_slots) {
+            case 1:
+                if (bf) hipLaunchKernelGGL((mfma_dma_kernel<true, 1>), grid, dim3(kMfmaThreads), 0, s, a);
+                else hipLaunchKernelGGL((mfma_dma_kernel<false, 1>), grid, dim3(kMfmaThreads), 0, s, a);
+                return TCA_OK;
+            case 2:
+                if (bf) hipLaunchKernelGGL((mfma_dma_kernel<true, 2>), grid, dim3(kMfmaThreads), 0, s, a);
+                else hipLaunchKernelGGL((mfma_dma_kernel<false, 2>), grid, dim3(kMfmaThreads), 0, s, a);
+                return TCA_OK;
+            default: break;  // four slots per thread: register-staged kernel (LDS budget)
+        }
+    }
     switch (p->mfma_slots) {
         case 1:
             if (bf) hipLaunchKernelGGL((mfma_tile_kernel<true, 1>), grid, dim3(kMfmaThreads), 0, s, a);
@@ -268,12 +286,15 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
         delete p;
         return fail(TCA_ERR_HIP, "no HIP device");
     }
-    // Dense-enough 64-row windows go to the MFMA tile kernel (fp16 / bf16).
+    // Dense-enough row windows go to an MFMA tile kernel (fp16 / bf16): 64-row
+    // windows x 128 columns (register-staged) or 128 x 64 (LDS-DMA kernel).
     // TCA_MFMA_MIN_DENSITY (tuning only) overrides the routing threshold.
     const char* md = std::getenv("TCA_MFMA_MIN_DENSITY");
+    const MfmaShape& shape = mfma_shape(flags);
     plan_mfma(rowptr, colidx, M, N, dtype, (flags & TCA_PLAN_FORCE_MFMA) != 0, (flags & TCA_PLAN_NO_MFMA) != 0,
-              md ? std::atof(md) : kMfmaMinDensity, &p->mfma);
-    p->mfma_col_blocks = (N + kTileCols - 1) / kTileCols;
+              md ? std::atof(md) : kMfmaMinDensity, shape, &p->mfma);
+    p->mfma_dma = (flags & TCA_PLAN_MFMA_DMA) != 0;
+    p->mfma_col_blocks = (N + shape.tile_cols - 1) / shape.tile_cols;
     {
         int32_t most = 0;
         for (size_t i = 0; i + 1 < p->mfma.eoff.size(); i++) most = std::max(most, p->mfma.eoff[i + 1] - p->mfma.eoff[i]);
@@ -308,11 +329,20 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
                                             : static_cast<uint32_t>(p->mfma.ucols[i]) * static_cast<uint32_t>(N) * 2u;
         if ((st = dev_upload(&p->d_ucols, uoff.data(), uoff.size()))) return bail(st);
         if ((st = dev_upload(&p->d_eoff, p->mfma.eoff.data(), p->mfma.eoff.size()))) return bail(st);
+        // Packed entries.  Register-staged kernel: walk order, then one
+        // kNoEntry sentinel.  LDS-DMA kernel: step g at g * 256 * slots, its
+        // unused words kNoEntry, then 16 zero bytes (padding B source).
         const size_t ne = p->mfma.entries.size();
+        const size_t nsteps_all = p->mfma.eoff.size() - 1;
+        const size_t ewords = 256u * static_cast<size_t>(p->mfma_slots);
+        const size_t npacked = p->mfma_dma ? nsteps_all * ewords + 4 : ne + 1;
+        p->mfma_zeros_at = p->mfma_dma ? nsteps_all * ewords : 0;
         std::vector<int> dst(ne);
         std::vector<uint16_t> cell(ne);
-        std::vector<uint32_t> packed(ne + 1, 0u);
+        std::vector<uint32_t> packed(npacked, kNoEntry);
+        if (p->mfma_dma) std::fill(packed.end() - 4, packed.end(), 0u);
         std::vector<int4> segs;
+        const int row_mask = 127, k_shift = 7, idx_shift = 12;
         for (size_t w = 0, e = 0, base = 0; w < p->mfma.windows.size(); w++) {
             // The window's entries, indexed by their offset in its CSR range.
             const Int4 win = p->mfma.windows[w];
@@ -320,20 +350,22 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
             const size_t cnt = e_end - e;
             if (!segs.empty() && segs.back().x + segs.back().y == win.w) segs.back().y += static_cast<int>(cnt);
             else segs.push_back(int4{win.w, static_cast<int>(cnt), static_cast<int>(base), 0});
-            for (; e < e_end; e++) {
-                const uint32_t en = p->mfma.entries[e];
-                const size_t k = base + (en >> 11);
-                dst[k] = static_cast<int>(e);
-                cell[k] = static_cast<uint16_t>(a_cell(static_cast<int>(en & 63u), static_cast<int>((en >> 6) & 31u)));
-            }
+            for (int32_t g = win.z; g < win.z + win.y; g++)
+                for (; e < static_cast<size_t>(p->mfma.eoff[g + 1]); e++) {
+                    const uint32_t en = p->mfma.entries[e];
+                    const size_t k = base + (en >> idx_shift);
+                    dst[k] = p->mfma_dma ? static_cast<int>(g * ewords + (e - p->mfma.eoff[g])) : static_cast<int>(e);
+                    cell[k] = static_cast<uint16_t>(
+                        a_cell(static_cast<int>(en & row_mask), static_cast<int>((en >> k_shift) & 31u)));
+                }
             base += cnt;
         }
-        packed[ne] = kNoEntry;
         p->n_pk_seg = static_cast<int32_t>(segs.size());
+        p->n_packed = npacked;
         if ((st = dev_upload(&p->d_pk_seg, segs.data(), segs.size()))) return bail(st);
         if ((st = dev_upload(&p->d_pk_dst, dst.data(), ne))) return bail(st);
         if ((st = dev_upload(&p->d_pk_cell, cell.data(), ne))) return bail(st);
-        if ((st = dev_upload(&p->d_packed, packed.data(), ne + 1))) return bail(st);
+        if ((st = dev_upload(&p->d_packed, packed.data(), npacked))) return bail(st);
     }
     if (hipDeviceSynchronize() != hipSuccess) return bail(fail(TCA_ERR_HIP, "hipDeviceSynchronize failed"));
 
@@ -363,7 +395,10 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
     in.cond_cols_mfma = p->mfma.cond_cols;
     in.mfma_blocks = in.n_windows_mfma * p->mfma_col_blocks;
     in.mfma_blockdim = kMfmaThreads;
-    in.mfma_lds_bytes = p->mfma_slots == 1 ? mfma_lds_bytes<1>() : p->mfma_slots == 2 ? mfma_lds_bytes<2>() : mfma_lds_bytes<4>();
+    if (p->mfma_dma && p->mfma_slots <= 2)
+        in.mfma_lds_bytes = p->mfma_slots == 1 ? mfma_dma_lds_bytes<1>() : mfma_dma_lds_bytes<2>();
+    else
+        in.mfma_lds_bytes = p->mfma_slots == 1 ? mfma_lds_bytes<1>() : p->mfma_slots == 2 ? mfma_lds_bytes<2>() : mfma_lds_bytes<4>();
     in.scratch_bytes = static_cast<int64_t>(n_seg_total * N * sizeof(float));
     in.plan_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
     *plan = p;

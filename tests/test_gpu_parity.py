@@ -137,25 +137,30 @@ def test_exact_bit_equal_all_widths(torch_cuda, dtype):
         assert np.array_equal(got, want), (dtype, n, np.abs(got - want).max())
 
 
+@pytest.mark.parametrize("variant", [0, S.TCA_PLAN_MFMA_DMA], ids=["regs", "dma"])
 @pytest.mark.parametrize("dtype", [S.TCA_F16, S.TCA_BF16])
-def test_mfma_exact_bit_equal(torch_cuda, dtype):
+def test_mfma_exact_bit_equal(torch_cuda, dtype, variant):
     """Condensed-tile MFMA path (forced on every eligible window) is bit-equal
     to the oracle on exact-arithmetic inputs, for partial windows, partial
     column blocks and empty rows.  The cases cover one, two and four entry
     slots per thread (up to 256, 512 and 1024 nonzeros in a step) and windows
-    whose steps span several pipeline blocks."""
+    whose steps span several pipeline blocks, for both tile kernels (register
+    staging and global->LDS transfers).  The LDS-DMA kernel takes at most 512
+    nonzeros per step of its 128-row windows: the cases marked dense stay on
+    the row kernel under it (still checked against the oracle)."""
     rng = np.random.default_rng(71 + dtype)
+    dense = {(200, 64, 0.45), (128, 2048, 0.2), (64, 1500, 0.4)}
     for m, k, p in [(64, 256, 0.1), (130, 700, 0.05), (200, 64, 0.45), (17, 40, 0.3), (96, 5000, 0.004),
-                    (128, 2048, 0.2), (64, 1500, 0.4)]:
+                    (128, 2048, 0.2), (64, 1500, 0.4), (128, 2048, 0.1), (100, 1000, 0.12)]:
         lens = rng.binomial(k, p, m)
         lens[rng.random(m) < 0.1] = 0
         a = make_csr(rng, lens, k, dtype)
         for n in (8, 16, 64, 128, 136, 256, 512):
             b = S.to_storage(exact_dense(rng, (k, n)), dtype)
-            with S.Plan(a, n, S.TCA_PLAN_FORCE_MFMA) as pl:
+            with S.Plan(a, n, S.TCA_PLAN_FORCE_MFMA | variant) as pl:
                 info = pl.info()
                 got = run_gpu(torch_cuda, a, b, plan=pl)
-            assert info["n_windows_mfma"] > 0, (m, k, n)
+            assert info["n_windows_mfma"] > 0 or (variant and (m, k, p) in dense), (m, k, n)
             want = oracle_c(a, b)
             assert np.array_equal(got, want), (m, k, p, n, np.abs(got - want).max())
 

@@ -235,17 +235,21 @@ def test_condense_windows_bit_exact_with_oracle(m, k, p, win):
 
 @pytest.mark.parametrize("m,k,n,p,flags", [(200, 700, 128, 0.06, S.TCA_PLAN_FORCE_MFMA),
                                            (130, 300, 64, 0.02, S.TCA_PLAN_FORCE_MFMA),
-                                           (64, 2048, 256, 0.3, S.TCA_PLAN_FORCE_MFMA)])
+                                           (64, 2048, 256, 0.3, S.TCA_PLAN_FORCE_MFMA),
+                                           (300, 700, 128, 0.06, S.TCA_PLAN_FORCE_MFMA | S.TCA_PLAN_MFMA_DMA),
+                                           (129, 1500, 64, 0.1, S.TCA_PLAN_FORCE_MFMA | S.TCA_PLAN_MFMA_DMA)])
 def test_mfma_window_plan_decodes_to_the_csr(m, k, n, p, flags):
     """Every MFMA window's steps, B-row lists and entries reproduce the CSR
-    exactly, with the oracle's condensed positions."""
+    exactly, with the oracle's condensed positions (64-row windows for the
+    register-staged tile kernel, 128-row windows for the LDS-DMA kernel)."""
     a, _ = S.gen_bernoulli(m, k, p, seed=7, dtype=S.TCA_F16)
     windows, ucols, eoff, entries = S.plan_mfma_windows(a, n, flags=flags)
     assert len(windows) > 0
-    uo, uc, cp = oracle.condense_windows(a.rowptr, a.colidx, m, 64)
+    win = 128 if flags & S.TCA_PLAN_MFMA_DMA else 64
+    uo, uc, cp = oracle.condense_windows(a.rowptr, a.colidx, m, win)
     for row0, steps, gstep, nz0 in windows:
-        w = row0 // 64
-        assert row0 % 64 == 0 and nz0 == a.rowptr[row0]
+        w = row0 // win
+        assert row0 % win == 0 and nz0 == a.rowptr[row0]
         u = uc[uo[w]:uo[w + 1]]
         assert steps == (len(u) + 31) // 32
         cols = ucols[gstep * 32:(gstep + steps) * 32]
@@ -253,12 +257,12 @@ def test_mfma_window_plan_decodes_to_the_csr(m, k, n, p, flags):
         seen = []
         for s in range(steps):
             for e in entries[eoff[gstep + s]:eoff[gstep + s + 1]]:
-                r, kk, rel = int(e) & 63, (int(e) >> 6) & 31, int(e) >> 11
+                r, kk, rel = int(e) & 127, (int(e) >> 7) & 31, int(e) >> 12
                 j = nz0 + rel
                 assert a.rowptr[row0 + r] <= j < a.rowptr[row0 + r + 1]
                 assert cp[j] == 32 * s + kk and cols[32 * s + kk] == a.colidx[j]
                 seen.append(j)
-        r1 = min(m, row0 + 64)
+        r1 = min(m, row0 + win)
         assert sorted(seen) == list(range(a.rowptr[row0], a.rowptr[r1]))
     none = S.plan_mfma_windows(a, n, flags=S.TCA_PLAN_NO_MFMA)[0]
     assert len(none) == 0
