@@ -9,27 +9,32 @@
 // serves, so each gathered B row feeds twice the rows.
 //   * consumer wavefront w (one per SIMD) takes step 4 i + w of iteration i:
 //     8 row blocks x 4 column blocks = 32 v_mfma_f32_16x16x32 into 128
-//     accumulators.  Each step's A and B tiles are read from LDS by one
-//     wavefront only; the four partial 128 x 64 tiles are added through LDS
-//     once at the end;
-//   * each consumer builds its own A tiles: it reads its step's packed entries
-//     from LDS and scatters them into a private, double-buffered A tile;
-//   * producer wavefronts only issue global_load_lds_dwordx4 transfers (lane
-//     L of one instruction writes 16 bytes at M0 + 16 L): per step one 1 KiB
-//     instruction of B rows per producer and 256 entry words per instruction.
-//     Their plan metadata (B row offsets) comes through scalar loads one
-//     iteration ahead, so the only vector-memory operations of a producer
-//     are its transfers: each iteration issues the same number N of them,
-//     and s_waitcnt vmcnt(N) after issuing retires exactly the previous
-//     iteration's transfers.  (An LDS transfer costs a producer wavefront
-//     ~100 cycles to issue whatever its width, so the kernel issues as few
-//     and as wide ones as it can.)
-// Pipeline, iteration i (one barrier each):
-//   producers: issue B(i + 2), entries(i + 3); wait for B(i + 1), entries(i + 2)
-//   consumers: MFMAs of step 4 i + w with A(i) and B(i); build A(i + 1)
-// Rings: B 3 slots, entries 3 slots, A 2 slots per consumer.
-// Packed entries of global step g sit at g * 256 * kSlots (unused words
-// kNoEntry), so a step's entries are one or two aligned 1 KiB transfers.
+//     accumulators, nothing else (VALU or LDS instructions placed between a
+//     wavefront's back-to-back MFMAs wait for the MFMA in flight).  Each
+//     step's A and B tiles are read from LDS by one wavefront only; the four
+//     partial 128 x 64 tiles are added through LDS once at the end;
+//   * producer wavefront p issues global_load_lds_dwordx4 transfers (lane L
+//     of one instruction writes 16 bytes at M0 + 16 L): the packed block of
+//     step 4 i + p (its entries and, in the last 32 words, the byte offsets
+//     of the step's 32 B rows) and its share (8 rows) of every step's B
+//     tile.  The B row offsets of a step are read from its packed block in
+//     LDS, one ds_read_b32 per lane and step, so a producer issues no other
+//     memory operation and builds each address with a few VALU operations.
+//     It also builds the A tile of step 4 i + p from the entries it
+//     transferred itself (each lane reads back its own 16 bytes, so its own
+//     vmcnt wait is the only synchronisation) into that consumer's
+//     double-buffered A slot.  Each iteration issues the same transfers in
+//     the same order, and one s_waitcnt vmcnt(N) retires exactly what is due.
+// Pipeline, iteration i (one barrier each), lookahead LB = 3 (one entry slot
+// per thread) or 2 (two), LE = LB + 2:
+//   producers: issue blocks(i + LE), then B(i + LB) (row offsets from
+//              blocks(i + LB)); build A(i + 1) from blocks(i + 1); wait
+//              until blocks(i + LE - 1) and B(i + 1) have landed
+//   consumers: MFMAs of step 4 i + w with A(i) and B(i)
+// Rings: B LB + 1 slots, blocks LE slots, A 2 slots per step of an iteration.
+// The packed block of global step g sits at g * 256 * kSlots words: up to
+// 256 * kSlots - 32 entries (unused words kNoEntry), then the 32 B row
+// offsets (kNoEntry for padding columns).
 // Every transfer address is in bounds: padding columns, steps past the
 // window and columns past N read 16 zero bytes (MfmaArgs::zeros), which also
 // stand for the entries of steps past the window (cell 0, value 0).
@@ -42,15 +47,26 @@
 
 namespace tca {
 
-constexpr int kDmaSteps = 4;     // steps per iteration = consumer wavefronts
-constexpr int kDmaBRing = 3;     // B tile slots (iterations)
-constexpr int kDmaERing = 3;     // packed-entry slots (iterations)
-constexpr int kDmaARing = 2;     // A tile slots per consumer
+constexpr int kDmaSteps = 4;      // steps per iteration = consumer wavefronts
 constexpr int kDmaWinRows = 128;  // rows per window (8 row blocks of 16)
 constexpr int kDmaTileCols = 64;  // columns of C per workgroup
-constexpr int kDmaBRow = kDmaTileCols;               // halves per B-tile row in LDS (128 bytes)
-constexpr int kDmaATile = kDmaWinRows * kStepK;      // halves of one A tile (fragment order)
-constexpr int kDmaAElems = kDmaATile + 64;           // A tile + one dummy cell per lane
+constexpr int kDmaBRow = kDmaTileCols;           // halves per B-tile row in LDS (128 bytes)
+constexpr int kDmaATile = kDmaWinRows * kStepK;  // halves of one A tile (fragment order)
+constexpr int kDmaAElems = kDmaATile + 64;       // A tile + one dummy cell per lane
+constexpr int kDmaStepMeta = kStepK;             // B row offsets at the end of a step's packed block
+
+// Pipeline shape by entry slots (256 words each) per step.
+template <int kSlots>
+struct MfmaDmaShape {
+    static constexpr int kLB = kSlots == 1 ? 3 : 2;  // B lookahead (iterations)
+    static constexpr int kLE = kLB + 2;              // packed-block lookahead
+    static constexpr int kNB = kLB + 1;              // B ring slots
+    static constexpr int kNE = kLE;                  // packed-block ring slots
+    static constexpr int kNA = 2;                    // A slots per step of an iteration
+    static constexpr int kEWords = 256 * kSlots;     // words of a step's packed block
+};
+// Nonzeros a step may hold under the LDS-DMA kernel (two slots).
+constexpr int kDmaMaxStepEntries = 2 * 256 - kDmaStepMeta;
 
 // XOR permutation of the 16-byte pieces of a 128-byte B-tile row: with it the
 // ds_read_b64_tr_b16 fragment reads (two passes of 32 lanes, 8 rows x 32
@@ -59,9 +75,11 @@ __host__ __device__ constexpr int bswz64(int r) { return 2 * (((r >> 1) & 1) | (
 
 template <int kSlots>
 constexpr int mfma_dma_lds_bytes() {
-    constexpr int main = kDmaBRing * kDmaSteps * kStepK * kDmaBRow * 2 + kDmaERing * kDmaSteps * 256 * kSlots * 4 +
-                         kDmaSteps * kDmaARing * kDmaAElems * 2;
+    using SH = MfmaDmaShape<kSlots>;
+    constexpr int main = SH::kNB * kDmaSteps * kStepK * kDmaBRow * 2 + SH::kNE * kDmaSteps * SH::kEWords * 4 +
+                         kDmaSteps * SH::kNA * kDmaAElems * 2;
     constexpr int red = kDmaSteps * 32 * 64 * 16;  // four partial 128 x 64 fp32 tiles
+    static_assert(main <= 160 * 1024, "LDS budget");
     return main > red ? main : red;
 }
 
@@ -85,14 +103,20 @@ __device__ __forceinline__ uint32_t lds_addr(P* p) {
 template <bool kBf16, int kSlots>
 __global__ __launch_bounds__(kMfmaThreads) void mfma_dma_kernel(MfmaArgs a) {
     static_assert(kSlots == 1 || kSlots == 2, "entry slots per step (x 256)");
-    constexpr int KS = kDmaSteps, NB = kDmaBRing, NE = kDmaERing, NA = kDmaARing;
+    using SH = MfmaDmaShape<kSlots>;
+    constexpr int KS = kDmaSteps, NB = SH::kNB, NE = SH::kNE, NA = SH::kNA, LB = SH::kLB, LE = SH::kLE;
     constexpr int kBElems = kStepK * kDmaBRow;  // halves per B tile (4 KiB)
-    constexpr int kEWords = 256 * kSlots;       // entry words per step
+    constexpr int kEWords = SH::kEWords;        // words of a step's packed block
+    constexpr int kMetaAt = kEWords - kDmaStepMeta;
     constexpr int kBBytes = NB * KS * kBElems * 2;
     constexpr int kEBytes = NE * KS * kEWords * 4;
-    // Transfers per producer wavefront and iteration: one B instruction per
-    // step, kSlots entry instructions for one step.
-    constexpr int kOps = KS + kSlots;
+    // Transfers per producer wavefront and iteration: kSlots for one packed
+    // block, then one B instruction per step.  The wait of iteration i must
+    // retire the block issued in iteration i - 1 and B(i + 1): with LB = 3 the
+    // B instructions of iteration i - 1 may stay in flight, with LB = 2 they
+    // are B(i + 1) themselves.
+    constexpr int kOps = kSlots + KS;
+    constexpr int kWait = LB == 3 ? KS + kOps : kOps;
     __shared__ __attribute__((aligned(16))) char smem[mfma_dma_lds_bytes<kSlots>()];
     auto Bs = reinterpret_cast<uint16_t(*)[KS][kBElems]>(smem);                         // [NB][KS][kBElems]
     auto Es = reinterpret_cast<uint32_t(*)[KS][kEWords]>(smem + kBBytes);                // [NE][KS][kEWords]
@@ -125,29 +149,10 @@ __global__ __launch_bounds__(kMfmaThreads) void mfma_dma_kernel(MfmaArgs a) {
         const int br = 8 * lh + (li >> 2);
         const int bx = bswz64(br), bh = (li & 3) >> 1;
         const int b_row = br * kDmaBRow + 4 * (li & 1);
-        const int pad = kDmaATile + lane;
-        int pos_prev[4 * kSlots], pos_cur[4 * kSlots];
-#pragma unroll
-        for (int k = 0; k < 4 * kSlots; k++) pos_prev[k] = pos_cur[k] = pad;
         int bslot = 0;  // B ring slot of iteration i
-        int eslot = 1;  // entry ring slot of iteration i + 1
-        for (int i = -3; i < niters; i++) {
-            uint32_t ent[4 * kSlots];
-            if (i + 1 >= 0) {
-                // entries of A(i + 1): lane reads words 4 lane .. 4 lane + 3 of each 256
-#pragma unroll
-                for (int k = 0; k < kSlots; k++) {
-                    const i32x4v e4 = *reinterpret_cast<const i32x4v*>(&Es[eslot][w][256 * k + 4 * lane]);
-#pragma unroll
-                    for (int q = 0; q < 4; q++) ent[4 * k + q] = static_cast<uint32_t>(e4[q]);
-                }
-            }
-            // Fragments of step 4 i + w are all read first (the MFMAs then run
-            // back to back); the A(i + 1) scatter goes between MFMA groups.
-            const bool active = i >= 0 && KS * i + w < nsteps;
-            const bool build = i + 1 >= 0;
-            i32x4v af[8], bq[4];
-            if (active) {
+        for (int i = -LE; i < niters; i++) {
+            if (i >= 0 && KS * i + w < nsteps) {
+                i32x4v af[8], bq[4];
                 const uint16_t* Ab = &As[w][i & 1][8 * lane];
                 const uint16_t* Bb = &Bs[bslot][w][b_row];
 #pragma unroll
@@ -162,48 +167,20 @@ __global__ __launch_bounds__(kMfmaThreads) void mfma_dma_kernel(MfmaArgs a) {
                                    __builtin_bit_cast(int, __builtin_shufflevector(hi, hi, 0, 1)),
                                    __builtin_bit_cast(int, __builtin_shufflevector(hi, hi, 2, 3))};
                 }
-            }
-            auto mfmas = [&](int c) {
 #pragma unroll
-                for (int b = 0; b < 8; b++) {
-                    if constexpr (kBf16)
-                        acc[b][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                            __builtin_bit_cast(bf16x8, af[b]), __builtin_bit_cast(bf16x8, bq[c]), acc[b][c], 0, 0, 0);
-                    else
-                        acc[b][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                            __builtin_bit_cast(f16x8, af[b]), __builtin_bit_cast(f16x8, bq[c]), acc[b][c], 0, 0, 0);
-                }
-            };
-            // A(i + 1) goes to slot (i + 1) & 1 after A(i - 1)'s cells there are cleared
-            uint16_t* Aw = &As[w][(i + 1) & 1][0];
-            if (active) mfmas(0);
-            __builtin_amdgcn_sched_barrier(0);
-            if (build) {
+                for (int c = 0; c < 4; c++)
 #pragma unroll
-                for (int k = 0; k < 4 * kSlots; k++) Aw[pos_prev[k]] = 0;
-            }
-            __builtin_amdgcn_sched_barrier(0);
-            if (active) mfmas(1);
-            __builtin_amdgcn_sched_barrier(0);
-            if (build) {
-#pragma unroll
-                for (int k = 0; k < 4 * kSlots; k++) {
-                    const uint32_t e = ent[k];
-                    const bool ok = e != kNoEntry;
-                    const int pos = ok ? static_cast<int>(e & 0xffffu) : pad;
-                    Aw[pos] = ok ? static_cast<uint16_t>(e >> 16) : uint16_t(0);
-                    pos_prev[k] = pos_cur[k];
-                    pos_cur[k] = pos;
-                }
-            }
-            __builtin_amdgcn_sched_barrier(0);
-            if (active) {
-                mfmas(2);
-                mfmas(3);
+                    for (int b = 0; b < 8; b++) {
+                        if constexpr (kBf16)
+                            acc[b][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                                __builtin_bit_cast(bf16x8, af[b]), __builtin_bit_cast(bf16x8, bq[c]), acc[b][c], 0, 0, 0);
+                        else
+                            acc[b][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                                __builtin_bit_cast(f16x8, af[b]), __builtin_bit_cast(f16x8, bq[c]), acc[b][c], 0, 0, 0);
+                    }
             }
             __syncthreads();
             if (i >= 0) bslot = bslot == NB - 1 ? 0 : bslot + 1;
-            eslot = eslot == NE - 1 ? 0 : eslot + 1;
         }
     } else {
         // ================= producer: transfers only =================
@@ -220,57 +197,70 @@ __global__ __launch_bounds__(kMfmaThreads) void mfma_dma_kernel(MfmaArgs a) {
             const int col = c0 + 8 * ((lane & 7) ^ bswz64(row));
             bcol = col < a.N ? col * 2 : -1;
         }
-        // B row offsets of rows 8 pw .. 8 pw + 7 for the steps of B(ib), by
-        // scalar loads (constant address space: uniform loads from it are
-        // scalar loads, which keeps vmcnt counting the transfers alone).
-        typedef __attribute__((address_space(4))) const uint32_t* cu32p;
-        const cu32p ucols_c = (cu32p)(a.ucols);
-        uint32_t mu[KS][8];
-        auto load_meta = [&](int ib) {
+        const int pad = kDmaATile + lane;
+        int pos_prev[4 * kSlots], pos_cur[4 * kSlots];
 #pragma unroll
-            for (int sp = 0; sp < KS; sp++) {
-                const int j = min(max(KS * ib + sp, 0), nsteps - 1);
-                const cu32p up = ucols_c + static_cast<size_t>(sbase + j) * kStepK + 8 * pw;
-#pragma unroll
-                for (int r = 0; r < 8; r++) mu[sp][r] = up[r];
-            }
-        };
-        int bslot = 0;  // ring slot of B(i + 2)
-        int eslot = 0;  // ring slot of entries(i + 3)
-        load_meta(-1);
-        for (int i = -3; i < niters; i++) {
-            if (i + 2 >= 0) {
-#pragma unroll
-                for (int sp = 0; sp < KS; sp++) {
-                    const bool in = KS * (i + 2) + sp < nsteps;
-                    // this lane's row offset: a select tree over the step's
-                    // eight values (held as values, so the selects stay
-                    // v_cndmask instead of an indexed private array)
-                    uint32_t m[8];
-#pragma unroll
-                    for (int r = 0; r < 8; r++) m[r] = __builtin_amdgcn_readfirstlane(mu[sp][r]);
-                    const uint32_t u01 = (g8 & 1) ? m[1] : m[0], u23 = (g8 & 1) ? m[3] : m[2];
-                    const uint32_t u45 = (g8 & 1) ? m[5] : m[4], u67 = (g8 & 1) ? m[7] : m[6];
-                    const uint32_t u03 = (g8 & 2) ? u23 : u01, u47 = (g8 & 2) ? u67 : u45;
-                    const uint32_t uo = (g8 & 4) ? u47 : u03;
-                    const char* src = (in && uo != kNoEntry && bcol >= 0) ? Bg + uo + bcol : Zg;
-                    dma_x4(src, lds_addr(&Bs[bslot][sp][kDmaBRow * 8 * pw]));
-                }
-            }
+        for (int k = 0; k < 4 * kSlots; k++) pos_prev[k] = pos_cur[k] = pad;
+        // B(n) sits in ring slot n mod NB.  Every iteration issues the same
+        // transfers, the first ones B(-2), B(-1) from the zero bytes, so that
+        // one wait count holds from the first iteration on.
+        int bslot = NB - 2;
+        int eslot = 0;             // block ring slot of blocks(i + LE): blocks(n) sit in slot n % NE
+        for (int i = -LE; i < niters; i++) {
             {
-                // entries of step 4 (i + 3) + pw
-                const int j = KS * (i + 3) + pw;
+                // packed block of step 4 (i + LE) + p (issued first: see the wait below)
+                const int j = KS * (i + LE) + pw;
                 const uint32_t* ep = a.packed + static_cast<size_t>(sbase + j) * kEWords + 4 * lane;
 #pragma unroll
                 for (int k = 0; k < kSlots; k++)
                     dma_x4(j < nsteps ? static_cast<const void*>(ep + 256 * k) : static_cast<const void*>(Zg),
                            lds_addr(&Es[eslot][pw][256 * k]));
             }
-            // next iteration's metadata (after the transfers that used this one)
-            load_meta(i + 3);
-            wait_vmcnt<kOps>();  // everything issued before this iteration has landed
+            {
+                // rows 8 p .. 8 p + 7 of B(i + LB); row offsets from blocks(i + LB),
+                // which landed by every producer's wait of iteration i - 1
+                const bool real = i + LB >= 0;
+                const int em = eslot >= LE - LB ? eslot - (LE - LB) : eslot + LB;  // (i + LB) % NE
+                uint32_t uo[KS];
+#pragma unroll
+                for (int sp = 0; sp < KS; sp++) uo[sp] = real ? Es[em][sp][kMetaAt + 8 * pw + g8] : kNoEntry;
+#pragma unroll
+                for (int sp = 0; sp < KS; sp++) {
+                    const bool in = real && KS * (i + LB) + sp < nsteps;
+                    const char* src = (in && uo[sp] != kNoEntry && bcol >= 0) ? Bg + uo[sp] + bcol : Zg;
+                    dma_x4(src, lds_addr(&Bs[bslot][sp][kDmaBRow * 8 * pw]));
+                }
+                bslot = bslot == NB - 1 ? 0 : bslot + 1;
+            }
+            if (i + 1 >= 0) {
+                // A(i + 1) of step 4 (i + 1) + p into consumer p's slot (i + 1) & 1,
+                // after clearing A(i - 1)'s cells there.  Every lane reads back
+                // the 16 bytes it transferred; the block's last 32 words (lanes
+                // 56..63 of its last 256) are the B row offsets, not entries.
+                const int er = eslot + 1 - (eslot + 1 >= NE ? NE : 0);  // (i + 1) % NE
+                uint32_t ent[4 * kSlots];
+#pragma unroll
+                for (int k = 0; k < kSlots; k++) {
+                    const i32x4v e4 = *reinterpret_cast<const i32x4v*>(&Es[er][pw][256 * k + 4 * lane]);
+                    const bool meta = k == kSlots - 1 && lane >= 56;
+#pragma unroll
+                    for (int q = 0; q < 4; q++) ent[4 * k + q] = meta ? kNoEntry : static_cast<uint32_t>(e4[q]);
+                }
+                uint16_t* Aw = &As[pw][(i + 1) & 1][0];
+#pragma unroll
+                for (int k = 0; k < 4 * kSlots; k++) Aw[pos_prev[k]] = 0;
+#pragma unroll
+                for (int k = 0; k < 4 * kSlots; k++) {
+                    const uint32_t e = ent[k];
+                    const bool ok = e != kNoEntry;
+                    const int pos = ok ? static_cast<int>(e & 0xffffu) : pad;
+                    Aw[pos] = ok ? static_cast<uint16_t>(e >> 16) : uint16_t(0);
+                    pos_prev[k] = pos_cur[k];
+                    pos_cur[k] = pos;
+                }
+            }
+            wait_vmcnt<kWait>();
             __syncthreads();
-            if (i + 2 >= 0) bslot = bslot == NB - 1 ? 0 : bslot + 1;
             eslot = eslot == NE - 1 ? 0 : eslot + 1;
         }
         wait_vmcnt<0>();

@@ -144,6 +144,10 @@ void launch_pack(const tca_spmm_plan* p, const void* val, hipStream_t s) {
                        p->d_pk_dst, p->d_pk_cell, n_ent, static_cast<const uint16_t*>(val), p->d_packed);
 }
 
+static_assert(kMfmaDmaShape.max_step_entries == kDmaMaxStepEntries, "planner and LDS-DMA kernel agree on step size");
+static_assert(kMfmaDmaShape.win_rows == kDmaWinRows && kMfmaDmaShape.tile_cols == kDmaTileCols, "LDS-DMA tile shape");
+static_assert(kMfmaRegsShape.win_rows == kWinRows && kMfmaRegsShape.tile_cols == kTileCols, "register tile shape");
+
 int launch_mfma(const tca_spmm_plan* p, const void* B, float* C, hipStream_t s) {
     if (p->mfma.windows.empty()) return TCA_OK;
     MfmaArgs a;
@@ -298,7 +302,10 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
     {
         int32_t most = 0;
         for (size_t i = 0; i + 1 < p->mfma.eoff.size(); i++) most = std::max(most, p->mfma.eoff[i + 1] - p->mfma.eoff[i]);
-        p->mfma_slots = most <= 256 ? 1 : most <= 512 ? 2 : 4;
+        if (p->mfma_dma)  // a step's packed block also holds its 32 B row offsets
+            p->mfma_slots = most <= 256 - kDmaStepMeta ? 1 : 2;
+        else
+            p->mfma_slots = most <= 256 ? 1 : most <= 512 ? 2 : 4;
     }
     plan_rows(rowptr, M, N, static_cast<int32_t>(dtype_size(dtype)), p->mfma.row_mfma, default_slices(K, N, dtype),
               &p->rows);
@@ -330,8 +337,9 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
         if ((st = dev_upload(&p->d_ucols, uoff.data(), uoff.size()))) return bail(st);
         if ((st = dev_upload(&p->d_eoff, p->mfma.eoff.data(), p->mfma.eoff.size()))) return bail(st);
         // Packed entries.  Register-staged kernel: walk order, then one
-        // kNoEntry sentinel.  LDS-DMA kernel: step g at g * 256 * slots, its
-        // unused words kNoEntry, then 16 zero bytes (padding B source).
+        // kNoEntry sentinel.  LDS-DMA kernel: step g's block at g * 256 * slots
+        // words, its entries first (unused words kNoEntry) and its 32 B row
+        // byte offsets last; after the blocks 16 zero bytes (padding B source).
         const size_t ne = p->mfma.entries.size();
         const size_t nsteps_all = p->mfma.eoff.size() - 1;
         const size_t ewords = 256u * static_cast<size_t>(p->mfma_slots);
@@ -340,7 +348,12 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
         std::vector<int> dst(ne);
         std::vector<uint16_t> cell(ne);
         std::vector<uint32_t> packed(npacked, kNoEntry);
-        if (p->mfma_dma) std::fill(packed.end() - 4, packed.end(), 0u);
+        if (p->mfma_dma) {
+            std::fill(packed.end() - 4, packed.end(), 0u);
+            for (size_t g = 0; g < nsteps_all; g++)
+                std::copy(uoff.begin() + g * kStepK, uoff.begin() + (g + 1) * kStepK,
+                          packed.begin() + (g + 1) * ewords - kDmaStepMeta);
+        }
         std::vector<int4> segs;
         const int row_mask = 127, k_shift = 7, idx_shift = 12;
         for (size_t w = 0, e = 0, base = 0; w < p->mfma.windows.size(); w++) {
