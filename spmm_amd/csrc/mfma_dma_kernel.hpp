@@ -1,5 +1,5 @@
 // mfma_dma_kernel.hpp -- condensed-tile SpMM on gfx950 matrix cores, K-split
-// across the consumer wavefronts, operands staged by global -> LDS transfers.
+// across the consumer wavefronts, B tiles staged by global -> LDS transfers.
 //
 // A workgroup owns a 128-row window of A and a 64-column block of C and
 // walks the window's steps (32 condensed columns of A = 32 gathered rows of
@@ -7,37 +7,37 @@
 // 64 x 128 tiles of mfma_tile_kernel (mfma_kernel.hpp): the column union of
 // 128 rows is barely larger than that of 64 rows on the matrices this path
 // serves, so each gathered B row feeds twice the rows.
-//   * consumer wavefront w (one per SIMD) takes step 4 i + w of iteration i:
-//     8 row blocks x 4 column blocks = 32 v_mfma_f32_16x16x32 into 128
-//     accumulators, nothing else (VALU or LDS instructions placed between a
-//     wavefront's back-to-back MFMAs wait for the MFMA in flight).  Each
-//     step's A and B tiles are read from LDS by one wavefront only; the four
-//     partial 128 x 64 tiles are added through LDS once at the end;
-//   * producer wavefront p issues global_load_lds_dwordx4 transfers (lane L
-//     of one instruction writes 16 bytes at M0 + 16 L): the packed block of
-//     step 4 i + p (its entries and, in the last 32 words, the byte offsets
-//     of the step's 32 B rows) and its share (8 rows) of every step's B
-//     tile.  The B row offsets of a step are read from its packed block in
-//     LDS, one ds_read_b32 per lane and step, so a producer issues no other
-//     memory operation and builds each address with a few VALU operations.
-//     It also builds the A tile of step 4 i + p from the entries it
-//     transferred itself (each lane reads back its own 16 bytes, so its own
-//     vmcnt wait is the only synchronisation) into that consumer's
-//     double-buffered A slot.  Each iteration issues the same transfers in
-//     the same order, and one s_waitcnt vmcnt(N) retires exactly what is due.
-// Pipeline, iteration i (one barrier each), lookahead LB = 3 (one entry slot
-// per thread) or 2 (two), LE = LB + 2:
-//   producers: issue blocks(i + LE), then B(i + LB) (row offsets from
-//              blocks(i + LB)); build A(i + 1) from blocks(i + 1); wait
-//              until blocks(i + LE - 1) and B(i + 1) have landed
-//   consumers: MFMAs of step 4 i + w with A(i) and B(i)
-// Rings: B LB + 1 slots, blocks LE slots, A 2 slots per step of an iteration.
-// The packed block of global step g sits at g * 256 * kSlots words: up to
-// 256 * kSlots - 32 entries (unused words kNoEntry), then the 32 B row
-// offsets (kNoEntry for padding columns).
-// Every transfer address is in bounds: padding columns, steps past the
-// window and columns past N read 16 zero bytes (MfmaArgs::zeros), which also
-// stand for the entries of steps past the window (cell 0, value 0).
+//
+// Roles (8 wavefronts, one consumer and one producer per SIMD):
+//   * consumer wavefront w takes step 4 i + w of iteration i.  It loads the
+//     packed entries of its next step with ordinary global loads one
+//     iteration ahead, scatters them into its private, double-buffered A
+//     tile (before its MFMAs: VALU or LDS instructions placed between a
+//     wavefront's back-to-back MFMAs wait for the MFMA in flight), reads its
+//     A and B fragments and runs 8 row blocks x 4 column blocks = 32
+//     v_mfma_f32_16x16x32 into 128 accumulators.  The four partial
+//     128 x 64 tiles are added through LDS once at the end;
+//   * producer wavefront p issues only global_load_lds_dwordx4 transfers (lane
+//     L of one instruction writes 16 bytes at M0 + 16 L): rows 8 p .. 8 p + 7
+//     of every step's B tile.  It executes no LDS instruction at all: an LDS
+//     instruction of a wavefront waits until that wavefront's earlier LDS
+//     transfers have landed (measured on the MI355X: ~360 cycles with 8 in
+//     flight against ~60 without, and no wait behind another wavefront's
+//     transfers), which would put the gather latency on the critical path.
+//     Its B row offsets come through scalar loads issued after the transfers
+//     that use the previous ones, and each iteration issues the same four
+//     transfers, so one s_waitcnt vmcnt(N) retires exactly what is due.
+// Pipeline, iteration i (one barrier each), lookahead LB = 3:
+//   producers: issue B(i + 3); load the row offsets of B(i + 4); wait until
+//              B(i + 1) has landed (B(i + 2), B(i + 3) stay in flight)
+//   consumers: load the entries of A(i + 2); read A(i), B(i) fragments;
+//              build A(i + 1) from the entries loaded in iteration i - 1;
+//              MFMAs of step 4 i + w
+// Rings: B 4 slots, A 2 slots per step of an iteration.
+// The packed block of global step g sits at g * 256 * kSlots words (unused
+// words kNoEntry).  Every transfer address is in bounds: padding columns,
+// steps past the window and columns past N read 16 zero bytes
+// (MfmaArgs::zeros).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -53,33 +53,25 @@ constexpr int kDmaTileCols = 64;  // columns of C per workgroup
 constexpr int kDmaBRow = kDmaTileCols;           // halves per B-tile row in LDS (128 bytes)
 constexpr int kDmaATile = kDmaWinRows * kStepK;  // halves of one A tile (fragment order)
 constexpr int kDmaAElems = kDmaATile + 64;       // A tile + one dummy cell per lane
-constexpr int kDmaStepMeta = kStepK;             // B row offsets at the end of a step's packed block
-
-// Pipeline shape by entry slots (256 words each) per step.
-template <int kSlots>
-struct MfmaDmaShape {
-    static constexpr int kLB = kSlots == 1 ? 3 : 2;  // B lookahead (iterations)
-    static constexpr int kLE = kLB + 2;              // packed-block lookahead
-    static constexpr int kNB = kLB + 1;              // B ring slots
-    static constexpr int kNE = kLE;                  // packed-block ring slots
-    static constexpr int kNA = 2;                    // A slots per step of an iteration
-    static constexpr int kEWords = 256 * kSlots;     // words of a step's packed block
-};
-// Nonzeros a step may hold under the LDS-DMA kernel (two slots).
-constexpr int kDmaMaxStepEntries = 2 * 256 - kDmaStepMeta;
+constexpr int kDmaLB = 3;                        // B lookahead (iterations)
+constexpr int kDmaNB = kDmaLB + 1;               // B ring slots
+constexpr int kDmaNA = 2;                        // A slots per step of an iteration
+// Transfers a producer issues per iteration (one per step) and its wait
+// count: B(i + 1) must land in iteration i while B(i + 2), B(i + 3) may not.
+constexpr int kDmaOps = kDmaSteps;
+constexpr int kDmaWait = (kDmaLB - 1) * kDmaOps;
+// Nonzeros a step may hold under the LDS-DMA kernel (two 256-word slots).
+constexpr int kDmaMaxStepEntries = 2 * 256;
 
 // XOR permutation of the 16-byte pieces of a 128-byte B-tile row: with it the
 // ds_read_b64_tr_b16 fragment reads (two passes of 32 lanes, 8 rows x 32
 // bytes each) touch every LDS bank once.
 __host__ __device__ constexpr int bswz64(int r) { return 2 * (((r >> 1) & 1) | ((r >> 2) & 2)); }
 
-template <int kSlots>
 constexpr int mfma_dma_lds_bytes() {
-    using SH = MfmaDmaShape<kSlots>;
-    constexpr int main = SH::kNB * kDmaSteps * kStepK * kDmaBRow * 2 + SH::kNE * kDmaSteps * SH::kEWords * 4 +
-                         kDmaSteps * SH::kNA * kDmaAElems * 2;
+    constexpr int main = kDmaNB * kDmaSteps * kStepK * kDmaBRow * 2 + kDmaSteps * kDmaNA * kDmaAElems * 2;
     constexpr int red = kDmaSteps * 32 * 64 * 16;  // four partial 128 x 64 fp32 tiles
-    static_assert(main <= 160 * 1024, "LDS budget");
+    static_assert(main <= 160 * 1024 && red <= 160 * 1024, "LDS budget");
     return main > red ? main : red;
 }
 
@@ -103,24 +95,13 @@ __device__ __forceinline__ uint32_t lds_addr(P* p) {
 template <bool kBf16, int kSlots>
 __global__ __launch_bounds__(kMfmaThreads) void mfma_dma_kernel(MfmaArgs a) {
     static_assert(kSlots == 1 || kSlots == 2, "entry slots per step (x 256)");
-    using SH = MfmaDmaShape<kSlots>;
-    constexpr int KS = kDmaSteps, NB = SH::kNB, NE = SH::kNE, NA = SH::kNA, LB = SH::kLB, LE = SH::kLE;
+    constexpr int KS = kDmaSteps, NB = kDmaNB, NA = kDmaNA, LB = kDmaLB;
     constexpr int kBElems = kStepK * kDmaBRow;  // halves per B tile (4 KiB)
-    constexpr int kEWords = SH::kEWords;        // words of a step's packed block
-    constexpr int kMetaAt = kEWords - kDmaStepMeta;
+    constexpr int kEWords = 256 * kSlots;       // words of a step's packed block
     constexpr int kBBytes = NB * KS * kBElems * 2;
-    constexpr int kEBytes = NE * KS * kEWords * 4;
-    // Transfers per producer wavefront and iteration: kSlots for one packed
-    // block, then one B instruction per step.  The wait of iteration i must
-    // retire the block issued in iteration i - 1 and B(i + 1): with LB = 3 the
-    // B instructions of iteration i - 1 may stay in flight, with LB = 2 they
-    // are B(i + 1) themselves.
-    constexpr int kOps = kSlots + KS;
-    constexpr int kWait = LB == 3 ? KS + kOps : kOps;
-    __shared__ __attribute__((aligned(16))) char smem[mfma_dma_lds_bytes<kSlots>()];
-    auto Bs = reinterpret_cast<uint16_t(*)[KS][kBElems]>(smem);                         // [NB][KS][kBElems]
-    auto Es = reinterpret_cast<uint32_t(*)[KS][kEWords]>(smem + kBBytes);                // [NE][KS][kEWords]
-    auto As = reinterpret_cast<uint16_t(*)[NA][kDmaAElems]>(smem + kBBytes + kEBytes);  // [KS][NA][..]
+    __shared__ __attribute__((aligned(16))) char smem[mfma_dma_lds_bytes()];
+    auto Bs = reinterpret_cast<uint16_t(*)[KS][kBElems]>(smem);                // [NB][KS][kBElems]
+    auto As = reinterpret_cast<uint16_t(*)[NA][kDmaAElems]>(smem + kBBytes);  // [KS][NA][..]
 
     const int t = threadIdx.x;
     const int wv = __builtin_amdgcn_readfirstlane(t >> 6);  // wavefront (uniform)
@@ -149,10 +130,33 @@ __global__ __launch_bounds__(kMfmaThreads) void mfma_dma_kernel(MfmaArgs a) {
         const int br = 8 * lh + (li >> 2);
         const int bx = bswz64(br), bh = (li & 3) >> 1;
         const int b_row = br * kDmaBRow + 4 * (li & 1);
-        int bslot = 0;  // B ring slot of iteration i
-        for (int i = -LE; i < niters; i++) {
-            if (i >= 0 && KS * i + w < nsteps) {
-                i32x4v af[8], bq[4];
+        const int pad = kDmaATile + lane;
+        int pos_prev[4 * kSlots], pos_cur[4 * kSlots];
+#pragma unroll
+        for (int k = 0; k < 4 * kSlots; k++) pos_prev[k] = pos_cur[k] = pad;
+        // packed entries of step 4 n + w; the load always reads a step of the
+        // window and `valid` says whether they count (the select happens where
+        // they are used, so the load is not waited for earlier).  Lane reads
+        // words 4 lane .. 4 lane + 3 of each 256.
+        auto load_entries = [&](int n, i32x4v* e4, bool& valid) {
+            const int j = KS * n + w;
+            valid = j >= 0 && j < nsteps;
+            const int jc = valid ? j : 0;
+            const i32x4v* ep =
+                reinterpret_cast<const i32x4v*>(a.packed + static_cast<size_t>(sbase + jc) * kEWords) + lane;
+#pragma unroll
+            for (int k = 0; k < kSlots; k++) e4[k] = ep[64 * k];
+        };
+        int bslot = 0;  // B ring slot of iteration i: B(n) sits in slot n % NB
+        // One iteration; `cur` holds the entries of A(i + 1) (loaded in
+        // iteration i - 1), `nxt` receives those of A(i + 2).  The loop below
+        // alternates the two buffers instead of copying, so the compiler waits
+        // for a load only where its data is used.
+        auto iteration = [&](const int i, const i32x4v* cur, bool cur_valid, i32x4v* nxt, bool& nxt_valid) {
+            load_entries(i + 2, nxt, nxt_valid);
+            const bool active = i >= 0 && KS * i + w < nsteps;
+            i32x4v af[8], bq[4];
+            if (active) {
                 const uint16_t* Ab = &As[w][i & 1][8 * lane];
                 const uint16_t* Bb = &Bs[bslot][w][b_row];
 #pragma unroll
@@ -167,6 +171,24 @@ __global__ __launch_bounds__(kMfmaThreads) void mfma_dma_kernel(MfmaArgs a) {
                                    __builtin_bit_cast(int, __builtin_shufflevector(hi, hi, 0, 1)),
                                    __builtin_bit_cast(int, __builtin_shufflevector(hi, hi, 2, 3))};
                 }
+            }
+            if (i + 1 >= 0) {
+                // A(i + 1) into slot (i + 1) & 1 after A(i - 1)'s cells there are cleared
+                uint16_t* Aw = &As[w][(i + 1) & 1][0];
+#pragma unroll
+                for (int k = 0; k < 4 * kSlots; k++) Aw[pos_prev[k]] = 0;
+#pragma unroll
+                for (int k = 0; k < 4 * kSlots; k++) {
+                    const uint32_t e = cur_valid ? static_cast<uint32_t>(cur[k / 4][k % 4]) : kNoEntry;
+                    const bool ok = e != kNoEntry;
+                    const int pos = ok ? static_cast<int>(e & 0xffffu) : pad;
+                    Aw[pos] = ok ? static_cast<uint16_t>(e >> 16) : uint16_t(0);
+                    pos_prev[k] = pos_cur[k];
+                    pos_cur[k] = pos;
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            if (active) {
 #pragma unroll
                 for (int c = 0; c < 4; c++)
 #pragma unroll
@@ -181,15 +203,23 @@ __global__ __launch_bounds__(kMfmaThreads) void mfma_dma_kernel(MfmaArgs a) {
             }
             __syncthreads();
             if (i >= 0) bslot = bslot == NB - 1 ? 0 : bslot + 1;
+        };
+        i32x4v ent0[kSlots], ent1[kSlots];
+        bool val0, val1;
+        load_entries(1 - LB, ent0, val0);  // entries of A(i + 1) for the first iteration i = -LB
+        int i = -LB;
+        for (; i + 1 < niters; i += 2) {
+            iteration(i, ent0, val0, ent1, val1);
+            iteration(i + 1, ent1, val1, ent0, val0);
         }
+        if (i < niters) iteration(i, ent0, val0, ent1, val1);
     } else {
-        // ================= producer: transfers only =================
+        // ================= producer: B transfers only =================
         const int pw = wv - KS;
         const char* Bg = static_cast<const char*>(a.B);
         const char* Zg = static_cast<const char*>(a.zeros);
-        // B transfer role: rows 8 pw .. 8 pw + 7 of every step; this lane fills
-        // row 8 pw + lane / 8, physical piece lane % 8 (logical piece
-        // (lane % 8) ^ bswz64(row)).
+        // This lane fills row 8 pw + lane / 8 of every step's B tile, physical
+        // piece lane % 8 (logical piece (lane % 8) ^ bswz64(row)).
         const int g8 = lane >> 3;
         int bcol;
         {
@@ -197,71 +227,48 @@ __global__ __launch_bounds__(kMfmaThreads) void mfma_dma_kernel(MfmaArgs a) {
             const int col = c0 + 8 * ((lane & 7) ^ bswz64(row));
             bcol = col < a.N ? col * 2 : -1;
         }
-        const int pad = kDmaATile + lane;
-        int pos_prev[4 * kSlots], pos_cur[4 * kSlots];
+        // B row offsets of rows 8 pw .. 8 pw + 7 for the steps of B(ib), by
+        // scalar loads (constant address space: uniform loads from it are
+        // scalar loads, which keeps vmcnt counting the transfers alone).
+        typedef __attribute__((address_space(4))) const uint32_t* cu32p;
+        const cu32p ucols_c = (cu32p)(a.ucols);
+        uint32_t mu[KS][8];
+        auto load_meta = [&](int ib) {
 #pragma unroll
-        for (int k = 0; k < 4 * kSlots; k++) pos_prev[k] = pos_cur[k] = pad;
-        // B(n) sits in ring slot n mod NB.  Every iteration issues the same
-        // transfers, the first ones B(-2), B(-1) from the zero bytes, so that
-        // one wait count holds from the first iteration on.
-        int bslot = NB - 2;
-        int eslot = 0;             // block ring slot of blocks(i + LE): blocks(n) sit in slot n % NE
-        for (int i = -LE; i < niters; i++) {
-            {
-                // packed block of step 4 (i + LE) + p (issued first: see the wait below)
-                const int j = KS * (i + LE) + pw;
-                const uint32_t* ep = a.packed + static_cast<size_t>(sbase + j) * kEWords + 4 * lane;
+            for (int sp = 0; sp < KS; sp++) {
+                const int j = min(max(KS * ib + sp, 0), nsteps - 1);
+                const cu32p up = ucols_c + static_cast<size_t>(sbase + j) * kStepK + 8 * pw;
 #pragma unroll
-                for (int k = 0; k < kSlots; k++)
-                    dma_x4(j < nsteps ? static_cast<const void*>(ep + 256 * k) : static_cast<const void*>(Zg),
-                           lds_addr(&Es[eslot][pw][256 * k]));
+                for (int r = 0; r < 8; r++) mu[sp][r] = up[r];
             }
-            {
-                // rows 8 p .. 8 p + 7 of B(i + LB); row offsets from blocks(i + LB),
-                // which landed by every producer's wait of iteration i - 1
-                const bool real = i + LB >= 0;
-                const int em = eslot >= LE - LB ? eslot - (LE - LB) : eslot + LB;  // (i + LB) % NE
-                uint32_t uo[KS];
+        };
+        int bslot = 0;  // ring slot of B(i + LB): B(n) sits in slot n % NB
+        load_meta(0);
+        for (int i = -LB; i < niters; i++) {
 #pragma unroll
-                for (int sp = 0; sp < KS; sp++) uo[sp] = real ? Es[em][sp][kMetaAt + 8 * pw + g8] : kNoEntry;
+            for (int sp = 0; sp < KS; sp++) {
+                // rows 8 pw .. 8 pw + 7 of B(i + LB), step sp
+                const bool in = KS * (i + LB) + sp < nsteps;
+                // this lane's row offset: a select tree over the step's eight
+                // values (held as values, so the selects stay v_cndmask
+                // instead of an indexed private array)
+                uint32_t m[8];
 #pragma unroll
-                for (int sp = 0; sp < KS; sp++) {
-                    const bool in = real && KS * (i + LB) + sp < nsteps;
-                    const char* src = (in && uo[sp] != kNoEntry && bcol >= 0) ? Bg + uo[sp] + bcol : Zg;
-                    dma_x4(src, lds_addr(&Bs[bslot][sp][kDmaBRow * 8 * pw]));
-                }
-                bslot = bslot == NB - 1 ? 0 : bslot + 1;
+                for (int r = 0; r < 8; r++) m[r] = __builtin_amdgcn_readfirstlane(mu[sp][r]);
+                const uint32_t u01 = (g8 & 1) ? m[1] : m[0], u23 = (g8 & 1) ? m[3] : m[2];
+                const uint32_t u45 = (g8 & 1) ? m[5] : m[4], u67 = (g8 & 1) ? m[7] : m[6];
+                const uint32_t u03 = (g8 & 2) ? u23 : u01, u47 = (g8 & 2) ? u67 : u45;
+                const uint32_t uo = (g8 & 4) ? u47 : u03;
+                const char* src = (in && uo != kNoEntry && bcol >= 0) ? Bg + uo + bcol : Zg;
+                dma_x4(src, lds_addr(&Bs[bslot][sp][kDmaBRow * 8 * pw]));
             }
-            if (i + 1 >= 0) {
-                // A(i + 1) of step 4 (i + 1) + p into consumer p's slot (i + 1) & 1,
-                // after clearing A(i - 1)'s cells there.  Every lane reads back
-                // the 16 bytes it transferred; the block's last 32 words (lanes
-                // 56..63 of its last 256) are the B row offsets, not entries.
-                const int er = eslot + 1 - (eslot + 1 >= NE ? NE : 0);  // (i + 1) % NE
-                uint32_t ent[4 * kSlots];
-#pragma unroll
-                for (int k = 0; k < kSlots; k++) {
-                    const i32x4v e4 = *reinterpret_cast<const i32x4v*>(&Es[er][pw][256 * k + 4 * lane]);
-                    const bool meta = k == kSlots - 1 && lane >= 56;
-#pragma unroll
-                    for (int q = 0; q < 4; q++) ent[4 * k + q] = meta ? kNoEntry : static_cast<uint32_t>(e4[q]);
-                }
-                uint16_t* Aw = &As[pw][(i + 1) & 1][0];
-#pragma unroll
-                for (int k = 0; k < 4 * kSlots; k++) Aw[pos_prev[k]] = 0;
-#pragma unroll
-                for (int k = 0; k < 4 * kSlots; k++) {
-                    const uint32_t e = ent[k];
-                    const bool ok = e != kNoEntry;
-                    const int pos = ok ? static_cast<int>(e & 0xffffu) : pad;
-                    Aw[pos] = ok ? static_cast<uint16_t>(e >> 16) : uint16_t(0);
-                    pos_prev[k] = pos_cur[k];
-                    pos_cur[k] = pos;
-                }
-            }
-            wait_vmcnt<kWait>();
-            __syncthreads();
-            eslot = eslot == NE - 1 ? 0 : eslot + 1;
+            bslot = bslot == NB - 1 ? 0 : bslot + 1;
+            // next iteration's row offsets (after the transfers that used these)
+            load_meta(i + LB + 1);
+            wait_vmcnt<kDmaWait>();  // B(i + 1) has landed
+            // A plain barrier: this wavefront has no LDS instruction to order,
+            // and waiting for its scalar loads here would stall the barrier.
+            __builtin_amdgcn_s_barrier();
         }
         wait_vmcnt<0>();
     }

@@ -77,12 +77,11 @@ struct MfmaShape {
     int32_t fill_iters;        // pipeline fill, in iterations
 };
 // Register-staged kernel: 64 x 128 tiles, up to 1024 nonzeros per step, a
-// 4-step iteration ~0.95 us.  LDS-DMA kernel: 128 x 64 tiles, up to 480
-// (two 256-word slots less the step's 32 B row offsets).
+// 4-step iteration ~0.95 us.  LDS-DMA kernel: 128 x 64 tiles, up to 512.
 constexpr MfmaShape kMfmaRegsShape = {64, 128, 1024, 3.0, 0.95, 4};
-constexpr MfmaShape kMfmaDmaShape = {128, 64, 480, 3.0, 0.95, 5};
+constexpr MfmaShape kMfmaDmaShape = {128, 64, 512, 3.0, 0.95, 3};
 inline const MfmaShape& mfma_shape(uint32_t flags) {
-    return (flags & TCA_PLAN_MFMA_DMA) ? kMfmaDmaShape : kMfmaRegsShape;
+    return (flags & TCA_PLAN_MFMA_REGS) ? kMfmaRegsShape : kMfmaDmaShape;
 }
 
 struct MfmaPlan {

@@ -297,15 +297,12 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
     const MfmaShape& shape = mfma_shape(flags);
     plan_mfma(rowptr, colidx, M, N, dtype, (flags & TCA_PLAN_FORCE_MFMA) != 0, (flags & TCA_PLAN_NO_MFMA) != 0,
               md ? std::atof(md) : kMfmaMinDensity, shape, &p->mfma);
-    p->mfma_dma = (flags & TCA_PLAN_MFMA_DMA) != 0;
+    p->mfma_dma = (flags & TCA_PLAN_MFMA_REGS) == 0;
     p->mfma_col_blocks = (N + shape.tile_cols - 1) / shape.tile_cols;
     {
         int32_t most = 0;
         for (size_t i = 0; i + 1 < p->mfma.eoff.size(); i++) most = std::max(most, p->mfma.eoff[i + 1] - p->mfma.eoff[i]);
-        if (p->mfma_dma)  // a step's packed block also holds its 32 B row offsets
-            p->mfma_slots = most <= 256 - kDmaStepMeta ? 1 : 2;
-        else
-            p->mfma_slots = most <= 256 ? 1 : most <= 512 ? 2 : 4;
+        p->mfma_slots = most <= 256 ? 1 : most <= 512 ? 2 : 4;
     }
     plan_rows(rowptr, M, N, static_cast<int32_t>(dtype_size(dtype)), p->mfma.row_mfma, default_slices(K, N, dtype),
               &p->rows);
@@ -338,8 +335,8 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
         if ((st = dev_upload(&p->d_eoff, p->mfma.eoff.data(), p->mfma.eoff.size()))) return bail(st);
         // Packed entries.  Register-staged kernel: walk order, then one
         // kNoEntry sentinel.  LDS-DMA kernel: step g's block at g * 256 * slots
-        // words, its entries first (unused words kNoEntry) and its 32 B row
-        // byte offsets last; after the blocks 16 zero bytes (padding B source).
+        // words (unused words kNoEntry); after the blocks 16 zero bytes
+        // (padding B source).
         const size_t ne = p->mfma.entries.size();
         const size_t nsteps_all = p->mfma.eoff.size() - 1;
         const size_t ewords = 256u * static_cast<size_t>(p->mfma_slots);
@@ -348,12 +345,7 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
         std::vector<int> dst(ne);
         std::vector<uint16_t> cell(ne);
         std::vector<uint32_t> packed(npacked, kNoEntry);
-        if (p->mfma_dma) {
-            std::fill(packed.end() - 4, packed.end(), 0u);
-            for (size_t g = 0; g < nsteps_all; g++)
-                std::copy(uoff.begin() + g * kStepK, uoff.begin() + (g + 1) * kStepK,
-                          packed.begin() + (g + 1) * ewords - kDmaStepMeta);
-        }
+        if (p->mfma_dma) std::fill(packed.end() - 4, packed.end(), 0u);
         std::vector<int4> segs;
         const int row_mask = 127, k_shift = 7, idx_shift = 12;
         for (size_t w = 0, e = 0, base = 0; w < p->mfma.windows.size(); w++) {
@@ -409,7 +401,7 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
     in.mfma_blocks = in.n_windows_mfma * p->mfma_col_blocks;
     in.mfma_blockdim = kMfmaThreads;
     if (p->mfma_dma && p->mfma_slots <= 2)
-        in.mfma_lds_bytes = p->mfma_slots == 1 ? mfma_dma_lds_bytes<1>() : mfma_dma_lds_bytes<2>();
+        in.mfma_lds_bytes = mfma_dma_lds_bytes();
     else
         in.mfma_lds_bytes = p->mfma_slots == 1 ? mfma_lds_bytes<1>() : p->mfma_slots == 2 ? mfma_lds_bytes<2>() : mfma_lds_bytes<4>();
     in.scratch_bytes = static_cast<int64_t>(n_seg_total * N * sizeof(float));

@@ -137,7 +137,7 @@ def test_exact_bit_equal_all_widths(torch_cuda, dtype):
         assert np.array_equal(got, want), (dtype, n, np.abs(got - want).max())
 
 
-@pytest.mark.parametrize("variant", [0, S.TCA_PLAN_MFMA_DMA], ids=["regs", "dma"])
+@pytest.mark.parametrize("variant", [S.TCA_PLAN_MFMA_REGS, 0], ids=["regs", "dma"])
 @pytest.mark.parametrize("dtype", [S.TCA_F16, S.TCA_BF16])
 def test_mfma_exact_bit_equal(torch_cuda, dtype, variant):
     """Condensed-tile MFMA path (forced on every eligible window) is bit-equal
@@ -160,7 +160,7 @@ def test_mfma_exact_bit_equal(torch_cuda, dtype, variant):
             with S.Plan(a, n, S.TCA_PLAN_FORCE_MFMA | variant) as pl:
                 info = pl.info()
                 got = run_gpu(torch_cuda, a, b, plan=pl)
-            assert info["n_windows_mfma"] > 0 or (variant and (m, k, p) in dense), (m, k, n)
+            assert info["n_windows_mfma"] > 0 or (variant == 0 and (m, k, p) in dense), (m, k, n)
             want = oracle_c(a, b)
             assert np.array_equal(got, want), (m, k, p, n, np.abs(got - want).max())
 
@@ -306,7 +306,7 @@ def test_phase_timing_reports_the_kernels_a_plan_uses(torch_cuda):
     ones are positive, and the run afterwards is still exact."""
     torch = torch_cuda
     rng = np.random.default_rng(97)
-    a, _ = S.gen_bernoulli(256, 512, 0.2, seed=9, dtype=S.TCA_F16)
+    a, _ = S.gen_bernoulli(256, 512, 0.08, seed=9, dtype=S.TCA_F16)
     a = S.CSR(a.nrow, a.ncol, a.rowptr, a.colidx, S.to_storage(exact_values(rng, a.nnz), S.TCA_F16), S.TCA_F16)
     b = S.to_storage(exact_dense(rng, (512, 256)), S.TCA_F16)
     dev = torch.device("cuda:0")

@@ -233,11 +233,11 @@ def test_condense_windows_bit_exact_with_oracle(m, k, p, win):
     assert np.array_equal(uoff, ou) and np.array_equal(ucols, oc) and np.array_equal(cpos, op)
 
 
-@pytest.mark.parametrize("m,k,n,p,flags", [(200, 700, 128, 0.06, S.TCA_PLAN_FORCE_MFMA),
-                                           (130, 300, 64, 0.02, S.TCA_PLAN_FORCE_MFMA),
-                                           (64, 2048, 256, 0.3, S.TCA_PLAN_FORCE_MFMA),
-                                           (300, 700, 128, 0.06, S.TCA_PLAN_FORCE_MFMA | S.TCA_PLAN_MFMA_DMA),
-                                           (129, 1500, 64, 0.1, S.TCA_PLAN_FORCE_MFMA | S.TCA_PLAN_MFMA_DMA)])
+@pytest.mark.parametrize("m,k,n,p,flags", [(200, 700, 128, 0.06, S.TCA_PLAN_FORCE_MFMA | S.TCA_PLAN_MFMA_REGS),
+                                           (130, 300, 64, 0.02, S.TCA_PLAN_FORCE_MFMA | S.TCA_PLAN_MFMA_REGS),
+                                           (64, 2048, 256, 0.3, S.TCA_PLAN_FORCE_MFMA | S.TCA_PLAN_MFMA_REGS),
+                                           (300, 700, 128, 0.06, S.TCA_PLAN_FORCE_MFMA),
+                                           (129, 1500, 64, 0.1, S.TCA_PLAN_FORCE_MFMA)])
 def test_mfma_window_plan_decodes_to_the_csr(m, k, n, p, flags):
     """Every MFMA window's steps, B-row lists and entries reproduce the CSR
     exactly, with the oracle's condensed positions (64-row windows for the
@@ -245,7 +245,7 @@ def test_mfma_window_plan_decodes_to_the_csr(m, k, n, p, flags):
     a, _ = S.gen_bernoulli(m, k, p, seed=7, dtype=S.TCA_F16)
     windows, ucols, eoff, entries = S.plan_mfma_windows(a, n, flags=flags)
     assert len(windows) > 0
-    win = 128 if flags & S.TCA_PLAN_MFMA_DMA else 64
+    win = 64 if flags & S.TCA_PLAN_MFMA_REGS else 128
     uo, uc, cp = oracle.condense_windows(a.rowptr, a.colidx, m, win)
     for row0, steps, gstep, nz0 in windows:
         w = row0 // win
@@ -270,20 +270,24 @@ def test_mfma_window_plan_decodes_to_the_csr(m, k, n, p, flags):
     assert len(S.plan_mfma_windows(a, 100, flags=S.TCA_PLAN_FORCE_MFMA)[0]) == 0  # N % 8 != 0
 
 
-def test_mfma_default_routing_follows_the_cost_model():
-    """Default routing: the lognormal 4096 x 4096 layer (config 1) goes to the
-    tile kernel, the small 2048 x 512 Bernoulli layer (config 0) stays on the
-    row kernel (too few steps and workgroups to amortise the pipeline fill),
-    and a very sparse matrix (density below 0.04) stays on the row kernel."""
+@pytest.mark.parametrize("kernel", [0, S.TCA_PLAN_MFMA_REGS], ids=["dma", "regs"])
+def test_mfma_default_routing_follows_the_cost_model(kernel):
+    """Default routing, for both tile kernels: the lognormal 4096 x 4096 layer
+    (config 1) goes to the tile kernel, the small 2048 x 512 Bernoulli layer
+    (config 0) stays on the row kernel (too few steps and workgroups to
+    amortise the pipeline fill), and a very sparse matrix (density below
+    0.04) stays on the row kernel."""
+    win = 64 if kernel else 128
     a1, n1, _ = S.gen_config(1, seed=1)
-    w1 = S.plan_mfma_windows(a1, n1)[0]
-    assert len(w1) == (a1.nrow + 63) // 64
+    w1 = S.plan_mfma_windows(a1, n1, flags=kernel)[0]
+    assert len(w1) == (a1.nrow + win - 1) // win
     a0, n0, _ = S.gen_config(0, seed=1)
-    assert len(S.plan_mfma_windows(a0, n0)[0]) == 0
+    assert len(S.plan_mfma_windows(a0, n0, flags=kernel)[0]) == 0
     sparse, _ = S.gen_lognormal_rows(4096, 4096, 50, seed=5)
-    assert len(S.plan_mfma_windows(sparse, 512)[0]) == 0
+    assert len(S.plan_mfma_windows(sparse, 512, flags=kernel)[0]) == 0
     # the density floor is overridable for tuning, the cost model still applies
-    assert len(S.plan_mfma_windows(a0, n0, flags=S.TCA_PLAN_FORCE_MFMA)[0]) == (a0.nrow + 63) // 64
+    forced = S.plan_mfma_windows(a0, n0, flags=S.TCA_PLAN_FORCE_MFMA | kernel)[0]
+    assert len(forced) == (a0.nrow + win - 1) // win
 
 
 @pytest.mark.parametrize("m,k,p", [(50, 70, 0.1), (1, 1, 1.0), (300, 20, 0.3), (20, 300, 0.05), (5, 5, 0.0)])
