@@ -28,17 +28,18 @@ WORKLOADS = {
 
 
 # Dominant kernel of each phase (tca_spmm_time_phases order).
-PHASE_KERNELS = {"pack": "mfma_pack_kernel", "tiles": "mfma_dma_kernel", "rows": "row_kernel",
+PHASE_KERNELS = {"pack": "mfma_pack_kernel", "tiles": "mfma_pair_kernel", "rows": "row_kernel",
                  "segments": "seg_finalize_kernel"}
 REGS_TILE_KERNEL = "mfma_tile_kernel"  # the "tiles" phase under plan flag TCA_PLAN_MFMA_REGS
+DMA_TILE_KERNEL = "mfma_dma_kernel"    # the "tiles" phase under plan flag TCA_PLAN_MFMA_DMA
 
 # HBM bytes per launch of the dominant kernel, measured with rocprofv3 --pmc
 # FETCH_SIZE and WRITE_SIZE (KiB per dispatch, already scaled by the copy
 # calibration: FETCH x 2.00, WRITE x 1.00), keyed by (config, phase, flags).
 # Source: the profiles/ summaries named in each entry.
 MEASURED_TRAFFIC_KIB = {
-    # profiles/mfma_dma_kernel_config1.md (LDS-DMA tile kernel, the default)
-    (1, "tiles", 0): (39252.0 * 2.0, 8319.2),
+    # profiles/mfma_dma_kernel_config1.md (LDS-DMA tile kernel)
+    (1, "tiles", 8): (39252.0 * 2.0, 8319.2),  # flags 8 = TCA_PLAN_MFMA_DMA
     # profiles/mfma_tile_kernel_config1.md (register-staged tile kernel)
     (1, "tiles", 4): (12768.8 * 2.0, 10785.3),  # flags 4 = TCA_PLAN_MFMA_REGS
 }
@@ -58,7 +59,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline time budget")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--flags", type=int, default=0,
-                    help="plan flags (1 = no MFMA, 2 = force MFMA, 4 = register-staged tile kernel)")
+                    help="plan flags (1 = no MFMA, 2 = force MFMA, 4 = register-staged tile kernel, "
+                         "8 = LDS-DMA tile kernel)")
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
                     help="before timing, run one device-to-device copy of MIB MiB (a known-size kernel to "
                          "scale rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
@@ -155,6 +157,8 @@ def main():
     kernel_name = PHASE_KERNELS[dominant]
     if dominant == "tiles" and args.flags & S.TCA_PLAN_MFMA_REGS:
         kernel_name = REGS_TILE_KERNEL
+    elif dominant == "tiles" and args.flags & S.TCA_PLAN_MFMA_DMA:
+        kernel_name = DMA_TILE_KERNEL
     traffic = int(round((kib[0] + kib[1]) * 1024)) if kib else None
     log(f"kernel avg {ms_per_step * 1e3:.2f} us/step, wall {wall_ms:.2f} ms for {args.warmup}+{args.steps} steps")
 

@@ -50,7 +50,8 @@ typedef enum tca_status {
 #define TCA_PLAN_DEFAULT 0u
 #define TCA_PLAN_NO_MFMA 1u    /* route every row to the wavefront-per-row kernel */
 #define TCA_PLAN_FORCE_MFMA 2u /* route every eligible 64-row window to the MFMA tile kernel (fp16/bf16, N % 8 == 0) */
-#define TCA_PLAN_MFMA_REGS 4u  /* register-staged 64 x 128 tile kernel instead of the default LDS-DMA 128 x 64 one */
+#define TCA_PLAN_MFMA_REGS 4u  /* register-staged 64 x 128 tile kernel instead of the default paired 128 x 64 one */
+#define TCA_PLAN_MFMA_DMA 8u   /* LDS-DMA 128 x 64 tile kernel instead of the default paired one */
 
 typedef struct tca_spmm_plan tca_spmm_plan;
 

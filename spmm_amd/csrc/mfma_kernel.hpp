@@ -98,7 +98,8 @@ struct MfmaArgs {
     int col_blocks;          // blockIdx.x = window * col_blocks + column block
     uint32_t B_bytes, packed_bytes, ucols_bytes, eoff_bytes;
     int sentinel;            // index of the kNoEntry entry, loaded for empty slots
-    const void* zeros;       // 16 zero bytes (source of padding B pieces, LDS-DMA kernel)
+    const void* zeros;       // 16 zero bytes (source of padding B pieces, LDS-DMA and paired kernels)
+    const i32x2v* emeta;     // [global step] {first word of the packed block, groups of 64 entries} (paired kernel)
 };
 
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
@@ -114,26 +115,31 @@ struct MfmaDepth {
 
 constexpr int kMfmaThreads = 512;  // 4 consumer + 4 producer wavefronts
 
-// Per run: pair each MFMA entry's A-tile cell with its value, in step order,
-// so the tile kernel loads one coalesced word per nonzero (the values are
-// read once here instead of once per column block).  The MFMA windows'
-// nonzeros are walked in CSR order: runs of consecutive windows form
-// segments {first nonzero, count, first walk index}, so every load is
-// coalesced and independent of other loads; only the stores scatter.
-__global__ __launch_bounds__(256) void mfma_pack_kernel(const int4* __restrict__ segs, int nsegs,
-                                                        const int* __restrict__ dst, const uint16_t* __restrict__ cell,
+// Per run: pair each MFMA entry's A-tile cell with its value, in the packed
+// array's word order, so the tile kernels load one coalesced word per entry
+// (the values are read once here instead of once per column block).  Word x
+// gets cell[x] | val[src[x]] << 16; words that hold no entry (src[x] < 0)
+// keep their plan-time content: cell[x] with value bits 0, or kNoEntry where
+// cell[x] is 0xffff.  Four words per thread: the loads of src and cell and
+// the stores are coalesced, only the value loads gather (from the CSR range
+// of one window at a time).
+__global__ __launch_bounds__(256) void mfma_pack_kernel(const int* __restrict__ src, const uint16_t* __restrict__ cell,
                                                         int n, const uint16_t* __restrict__ val,
                                                         uint32_t* __restrict__ packed) {
-    const int i = blockIdx.x * 256 + threadIdx.x;
-    if (i >= n) return;
-    int lo = 0, hi = nsegs - 1;  // last segment with first walk index <= i
-    while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (segs[mid].z <= i) lo = mid;
-        else hi = mid - 1;
+    const int x = (blockIdx.x * 256 + threadIdx.x) * 4;
+    if (x >= n) return;
+    auto word = [&](int s, uint32_t c) -> uint32_t {
+        const uint32_t hi = s >= 0 ? static_cast<uint32_t>(val[s]) : (c == 0xffffu ? 0xffffu : 0u);
+        return c | (hi << 16);
+    };
+    if (x + 4 <= n) {
+        const int4 s = *reinterpret_cast<const int4*>(src + x);
+        const uint2 c = *reinterpret_cast<const uint2*>(cell + x);
+        *reinterpret_cast<uint4*>(packed + x) = uint4{word(s.x, c.x & 0xffffu), word(s.y, c.x >> 16),
+                                                       word(s.z, c.y & 0xffffu), word(s.w, c.y >> 16)};
+    } else {
+        for (int k = x; k < n; k++) packed[k] = word(src[k], cell[k]);
     }
-    const int4 sg = segs[lo];
-    packed[dst[i]] = static_cast<uint32_t>(cell[i]) | (static_cast<uint32_t>(val[sg.x + (i - sg.z)]) << 16);
 }
 
 // Static LDS of mfma_tile_kernel<*, kSlots> in bytes.

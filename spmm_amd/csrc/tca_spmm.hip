@@ -13,6 +13,7 @@
 #include "row_kernel.hpp"
 #include "mfma_kernel.hpp"
 #include "mfma_dma_kernel.hpp"
+#include "mfma_pair_kernel.hpp"
 #include "sddmm_kernel.hpp"
 
 using namespace tca;
@@ -33,15 +34,17 @@ struct tca_spmm_plan {
     int32_t mfma_col_blocks = 0;
     int32_t mfma_slots = 1;  // entries per thread and step in the MFMA kernel (1, 2 or 4)
     bool mfma_dma = false;   // LDS-DMA tile kernel instead of the register-staged one
+    bool mfma_pair = false;  // paired (MFMA + staging wavefront) tile kernel
+    int32_t mfma_groups = 0; // paired kernel: groups of 64 entries a step may hold (4 or 8)
     size_t mfma_zeros_at = 0;  // word offset of 16 zero bytes in d_packed (LDS-DMA kernel)
     size_t n_packed = 0;       // words of d_packed
     int4* d_windows = nullptr;
     uint32_t* d_ucols = nullptr;
     int* d_eoff = nullptr;
-    int4* d_pk_seg = nullptr;       // runs of consecutive MFMA windows: {first nonzero, count, first walk index, 0}
-    int32_t n_pk_seg = 0;
-    int* d_pk_dst = nullptr;        // MFMA nonzeros in CSR order: entry (step-order) position
-    uint16_t* d_pk_cell = nullptr;  // ... its A-tile cell
+    i32x2v* d_emeta = nullptr;      // paired kernel: {first word of each step's packed block, groups of 64}
+    int32_t n_pk_words = 0;         // words of d_packed that the pack kernel writes
+    int* d_pk_src = nullptr;        // per packed word: CSR index of its nonzero, -1 for none
+    uint16_t* d_pk_cell = nullptr;  // per packed word: its cell (low 16 bits)
     uint32_t* d_packed = nullptr;   // cell | value << 16 per entry (rewritten each run) + sentinel
     int32_t ntasks = 0;
     int* d_rowptr = nullptr;
@@ -83,8 +86,8 @@ void free_plan_device(tca_spmm_plan* p) {
     (void)hipFree(p->d_windows);
     (void)hipFree(p->d_ucols);
     (void)hipFree(p->d_eoff);
-    (void)hipFree(p->d_pk_seg);
-    (void)hipFree(p->d_pk_dst);
+    (void)hipFree(p->d_emeta);
+    (void)hipFree(p->d_pk_src);
     (void)hipFree(p->d_pk_cell);
     (void)hipFree(p->d_packed);
 }
@@ -138,14 +141,15 @@ int launch_rows_e(const tca_spmm_plan* p, const void* val, const void* B, float*
 
 // Pairs the MFMA entries with this run's values (before the tile kernel).
 void launch_pack(const tca_spmm_plan* p, const void* val, hipStream_t s) {
-    const int n_ent = static_cast<int>(p->mfma.entries.size());
-    if (p->mfma.windows.empty() || n_ent == 0) return;
-    hipLaunchKernelGGL(mfma_pack_kernel, dim3((n_ent + 255) / 256), dim3(256), 0, s, p->d_pk_seg, p->n_pk_seg,
-                       p->d_pk_dst, p->d_pk_cell, n_ent, static_cast<const uint16_t*>(val), p->d_packed);
+    const int n = p->n_pk_words;
+    if (p->mfma.windows.empty() || n == 0) return;
+    hipLaunchKernelGGL(mfma_pack_kernel, dim3((n + 1023) / 1024), dim3(256), 0, s, p->d_pk_src, p->d_pk_cell, n,
+                       static_cast<const uint16_t*>(val), p->d_packed);
 }
 
 static_assert(kMfmaDmaShape.max_step_entries == kDmaMaxStepEntries, "planner and LDS-DMA kernel agree on step size");
 static_assert(kMfmaDmaShape.win_rows == kDmaWinRows && kMfmaDmaShape.tile_cols == kDmaTileCols, "LDS-DMA tile shape");
+static_assert(kMfmaDmaShape.max_step_entries <= 8 * kPairGroup, "paired kernel: at most 8 entry groups per step");
 static_assert(kMfmaRegsShape.win_rows == kWinRows && kMfmaRegsShape.tile_cols == kTileCols, "register tile shape");
 
 int launch_mfma(const tca_spmm_plan* p, const void* B, float* C, hipStream_t s) {
@@ -154,6 +158,7 @@ int launch_mfma(const tca_spmm_plan* p, const void* B, float* C, hipStream_t s) 
     a.windows = p->d_windows;
     a.ucols = p->d_ucols;
     a.eoff = p->d_eoff;
+    a.emeta = p->d_emeta;
     a.packed = p->d_packed;
     a.B = B;
     a.C = C;
@@ -170,6 +175,19 @@ int launch_mfma(const tca_spmm_plan* p, const void* B, float* C, hipStream_t s) 
     a.eoff_bytes = static_cast<uint32_t>(p->mfma.eoff.size() * 4);
     const dim3 grid(static_cast<unsigned>(p->mfma.windows.size()) * p->mfma_col_blocks);
     const bool bf = p->dtype == TCA_BF16;
+    if (p->mfma_pair) {
+        switch (p->mfma_groups) {
+            case 4:
+                if (bf) hipLaunchKernelGGL((mfma_pair_kernel<true, 4>), grid, dim3(kPairThreads), 0, s, a);
+                else hipLaunchKernelGGL((mfma_pair_kernel<false, 4>), grid, dim3(kPairThreads), 0, s, a);
+                return TCA_OK;
+            case 8:
+                if (bf) hipLaunchKernelGGL((mfma_pair_kernel<true, 8>), grid, dim3(kPairThreads), 0, s, a);
+                else hipLaunchKernelGGL((mfma_pair_kernel<false, 8>), grid, dim3(kPairThreads), 0, s, a);
+                return TCA_OK;
+            default: return fail(TCA_ERR_INVALID, "bad MFMA entry group count %d", p->mfma_groups);
+        }
+    }
     if (p->mfma_dma && p->mfma_slots <= 2) {
         switch (p->mfma_slots) {
             case 1:
@@ -291,18 +309,20 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
         return fail(TCA_ERR_HIP, "no HIP device");
     }
     // Dense-enough row windows go to an MFMA tile kernel (fp16 / bf16): 64-row
-    // windows x 128 columns (register-staged) or 128 x 64 (LDS-DMA kernel).
+    // windows x 128 columns (register-staged) or 128 x 64 (paired or LDS-DMA kernel).
     // TCA_MFMA_MIN_DENSITY (tuning only) overrides the routing threshold.
     const char* md = std::getenv("TCA_MFMA_MIN_DENSITY");
     const MfmaShape& shape = mfma_shape(flags);
     plan_mfma(rowptr, colidx, M, N, dtype, (flags & TCA_PLAN_FORCE_MFMA) != 0, (flags & TCA_PLAN_NO_MFMA) != 0,
               md ? std::atof(md) : kMfmaMinDensity, shape, &p->mfma);
-    p->mfma_dma = (flags & TCA_PLAN_MFMA_REGS) == 0;
+    p->mfma_dma = (flags & TCA_PLAN_MFMA_REGS) == 0 && (flags & TCA_PLAN_MFMA_DMA) != 0;
+    p->mfma_pair = (flags & (TCA_PLAN_MFMA_REGS | TCA_PLAN_MFMA_DMA)) == 0;
     p->mfma_col_blocks = (N + shape.tile_cols - 1) / shape.tile_cols;
     {
         int32_t most = 0;
         for (size_t i = 0; i + 1 < p->mfma.eoff.size(); i++) most = std::max(most, p->mfma.eoff[i + 1] - p->mfma.eoff[i]);
         p->mfma_slots = most <= 256 ? 1 : most <= 512 ? 2 : 4;
+        p->mfma_groups = most <= 4 * kPairGroup ? 4 : 8;
     }
     plan_rows(rowptr, M, N, static_cast<int32_t>(dtype_size(dtype)), p->mfma.row_mfma, default_slices(K, N, dtype),
               &p->rows);
@@ -327,50 +347,85 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
         // Device forms: B row byte offsets (padding 0xffffffff); per entry its
         // fragment-order A-tile cell and nonzero index (the pack kernel pairs
         // them with the run's values), and the packed array's kNoEntry sentinel.
+        // (Paired kernel: each step's 32 offsets permuted, word 4 r + k = column r + 8 k.)
         std::vector<uint32_t> uoff(p->mfma.ucols.size());
-        for (size_t i = 0; i < uoff.size(); i++)
-            uoff[i] = p->mfma.ucols[i] < 0 ? kNoEntry
-                                            : static_cast<uint32_t>(p->mfma.ucols[i]) * static_cast<uint32_t>(N) * 2u;
+        for (size_t i = 0; i < uoff.size(); i++) {
+            const size_t src = p->mfma_pair ? (i & ~size_t(31)) + ((i & 31) >> 2) + 8 * (i & 3) : i;
+            uoff[i] = p->mfma.ucols[src] < 0 ? kNoEntry
+                                              : static_cast<uint32_t>(p->mfma.ucols[src]) * static_cast<uint32_t>(N) * 2u;
+        }
         if ((st = dev_upload(&p->d_ucols, uoff.data(), uoff.size()))) return bail(st);
         if ((st = dev_upload(&p->d_eoff, p->mfma.eoff.data(), p->mfma.eoff.size()))) return bail(st);
         // Packed entries.  Register-staged kernel: walk order, then one
         // kNoEntry sentinel.  LDS-DMA kernel: step g's block at g * 256 * slots
-        // words (unused words kNoEntry); after the blocks 16 zero bytes
-        // (padding B source).
+        // words (unused words kNoEntry).  Paired kernel: step g's block at
+        // ebase[g], whole chunks of 256 words (at least one), entries placed
+        // by pair_entry_word, unused words the dummy cell of the lane that
+        // loads them, with value 0.  Both tile kernels find 16 zero bytes
+        // (padding B source) after the blocks.
         const size_t ne = p->mfma.entries.size();
         const size_t nsteps_all = p->mfma.eoff.size() - 1;
         const size_t ewords = 256u * static_cast<size_t>(p->mfma_slots);
-        const size_t npacked = p->mfma_dma ? nsteps_all * ewords + 4 : ne + 1;
-        p->mfma_zeros_at = p->mfma_dma ? nsteps_all * ewords : 0;
-        std::vector<int> dst(ne);
-        std::vector<uint16_t> cell(ne);
+        std::vector<int> ebase;
+        std::vector<i32x2v> emeta;
+        if (p->mfma_pair) {
+            ebase.resize(nsteps_all + 1);
+            emeta.resize(nsteps_all);
+            ebase[0] = 0;
+            for (size_t g = 0; g < nsteps_all; g++) {
+                const int cnt = p->mfma.eoff[g + 1] - p->mfma.eoff[g];
+                const int chunks = std::max(1, (cnt + kPairChunk - 1) / kPairChunk);
+                ebase[g + 1] = ebase[g] + chunks * kPairChunk;
+                emeta[g] = i32x2v{ebase[g], std::max(1, (cnt + kPairGroup - 1) / kPairGroup)};
+            }
+        }
+        const size_t nblocks = p->mfma_pair ? static_cast<size_t>(ebase.back()) : nsteps_all * ewords;
+        const bool tiles_lds = p->mfma_dma || p->mfma_pair;
+        const size_t npacked = tiles_lds ? nblocks + 4 : ne + 1;
+        p->mfma_zeros_at = tiles_lds ? nblocks : 0;
+        // pack kernel inputs, per word it writes (all words before the zeros /
+        // the sentinel): the nonzero's CSR index and the cell
+        const size_t nwords = tiles_lds ? nblocks : ne;
+        std::vector<int> src(nwords, -1);
+        std::vector<uint16_t> cell(nwords, 0xffffu);
         std::vector<uint32_t> packed(npacked, kNoEntry);
-        if (p->mfma_dma) std::fill(packed.end() - 4, packed.end(), 0u);
-        std::vector<int4> segs;
+        if (tiles_lds) std::fill(packed.end() - 4, packed.end(), 0u);
+        if (p->mfma_pair) {
+            for (size_t w = 0; w < p->mfma.windows.size(); w++) {
+                const Int4 win = p->mfma.windows[w];
+                for (int32_t j = 0; j < win.y; j++)
+                    for (int32_t x = ebase[win.z + j]; x < ebase[win.z + j + 1]; x++) {
+                        packed[x] = pair_cell_addr(j % kPairSteps, kDmaATile + ((x - ebase[win.z + j]) % kPairChunk) / 4);
+                        cell[x] = static_cast<uint16_t>(packed[x]);
+                    }
+            }
+        }
         const int row_mask = 127, k_shift = 7, idx_shift = 12;
-        for (size_t w = 0, e = 0, base = 0; w < p->mfma.windows.size(); w++) {
-            // The window's entries, indexed by their offset in its CSR range.
+        for (size_t w = 0, e = 0; w < p->mfma.windows.size(); w++) {
             const Int4 win = p->mfma.windows[w];
-            const size_t e_end = static_cast<size_t>(p->mfma.eoff[win.z + win.y]);
-            const size_t cnt = e_end - e;
-            if (!segs.empty() && segs.back().x + segs.back().y == win.w) segs.back().y += static_cast<int>(cnt);
-            else segs.push_back(int4{win.w, static_cast<int>(cnt), static_cast<int>(base), 0});
             for (int32_t g = win.z; g < win.z + win.y; g++)
                 for (; e < static_cast<size_t>(p->mfma.eoff[g + 1]); e++) {
                     const uint32_t en = p->mfma.entries[e];
-                    const size_t k = base + (en >> idx_shift);
-                    dst[k] = p->mfma_dma ? static_cast<int>(g * ewords + (e - p->mfma.eoff[g])) : static_cast<int>(e);
-                    cell[k] = static_cast<uint16_t>(
-                        a_cell(static_cast<int>(en & row_mask), static_cast<int>((en >> k_shift) & 31u)));
+                    const int acell = a_cell(static_cast<int>(en & row_mask), static_cast<int>((en >> k_shift) & 31u));
+                    size_t x;
+                    uint16_t c;
+                    if (p->mfma_pair) {
+                        x = static_cast<size_t>(ebase[g] + pair_entry_word(static_cast<int>(e - p->mfma.eoff[g])));
+                        c = static_cast<uint16_t>(pair_cell_addr((g - win.z) % kPairSteps, acell));
+                    } else {
+                        x = p->mfma_dma ? g * ewords + (e - p->mfma.eoff[g]) : e;
+                        c = static_cast<uint16_t>(acell);
+                    }
+                    src[x] = win.w + static_cast<int>(en >> idx_shift);
+                    cell[x] = c;
                 }
-            base += cnt;
         }
-        p->n_pk_seg = static_cast<int32_t>(segs.size());
+        p->n_pk_words = static_cast<int32_t>(nwords);
         p->n_packed = npacked;
-        if ((st = dev_upload(&p->d_pk_seg, segs.data(), segs.size()))) return bail(st);
-        if ((st = dev_upload(&p->d_pk_dst, dst.data(), ne))) return bail(st);
-        if ((st = dev_upload(&p->d_pk_cell, cell.data(), ne))) return bail(st);
+        if ((st = dev_upload(&p->d_pk_src, src.data(), nwords))) return bail(st);
+        if ((st = dev_upload(&p->d_pk_cell, cell.data(), nwords))) return bail(st);
         if ((st = dev_upload(&p->d_packed, packed.data(), npacked))) return bail(st);
+        if ((st = dev_upload(&p->d_emeta, emeta.data(), emeta.size()))) return bail(st);
     }
     if (hipDeviceSynchronize() != hipSuccess) return bail(fail(TCA_ERR_HIP, "hipDeviceSynchronize failed"));
 
@@ -400,7 +455,9 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
     in.cond_cols_mfma = p->mfma.cond_cols;
     in.mfma_blocks = in.n_windows_mfma * p->mfma_col_blocks;
     in.mfma_blockdim = kMfmaThreads;
-    if (p->mfma_dma && p->mfma_slots <= 2)
+    if (p->mfma_pair)
+        in.mfma_lds_bytes = mfma_pair_lds_bytes();
+    else if (p->mfma_dma && p->mfma_slots <= 2)
         in.mfma_lds_bytes = mfma_dma_lds_bytes();
     else
         in.mfma_lds_bytes = p->mfma_slots == 1 ? mfma_lds_bytes<1>() : p->mfma_slots == 2 ? mfma_lds_bytes<2>() : mfma_lds_bytes<4>();

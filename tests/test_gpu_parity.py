@@ -137,17 +137,18 @@ def test_exact_bit_equal_all_widths(torch_cuda, dtype):
         assert np.array_equal(got, want), (dtype, n, np.abs(got - want).max())
 
 
-@pytest.mark.parametrize("variant", [S.TCA_PLAN_MFMA_REGS, 0], ids=["regs", "dma"])
+@pytest.mark.parametrize("variant", [S.TCA_PLAN_MFMA_REGS, S.TCA_PLAN_MFMA_DMA, 0], ids=["regs", "dma", "pair"])
 @pytest.mark.parametrize("dtype", [S.TCA_F16, S.TCA_BF16])
 def test_mfma_exact_bit_equal(torch_cuda, dtype, variant):
     """Condensed-tile MFMA path (forced on every eligible window) is bit-equal
     to the oracle on exact-arithmetic inputs, for partial windows, partial
     column blocks and empty rows.  The cases cover one, two and four entry
     slots per thread (up to 256, 512 and 1024 nonzeros in a step) and windows
-    whose steps span several pipeline blocks, for both tile kernels (register
-    staging and global->LDS transfers).  The LDS-DMA kernel takes at most 512
-    nonzeros per step of its 128-row windows: the cases marked dense stay on
-    the row kernel under it (still checked against the oracle)."""
+    whose steps span several pipeline blocks, for the three tile kernels
+    (register staging, global->LDS transfers, paired MFMA and staging
+    wavefronts).  The two 128-row kernels take at most 512 nonzeros per step:
+    the cases marked dense stay on the row kernel under them (still checked
+    against the oracle)."""
     rng = np.random.default_rng(71 + dtype)
     dense = {(200, 64, 0.45), (128, 2048, 0.2), (64, 1500, 0.4)}
     for m, k, p in [(64, 256, 0.1), (130, 700, 0.05), (200, 64, 0.45), (17, 40, 0.3), (96, 5000, 0.004),
@@ -160,7 +161,7 @@ def test_mfma_exact_bit_equal(torch_cuda, dtype, variant):
             with S.Plan(a, n, S.TCA_PLAN_FORCE_MFMA | variant) as pl:
                 info = pl.info()
                 got = run_gpu(torch_cuda, a, b, plan=pl)
-            assert info["n_windows_mfma"] > 0 or (variant == 0 and (m, k, p) in dense), (m, k, n)
+            assert info["n_windows_mfma"] > 0 or (variant != S.TCA_PLAN_MFMA_REGS and (m, k, p) in dense), (m, k, n)
             want = oracle_c(a, b)
             assert np.array_equal(got, want), (m, k, p, n, np.abs(got - want).max())
 

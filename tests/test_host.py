@@ -270,9 +270,10 @@ def test_mfma_window_plan_decodes_to_the_csr(m, k, n, p, flags):
     assert len(S.plan_mfma_windows(a, 100, flags=S.TCA_PLAN_FORCE_MFMA)[0]) == 0  # N % 8 != 0
 
 
-@pytest.mark.parametrize("kernel", [0, S.TCA_PLAN_MFMA_REGS], ids=["dma", "regs"])
+@pytest.mark.parametrize("kernel", [0, S.TCA_PLAN_MFMA_REGS], ids=["128x64", "regs"])
 def test_mfma_default_routing_follows_the_cost_model(kernel):
-    """Default routing, for both tile kernels: the lognormal 4096 x 4096 layer
+    """Default routing, for both tile shapes (128-row windows of the paired and
+    LDS-DMA kernels, 64-row windows of the register-staged one): the lognormal 4096 x 4096 layer
     (config 1) goes to the tile kernel, the small 2048 x 512 Bernoulli layer
     (config 0) stays on the row kernel (too few steps and workgroups to
     amortise the pipeline fill), and a very sparse matrix (density below
