@@ -38,6 +38,8 @@ DMA_TILE_KERNEL = "mfma_dma_kernel"    # the "tiles" phase under plan flag TCA_P
 # calibration: FETCH x 2.00, WRITE x 1.00), keyed by (config, phase, flags).
 # Source: the profiles/ summaries named in each entry.
 MEASURED_TRAFFIC_KIB = {
+    # profiles/mfma_pair_kernel_config1.md (paired tile kernel, the default)
+    (1, "tiles", 0): (21323.1 * 2.0, 8436.0),
     # profiles/mfma_dma_kernel_config1.md (LDS-DMA tile kernel)
     (1, "tiles", 8): (39252.0 * 2.0, 8319.2),  # flags 8 = TCA_PLAN_MFMA_DMA
     # profiles/mfma_tile_kernel_config1.md (register-staged tile kernel)
