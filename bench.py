@@ -32,6 +32,7 @@ PHASE_KERNELS = {"pack": "mfma_pack_kernel", "tiles": "mfma_pair_kernel", "rows"
                  "segments": "seg_finalize_kernel"}
 REGS_TILE_KERNEL = "mfma_tile_kernel"  # the "tiles" phase under plan flag TCA_PLAN_MFMA_REGS
 DMA_TILE_KERNEL = "mfma_dma_kernel"    # the "tiles" phase under plan flag TCA_PLAN_MFMA_DMA
+DENSE_TILE_KERNEL = "mfma_dense_kernel"  # the "tiles" phase under plan flag TCA_PLAN_MFMA_DENSE
 
 # HBM bytes per launch of the dominant kernel, measured with rocprofv3 --pmc
 # FETCH_SIZE and WRITE_SIZE (KiB per dispatch, already scaled by the copy
@@ -62,7 +63,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--flags", type=int, default=0,
                     help="plan flags (1 = no MFMA, 2 = force MFMA, 4 = register-staged tile kernel, "
-                         "8 = LDS-DMA tile kernel)")
+                         "8 = LDS-DMA tile kernel, 16 = dense-tile kernel)")
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
                     help="before timing, run one device-to-device copy of MIB MiB (a known-size kernel to "
                          "scale rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
@@ -161,6 +162,8 @@ def main():
         kernel_name = REGS_TILE_KERNEL
     elif dominant == "tiles" and args.flags & S.TCA_PLAN_MFMA_DMA:
         kernel_name = DMA_TILE_KERNEL
+    elif dominant == "tiles" and args.flags & S.TCA_PLAN_MFMA_DENSE:
+        kernel_name = DENSE_TILE_KERNEL
     traffic = int(round((kib[0] + kib[1]) * 1024)) if kib else None
     log(f"kernel avg {ms_per_step * 1e3:.2f} us/step, wall {wall_ms:.2f} ms for {args.warmup}+{args.steps} steps")
 

@@ -52,6 +52,7 @@ typedef enum tca_status {
 #define TCA_PLAN_FORCE_MFMA 2u /* route every eligible 64-row window to the MFMA tile kernel (fp16/bf16, N % 8 == 0) */
 #define TCA_PLAN_MFMA_REGS 4u  /* register-staged 64 x 128 tile kernel instead of the default paired 128 x 64 one */
 #define TCA_PLAN_MFMA_DMA 8u   /* LDS-DMA 128 x 64 tile kernel instead of the default paired one */
+#define TCA_PLAN_MFMA_DENSE 16u /* dense-tile 128 x 64 kernel (plan keeps dense condensed windows) */
 
 typedef struct tca_spmm_plan tca_spmm_plan;
 

@@ -18,6 +18,7 @@ LIB_PATH = os.path.join(_HERE, "lib", "libtcaspmm.so")
 TCA_F16, TCA_F32, TCA_BF16 = 0, 1, 2
 DTYPE_NAMES = {TCA_F16: "f16", TCA_F32: "f32", TCA_BF16: "bf16"}
 TCA_PLAN_DEFAULT, TCA_PLAN_NO_MFMA, TCA_PLAN_FORCE_MFMA, TCA_PLAN_MFMA_REGS, TCA_PLAN_MFMA_DMA = 0, 1, 2, 4, 8
+TCA_PLAN_MFMA_DENSE = 16
 
 i32 = ctypes.c_int32
 i64 = ctypes.c_int64

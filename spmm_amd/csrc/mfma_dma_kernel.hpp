@@ -28,7 +28,7 @@
 //     that use the previous ones, and each iteration issues the same four
 //     transfers, so one s_waitcnt vmcnt(N) retires exactly what is due.
 // Pipeline, iteration i (one barrier each), lookahead LB = 3:
-//   producers: issue B(i + 3); load the row offsets of B(i + 4); wait until
+//   producers: issue B(i + 3); load the row offsets of B(i + 5); wait until
 //              B(i + 1) has landed (B(i + 2), B(i + 3) stay in flight)
 //   consumers: load the entries of A(i + 2); read A(i), B(i) fragments;
 //              build A(i + 1) from the entries loaded in iteration i - 1;
@@ -232,8 +232,7 @@ __global__ __launch_bounds__(kMfmaThreads) void mfma_dma_kernel(MfmaArgs a) {
         // scalar loads, which keeps vmcnt counting the transfers alone).
         typedef __attribute__((address_space(4))) const uint32_t* cu32p;
         const cu32p ucols_c = (cu32p)(a.ucols);
-        uint32_t mu[KS][8];
-        auto load_meta = [&](int ib) {
+        auto load_meta = [&](int ib, uint32_t (&mu)[KS][8]) {
 #pragma unroll
             for (int sp = 0; sp < KS; sp++) {
                 const int j = min(max(KS * ib + sp, 0), nsteps - 1);
@@ -242,9 +241,10 @@ __global__ __launch_bounds__(kMfmaThreads) void mfma_dma_kernel(MfmaArgs a) {
                 for (int r = 0; r < 8; r++) mu[sp][r] = up[r];
             }
         };
-        int bslot = 0;  // ring slot of B(i + LB): B(n) sits in slot n % NB
-        load_meta(0);
-        for (int i = -LB; i < niters; i++) {
+        // iteration i: B(i + LB) from `mu`, whose registers then receive the
+        // offsets of B(i + LB + 2) (two buffers, so the scalar loads have a
+        // whole iteration before their first use)
+        auto iteration = [&](const int i, int& bslot, uint32_t (&mu)[KS][8]) {
 #pragma unroll
             for (int sp = 0; sp < KS; sp++) {
                 // rows 8 pw .. 8 pw + 7 of B(i + LB), step sp
@@ -263,13 +263,22 @@ __global__ __launch_bounds__(kMfmaThreads) void mfma_dma_kernel(MfmaArgs a) {
                 dma_x4(src, lds_addr(&Bs[bslot][sp][kDmaBRow * 8 * pw]));
             }
             bslot = bslot == NB - 1 ? 0 : bslot + 1;
-            // next iteration's row offsets (after the transfers that used these)
-            load_meta(i + LB + 1);
+            load_meta(i + LB + 2, mu);
             wait_vmcnt<kDmaWait>();  // B(i + 1) has landed
             // A plain barrier: this wavefront has no LDS instruction to order,
             // and waiting for its scalar loads here would stall the barrier.
             __builtin_amdgcn_s_barrier();
+        };
+        int bslot = 0;  // ring slot of B(i + LB): B(n) sits in slot n % NB
+        uint32_t mu0[KS][8], mu1[KS][8];
+        load_meta(0, mu0);
+        load_meta(1, mu1);
+        int i = -LB;
+        for (; i + 1 < niters; i += 2) {
+            iteration(i, bslot, mu0);
+            iteration(i + 1, bslot, mu1);
         }
+        if (i < niters) iteration(i, bslot, mu0);
         wait_vmcnt<0>();
     }
 

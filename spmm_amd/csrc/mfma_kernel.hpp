@@ -100,6 +100,8 @@ struct MfmaArgs {
     int sentinel;            // index of the kNoEntry entry, loaded for empty slots
     const void* zeros;       // 16 zero bytes (source of padding B pieces, LDS-DMA and paired kernels)
     const i32x2v* emeta;     // [global step] {first word of the packed block, groups of 64 entries} (paired kernel)
+    const void* adense;      // [global step] dense A tile, 8 KiB in fragment order (dense kernel)
+    int n_windows;           // windows (dense kernel: its workgroup -> window mapping)
 };
 
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;

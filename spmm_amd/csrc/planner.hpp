@@ -78,10 +78,16 @@ struct MfmaShape {
 };
 // Register-staged kernel: 64 x 128 tiles, up to 1024 nonzeros per step, a
 // 4-step iteration ~0.95 us.  LDS-DMA kernel: 128 x 64 tiles, up to 512.
+// Dense-tile kernel: 128 x 64 tiles, no per-step entry limit (a step is a
+// dense 128 x 32 tile), a 4-step iteration ~0.5 us.
 constexpr MfmaShape kMfmaRegsShape = {64, 128, 1024, 3.0, 0.95, 4};
 constexpr MfmaShape kMfmaDmaShape = {128, 64, 512, 3.0, 0.95, 3};
+constexpr MfmaShape kMfmaDenseShape = {128, 64, 128 * 32, 3.0, 0.5, 3};
 inline const MfmaShape& mfma_shape(uint32_t flags) {
-    return (flags & TCA_PLAN_MFMA_REGS) ? kMfmaRegsShape : kMfmaDmaShape;
+    if (flags & TCA_PLAN_MFMA_REGS) return kMfmaRegsShape;
+    if (flags & TCA_PLAN_MFMA_DMA) return kMfmaDmaShape;
+    if (flags & TCA_PLAN_MFMA_DENSE) return kMfmaDenseShape;
+    return kMfmaDmaShape;
 }
 
 struct MfmaPlan {

@@ -131,10 +131,16 @@ __device__ __forceinline__ void accumulate_span(float (&acc)[E], int beg, int en
                                                 int logS) {
     const uint32_t rowbytes = static_cast<uint32_t>(a.N) * sizeof(T);
     const uint32_t colbytes = static_cast<uint32_t>(col) * sizeof(T);
+    // Indices and values of the first chunk of 64; each chunk's loop below
+    // first issues the loads of the next chunk, so they travel while the B
+    // rows of this one are gathered.
+    int myc = load_idx(rcol, beg + lane, beg + lane < end);
+    float mya = load_val<T>(rval, beg + lane, beg + lane < end);
     for (int base = beg; base < end; base += 64) {
         const int n = min(64, end - base);
-        const int myc = load_idx(rcol, base + lane, lane < n);
-        const float mya = load_val<T>(rval, base + lane, lane < n);
+        const int nb = base + 64;
+        const int nmyc = load_idx(rcol, nb + lane, nb + lane < end);
+        const float nmya = load_val<T>(rval, nb + lane, nb + lane < end);
         const int rounds = (n + (1 << logS) - 1) >> logS;
         for (int r = 0; r < rounds; r += kRowUnroll) {
             Pack<T, E> bv[kRowUnroll];
@@ -159,6 +165,8 @@ __device__ __forceinline__ void accumulate_span(float (&acc)[E], int beg, int en
 #pragma unroll
             for (int u = 0; u < kRowUnroll; u++) fma_pack<T, E>(acc, av[u], bv[u]);
         }
+        myc = nmyc;
+        mya = nmya;
     }
 }
 

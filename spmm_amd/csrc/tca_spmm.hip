@@ -14,6 +14,7 @@
 #include "mfma_kernel.hpp"
 #include "mfma_dma_kernel.hpp"
 #include "mfma_pair_kernel.hpp"
+#include "mfma_dense_kernel.hpp"
 #include "sddmm_kernel.hpp"
 
 using namespace tca;
@@ -35,6 +36,12 @@ struct tca_spmm_plan {
     int32_t mfma_slots = 1;  // entries per thread and step in the MFMA kernel (1, 2 or 4)
     bool mfma_dma = false;   // LDS-DMA tile kernel instead of the register-staged one
     bool mfma_pair = false;  // paired (MFMA + staging wavefront) tile kernel
+    bool mfma_dense = false; // dense-tile kernel (plan keeps dense condensed windows)
+    uint16_t* d_adense = nullptr;  // dense kernel: [global step] 8 KiB A tile, then 1 KiB of zeros
+    size_t adense_halves = 0;
+    int32_t n_dn = 0;              // dense kernel: nonzeros the pack writes
+    int* d_dn_src = nullptr;       // per nonzero (sorted by position): its CSR index
+    uint32_t* d_dn_pos = nullptr;  // and its half index in d_adense
     int32_t mfma_groups = 0; // paired kernel: groups of 64 entries a step may hold (4 or 8)
     size_t mfma_zeros_at = 0;  // word offset of 16 zero bytes in d_packed (LDS-DMA kernel)
     size_t n_packed = 0;       // words of d_packed
@@ -90,6 +97,9 @@ void free_plan_device(tca_spmm_plan* p) {
     (void)hipFree(p->d_pk_src);
     (void)hipFree(p->d_pk_cell);
     (void)hipFree(p->d_packed);
+    (void)hipFree(p->d_adense);
+    (void)hipFree(p->d_dn_src);
+    (void)hipFree(p->d_dn_pos);
 }
 
 template <typename T, int E>
@@ -141,6 +151,12 @@ int launch_rows_e(const tca_spmm_plan* p, const void* val, const void* B, float*
 
 // Pairs the MFMA entries with this run's values (before the tile kernel).
 void launch_pack(const tca_spmm_plan* p, const void* val, hipStream_t s) {
+    if (p->mfma_dense) {
+        if (p->n_dn > 0)
+            hipLaunchKernelGGL(dense_pack_kernel, dim3((p->n_dn + 255) / 256), dim3(256), 0, s, p->d_dn_src,
+                               p->d_dn_pos, p->n_dn, static_cast<const uint16_t*>(val), p->d_adense);
+        return;
+    }
     const int n = p->n_pk_words;
     if (p->mfma.windows.empty() || n == 0) return;
     hipLaunchKernelGGL(mfma_pack_kernel, dim3((n + 1023) / 1024), dim3(256), 0, s, p->d_pk_src, p->d_pk_cell, n,
@@ -175,6 +191,15 @@ int launch_mfma(const tca_spmm_plan* p, const void* B, float* C, hipStream_t s) 
     a.eoff_bytes = static_cast<uint32_t>(p->mfma.eoff.size() * 4);
     const dim3 grid(static_cast<unsigned>(p->mfma.windows.size()) * p->mfma_col_blocks);
     const bool bf = p->dtype == TCA_BF16;
+    if (p->mfma_dense) {
+        a.adense = p->d_adense;
+        a.zeros = p->d_adense + (p->adense_halves - 512);
+        a.n_windows = static_cast<int>(p->mfma.windows.size());
+        const dim3 dgrid(mfma_dense_grid(a.n_windows, p->mfma_col_blocks));
+        if (bf) hipLaunchKernelGGL((mfma_dense_kernel<true>), dgrid, dim3(kDnThreads), 0, s, a);
+        else hipLaunchKernelGGL((mfma_dense_kernel<false>), dgrid, dim3(kDnThreads), 0, s, a);
+        return TCA_OK;
+    }
     if (p->mfma_pair) {
         switch (p->mfma_groups) {
             case 4:
@@ -312,12 +337,21 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
     // windows x 128 columns (register-staged) or 128 x 64 (paired or LDS-DMA kernel).
     // TCA_MFMA_MIN_DENSITY (tuning only) overrides the routing threshold.
     const char* md = std::getenv("TCA_MFMA_MIN_DENSITY");
-    const MfmaShape& shape = mfma_shape(flags);
+    const MfmaShape* shape = &mfma_shape(flags);
+    const double min_density = md ? std::atof(md) : kMfmaMinDensity;
     plan_mfma(rowptr, colidx, M, N, dtype, (flags & TCA_PLAN_FORCE_MFMA) != 0, (flags & TCA_PLAN_NO_MFMA) != 0,
-              md ? std::atof(md) : kMfmaMinDensity, shape, &p->mfma);
+              min_density, *shape, &p->mfma);
     p->mfma_dma = (flags & TCA_PLAN_MFMA_REGS) == 0 && (flags & TCA_PLAN_MFMA_DMA) != 0;
-    p->mfma_pair = (flags & (TCA_PLAN_MFMA_REGS | TCA_PLAN_MFMA_DMA)) == 0;
-    p->mfma_col_blocks = (N + shape.tile_cols - 1) / shape.tile_cols;
+    p->mfma_dense = (flags & (TCA_PLAN_MFMA_REGS | TCA_PLAN_MFMA_DMA)) == 0 && (flags & TCA_PLAN_MFMA_DENSE) != 0;
+    if (p->mfma_dense && (p->mfma.eoff.size() - 1) * static_cast<size_t>(kDnATileBytes) > kDenseMaxBytes) {
+        // Dense windows past the budget: the paired kernel, which keeps only the entries.
+        p->mfma_dense = false;
+        shape = &kMfmaDmaShape;
+        plan_mfma(rowptr, colidx, M, N, dtype, (flags & TCA_PLAN_FORCE_MFMA) != 0, (flags & TCA_PLAN_NO_MFMA) != 0,
+                  min_density, *shape, &p->mfma);
+    }
+    p->mfma_pair = (flags & (TCA_PLAN_MFMA_REGS | TCA_PLAN_MFMA_DMA)) == 0 && !p->mfma_dense;
+    p->mfma_col_blocks = (N + shape->tile_cols - 1) / shape->tile_cols;
     {
         int32_t most = 0;
         for (size_t i = 0; i + 1 < p->mfma.eoff.size(); i++) most = std::max(most, p->mfma.eoff[i + 1] - p->mfma.eoff[i]);
@@ -356,6 +390,41 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
         }
         if ((st = dev_upload(&p->d_ucols, uoff.data(), uoff.size()))) return bail(st);
         if ((st = dev_upload(&p->d_eoff, p->mfma.eoff.data(), p->mfma.eoff.size()))) return bail(st);
+    }
+    if (!p->mfma.windows.empty() && p->mfma_dense) {
+        // Dense condensed windows: 8 KiB per global step (128 rows x 32
+        // condensed columns in fragment order), zero except at the entries,
+        // whose values the pack kernel writes each run; 1 KiB of zeros after
+        // them (the B source for padding rows).  Entries sorted by position.
+        const size_t nsteps_all = p->mfma.eoff.size() - 1;
+        p->adense_halves = nsteps_all * static_cast<size_t>(kDmaATile) + 512;
+        std::vector<std::pair<uint32_t, int32_t>> ent;
+        ent.reserve(p->mfma.entries.size());
+        for (size_t w = 0, e = 0; w < p->mfma.windows.size(); w++) {
+            const Int4 win = p->mfma.windows[w];
+            for (int32_t g = win.z; g < win.z + win.y; g++)
+                for (; e < static_cast<size_t>(p->mfma.eoff[g + 1]); e++) {
+                    const uint32_t en = p->mfma.entries[e];
+                    const uint32_t pos = static_cast<uint32_t>(g) * kDmaATile +
+                                         static_cast<uint32_t>(a_cell(static_cast<int>(en & 127u),
+                                                                      static_cast<int>((en >> 7) & 31u)));
+                    ent.emplace_back(pos, win.w + static_cast<int32_t>(en >> 12));
+                }
+        }
+        std::sort(ent.begin(), ent.end());
+        std::vector<int32_t> dsrc(ent.size());
+        std::vector<uint32_t> dpos(ent.size());
+        for (size_t x = 0; x < ent.size(); x++) {
+            dpos[x] = ent[x].first;
+            dsrc[x] = ent[x].second;
+        }
+        p->n_dn = static_cast<int32_t>(ent.size());
+        if ((st = dev_upload(&p->d_dn_src, dsrc.data(), dsrc.size()))) return bail(st);
+        if ((st = dev_upload(&p->d_dn_pos, dpos.data(), dpos.size()))) return bail(st);
+        if ((st = dev_upload(&p->d_adense, nullptr, p->adense_halves))) return bail(st);
+        if (hipMemset(p->d_adense, 0, p->adense_halves * 2) != hipSuccess)
+            return bail(fail(TCA_ERR_HIP, "hipMemset of the dense tiles failed"));
+    } else if (!p->mfma.windows.empty()) {
         // Packed entries.  Register-staged kernel: walk order, then one
         // kNoEntry sentinel.  LDS-DMA kernel: step g's block at g * 256 * slots
         // words (unused words kNoEntry).  Paired kernel: step g's block at
@@ -453,9 +522,12 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
     in.rows_mfma = p->mfma.rows;
     in.nnz_mfma = p->mfma.nnz;
     in.cond_cols_mfma = p->mfma.cond_cols;
-    in.mfma_blocks = in.n_windows_mfma * p->mfma_col_blocks;
+    in.mfma_blocks = p->mfma_dense ? mfma_dense_grid(in.n_windows_mfma, p->mfma_col_blocks)
+                                   : in.n_windows_mfma * p->mfma_col_blocks;
     in.mfma_blockdim = kMfmaThreads;
-    if (p->mfma_pair)
+    if (p->mfma_dense)
+        in.mfma_lds_bytes = mfma_dense_lds_bytes();
+    else if (p->mfma_pair)
         in.mfma_lds_bytes = mfma_pair_lds_bytes();
     else if (p->mfma_dma && p->mfma_slots <= 2)
         in.mfma_lds_bytes = mfma_dma_lds_bytes();

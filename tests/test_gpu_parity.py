@@ -137,7 +137,8 @@ def test_exact_bit_equal_all_widths(torch_cuda, dtype):
         assert np.array_equal(got, want), (dtype, n, np.abs(got - want).max())
 
 
-@pytest.mark.parametrize("variant", [S.TCA_PLAN_MFMA_REGS, S.TCA_PLAN_MFMA_DMA, 0], ids=["regs", "dma", "pair"])
+@pytest.mark.parametrize("variant", [S.TCA_PLAN_MFMA_REGS, S.TCA_PLAN_MFMA_DMA, 0, S.TCA_PLAN_MFMA_DENSE],
+                         ids=["regs", "dma", "pair", "dense"])
 @pytest.mark.parametrize("dtype", [S.TCA_F16, S.TCA_BF16])
 def test_mfma_exact_bit_equal(torch_cuda, dtype, variant):
     """Condensed-tile MFMA path (forced on every eligible window) is bit-equal
