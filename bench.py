@@ -45,6 +45,11 @@ MEASURED_TRAFFIC_KIB = {
     (1, "tiles", 8): (39252.0 * 2.0, 8319.2),  # flags 8 = TCA_PLAN_MFMA_DMA
     # profiles/mfma_tile_kernel_config1.md (register-staged tile kernel)
     (1, "tiles", 4): (12768.8 * 2.0, 10785.3),  # flags 4 = TCA_PLAN_MFMA_REGS
+    # profiles/row_kernel_graph_configs.md (row kernel, default routing)
+    (0, "rows", 0): (1611.8 * 2.0, 3001.0),
+    (2, "rows", 0): (12064593.2 * 2.0, 122066.5),
+    (3, "rows", 0): (12350070.5 * 2.0, 1225462.5),
+    (4, "rows", 0): (1298864.7 * 2.0, 402965.0),
 }
 
 
@@ -216,7 +221,9 @@ def main():
         "roofline": {"bound": "hbm", "kernel": kernel_name, "bytes_alg": bytes_dom,
                      "kernel_us": round(dom_ms * 1e3, 3),
                      "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": traffic},
+                     "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": traffic,
+                     # measured L2 <-> fabric bytes of the same launch over its time (HBM or MALL)
+                     "traffic_gbs": round(traffic / (dom_ms * 1e-3) / 1e9, 2) if traffic else None},
         "cpu_baseline": cpu,
     }
     plan.close()
