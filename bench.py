@@ -72,6 +72,9 @@ def main():
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
                     help="before timing, run one device-to-device copy of MIB MiB (a known-size kernel to "
                          "scale rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
+    ap.add_argument("--bell", type=int, default=0, metavar="BS",
+                    help="time the Blocked-ELL kernel (tca_bell_spmm) on A converted to blocks of BS x BS "
+                         "instead of the CSR plan (fp16 / bf16 configurations)")
     ap.add_argument("--traffic-kib", type=float, nargs=2, default=None, metavar=("FETCH", "WRITE"),
                     help="measured FETCH_SIZE and WRITE_SIZE of the dominant kernel per launch, already scaled "
                          "by the copy calibration (KiB); reported as roofline.traffic in bytes")
@@ -103,6 +106,9 @@ def main():
     val = dev_tensor(a.values)
     bd = dev_tensor(b)
     c = torch.empty((a.nrow, n), dtype=torch.float32, device=dev)
+    if args.bell:
+        bell(args, a, n, bd, c, dev_tensor)
+        return
     plan = S.Plan(a, n, args.flags)
     info = plan.info()
     log("plan:", json.dumps(info))
@@ -227,6 +233,58 @@ def main():
         "cpu_baseline": cpu,
     }
     plan.close()
+    print(json.dumps(out), flush=True)
+
+
+def bell(args, a, n, bd, c, dev_tensor):
+    """The Blocked-ELL kernel on the configuration's A (one JSON line, same schema)."""
+    import numpy as np
+    import torch
+
+    import spmm_amd as S
+
+    t0 = time.perf_counter()
+    colind, vals = S.csr_to_bell(a, args.bell)
+    conv_ms = (time.perf_counter() - t0) * 1e3
+    dcol, dval = dev_tensor(colind), dev_tensor(vals)
+    m, k, nnz = a.nrow, a.ncol, a.nnz
+    log(f"Blocked-ELL bs={args.bell}: {colind.shape[0]} block rows x {colind.shape[1]} blocks, "
+        f"{vals.nbytes / 1e6:.1f} MB of values, conversion {conv_ms:.1f} ms")
+    stream = torch.cuda.current_stream()
+    run = lambda: S.bell_spmm(dcol, dval, m, k, n, args.bell, a.dtype, bd, c, stream=stream.cuda_stream)
+    for _ in range(args.warmup):
+        run()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(args.steps):
+        run()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    if not torch.isfinite(c).all().item():
+        sys.exit("non-finite output")
+    s_a = 4 if a.dtype == S.TCA_F32 else 2
+    bytes_alg = 4 * (m + 1) + nnz * (4 + s_a) + k * n * s_a + m * n * 4
+    # bytes the format itself must move: its block values and column list, B, C
+    bytes_fmt = vals.nbytes + colind.nbytes + k * n * s_a + m * n * 4
+    mfma_flops = 2.0 * vals.shape[0] * vals.shape[1] * n  # every stored block multiplied
+    out = {
+        "metric": METRIC, "value": round(2.0 * nnz * n / (ms * 1e-3) / 1e9, 3), "unit": "GFLOP/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 6), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None,
+        "dtype": ("f16" if a.dtype == S.TCA_F16 else "bf16") + "->f32acc",
+        "data": "synthetic (seeded generators, seed %d)" % args.seed,
+        "config": {"workload": WORKLOADS[args.config] + f", Blocked-ELL {args.bell}x{args.bell}", "M": m, "K": k,
+                   "N": n, "nnz": nnz, "bytes_alg": bytes_alg, "ell_blocks": int(colind.shape[1]),
+                   "bell_value_bytes": int(vals.nbytes), "conversion_ms": round(conv_ms, 3),
+                   "mfma_tflops": round(mfma_flops / (ms * 1e-3) / 1e12, 2)},
+        "roofline": {"bound": "hbm", "kernel": "bell_mfma_kernel", "bytes_alg": bytes_alg,
+                     "kernel_us": round(ms * 1e3, 3), "achieved": round(bytes_alg / (ms * 1e-3) / 1e9, 2),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(bytes_alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 5),
+                     "traffic": None, "format_bytes_gbs": round(bytes_fmt / (ms * 1e-3) / 1e9, 2)},
+        "cpu_baseline": None,
+    }
     print(json.dumps(out), flush=True)
 
 

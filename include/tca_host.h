@@ -120,6 +120,21 @@ int tca_csr_transpose(const int32_t* rowptr, const int32_t* colidx, int32_t M, i
 /* Value conversion of a CSR (same structure, new dtype, RNE rounding). */
 int tca_csr_convert(const tca_csr* a, int32_t dtype, tca_csr* out);
 
+/* Blocked-ELL, the format reference perform_cuSPARSE_BlockSpMM builds for
+ * cusparseCreateBlockedEll (src/spmm_cusparse.cu:201-342): blocks of
+ * bsize x bsize; block row i (rows i*bsize .. i*bsize + bsize - 1, rows past
+ * M zero) lists the block columns j that hold a nonzero value (|v| != 0, as
+ * the reference counts them at :261-269), ascending, padded with -1 to
+ * ell_blocks = the longest such list.  colind is [ceil(M/bsize)][ell_blocks];
+ * ell_values is row-major [ceil(M/bsize)*bsize][ell_blocks*bsize] of dtype:
+ * element (r, e*bsize + c) = A[r][colind[r/bsize][e]*bsize + c], zero for
+ * padding blocks and for columns past K.
+ * With colind == NULL and ell_values == NULL only *ell_blocks is computed
+ * (the size query); otherwise both arrays must be sized from it. */
+int tca_csr_to_bell(const int32_t* rowptr, const int32_t* colidx, const void* values, int32_t M, int32_t K,
+                    int32_t nnz, int32_t dtype, int32_t bsize, int32_t* ell_blocks, int32_t* colind,
+                    void* ell_values);
+
 /* ---- scalar conversion (IEEE binary16 / bfloat16, round to nearest even) ---- */
 uint16_t tca_f32_to_f16(float x);
 float tca_f16_to_f32(uint16_t h);

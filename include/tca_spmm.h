@@ -139,6 +139,17 @@ int tca_sddmm(const tca_spmm_plan* plan, const float* d_G, const void* d_B, floa
 int tca_gather_values(const int32_t* d_perm, int32_t n, const void* d_val, int32_t dtype, float* d_out,
                       void* stream);
 
+/* C = A * B with A in Blocked-ELL (layout of tca_csr_to_bell, the format
+ * reference perform_cuSPARSE_BlockSpMM hands to cusparseSpMM,
+ * src/spmm_cusparse.cu:181-445), on the matrix cores.  d_colind is
+ * [ceil(M/bsize)][ell_blocks], d_values [ceil(M/bsize)*bsize][ell_blocks*bsize]
+ * (fp16 or bf16, 16-byte aligned), B K x N row-major (same dtype, 16-byte
+ * aligned), C M x N fp32, every row written (beta = 0).  bsize 32 or 64,
+ * N % 8 == 0.  Stream-ordered, deterministic.  The reference times
+ * cusparseSpMM on this format; this is its replacement. */
+int tca_bell_spmm(const int32_t* d_colind, const void* d_values, int32_t M, int32_t K, int32_t N, int32_t bsize,
+                  int32_t ell_blocks, int32_t dtype, const void* d_B, float* d_C, void* stream);
+
 int tca_spmm_plan_info(const tca_spmm_plan* plan, tca_plan_info* info);
 
 int tca_spmm_plan_destroy(tca_spmm_plan* plan);

@@ -20,6 +20,10 @@ Each function names the reference lines it restates.  How each is pinned
   closed form), closed forms (identity, permutation, all-ones rows), scipy
   fixtures and dense brute force.
 * ``compare_mat``      -- hand-built cases for each branch of the verdict.
+* ``dense_to_bell`` / ``bell_to_dense`` -- the round trip
+  ``bell_to_dense(dense_to_bell(D)) == D`` (padded), hand-built cases (a
+  block row with no blocks, zero-valued entries, ragged M and K), and the
+  block lists against a brute-force scan of every block.
 """
 from __future__ import annotations
 
@@ -195,6 +199,54 @@ def dense_spmm(a, b, threads: int = 0) -> np.ndarray:
     lib.oracle_dense_spmm_f32(_ptr(aa, ctypes.c_float), _ptr(bb, ctypes.c_float),
                               _ptr(c, ctypes.c_float), m, n, k, threads)
     return c
+
+
+def dense_to_bell(dense: np.ndarray, bsize: int):
+    """Blocked-ELL of a dense M x K matrix as the reference builds it for
+    cusparseCreateBlockedEll (src/spmm_cusparse.cu:201-342): M and K are
+    padded to multiples of bsize (:201-211); a block counts the nonzero
+    values in it (:261-269); block row i lists, ascending, the block columns
+    with a nonzero count, padded with -1 to the longest list (:281-309);
+    values[r][e * bsize + c] = A[r][colind[r / bsize][e] * bsize + c], zero
+    for padding blocks (:311-332).  Returns (colind, values)."""
+    m, k = dense.shape
+    brows, bcols = -(-m // bsize), -(-k // bsize)
+    pad = np.zeros((brows * bsize, bcols * bsize), dense.dtype)
+    pad[:m, :k] = dense
+    counts = [[int(np.count_nonzero(pad[i * bsize:(i + 1) * bsize, j * bsize:(j + 1) * bsize]
+                                    .astype(np.float32)))
+               for j in range(bcols)] for i in range(brows)]
+    width = max([sum(1 for x in row if x > 0) for row in counts] + [0])
+    colind = np.full((brows, width), -1, np.int32)
+    for i in range(brows):
+        e = 0
+        for j in range(bcols):
+            if counts[i][j] > 0:
+                colind[i, e] = j
+                e += 1
+    values = np.zeros((brows * bsize, width * bsize), dense.dtype)
+    for i in range(brows):
+        for e in range(width):
+            j = colind[i, e]
+            if j >= 0:
+                values[i * bsize:(i + 1) * bsize, e * bsize:(e + 1) * bsize] = \
+                    pad[i * bsize:(i + 1) * bsize, j * bsize:(j + 1) * bsize]
+    return colind, values
+
+
+def bell_to_dense(colind: np.ndarray, values: np.ndarray, bsize: int, k: int) -> np.ndarray:
+    """Dense (block-padded rows) x K matrix of a Blocked-ELL (the inverse of
+    dense_to_bell; -1 blocks hold nothing)."""
+    brows, width = colind.shape
+    bcols = -(-k // bsize)
+    out = np.zeros((brows * bsize, bcols * bsize), values.dtype)
+    for i in range(brows):
+        for e in range(width):
+            j = colind[i, e]
+            if j >= 0:
+                out[i * bsize:(i + 1) * bsize, j * bsize:(j + 1) * bsize] = \
+                    values[i * bsize:(i + 1) * bsize, e * bsize:(e + 1) * bsize]
+    return out[:, :k]
 
 
 def compare_mat(gold, cmp, tol: float = 1e-3):

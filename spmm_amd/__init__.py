@@ -26,7 +26,7 @@ from ._lib import (TCA_BF16, TCA_F16, TCA_F32, TCA_PLAN_DEFAULT, TCA_PLAN_FORCE_
 
 __all__ = ["CSR", "Plan", "TcaError", "TCA_F16", "TCA_F32", "TCA_BF16", "TCA_PLAN_DEFAULT", "TCA_PLAN_NO_MFMA",
            "TCA_PLAN_FORCE_MFMA", "TCA_PLAN_MFMA_REGS", "TCA_PLAN_MFMA_DMA", "TCA_PLAN_MFMA_DENSE", "read_smtx", "read_smtx_dense", "write_smtx", "read_mtx", "write_values", "write_csr_binary",
-           "read_csr_binary", "launch_floor", "dense_to_csr",
+           "read_csr_binary", "launch_floor", "dense_to_csr", "csr_to_bell", "bell_spmm",
            "csr_to_dense", "compare_mat", "gen_config", "gen_dense", "gen_bernoulli", "gen_lognormal_rows",
            "gen_rmat", "gen_zipf_rows", "naive_csr_spmm", "plan_row_tasks", "plan_mfma_windows", "our_spmm_balanced", "condense_windows", "np_dtype",
            "to_storage", "from_storage"]
@@ -161,6 +161,32 @@ def read_mtx(path: str, pattern_only: bool = False, zero_based: bool = False, dt
     s = _lib.TcaCsr()
     call("tca_mtx_read_csr", path.encode(), int(pattern_only), int(zero_based), dtype, ctypes.byref(s))
     return CSR.from_struct(s)
+
+
+def csr_to_bell(a: CSR, bsize: int):
+    """Blocked-ELL of A (tca_csr_to_bell): (colind [brows, ell_blocks] int32,
+    values [brows * bsize, ell_blocks * bsize] in A's storage dtype)."""
+    rp = np.ascontiguousarray(a.rowptr, np.int32)
+    ci = np.ascontiguousarray(a.colidx, np.int32)
+    v = np.ascontiguousarray(a.values)
+    eb = ctypes.c_int32()
+    call("tca_csr_to_bell", np_ptr(rp, ctypes.c_int32), np_ptr(ci, ctypes.c_int32), v.ctypes.data_as(ctypes.c_void_p),
+         a.nrow, a.ncol, a.nnz, a.dtype, bsize, ctypes.byref(eb), None, None)
+    brows = (a.nrow + bsize - 1) // bsize
+    colind = np.zeros((brows, eb.value), np.int32)
+    vals = np.zeros((brows * bsize, eb.value * bsize), v.dtype)
+    call("tca_csr_to_bell", np_ptr(rp, ctypes.c_int32), np_ptr(ci, ctypes.c_int32), v.ctypes.data_as(ctypes.c_void_p),
+         a.nrow, a.ncol, a.nnz, a.dtype, bsize, ctypes.byref(eb), np_ptr(colind, ctypes.c_int32),
+         vals.ctypes.data_as(ctypes.c_void_p))
+    return colind, vals
+
+
+def bell_spmm(colind, values, m: int, k: int, n: int, bsize: int, dtype: int, b, c, stream=None) -> None:
+    """C = A * B for a Blocked-ELL A on the device (tca_bell_spmm); colind,
+    values, b, c are torch tensors or device addresses."""
+    ell_blocks = int(colind.shape[1]) if hasattr(colind, "shape") else 0
+    call("tca_bell_spmm", _addr(colind), _addr(values), m, k, n, bsize, ell_blocks, dtype, _addr(b), _addr(c),
+         _addr(stream) if stream is not None else None)
 
 
 def dense_to_csr(dense: np.ndarray, dtype: int) -> CSR:

@@ -76,6 +76,7 @@ SIGNATURES = {
     "tca_sddmm": (i32, [vp, vp, vp, vp, vp]),
     "tca_launch_floor": (i32, [vp, i32, f32p]),
     "tca_gather_values": (i32, [vp, i32, vp, i32, vp, vp]),
+    "tca_bell_spmm": (i32, [vp, vp, i32, i32, i32, i32, i32, i32, vp, vp, vp]),
     "tca_spmm_plan_info": (i32, [vp, ctypes.POINTER(TcaPlanInfo)]),
     "tca_spmm_plan_destroy": (i32, [vp]),
     "tca_spmm_host": (i32, [i32p, i32p, vp, i32, i32, i32, vp, f32p, i32, i32, i32, i32,
@@ -108,6 +109,7 @@ SIGNATURES = {
     "tca_coo_to_csr": (i32, [ctypes.POINTER(TcaCoo), ctypes.POINTER(TcaCsr)]),
     "tca_csr_transpose": (i32, [i32p, i32p, i32, i32, i32, i32p, i32p, i32p]),
     "tca_csr_convert": (i32, [ctypes.POINTER(TcaCsr), i32, ctypes.POINTER(TcaCsr)]),
+    "tca_csr_to_bell": (i32, [i32p, i32p, vp, i32, i32, i32, i32, i32, i32p, i32p, vp]),
     "tca_f32_to_f16": (ctypes.c_uint16, [ctypes.c_float]),
     "tca_f16_to_f32": (ctypes.c_float, [ctypes.c_uint16]),
     "tca_f32_to_bf16": (ctypes.c_uint16, [ctypes.c_float]),

@@ -262,6 +262,57 @@ int tca_csr_convert(const tca_csr* a, int32_t dtype, tca_csr* out) {
     return TCA_OK;
 }
 
+int tca_csr_to_bell(const int32_t* rowptr, const int32_t* colidx, const void* values, int32_t M, int32_t K,
+                    int32_t nnz, int32_t dtype, int32_t bsize, int32_t* ell_blocks, int32_t* colind,
+                    void* ell_values) {
+    if (!rowptr || (nnz > 0 && (!colidx || !values)) || !ell_blocks || M < 0 || K < 1 || nnz < 0 ||
+        !dtype_ok(dtype) || bsize < 1 || ((colind == nullptr) != (ell_values == nullptr)))
+        return fail(TCA_ERR_INVALID, "tca_csr_to_bell: bad argument");
+    int st = tca_csr_validate(rowptr, colidx, M, K, nnz);
+    if (st) return st;
+    const int32_t brows = (M + bsize - 1) / bsize;
+    const int32_t bcols = (K + bsize - 1) / bsize;
+    // Block columns holding a nonzero value, per block row, ascending.
+    std::vector<std::vector<int32_t>> blocks(brows);
+#pragma omp parallel for schedule(dynamic, 16)
+    for (int32_t i = 0; i < brows; i++) {
+        std::vector<uint8_t> seen(bcols, 0);
+        const int32_t r1 = std::min<int64_t>(M, static_cast<int64_t>(i + 1) * bsize);
+        for (int32_t j = rowptr[static_cast<int64_t>(i) * bsize]; j < rowptr[r1]; j++)
+            if (load_as_f32(values, dtype, j) != 0.0f) seen[colidx[j] / bsize] = 1;
+        for (int32_t b = 0; b < bcols; b++)
+            if (seen[b]) blocks[i].push_back(b);
+    }
+    int32_t width = 0;
+    for (const auto& b : blocks) width = std::max<int32_t>(width, static_cast<int32_t>(b.size()));
+    *ell_blocks = width;
+    if (!colind) return TCA_OK;
+    const size_t es = dtype_size(dtype);
+    const int64_t ecols = static_cast<int64_t>(width) * bsize;
+    std::memset(ell_values, 0, static_cast<size_t>(brows) * bsize * ecols * es);
+#pragma omp parallel for schedule(dynamic, 16)
+    for (int32_t i = 0; i < brows; i++) {
+        // slot of each present block column in this block row
+        std::vector<int32_t> slot(bcols, -1);
+        for (int32_t e = 0; e < width; e++) {
+            const int32_t b = e < static_cast<int32_t>(blocks[i].size()) ? blocks[i][e] : -1;
+            colind[static_cast<int64_t>(i) * width + e] = b;
+            if (b >= 0) slot[b] = e;
+        }
+        const int32_t r1 = std::min<int64_t>(M, static_cast<int64_t>(i + 1) * bsize);
+        for (int32_t r = i * bsize; r < r1; r++)
+            for (int32_t j = rowptr[r]; j < rowptr[r + 1]; j++) {
+                const int32_t c = colidx[j];
+                const int32_t e = slot[c / bsize];
+                if (e < 0) continue;  // a block of zeros only
+                std::memcpy(static_cast<char*>(ell_values) +
+                                (static_cast<size_t>(r) * ecols + static_cast<size_t>(e) * bsize + c % bsize) * es,
+                            static_cast<const char*>(values) + static_cast<size_t>(j) * es, es);
+            }
+    }
+    return TCA_OK;
+}
+
 int tca_compare_mat(const float* gold, const float* cmp, int64_t n, float tol, float floor,
                     int32_t verbose, tca_compare_result* res) {
     if (!gold || !cmp || !res || n < 0) return fail(TCA_ERR_INVALID, "tca_compare_mat: bad argument");

@@ -15,6 +15,7 @@
 #include "mfma_dma_kernel.hpp"
 #include "mfma_pair_kernel.hpp"
 #include "mfma_dense_kernel.hpp"
+#include "bell_kernel.hpp"
 #include "sddmm_kernel.hpp"
 
 using namespace tca;
@@ -618,6 +619,49 @@ int tca_sddmm(const tca_spmm_plan* p, const float* d_G, const void* d_B, float* 
         default:
             hipLaunchKernelGGL(sddmm_kernel<float>, grid, block, 0, s, p->d_rowptr, p->d_colidx, p->M, p->N, d_G,
                                static_cast<const float*>(d_B), d_out);
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(TCA_ERR_HIP, "kernel launch: %s", hipGetErrorString(e));
+    return TCA_OK;
+}
+
+int tca_bell_spmm(const int32_t* d_colind, const void* d_values, int32_t M, int32_t K, int32_t N, int32_t bsize,
+                  int32_t ell_blocks, int32_t dtype, const void* d_B, float* d_C, void* stream) {
+    if (M < 0 || K < 1 || N < 1 || ell_blocks < 0)
+        return fail(TCA_ERR_INVALID, "tca_bell_spmm: bad shape M=%d K=%d N=%d ell_blocks=%d", M, K, N, ell_blocks);
+    if (bsize != 32 && bsize != 64) return fail(TCA_ERR_UNSUPPORTED, "tca_bell_spmm: block size %d (32 or 64)", bsize);
+    if (dtype != TCA_F16 && dtype != TCA_BF16) return fail(TCA_ERR_UNSUPPORTED, "tca_bell_spmm: fp16 / bf16 values only");
+    if (N % 8 != 0) return fail(TCA_ERR_UNSUPPORTED, "tca_bell_spmm: N %% 8 != 0");
+    // B is addressed through 32-bit buffer offsets, rows up to the block-padded K.
+    if ((static_cast<uint64_t>(K) + bsize) * static_cast<uint64_t>(N) * 2 >= 0xfffffff0ull)
+        return fail(TCA_ERR_UNSUPPORTED, "tca_bell_spmm: B exceeds the 4 GiB buffer range");
+    if (M == 0) return TCA_OK;
+    if (!d_B || !d_C || (ell_blocks > 0 && (!d_colind || !d_values)))
+        return fail(TCA_ERR_INVALID, "tca_bell_spmm: NULL device pointer");
+    if (reinterpret_cast<uintptr_t>(d_B) % 16 || reinterpret_cast<uintptr_t>(d_values) % 16 ||
+        reinterpret_cast<uintptr_t>(d_C) % 4)
+        return fail(TCA_ERR_INVALID, "tca_bell_spmm: B and values must be 16-byte aligned, C 4-byte");
+    BellArgs a;
+    a.colind = d_colind;
+    a.values = d_values;
+    a.B = d_B;
+    a.C = d_C;
+    a.M = M;
+    a.N = N;
+    a.ell_blocks = ell_blocks;
+    a.col_groups = (N + kBellCols - 1) / kBellCols;
+    a.B_bytes = static_cast<uint32_t>(static_cast<uint64_t>(K) * N * 2);
+    const int64_t brows = (static_cast<int64_t>(M) + bsize - 1) / bsize;
+    if (brows * a.col_groups > 0x7fffffff) return fail(TCA_ERR_UNSUPPORTED, "tca_bell_spmm: grid too large");
+    const dim3 grid(static_cast<unsigned>(brows * a.col_groups));
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const bool bf = dtype == TCA_BF16;
+    if (bsize == 32) {
+        if (bf) hipLaunchKernelGGL((bell_mfma_kernel<true, 32>), grid, dim3(kBellThreads), 0, s, a);
+        else hipLaunchKernelGGL((bell_mfma_kernel<false, 32>), grid, dim3(kBellThreads), 0, s, a);
+    } else {
+        if (bf) hipLaunchKernelGGL((bell_mfma_kernel<true, 64>), grid, dim3(kBellThreads), 0, s, a);
+        else hipLaunchKernelGGL((bell_mfma_kernel<false, 64>), grid, dim3(kBellThreads), 0, s, a);
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(TCA_ERR_HIP, "kernel launch: %s", hipGetErrorString(e));
