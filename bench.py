@@ -75,6 +75,8 @@ def main():
     ap.add_argument("--bell", type=int, default=0, metavar="BS",
                     help="time the Blocked-ELL kernel (tca_bell_spmm) on A converted to blocks of BS x BS "
                          "instead of the CSR plan (fp16 / bf16 configurations)")
+    ap.add_argument("--sparse24", action="store_true",
+                    help="time the 2:4 sparse-MFMA kernel (tca_spmm_24) on A pruned to 2:4 (fp16 / bf16 configurations)")
     ap.add_argument("--traffic-kib", type=float, nargs=2, default=None, metavar=("FETCH", "WRITE"),
                     help="measured FETCH_SIZE and WRITE_SIZE of the dominant kernel per launch, already scaled "
                          "by the copy calibration (KiB); reported as roofline.traffic in bytes")
@@ -108,6 +110,9 @@ def main():
     c = torch.empty((a.nrow, n), dtype=torch.float32, device=dev)
     if args.bell:
         bell(args, a, n, bd, c, dev_tensor)
+        return
+    if args.sparse24:
+        sparse24(args, a, n, bd, c, dev_tensor)
         return
     plan = S.Plan(a, n, args.flags)
     info = plan.info()
@@ -283,6 +288,60 @@ def bell(args, a, n, bd, c, dev_tensor):
                      "kernel_us": round(ms * 1e3, 3), "achieved": round(bytes_alg / (ms * 1e-3) / 1e9, 2),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(bytes_alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 5),
                      "traffic": None, "format_bytes_gbs": round(bytes_fmt / (ms * 1e-3) / 1e9, 2)},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(out), flush=True)
+
+
+def _time_launches(run, warmup, steps):
+    import torch
+    for _ in range(warmup):
+        run()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(steps):
+        run()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def sparse24(args, a, n, bd, c, dev_tensor):
+    """The 2:4 sparse-MFMA kernel on the configuration's A pruned to 2:4 (one JSON line)."""
+    import torch
+
+    import spmm_amd as S
+
+    t0 = time.perf_counter()
+    p = S.prune_24(a)
+    vals, meta = S.csr_to_24(p)
+    conv_ms = (time.perf_counter() - t0) * 1e3
+    dv, dm = dev_tensor(vals), dev_tensor(meta)
+    m, k, nnz = p.nrow, p.ncol, p.nnz
+    log(f"2:4: {a.nnz - nnz} of {a.nnz} nonzeros pruned, {vals.nbytes / 1e6:.1f} MB compressed, "
+        f"prune + compress {conv_ms:.1f} ms")
+    stream = torch.cuda.current_stream()
+    ms = _time_launches(lambda: S.spmm_24(dv, dm, m, k, n, p.dtype, bd, c, stream=stream.cuda_stream),
+                        args.warmup, args.steps)
+    if not torch.isfinite(c).all().item():
+        sys.exit("non-finite output")
+    bytes_alg = 4 * (m + 1) + nnz * 6 + k * n * 2 + m * n * 4
+    kp = (k + 63) // 64 * 64
+    dense_flops = 2.0 * m * kp * n  # the dense product the sparse matrix cores stand in for
+    out = {
+        "metric": METRIC, "value": round(2.0 * nnz * n / (ms * 1e-3) / 1e9, 3), "unit": "GFLOP/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 6), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None,
+        "dtype": ("f16" if p.dtype == S.TCA_F16 else "bf16") + "->f32acc",
+        "data": "synthetic (seeded generators, seed %d)" % args.seed,
+        "config": {"workload": WORKLOADS[args.config] + ", A pruned to 2:4", "M": m, "K": k, "N": n, "nnz": nnz,
+                   "nnz_before_pruning": a.nnz, "bytes_alg": bytes_alg, "prune_compress_ms": round(conv_ms, 3),
+                   "dense_equivalent_tflops": round(dense_flops / (ms * 1e-3) / 1e12, 2)},
+        "roofline": {"bound": "mfma", "kernel": "sparse24_kernel", "kernel_us": round(ms * 1e3, 3),
+                     "achieved": round(dense_flops / 2 / (ms * 1e-3) / 1e12, 2), "peak": 2500.0, "unit": "TFLOP/s",
+                     "frac": round(dense_flops / 2 / (ms * 1e-3) / 1e12 / 2500.0, 5), "traffic": None},
         "cpu_baseline": None,
     }
     print(json.dumps(out), flush=True)

@@ -135,6 +135,32 @@ int tca_csr_to_bell(const int32_t* rowptr, const int32_t* colidx, const void* va
                     int32_t nnz, int32_t dtype, int32_t bsize, int32_t* ell_blocks, int32_t* colind,
                     void* ell_values);
 
+/* 2:4 structured sparsity, the format of reference
+ * perform_cuSPARSELT_24sparsity (src/spmm_cusparse.cu:2-179), which prunes A
+ * with cusparseLtSpMMAPrune(CUSPARSELT_PRUNE_SPMMA_STRIP) and multiplies the
+ * compressed A.  Groups are 4 consecutive columns of a row (columns
+ * 4g .. 4g + 3).
+ *
+ * tca_prune_24: the pruned copy of A keeping, in every group, the two
+ * entries of largest |value| (STRIP: the kept pair maximises the group's L1
+ * norm); equal magnitudes keep the lower column.  Entries whose value is
+ * zero are dropped first.  out's arrays are allocated by the library (free
+ * with tca_csr_free).
+ *
+ * tca_csr_to_24: compression of a 2:4 matrix (at most two nonzeros per
+ * group, else TCA_ERR_INVALID).  Kp = K rounded up to a multiple of 64.
+ * vals24 is [M][Kp / 2] of dtype, meta24 [M][Kp / 16] uint16: word q of row
+ * r describes columns 16 q .. 16 q + 15 as 4 groups G; bits 4G .. 4G + 1
+ * give the position (0..3) inside group G of the value at
+ * vals24[r][8 q + 2 G], bits 4G + 2 .. 4G + 3 that of vals24[r][8 q + 2 G + 1];
+ * the positions of a group are ascending and distinct, unused values zero.
+ * This is the operand layout of gfx950's v_smfmac_f32_16x16x64 (a lane reads
+ * one 16-byte run of vals24 and one meta word). */
+int tca_prune_24(const int32_t* rowptr, const int32_t* colidx, const void* values, int32_t M, int32_t K,
+                 int32_t nnz, int32_t dtype, tca_csr* out);
+int tca_csr_to_24(const int32_t* rowptr, const int32_t* colidx, const void* values, int32_t M, int32_t K,
+                  int32_t nnz, int32_t dtype, void* vals24, uint16_t* meta24);
+
 /* ---- scalar conversion (IEEE binary16 / bfloat16, round to nearest even) ---- */
 uint16_t tca_f32_to_f16(float x);
 float tca_f16_to_f32(uint16_t h);

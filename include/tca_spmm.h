@@ -150,6 +150,16 @@ int tca_gather_values(const int32_t* d_perm, int32_t n, const void* d_val, int32
 int tca_bell_spmm(const int32_t* d_colind, const void* d_values, int32_t M, int32_t K, int32_t N, int32_t bsize,
                   int32_t ell_blocks, int32_t dtype, const void* d_B, float* d_C, void* stream);
 
+/* C = A * B with A in compressed 2:4 form (layout of tca_csr_to_24; the
+ * format reference perform_cuSPARSELT_24sparsity multiplies with
+ * cusparseLtMatmul, src/spmm_cusparse.cu:2-179) on gfx950's sparse matrix
+ * cores (v_smfmac_f32_16x16x64).  d_vals [M][Kp/2] and B (K x N row-major)
+ * fp16 or bf16, 16-byte aligned; d_meta [M][Kp/16] uint16; C M x N fp32,
+ * every row written (beta = 0; the reference writes fp16 C).  Kp = K rounded
+ * up to 64; N % 8 == 0.  Stream-ordered, deterministic. */
+int tca_spmm_24(const void* d_vals, const uint16_t* d_meta, int32_t M, int32_t K, int32_t N, int32_t dtype,
+                const void* d_B, float* d_C, void* stream);
+
 int tca_spmm_plan_info(const tca_spmm_plan* plan, tca_plan_info* info);
 
 int tca_spmm_plan_destroy(tca_spmm_plan* plan);

@@ -24,6 +24,11 @@ Each function names the reference lines it restates.  How each is pinned
   ``bell_to_dense(dense_to_bell(D)) == D`` (padded), hand-built cases (a
   block row with no blocks, zero-valued entries, ragged M and K), and the
   block lists against a brute-force scan of every block.
+* ``prune_24`` / ``decompress_24`` -- the kept pair of every group against
+  a brute-force search of the six pairs for the largest L1 norm (lowest
+  columns on ties); ``decompress_24(compress(P)) == P`` and hand-built index
+  words.  cuSPARSELt (the reference's library for this step) is not present;
+  its documented STRIP rule is restated, its tie order is not pinned.
 """
 from __future__ import annotations
 
@@ -246,6 +251,43 @@ def bell_to_dense(colind: np.ndarray, values: np.ndarray, bsize: int, k: int) ->
             if j >= 0:
                 out[i * bsize:(i + 1) * bsize, j * bsize:(j + 1) * bsize] = \
                     values[i * bsize:(i + 1) * bsize, e * bsize:(e + 1) * bsize]
+    return out[:, :k]
+
+
+def prune_24(dense: np.ndarray) -> np.ndarray:
+    """2:4 pruning of a dense M x K matrix along its rows as the reference
+    requests it from cusparseLtSpMMAPrune(CUSPARSELT_PRUNE_SPMMA_STRIP)
+    (src/spmm_cusparse.cu:83-84): in every group of 4 consecutive columns
+    keep the two entries of largest magnitude (the pair with the largest L1
+    norm), zero the others; equal magnitudes keep the lower column."""
+    out = np.zeros_like(dense)
+    m, k = dense.shape
+    for r in range(m):
+        for g0 in range(0, k, 4):
+            grp = dense[r, g0:g0 + 4].astype(np.float32)
+            order = sorted((i for i in range(len(grp)) if grp[i] != 0), key=lambda i: (-abs(grp[i]), i))
+            for i in order[:2]:
+                out[r, g0 + i] = dense[r, g0 + i]
+    return out
+
+
+def decompress_24(vals: np.ndarray, meta: np.ndarray, k: int) -> np.ndarray:
+    """Dense M x K matrix of a compressed 2:4 A (vals [M, Kp/2], meta
+    [M, Kp/16]; word q covers columns 16 q .. 16 q + 15, group G's two
+    values at vals[8 q + 2 G], [8 q + 2 G + 1] sit at positions bits
+    4G..4G+1 and 4G+2..4G+3)."""
+    m = vals.shape[0]
+    kp = meta.shape[1] * 16
+    out = np.zeros((m, kp), vals.dtype)
+    for r in range(m):
+        for q in range(meta.shape[1]):
+            w = int(meta[r, q])
+            for g in range(4):
+                for s in range(2):
+                    pos = (w >> (4 * g + 2 * s)) & 3
+                    v = vals[r, 8 * q + 2 * g + s]
+                    if v != 0:
+                        out[r, 16 * q + 4 * g + pos] = v
     return out[:, :k]
 
 

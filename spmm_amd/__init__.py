@@ -26,7 +26,7 @@ from ._lib import (TCA_BF16, TCA_F16, TCA_F32, TCA_PLAN_DEFAULT, TCA_PLAN_FORCE_
 
 __all__ = ["CSR", "Plan", "TcaError", "TCA_F16", "TCA_F32", "TCA_BF16", "TCA_PLAN_DEFAULT", "TCA_PLAN_NO_MFMA",
            "TCA_PLAN_FORCE_MFMA", "TCA_PLAN_MFMA_REGS", "TCA_PLAN_MFMA_DMA", "TCA_PLAN_MFMA_DENSE", "read_smtx", "read_smtx_dense", "write_smtx", "read_mtx", "write_values", "write_csr_binary",
-           "read_csr_binary", "launch_floor", "dense_to_csr", "csr_to_bell", "bell_spmm",
+           "read_csr_binary", "launch_floor", "dense_to_csr", "csr_to_bell", "bell_spmm", "prune_24", "csr_to_24", "spmm_24",
            "csr_to_dense", "compare_mat", "gen_config", "gen_dense", "gen_bernoulli", "gen_lognormal_rows",
            "gen_rmat", "gen_zipf_rows", "naive_csr_spmm", "plan_row_tasks", "plan_mfma_windows", "our_spmm_balanced", "condense_windows", "np_dtype",
            "to_storage", "from_storage"]
@@ -186,6 +186,38 @@ def bell_spmm(colind, values, m: int, k: int, n: int, bsize: int, dtype: int, b,
     values, b, c are torch tensors or device addresses."""
     ell_blocks = int(colind.shape[1]) if hasattr(colind, "shape") else 0
     call("tca_bell_spmm", _addr(colind), _addr(values), m, k, n, bsize, ell_blocks, dtype, _addr(b), _addr(c),
+         _addr(stream) if stream is not None else None)
+
+
+def prune_24(a: CSR) -> CSR:
+    """A pruned to 2:4 along its rows (tca_prune_24: the two largest |value|
+    of every 4 consecutive columns, lower column on ties)."""
+    rp = np.ascontiguousarray(a.rowptr, np.int32)
+    ci = np.ascontiguousarray(a.colidx, np.int32)
+    v = np.ascontiguousarray(a.values)
+    s = _lib.TcaCsr()
+    call("tca_prune_24", np_ptr(rp, ctypes.c_int32), np_ptr(ci, ctypes.c_int32), v.ctypes.data_as(ctypes.c_void_p),
+         a.nrow, a.ncol, a.nnz, a.dtype, ctypes.byref(s))
+    return CSR.from_struct(s)
+
+
+def csr_to_24(a: CSR):
+    """Compressed 2:4 form of a 2:4 matrix (tca_csr_to_24): (vals [M, Kp/2]
+    uint16 storage, meta [M, Kp/16] uint16), Kp = K rounded up to 64."""
+    rp = np.ascontiguousarray(a.rowptr, np.int32)
+    ci = np.ascontiguousarray(a.colidx, np.int32)
+    v = np.ascontiguousarray(a.values)
+    kp = (a.ncol + 63) // 64 * 64
+    vals = np.zeros((a.nrow, kp // 2), np.uint16)
+    meta = np.zeros((a.nrow, kp // 16), np.uint16)
+    call("tca_csr_to_24", np_ptr(rp, ctypes.c_int32), np_ptr(ci, ctypes.c_int32), v.ctypes.data_as(ctypes.c_void_p),
+         a.nrow, a.ncol, a.nnz, a.dtype, vals.ctypes.data_as(ctypes.c_void_p), meta.ctypes.data_as(ctypes.c_void_p))
+    return vals, meta
+
+
+def spmm_24(vals, meta, m: int, k: int, n: int, dtype: int, b, c, stream=None) -> None:
+    """C = A * B for a compressed 2:4 A on the device (tca_spmm_24)."""
+    call("tca_spmm_24", _addr(vals), _addr(meta), m, k, n, dtype, _addr(b), _addr(c),
          _addr(stream) if stream is not None else None)
 
 

@@ -77,6 +77,7 @@ SIGNATURES = {
     "tca_launch_floor": (i32, [vp, i32, f32p]),
     "tca_gather_values": (i32, [vp, i32, vp, i32, vp, vp]),
     "tca_bell_spmm": (i32, [vp, vp, i32, i32, i32, i32, i32, i32, vp, vp, vp]),
+    "tca_spmm_24": (i32, [vp, vp, i32, i32, i32, i32, vp, vp, vp]),
     "tca_spmm_plan_info": (i32, [vp, ctypes.POINTER(TcaPlanInfo)]),
     "tca_spmm_plan_destroy": (i32, [vp]),
     "tca_spmm_host": (i32, [i32p, i32p, vp, i32, i32, i32, vp, f32p, i32, i32, i32, i32,
@@ -110,6 +111,8 @@ SIGNATURES = {
     "tca_csr_transpose": (i32, [i32p, i32p, i32, i32, i32, i32p, i32p, i32p]),
     "tca_csr_convert": (i32, [ctypes.POINTER(TcaCsr), i32, ctypes.POINTER(TcaCsr)]),
     "tca_csr_to_bell": (i32, [i32p, i32p, vp, i32, i32, i32, i32, i32, i32p, i32p, vp]),
+    "tca_prune_24": (i32, [i32p, i32p, vp, i32, i32, i32, i32, ctypes.POINTER(TcaCsr)]),
+    "tca_csr_to_24": (i32, [i32p, i32p, vp, i32, i32, i32, i32, vp, vp]),
     "tca_f32_to_f16": (ctypes.c_uint16, [ctypes.c_float]),
     "tca_f16_to_f32": (ctypes.c_float, [ctypes.c_uint16]),
     "tca_f32_to_bf16": (ctypes.c_uint16, [ctypes.c_float]),

@@ -313,6 +313,108 @@ int tca_csr_to_bell(const int32_t* rowptr, const int32_t* colidx, const void* va
     return TCA_OK;
 }
 
+int tca_prune_24(const int32_t* rowptr, const int32_t* colidx, const void* values, int32_t M, int32_t K,
+                 int32_t nnz, int32_t dtype, tca_csr* out) {
+    if (!rowptr || (nnz > 0 && (!colidx || !values)) || !out || M < 0 || K < 1 || nnz < 0 || !dtype_ok(dtype))
+        return fail(TCA_ERR_INVALID, "tca_prune_24: bad argument");
+    int st = tca_csr_validate(rowptr, colidx, M, K, nnz);
+    if (st) return st;
+    // keep[j]: entry j survives.  Columns ascend within a row, so a group's
+    // entries are consecutive.
+    std::vector<uint8_t> keep(static_cast<size_t>(nnz), 0);
+    std::vector<int32_t> cnt(static_cast<size_t>(M) + 1, 0);
+#pragma omp parallel for schedule(dynamic, 64)
+    for (int32_t r = 0; r < M; r++) {
+        int32_t j = rowptr[r];
+        while (j < rowptr[r + 1]) {
+            int32_t e = j;
+            while (e < rowptr[r + 1] && colidx[e] / 4 == colidx[j] / 4) e++;
+            // the two largest |value| of entries j .. e - 1 (nonzero only), lower column first on ties
+            int32_t b0 = -1, b1 = -1;
+            for (int32_t x = j; x < e; x++) {
+                const float v = std::fabs(load_as_f32(values, dtype, x));
+                if (!(v > 0.0f)) continue;
+                if (b0 < 0 || v > std::fabs(load_as_f32(values, dtype, b0))) {
+                    b1 = b0;
+                    b0 = x;
+                } else if (b1 < 0 || v > std::fabs(load_as_f32(values, dtype, b1))) {
+                    b1 = x;
+                }
+            }
+            if (b0 >= 0) keep[b0] = 1;
+            if (b1 >= 0) keep[b1] = 1;
+            j = e;
+        }
+        int32_t c = 0;
+        for (int32_t x = rowptr[r]; x < rowptr[r + 1]; x++) c += keep[x];
+        cnt[r + 1] = c;
+    }
+    for (int32_t r = 0; r < M; r++) cnt[r + 1] += cnt[r];
+    st = alloc_csr(out, M, K, cnt[M], dtype);
+    if (st) return st;
+    const size_t es = dtype_size(dtype);
+    std::copy(cnt.begin(), cnt.end(), out->row_offset);
+    for (int32_t r = 0, t = 0; r < M; r++)
+        for (int32_t x = rowptr[r]; x < rowptr[r + 1]; x++)
+            if (keep[x]) {
+                out->col_idx[t] = colidx[x];
+                std::memcpy(static_cast<char*>(out->value) + static_cast<size_t>(t) * es,
+                            static_cast<const char*>(values) + static_cast<size_t>(x) * es, es);
+                t++;
+            }
+    return TCA_OK;
+}
+
+int tca_csr_to_24(const int32_t* rowptr, const int32_t* colidx, const void* values, int32_t M, int32_t K,
+                  int32_t nnz, int32_t dtype, void* vals24, uint16_t* meta24) {
+    if (!rowptr || (nnz > 0 && (!colidx || !values)) || M < 0 || K < 1 || nnz < 0 ||
+        (dtype != TCA_F16 && dtype != TCA_BF16) || (M > 0 && (!vals24 || !meta24)))
+        return fail(TCA_ERR_INVALID, "tca_csr_to_24: bad argument (fp16 / bf16 values)");
+    int st = tca_csr_validate(rowptr, colidx, M, K, nnz);
+    if (st) return st;
+    const int64_t kp = (static_cast<int64_t>(K) + 63) / 64 * 64;
+    const int64_t vcols = kp / 2, mcols = kp / 16;
+    uint16_t* const v16 = static_cast<uint16_t*>(vals24);
+    const uint16_t* const src = static_cast<const uint16_t*>(values);
+    int bad = -1;
+#pragma omp parallel for schedule(dynamic, 64)
+    for (int32_t r = 0; r < M; r++) {
+        uint16_t* vr = v16 + static_cast<size_t>(r) * vcols;
+        uint16_t* mr = meta24 + static_cast<size_t>(r) * mcols;
+        std::fill(vr, vr + vcols, uint16_t(0));
+        // unused pairs: positions 0 and 1 (ascending, distinct), values zero
+        std::fill(mr, mr + mcols, uint16_t(0x4444));
+        int32_t j = rowptr[r];
+        while (j < rowptr[r + 1]) {
+            const int32_t g = colidx[j] / 4;
+            int32_t e = j;
+            while (e < rowptr[r + 1] && colidx[e] / 4 == g) e++;
+            if (e - j > 2) {
+#pragma omp critical
+                bad = r;
+                break;
+            }
+            int32_t p0, p1, x0 = -1, x1 = -1;
+            if (e - j == 2) {
+                p0 = colidx[j] % 4, p1 = colidx[j + 1] % 4, x0 = j, x1 = j + 1;
+            } else {
+                // one entry: pair it with a zero at another position, ascending
+                const int32_t p = colidx[j] % 4;
+                if (p == 3) p0 = 2, p1 = 3, x1 = j;
+                else p0 = p, p1 = p + 1, x0 = j;
+            }
+            const int32_t q = g / 4, G = g % 4;
+            if (x0 >= 0) vr[8 * q + 2 * G] = src[x0];
+            if (x1 >= 0) vr[8 * q + 2 * G + 1] = src[x1];
+            const uint16_t nib = static_cast<uint16_t>(p0 | (p1 << 2));
+            mr[q] = static_cast<uint16_t>((mr[q] & ~(0xf << (4 * G))) | (nib << (4 * G)));
+            j = e;
+        }
+    }
+    if (bad >= 0) return fail(TCA_ERR_INVALID, "tca_csr_to_24: row %d has more than two nonzeros in a group of 4", bad);
+    return TCA_OK;
+}
+
 int tca_compare_mat(const float* gold, const float* cmp, int64_t n, float tol, float floor,
                     int32_t verbose, tca_compare_result* res) {
     if (!gold || !cmp || !res || n < 0) return fail(TCA_ERR_INVALID, "tca_compare_mat: bad argument");

@@ -16,6 +16,7 @@
 #include "mfma_pair_kernel.hpp"
 #include "mfma_dense_kernel.hpp"
 #include "bell_kernel.hpp"
+#include "sparse24_kernel.hpp"
 #include "sddmm_kernel.hpp"
 
 using namespace tca;
@@ -663,6 +664,40 @@ int tca_bell_spmm(const int32_t* d_colind, const void* d_values, int32_t M, int3
         if (bf) hipLaunchKernelGGL((bell_mfma_kernel<true, 64>), grid, dim3(kBellThreads), 0, s, a);
         else hipLaunchKernelGGL((bell_mfma_kernel<false, 64>), grid, dim3(kBellThreads), 0, s, a);
     }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(TCA_ERR_HIP, "kernel launch: %s", hipGetErrorString(e));
+    return TCA_OK;
+}
+
+int tca_spmm_24(const void* d_vals, const uint16_t* d_meta, int32_t M, int32_t K, int32_t N, int32_t dtype,
+                const void* d_B, float* d_C, void* stream) {
+    if (M < 0 || K < 1 || N < 1) return fail(TCA_ERR_INVALID, "tca_spmm_24: bad shape M=%d K=%d N=%d", M, K, N);
+    if (dtype != TCA_F16 && dtype != TCA_BF16) return fail(TCA_ERR_UNSUPPORTED, "tca_spmm_24: fp16 / bf16 values only");
+    if (N % 8 != 0) return fail(TCA_ERR_UNSUPPORTED, "tca_spmm_24: N %% 8 != 0");
+    if ((static_cast<uint64_t>(K) + 64) * static_cast<uint64_t>(N) * 2 >= 0xfffffff0ull)
+        return fail(TCA_ERR_UNSUPPORTED, "tca_spmm_24: B exceeds the 4 GiB buffer range");
+    if (M == 0) return TCA_OK;
+    if (!d_vals || !d_meta || !d_B || !d_C) return fail(TCA_ERR_INVALID, "tca_spmm_24: NULL device pointer");
+    if (reinterpret_cast<uintptr_t>(d_B) % 16 || reinterpret_cast<uintptr_t>(d_vals) % 16 ||
+        reinterpret_cast<uintptr_t>(d_meta) % 2 || reinterpret_cast<uintptr_t>(d_C) % 4)
+        return fail(TCA_ERR_INVALID, "tca_spmm_24: B and vals must be 16-byte aligned, meta 2-byte, C 4-byte");
+    S24Args a;
+    a.vals = d_vals;
+    a.meta = d_meta;
+    a.B = d_B;
+    a.C = d_C;
+    a.M = M;
+    a.N = N;
+    a.Kp = (K + 63) / 64 * 64;
+    a.col_groups = (N + kS24Cols - 1) / kS24Cols;
+    a.B_bytes = static_cast<uint32_t>(static_cast<uint64_t>(K) * N * 2);
+    const int64_t groups = (static_cast<int64_t>(M) + kS24Rows - 1) / kS24Rows * a.col_groups;
+    if (groups > 0x7fffffff) return fail(TCA_ERR_UNSUPPORTED, "tca_spmm_24: grid too large");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (dtype == TCA_BF16)
+        hipLaunchKernelGGL(sparse24_kernel<true>, dim3(static_cast<unsigned>(groups)), dim3(kS24Threads), 0, s, a);
+    else
+        hipLaunchKernelGGL(sparse24_kernel<false>, dim3(static_cast<unsigned>(groups)), dim3(kS24Threads), 0, s, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(TCA_ERR_HIP, "kernel launch: %s", hipGetErrorString(e));
     return TCA_OK;
