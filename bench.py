@@ -75,6 +75,9 @@ def main():
     ap.add_argument("--bell", type=int, default=0, metavar="BS",
                     help="time the Blocked-ELL kernel (tca_bell_spmm) on A converted to blocks of BS x BS "
                          "instead of the CSR plan (fp16 / bf16 configurations)")
+    ap.add_argument("--device-plan", action="store_true",
+                    help="build the plan on the GPU from device-resident CSR arrays (tca_spmm_plan_create_device; "
+                         "row-kernel plans) instead of the host planner")
     ap.add_argument("--sparse24", action="store_true",
                     help="time the 2:4 sparse-MFMA kernel (tca_spmm_24) on A pruned to 2:4 (fp16 / bf16 configurations)")
     ap.add_argument("--traffic-kib", type=float, nargs=2, default=None, metavar=("FETCH", "WRITE"),
@@ -114,7 +117,13 @@ def main():
     if args.sparse24:
         sparse24(args, a, n, bd, c, dev_tensor)
         return
-    plan = S.Plan(a, n, args.flags)
+    if args.device_plan:
+        drp, dci = dev_tensor(a.rowptr), dev_tensor(a.colidx)
+        torch.cuda.synchronize()
+        plan = S.Plan.from_device(drp, dci, a.nrow, a.ncol, a.nnz, n, a.dtype, args.flags,
+                                  stream=torch.cuda.current_stream().cuda_stream)
+    else:
+        plan = S.Plan(a, n, args.flags)
     info = plan.info()
     log("plan:", json.dumps(info))
     stream = torch.cuda.current_stream()

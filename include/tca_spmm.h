@@ -160,6 +160,27 @@ int tca_bell_spmm(const int32_t* d_colind, const void* d_values, int32_t M, int3
 int tca_spmm_24(const void* d_vals, const uint16_t* d_meta, int32_t M, int32_t K, int32_t N, int32_t dtype,
                 const void* d_B, float* d_C, void* stream);
 
+/* Planning on the GPU from a device-resident CSR (d_rowptr [M+1], d_colidx
+ * [nnz], sorted columns), with no host copy of the structure: the plan's
+ * row-kernel task list is built by device kernels (row lengths, a stable
+ * descending radix sort, category bounds, a segment scan, task emission)
+ * and equals the host planner's plan with TCA_PLAN_NO_MFMA, task for task.
+ * The structure is validated on the device (TCA_ERR_INVALID as the host
+ * planner).  Only row-kernel plans: the MFMA flags give TCA_ERR_UNSUPPORTED.
+ * The plan copies the structure; the caller's buffers may be freed after
+ * the call, which synchronises `stream`.  Replaces reference
+ * workload_manager (src/our_spmm.cu:353-477), which plans on the host from
+ * host arrays on every call. */
+int tca_spmm_plan_create_device(const int32_t* d_rowptr, const int32_t* d_colidx, int32_t M, int32_t K, int32_t nnz,
+                                int32_t N, int32_t dtype, uint32_t flags, void* stream, tca_spmm_plan** plan);
+
+/* The row-kernel task list of a plan, copied to the host (int4 tasks as 4
+ * int32 each, the multi-task row permutation, the long-row table); with
+ * tasks == NULL only the counts are returned.  No counterpart in the
+ * reference: for tests and tools comparing plans. */
+int tca_spmm_plan_export_rows(const tca_spmm_plan* plan, int32_t* n_tasks, int32_t* n_perm, int32_t* n_long,
+                              int32_t* tasks, int32_t* perm, int32_t* longrows);
+
 int tca_spmm_plan_info(const tca_spmm_plan* plan, tca_plan_info* info);
 
 int tca_spmm_plan_destroy(tca_spmm_plan* plan);

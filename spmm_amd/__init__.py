@@ -375,6 +375,31 @@ class Plan:
              n, a.dtype, flags, ctypes.byref(self._p))
         self.m, self.k, self.n, self.nnz, self.dtype = a.nrow, a.ncol, n, a.nnz, a.dtype
 
+    @classmethod
+    def from_device(cls, rowptr, colidx, m: int, k: int, nnz: int, n: int, dtype: int,
+                    flags: int = TCA_PLAN_DEFAULT, stream=None) -> "Plan":
+        """A plan built on the GPU from a device-resident CSR
+        (tca_spmm_plan_create_device); rowptr / colidx are int32 torch
+        tensors (or device addresses)."""
+        self = cls.__new__(cls)
+        self._p = ctypes.c_void_p()
+        call("tca_spmm_plan_create_device", _addr(rowptr), _addr(colidx), m, k, nnz, n, dtype, flags,
+             _addr(stream) if stream is not None else None, ctypes.byref(self._p))
+        self.m, self.k, self.n, self.nnz, self.dtype = m, k, n, nnz, dtype
+        return self
+
+    def export_rows(self):
+        """The row-kernel task list (tasks [T, 4], perm, longrows [L, 4]) as numpy arrays."""
+        nt, npm, nl = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
+        call("tca_spmm_plan_export_rows", self._p, ctypes.byref(nt), ctypes.byref(npm), ctypes.byref(nl),
+             None, None, None)
+        tasks = np.zeros((max(nt.value, 1), 4), np.int32)
+        perm = np.zeros(max(npm.value, 1), np.int32)
+        longrows = np.zeros((max(nl.value, 1), 4), np.int32)
+        call("tca_spmm_plan_export_rows", self._p, ctypes.byref(nt), ctypes.byref(npm), ctypes.byref(nl),
+             np_ptr(tasks, ctypes.c_int32), np_ptr(perm, ctypes.c_int32), np_ptr(longrows, ctypes.c_int32))
+        return tasks[:nt.value], perm[:npm.value], longrows[:nl.value]
+
     def info(self) -> dict:
         i = _lib.TcaPlanInfo()
         call("tca_spmm_plan_info", self._p, ctypes.byref(i))

@@ -78,6 +78,8 @@ SIGNATURES = {
     "tca_gather_values": (i32, [vp, i32, vp, i32, vp, vp]),
     "tca_bell_spmm": (i32, [vp, vp, i32, i32, i32, i32, i32, i32, vp, vp, vp]),
     "tca_spmm_24": (i32, [vp, vp, i32, i32, i32, i32, vp, vp, vp]),
+    "tca_spmm_plan_create_device": (i32, [vp, vp, i32, i32, i32, i32, i32, u32, vp, ctypes.POINTER(vp)]),
+    "tca_spmm_plan_export_rows": (i32, [vp, i32p, i32p, i32p, i32p, i32p, i32p]),
     "tca_spmm_plan_info": (i32, [vp, ctypes.POINTER(TcaPlanInfo)]),
     "tca_spmm_plan_destroy": (i32, [vp]),
     "tca_spmm_host": (i32, [i32p, i32p, vp, i32, i32, i32, vp, f32p, i32, i32, i32, i32,

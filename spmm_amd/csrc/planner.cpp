@@ -51,11 +51,9 @@ void plan_geometry(int32_t N, int32_t es, int32_t slices, RowPlan* p) {
     p->log_lanes = ilog2(next_pow2(p->chunk_lanes));
 }
 
-void plan_rows(const int32_t* rowptr, int32_t M, int32_t N, int32_t es, const std::vector<uint8_t>& skip,
-               int32_t slices, RowPlan* p) {
+void plan_row_params(int64_t nnz, int32_t N, int32_t es, int32_t slices, RowPlan* p) {
     plan_geometry(N, es, slices, p);
     const int32_t slots = 64 >> p->log_lanes;
-    const int64_t nnz = rowptr[M];
     // Work per wavefront task: about nnz / 16384 nonzeros (two resident
     // wavefronts on each of 256 CUs x 4 SIMDs x 8 slots, so long rows do
     // not leave a latency tail), a power of two of at least 256 nonzeros and
@@ -76,6 +74,12 @@ void plan_rows(const int32_t* rowptr, int32_t M, int32_t N, int32_t es, const st
     // Short rows share a wavefront, one slot each, when slots > 1.
     p->multi_max = slots > 1 ? 2 * slots : -1;
     if (const char* s = std::getenv("TCA_MULTI")) p->multi_max = slots > 1 ? std::atoi(s) : -1;
+}
+
+void plan_rows(const int32_t* rowptr, int32_t M, int32_t N, int32_t es, const std::vector<uint8_t>& skip,
+               int32_t slices, RowPlan* p) {
+    plan_row_params(rowptr[M], N, es, slices, p);
+    const int32_t slots = 64 >> p->log_lanes;
 
     std::vector<int32_t> rows;
     rows.reserve(M);

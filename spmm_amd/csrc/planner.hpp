@@ -120,8 +120,16 @@ int32_t default_slices(int32_t K, int32_t N, int32_t dtype);
 // 64 lanes each.  `slices` > 0 forces the number of chunks (tuning).
 void plan_geometry(int32_t N, int32_t es, int32_t slices, RowPlan* p);
 
+// Lane geometry and task-length thresholds (row_len, wide_len, seg_len,
+// multi_max) of the row kernel for a matrix of nnz nonzeros.
+void plan_row_params(int64_t nnz, int32_t N, int32_t es, int32_t slices, RowPlan* p);
+
 // Builds the row-kernel task list for rows with skip[r] == 0 (skip may be
-// empty).  Rows are assigned longest first.
+// empty).  Rows are assigned longest first.  The categories, in task order:
+// wide rows (row_len < length <= wide_len, 4 tasks each), long rows
+// (length > wide_len, segments of at most seg_len, summed in segment order),
+// row tasks (multi_max < length <= row_len), then groups of `slots` short
+// rows (length <= multi_max).
 void plan_rows(const int32_t* rowptr, int32_t M, int32_t N, int32_t es, const std::vector<uint8_t>& skip,
                int32_t slices, RowPlan* p);
 

@@ -17,6 +17,9 @@
 #include "mfma_dense_kernel.hpp"
 #include "bell_kernel.hpp"
 #include "sparse24_kernel.hpp"
+#include "device_planner.hpp"
+
+#include <hipcub/hipcub.hpp>
 #include "sddmm_kernel.hpp"
 
 using namespace tca;
@@ -61,6 +64,10 @@ struct tca_spmm_plan {
     int4* d_tasks = nullptr;
     int* d_perm = nullptr;
     int4* d_longrows = nullptr;
+    int32_t n_longrows = 0;   // rows split into segments (entries of d_longrows)
+    size_t n_seg_total = 0;   // their segments (rows of d_partials)
+    int32_t n_perm = 0;       // rows in multi tasks (entries of d_perm)
+    bool device_planned = false;
     float* d_partials = nullptr;
     tca_plan_info info{};
 };
@@ -130,8 +137,8 @@ void launch_rows_t(const tca_spmm_plan* p, const void* val, const void* B, float
 
 // Adds the segments of long rows (after the row kernel, same stream).
 void launch_finalize(const tca_spmm_plan* p, float* C, hipStream_t s) {
-    if (p->rows.longrows.empty()) return;
-    const dim3 fgrid(static_cast<unsigned>(p->rows.longrows.size()), (p->N + 255) / 256);
+    if (p->n_longrows == 0) return;
+    const dim3 fgrid(static_cast<unsigned>(p->n_longrows), (p->N + 255) / 256);
     hipLaunchKernelGGL(seg_finalize_kernel, fgrid, dim3(64), 0, s, p->d_longrows, p->d_partials, C, p->N);
 }
 
@@ -265,6 +272,46 @@ int run_phases(const tca_spmm_plan* p, const void* val, const void* B, float* C,
     return TCA_OK;
 }
 
+// Plan statistics (tca_plan_info) from a built plan.
+void fill_info(tca_spmm_plan* p) {
+    tca_plan_info& in = p->info;
+    in.M = p->M;
+    in.K = p->K;
+    in.N = p->N;
+    in.nnz = p->nnz;
+    in.dtype = p->dtype;
+    in.elems_per_lane = p->rows.elems_per_lane;
+    in.lanes_per_row = 1 << p->rows.log_lanes;
+    in.col_chunks = p->rows.col_chunks;
+    in.n_row_tasks = p->ntasks;
+    in.n_multi_tasks = p->rows.n_multi;
+    in.n_seg_tasks = p->rows.n_seg;
+    in.n_long_rows = p->n_longrows;
+    in.n_wide_tasks = p->rows.n_wide;
+    in.chunk_lanes = p->rows.chunk_lanes;
+    in.row_len = p->rows.row_len;
+    in.wide_len = p->rows.wide_len;
+    in.row_blocks = ((p->ntasks + kRowWaves - 1) / kRowWaves) * p->rows.col_chunks;
+    in.row_blockdim = 64 * kRowWaves;
+    in.seg_len = p->rows.seg_len;
+    in.n_windows_mfma = static_cast<int32_t>(p->mfma.windows.size());
+    in.rows_mfma = p->mfma.rows;
+    in.nnz_mfma = p->mfma.nnz;
+    in.cond_cols_mfma = p->mfma.cond_cols;
+    in.mfma_blocks = p->mfma_dense ? mfma_dense_grid(in.n_windows_mfma, p->mfma_col_blocks)
+                                   : in.n_windows_mfma * p->mfma_col_blocks;
+    in.mfma_blockdim = kMfmaThreads;
+    if (p->mfma_dense)
+        in.mfma_lds_bytes = mfma_dense_lds_bytes();
+    else if (p->mfma_pair)
+        in.mfma_lds_bytes = mfma_pair_lds_bytes();
+    else if (p->mfma_dma && p->mfma_slots <= 2)
+        in.mfma_lds_bytes = mfma_dma_lds_bytes();
+    else
+        in.mfma_lds_bytes = p->mfma_slots == 1 ? mfma_lds_bytes<1>() : p->mfma_slots == 2 ? mfma_lds_bytes<2>() : mfma_lds_bytes<4>();
+    in.scratch_bytes = static_cast<int64_t>(p->n_seg_total * p->N * sizeof(float));
+}
+
 }  // namespace
 
 extern "C" {
@@ -365,6 +412,9 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
     p->ntasks = static_cast<int32_t>(p->rows.tasks.size());
     const size_t n_seg_total =
         p->rows.longrows.empty() ? 0 : static_cast<size_t>(p->rows.longrows.back().y + p->rows.longrows.back().z);
+    p->n_longrows = static_cast<int32_t>(p->rows.longrows.size());
+    p->n_seg_total = n_seg_total;
+    p->n_perm = static_cast<int32_t>(p->rows.perm.size());
     const auto t1 = std::chrono::steady_clock::now();
 
     auto bail = [&](int s) {
@@ -500,44 +550,179 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
     }
     if (hipDeviceSynchronize() != hipSuccess) return bail(fail(TCA_ERR_HIP, "hipDeviceSynchronize failed"));
 
-    tca_plan_info& in = p->info;
-    in.M = M;
-    in.K = K;
-    in.N = N;
-    in.nnz = nnz;
-    in.dtype = dtype;
-    in.elems_per_lane = p->rows.elems_per_lane;
-    in.lanes_per_row = 1 << p->rows.log_lanes;
-    in.col_chunks = p->rows.col_chunks;
-    in.n_row_tasks = p->ntasks;
-    in.n_multi_tasks = p->rows.n_multi;
-    in.n_seg_tasks = p->rows.n_seg;
-    in.n_long_rows = static_cast<int32_t>(p->rows.longrows.size());
-    in.n_wide_tasks = p->rows.n_wide;
-    in.chunk_lanes = p->rows.chunk_lanes;
-    in.row_len = p->rows.row_len;
-    in.wide_len = p->rows.wide_len;
-    in.row_blocks = ((p->ntasks + kRowWaves - 1) / kRowWaves) * p->rows.col_chunks;
-    in.row_blockdim = 64 * kRowWaves;
-    in.seg_len = p->rows.seg_len;
-    in.n_windows_mfma = static_cast<int32_t>(p->mfma.windows.size());
-    in.rows_mfma = p->mfma.rows;
-    in.nnz_mfma = p->mfma.nnz;
-    in.cond_cols_mfma = p->mfma.cond_cols;
-    in.mfma_blocks = p->mfma_dense ? mfma_dense_grid(in.n_windows_mfma, p->mfma_col_blocks)
-                                   : in.n_windows_mfma * p->mfma_col_blocks;
-    in.mfma_blockdim = kMfmaThreads;
-    if (p->mfma_dense)
-        in.mfma_lds_bytes = mfma_dense_lds_bytes();
-    else if (p->mfma_pair)
-        in.mfma_lds_bytes = mfma_pair_lds_bytes();
-    else if (p->mfma_dma && p->mfma_slots <= 2)
-        in.mfma_lds_bytes = mfma_dma_lds_bytes();
-    else
-        in.mfma_lds_bytes = p->mfma_slots == 1 ? mfma_lds_bytes<1>() : p->mfma_slots == 2 ? mfma_lds_bytes<2>() : mfma_lds_bytes<4>();
-    in.scratch_bytes = static_cast<int64_t>(n_seg_total * N * sizeof(float));
-    in.plan_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
+    fill_info(p);
+    p->info.plan_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
     *plan = p;
+    return TCA_OK;
+}
+
+int tca_spmm_plan_create_device(const int32_t* d_rowptr, const int32_t* d_colidx, int32_t M, int32_t K, int32_t nnz,
+                                int32_t N, int32_t dtype, uint32_t flags, void* stream, tca_spmm_plan** plan) {
+    if (!plan) return fail(TCA_ERR_INVALID, "plan is NULL");
+    *plan = nullptr;
+    if (M < 0 || K < 1 || N < 1 || nnz < 0) return fail(TCA_ERR_INVALID, "bad shape M=%d K=%d N=%d nnz=%d", M, K, N, nnz);
+    if (!dtype_ok(dtype)) return fail(TCA_ERR_INVALID, "unknown dtype %d", dtype);
+    if (!d_rowptr || (nnz > 0 && !d_colidx)) return fail(TCA_ERR_INVALID, "NULL device pointer");
+    if (flags & (TCA_PLAN_FORCE_MFMA | TCA_PLAN_MFMA_REGS | TCA_PLAN_MFMA_DMA | TCA_PLAN_MFMA_DENSE))
+        return fail(TCA_ERR_UNSUPPORTED, "device planning builds row-kernel plans only (MFMA flags need the host planner)");
+    const uint64_t b_bytes = static_cast<uint64_t>(K) * static_cast<uint64_t>(N) * dtype_size(dtype);
+    if (b_bytes >= 0xfffffff0ull || static_cast<uint64_t>(nnz) * 4 >= 0xfffffff0ull)
+        return fail(TCA_ERR_UNSUPPORTED, "B (%llu bytes) or the nonzeros exceed the 4 GiB buffer range",
+                    (unsigned long long)b_bytes);
+    const auto t0 = std::chrono::steady_clock::now();
+    tca_spmm_plan* p = new (std::nothrow) tca_spmm_plan();
+    if (!p) return fail(TCA_ERR_ALLOC, "plan allocation failed");
+    p->M = M;
+    p->K = K;
+    p->N = N;
+    p->nnz = nnz;
+    p->dtype = dtype;
+    p->flags = flags | TCA_PLAN_NO_MFMA;
+    p->device_planned = true;
+    p->mfma.row_mfma.clear();
+    if (hipGetDevice(&p->device) != hipSuccess) {
+        delete p;
+        return fail(TCA_ERR_HIP, "no HIP device");
+    }
+    plan_row_params(nnz, N, static_cast<int32_t>(dtype_size(dtype)), default_slices(K, N, dtype), &p->rows);
+    const int slots = 64 >> p->rows.log_lanes;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+
+    // temporaries of the planning, freed on every exit
+    uint32_t *keys = nullptr, *keys_s = nullptr;
+    int *rows = nullptr, *rows_s = nullptr, *cnt = nullptr, *nseg = nullptr, *segoff = nullptr;
+    uint8_t* start = nullptr;
+    void* tmp = nullptr;
+    auto bail = [&](int st) {
+        (void)hipStreamSynchronize(s);
+        for (void* q : {(void*)keys, (void*)keys_s, (void*)rows, (void*)rows_s, (void*)cnt, (void*)nseg, (void*)segoff,
+                        (void*)start, tmp})
+            (void)hipFree(q);
+        if (st != TCA_OK) {
+            free_plan_device(p);
+            delete p;
+        }
+        return st;
+    };
+    int st;
+    // The plan owns its copy of the structure (row kernel and SDDMM read it).
+    if ((st = dev_upload(&p->d_rowptr, nullptr, static_cast<size_t>(M) + 1))) return bail(st);
+    if ((st = dev_upload(&p->d_colidx, nullptr, static_cast<size_t>(nnz)))) return bail(st);
+    if (hipMemcpyAsync(p->d_rowptr, d_rowptr, sizeof(int) * (static_cast<size_t>(M) + 1), hipMemcpyDeviceToDevice, s) !=
+            hipSuccess ||
+        (nnz > 0 && hipMemcpyAsync(p->d_colidx, d_colidx, sizeof(int) * static_cast<size_t>(nnz),
+                                   hipMemcpyDeviceToDevice, s) != hipSuccess))
+        return bail(fail(TCA_ERR_HIP, "structure copy failed"));
+    // CSR checks
+    if ((st = dev_upload(&cnt, nullptr, 4))) return bail(st);  // [0..2] bounds, [3] error bits
+    if ((st = dev_upload(&start, nullptr, static_cast<size_t>(nnz) + 1))) return bail(st);
+    if (hipMemsetAsync(cnt, 0, 4 * sizeof(int), s) != hipSuccess ||
+        hipMemsetAsync(start, 0, static_cast<size_t>(nnz) + 1, s) != hipSuccess)
+        return bail(fail(TCA_ERR_HIP, "hipMemsetAsync failed"));
+    const dim3 blk(256);
+    auto grid_for = [](int64_t n) { return dim3(static_cast<unsigned>(std::min<int64_t>((n + 255) / 256, 65536))); };
+    if (M > 0) {
+        hipLaunchKernelGGL(dp_check_rows_kernel, grid_for(M), blk, 0, s, p->d_rowptr, M, nnz, start, cnt + 3);
+        if (nnz > 0) hipLaunchKernelGGL(dp_check_cols_kernel, grid_for(nnz), blk, 0, s, p->d_colidx, nnz, K, start, cnt + 3);
+    }
+    // rows longest first (stable descending radix sort of the lengths)
+    int h_cnt[4] = {0, 0, 0, 0};
+    if (M > 0) {
+        if ((st = dev_upload(&keys, nullptr, M)) || (st = dev_upload(&keys_s, nullptr, M)) ||
+            (st = dev_upload(&rows, nullptr, M)) || (st = dev_upload(&rows_s, nullptr, M)))
+            return bail(st);
+        hipLaunchKernelGGL(dp_lengths_kernel, grid_for(M), blk, 0, s, p->d_rowptr, M, keys, rows);
+        size_t tmp_bytes = 0;
+        if (hipcub::DeviceRadixSort::SortPairsDescending(nullptr, tmp_bytes, keys, keys_s, rows, rows_s, M, 0, 32, s) !=
+            hipSuccess)
+            return bail(fail(TCA_ERR_HIP, "radix sort sizing failed"));
+        if (hipMalloc(&tmp, tmp_bytes) != hipSuccess) return bail(fail(TCA_ERR_ALLOC, "radix sort workspace"));
+        if (hipcub::DeviceRadixSort::SortPairsDescending(tmp, tmp_bytes, keys, keys_s, rows, rows_s, M, 0, 32, s) !=
+            hipSuccess)
+            return bail(fail(TCA_ERR_HIP, "radix sort failed"));
+        hipLaunchKernelGGL(dp_bounds_kernel, dim3(1), dim3(64), 0, s, keys_s, M, p->rows.wide_len, p->rows.row_len,
+                           p->rows.multi_max, cnt);
+    }
+    if (hipMemcpyAsync(h_cnt, cnt, sizeof h_cnt, hipMemcpyDeviceToHost, s) != hipSuccess ||
+        hipStreamSynchronize(s) != hipSuccess)
+        return bail(fail(TCA_ERR_HIP, "planning kernels failed"));
+    if (h_cnt[3] & 1) return bail(fail(TCA_ERR_INVALID, "CSR row offsets are not 0 .. nnz non-decreasing"));
+    if (h_cnt[3] & 2) return bail(fail(TCA_ERR_INVALID, "CSR columns out of range or not strictly ascending in a row"));
+    const int n_long = h_cnt[0], end_wide = h_cnt[1], end_row = h_cnt[2];
+    // segment slots of the long rows: exclusive sum of their segment counts
+    int seg_total = 0;
+    if (n_long > 0) {
+        if ((st = dev_upload(&nseg, nullptr, static_cast<size_t>(n_long) + 1)) ||
+            (st = dev_upload(&segoff, nullptr, static_cast<size_t>(n_long) + 1)))
+            return bail(st);
+        if (hipMemsetAsync(nseg, 0, sizeof(int) * (static_cast<size_t>(n_long) + 1), s) != hipSuccess)
+            return bail(fail(TCA_ERR_HIP, "hipMemsetAsync failed"));
+        hipLaunchKernelGGL(dp_nseg_kernel, grid_for(n_long), blk, 0, s, keys_s, n_long, p->rows.seg_len, nseg);
+        (void)hipFree(tmp);
+        tmp = nullptr;
+        size_t tmp_bytes = 0;
+        if (hipcub::DeviceScan::ExclusiveSum(nullptr, tmp_bytes, nseg, segoff, n_long + 1, s) != hipSuccess ||
+            hipMalloc(&tmp, tmp_bytes) != hipSuccess ||
+            hipcub::DeviceScan::ExclusiveSum(tmp, tmp_bytes, nseg, segoff, n_long + 1, s) != hipSuccess ||
+            hipMemcpyAsync(&seg_total, segoff + n_long, sizeof(int), hipMemcpyDeviceToHost, s) != hipSuccess ||
+            hipStreamSynchronize(s) != hipSuccess)
+            return bail(fail(TCA_ERR_HIP, "segment scan failed"));
+    }
+    const int n_wide = end_wide - n_long, n_row = end_row - end_wide, n_short = M - end_row;
+    const int n_multi = (n_short + slots - 1) / slots;
+    p->ntasks = 4 * n_wide + seg_total + n_row + n_multi;
+    p->rows.n_wide = 4 * n_wide;
+    p->rows.n_seg = seg_total;
+    p->rows.n_rowtasks = n_row;
+    p->rows.n_multi = n_multi;
+    p->n_longrows = n_long;
+    p->n_seg_total = static_cast<size_t>(seg_total);
+    p->n_perm = n_short;
+    if ((st = dev_upload(&p->d_tasks, nullptr, p->ntasks)) || (st = dev_upload(&p->d_perm, nullptr, n_short)) ||
+        (st = dev_upload(&p->d_longrows, nullptr, n_long)) ||
+        (st = dev_upload(&p->d_partials, nullptr, p->n_seg_total * N)))
+        return bail(st);
+    if (M > 0) {
+        DpEmitArgs ea;
+        ea.rowptr = p->d_rowptr;
+        ea.len = keys_s;
+        ea.rows = rows_s;
+        ea.segoff = segoff;
+        ea.tasks = p->d_tasks;
+        ea.perm = p->d_perm;
+        ea.longrows = p->d_longrows;
+        ea.M = M;
+        ea.n_long = n_long;
+        ea.end_wide = end_wide;
+        ea.end_row = end_row;
+        ea.slots = slots;
+        ea.seg_total = seg_total;
+        hipLaunchKernelGGL(dp_emit_kernel, grid_for(M), blk, 0, s, ea);
+    }
+    if (hipGetLastError() != hipSuccess || hipStreamSynchronize(s) != hipSuccess)
+        return bail(fail(TCA_ERR_HIP, "task emission failed"));
+    st = bail(TCA_OK);  // frees the temporaries only
+    fill_info(p);
+    p->info.plan_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+    *plan = p;
+    return TCA_OK;
+}
+
+int tca_spmm_plan_export_rows(const tca_spmm_plan* p, int32_t* n_tasks, int32_t* n_perm, int32_t* n_long,
+                              int32_t* tasks, int32_t* perm, int32_t* longrows) {
+    if (!p || !n_tasks || !n_perm || !n_long) return fail(TCA_ERR_INVALID, "tca_spmm_plan_export_rows: bad argument");
+    if (tasks) {
+        if (*n_tasks < p->ntasks || *n_perm < p->n_perm || *n_long < p->n_longrows || !perm || !longrows)
+            return fail(TCA_ERR_INVALID, "tca_spmm_plan_export_rows: output buffers too small");
+        if ((p->ntasks && hipMemcpy(tasks, p->d_tasks, sizeof(int4) * p->ntasks, hipMemcpyDeviceToHost) != hipSuccess) ||
+            (p->n_perm && hipMemcpy(perm, p->d_perm, sizeof(int) * p->n_perm, hipMemcpyDeviceToHost) != hipSuccess) ||
+            (p->n_longrows &&
+             hipMemcpy(longrows, p->d_longrows, sizeof(int4) * p->n_longrows, hipMemcpyDeviceToHost) != hipSuccess))
+            return fail(TCA_ERR_HIP, "tca_spmm_plan_export_rows: copy failed");
+    }
+    *n_tasks = p->ntasks;
+    *n_perm = p->n_perm;
+    *n_long = p->n_longrows;
     return TCA_OK;
 }
 
@@ -748,7 +933,7 @@ int tca_spmm_time_phases(const tca_spmm_plan* p, const void* d_val, const void* 
     }
     int st = TCA_OK;
     const bool used[TCA_PHASES] = {!p->mfma.windows.empty() && !p->mfma.entries.empty(), !p->mfma.windows.empty(),
-                                   p->ntasks > 0, !p->rows.longrows.empty()};
+                                   p->ntasks > 0, p->n_longrows > 0};
     for (int k = 0; k < TCA_PHASES && st == TCA_OK; k++) {
         if (!used[k]) continue;
         (void)hipEventRecord(e0, s);

@@ -70,3 +70,17 @@ def test_rejects_invalid_csr_before_touching_device():
     st = L.lib.tca_spmm_plan_create(L.np_ptr(rp, ctypes.c_int32), L.np_ptr(ci, ctypes.c_int32), 3, 4, 3, 8, 0, 0,
                                     ctypes.byref(p))
     assert st == 1 and b"ascending" in L.lib.tca_last_error()
+
+
+def test_device_plan_argument_checks_need_no_gpu():
+    """Flags and NULL pointers are rejected before any device call."""
+    import ctypes
+    import spmm_amd as S
+    p = ctypes.c_void_p()
+    with pytest.raises(S.TcaError) as ei:
+        S._lib.call("tca_spmm_plan_create_device", 16, 16, 4, 4, 4, 8, S.TCA_F32, S.TCA_PLAN_FORCE_MFMA, None,
+                    ctypes.byref(p))
+    assert ei.value.status == 4
+    with pytest.raises(S.TcaError) as ei:
+        S._lib.call("tca_spmm_plan_create_device", None, None, 4, 4, 4, 8, S.TCA_F32, 0, None, ctypes.byref(p))
+    assert ei.value.status == 1

@@ -1,0 +1,87 @@
+"""Planning on the GPU (tca_spmm_plan_create_device): the task list built by
+device kernels from a device-resident CSR equals the host planner's
+(TCA_PLAN_NO_MFMA) entry for entry, and both plans give bit-identical
+products; invalid structures are rejected on the device."""
+import numpy as np
+import pytest
+
+from conftest import exact_dense
+from oracle import oracle
+from test_gpu_parity import _dev
+
+import spmm_amd as S
+
+pytestmark = pytest.mark.gpu
+
+
+def _cases():
+    yield "bernoulli", S.gen_bernoulli(3000, 2000, 0.01, seed=1, dtype=S.TCA_F16)[0], 256
+    yield "lognormal", S.gen_lognormal_rows(4096, 4096, 205, seed=1, dtype=S.TCA_F16)[0], 512
+    yield "lognormal-f32", S.gen_lognormal_rows(2000, 3000, 50, seed=2, dtype=S.TCA_F32)[0], 128
+    yield "rmat", S.gen_rmat(14, 12000, 400000, seed=3, dtype=S.TCA_F32)[0], 128
+    yield "zipf", S.gen_zipf_rows(60000, 60000, 2000000, seed=4, dtype=S.TCA_F16)[0], 64
+    yield "narrow", S.gen_bernoulli(500, 700, 0.05, seed=5, dtype=S.TCA_F16)[0], 8
+    yield "wide-n", S.gen_bernoulli(300, 400, 0.05, seed=6, dtype=S.TCA_F32)[0], 1000
+
+
+@pytest.mark.parametrize("name,a,n", list(_cases()), ids=[c[0] for c in _cases()])
+def test_device_plan_equals_host_plan(torch_cuda, name, a, n):
+    torch = torch_cuda
+    print(f"device plan {name}: M={a.nrow} K={a.ncol} nnz={a.nnz} N={n}", flush=True)
+    drp, dci = _dev(torch, a.rowptr), _dev(torch, a.colidx)
+    with S.Plan(a, n, S.TCA_PLAN_NO_MFMA) as hp:
+        dp = S.Plan.from_device(drp, dci, a.nrow, a.ncol, a.nnz, n, a.dtype)
+        try:
+            ht, hperm, hl = hp.export_rows()
+            dt, dperm, dl = dp.export_rows()
+            assert np.array_equal(ht, dt) and np.array_equal(hperm, dperm) and np.array_equal(hl, dl), name
+            hi, di = hp.info(), dp.info()
+            for key in ("n_row_tasks", "n_multi_tasks", "n_seg_tasks", "n_long_rows", "n_wide_tasks", "scratch_bytes"):
+                assert hi[key] == di[key], (name, key)
+            rng = np.random.default_rng(7)
+            b = S.to_storage(exact_dense(rng, (a.ncol, n)), a.dtype)
+            val, bd = _dev(torch, a.values), _dev(torch, b)
+            outs = []
+            for pl in (hp, dp):
+                c = torch.full((a.nrow, n), float("nan"), dtype=torch.float32, device="cuda:0")
+                pl.run(val, bd, c)
+                torch.cuda.synchronize()
+                outs.append(c.cpu().numpy())
+            assert np.array_equal(outs[0], outs[1]), name
+            assert np.all(np.isfinite(outs[1]))
+        finally:
+            dp.close()
+
+
+def test_device_plan_result_matches_oracle(torch_cuda):
+    torch = torch_cuda
+    a = S.gen_lognormal_rows(1000, 1500, 80, seed=9, dtype=S.TCA_F16)[0]
+    rng = np.random.default_rng(9)
+    v = rng.choice(np.array([-2.0, -1.0, -0.5, 0.5, 1.0, 2.0], np.float32), size=a.nnz)
+    a = S.CSR(a.nrow, a.ncol, a.rowptr, a.colidx, S.to_storage(v, S.TCA_F16), S.TCA_F16)
+    b = S.to_storage(exact_dense(rng, (a.ncol, 128)), S.TCA_F16)
+    dp = S.Plan.from_device(_dev(torch, a.rowptr), _dev(torch, a.colidx), a.nrow, a.ncol, a.nnz, 128, a.dtype)
+    c = torch.empty((a.nrow, 128), dtype=torch.float32, device="cuda:0")
+    dp.run(_dev(torch, a.values), _dev(torch, b), c)
+    torch.cuda.synchronize()
+    dp.close()
+    want = oracle.csr_spmm(a.rowptr, a.colidx, a.values_f32(), S.from_storage(b, S.TCA_F16))
+    assert np.array_equal(c.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("bad", ["rowptr-decreasing", "rowptr-end", "col-range", "col-order"])
+def test_device_plan_rejects_invalid_structure(torch_cuda, bad):
+    torch = torch_cuda
+    rowptr = np.array([0, 2, 3, 5], np.int32)
+    colidx = np.array([0, 3, 1, 2, 4], np.int32)
+    if bad == "rowptr-decreasing":
+        rowptr[2] = 1
+    elif bad == "rowptr-end":
+        rowptr[3] = 4
+    elif bad == "col-range":
+        colidx[4] = 5
+    else:
+        colidx[1] = 0
+    with pytest.raises(S.TcaError) as ei:
+        S.Plan.from_device(_dev(torch, rowptr), _dev(torch, colidx), 3, 5, 5, 64, S.TCA_F32)
+    assert ei.value.status == 1
