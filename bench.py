@@ -27,29 +27,38 @@ WORKLOADS = {
 }
 
 
-# Dominant kernel of each phase (tca_spmm_time_phases order).
-PHASE_KERNELS = {"pack": "mfma_pack_kernel", "tiles": "mfma_pair_kernel", "rows": "row_kernel",
-                 "segments": "seg_finalize_kernel"}
-REGS_TILE_KERNEL = "mfma_tile_kernel"  # the "tiles" phase under plan flag TCA_PLAN_MFMA_REGS
-DMA_TILE_KERNEL = "mfma_dma_kernel"    # the "tiles" phase under plan flag TCA_PLAN_MFMA_DMA
-DENSE_TILE_KERNEL = "mfma_dense_kernel"  # the "tiles" phase under plan flag TCA_PLAN_MFMA_DENSE
+# Kernels of each phase (tca_spmm_time_phases order); the tile and pack
+# kernels depend on the plan (tca_plan_info.tile_kernel).
+TILE_KERNELS = {1: "mfma_tile_kernel", 2: "mfma_dma_kernel", 3: "mfma_pair_kernel", 4: "mfma_dense_kernel",
+                5: "mfma_dense_kernel", 6: "mfma_sparse_kernel"}
+
+
+def phase_kernel(phase: str, tile_kernel: int) -> str:
+    if phase == "tiles":
+        return TILE_KERNELS.get(tile_kernel, "none")
+    if phase == "pack":
+        return "dense_pack_kernel" if tile_kernel in (4, 5, 6) else "mfma_pack_kernel"
+    return {"rows": "row_kernel", "segments": "seg_finalize_kernel"}[phase]
+
 
 # HBM bytes per launch of the dominant kernel, measured with rocprofv3 --pmc
 # FETCH_SIZE and WRITE_SIZE (KiB per dispatch, already scaled by the copy
-# calibration: FETCH x 2.00, WRITE x 1.00), keyed by (config, phase, flags).
+# calibration: FETCH x 2.00, WRITE x 1.00), keyed by (config, kernel).
 # Source: the profiles/ summaries named in each entry.
 MEASURED_TRAFFIC_KIB = {
-    # profiles/mfma_pair_kernel_config1.md (paired tile kernel, the default)
-    (1, "tiles", 0): (21323.1 * 2.0, 8436.0),
+    # profiles/mfma_dense_kernel_config1.md (dense tiles over all of K, the default on config 1)
+    (1, "mfma_dense_kernel"): (32839.5 * 2.0, 8248.8),
+    # profiles/mfma_pair_kernel_config1.md (paired tile kernel)
+    (1, "mfma_pair_kernel"): (21323.1 * 2.0, 8436.0),
     # profiles/mfma_dma_kernel_config1.md (LDS-DMA tile kernel)
-    (1, "tiles", 8): (39252.0 * 2.0, 8319.2),  # flags 8 = TCA_PLAN_MFMA_DMA
+    (1, "mfma_dma_kernel"): (39252.0 * 2.0, 8319.2),
     # profiles/mfma_tile_kernel_config1.md (register-staged tile kernel)
-    (1, "tiles", 4): (12768.8 * 2.0, 10785.3),  # flags 4 = TCA_PLAN_MFMA_REGS
+    (1, "mfma_tile_kernel"): (12768.8 * 2.0, 10785.3),
     # profiles/row_kernel_graph_configs.md (row kernel, default routing)
-    (0, "rows", 0): (1611.8 * 2.0, 3001.0),
-    (2, "rows", 0): (12064593.2 * 2.0, 122066.5),
-    (3, "rows", 0): (12350070.5 * 2.0, 1225462.5),
-    (4, "rows", 0): (1298864.7 * 2.0, 402965.0),
+    (0, "row_kernel"): (1611.8 * 2.0, 3001.0),
+    (2, "row_kernel"): (12064593.2 * 2.0, 122066.5),
+    (3, "row_kernel"): (12350070.5 * 2.0, 1225462.5),
+    (4, "row_kernel"): (1298864.7 * 2.0, 402965.0),
 }
 
 
@@ -68,7 +77,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--flags", type=int, default=0,
                     help="plan flags (1 = no MFMA, 2 = force MFMA, 4 = register-staged tile kernel, "
-                         "8 = LDS-DMA tile kernel, 16 = dense-tile kernel)")
+                         "8 = LDS-DMA tile kernel, 16 = dense-tile kernel, 32 = 2:4 sparse-core tiles, "
+                         "64 = paired tile kernel)")
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
                     help="before timing, run one device-to-device copy of MIB MiB (a known-size kernel to "
                          "scale rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
@@ -181,14 +191,8 @@ def main():
     bytes_dom = 4 * (rows_k + 1) + nnz_k * (4 + s_a) + k * n * s_a + rows_k * n * 4
     dom_ms = phases[dominant]
     achieved = bytes_dom / (dom_ms * 1e-3) / 1e9
-    kib = args.traffic_kib or MEASURED_TRAFFIC_KIB.get((args.config, dominant, args.flags))
-    kernel_name = PHASE_KERNELS[dominant]
-    if dominant == "tiles" and args.flags & S.TCA_PLAN_MFMA_REGS:
-        kernel_name = REGS_TILE_KERNEL
-    elif dominant == "tiles" and args.flags & S.TCA_PLAN_MFMA_DMA:
-        kernel_name = DMA_TILE_KERNEL
-    elif dominant == "tiles" and args.flags & S.TCA_PLAN_MFMA_DENSE:
-        kernel_name = DENSE_TILE_KERNEL
+    kernel_name = phase_kernel(dominant, info["tile_kernel"])
+    kib = args.traffic_kib or MEASURED_TRAFFIC_KIB.get((args.config, kernel_name))
     traffic = int(round((kib[0] + kib[1]) * 1024)) if kib else None
     log(f"kernel avg {ms_per_step * 1e3:.2f} us/step, wall {wall_ms:.2f} ms for {args.warmup}+{args.steps} steps")
 
@@ -237,7 +241,8 @@ def main():
                    "plan_ms": round(info["plan_ms"], 3),
                    "phases_us": {kk: round(v * 1e3, 3) for kk, v in phases.items()},
                    "cold_cache_us": round(cold_ms * 1e3, 3), "launch_floor_us": round(floor_ms * 1e3, 3),
-                   "mfma_windows": info["n_windows_mfma"], "rows_mfma": info["rows_mfma"]},
+                   "mfma_windows": info["n_windows_mfma"], "rows_mfma": info["rows_mfma"],
+                   "tile_kernel": TILE_KERNELS.get(info["tile_kernel"], "none")},
         "roofline": {"bound": "hbm", "kernel": kernel_name, "bytes_alg": bytes_dom,
                      "kernel_us": round(dom_ms * 1e3, 3),
                      "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",

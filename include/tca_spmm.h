@@ -50,9 +50,14 @@ typedef enum tca_status {
 #define TCA_PLAN_DEFAULT 0u
 #define TCA_PLAN_NO_MFMA 1u    /* route every row to the wavefront-per-row kernel */
 #define TCA_PLAN_FORCE_MFMA 2u /* route every eligible 64-row window to the MFMA tile kernel (fp16/bf16, N % 8 == 0) */
-#define TCA_PLAN_MFMA_REGS 4u  /* register-staged 64 x 128 tile kernel instead of the default paired 128 x 64 one */
-#define TCA_PLAN_MFMA_DMA 8u   /* LDS-DMA 128 x 64 tile kernel instead of the default paired one */
+#define TCA_PLAN_MFMA_REGS 4u  /* register-staged 64 x 128 tile kernel instead of the default one */
+#define TCA_PLAN_MFMA_DMA 8u   /* LDS-DMA 128 x 64 tile kernel instead of the default one */
 #define TCA_PLAN_MFMA_DENSE 16u /* dense-tile 128 x 64 kernel (plan keeps dense condensed windows) */
+/* Default tile kernel: dense tiles spanning all of K when the routed windows'
+ * column unions cover on average >= 85 % of K (B rows then need no gather
+ * table), else the paired kernel. */
+#define TCA_PLAN_MFMA_SPARSE 32u /* 2:4-grouped windows on the sparse matrix cores (v_smfmac) */
+#define TCA_PLAN_MFMA_PAIR 64u  /* paired (MFMA + staging wavefront) 128 x 64 kernel, whatever the windows */
 
 typedef struct tca_spmm_plan tca_spmm_plan;
 
@@ -83,7 +88,17 @@ typedef struct tca_plan_info {
     int32_t chunk_lanes;      /* lanes holding data in one column chunk */
     int32_t row_len;          /* rows up to this length take one wavefront */
     int32_t wide_len;         /* rows up to this length take one workgroup; longer rows are segmented */
+    int32_t tile_kernel;      /* MFMA tile kernel of the plan: TCA_TILES_* */
 } tca_plan_info;
+
+/* tca_plan_info.tile_kernel */
+#define TCA_TILES_NONE 0       /* no window routed to the matrix cores */
+#define TCA_TILES_REGS 1       /* register-staged 64 x 128 tiles (TCA_PLAN_MFMA_REGS) */
+#define TCA_TILES_DMA 2        /* LDS-DMA 128 x 64 tiles (TCA_PLAN_MFMA_DMA) */
+#define TCA_TILES_PAIR 3       /* paired MFMA + staging wavefronts (default when windows are narrow) */
+#define TCA_TILES_DENSE 4      /* dense condensed tiles (TCA_PLAN_MFMA_DENSE) */
+#define TCA_TILES_DENSE_K 5    /* dense tiles spanning all of K (default when the windows cover most of K) */
+#define TCA_TILES_SPARSE 6     /* 2:4-grouped tiles on the sparse matrix cores (TCA_PLAN_MFMA_SPARSE) */
 
 /* Replaces reference workload_manager (src/our_spmm.cu:353-477) plus the
  * device uploads of our_spmm_balanced (src/our_spmm.cu:503-525).

@@ -19,6 +19,8 @@ TCA_F16, TCA_F32, TCA_BF16 = 0, 1, 2
 DTYPE_NAMES = {TCA_F16: "f16", TCA_F32: "f32", TCA_BF16: "bf16"}
 TCA_PLAN_DEFAULT, TCA_PLAN_NO_MFMA, TCA_PLAN_FORCE_MFMA, TCA_PLAN_MFMA_REGS, TCA_PLAN_MFMA_DMA = 0, 1, 2, 4, 8
 TCA_PLAN_MFMA_DENSE = 16
+TCA_PLAN_MFMA_SPARSE = 32
+TCA_PLAN_MFMA_PAIR = 64
 
 i32 = ctypes.c_int32
 i64 = ctypes.c_int64
@@ -47,7 +49,8 @@ class TcaPlanInfo(ctypes.Structure):
                 ("n_windows_mfma", i32), ("rows_mfma", i32), ("nnz_mfma", i64), ("cond_cols_mfma", i64),
                 ("row_blocks", i32), ("row_blockdim", i32), ("mfma_blocks", i32), ("mfma_blockdim", i32),
                 ("mfma_lds_bytes", i32), ("seg_len", i32), ("scratch_bytes", i64), ("plan_ms", ctypes.c_double),
-                ("n_wide_tasks", i32), ("chunk_lanes", i32), ("row_len", i32), ("wide_len", i32)]
+                ("n_wide_tasks", i32), ("chunk_lanes", i32), ("row_len", i32), ("wide_len", i32),
+                ("tile_kernel", i32)]
 
     def as_dict(self):
         return {name: getattr(self, name) for name, _ in self._fields_}

@@ -54,6 +54,7 @@ constexpr int kDnOps = 3 * kDnSteps;                          // transfers per p
 constexpr int kDnWait = (kDnLB - 2) * kDnOps;                 // tile i + 2 lands in iteration i
 constexpr int kXcds = 8;                                      // XCDs of the MI355X
 constexpr size_t kDenseMaxBytes = size_t(2) << 30;            // dense tiles a plan may keep
+constexpr double kNaturalCover = 0.85;  // windows covering this share of K keep all of K in column order
 
 constexpr int mfma_dense_lds_bytes() {
     constexpr int main = kDnSlots * kDnSlotBytes;
@@ -78,7 +79,10 @@ __global__ __launch_bounds__(256) void dense_pack_kernel(const int* __restrict__
     if (x < n) adense[pos[x]] = val[src[x]];
 }
 
-template <bool kBf16>
+// kNatural: the windows span all of K in column order (step j = columns
+// 32 j .. 32 j + 31), so a B row's offset is its row number times the row
+// pitch and the producers need no row-offset table.
+template <bool kBf16, bool kNatural>
 __global__ __launch_bounds__(kDnThreads) void mfma_dense_kernel(MfmaArgs a) {
     constexpr int KS = kDnSteps, LB = kDnLB, NS = kDnSlots;
     __shared__ __attribute__((aligned(16))) char smem[mfma_dense_lds_bytes()];
@@ -213,24 +217,33 @@ __global__ __launch_bounds__(kDnThreads) void mfma_dense_kernel(MfmaArgs a) {
                 dma_x4(asrc, lds_addr(adst));
                 dma_x4(asrc + 1024, lds_addr(adst + 1024));
                 // B rows 8 pw .. 8 pw + 7: this lane's row offset by a select tree
-                uint32_t m[8];
+                // (natural order: the row is 32 j + 8 pw + lane / 8)
+                uint32_t uo;
+                if constexpr (kNatural) {
+                    const int brow = kStepK * j + 8 * pw + g8;
+                    uo = brow < a.K ? static_cast<uint32_t>(brow) * static_cast<uint32_t>(a.N) * 2u : kNoEntry;
+                } else {
+                    uint32_t m[8];
 #pragma unroll
-                for (int r = 0; r < 8; r++) m[r] = __builtin_amdgcn_readfirstlane(mu[sp][r]);
-                const uint32_t u01 = (g8 & 1) ? m[1] : m[0], u23 = (g8 & 1) ? m[3] : m[2];
-                const uint32_t u45 = (g8 & 1) ? m[5] : m[4], u67 = (g8 & 1) ? m[7] : m[6];
-                const uint32_t u03 = (g8 & 2) ? u23 : u01, u47 = (g8 & 2) ? u67 : u45;
-                const uint32_t uo = (g8 & 4) ? u47 : u03;
+                    for (int r = 0; r < 8; r++) m[r] = __builtin_amdgcn_readfirstlane(mu[sp][r]);
+                    const uint32_t u01 = (g8 & 1) ? m[1] : m[0], u23 = (g8 & 1) ? m[3] : m[2];
+                    const uint32_t u45 = (g8 & 1) ? m[5] : m[4], u67 = (g8 & 1) ? m[7] : m[6];
+                    const uint32_t u03 = (g8 & 2) ? u23 : u01, u47 = (g8 & 2) ? u67 : u45;
+                    uo = (g8 & 4) ? u47 : u03;
+                }
                 const char* bsrc = (in && uo != kNoEntry && bcol >= 0) ? Bg + uo + bcol : Zg;
                 dma_x4(bsrc, lds_addr(slot + KS * kDnATileBytes + sp * kDnBTileBytes + 8 * pw * (kDmaBRow * 2)));
             }
-            load_meta(n + 2, mu);
+            if constexpr (!kNatural) load_meta(n + 2, mu);
             wait_vmcnt<kDnWait>();  // tile i + 2 has landed
             // A plain barrier: this wavefront has no LDS instruction to order.
             __builtin_amdgcn_s_barrier();
         };
         uint32_t mu0[KS][8], mu1[KS][8];
-        load_meta(0, mu0);
-        load_meta(1, mu1);
+        if constexpr (!kNatural) {
+            load_meta(0, mu0);
+            load_meta(1, mu1);
+        }
         int i = -LB;
         for (; i + 1 < niters; i += 2) {
             iteration(i, mu0);

@@ -102,6 +102,7 @@ struct MfmaArgs {
     const i32x2v* emeta;     // [global step] {first word of the packed block, groups of 64 entries} (paired kernel)
     const void* adense;      // [global step] dense A tile, 8 KiB in fragment order (dense kernel)
     int n_windows;           // windows (dense kernel: its workgroup -> window mapping)
+    int K;                   // rows of B (dense kernel, windows in natural column order)
 };
 
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;

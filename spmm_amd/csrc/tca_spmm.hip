@@ -18,6 +18,7 @@
 #include "bell_kernel.hpp"
 #include "sparse24_kernel.hpp"
 #include "device_planner.hpp"
+#include "mfma_sparse_kernel.hpp"
 
 #include <hipcub/hipcub.hpp>
 #include "sddmm_kernel.hpp"
@@ -42,6 +43,9 @@ struct tca_spmm_plan {
     bool mfma_dma = false;   // LDS-DMA tile kernel instead of the register-staged one
     bool mfma_pair = false;  // paired (MFMA + staging wavefront) tile kernel
     bool mfma_dense = false; // dense-tile kernel (plan keeps dense condensed windows)
+    bool mfma_sparse = false; // 2:4-grouped windows on the sparse matrix cores
+    bool mfma_natural = false; // dense kernel: windows span all of K in column order (B rows contiguous)
+    int32_t n_windows24 = 0;  // windows of the 2:4 plan
     uint16_t* d_adense = nullptr;  // dense kernel: [global step] 8 KiB A tile, then 1 KiB of zeros
     size_t adense_halves = 0;
     int32_t n_dn = 0;              // dense kernel: nonzeros the pack writes
@@ -160,7 +164,7 @@ int launch_rows_e(const tca_spmm_plan* p, const void* val, const void* B, float*
 
 // Pairs the MFMA entries with this run's values (before the tile kernel).
 void launch_pack(const tca_spmm_plan* p, const void* val, hipStream_t s) {
-    if (p->mfma_dense) {
+    if (p->mfma_dense || p->mfma_sparse) {
         if (p->n_dn > 0)
             hipLaunchKernelGGL(dense_pack_kernel, dim3((p->n_dn + 255) / 256), dim3(256), 0, s, p->d_dn_src,
                                p->d_dn_pos, p->n_dn, static_cast<const uint16_t*>(val), p->d_adense);
@@ -200,13 +204,29 @@ int launch_mfma(const tca_spmm_plan* p, const void* B, float* C, hipStream_t s) 
     a.eoff_bytes = static_cast<uint32_t>(p->mfma.eoff.size() * 4);
     const dim3 grid(static_cast<unsigned>(p->mfma.windows.size()) * p->mfma_col_blocks);
     const bool bf = p->dtype == TCA_BF16;
+    if (p->mfma_sparse) {
+        a.adense = p->d_adense;
+        a.packed = p->d_packed;  // index words
+        a.zeros = p->d_adense + (p->adense_halves - 512);
+        a.n_windows = p->n_windows24;
+        const dim3 sgrid(mfma_dense_grid(a.n_windows, p->mfma_col_blocks));
+        if (bf) hipLaunchKernelGGL((mfma_sparse_kernel<true>), sgrid, dim3(kSpThreads), 0, s, a);
+        else hipLaunchKernelGGL((mfma_sparse_kernel<false>), sgrid, dim3(kSpThreads), 0, s, a);
+        return TCA_OK;
+    }
     if (p->mfma_dense) {
         a.adense = p->d_adense;
         a.zeros = p->d_adense + (p->adense_halves - 512);
         a.n_windows = static_cast<int>(p->mfma.windows.size());
+        a.K = p->K;
         const dim3 dgrid(mfma_dense_grid(a.n_windows, p->mfma_col_blocks));
-        if (bf) hipLaunchKernelGGL((mfma_dense_kernel<true>), dgrid, dim3(kDnThreads), 0, s, a);
-        else hipLaunchKernelGGL((mfma_dense_kernel<false>), dgrid, dim3(kDnThreads), 0, s, a);
+        if (p->mfma_natural) {
+            if (bf) hipLaunchKernelGGL((mfma_dense_kernel<true, true>), dgrid, dim3(kDnThreads), 0, s, a);
+            else hipLaunchKernelGGL((mfma_dense_kernel<false, true>), dgrid, dim3(kDnThreads), 0, s, a);
+        } else {
+            if (bf) hipLaunchKernelGGL((mfma_dense_kernel<true, false>), dgrid, dim3(kDnThreads), 0, s, a);
+            else hipLaunchKernelGGL((mfma_dense_kernel<false, false>), dgrid, dim3(kDnThreads), 0, s, a);
+        }
         return TCA_OK;
     }
     if (p->mfma_pair) {
@@ -298,10 +318,12 @@ void fill_info(tca_spmm_plan* p) {
     in.rows_mfma = p->mfma.rows;
     in.nnz_mfma = p->mfma.nnz;
     in.cond_cols_mfma = p->mfma.cond_cols;
-    in.mfma_blocks = p->mfma_dense ? mfma_dense_grid(in.n_windows_mfma, p->mfma_col_blocks)
+    in.mfma_blocks = (p->mfma_dense || p->mfma_sparse) ? mfma_dense_grid(in.n_windows_mfma, p->mfma_col_blocks)
                                    : in.n_windows_mfma * p->mfma_col_blocks;
     in.mfma_blockdim = kMfmaThreads;
-    if (p->mfma_dense)
+    if (p->mfma_sparse)
+        in.mfma_lds_bytes = mfma_sparse_lds_bytes();
+    else if (p->mfma_dense)
         in.mfma_lds_bytes = mfma_dense_lds_bytes();
     else if (p->mfma_pair)
         in.mfma_lds_bytes = mfma_pair_lds_bytes();
@@ -310,6 +332,12 @@ void fill_info(tca_spmm_plan* p) {
     else
         in.mfma_lds_bytes = p->mfma_slots == 1 ? mfma_lds_bytes<1>() : p->mfma_slots == 2 ? mfma_lds_bytes<2>() : mfma_lds_bytes<4>();
     in.scratch_bytes = static_cast<int64_t>(p->n_seg_total * p->N * sizeof(float));
+    in.tile_kernel = p->mfma.windows.empty() ? TCA_TILES_NONE
+                     : p->mfma_sparse       ? TCA_TILES_SPARSE
+                     : p->mfma_dense        ? (p->mfma_natural ? TCA_TILES_DENSE_K : TCA_TILES_DENSE)
+                     : p->mfma_pair         ? TCA_TILES_PAIR
+                     : (p->mfma_dma && p->mfma_slots <= 2) ? TCA_TILES_DMA
+                                                           : TCA_TILES_REGS;
 }
 
 }  // namespace
@@ -392,6 +420,16 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
               min_density, *shape, &p->mfma);
     p->mfma_dma = (flags & TCA_PLAN_MFMA_REGS) == 0 && (flags & TCA_PLAN_MFMA_DMA) != 0;
     p->mfma_dense = (flags & (TCA_PLAN_MFMA_REGS | TCA_PLAN_MFMA_DMA)) == 0 && (flags & TCA_PLAN_MFMA_DENSE) != 0;
+    if ((flags & (TCA_PLAN_MFMA_REGS | TCA_PLAN_MFMA_DMA | TCA_PLAN_MFMA_DENSE | TCA_PLAN_MFMA_SPARSE |
+                  TCA_PLAN_MFMA_PAIR)) == 0 &&
+        !p->mfma.windows.empty() &&
+        static_cast<double>(p->mfma.cond_cols) >= kNaturalCover * static_cast<double>(p->mfma.windows.size()) * K &&
+        p->mfma.windows.size() * static_cast<size_t>((K + 31) / 32) * kDnATileBytes <= kDenseMaxBytes) {
+        // Default kernel choice: windows that cover most of K run on the dense
+        // tiles in natural column order (measured on MI355X, config 1:
+        // 34.5 us per SpMM against 36.8 us for the paired kernel).
+        p->mfma_dense = true;
+    }
     if (p->mfma_dense && (p->mfma.eoff.size() - 1) * static_cast<size_t>(kDnATileBytes) > kDenseMaxBytes) {
         // Dense windows past the budget: the paired kernel, which keeps only the entries.
         p->mfma_dense = false;
@@ -399,7 +437,20 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
         plan_mfma(rowptr, colidx, M, N, dtype, (flags & TCA_PLAN_FORCE_MFMA) != 0, (flags & TCA_PLAN_NO_MFMA) != 0,
                   min_density, *shape, &p->mfma);
     }
-    p->mfma_pair = (flags & (TCA_PLAN_MFMA_REGS | TCA_PLAN_MFMA_DMA)) == 0 && !p->mfma_dense;
+    p->mfma_sparse = (flags & (TCA_PLAN_MFMA_REGS | TCA_PLAN_MFMA_DMA | TCA_PLAN_MFMA_DENSE)) == 0 &&
+                     (flags & TCA_PLAN_MFMA_SPARSE) != 0;
+    Mfma24Plan m24;
+    if (p->mfma_sparse && !p->mfma.windows.empty()) {
+        plan_mfma24(p->mfma, rowptr, colidx, &m24);
+        const size_t steps24 = m24.windows.empty() ? 0 : static_cast<size_t>(m24.windows.back().z + m24.windows.back().y);
+        if (steps24 * (kSpATile + kSpITile) > kDenseMaxBytes) {
+            p->mfma_sparse = false;  // past the budget: the paired kernel
+            shape = &kMfmaDmaShape;
+            plan_mfma(rowptr, colidx, M, N, dtype, (flags & TCA_PLAN_FORCE_MFMA) != 0, (flags & TCA_PLAN_NO_MFMA) != 0,
+                      min_density, *shape, &p->mfma);
+        }
+    }
+    p->mfma_pair = (flags & (TCA_PLAN_MFMA_REGS | TCA_PLAN_MFMA_DMA)) == 0 && !p->mfma_dense && !p->mfma_sparse;
     p->mfma_col_blocks = (N + shape->tile_cols - 1) / shape->tile_cols;
     {
         int32_t most = 0;
@@ -443,16 +494,73 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
         if ((st = dev_upload(&p->d_ucols, uoff.data(), uoff.size()))) return bail(st);
         if ((st = dev_upload(&p->d_eoff, p->mfma.eoff.data(), p->mfma.eoff.size()))) return bail(st);
     }
-    if (!p->mfma.windows.empty() && p->mfma_dense) {
+    if (!p->mfma.windows.empty() && p->mfma_sparse) {
+        // 2:4 windows: their own window table and 64-column steps of B rows;
+        // compressed value tiles (zero, values written per run), fixed index
+        // words, 1 KiB of zeros after the value tiles.
+        (void)hipFree(p->d_windows);
+        (void)hipFree(p->d_ucols);
+        p->d_windows = nullptr;
+        p->d_ucols = nullptr;
+        p->n_windows24 = static_cast<int32_t>(m24.windows.size());
+        p->mfma.cond_cols = static_cast<int64_t>(m24.cols.size());  // padded 2:4 condensed columns
+        if ((st = dev_upload(&p->d_windows, m24.windows.data(), m24.windows.size()))) return bail(st);
+        std::vector<uint32_t> uoff(m24.cols.size());
+        for (size_t i = 0; i < uoff.size(); i++)
+            uoff[i] = m24.cols[i] < 0 ? kNoEntry : static_cast<uint32_t>(m24.cols[i]) * static_cast<uint32_t>(N) * 2u;
+        if ((st = dev_upload(&p->d_ucols, uoff.data(), uoff.size()))) return bail(st);
+        const size_t steps24 = m24.cols.size() / kSpStepK;
+        p->adense_halves = steps24 * (kSpATile / 2) + 512;
+        if ((st = dev_upload(&p->d_adense, nullptr, p->adense_halves))) return bail(st);
+        if (hipMemset(p->d_adense, 0, p->adense_halves * 2) != hipSuccess)
+            return bail(fail(TCA_ERR_HIP, "hipMemset of the compressed tiles failed"));
+        if ((st = dev_upload(&p->d_packed, m24.idx.data(), m24.idx.size()))) return bail(st);
+        std::vector<int32_t> dsrc(m24.pos.size());
+        std::vector<uint32_t> dpos(m24.pos.size());
+        for (size_t x = 0; x < m24.pos.size(); x++) {
+            dpos[x] = m24.pos[x].first;
+            dsrc[x] = m24.pos[x].second;
+        }
+        p->n_dn = static_cast<int32_t>(dsrc.size());
+        if ((st = dev_upload(&p->d_dn_src, dsrc.data(), dsrc.size()))) return bail(st);
+        if ((st = dev_upload(&p->d_dn_pos, dpos.data(), dpos.size()))) return bail(st);
+    } else if (!p->mfma.windows.empty() && p->mfma_dense) {
         // Dense condensed windows: 8 KiB per global step (128 rows x 32
         // condensed columns in fragment order), zero except at the entries,
         // whose values the pack kernel writes each run; 1 KiB of zeros after
         // them (the B source for padding rows).  Entries sorted by position.
-        const size_t nsteps_all = p->mfma.eoff.size() - 1;
-        p->adense_halves = nsteps_all * static_cast<size_t>(kDmaATile) + 512;
+        // Windows whose column unions cover most of K (on average >= 85 %) keep
+        // their columns in natural order instead: every window spans all of K,
+        // step j holds columns 32 j .. 32 j + 31, so the kernel's B rows are
+        // contiguous and need no row-offset table.
+        const int32_t ksteps = (K + 31) / 32;
+        const size_t nwin = p->mfma.windows.size();
+        p->mfma_natural = static_cast<double>(p->mfma.cond_cols) >= kNaturalCover * static_cast<double>(nwin) * K &&
+                          nwin * static_cast<size_t>(ksteps) * kDnATileBytes <= kDenseMaxBytes;
         std::vector<std::pair<uint32_t, int32_t>> ent;
         ent.reserve(p->mfma.entries.size());
-        for (size_t w = 0, e = 0; w < p->mfma.windows.size(); w++) {
+        if (p->mfma_natural) {
+            std::vector<Int4> wn(nwin);
+            for (size_t w = 0; w < nwin; w++) {
+                const Int4 win = p->mfma.windows[w];
+                wn[w] = {win.x, ksteps, static_cast<int32_t>(w) * ksteps, win.w};
+                const int32_t r1 = std::min(M, win.x + kDmaWinRows);
+                for (int32_t r = win.x; r < r1; r++)
+                    for (int32_t j = rowptr[r]; j < rowptr[r + 1]; j++) {
+                        const int32_t c = colidx[j];
+                        ent.emplace_back(static_cast<uint32_t>(wn[w].z + c / 32) * kDmaATile +
+                                             static_cast<uint32_t>(a_cell(r - win.x, c % 32)),
+                                         j);
+                    }
+            }
+            (void)hipFree(p->d_windows);
+            p->d_windows = nullptr;
+            if ((st = dev_upload(&p->d_windows, wn.data(), wn.size()))) return bail(st);
+            p->mfma.cond_cols = static_cast<int64_t>(nwin) * ksteps * 32;
+        }
+        const size_t nsteps_all = p->mfma_natural ? nwin * static_cast<size_t>(ksteps) : p->mfma.eoff.size() - 1;
+        p->adense_halves = nsteps_all * static_cast<size_t>(kDmaATile) + 512;
+        for (size_t w = 0, e = 0; w < p->mfma.windows.size() && !p->mfma_natural; w++) {
             const Int4 win = p->mfma.windows[w];
             for (int32_t g = win.z; g < win.z + win.y; g++)
                 for (; e < static_cast<size_t>(p->mfma.eoff[g + 1]); e++) {

@@ -137,8 +137,9 @@ def test_exact_bit_equal_all_widths(torch_cuda, dtype):
         assert np.array_equal(got, want), (dtype, n, np.abs(got - want).max())
 
 
-@pytest.mark.parametrize("variant", [S.TCA_PLAN_MFMA_REGS, S.TCA_PLAN_MFMA_DMA, 0, S.TCA_PLAN_MFMA_DENSE],
-                         ids=["regs", "dma", "pair", "dense"])
+@pytest.mark.parametrize("variant", [S.TCA_PLAN_MFMA_REGS, S.TCA_PLAN_MFMA_DMA, S.TCA_PLAN_MFMA_PAIR, 0,
+                                     S.TCA_PLAN_MFMA_DENSE, S.TCA_PLAN_MFMA_SPARSE],
+                         ids=["regs", "dma", "pair", "default", "dense", "sparse"])
 @pytest.mark.parametrize("dtype", [S.TCA_F16, S.TCA_BF16])
 def test_mfma_exact_bit_equal(torch_cuda, dtype, variant):
     """Condensed-tile MFMA path (forced on every eligible window) is bit-equal
@@ -163,6 +164,9 @@ def test_mfma_exact_bit_equal(torch_cuda, dtype, variant):
                 info = pl.info()
                 got = run_gpu(torch_cuda, a, b, plan=pl)
             assert info["n_windows_mfma"] > 0 or (variant != S.TCA_PLAN_MFMA_REGS and (m, k, p) in dense), (m, k, n)
+            want_kernel = {S.TCA_PLAN_MFMA_REGS: {1}, S.TCA_PLAN_MFMA_DMA: {2, 1}, S.TCA_PLAN_MFMA_PAIR: {3},
+                           0: {3, 5}, S.TCA_PLAN_MFMA_DENSE: {4, 5}, S.TCA_PLAN_MFMA_SPARSE: {6}}[variant]
+            assert info["tile_kernel"] in want_kernel or info["n_windows_mfma"] == 0, (variant, info["tile_kernel"])
             want = oracle_c(a, b)
             assert np.array_equal(got, want), (m, k, p, n, np.abs(got - want).max())
 
