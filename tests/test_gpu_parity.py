@@ -154,7 +154,7 @@ def test_mfma_exact_bit_equal(torch_cuda, dtype, variant):
     rng = np.random.default_rng(71 + dtype)
     dense = {(200, 64, 0.45), (128, 2048, 0.2), (64, 1500, 0.4)}
     for m, k, p in [(64, 256, 0.1), (130, 700, 0.05), (200, 64, 0.45), (17, 40, 0.3), (96, 5000, 0.004),
-                    (128, 2048, 0.2), (64, 1500, 0.4), (128, 2048, 0.1), (100, 1000, 0.12)]:
+                    (128, 2048, 0.2), (64, 1500, 0.4), (128, 2048, 0.1), (100, 1000, 0.12), (150, 30, 0.1)]:
         lens = rng.binomial(k, p, m)
         lens[rng.random(m) < 0.1] = 0
         a = make_csr(rng, lens, k, dtype)
@@ -309,7 +309,8 @@ def test_config_full_size_large(torch_cuda, cfg):
 
 def test_phase_timing_reports_the_kernels_a_plan_uses(torch_cuda):
     """tca_spmm_time_phases: a phase the plan does not use reads 0, the used
-    ones are positive, and the run afterwards is still exact."""
+    ones are positive, and C holds the exact product afterwards (default
+    MFMA plan, paired-kernel plan, row-kernel plan)."""
     torch = torch_cuda
     rng = np.random.default_rng(97)
     a, _ = S.gen_bernoulli(256, 512, 0.08, seed=9, dtype=S.TCA_F16)
@@ -318,7 +319,9 @@ def test_phase_timing_reports_the_kernels_a_plan_uses(torch_cuda):
     dev = torch.device("cuda:0")
     val = torch.from_numpy(a.values.view(np.int16)).to(dev)
     bd = torch.from_numpy(b.view(np.int16)).to(dev)
-    for flags, used in ((S.TCA_PLAN_FORCE_MFMA, {"pack", "tiles"}), (S.TCA_PLAN_NO_MFMA, {"rows"})):
+    for flags, used in ((S.TCA_PLAN_FORCE_MFMA, {"pack", "tiles"}),
+                        (S.TCA_PLAN_FORCE_MFMA | S.TCA_PLAN_MFMA_PAIR, {"pack", "tiles"}),
+                        (S.TCA_PLAN_NO_MFMA, {"rows"})):
         c = torch.zeros((a.nrow, 256), dtype=torch.float32, device=dev)
         with S.Plan(a, 256, flags) as pl:
             ph = pl.time_phases(val, bd, c, warmup=1, iters=3)
