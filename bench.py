@@ -217,10 +217,23 @@ def main():
             if time.perf_counter() - tc0 > args.cpu_seconds or len(times) >= 200:
                 break
         tmed = float(np.median(times))
+        # the same product on one thread, on the leading rows holding ~1/8 of the sample
+        rows1 = max(1, int(np.searchsorted(rp, s_nnz // 8, side="right") - 1))
+        nnz1 = int(rp[rows1])
+        times1 = []
+        tc0 = time.perf_counter()
+        while nnz1 > 0:
+            t1 = time.perf_counter()
+            oracle.csr_spmm(rp[:rows1 + 1], a.colidx[:nnz1], vf[:nnz1], bf, 1)
+            times1.append(time.perf_counter() - t1)
+            if time.perf_counter() - tc0 > args.cpu_seconds / 2 or len(times1) >= 50:
+                break
         cpu = {"value": round(2.0 * s_nnz * n / tmed / 1e9, 3), "unit": "GFLOP/s", "cores": threads,
                "kind": "port",
                "sample": f"oracle CSR SpMM (fp32 mul+add, k ascending) on rows [0,{rows}) = {s_nnz} nnz of the "
-                         f"same matrix, N={n}, median of {len(times)} runs"}
+                         f"same matrix, N={n}, median of {len(times)} runs",
+               "value_1thread": round(2.0 * nnz1 * n / float(np.median(times1)) / 1e9, 3) if times1 else None,
+               "sample_1thread": f"same, 1 thread, rows [0,{rows1}) = {nnz1} nnz, median of {len(times1)} runs"}
         log("cpu baseline:", json.dumps(cpu))
 
     out = {
