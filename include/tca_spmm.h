@@ -176,16 +176,26 @@ int tca_spmm_24(const void* d_vals, const uint16_t* d_meta, int32_t M, int32_t K
                 const void* d_B, float* d_C, void* stream);
 
 /* Planning on the GPU from a device-resident CSR (d_rowptr [M+1], d_colidx
- * [nnz], sorted columns), with no host copy of the structure: the plan's
- * row-kernel task list is built by device kernels (row lengths, a stable
- * descending radix sort, category bounds, a segment scan, task emission)
- * and equals the host planner's plan with TCA_PLAN_NO_MFMA, task for task.
- * The structure is validated on the device (TCA_ERR_INVALID as the host
- * planner).  Only row-kernel plans: the MFMA flags give TCA_ERR_UNSUPPORTED.
- * The plan copies the structure; the caller's buffers may be freed after
- * the call, which synchronises `stream`.  Replaces reference
- * workload_manager (src/our_spmm.cu:353-477), which plans on the host from
- * host arrays on every call. */
+ * [nnz], sorted columns), with no host copy of the structure.  The matrix-core
+ * windows are routed by the host planner's rule from statistics computed on
+ * the device (column-union bitmaps of the 128-row windows, union sizes,
+ * nonzeros per condensed step; a few integers per window come back) and,
+ * for the routed windows, the dense tiles are laid out on the device: in
+ * natural column order when the windows cover most of K (the host default,
+ * TCA_TILES_DENSE_K), else condensed (TCA_TILES_DENSE; the host default
+ * there is the paired kernel, whose layout only the host builds).  The
+ * row-kernel task list of the other rows is built by device kernels (row
+ * lengths, a stable descending radix sort, category bounds, a segment scan,
+ * task emission).  With TCA_PLAN_NO_MFMA, TCA_PLAN_MFMA_DENSE (optionally
+ * with TCA_PLAN_FORCE_MFMA), or by default when the windows cover most of K,
+ * the plan equals the host planner's for the same flags, entry for entry.
+ * TCA_PLAN_MFMA_REGS, _DMA, _PAIR and _SPARSE give TCA_ERR_UNSUPPORTED;
+ * window tables above 2^25 words (windows x ceil(K / 32)) leave every row on
+ * the row kernel.  The structure is validated on the device
+ * (TCA_ERR_INVALID as the host planner).  The plan copies the structure;
+ * the caller's buffers may be freed after the call, which synchronises
+ * `stream`.  Replaces reference workload_manager (src/our_spmm.cu:353-477),
+ * which plans on the host from host arrays on every call. */
 int tca_spmm_plan_create_device(const int32_t* d_rowptr, const int32_t* d_colidx, int32_t M, int32_t K, int32_t nnz,
                                 int32_t N, int32_t dtype, uint32_t flags, void* stream, tca_spmm_plan** plan);
 
@@ -195,6 +205,17 @@ int tca_spmm_plan_create_device(const int32_t* d_rowptr, const int32_t* d_colidx
  * reference: for tests and tools comparing plans. */
 int tca_spmm_plan_export_rows(const tca_spmm_plan* plan, int32_t* n_tasks, int32_t* n_perm, int32_t* n_long,
                               int32_t* tasks, int32_t* perm, int32_t* longrows);
+
+/* The dense-tile data of a plan whose tile kernel is TCA_TILES_DENSE or
+ * TCA_TILES_DENSE_K, copied to the host: the windows ({first row, steps,
+ * first global step, first nonzero} as 4 int32 each), per routed nonzero its
+ * half index in the dense tiles and its CSR index (sorted by position), and
+ * for condensed tiles the B row byte offsets of every step's 32 columns
+ * (0xffffffff padding; none for natural order).  With windows == NULL only
+ * the counts are returned; other plans report zero counts.  No counterpart
+ * in the reference: for tests and tools comparing plans. */
+int tca_spmm_plan_export_tiles(const tca_spmm_plan* plan, int32_t* n_windows, int32_t* n_entries, int32_t* n_ucols,
+                               int32_t* windows, uint32_t* pos, int32_t* src, uint32_t* ucols);
 
 int tca_spmm_plan_info(const tca_spmm_plan* plan, tca_plan_info* info);
 

@@ -400,6 +400,21 @@ class Plan:
              np_ptr(tasks, ctypes.c_int32), np_ptr(perm, ctypes.c_int32), np_ptr(longrows, ctypes.c_int32))
         return tasks[:nt.value], perm[:npm.value], longrows[:nl.value]
 
+    def export_tiles(self):
+        """The dense-tile data (windows [W, 4], entry positions, entry CSR
+        indices, B row offsets of condensed columns) as numpy arrays."""
+        nw, ne, nu = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
+        call("tca_spmm_plan_export_tiles", self._p, ctypes.byref(nw), ctypes.byref(ne), ctypes.byref(nu),
+             None, None, None, None)
+        win = np.zeros((max(nw.value, 1), 4), np.int32)
+        pos = np.zeros(max(ne.value, 1), np.uint32)
+        src = np.zeros(max(ne.value, 1), np.int32)
+        ucols = np.zeros(max(nu.value, 1), np.uint32)
+        call("tca_spmm_plan_export_tiles", self._p, ctypes.byref(nw), ctypes.byref(ne), ctypes.byref(nu),
+             np_ptr(win, ctypes.c_int32), np_ptr(pos, ctypes.c_uint32), np_ptr(src, ctypes.c_int32),
+             np_ptr(ucols, ctypes.c_uint32))
+        return win[:nw.value], pos[:ne.value], src[:ne.value], ucols[:nu.value]
+
     def info(self) -> dict:
         i = _lib.TcaPlanInfo()
         call("tca_spmm_plan_info", self._p, ctypes.byref(i))

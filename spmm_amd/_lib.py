@@ -28,6 +28,7 @@ u32 = ctypes.c_uint32
 u64 = ctypes.c_uint64
 vp = ctypes.c_void_p
 i32p = ctypes.POINTER(ctypes.c_int32)
+u32p = ctypes.POINTER(ctypes.c_uint32)
 i64p = ctypes.POINTER(ctypes.c_int64)
 f32p = ctypes.POINTER(ctypes.c_float)
 
@@ -83,6 +84,7 @@ SIGNATURES = {
     "tca_spmm_24": (i32, [vp, vp, i32, i32, i32, i32, vp, vp, vp]),
     "tca_spmm_plan_create_device": (i32, [vp, vp, i32, i32, i32, i32, i32, u32, vp, ctypes.POINTER(vp)]),
     "tca_spmm_plan_export_rows": (i32, [vp, i32p, i32p, i32p, i32p, i32p, i32p]),
+    "tca_spmm_plan_export_tiles": (i32, [vp, i32p, i32p, i32p, i32p, u32p, i32p, u32p]),
     "tca_spmm_plan_info": (i32, [vp, ctypes.POINTER(TcaPlanInfo)]),
     "tca_spmm_plan_destroy": (i32, [vp]),
     "tca_spmm_host": (i32, [i32p, i32p, vp, i32, i32, i32, vp, f32p, i32, i32, i32, i32,

@@ -8,13 +8,26 @@
 //   [4 W + S, .. + R)     one task per medium row,
 //   then                  groups of `slots` consecutive short rows.
 // Long rows come first in the order, then wide, medium and short rows, so
-// the category boundaries are three positions in the sorted lengths.
+// the category boundaries are three positions in the sorted lengths.  The
+// sort keys are length + 1, and 0 for the rows of the windows routed to the
+// matrix cores, which so sort last and are left out (the first Mp rows of
+// the order are planned).
+//
+// MFMA windows (plan_mfma in planner.cpp, the same routing through
+// route_windows) from per-window statistics computed here: the column union
+// of each 128-row window as a bitmap, its size and the exclusive popcount
+// prefix of its words (a column's condensed position is the prefix of its
+// word plus the set bits below it in the word), and the nonzeros of every
+// 32-column condensed step.  For the routed windows the dense-tile
+// positions of the nonzeros (natural column order, or condensed) and the B
+// row offsets of the condensed columns are written here too.
 #pragma once
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 #include "planner.hpp"
+#include "mfma_dma_kernel.hpp"
 
 namespace tca {
 
@@ -42,17 +55,20 @@ __global__ void dp_check_cols_kernel(const int* __restrict__ colidx, int nnz, in
     }
 }
 
-// keys = row lengths, vals = row ids (the radix sort's input)
-__global__ void dp_lengths_kernel(const int* __restrict__ rowptr, int M, uint32_t* __restrict__ keys,
-                                  int* __restrict__ rows) {
+// keys = row lengths + 1 (0 for rows of routed windows: wmap[r / 128] >= 0),
+// vals = row ids (the radix sort's input).  wmap may be NULL.
+__global__ void dp_lengths_kernel(const int* __restrict__ rowptr, int M, const int* __restrict__ wmap,
+                                  uint32_t* __restrict__ keys, int* __restrict__ rows) {
     for (int r = blockIdx.x * blockDim.x + threadIdx.x; r < M; r += gridDim.x * blockDim.x) {
-        keys[r] = static_cast<uint32_t>(rowptr[r + 1] - rowptr[r]);
+        const bool tiles = wmap && wmap[r / kDmaWinRows] >= 0;
+        keys[r] = tiles ? 0u : static_cast<uint32_t>(rowptr[r + 1] - rowptr[r]) + 1u;
         rows[r] = r;
     }
 }
 
-// Boundaries in the descending lengths: out[0] = rows longer than wide_len,
-// out[1] = longer than row_len, out[2] = longer than multi_max.
+// Boundaries in the first M descending keys (length + 1): out[0] = rows
+// longer than wide_len, out[1] = longer than row_len, out[2] = longer than
+// multi_max.
 __global__ void dp_bounds_kernel(const uint32_t* __restrict__ len, int M, int wide_len, int row_len, int multi_max,
                                  int* __restrict__ out) {
     const int th[3] = {wide_len, row_len, multi_max};
@@ -65,7 +81,7 @@ __global__ void dp_bounds_kernel(const uint32_t* __restrict__ len, int M, int wi
     int lo = 0, hi = M;  // first index whose length <= th[k]
     while (lo < hi) {
         const int mid = lo + (hi - lo) / 2;
-        if (static_cast<int64_t>(len[mid]) > th[k]) lo = mid + 1;
+        if (static_cast<int64_t>(len[mid]) - 1 > th[k]) lo = mid + 1;
         else hi = mid;
     }
     out[k] = lo;
@@ -74,18 +90,18 @@ __global__ void dp_bounds_kernel(const uint32_t* __restrict__ len, int M, int wi
 // segments of each long row (n_long of them, the first in the order)
 __global__ void dp_nseg_kernel(const uint32_t* __restrict__ len, int n_long, int seg_len, int* __restrict__ nseg) {
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n_long; i += gridDim.x * blockDim.x)
-        nseg[i] = (static_cast<int>(len[i]) + seg_len - 1) / seg_len;
+        nseg[i] = (static_cast<int>(len[i]) - 1 + seg_len - 1) / seg_len;
 }
 
 struct DpEmitArgs {
     const int* rowptr;
-    const uint32_t* len;  // sorted lengths
+    const uint32_t* len;  // sorted keys (length + 1)
     const int* rows;      // rows in that order
     const int* segoff;    // first segment slot of each long row (exclusive sum)
     int4* tasks;
     int* perm;
     int4* longrows;
-    int M, n_long, end_wide, end_row, slots, seg_total;
+    int M, n_long, end_wide, end_row, slots, seg_total;  // M: the rows planned (Mp)
 };
 
 // Every row of the order writes its own tasks (see the file comment).
@@ -93,7 +109,7 @@ __global__ void dp_emit_kernel(DpEmitArgs a) {
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < a.M; i += gridDim.x * blockDim.x) {
         const int r = a.rows[i];
         const int beg = a.rowptr[r];
-        const int64_t L = a.len[i];
+        const int64_t L = static_cast<int64_t>(a.len[i]) - 1;
         const int n_wide = a.end_wide - a.n_long;
         if (i < a.n_long) {
             const int off = a.segoff[i];
@@ -120,6 +136,155 @@ __global__ void dp_emit_kernel(DpEmitArgs a) {
                 a.tasks[4 * n_wide + a.seg_total + (a.end_row - a.end_wide) + g] =
                     make_int4(k, cnt, static_cast<int>(L), kTaskMulti);
             }
+        }
+    }
+}
+
+// ---------------- MFMA windows ----------------
+
+// Column-union bitmaps: bit c % 32 of bm[w * kw + c / 32] for every column c
+// of window w (rows 128 w .. 128 w + 127).  One wavefront per row.
+__global__ void dm_bitmap_kernel(const int* __restrict__ rowptr, const int* __restrict__ colidx, int M, int kw,
+                                 uint32_t* __restrict__ bm) {
+    const int lane = threadIdx.x & 63;
+    const int waves = (gridDim.x * blockDim.x) >> 6;
+    for (int r = (blockIdx.x * blockDim.x + threadIdx.x) >> 6; r < M; r += waves) {
+        uint32_t* const b = bm + static_cast<size_t>(r / kDmaWinRows) * kw;
+        for (int j = rowptr[r] + lane; j < rowptr[r + 1]; j += 64) {
+            const int c = colidx[j];
+            atomicOr(b + (c >> 5), 1u << (c & 31));
+        }
+    }
+}
+
+// One workgroup (256 threads) per window: wrow[w] = rowptr[128 w] (and
+// wrow[nw] = rowptr[M]), wordpre = exclusive popcount prefix of the window's
+// words, ucount[w] = the union size.
+__global__ __launch_bounds__(256) void dm_union_kernel(const int* __restrict__ rowptr, int M, int nw, int kw,
+                                                       const uint32_t* __restrict__ bm, int* __restrict__ wordpre,
+                                                       int* __restrict__ ucount, int* __restrict__ wrow) {
+    const int w = blockIdx.x;
+    const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+    __shared__ int part[4];
+    __shared__ int carry;
+    if (t == 0) {
+        carry = 0;
+        wrow[w] = rowptr[w * kDmaWinRows];
+        if (w == nw - 1) wrow[nw] = rowptr[M];
+    }
+    __syncthreads();
+    const size_t wb = static_cast<size_t>(w) * kw;
+    for (int base = 0; base < kw; base += 256) {
+        const int i = base + t;
+        const int v = i < kw ? __popc(bm[wb + i]) : 0;
+        int x = v;  // inclusive scan within the wavefront
+        for (int d = 1; d < 64; d <<= 1) {
+            const int y = __shfl_up(x, d, 64);
+            if (lane >= d) x += y;
+        }
+        if (lane == 63) part[wv] = x;
+        __syncthreads();
+        int off = carry;
+        for (int k = 0; k < wv; k++) off += part[k];
+        if (i < kw) wordpre[wb + i] = off + x - v;
+        __syncthreads();
+        if (t == 255) carry = off + x;
+        __syncthreads();
+    }
+    if (t == 0) ucount[w] = carry;
+}
+
+// condensed position of column c in the window whose words start at wb
+__device__ inline int dm_cpos(const uint32_t* __restrict__ bm, const int* __restrict__ wordpre, size_t wb, int c) {
+    const uint32_t word = bm[wb + (c >> 5)];
+    return wordpre[wb + (c >> 5)] + __popc(word & ((1u << (c & 31)) - 1u));
+}
+
+// Nonzeros per condensed step: cnt[w * kw + cpos / 32] (a window has at most
+// kw steps).  One wavefront per row.
+__global__ void dm_stepcount_kernel(const int* __restrict__ rowptr, const int* __restrict__ colidx, int M, int kw,
+                                    const uint32_t* __restrict__ bm, const int* __restrict__ wordpre,
+                                    int* __restrict__ cnt) {
+    const int lane = threadIdx.x & 63;
+    const int waves = (gridDim.x * blockDim.x) >> 6;
+    for (int r = (blockIdx.x * blockDim.x + threadIdx.x) >> 6; r < M; r += waves) {
+        const size_t wb = static_cast<size_t>(r / kDmaWinRows) * kw;
+        for (int j = rowptr[r] + lane; j < rowptr[r + 1]; j += 64)
+            atomicAdd(cnt + wb + (dm_cpos(bm, wordpre, wb, colidx[j]) >> 5), 1);
+    }
+}
+
+// Most nonzeros in one step of each window (one workgroup per window).
+__global__ __launch_bounds__(256) void dm_stepmax_kernel(const int* __restrict__ cnt, int kw,
+                                                         const int* __restrict__ ucount, int* __restrict__ maxper) {
+    const int w = blockIdx.x, t = threadIdx.x;
+    const int steps = (ucount[w] + 31) / 32;
+    int m = 0;
+    for (int s = t; s < steps; s += 256) m = max(m, cnt[static_cast<size_t>(w) * kw + s]);
+    __shared__ int red[256];
+    red[t] = m;
+    __syncthreads();
+    for (int d = 128; d > 0; d >>= 1) {
+        if (t < d) red[t] = max(red[t], red[t + d]);
+        __syncthreads();
+    }
+    if (t == 0) maxper[w] = red[0];
+}
+
+struct DmEntryArgs {
+    const int* rowptr;
+    const int* colidx;
+    const uint32_t* bm;
+    const int* wordpre;
+    const int* wmap;    // [window] routed index, -1 for none
+    const int* wgbase;  // [routed index] first global step
+    uint32_t* keys;     // [nonzero] half index in the dense tiles, 0xffffffff outside routed windows
+    int* vals;          // [nonzero] its index
+    int M, kw;
+    int natural;        // windows span all of K in column order
+};
+
+// Dense-tile position of every nonzero (the dense pack's list, sorted
+// afterwards).  One wavefront per row.
+__global__ void dm_entries_kernel(DmEntryArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int waves = (gridDim.x * blockDim.x) >> 6;
+    for (int r = (blockIdx.x * blockDim.x + threadIdx.x) >> 6; r < a.M; r += waves) {
+        const int w = r / kDmaWinRows;
+        const int t = a.wmap[w];
+        const size_t wb = static_cast<size_t>(w) * a.kw;
+        for (int j = a.rowptr[r] + lane; j < a.rowptr[r + 1]; j += 64) {
+            uint32_t key = 0xffffffffu;
+            if (t >= 0) {
+                const int c = a.colidx[j];
+                const int pc = a.natural ? c : dm_cpos(a.bm, a.wordpre, wb, c);
+                const uint32_t g = static_cast<uint32_t>(a.wgbase[t] + (pc >> 5));
+                key = g * static_cast<uint32_t>(kDmaATile) + static_cast<uint32_t>(a_cell(r - w * kDmaWinRows, pc & 31));
+            }
+            a.keys[j] = key;
+            a.vals[j] = j;
+        }
+    }
+}
+
+// B row byte offsets (row * N * 2) of the condensed columns of the routed
+// windows, step by step; ucols is prefilled with 0xff bytes (padding).
+__global__ void dm_ucols_kernel(int nw, int kw, const uint32_t* __restrict__ bm, const int* __restrict__ wordpre,
+                                const int* __restrict__ wmap, const int* __restrict__ wgbase, int N,
+                                uint32_t* __restrict__ ucols) {
+    const int64_t total = static_cast<int64_t>(nw) * kw;
+    for (int64_t q = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; q < total;
+         q += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int w = static_cast<int>(q / kw), i = static_cast<int>(q % kw);
+        const int t = wmap[w];
+        if (t < 0) continue;
+        uint32_t word = bm[q];
+        int pos = wordpre[q];
+        uint32_t* const out = ucols + static_cast<size_t>(wgbase[t]) * 32;
+        while (word) {
+            const int b = __ffs(word) - 1;
+            word &= word - 1;
+            out[pos++] = static_cast<uint32_t>(32 * i + b) * static_cast<uint32_t>(N) * 2u;
         }
     }
 }

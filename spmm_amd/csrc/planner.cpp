@@ -162,30 +162,21 @@ void condense(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_t w
     }
 }
 
-void plan_mfma(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_t N, int32_t dtype, bool force,
-               bool disable, double min_density, const MfmaShape& shape, MfmaPlan* p) {
+void route_windows(const std::vector<WinStat>& st, int32_t M, int64_t nnz_total, int32_t N, bool force,
+                   double min_density, const MfmaShape& shape, std::vector<uint8_t>* take_out) {
     constexpr int32_t kStep = 32;
     const int32_t kWin = shape.win_rows, kMaxStep = shape.max_step_entries;
-    *p = MfmaPlan();
-    p->win_rows = kWin;
-    p->row_mfma.assign(M, 0);
-    if (disable || dtype == TCA_F32 || N % 8 != 0 || M == 0) return;
-    std::vector<int64_t> uoff;
-    std::vector<int32_t> ucols, cpos(rowptr[M]);
-    condense(rowptr, colidx, M, kWin, &uoff, &ucols, &cpos);
-    const int32_t nw = (M + kWin - 1) / kWin;
-    std::vector<uint8_t> take(nw, 0), ok(nw, 0);  // routed / structurally able
-#pragma omp parallel for schedule(dynamic, 16)
+    const int32_t nw = static_cast<int32_t>(st.size());
+    std::vector<uint8_t>& take = *take_out;
+    take.assign(nw, 0);
+    std::vector<uint8_t> ok(nw, 0);  // structurally able
     for (int32_t w = 0; w < nw; w++) {
         const int32_t r0 = w * kWin, r1 = std::min(M, r0 + kWin);
-        const int64_t nz = rowptr[r1] - rowptr[r0];
-        const int64_t ucount = uoff[w + 1] - uoff[w];
+        const int64_t nz = st[w].nz;
         if (nz == 0 || nz >= (int64_t(1) << 20)) continue;
-        const int64_t steps = (ucount + kStep - 1) / kStep;
+        const int64_t steps = (st[w].ucount + kStep - 1) / kStep;
         // nonzeros per step must fit the kernel's entry slots
-        std::vector<int32_t> per(steps, 0);
-        for (int32_t j = rowptr[r0]; j < rowptr[r1]; j++) per[cpos[j] / kStep]++;
-        if (*std::max_element(per.begin(), per.end()) > kMaxStep) continue;
+        if (st[w].maxper > kMaxStep) continue;
         const double density = static_cast<double>(nz) / (static_cast<double>(r1 - r0) * steps * kStep);
         ok[w] = 1;
         if (force || density >= min_density) take[w] = 1;
@@ -195,10 +186,9 @@ void plan_mfma(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_t 
         int64_t n_take = 0, nz_take = 0, max_steps = 0;
         for (int32_t w = 0; w < nw; w++) {
             if (!take[w]) continue;
-            const int32_t r0 = w * kWin, r1 = std::min(M, r0 + kWin);
             n_take++;
-            nz_take += rowptr[r1] - rowptr[r0];
-            max_steps = std::max<int64_t>(max_steps, (uoff[w + 1] - uoff[w] + kStep - 1) / kStep);
+            nz_take += st[w].nz;
+            max_steps = std::max<int64_t>(max_steps, (st[w].ucount + kStep - 1) / kStep);
         }
         const int64_t wgs = n_take * ((N + shape.tile_cols - 1) / shape.tile_cols);
         const int64_t rounds = (wgs + 255) / 256;
@@ -207,13 +197,42 @@ void plan_mfma(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_t 
         const double t_row = static_cast<double>(nz_take) * N * 2.0 / kRowGatherBytesPerUs;
         if (n_take > 0 && t_tile >= t_row) {
             std::fill(take.begin(), take.end(), 0);
-        } else if (n_take > 0 && static_cast<double>(nz_take) >= 0.95 * rowptr[M]) {
+        } else if (n_take > 0 && static_cast<double>(nz_take) >= 0.95 * nnz_total) {
             // Nearly everything goes to the tile kernel: take the remaining
             // qualifying windows too rather than launch the row kernel for a
             // few rows (the launch alone costs more than their tiles).
             std::copy(ok.begin(), ok.end(), take.begin());
         }
     }
+}
+
+void plan_mfma(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_t N, int32_t dtype, bool force,
+               bool disable, double min_density, const MfmaShape& shape, MfmaPlan* p) {
+    constexpr int32_t kStep = 32;
+    const int32_t kWin = shape.win_rows;
+    *p = MfmaPlan();
+    p->win_rows = kWin;
+    p->row_mfma.assign(M, 0);
+    if (disable || dtype == TCA_F32 || N % 8 != 0 || M == 0) return;
+    std::vector<int64_t> uoff;
+    std::vector<int32_t> ucols, cpos(rowptr[M]);
+    condense(rowptr, colidx, M, kWin, &uoff, &ucols, &cpos);
+    const int32_t nw = (M + kWin - 1) / kWin;
+    std::vector<WinStat> st(nw);
+#pragma omp parallel for schedule(dynamic, 16)
+    for (int32_t w = 0; w < nw; w++) {
+        const int32_t r0 = w * kWin, r1 = std::min(M, r0 + kWin);
+        st[w].nz = rowptr[r1] - rowptr[r0];
+        st[w].ucount = static_cast<int32_t>(uoff[w + 1] - uoff[w]);
+        st[w].maxper = 0;
+        if (st[w].nz == 0) continue;
+        const int64_t steps = (st[w].ucount + kStep - 1) / kStep;
+        std::vector<int32_t> per(steps, 0);
+        for (int32_t j = rowptr[r0]; j < rowptr[r1]; j++) per[cpos[j] / kStep]++;
+        st[w].maxper = *std::max_element(per.begin(), per.end());
+    }
+    std::vector<uint8_t> take;
+    route_windows(st, M, rowptr[M], N, force, min_density, shape, &take);
     for (int32_t w = 0; w < nw; w++) {
         if (!take[w]) continue;
         const int32_t r0 = w * kWin, r1 = std::min(M, r0 + kWin);

@@ -152,6 +152,20 @@ void plan_row_params(int64_t nnz, int32_t N, int32_t es, int32_t slices, RowPlan
 // (length > wide_len, segments of at most seg_len, summed in segment order),
 // row tasks (multi_max < length <= row_len), then groups of `slots` short
 // rows (length <= multi_max).
+// Per-window statistics the MFMA routing decides on: nonzeros, size of the
+// column union, most nonzeros in one 32-column condensed step.
+struct WinStat {
+    int64_t nz;
+    int32_t ucount;
+    int32_t maxper;
+};
+// Which windows (of shape.win_rows rows) go to the tile kernel: eligibility
+// (nonzeros per step fit the kernel, density >= min_density unless forced)
+// and the cost model against the row kernel.  Shared by the host planner
+// (plan_mfma) and the planner on the GPU (statistics computed there).
+void route_windows(const std::vector<WinStat>& st, int32_t M, int64_t nnz_total, int32_t N, bool force,
+                   double min_density, const MfmaShape& shape, std::vector<uint8_t>* take);
+
 void plan_rows(const int32_t* rowptr, int32_t M, int32_t N, int32_t es, const std::vector<uint8_t>& skip,
                int32_t slices, RowPlan* p);
 

@@ -54,6 +54,7 @@ struct tca_spmm_plan {
     int32_t mfma_groups = 0; // paired kernel: groups of 64 entries a step may hold (4 or 8)
     size_t mfma_zeros_at = 0;  // word offset of 16 zero bytes in d_packed (LDS-DMA kernel)
     size_t n_packed = 0;       // words of d_packed
+    size_t n_ucols = 0;        // words of d_ucols
     int4* d_windows = nullptr;
     uint32_t* d_ucols = nullptr;
     int* d_eoff = nullptr;
@@ -492,6 +493,7 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
                                               : static_cast<uint32_t>(p->mfma.ucols[src]) * static_cast<uint32_t>(N) * 2u;
         }
         if ((st = dev_upload(&p->d_ucols, uoff.data(), uoff.size()))) return bail(st);
+        p->n_ucols = uoff.size();
         if ((st = dev_upload(&p->d_eoff, p->mfma.eoff.data(), p->mfma.eoff.size()))) return bail(st);
     }
     if (!p->mfma.windows.empty() && p->mfma_sparse) {
@@ -671,8 +673,10 @@ int tca_spmm_plan_create_device(const int32_t* d_rowptr, const int32_t* d_colidx
     if (M < 0 || K < 1 || N < 1 || nnz < 0) return fail(TCA_ERR_INVALID, "bad shape M=%d K=%d N=%d nnz=%d", M, K, N, nnz);
     if (!dtype_ok(dtype)) return fail(TCA_ERR_INVALID, "unknown dtype %d", dtype);
     if (!d_rowptr || (nnz > 0 && !d_colidx)) return fail(TCA_ERR_INVALID, "NULL device pointer");
-    if (flags & (TCA_PLAN_FORCE_MFMA | TCA_PLAN_MFMA_REGS | TCA_PLAN_MFMA_DMA | TCA_PLAN_MFMA_DENSE))
-        return fail(TCA_ERR_UNSUPPORTED, "device planning builds row-kernel plans only (MFMA flags need the host planner)");
+    if (flags & (TCA_PLAN_MFMA_REGS | TCA_PLAN_MFMA_DMA | TCA_PLAN_MFMA_PAIR | TCA_PLAN_MFMA_SPARSE))
+        return fail(TCA_ERR_UNSUPPORTED,
+                    "device planning builds row-kernel and dense-tile plans (TCA_PLAN_MFMA_REGS, _DMA, _PAIR and "
+                    "_SPARSE need the host planner)");
     const uint64_t b_bytes = static_cast<uint64_t>(K) * static_cast<uint64_t>(N) * dtype_size(dtype);
     if (b_bytes >= 0xfffffff0ull || static_cast<uint64_t>(nnz) * 4 >= 0xfffffff0ull)
         return fail(TCA_ERR_UNSUPPORTED, "B (%llu bytes) or the nonzeros exceed the 4 GiB buffer range",
@@ -685,7 +689,7 @@ int tca_spmm_plan_create_device(const int32_t* d_rowptr, const int32_t* d_colidx
     p->N = N;
     p->nnz = nnz;
     p->dtype = dtype;
-    p->flags = flags | TCA_PLAN_NO_MFMA;
+    p->flags = flags;
     p->device_planned = true;
     p->mfma.row_mfma.clear();
     if (hipGetDevice(&p->device) != hipSuccess) {
@@ -697,14 +701,17 @@ int tca_spmm_plan_create_device(const int32_t* d_rowptr, const int32_t* d_colidx
     hipStream_t s = static_cast<hipStream_t>(stream);
 
     // temporaries of the planning, freed on every exit
-    uint32_t *keys = nullptr, *keys_s = nullptr;
+    uint32_t *keys = nullptr, *keys_s = nullptr, *bm = nullptr, *ekeys = nullptr, *ekeys_s = nullptr;
     int *rows = nullptr, *rows_s = nullptr, *cnt = nullptr, *nseg = nullptr, *segoff = nullptr;
+    int *wordpre = nullptr, *scnt = nullptr, *wstat = nullptr, *wmap = nullptr, *wgbase = nullptr, *evals = nullptr,
+        *evals_s = nullptr;
     uint8_t* start = nullptr;
     void* tmp = nullptr;
     auto bail = [&](int st) {
         (void)hipStreamSynchronize(s);
         for (void* q : {(void*)keys, (void*)keys_s, (void*)rows, (void*)rows_s, (void*)cnt, (void*)nseg, (void*)segoff,
-                        (void*)start, tmp})
+                        (void*)start, tmp, (void*)bm, (void*)ekeys, (void*)ekeys_s, (void*)wordpre, (void*)scnt,
+                        (void*)wstat, (void*)wmap, (void*)wgbase, (void*)evals, (void*)evals_s})
             (void)hipFree(q);
         if (st != TCA_OK) {
             free_plan_device(p);
@@ -733,13 +740,156 @@ int tca_spmm_plan_create_device(const int32_t* d_rowptr, const int32_t* d_colidx
         hipLaunchKernelGGL(dp_check_rows_kernel, grid_for(M), blk, 0, s, p->d_rowptr, M, nnz, start, cnt + 3);
         if (nnz > 0) hipLaunchKernelGGL(dp_check_cols_kernel, grid_for(nnz), blk, 0, s, p->d_colidx, nnz, K, start, cnt + 3);
     }
-    // rows longest first (stable descending radix sort of the lengths)
     int h_cnt[4] = {0, 0, 0, 0};
+    // the columns index the window bitmaps below: validate first
+    if (hipMemcpyAsync(h_cnt, cnt, sizeof h_cnt, hipMemcpyDeviceToHost, s) != hipSuccess ||
+        hipStreamSynchronize(s) != hipSuccess)
+        return bail(fail(TCA_ERR_HIP, "CSR checks failed"));
+    if (h_cnt[3] & 1) return bail(fail(TCA_ERR_INVALID, "CSR row offsets are not 0 .. nnz non-decreasing"));
+    if (h_cnt[3] & 2) return bail(fail(TCA_ERR_INVALID, "CSR columns out of range or not strictly ascending in a row"));
+
+    // MFMA windows: statistics on the GPU, the host planner's routing, then
+    // dense tiles (natural column order when the windows cover most of K,
+    // else condensed) built on the GPU.  Needs fp16 / bf16, N % 8 == 0 and
+    // window bitmaps of at most kDevBitmapWords words.
+    int32_t rows_mfma = 0;
+    {
+        constexpr size_t kDevBitmapWords = size_t(1) << 25;  // 128 MiB per table
+        const int nw = (M + kDmaWinRows - 1) / kDmaWinRows, kw = (K + 31) / 32;
+        if ((flags & TCA_PLAN_NO_MFMA) == 0 && dtype != TCA_F32 && N % 8 == 0 && M > 0 && nnz > 0 &&
+            static_cast<size_t>(nw) * kw <= kDevBitmapWords) {
+            const size_t nb = static_cast<size_t>(nw) * kw;
+            if ((st = dev_upload(&bm, nullptr, nb)) || (st = dev_upload(&wordpre, nullptr, nb)) ||
+                (st = dev_upload(&scnt, nullptr, nb)) || (st = dev_upload(&wstat, nullptr, 3 * static_cast<size_t>(nw) + 1)))
+                return bail(st);
+            if (hipMemsetAsync(bm, 0, nb * 4, s) != hipSuccess || hipMemsetAsync(scnt, 0, nb * 4, s) != hipSuccess)
+                return bail(fail(TCA_ERR_HIP, "hipMemsetAsync failed"));
+            int* const ucount = wstat;
+            int* const maxper = wstat + nw;
+            int* const wrow = wstat + 2 * nw;  // nw + 1
+            const dim3 rgrid(static_cast<unsigned>(std::min<int64_t>((static_cast<int64_t>(M) + 3) / 4, 65536)));
+            hipLaunchKernelGGL(dm_bitmap_kernel, rgrid, blk, 0, s, p->d_rowptr, p->d_colidx, M, kw, bm);
+            hipLaunchKernelGGL(dm_union_kernel, dim3(nw), blk, 0, s, p->d_rowptr, M, nw, kw, bm, wordpre, ucount, wrow);
+            hipLaunchKernelGGL(dm_stepcount_kernel, rgrid, blk, 0, s, p->d_rowptr, p->d_colidx, M, kw, bm, wordpre,
+                               scnt);
+            hipLaunchKernelGGL(dm_stepmax_kernel, dim3(nw), blk, 0, s, scnt, kw, ucount, maxper);
+            std::vector<int> h(3 * static_cast<size_t>(nw) + 1);
+            if (hipMemcpyAsync(h.data(), wstat, sizeof(int) * h.size(), hipMemcpyDeviceToHost, s) != hipSuccess ||
+                hipStreamSynchronize(s) != hipSuccess)
+                return bail(fail(TCA_ERR_HIP, "window statistics failed"));
+            std::vector<WinStat> ws(nw);
+            for (int w = 0; w < nw; w++)
+                ws[w] = {static_cast<int64_t>(h[2 * nw + w + 1]) - h[2 * nw + w], h[w], h[nw + w]};
+            const char* md = std::getenv("TCA_MFMA_MIN_DENSITY");
+            std::vector<uint8_t> take;
+            route_windows(ws, M, nnz, N, (flags & TCA_PLAN_FORCE_MFMA) != 0, md ? std::atof(md) : kMfmaMinDensity,
+                          mfma_shape(flags), &take);
+            // the host planner's choice between natural and condensed dense tiles
+            std::vector<int> h_wmap(nw, -1), h_base;
+            int64_t cond_cols = 0, steps_all = 0, nz_take = 0;
+            int n_take = 0;
+            for (int w = 0; w < nw; w++) {
+                if (!take[w]) continue;
+                h_wmap[w] = n_take++;
+                const int steps = (h[w] + 31) / 32;
+                h_base.push_back(static_cast<int>(steps_all));
+                steps_all += steps;
+                cond_cols += static_cast<int64_t>(steps) * 32;
+                nz_take += ws[w].nz;
+                rows_mfma += std::min(M, (w + 1) * kDmaWinRows) - w * kDmaWinRows;
+            }
+            const int32_t ksteps = (K + 31) / 32;
+            const bool natural = n_take > 0 &&
+                                 static_cast<double>(cond_cols) >= kNaturalCover * static_cast<double>(n_take) * K &&
+                                 static_cast<size_t>(n_take) * ksteps * kDnATileBytes <= kDenseMaxBytes;
+            if (natural) {
+                for (int t = 0; t < n_take; t++) h_base[t] = t * ksteps;
+                steps_all = static_cast<int64_t>(n_take) * ksteps;
+                cond_cols = steps_all * 32;
+            }
+            if (n_take > 0 && static_cast<size_t>(steps_all) * kDnATileBytes > kDenseMaxBytes) {
+                n_take = 0;  // past the dense-tile budget: every row on the row kernel
+                rows_mfma = 0;
+            }
+            if (n_take > 0) {
+                std::vector<Int4> win;
+                for (int w = 0; w < nw; w++)
+                    if (h_wmap[w] >= 0) {
+                        const int t = h_wmap[w];
+                        win.push_back({w * kDmaWinRows, natural ? ksteps : (h[w] + 31) / 32, h_base[t], h[2 * nw + w]});
+                    }
+                if ((st = dev_upload(&wmap, h_wmap.data(), h_wmap.size())) ||
+                    (st = dev_upload(&wgbase, h_base.data(), h_base.size())) ||
+                    (st = dev_upload(&p->d_windows, win.data(), win.size())) ||
+                    (st = dev_upload(&ekeys, nullptr, nnz)) || (st = dev_upload(&ekeys_s, nullptr, nnz)) ||
+                    (st = dev_upload(&evals, nullptr, nnz)) || (st = dev_upload(&evals_s, nullptr, nnz)))
+                    return bail(st);
+                DmEntryArgs ea;
+                ea.rowptr = p->d_rowptr;
+                ea.colidx = p->d_colidx;
+                ea.bm = bm;
+                ea.wordpre = wordpre;
+                ea.wmap = wmap;
+                ea.wgbase = wgbase;
+                ea.keys = ekeys;
+                ea.vals = evals;
+                ea.M = M;
+                ea.kw = kw;
+                ea.natural = natural ? 1 : 0;
+                hipLaunchKernelGGL(dm_entries_kernel, rgrid, blk, 0, s, ea);
+                // ascending positions: the routed nonzeros first, in the host planner's order
+                size_t tmp_bytes = 0;
+                if (hipcub::DeviceRadixSort::SortPairs(nullptr, tmp_bytes, ekeys, ekeys_s, evals, evals_s, nnz, 0, 32, s) !=
+                        hipSuccess ||
+                    hipMalloc(&tmp, tmp_bytes) != hipSuccess ||
+                    hipcub::DeviceRadixSort::SortPairs(tmp, tmp_bytes, ekeys, ekeys_s, evals, evals_s, nnz, 0, 32, s) !=
+                        hipSuccess)
+                    return bail(fail(TCA_ERR_HIP, "entry sort failed"));
+                (void)hipFree(tmp);
+                tmp = nullptr;
+                p->n_dn = static_cast<int32_t>(nz_take);
+                if ((st = dev_upload(&p->d_dn_pos, nullptr, static_cast<size_t>(nz_take))) ||
+                    (st = dev_upload(&p->d_dn_src, nullptr, static_cast<size_t>(nz_take))))
+                    return bail(st);
+                if (hipMemcpyAsync(p->d_dn_pos, ekeys_s, 4 * static_cast<size_t>(nz_take), hipMemcpyDeviceToDevice, s) !=
+                        hipSuccess ||
+                    hipMemcpyAsync(p->d_dn_src, evals_s, 4 * static_cast<size_t>(nz_take), hipMemcpyDeviceToDevice, s) !=
+                        hipSuccess)
+                    return bail(fail(TCA_ERR_HIP, "entry copy failed"));
+                if (!natural) {
+                    if ((st = dev_upload(&p->d_ucols, nullptr, static_cast<size_t>(steps_all) * 32))) return bail(st);
+                    p->n_ucols = static_cast<size_t>(steps_all) * 32;
+                    if (hipMemsetAsync(p->d_ucols, 0xff, 4 * static_cast<size_t>(steps_all) * 32, s) != hipSuccess)
+                        return bail(fail(TCA_ERR_HIP, "hipMemsetAsync failed"));
+                    hipLaunchKernelGGL(dm_ucols_kernel, grid_for(static_cast<int64_t>(nw) * kw), blk, 0, s, nw, kw, bm,
+                                       wordpre, wmap, wgbase, N, p->d_ucols);
+                }
+                p->adense_halves = static_cast<size_t>(steps_all) * kDmaATile + 512;
+                if ((st = dev_upload(&p->d_adense, nullptr, p->adense_halves))) return bail(st);
+                if (hipMemsetAsync(p->d_adense, 0, p->adense_halves * 2, s) != hipSuccess)
+                    return bail(fail(TCA_ERR_HIP, "hipMemsetAsync of the dense tiles failed"));
+                p->mfma.win_rows = kDmaWinRows;
+                p->mfma.windows = std::move(win);
+                p->mfma.rows = rows_mfma;
+                p->mfma.nnz = nz_take;
+                p->mfma.cond_cols = cond_cols;
+                p->mfma_dense = true;
+                p->mfma_natural = natural;
+                p->mfma_col_blocks = (N + kDmaTileCols - 1) / kDmaTileCols;
+            }
+        }
+    }
+    if (p->mfma.windows.empty()) p->flags |= TCA_PLAN_NO_MFMA;
+    const int Mp = M - rows_mfma;  // rows of the row kernel
+
+    // rows longest first (stable descending radix sort of length + 1; rows of
+    // the routed windows have key 0 and sort last)
     if (M > 0) {
         if ((st = dev_upload(&keys, nullptr, M)) || (st = dev_upload(&keys_s, nullptr, M)) ||
             (st = dev_upload(&rows, nullptr, M)) || (st = dev_upload(&rows_s, nullptr, M)))
             return bail(st);
-        hipLaunchKernelGGL(dp_lengths_kernel, grid_for(M), blk, 0, s, p->d_rowptr, M, keys, rows);
+        hipLaunchKernelGGL(dp_lengths_kernel, grid_for(M), blk, 0, s, p->d_rowptr, M,
+                           p->mfma.windows.empty() ? nullptr : wmap, keys, rows);
         size_t tmp_bytes = 0;
         if (hipcub::DeviceRadixSort::SortPairsDescending(nullptr, tmp_bytes, keys, keys_s, rows, rows_s, M, 0, 32, s) !=
             hipSuccess)
@@ -748,14 +898,13 @@ int tca_spmm_plan_create_device(const int32_t* d_rowptr, const int32_t* d_colidx
         if (hipcub::DeviceRadixSort::SortPairsDescending(tmp, tmp_bytes, keys, keys_s, rows, rows_s, M, 0, 32, s) !=
             hipSuccess)
             return bail(fail(TCA_ERR_HIP, "radix sort failed"));
-        hipLaunchKernelGGL(dp_bounds_kernel, dim3(1), dim3(64), 0, s, keys_s, M, p->rows.wide_len, p->rows.row_len,
-                           p->rows.multi_max, cnt);
+        if (Mp > 0)
+            hipLaunchKernelGGL(dp_bounds_kernel, dim3(1), dim3(64), 0, s, keys_s, Mp, p->rows.wide_len, p->rows.row_len,
+                               p->rows.multi_max, cnt);
     }
     if (hipMemcpyAsync(h_cnt, cnt, sizeof h_cnt, hipMemcpyDeviceToHost, s) != hipSuccess ||
         hipStreamSynchronize(s) != hipSuccess)
         return bail(fail(TCA_ERR_HIP, "planning kernels failed"));
-    if (h_cnt[3] & 1) return bail(fail(TCA_ERR_INVALID, "CSR row offsets are not 0 .. nnz non-decreasing"));
-    if (h_cnt[3] & 2) return bail(fail(TCA_ERR_INVALID, "CSR columns out of range or not strictly ascending in a row"));
     const int n_long = h_cnt[0], end_wide = h_cnt[1], end_row = h_cnt[2];
     // segment slots of the long rows: exclusive sum of their segment counts
     int seg_total = 0;
@@ -776,7 +925,7 @@ int tca_spmm_plan_create_device(const int32_t* d_rowptr, const int32_t* d_colidx
             hipStreamSynchronize(s) != hipSuccess)
             return bail(fail(TCA_ERR_HIP, "segment scan failed"));
     }
-    const int n_wide = end_wide - n_long, n_row = end_row - end_wide, n_short = M - end_row;
+    const int n_wide = end_wide - n_long, n_row = end_row - end_wide, n_short = Mp - end_row;
     const int n_multi = (n_short + slots - 1) / slots;
     p->ntasks = 4 * n_wide + seg_total + n_row + n_multi;
     p->rows.n_wide = 4 * n_wide;
@@ -790,7 +939,7 @@ int tca_spmm_plan_create_device(const int32_t* d_rowptr, const int32_t* d_colidx
         (st = dev_upload(&p->d_longrows, nullptr, n_long)) ||
         (st = dev_upload(&p->d_partials, nullptr, p->n_seg_total * N)))
         return bail(st);
-    if (M > 0) {
+    if (Mp > 0) {
         DpEmitArgs ea;
         ea.rowptr = p->d_rowptr;
         ea.len = keys_s;
@@ -799,13 +948,13 @@ int tca_spmm_plan_create_device(const int32_t* d_rowptr, const int32_t* d_colidx
         ea.tasks = p->d_tasks;
         ea.perm = p->d_perm;
         ea.longrows = p->d_longrows;
-        ea.M = M;
+        ea.M = Mp;
         ea.n_long = n_long;
         ea.end_wide = end_wide;
         ea.end_row = end_row;
         ea.slots = slots;
         ea.seg_total = seg_total;
-        hipLaunchKernelGGL(dp_emit_kernel, grid_for(M), blk, 0, s, ea);
+        hipLaunchKernelGGL(dp_emit_kernel, grid_for(Mp), blk, 0, s, ea);
     }
     if (hipGetLastError() != hipSuccess || hipStreamSynchronize(s) != hipSuccess)
         return bail(fail(TCA_ERR_HIP, "task emission failed"));
@@ -831,6 +980,28 @@ int tca_spmm_plan_export_rows(const tca_spmm_plan* p, int32_t* n_tasks, int32_t*
     *n_tasks = p->ntasks;
     *n_perm = p->n_perm;
     *n_long = p->n_longrows;
+    return TCA_OK;
+}
+
+int tca_spmm_plan_export_tiles(const tca_spmm_plan* p, int32_t* n_windows, int32_t* n_entries, int32_t* n_ucols,
+                               int32_t* windows, uint32_t* pos, int32_t* src, uint32_t* ucols) {
+    if (!p || !n_windows || !n_entries || !n_ucols) return fail(TCA_ERR_INVALID, "tca_spmm_plan_export_tiles: bad argument");
+    const bool dense = p->mfma_dense && !p->mfma.windows.empty();
+    const int32_t nw = dense ? static_cast<int32_t>(p->mfma.windows.size()) : 0;
+    const int32_t ne = dense ? p->n_dn : 0;
+    const int32_t nu = dense && !p->mfma_natural ? static_cast<int32_t>(p->n_ucols) : 0;
+    if (windows) {
+        if (*n_windows < nw || *n_entries < ne || *n_ucols < nu || !pos || !src || !ucols)
+            return fail(TCA_ERR_INVALID, "tca_spmm_plan_export_tiles: output buffers too small");
+        if ((nw && hipMemcpy(windows, p->d_windows, sizeof(int4) * nw, hipMemcpyDeviceToHost) != hipSuccess) ||
+            (ne && hipMemcpy(pos, p->d_dn_pos, sizeof(uint32_t) * ne, hipMemcpyDeviceToHost) != hipSuccess) ||
+            (ne && hipMemcpy(src, p->d_dn_src, sizeof(int32_t) * ne, hipMemcpyDeviceToHost) != hipSuccess) ||
+            (nu && hipMemcpy(ucols, p->d_ucols, sizeof(uint32_t) * nu, hipMemcpyDeviceToHost) != hipSuccess))
+            return fail(TCA_ERR_HIP, "tca_spmm_plan_export_tiles: copy failed");
+    }
+    *n_windows = nw;
+    *n_entries = ne;
+    *n_ucols = nu;
     return TCA_OK;
 }
 
@@ -1040,7 +1211,8 @@ int tca_spmm_time_phases(const tca_spmm_plan* p, const void* d_val, const void* 
         return fail(TCA_ERR_HIP, "hipEventCreate failed");
     }
     int st = TCA_OK;
-    const bool used[TCA_PHASES] = {!p->mfma.windows.empty() && !p->mfma.entries.empty(), !p->mfma.windows.empty(),
+    const bool used[TCA_PHASES] = {!p->mfma.windows.empty() && (!p->mfma.entries.empty() || p->n_dn > 0),
+                                   !p->mfma.windows.empty(),
                                    p->ntasks > 0, p->n_longrows > 0};
     for (int k = 0; k < TCA_PHASES && st == TCA_OK; k++) {
         if (!used[k]) continue;

@@ -77,10 +77,11 @@ def test_device_plan_argument_checks_need_no_gpu():
     import ctypes
     import spmm_amd as S
     p = ctypes.c_void_p()
-    with pytest.raises(S.TcaError) as ei:
-        S._lib.call("tca_spmm_plan_create_device", 16, 16, 4, 4, 4, 8, S.TCA_F32, S.TCA_PLAN_FORCE_MFMA, None,
-                    ctypes.byref(p))
-    assert ei.value.status == 4
+    # the kernels whose layouts only the host planner builds
+    for flags in (S.TCA_PLAN_MFMA_REGS, S.TCA_PLAN_MFMA_DMA, S.TCA_PLAN_MFMA_PAIR, S.TCA_PLAN_MFMA_SPARSE):
+        with pytest.raises(S.TcaError) as ei:
+            S._lib.call("tca_spmm_plan_create_device", 16, 16, 4, 4, 4, 8, S.TCA_F16, flags, None, ctypes.byref(p))
+        assert ei.value.status == 4, flags
     with pytest.raises(S.TcaError) as ei:
         S._lib.call("tca_spmm_plan_create_device", None, None, 4, 4, 4, 8, S.TCA_F32, 0, None, ctypes.byref(p))
     assert ei.value.status == 1

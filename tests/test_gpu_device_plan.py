@@ -1,7 +1,9 @@
 """Planning on the GPU (tca_spmm_plan_create_device): the task list built by
 device kernels from a device-resident CSR equals the host planner's
-(TCA_PLAN_NO_MFMA) entry for entry, and both plans give bit-identical
-products; invalid structures are rejected on the device."""
+(TCA_PLAN_NO_MFMA) entry for entry, the matrix-core windows and their dense
+tiles (natural and condensed) equal the host planner's for the same flags,
+and the plans give bit-identical products; invalid structures are rejected
+on the device."""
 import numpy as np
 import pytest
 
@@ -30,7 +32,7 @@ def test_device_plan_equals_host_plan(torch_cuda, name, a, n):
     print(f"device plan {name}: M={a.nrow} K={a.ncol} nnz={a.nnz} N={n}", flush=True)
     drp, dci = _dev(torch, a.rowptr), _dev(torch, a.colidx)
     with S.Plan(a, n, S.TCA_PLAN_NO_MFMA) as hp:
-        dp = S.Plan.from_device(drp, dci, a.nrow, a.ncol, a.nnz, n, a.dtype)
+        dp = S.Plan.from_device(drp, dci, a.nrow, a.ncol, a.nnz, n, a.dtype, S.TCA_PLAN_NO_MFMA)
         try:
             ht, hperm, hl = hp.export_rows()
             dt, dperm, dl = dp.export_rows()
@@ -49,6 +51,76 @@ def test_device_plan_equals_host_plan(torch_cuda, name, a, n):
                 outs.append(c.cpu().numpy())
             assert np.array_equal(outs[0], outs[1]), name
             assert np.all(np.isfinite(outs[1]))
+        finally:
+            dp.close()
+
+
+def _mixed(seed):
+    """Dense windows (rows 0..383, ~40 % of K) over sparse ones: some windows
+    are routed, the rest stay on the row kernel, the routed ones condense."""
+    rng = np.random.default_rng(seed)
+    m, k = 900, 2000
+    lens = np.where(np.arange(m) < 384, rng.integers(60, 120, m), rng.integers(0, 6, m))
+    rowptr = np.zeros(m + 1, np.int32)
+    np.cumsum(lens, out=rowptr[1:])
+    cols = []
+    for r in range(m):
+        pool = 800 if r < 384 else k
+        cols.append(np.sort(rng.choice(pool, lens[r], replace=False)).astype(np.int32))
+    colidx = np.concatenate(cols).astype(np.int32)
+    return S.CSR(m, k, rowptr, colidx, S.to_storage(np.ones(len(colidx), np.float32), S.TCA_F16), S.TCA_F16)
+
+
+def _mfma_cases():
+    yield "lognormal-natural", S.gen_lognormal_rows(4096, 4096, 205, seed=1, dtype=S.TCA_F16)[0], 512
+    yield "ragged-natural", S.gen_lognormal_rows(1000, 1500, 80, seed=9, dtype=S.TCA_BF16)[0], 136
+    yield "mixed-condensed", _mixed(3), 256
+    yield "bernoulli", S.gen_bernoulli(3000, 2000, 0.01, seed=1, dtype=S.TCA_F16)[0], 256
+
+
+@pytest.mark.parametrize("flags", [S.TCA_PLAN_DEFAULT, S.TCA_PLAN_MFMA_DENSE,
+                                   S.TCA_PLAN_FORCE_MFMA | S.TCA_PLAN_MFMA_DENSE],
+                         ids=["default", "dense", "force-dense"])
+@pytest.mark.parametrize("name,a,n", list(_mfma_cases()), ids=[c[0] for c in _mfma_cases()])
+def test_device_mfma_plan_equals_host_plan(torch_cuda, name, a, n, flags):
+    """Windows, dense-tile positions, B row offsets and row tasks equal the
+    host planner's; products bit-identical and equal to the oracle on exact
+    inputs.  (By default, windows that do not cover most of K run on the
+    paired kernel when planned on the host and on condensed dense tiles when
+    planned on the GPU: there only the products are compared.)"""
+    torch = torch_cuda
+    print(f"device mfma plan {name} flags={flags}: M={a.nrow} K={a.ncol} nnz={a.nnz} N={n}", flush=True)
+    rng = np.random.default_rng(11)
+    v = rng.choice(np.array([-2.0, -1.0, -0.5, 0.5, 1.0, 2.0], np.float32), size=a.nnz)
+    a = S.CSR(a.nrow, a.ncol, a.rowptr, a.colidx, S.to_storage(v, a.dtype), a.dtype)
+    b = S.to_storage(exact_dense(rng, (a.ncol, n)), a.dtype)
+    with S.Plan(a, n, flags) as hp:
+        dp = S.Plan.from_device(_dev(torch, a.rowptr), _dev(torch, a.colidx), a.nrow, a.ncol, a.nnz, n, a.dtype, flags)
+        try:
+            hi, di = hp.info(), dp.info()
+            same = not (flags == S.TCA_PLAN_DEFAULT and hi["tile_kernel"] == 3)
+            for key in ("n_windows_mfma", "rows_mfma", "nnz_mfma"):
+                assert hi[key] == di[key], (name, key, hi[key], di[key])
+            if same:
+                for key in ("cond_cols_mfma", "tile_kernel", "mfma_blocks", "n_row_tasks", "n_multi_tasks",
+                            "n_seg_tasks", "n_long_rows", "n_wide_tasks"):
+                    assert hi[key] == di[key], (name, key, hi[key], di[key])
+                for x, y in zip(hp.export_rows(), dp.export_rows()):
+                    assert np.array_equal(x, y), name
+                for x, y in zip(hp.export_tiles(), dp.export_tiles()):
+                    assert np.array_equal(x, y), name
+            else:
+                assert di["tile_kernel"] == 4, di["tile_kernel"]
+            val, bd = _dev(torch, a.values), _dev(torch, b)
+            outs = []
+            for pl in (hp, dp):
+                c = torch.full((a.nrow, n), float("nan"), dtype=torch.float32, device="cuda:0")
+                pl.run(val, bd, c)
+                torch.cuda.synchronize()
+                outs.append(c.cpu().numpy())
+            want = oracle.csr_spmm(a.rowptr, a.colidx, a.values_f32(), S.from_storage(b, a.dtype))
+            assert np.array_equal(outs[1], want), name
+            assert np.array_equal(outs[0], outs[1]), name
         finally:
             dp.close()
 
