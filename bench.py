@@ -127,11 +127,19 @@ def main():
     if args.sparse24:
         sparse24(args, a, n, bd, c, dev_tensor)
         return
+    plan_first_ms = None
     if args.device_plan:
         drp, dci = dev_tensor(a.rowptr), dev_tensor(a.colidx)
         torch.cuda.synchronize()
-        plan = S.Plan.from_device(drp, dci, a.nrow, a.ncol, a.nnz, n, a.dtype, args.flags,
-                                  stream=torch.cuda.current_stream().cuda_stream)
+        # the first plan of a process also loads the planning kernels' code
+        # objects; the plan used below is the fourth (steady state)
+        for k in range(4):
+            plan = S.Plan.from_device(drp, dci, a.nrow, a.ncol, a.nnz, n, a.dtype, args.flags,
+                                      stream=torch.cuda.current_stream().cuda_stream)
+            if k == 0:
+                plan_first_ms = plan.info()["plan_ms"]
+            if k < 3:
+                plan.close()
     else:
         plan = S.Plan(a, n, args.flags)
     info = plan.info()
@@ -252,6 +260,8 @@ def main():
         "config": {"workload": WORKLOADS[args.config], "M": m, "K": k, "N": n, "nnz": nnz,
                    "bytes_alg": bytes_alg, "hbm_gbs_whole_step": round(hbm_gbs, 2),
                    "plan_ms": round(info["plan_ms"], 3),
+                   **({"plan_on_gpu": True, "plan_first_ms": round(plan_first_ms, 3)} if plan_first_ms is not None
+                      else {}),
                    "phases_us": {kk: round(v * 1e3, 3) for kk, v in phases.items()},
                    "cold_cache_us": round(cold_ms * 1e3, 3), "launch_floor_us": round(floor_ms * 1e3, 3),
                    "mfma_windows": info["n_windows_mfma"], "rows_mfma": info["rows_mfma"],
