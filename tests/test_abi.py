@@ -85,3 +85,15 @@ def test_device_plan_argument_checks_need_no_gpu():
     with pytest.raises(S.TcaError) as ei:
         S._lib.call("tca_spmm_plan_create_device", None, None, 4, 4, 4, 8, S.TCA_F32, 0, None, ctypes.byref(p))
     assert ei.value.status == 1
+
+
+def test_python_constants_match_the_header():
+    """Every TCA_PLAN_*, TCA_TILES_* and dtype #define of include/tca_spmm.h
+    has the same value in the Python binding."""
+    import re
+    import spmm_amd as S
+    head = open(os.path.join(ROOT, "include", "tca_spmm.h")).read()
+    found = re.findall(r"#define (TCA_(?:PLAN|TILES)_\w+) (\d+)u?", head)
+    assert len(found) >= 15
+    for name, value in found:
+        assert getattr(S, name) == int(value), name
