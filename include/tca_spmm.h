@@ -58,6 +58,8 @@ typedef enum tca_status {
  * table), else the paired kernel. */
 #define TCA_PLAN_MFMA_SPARSE 32u /* 2:4-grouped windows on the sparse matrix cores (v_smfmac) */
 #define TCA_PLAN_MFMA_PAIR 64u  /* paired (MFMA + staging wavefront) 128 x 64 kernel, whatever the windows */
+#define TCA_PLAN_MFMA_COMPACT 128u /* dense-tile kernel on compacted steps (only the non-empty 16-byte
+                                      fragment cells, at most 255 per step; else plain dense tiles) */
 
 typedef struct tca_spmm_plan tca_spmm_plan;
 
@@ -99,6 +101,7 @@ typedef struct tca_plan_info {
 #define TCA_TILES_DENSE 4      /* dense condensed tiles (TCA_PLAN_MFMA_DENSE) */
 #define TCA_TILES_DENSE_K 5    /* dense tiles spanning all of K (default when the windows cover most of K) */
 #define TCA_TILES_SPARSE 6     /* 2:4-grouped tiles on the sparse matrix cores (TCA_PLAN_MFMA_SPARSE) */
+#define TCA_TILES_COMPACT 7    /* dense tiles with compacted steps (TCA_PLAN_MFMA_COMPACT) */
 
 /* Replaces reference workload_manager (src/our_spmm.cu:353-477) plus the
  * device uploads of our_spmm_balanced (src/our_spmm.cu:503-525).

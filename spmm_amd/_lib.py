@@ -21,9 +21,10 @@ TCA_PLAN_DEFAULT, TCA_PLAN_NO_MFMA, TCA_PLAN_FORCE_MFMA, TCA_PLAN_MFMA_REGS, TCA
 TCA_PLAN_MFMA_DENSE = 16
 TCA_PLAN_MFMA_SPARSE = 32
 TCA_PLAN_MFMA_PAIR = 64
+TCA_PLAN_MFMA_COMPACT = 128
 # tile kernel of a plan (tca_plan_info.tile_kernel)
 TCA_TILES_NONE, TCA_TILES_REGS, TCA_TILES_DMA, TCA_TILES_PAIR = 0, 1, 2, 3
-TCA_TILES_DENSE, TCA_TILES_DENSE_K, TCA_TILES_SPARSE = 4, 5, 6
+TCA_TILES_DENSE, TCA_TILES_DENSE_K, TCA_TILES_SPARSE, TCA_TILES_COMPACT = 4, 5, 6, 7
 
 i32 = ctypes.c_int32
 i64 = ctypes.c_int64

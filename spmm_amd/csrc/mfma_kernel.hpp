@@ -103,6 +103,7 @@ struct MfmaArgs {
     const void* adense;      // [global step] dense A tile, 8 KiB in fragment order (dense kernel)
     int n_windows;           // windows (dense kernel: its workgroup -> window mapping)
     int K;                   // rows of B (dense kernel, windows in natural column order)
+    const uint64_t* amask;   // [global step][8] non-empty cells of each row block (compact dense kernel)
 };
 
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;

@@ -87,7 +87,7 @@ constexpr MfmaShape kMfmaDenseShape = {128, 64, 128 * 32, 3.0, 0.5, 3};
 inline const MfmaShape& mfma_shape(uint32_t flags) {
     if (flags & TCA_PLAN_MFMA_REGS) return kMfmaRegsShape;
     if (flags & TCA_PLAN_MFMA_DMA) return kMfmaDmaShape;
-    if (flags & (TCA_PLAN_MFMA_DENSE | TCA_PLAN_MFMA_SPARSE)) return kMfmaDenseShape;
+    if (flags & (TCA_PLAN_MFMA_DENSE | TCA_PLAN_MFMA_SPARSE | TCA_PLAN_MFMA_COMPACT)) return kMfmaDenseShape;
     return kMfmaDmaShape;
 }
 

@@ -15,6 +15,7 @@
 #include "mfma_dma_kernel.hpp"
 #include "mfma_pair_kernel.hpp"
 #include "mfma_dense_kernel.hpp"
+#include "mfma_compact_kernel.hpp"
 #include "bell_kernel.hpp"
 #include "sparse24_kernel.hpp"
 #include "device_planner.hpp"
@@ -45,6 +46,9 @@ struct tca_spmm_plan {
     bool mfma_dense = false; // dense-tile kernel (plan keeps dense condensed windows)
     bool mfma_sparse = false; // 2:4-grouped windows on the sparse matrix cores
     bool mfma_natural = false; // dense kernel: windows span all of K in column order (B rows contiguous)
+    bool mfma_compact = false; // dense kernel on compacted steps (non-empty fragment cells only)
+    int mfma_compact_lb = 3;   // compact kernel: transfer lookahead in iterations (3, or 4 by TCA_COMPACT_LB)
+    uint64_t* d_amask = nullptr;  // compact kernel: [global step][8] non-empty cells per row block
     int32_t n_windows24 = 0;  // windows of the 2:4 plan
     uint16_t* d_adense = nullptr;  // dense kernel: [global step] 8 KiB A tile, then 1 KiB of zeros
     size_t adense_halves = 0;
@@ -112,6 +116,7 @@ void free_plan_device(tca_spmm_plan* p) {
     (void)hipFree(p->d_pk_cell);
     (void)hipFree(p->d_packed);
     (void)hipFree(p->d_adense);
+    (void)hipFree(p->d_amask);
     (void)hipFree(p->d_dn_src);
     (void)hipFree(p->d_dn_pos);
 }
@@ -220,7 +225,22 @@ int launch_mfma(const tca_spmm_plan* p, const void* B, float* C, hipStream_t s) 
         a.zeros = p->d_adense + (p->adense_halves - 512);
         a.n_windows = static_cast<int>(p->mfma.windows.size());
         a.K = p->K;
+        a.amask = p->d_amask;
         const dim3 dgrid(mfma_dense_grid(a.n_windows, p->mfma_col_blocks));
+        if (p->mfma_compact) {
+            const int v = (bf ? 1 : 0) | (p->mfma_natural ? 2 : 0) | (p->mfma_compact_lb == 3 ? 4 : 0);
+            switch (v) {
+                case 0: hipLaunchKernelGGL((mfma_compact_kernel<false, false, 4>), dgrid, dim3(kDnThreads), 0, s, a); break;
+                case 1: hipLaunchKernelGGL((mfma_compact_kernel<true, false, 4>), dgrid, dim3(kDnThreads), 0, s, a); break;
+                case 2: hipLaunchKernelGGL((mfma_compact_kernel<false, true, 4>), dgrid, dim3(kDnThreads), 0, s, a); break;
+                case 3: hipLaunchKernelGGL((mfma_compact_kernel<true, true, 4>), dgrid, dim3(kDnThreads), 0, s, a); break;
+                case 4: hipLaunchKernelGGL((mfma_compact_kernel<false, false, 3>), dgrid, dim3(kDnThreads), 0, s, a); break;
+                case 5: hipLaunchKernelGGL((mfma_compact_kernel<true, false, 3>), dgrid, dim3(kDnThreads), 0, s, a); break;
+                case 6: hipLaunchKernelGGL((mfma_compact_kernel<false, true, 3>), dgrid, dim3(kDnThreads), 0, s, a); break;
+                default: hipLaunchKernelGGL((mfma_compact_kernel<true, true, 3>), dgrid, dim3(kDnThreads), 0, s, a); break;
+            }
+            return TCA_OK;
+        }
         if (p->mfma_natural) {
             if (bf) hipLaunchKernelGGL((mfma_dense_kernel<true, true>), dgrid, dim3(kDnThreads), 0, s, a);
             else hipLaunchKernelGGL((mfma_dense_kernel<false, true>), dgrid, dim3(kDnThreads), 0, s, a);
@@ -324,6 +344,8 @@ void fill_info(tca_spmm_plan* p) {
     in.mfma_blockdim = kMfmaThreads;
     if (p->mfma_sparse)
         in.mfma_lds_bytes = mfma_sparse_lds_bytes();
+    else if (p->mfma_dense && p->mfma_compact)
+        in.mfma_lds_bytes = p->mfma_compact_lb == 3 ? mfma_compact_lds_bytes<3>() : mfma_compact_lds_bytes<4>();
     else if (p->mfma_dense)
         in.mfma_lds_bytes = mfma_dense_lds_bytes();
     else if (p->mfma_pair)
@@ -335,6 +357,7 @@ void fill_info(tca_spmm_plan* p) {
     in.scratch_bytes = static_cast<int64_t>(p->n_seg_total * p->N * sizeof(float));
     in.tile_kernel = p->mfma.windows.empty() ? TCA_TILES_NONE
                      : p->mfma_sparse       ? TCA_TILES_SPARSE
+                     : p->mfma_compact      ? TCA_TILES_COMPACT
                      : p->mfma_dense        ? (p->mfma_natural ? TCA_TILES_DENSE_K : TCA_TILES_DENSE)
                      : p->mfma_pair         ? TCA_TILES_PAIR
                      : (p->mfma_dma && p->mfma_slots <= 2) ? TCA_TILES_DMA
@@ -420,7 +443,8 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
     plan_mfma(rowptr, colidx, M, N, dtype, (flags & TCA_PLAN_FORCE_MFMA) != 0, (flags & TCA_PLAN_NO_MFMA) != 0,
               min_density, *shape, &p->mfma);
     p->mfma_dma = (flags & TCA_PLAN_MFMA_REGS) == 0 && (flags & TCA_PLAN_MFMA_DMA) != 0;
-    p->mfma_dense = (flags & (TCA_PLAN_MFMA_REGS | TCA_PLAN_MFMA_DMA)) == 0 && (flags & TCA_PLAN_MFMA_DENSE) != 0;
+    p->mfma_dense = (flags & (TCA_PLAN_MFMA_REGS | TCA_PLAN_MFMA_DMA)) == 0 &&
+                    (flags & (TCA_PLAN_MFMA_DENSE | TCA_PLAN_MFMA_COMPACT)) != 0;
     if ((flags & (TCA_PLAN_MFMA_REGS | TCA_PLAN_MFMA_DMA | TCA_PLAN_MFMA_DENSE | TCA_PLAN_MFMA_SPARSE |
                   TCA_PLAN_MFMA_PAIR)) == 0 &&
         !p->mfma.windows.empty() &&
@@ -574,6 +598,37 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
                 }
         }
         std::sort(ent.begin(), ent.end());
+        if (flags & TCA_PLAN_MFMA_COMPACT) {
+            // Compacted steps: the non-empty 16-byte cells of each step in
+            // cell order (cell = dense half index / 8 within the step, i.e.
+            // row block * 64 + lane), at most kCpCells - 1 per step (the last
+            // cell stays zero for the empty lanes); else plain dense tiles.
+            std::vector<uint64_t> mask(nsteps_all * 8, 0);
+            std::vector<std::pair<uint32_t, int32_t>> cent(ent);
+            bool fits = true;
+            for (size_t x = 0; x < cent.size() && fits;) {
+                const uint32_t g = cent[x].first / kDmaATile;
+                int32_t rank = -1;
+                uint32_t last = ~0u;
+                for (; x < cent.size() && cent[x].first / kDmaATile == g; x++) {
+                    const uint32_t h = cent[x].first % kDmaATile, c = h / 8;
+                    if (c != last) {
+                        rank++;
+                        last = c;
+                        mask[static_cast<size_t>(g) * 8 + c / 64] |= uint64_t(1) << (c % 64);
+                    }
+                    if (rank >= kCpCells - 1) fits = false;
+                    cent[x].first = g * static_cast<uint32_t>(kCpCells * 8) + static_cast<uint32_t>(rank) * 8u + h % 8;
+                }
+            }
+            if (fits) {
+                ent.swap(cent);
+                p->mfma_compact = true;
+                p->adense_halves = nsteps_all * static_cast<size_t>(kCpCells * 8) + 512;
+                if (const char* lb = std::getenv("TCA_COMPACT_LB")) p->mfma_compact_lb = std::atoi(lb) == 4 ? 4 : 3;
+                if ((st = dev_upload(&p->d_amask, mask.data(), mask.size()))) return bail(st);
+            }
+        }
         std::vector<int32_t> dsrc(ent.size());
         std::vector<uint32_t> dpos(ent.size());
         for (size_t x = 0; x < ent.size(); x++) {

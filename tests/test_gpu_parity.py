@@ -138,8 +138,8 @@ def test_exact_bit_equal_all_widths(torch_cuda, dtype):
 
 
 @pytest.mark.parametrize("variant", [S.TCA_PLAN_MFMA_REGS, S.TCA_PLAN_MFMA_DMA, S.TCA_PLAN_MFMA_PAIR, 0,
-                                     S.TCA_PLAN_MFMA_DENSE, S.TCA_PLAN_MFMA_SPARSE],
-                         ids=["regs", "dma", "pair", "default", "dense", "sparse"])
+                                     S.TCA_PLAN_MFMA_DENSE, S.TCA_PLAN_MFMA_SPARSE, S.TCA_PLAN_MFMA_COMPACT],
+                         ids=["regs", "dma", "pair", "default", "dense", "sparse", "compact"])
 @pytest.mark.parametrize("dtype", [S.TCA_F16, S.TCA_BF16])
 def test_mfma_exact_bit_equal(torch_cuda, dtype, variant):
     """Condensed-tile MFMA path (forced on every eligible window) is bit-equal
@@ -165,7 +165,8 @@ def test_mfma_exact_bit_equal(torch_cuda, dtype, variant):
                 got = run_gpu(torch_cuda, a, b, plan=pl)
             assert info["n_windows_mfma"] > 0 or (variant != S.TCA_PLAN_MFMA_REGS and (m, k, p) in dense), (m, k, n)
             want_kernel = {S.TCA_PLAN_MFMA_REGS: {1}, S.TCA_PLAN_MFMA_DMA: {2, 1}, S.TCA_PLAN_MFMA_PAIR: {3},
-                           0: {3, 5}, S.TCA_PLAN_MFMA_DENSE: {4, 5}, S.TCA_PLAN_MFMA_SPARSE: {6}}[variant]
+                           0: {3, 5}, S.TCA_PLAN_MFMA_DENSE: {4, 5}, S.TCA_PLAN_MFMA_SPARSE: {6},
+                           S.TCA_PLAN_MFMA_COMPACT: {7, 4, 5}}[variant]
             assert info["tile_kernel"] in want_kernel or info["n_windows_mfma"] == 0, (variant, info["tile_kernel"])
             want = oracle_c(a, b)
             assert np.array_equal(got, want), (m, k, p, n, np.abs(got - want).max())
@@ -185,6 +186,41 @@ def test_mfma_and_row_paths_agree(torch_cuda):
             assert (nwin > 0) == (flags == S.TCA_PLAN_FORCE_MFMA)
     assert np.array_equal(outs[S.TCA_PLAN_NO_MFMA], outs[S.TCA_PLAN_FORCE_MFMA])
     assert np.array_equal(outs[S.TCA_PLAN_DEFAULT], oracle_c(a, b))
+
+
+@pytest.mark.parametrize("lookahead", ["3", "4"])
+def test_compact_tiles_equal_dense_tiles(torch_cuda, lookahead, monkeypatch):
+    """Compacted steps (only the non-empty 16-byte fragment cells) give the
+    dense-tile kernel's products bit for bit (same fragments, same MFMA and
+    partial-sum order) on a config-1-like matrix, natural and condensed
+    column order, both lookaheads; a step with more than 255 non-empty
+    cells keeps the plain dense tiles."""
+    monkeypatch.setenv("TCA_COMPACT_LB", lookahead)
+    rng = np.random.default_rng(91)
+    for m, k, mean, n in [(1024, 2048, 100, 512), (640, 4096, 60, 136), (300, 8000, 20, 64)]:
+        print(f"compact vs dense LB={lookahead}: M={m} K={k} mean={mean} N={n}", flush=True)
+        a, _ = S.gen_lognormal_rows(m, k, mean, seed=7, dtype=S.TCA_F16)
+        a = S.CSR(a.nrow, a.ncol, a.rowptr, a.colidx, S.to_storage(exact_values(rng, a.nnz), S.TCA_F16), S.TCA_F16)
+        b = S.to_storage(exact_dense(rng, (k, n)), S.TCA_F16)
+        outs = {}
+        for flags in (S.TCA_PLAN_FORCE_MFMA | S.TCA_PLAN_MFMA_DENSE, S.TCA_PLAN_FORCE_MFMA | S.TCA_PLAN_MFMA_COMPACT):
+            with S.Plan(a, n, flags) as pl:
+                info = pl.info()
+                outs[flags] = run_gpu(torch_cuda, a, b, plan=pl)
+            assert info["n_windows_mfma"] > 0, (m, k)
+            if flags & S.TCA_PLAN_MFMA_COMPACT:
+                assert info["tile_kernel"] == S.TCA_TILES_COMPACT, info["tile_kernel"]
+        vals = list(outs.values())
+        assert np.array_equal(vals[0], vals[1]), (m, k, n, np.abs(vals[0] - vals[1]).max())
+        assert np.array_equal(vals[1], oracle_c(a, b)), (m, k, n)
+    # every cell of a step non-empty: no compaction
+    a, _ = S.gen_bernoulli(256, 512, 0.6, seed=9, dtype=S.TCA_F16)
+    a = S.CSR(a.nrow, a.ncol, a.rowptr, a.colidx, S.to_storage(exact_values(rng, a.nnz), S.TCA_F16), S.TCA_F16)
+    b = S.to_storage(exact_dense(rng, (512, 64)), S.TCA_F16)
+    with S.Plan(a, 64, S.TCA_PLAN_FORCE_MFMA | S.TCA_PLAN_MFMA_COMPACT) as pl:
+        assert pl.info()["tile_kernel"] in (S.TCA_TILES_DENSE, S.TCA_TILES_DENSE_K), pl.info()["tile_kernel"]
+        got = run_gpu(torch_cuda, a, b, plan=pl)
+    assert np.array_equal(got, oracle_c(a, b))
 
 
 def test_exact_long_rows_many_segments(torch_cuda):
