@@ -46,7 +46,9 @@ def phase_kernel(phase: str, tile_kernel: int) -> str:
 # calibration: FETCH x 2.00, WRITE x 1.00), keyed by (config, kernel).
 # Source: the profiles/ summaries named in each entry.
 MEASURED_TRAFFIC_KIB = {
-    # profiles/mfma_dense_kernel_config1.md (dense tiles over all of K, the default on config 1)
+    # profiles/mfma_compact_kernel_config1.md (compacted dense tiles over all of K, the default on config 1)
+    (1, "mfma_compact_kernel"): (24783.0 * 2.0, 8325.1),
+    # profiles/mfma_dense_kernel_config1.md (plain dense tiles over all of K, --flags 16)
     (1, "mfma_dense_kernel"): (32839.5 * 2.0, 8248.8),
     # profiles/mfma_pair_kernel_config1.md (paired tile kernel)
     (1, "mfma_pair_kernel"): (21323.1 * 2.0, 8436.0),

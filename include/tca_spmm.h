@@ -55,7 +55,8 @@ typedef enum tca_status {
 #define TCA_PLAN_MFMA_DENSE 16u /* dense-tile 128 x 64 kernel (plan keeps dense condensed windows) */
 /* Default tile kernel: dense tiles spanning all of K when the routed windows'
  * column unions cover on average >= 85 % of K (B rows then need no gather
- * table), else the paired kernel. */
+ * table), compacted (TCA_TILES_COMPACT) when no step has more than 255
+ * non-empty fragment cells, else the paired kernel. */
 #define TCA_PLAN_MFMA_SPARSE 32u /* 2:4-grouped windows on the sparse matrix cores (v_smfmac) */
 #define TCA_PLAN_MFMA_PAIR 64u  /* paired (MFMA + staging wavefront) 128 x 64 kernel, whatever the windows */
 #define TCA_PLAN_MFMA_COMPACT 128u /* dense-tile kernel on compacted steps (only the non-empty 16-byte

@@ -87,7 +87,9 @@ def test_device_mfma_plan_equals_host_plan(torch_cuda, name, a, n, flags):
     host planner's; products bit-identical and equal to the oracle on exact
     inputs.  (By default, windows that do not cover most of K run on the
     paired kernel when planned on the host and on condensed dense tiles when
-    planned on the GPU: there only the products are compared.)"""
+    planned on the GPU, and windows that do run on compacted dense tiles
+    when planned on the host and on plain dense tiles when planned on the
+    GPU: there only the products are compared.)"""
     torch = torch_cuda
     print(f"device mfma plan {name} flags={flags}: M={a.nrow} K={a.ncol} nnz={a.nnz} N={n}", flush=True)
     rng = np.random.default_rng(11)
@@ -98,7 +100,9 @@ def test_device_mfma_plan_equals_host_plan(torch_cuda, name, a, n, flags):
         dp = S.Plan.from_device(_dev(torch, a.rowptr), _dev(torch, a.colidx), a.nrow, a.ncol, a.nnz, n, a.dtype, flags)
         try:
             hi, di = hp.info(), dp.info()
-            same = not (flags == S.TCA_PLAN_DEFAULT and hi["tile_kernel"] == 3)
+            # host default tiles the device planner does not build: paired (3),
+            # compacted dense tiles (7); the device plans plain dense tiles
+            same = not (flags == S.TCA_PLAN_DEFAULT and hi["tile_kernel"] in (3, 7))
             for key in ("n_windows_mfma", "rows_mfma", "nnz_mfma"):
                 assert hi[key] == di[key], (name, key, hi[key], di[key])
             if same:
@@ -110,7 +114,7 @@ def test_device_mfma_plan_equals_host_plan(torch_cuda, name, a, n, flags):
                 for x, y in zip(hp.export_tiles(), dp.export_tiles()):
                     assert np.array_equal(x, y), name
             else:
-                assert di["tile_kernel"] == 4, di["tile_kernel"]
+                assert di["tile_kernel"] == (4 if hi["tile_kernel"] == 3 else 5), (hi["tile_kernel"], di["tile_kernel"])
             val, bd = _dev(torch, a.values), _dev(torch, b)
             outs = []
             for pl in (hp, dp):

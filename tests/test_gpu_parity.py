@@ -165,7 +165,7 @@ def test_mfma_exact_bit_equal(torch_cuda, dtype, variant):
                 got = run_gpu(torch_cuda, a, b, plan=pl)
             assert info["n_windows_mfma"] > 0 or (variant != S.TCA_PLAN_MFMA_REGS and (m, k, p) in dense), (m, k, n)
             want_kernel = {S.TCA_PLAN_MFMA_REGS: {1}, S.TCA_PLAN_MFMA_DMA: {2, 1}, S.TCA_PLAN_MFMA_PAIR: {3},
-                           0: {3, 5}, S.TCA_PLAN_MFMA_DENSE: {4, 5}, S.TCA_PLAN_MFMA_SPARSE: {6},
+                           0: {3, 5, 7}, S.TCA_PLAN_MFMA_DENSE: {4, 5}, S.TCA_PLAN_MFMA_SPARSE: {6},
                            S.TCA_PLAN_MFMA_COMPACT: {7, 4, 5}}[variant]
             assert info["tile_kernel"] in want_kernel or info["n_windows_mfma"] == 0, (variant, info["tile_kernel"])
             want = oracle_c(a, b)
