@@ -13,6 +13,9 @@ Each function names the reference lines it restates.  How each is pinned
 * ``dense_to_csr`` / ``csr_to_dense`` -- the fixture round trip
   (``.smtx -> dense -> CSR`` reproduces the file's arrays), CSR invariants,
   and the identity ``csr_to_dense(dense_to_csr(D)) == D``.
+* ``csr_to_coo`` / ``coo_to_csr`` -- scipy's COO -> CSR conversion on
+  shuffled unique entries, the dense brute force (entries placed in a dense
+  matrix, then ``dense_to_csr``), and the round trip.
 * ``condense_windows`` -- reconstruction: scattering every window's
   condensed tile back through its column union gives the dense window; the
   union equals the set of nonzero columns; brute force on tiny inputs.
@@ -131,6 +134,33 @@ def csr_to_dense(rowptr, colidx, values, ncol):
         s, e = int(rowptr[r]), int(rowptr[r + 1])
         d[r, colidx[s:e]] = values[s:e]
     return d
+
+
+# ------------------------------------------------------------ COO <-> CSR
+def csr_to_coo(rowptr, colidx, values):
+    """COO entries of a CSR matrix in CSR order.  The reference names the COO
+    format only (mat_format::coo, src/mat_format.cuh:10-15); the CSR side
+    follows convert_dense_to_csr's semantics (src/miscalleneous.cu:29-65)."""
+    m = len(rowptr) - 1
+    rows = np.repeat(np.arange(m, dtype=np.int32), np.diff(np.asarray(rowptr, np.int64)))
+    return rows, np.asarray(colidx, np.int32).copy(), np.asarray(values).copy()
+
+
+def coo_to_csr(nrow, ncol, rows, cols, values):
+    """CSR of COO entries in any order: rows ascending, columns ascending in a
+    row (the CSR indexing of src/miscalleneous.cu:29-65).  Returns None for a
+    duplicate or out-of-range entry."""
+    rows = np.asarray(rows, np.int64)
+    cols = np.asarray(cols, np.int64)
+    if len(rows) and (rows.min() < 0 or rows.max() >= nrow or cols.min() < 0 or cols.max() >= ncol):
+        return None
+    order = np.lexsort((cols, rows))
+    r, c = rows[order], cols[order]
+    if len(r) > 1 and np.any((r[1:] == r[:-1]) & (c[1:] == c[:-1])):
+        return None
+    rowptr = np.zeros(nrow + 1, np.int32)
+    np.cumsum(np.bincount(r, minlength=nrow), out=rowptr[1:])
+    return rowptr, c.astype(np.int32), np.asarray(values)[order]
 
 
 # ------------------------------------------------------- condensed windows

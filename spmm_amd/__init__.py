@@ -235,6 +235,40 @@ def csr_to_dense(a: CSR) -> np.ndarray:
     return out
 
 
+def csr_to_coo(a: CSR):
+    """(row_idx, col_idx, values) of A in CSR order (tca_csr_to_coo)."""
+    s = a.as_struct()
+    o = _lib.TcaCoo()
+    call("tca_csr_to_coo", ctypes.byref(s), ctypes.byref(o))
+    try:
+        n = o.nnz
+        rows = np.ctypeslib.as_array(o.row_idx, shape=(n,)).copy() if n else np.zeros(0, np.int32)
+        cols = np.ctypeslib.as_array(o.col_idx, shape=(n,)).copy() if n else np.zeros(0, np.int32)
+        st = _STORAGE[o.dtype]
+        if n:
+            buf = (ctypes.c_char * (n * np.dtype(st).itemsize)).from_address(o.value)
+            vals = np.frombuffer(buf, dtype=st).copy()
+        else:
+            vals = np.zeros(0, st)
+    finally:
+        lib.tca_coo_free(ctypes.byref(o))
+    return rows, cols, vals
+
+
+def coo_to_csr(nrow: int, ncol: int, rows, cols, values, dtype: int) -> CSR:
+    """CSR of a COO matrix in any entry order (tca_coo_to_csr): rows, then
+    columns ascending; duplicate or out-of-range entries raise TcaError."""
+    r = np.ascontiguousarray(rows, np.int32)
+    c = np.ascontiguousarray(cols, np.int32)
+    v = np.ascontiguousarray(values, _STORAGE[dtype])
+    if not (len(r) == len(c) == len(v)):
+        raise ValueError("coo_to_csr: rows, cols and values differ in length")
+    s = _lib.TcaCoo(nrow, ncol, len(r), np_ptr(r, ctypes.c_int32), np_ptr(c, ctypes.c_int32), v.ctypes.data, dtype)
+    o = _lib.TcaCsr()
+    call("tca_coo_to_csr", ctypes.byref(s), ctypes.byref(o))
+    return CSR.from_struct(o)
+
+
 def compare_mat(gold: np.ndarray, cmp: np.ndarray, tol: float = 1e-3, floor: float = 1e-6,
                 verbose: bool = False) -> dict:
     g = np.ascontiguousarray(gold, np.float32).ravel()

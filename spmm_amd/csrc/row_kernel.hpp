@@ -276,8 +276,9 @@ __global__ __launch_bounds__(64) void seg_finalize_kernel(const int4* __restrict
         }
         for (; k < lr.z; k++) s += src[k * stride];
         *reinterpret_cast<f32x4*>(C + static_cast<size_t>(lr.x) * N + col) = s;
-    } else {
-        for (int c = col; c < N; c++) {
+    } else {  // this thread's columns [col, col + 4) only
+        const int cend = min(col + 4, N);
+        for (int c = col; c < cend; c++) {
             float s = 0.f;
             for (int k = 0; k < lr.z; k++) s += partials[static_cast<size_t>(lr.y + k) * N + c];
             C[static_cast<size_t>(lr.x) * N + c] = s;

@@ -365,6 +365,32 @@ void fill_info(tca_spmm_plan* p) {
                                                            : TCA_TILES_REGS;
 }
 
+// The reference prints its one kernel's grid, block and dynamic LDS
+// (src/our_spmm.cu:552).  A plan here launches up to four kernels
+// (run_phases); one line per kernel it launches, in launch order, same
+// format, the kernel named after it.
+void print_launches(const tca_spmm_plan* p) {
+    const tca_plan_info& in = p->info;
+    auto line = [](long long blocks, int dim, double lds_bytes, const char* name) {
+        std::printf("num_block: %lld blockdim: %d shm: %fKB (%s)\n", blocks, dim, lds_bytes / 1024.0, name);
+    };
+    if (!p->mfma.windows.empty()) {
+        if (p->mfma_dense || p->mfma_sparse) {
+            if (p->n_dn > 0) line((p->n_dn + 255) / 256, 256, 0.0, "dense_pack_kernel");
+        } else if (p->n_pk_words > 0) {
+            line((p->n_pk_words + 1023) / 1024, 256, 0.0, "mfma_pack_kernel");
+        }
+        static const char* names[] = {"", "mfma_tile_kernel", "mfma_dma_kernel", "mfma_pair_kernel",
+                                      "mfma_dense_kernel", "mfma_dense_kernel", "mfma_sparse_kernel",
+                                      "mfma_compact_kernel"};
+        line(in.mfma_blocks, in.mfma_blockdim, in.mfma_lds_bytes, names[in.tile_kernel]);
+    }
+    if (p->ntasks > 0)  // static LDS of row_kernel: kRowWaves partial row chunks of 64 lanes x E floats
+        line(in.row_blocks, in.row_blockdim, 4.0 * kRowWaves * 64 * p->rows.elems_per_lane, "row_kernel");
+    if (p->n_longrows > 0)
+        line(static_cast<long long>(p->n_longrows) * ((p->N + 255) / 256), 64, 0.0, "seg_finalize_kernel");
+}
+
 }  // namespace
 
 extern "C" {
@@ -1336,8 +1362,7 @@ int tca_spmm_host(const int32_t* rowptr, const int32_t* colidx, const void* val,
         // Same two lines as reference our_spmm_balanced (src/our_spmm.cu:549,552),
         // describing this build's plan: the row kernel's grid, block and LDS.
         std::printf("preprocess %fms taken\n", std::chrono::duration<float, std::milli>(t1 - t0).count());
-        std::printf("num_block: %d blockdim: %d shm: %fKB\n", plan->info.row_blocks, plan->info.row_blockdim,
-                    plan->info.mfma_lds_bytes / 1024.0f);
+        print_launches(plan);
     }
     float ms = 0.f;
     st = tca_spmm_time(plan, dval, dB, dC, nullptr, 5, n_iter, &ms);

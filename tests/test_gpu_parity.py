@@ -239,6 +239,21 @@ def test_exact_long_rows_many_segments(torch_cuda):
         assert np.array_equal(got, oracle_c(a, b)), n
 
 
+@pytest.mark.parametrize("n", [3, 13, 1023])
+def test_exact_segments_ragged_widths(torch_cuda, n):
+    """Segmented long rows at widths that are not a multiple of 4: the segment
+    sums take the scalar path, each thread its own (up to) 4 columns."""
+    rng = np.random.default_rng(23 + n)
+    k = 12000
+    a = make_csr(rng, [11000, 7, 9000, 0, 11999], k, S.TCA_F32)
+    b = S.to_storage(exact_dense(rng, (k, n)), S.TCA_F32)
+    with S.Plan(a, n, S.TCA_PLAN_NO_MFMA) as p:
+        info = p.info()
+        got = run_gpu(torch_cuda, a, b, plan=p)
+    assert info["n_long_rows"] >= 3, info
+    assert np.array_equal(got, oracle_c(a, b)), n
+
+
 def test_plan_reuse_and_determinism(torch_cuda):
     """One plan, several B: tickets reset between launches; identical bits on repeat."""
     rng = np.random.default_rng(31)

@@ -44,6 +44,10 @@ def test_harness_on_reference_fixture(torch_cuda):
     assert f"Input file - {FIXTURE_SMTX}" in out
     assert "preprocess " in out and "ms taken" in out
     assert "num_block: " in out and "blockdim: " in out and "shm: " in out
+    # one line per kernel the plan launches, each with a non-empty grid
+    launches = [l for l in out.splitlines() if l.startswith("num_block: ")]
+    assert launches and any(l.endswith("(row_kernel)") for l in launches), launches
+    assert all(int(l.split()[1]) > 0 for l in launches), launches
     assert "our: \x1b[36m[" in out and "validation failed" not in out
 
 

@@ -401,3 +401,75 @@ def test_plan_covers_every_row_once(n, dtype):
     # wide groups first, then segments, rows and multi groups
     kinds = [w & 3 for *_, w in tasks]
     assert kinds == sorted(kinds, key=lambda k: {3: 0, 2: 1, 0: 2, 1: 3}[k])
+
+
+# ------------------------------------------------------------------ COO
+def _shuffled_coo(rng, m, k, density):
+    d = rng.standard_normal((m, k)).astype(np.float32)
+    d[rng.random((m, k)) >= density] = 0
+    r, c = np.nonzero(d)
+    perm = rng.permutation(len(r))
+    return d, r[perm].astype(np.int32), c[perm].astype(np.int32), d[r, c][perm]
+
+
+def test_oracle_coo_pinned_by_scipy_and_dense():
+    import scipy.sparse as sp
+    rng = np.random.default_rng(61)
+    d, r, c, v = _shuffled_coo(rng, 37, 53, 0.15)
+    rp, ci, vv = oracle.coo_to_csr(37, 53, r, c, v)
+    ref = sp.coo_matrix((v, (r, c)), shape=(37, 53)).tocsr()
+    ref.sort_indices()
+    assert np.array_equal(rp, ref.indptr) and np.array_equal(ci, ref.indices) and np.array_equal(vv, ref.data)
+    drp, dci, dv = oracle.dense_to_csr(d)
+    assert np.array_equal(rp, drp) and np.array_equal(ci, dci) and np.array_equal(vv, dv)
+    rr, cc, v2 = oracle.csr_to_coo(rp, ci, vv)
+    assert np.array_equal(oracle.coo_to_csr(37, 53, rr, cc, v2)[1], ci)
+    assert oracle.coo_to_csr(3, 3, [0, 1, 0], [1, 2, 1], [1.0, 2.0, 3.0]) is None   # duplicate
+    assert oracle.coo_to_csr(3, 3, [0, 3], [1, 2], [1.0, 2.0]) is None             # row out of range
+    # a planted mistake (columns left in entry order) fails the pin
+    bad = np.argsort(r, kind="stable")
+    assert not np.array_equal(c[bad], ref.indices)
+
+
+@pytest.mark.parametrize("dtype", [S.TCA_F16, S.TCA_BF16, S.TCA_F32])
+def test_coo_conversions_match_oracle(dtype):
+    rng = np.random.default_rng(62 + dtype)
+    d, r, c, v = _shuffled_coo(rng, 120, 90, 0.1)
+    vs = S.to_storage(v, dtype)
+    a = S.coo_to_csr(120, 90, r, c, vs, dtype)
+    rp, ci, ov = oracle.coo_to_csr(120, 90, r, c, vs)
+    assert np.array_equal(a.rowptr, rp) and np.array_equal(a.colidx, ci) and np.array_equal(a.values, ov)
+    rows, cols, vals = S.csr_to_coo(a)
+    orr, occ, ovv = oracle.csr_to_coo(rp, ci, ov)
+    assert np.array_equal(rows, orr) and np.array_equal(cols, occ) and np.array_equal(vals, ovv)
+    # round trip CSR -> COO -> CSR is the identity
+    b = S.coo_to_csr(120, 90, rows, cols, vals, dtype)
+    assert np.array_equal(b.rowptr, a.rowptr) and np.array_equal(b.colidx, a.colidx) and np.array_equal(b.values, a.values)
+
+
+def test_coo_edge_cases_and_rejections():
+    z = S.coo_to_csr(4, 7, [], [], np.zeros(0, np.float32), S.TCA_F32)
+    assert z.nnz == 0 and np.array_equal(z.rowptr, np.zeros(5, np.int32))
+    rows, cols, vals = S.csr_to_coo(z)
+    assert len(rows) == len(cols) == len(vals) == 0
+    # empty rows between entries, a single column
+    a = S.coo_to_csr(5, 1, [4, 0, 2], [0, 0, 0], np.array([3, 1, 2], np.float32), S.TCA_F32)
+    assert a.rowptr.tolist() == [0, 1, 1, 2, 2, 3] and a.values.tolist() == [1.0, 2.0, 3.0]
+    for rows_, cols_ in (([0, 0], [1, 1]),      # duplicate entry
+                         ([0, 5], [1, 1]),      # row out of range
+                         ([0, 1], [1, -1]),     # negative column
+                         ([0, 1], [1, 3])):     # column out of range
+        with pytest.raises(S.TcaError):
+            S.coo_to_csr(5, 3, rows_, cols_, np.ones(2, np.float32), S.TCA_F32)
+
+
+def test_compat_coo_round_trip_binary():
+    """The reference-named C++ wrappers (csr_to_coo / coo_to_csr in
+    tca_compat.hpp), host only: round trip, unsorted input, rejections."""
+    import subprocess
+    exe = os.path.join(ROOT, "spmm_amd", "bin", "compat_formats")
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0 and "compat formats ok" in r.stdout, r.stdout + r.stderr
+    for mode in ("dup", "range"):
+        r = subprocess.run([exe, mode], capture_output=True, text=True, timeout=60)
+        assert r.returncode != 0 and "coo_to_csr" in r.stderr, (mode, r.stdout, r.stderr)
