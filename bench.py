@@ -1,11 +1,14 @@
 """Benchmark of the TCA-SpMM hot path on one MI355X.
 
 A "step" is one SpMM C = A * B over one batch of synthetic input, with A, B
-and C resident in HBM before the timed region starts.  Default workload:
-Benchmark configuration 1 (4096 x 4096 pruned linear layer, lognormal row lengths
-with mean 205, fp16 values, B 4096 x 512 fp16, fp32 C).  Prints ONE JSON line.
+and C resident in HBM before the timed region starts.  Headline workload:
+benchmark configuration 2, the largest one that fits one GPU (GCN
+aggregation: symmetric R-MAT graph with 232,965 nodes and ~114.8M nonzeros
+including self-loops, D^-1/2 (A+I) D^-1/2 in fp32, B 232,965 x 128 fp32).
+The other four configurations are timed in the same run and reported under
+config.other_configs.  Prints ONE JSON line.
 
-    python bench.py [--steps K] [--warmup W] [--config 0..4] [--gpus 1]
+    python bench.py [--steps K] [--warmup W] [--config 0..4] [--gpus 1] [--no-others] [--no-cpu]
 """
 import argparse
 import json
@@ -41,31 +44,55 @@ def phase_kernel(phase: str, tile_kernel: int) -> str:
     return {"rows": "row_kernel", "segments": "seg_finalize_kernel"}[phase]
 
 
-# HBM bytes per launch of the dominant kernel, measured with rocprofv3 --pmc
-# FETCH_SIZE and WRITE_SIZE (KiB per dispatch, already scaled by the copy
-# calibration: FETCH x 2.00, WRITE x 1.00), keyed by (config, kernel).
-# Source: the profiles/ summaries named in each entry.
-MEASURED_TRAFFIC_KIB = {
-    # profiles/mfma_compact_kernel_config1.md (compacted dense tiles over all of K, the default on config 1)
-    (1, "mfma_compact_kernel"): (24783.0 * 2.0, 8325.1),
-    # profiles/mfma_dense_kernel_config1.md (plain dense tiles over all of K, --flags 16)
-    (1, "mfma_dense_kernel"): (32839.5 * 2.0, 8248.8),
-    # profiles/mfma_pair_kernel_config1.md (paired tile kernel)
-    (1, "mfma_pair_kernel"): (21323.1 * 2.0, 8436.0),
-    # profiles/mfma_dma_kernel_config1.md (LDS-DMA tile kernel)
-    (1, "mfma_dma_kernel"): (39252.0 * 2.0, 8319.2),
-    # profiles/mfma_tile_kernel_config1.md (register-staged tile kernel)
-    (1, "mfma_tile_kernel"): (12768.8 * 2.0, 10785.3),
-    # profiles/row_kernel_graph_configs.md (row kernel, default routing)
-    (0, "row_kernel"): (1611.8 * 2.0, 3001.0),
-    (2, "row_kernel"): (12064593.2 * 2.0, 122066.5),
-    (3, "row_kernel"): (12350070.5 * 2.0, 1225462.5),
-    (4, "row_kernel"): (1298864.7 * 2.0, 402965.0),
-}
+# HBM traffic of the dominant kernel comes from profiles/traffic.json: one
+# entry per (config, kernel) with the rocprofv3 FETCH_SIZE / WRITE_SIZE
+# readings (KiB per dispatch) and the copy-calibrated scale factors, keyed
+# by a hash of the library's kernel and planner sources at the time of the
+# profile.  When no entry matches the current sources, the traffic is
+# reported as null (a kernel changed since it was profiled).
+TRAFFIC_JSON = os.path.join(ROOT, "profiles", "traffic.json")
+
+
+def source_sha() -> str:
+    """sha256 over the device and planner sources of libtcaspmm.so."""
+    import hashlib
+    h = hashlib.sha256()
+    csrc = os.path.join(ROOT, "spmm_amd", "csrc")
+    files = sorted(f for f in os.listdir(csrc) if f.endswith((".hpp", ".hip", ".cpp")))
+    for f in files:
+        h.update(f.encode())
+        with open(os.path.join(csrc, f), "rb") as fh:
+            h.update(fh.read())
+    return h.hexdigest()[:16]
+
+
+def measured_traffic(config: int, kernel: str, sha: str):
+    """(bytes per launch, profile file) for this config and kernel at these sources, else (None, None)."""
+    try:
+        with open(TRAFFIC_JSON) as fh:
+            entries = json.load(fh)["entries"]
+    except (OSError, ValueError, KeyError):
+        return None, None
+    for e in entries:
+        if e["config"] == config and e["kernel"] == kernel and e["source_sha"] == sha:
+            kib = e["fetch_kib"] * e["fetch_scale"] + e["write_kib"] * e["write_scale"]
+            return int(round(kib * 1024)), e["profile"]
+    return None, None
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
+
+
+def cpu_threads() -> int:
+    """Threads for the CPU baseline: the CPU share this process is given (its
+    affinity set, capped by OMP_NUM_THREADS where the host sets it; the GPU
+    boxes grant 16 threads per GPU)."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and int(omp) > 0:
+        n = min(n, int(omp))
+    return max(1, n)
 
 
 def main():
@@ -73,10 +100,13 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", type=int, default=1, choices=range(5))
+    ap.add_argument("--config", type=int, default=2, choices=range(5),
+                    help="headline workload (default 2: GCN aggregation, the largest configuration)")
     ap.add_argument("--seed", type=int, default=1)
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline time budget")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-others", action="store_true",
+                    help="skip the other four configurations (reported under config.other_configs)")
     ap.add_argument("--flags", type=int, default=0,
                     help="plan flags (1 = no MFMA, 2 = force MFMA, 4 = register-staged tile kernel, "
                          "8 = LDS-DMA tile kernel, 16 = dense-tile kernel, 32 = 2:4 sparse-core tiles, "
@@ -92,29 +122,47 @@ def main():
                          "row-kernel plans) instead of the host planner")
     ap.add_argument("--sparse24", action="store_true",
                     help="time the 2:4 sparse-MFMA kernel (tca_spmm_24) on A pruned to 2:4 (fp16 / bf16 configurations)")
-    ap.add_argument("--traffic-kib", type=float, nargs=2, default=None, metavar=("FETCH", "WRITE"),
-                    help="measured FETCH_SIZE and WRITE_SIZE of the dominant kernel per launch, already scaled "
-                         "by the copy calibration (KiB); reported as roofline.traffic in bytes")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
               file=sys.stderr)
         sys.exit(2)
 
+    import torch
+
+    if not torch.cuda.is_available():
+        sys.exit("bench.py needs a GPU")
+
+    if args.bell or args.sparse24:
+        ctx = make_inputs(args.config, args.seed)
+        (bell if args.bell else sparse24)(args, *ctx)
+        return
+
+    sha = source_sha()
+    head = measure(args.config, args, sha, headline=True)
+    others = {}
+    if not args.no_others:
+        for cfg in range(5):
+            if cfg != args.config:
+                r = measure(cfg, args, sha, headline=False)
+                others[str(cfg)] = r
+                log(f"config {cfg}:", json.dumps(r))
+    head["config"]["other_configs"] = others
+    print(json.dumps(head), flush=True)
+
+
+def make_inputs(cfg: int, seed: int):
+    """Config cfg's A (CSR), N, and device copies of values and B; C allocated."""
     import numpy as np
     import torch
 
     import spmm_amd as S
 
-    if not torch.cuda.is_available():
-        sys.exit("bench.py needs a GPU")
     dev = torch.device("cuda:0")
-
     t0 = time.time()
-    a, n, st = S.gen_config(args.config, seed=args.seed)
-    b = S.gen_dense(a.ncol, n, 1 if args.config in (2, 3) else 0, seed=args.seed + 100, dtype=a.dtype)
-    log(f"generated config {args.config}: M={a.nrow} K={a.ncol} N={n} nnz={a.nnz} stats={st} "
-        f"in {time.time() - t0:.1f}s")
+    a, n, st = S.gen_config(cfg, seed=seed)
+    b = S.gen_dense(a.ncol, n, 1 if cfg in (2, 3) else 0, seed=seed + 100, dtype=a.dtype)
+    log(f"generated config {cfg}: M={a.nrow} K={a.ncol} N={n} nnz={a.nnz} stats={st} in {time.time() - t0:.1f}s")
 
     def dev_tensor(x):
         x = np.ascontiguousarray(x)
@@ -123,12 +171,18 @@ def main():
     val = dev_tensor(a.values)
     bd = dev_tensor(b)
     c = torch.empty((a.nrow, n), dtype=torch.float32, device=dev)
-    if args.bell:
-        bell(args, a, n, bd, c, dev_tensor)
-        return
-    if args.sparse24:
-        sparse24(args, a, n, bd, c, dev_tensor)
-        return
+    return a, n, bd, c, dev_tensor, b, val
+
+
+def measure(cfg: int, args, sha: str, headline: bool) -> dict:
+    """Times one configuration; the full bench record for the headline, a
+    short record (time, GFLOP/s, dominant kernel and its roofline) otherwise."""
+    import numpy as np
+    import torch
+
+    import spmm_amd as S
+
+    a, n, bd, c, dev_tensor, b, val = make_inputs(cfg, args.seed)
     plan_first_ms = None
     if args.device_plan:
         drp, dci = dev_tensor(a.rowptr), dev_tensor(a.colidx)
@@ -147,8 +201,8 @@ def main():
     info = plan.info()
     log("plan:", json.dumps(info))
     stream = torch.cuda.current_stream()
-    if args.calib_copy > 0:
-        src = torch.empty(args.calib_copy << 18, dtype=torch.float32, device=dev)
+    if args.calib_copy > 0 and headline:
+        src = torch.empty(args.calib_copy << 18, dtype=torch.float32, device=c.device)
         dst = torch.empty_like(src)
         dst.copy_(src)
         torch.cuda.synchronize()
@@ -162,28 +216,13 @@ def main():
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - wall0) * 1e3
     if not torch.isfinite(c).all().item():
-        sys.exit("non-finite output")
+        sys.exit(f"config {cfg}: non-finite output")
     # Per-kernel durations (hipEvents between the kernels on the launch stream)
     # for the roofline of the dominant kernel.
     phases = plan.time_phases(val, bd, c, stream=stream.cuda_stream, warmup=1, iters=args.steps)
     torch.cuda.synchronize()
     dominant = max(phases, key=phases.get)
     log("phases (ms):", json.dumps(phases))
-    # Cold-cache SpMM: L2s and MALL flushed by writing a 512 MiB buffer
-    # before each timed run (median of 5), and the empty-kernel launch floor.
-    flush = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
-    cold = []
-    for _ in range(5):
-        flush.fill_(1)
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        plan.run(val, bd, c, stream=stream.cuda_stream)
-        e1.record(stream)
-        torch.cuda.synchronize()
-        cold.append(e0.elapsed_time(e1))
-    del flush
-    cold_ms = float(np.median(cold))
-    floor_ms = S.launch_floor(stream=stream.cuda_stream, iters=100)
 
     s_a = 4 if a.dtype == S.TCA_F32 else 2
     m, k, nnz = a.nrow, a.ncol, a.nnz
@@ -202,46 +241,73 @@ def main():
     dom_ms = phases[dominant]
     achieved = bytes_dom / (dom_ms * 1e-3) / 1e9
     kernel_name = phase_kernel(dominant, info["tile_kernel"])
-    kib = args.traffic_kib or MEASURED_TRAFFIC_KIB.get((args.config, kernel_name))
-    traffic = int(round((kib[0] + kib[1]) * 1024)) if kib else None
-    log(f"kernel avg {ms_per_step * 1e3:.2f} us/step, wall {wall_ms:.2f} ms for {args.warmup}+{args.steps} steps")
+    traffic, traffic_src = measured_traffic(cfg, kernel_name, sha)
+    log(f"config {cfg}: {ms_per_step * 1e3:.2f} us/step, wall {wall_ms:.2f} ms for {args.warmup}+{args.steps} steps")
+    roofline = {"bound": "hbm", "kernel": kernel_name, "bytes_alg": bytes_dom,
+                "kernel_us": round(dom_ms * 1e3, 3),
+                "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": traffic,
+                # measured L2 <-> fabric bytes of the same launch over its time (HBM or MALL)
+                "traffic_gbs": round(traffic / (dom_ms * 1e-3) / 1e9, 2) if traffic else None,
+                "traffic_profile": traffic_src, "source_sha": sha}
+    dtype = "f32" if a.dtype == S.TCA_F32 else ("f16" if a.dtype == S.TCA_F16 else "bf16") + "->f32acc"
+    if not headline:
+        plan.close()
+        return {"workload": WORKLOADS[cfg], "M": m, "K": k, "N": n, "nnz": nnz, "dtype": dtype,
+                "ms_per_step": round(ms_per_step, 6), "gflops": round(gflops, 3), "bytes_alg": bytes_alg,
+                "hbm_gbs_whole_step": round(hbm_gbs, 2),
+                "phases_us": {kk: round(v * 1e3, 3) for kk, v in phases.items()},
+                "tile_kernel": TILE_KERNELS.get(info["tile_kernel"], "none"), "roofline": roofline}
+
+    # Cold-cache SpMM: L2s and MALL flushed by writing a 512 MiB buffer
+    # before each timed run (median of 5), and the empty-kernel launch floor.
+    flush = torch.empty(512 << 20, dtype=torch.uint8, device=c.device)
+    cold = []
+    for _ in range(5):
+        flush.fill_(1)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        plan.run(val, bd, c, stream=stream.cuda_stream)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        cold.append(e0.elapsed_time(e1))
+    del flush
+    cold_ms = float(np.median(cold))
+    floor_ms = S.launch_floor(stream=stream.cuda_stream, iters=100)
 
     cpu = None
     if not args.no_cpu:
         from oracle import oracle
-        threads = min(16, os.cpu_count() or 1)
+        threads = cpu_threads()
         vf = a.values_f32()
         bf = S.from_storage(b, a.dtype)
-        # Bounded sample: the leading rows whose nonzeros total at most 50M
-        # (the whole matrix for configs 0 and 1), timed for ~cpu_seconds.
-        lim = np.searchsorted(a.rowptr, min(nnz, 50_000_000), side="right") - 1
-        rows = max(1, int(lim))
-        rp = a.rowptr[:rows + 1]
-        s_nnz = int(rp[-1])
+        # The whole matrix, repeated for about cpu_seconds (median run).
         times = []
         tc0 = time.perf_counter()
         while True:
             t1 = time.perf_counter()
-            oracle.csr_spmm(rp, a.colidx[:s_nnz], vf[:s_nnz], bf, threads)
+            oracle.csr_spmm(a.rowptr, a.colidx, vf, bf, threads)
             times.append(time.perf_counter() - t1)
             if time.perf_counter() - tc0 > args.cpu_seconds or len(times) >= 200:
                 break
         tmed = float(np.median(times))
-        # the same product on one thread, on the leading rows holding ~1/8 of the sample
-        rows1 = max(1, int(np.searchsorted(rp, s_nnz // 8, side="right") - 1))
-        nnz1 = int(rp[rows1])
+        # the same product on one thread, on the leading rows holding ~1/16 of the nonzeros
+        rows1 = max(1, int(np.searchsorted(a.rowptr, nnz // 16, side="right") - 1))
+        nnz1 = int(a.rowptr[rows1])
         times1 = []
         tc0 = time.perf_counter()
         while nnz1 > 0:
             t1 = time.perf_counter()
-            oracle.csr_spmm(rp[:rows1 + 1], a.colidx[:nnz1], vf[:nnz1], bf, 1)
+            oracle.csr_spmm(a.rowptr[:rows1 + 1], a.colidx[:nnz1], vf[:nnz1], bf, 1)
             times1.append(time.perf_counter() - t1)
             if time.perf_counter() - tc0 > args.cpu_seconds / 2 or len(times1) >= 50:
                 break
-        cpu = {"value": round(2.0 * s_nnz * n / tmed / 1e9, 3), "unit": "GFLOP/s", "cores": threads,
+        cpu = {"value": round(flops / tmed / 1e9, 3), "unit": "GFLOP/s", "cores": threads,
                "kind": "port",
-               "sample": f"oracle CSR SpMM (fp32 mul+add, k ascending) on rows [0,{rows}) = {s_nnz} nnz of the "
-                         f"same matrix, N={n}, median of {len(times)} runs",
+               "sample": f"oracle CSR SpMM (fp32 mul+add, k ascending, OpenMP over rows) on the whole matrix "
+                         f"({nnz} nnz, N={n}), median of {len(times)} runs; {threads} threads = this process's "
+                         f"CPU share (host nproc {os.cpu_count()})",
+               "host_nproc": os.cpu_count(),
                "value_1thread": round(2.0 * nnz1 * n / float(np.median(times1)) / 1e9, 3) if times1 else None,
                "sample_1thread": f"same, 1 thread, rows [0,{rows1}) = {nnz1} nnz, median of {len(times1)} runs"}
         log("cpu baseline:", json.dumps(cpu))
@@ -257,9 +323,9 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32" if a.dtype == S.TCA_F32 else ("f16" if a.dtype == S.TCA_F16 else "bf16") + "->f32acc",
+        "dtype": dtype,
         "data": "synthetic (seeded generators, seed %d)" % args.seed,
-        "config": {"workload": WORKLOADS[args.config], "M": m, "K": k, "N": n, "nnz": nnz,
+        "config": {"workload": WORKLOADS[cfg], "config_index": cfg, "M": m, "K": k, "N": n, "nnz": nnz,
                    "bytes_alg": bytes_alg, "hbm_gbs_whole_step": round(hbm_gbs, 2),
                    "plan_ms": round(info["plan_ms"], 3),
                    **({"plan_on_gpu": True, "plan_first_ms": round(plan_first_ms, 3)} if plan_first_ms is not None
@@ -268,19 +334,14 @@ def main():
                    "cold_cache_us": round(cold_ms * 1e3, 3), "launch_floor_us": round(floor_ms * 1e3, 3),
                    "mfma_windows": info["n_windows_mfma"], "rows_mfma": info["rows_mfma"],
                    "tile_kernel": TILE_KERNELS.get(info["tile_kernel"], "none")},
-        "roofline": {"bound": "hbm", "kernel": kernel_name, "bytes_alg": bytes_dom,
-                     "kernel_us": round(dom_ms * 1e3, 3),
-                     "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": traffic,
-                     # measured L2 <-> fabric bytes of the same launch over its time (HBM or MALL)
-                     "traffic_gbs": round(traffic / (dom_ms * 1e-3) / 1e9, 2) if traffic else None},
+        "roofline": roofline,
         "cpu_baseline": cpu,
     }
     plan.close()
-    print(json.dumps(out), flush=True)
+    return out
 
 
-def bell(args, a, n, bd, c, dev_tensor):
+def bell(args, a, n, bd, c, dev_tensor, *_):
     """The Blocked-ELL kernel on the configuration's A (one JSON line, same schema)."""
     import numpy as np
     import torch
@@ -347,7 +408,7 @@ def _time_launches(run, warmup, steps):
     return e0.elapsed_time(e1) / steps
 
 
-def sparse24(args, a, n, bd, c, dev_tensor):
+def sparse24(args, a, n, bd, c, dev_tensor, *_):
     """The 2:4 sparse-MFMA kernel on the configuration's A pruned to 2:4 (one JSON line)."""
     import torch
 
