@@ -41,7 +41,7 @@ def phase_kernel(phase: str, tile_kernel: int) -> str:
         return TILE_KERNELS.get(tile_kernel, "none")
     if phase == "pack":
         return "dense_pack_kernel" if tile_kernel in (4, 5, 6, 7) else "mfma_pack_kernel"
-    return {"rows": "row_kernel", "segments": "seg_finalize_kernel"}[phase]
+    return {"rows": "row_kernel", "segments": "seg_finalize_kernel", "panels": "panel_kernel"}[phase]
 
 
 # HBM traffic of the dominant kernel comes from profiles/traffic.json: one
@@ -235,8 +235,11 @@ def measure(cfg: int, args, sha: str, headline: bool) -> dict:
     # and write its rows of C once).
     if dominant == "tiles":
         rows_k, nnz_k = info["rows_mfma"], info["nnz_mfma"]
+    elif dominant == "panels":
+        rows_k, nnz_k = info["rows_panels"], info["nnz_panels"]
     else:
-        rows_k, nnz_k = m - info["rows_mfma"], nnz - info["nnz_mfma"]
+        rows_k = m - info["rows_mfma"] - info["rows_panels"]
+        nnz_k = nnz - info["nnz_mfma"] - info["nnz_panels"]
     bytes_dom = 4 * (rows_k + 1) + nnz_k * (4 + s_a) + k * n * s_a + rows_k * n * 4
     dom_ms = phases[dominant]
     achieved = bytes_dom / (dom_ms * 1e-3) / 1e9
@@ -333,6 +336,9 @@ def measure(cfg: int, args, sha: str, headline: bool) -> dict:
                    "phases_us": {kk: round(v * 1e3, 3) for kk, v in phases.items()},
                    "cold_cache_us": round(cold_ms * 1e3, 3), "launch_floor_us": round(floor_ms * 1e3, 3),
                    "mfma_windows": info["n_windows_mfma"], "rows_mfma": info["rows_mfma"],
+                   "panels": info["n_panels"], "panel_units": info["n_panel_units"],
+                   "rows_panels": info["rows_panels"], "nnz_panels": info["nnz_panels"],
+                   "staged_panels": info["staged_panels"],
                    "tile_kernel": TILE_KERNELS.get(info["tile_kernel"], "none")},
         "roofline": roofline,
         "cpu_baseline": cpu,

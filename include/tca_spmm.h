@@ -61,6 +61,14 @@ typedef enum tca_status {
 #define TCA_PLAN_MFMA_PAIR 64u  /* paired (MFMA + staging wavefront) 128 x 64 kernel, whatever the windows */
 #define TCA_PLAN_MFMA_COMPACT 128u /* dense-tile kernel on compacted steps (only the non-empty 16-byte
                                       fragment cells, at most 255 per step; else plain dense tiles) */
+/* Row panels with B staged in LDS (the panel kernel): by default rows not in
+ * MFMA windows are grouped longest first into panels whose nonzeros reuse
+ * their column union at least twice on average; such panels run on the
+ * panel kernel, other rows on the row kernel.  Needs N % (16 E) == 0 for an
+ * E in {8, 4, 2} with E * element size in 8..32 bytes; by default also B
+ * rows of at least 256 bytes and at least 2^21 nonzeros in panels. */
+#define TCA_PLAN_NO_PANELS 256u    /* no panels: rows outside MFMA windows go to the row kernel */
+#define TCA_PLAN_FORCE_PANELS 512u /* every eligible row in panels, whatever their reuse */
 
 typedef struct tca_spmm_plan tca_spmm_plan;
 
@@ -92,6 +100,14 @@ typedef struct tca_plan_info {
     int32_t row_len;          /* rows up to this length take one wavefront */
     int32_t wide_len;         /* rows up to this length take one workgroup; longer rows are segmented */
     int32_t tile_kernel;      /* MFMA tile kernel of the plan: TCA_TILES_* */
+    int32_t n_panels;         /* row panels on the panel kernel (B rows staged in LDS) */
+    int32_t n_panel_units;    /* workgroup units of those panels */
+    int32_t rows_panels;      /* rows in panels */
+    int32_t panel_blocks;     /* workgroups of the panel kernel */
+    int64_t nnz_panels;       /* nonzeros in panels */
+    int64_t staged_panels;    /* B rows staged per run (column unions summed over panels) */
+    int32_t panel_blockdim;   /* threads per workgroup of the panel kernel */
+    int32_t panel_lds_bytes;  /* LDS per panel workgroup */
 } tca_plan_info;
 
 /* tca_plan_info.tile_kernel */
@@ -130,9 +146,10 @@ int tca_spmm_time(const tca_spmm_plan* plan, const void* d_val, const void* d_B,
                   void* stream, int32_t warmup, int32_t iters, float* avg_ms);
 
 /* Phases of one run, in stream order: value pack for the MFMA tiles, MFMA
- * tile kernel, row kernel, long-row segment sums. */
-#define TCA_PHASES 4
-enum { TCA_PHASE_PACK = 0, TCA_PHASE_TILES = 1, TCA_PHASE_ROWS = 2, TCA_PHASE_SEGMENTS = 3 };
+ * tile kernel, panel kernel, row kernel, segment sums of split rows (the
+ * panel phase has index 4 so the older indices stay as they were). */
+#define TCA_PHASES 5
+enum { TCA_PHASE_PACK = 0, TCA_PHASE_TILES = 1, TCA_PHASE_ROWS = 2, TCA_PHASE_SEGMENTS = 3, TCA_PHASE_PANELS = 4 };
 
 /* Per-phase timing: `warmup` + 1 full runs, then each phase the plan uses is
  * launched alone `iters` times back to back between two hipEvents on
@@ -274,6 +291,21 @@ int tca_plan_row_tasks(const int32_t* rowptr, int32_t M, int32_t K, int32_t N, i
 int tca_plan_mfma_windows(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_t N, int32_t dtype,
                           uint32_t flags, int32_t* n_windows, int32_t* n_steps, int64_t* n_entries,
                           int32_t* windows, int32_t* ucols, int32_t* eoff, uint32_t* entries);
+
+/* ---- host-only view of the panel plan (no device needed) ----
+ * The row panels tca_spmm_plan_create gives the panel kernel for this
+ * structure, width N, dtype and flags (after MFMA routing).  Call with
+ * rows == NULL to get sizes[16] = {panels, tiles, units, long rows, R, P,
+ * consumer waves, rows per lane group, elements per lane, column chunks,
+ * nonzeros in panels, staged columns, partial segments, rows in panels,
+ * count bytes per tile, 0}; then with rows[panels*R], cols[tiles*P],
+ * width[tiles], cnt[tiles * sizes[14]], pos[nnz], units[4*units], panel_units[panels],
+ * ustart[units*R], longrows[4*long rows].  Layouts: see PanelPlan in
+ * spmm_amd/csrc/planner.hpp.  No counterpart in the reference. */
+int tca_plan_panels(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_t K, int32_t N,
+                    int32_t dtype, uint32_t flags, int64_t* sizes, int32_t* rows, int32_t* cols,
+                    uint8_t* width, uint8_t* cnt, uint8_t* pos, int32_t* units, int32_t* panel_units,
+                    int32_t* ustart, int32_t* longrows);
 
 /* Launches a trivial kernel on the current device and synchronises
  * (reference warm_up_gpu_kernel, src/miscalleneous.cu:158-164, launched

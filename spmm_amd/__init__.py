@@ -20,11 +20,11 @@ from dataclasses import dataclass
 import numpy as np
 
 from . import _lib
-from ._lib import (TCA_BF16, TCA_F16, TCA_F32, TCA_PLAN_DEFAULT, TCA_PLAN_FORCE_MFMA, TCA_PLAN_MFMA_DMA, TCA_PLAN_MFMA_DENSE, TCA_PLAN_MFMA_SPARSE, TCA_PLAN_MFMA_PAIR, TCA_PLAN_MFMA_COMPACT, TCA_PLAN_MFMA_REGS, TCA_PLAN_NO_MFMA, TCA_TILES_NONE, TCA_TILES_REGS, TCA_TILES_DMA, TCA_TILES_PAIR, TCA_TILES_DENSE, TCA_TILES_DENSE_K, TCA_TILES_SPARSE, TCA_TILES_COMPACT,
+from ._lib import (TCA_BF16, TCA_F16, TCA_F32, TCA_PLAN_DEFAULT, TCA_PLAN_FORCE_MFMA, TCA_PLAN_MFMA_DMA, TCA_PLAN_MFMA_DENSE, TCA_PLAN_MFMA_SPARSE, TCA_PLAN_MFMA_PAIR, TCA_PLAN_MFMA_COMPACT, TCA_PLAN_MFMA_REGS, TCA_PLAN_NO_MFMA, TCA_PLAN_NO_PANELS, TCA_PLAN_FORCE_PANELS, TCA_TILES_NONE, TCA_TILES_REGS, TCA_TILES_DMA, TCA_TILES_PAIR, TCA_TILES_DENSE, TCA_TILES_DENSE_K, TCA_TILES_SPARSE, TCA_TILES_COMPACT,
                    TcaError,
                    call, lib, np_ptr)
 
-__all__ = ["CSR", "Plan", "TcaError", "TCA_F16", "TCA_F32", "TCA_BF16", "TCA_PLAN_DEFAULT", "TCA_PLAN_NO_MFMA",
+__all__ = ["CSR", "Plan", "TcaError", "TCA_F16", "TCA_F32", "TCA_BF16", "TCA_PLAN_DEFAULT", "TCA_PLAN_NO_MFMA", "TCA_PLAN_NO_PANELS", "TCA_PLAN_FORCE_PANELS",
            "TCA_PLAN_FORCE_MFMA", "TCA_PLAN_MFMA_REGS", "TCA_PLAN_MFMA_DMA", "TCA_PLAN_MFMA_DENSE", "TCA_PLAN_MFMA_SPARSE", "TCA_PLAN_MFMA_PAIR", "TCA_PLAN_MFMA_COMPACT", "TCA_TILES_NONE", "TCA_TILES_REGS", "TCA_TILES_DMA", "TCA_TILES_PAIR", "TCA_TILES_DENSE", "TCA_TILES_DENSE_K", "TCA_TILES_SPARSE", "TCA_TILES_COMPACT", "read_smtx", "read_smtx_dense", "write_smtx", "read_mtx", "write_values", "write_csr_binary",
            "read_csr_binary", "launch_floor", "dense_to_csr", "csr_to_bell", "bell_spmm", "prune_24", "csr_to_24", "spmm_24",
            "csr_to_dense", "compare_mat", "gen_config", "gen_dense", "gen_bernoulli", "gen_lognormal_rows",
@@ -342,6 +342,40 @@ def plan_mfma_windows(a: CSR, n: int, dtype: int = None, flags: int = TCA_PLAN_D
     return windows[:nw.value], ucols[:ns.value * 32], eoff, entries[:ne.value]
 
 
+def plan_panels(a: CSR, n: int, flags: int = TCA_PLAN_DEFAULT, dtype: int = None) -> dict:
+    """Host view of the panel plan (tca_plan_panels) as numpy arrays."""
+    dtype = a.dtype if dtype is None else dtype
+    rp = np.ascontiguousarray(a.rowptr, np.int32)
+    ci = np.ascontiguousarray(a.colidx, np.int32)
+    sizes = np.zeros(16, np.int64)
+    args = (np_ptr(rp, ctypes.c_int32), np_ptr(ci, ctypes.c_int32), a.nrow, a.ncol, n, dtype, flags,
+            np_ptr(sizes, ctypes.c_int64))
+    call("tca_plan_panels", *args, None, None, None, None, None, None, None, None, None)
+    (n_panels, n_tiles, n_units, n_long, R, P, waves, rpg, elems, chunks, nnz_p, staged, n_seg, n_rows,
+     stride, _) = (int(x) for x in sizes)
+    out = dict(panels=n_panels, tiles=n_tiles, n_units=n_units, R=R, P=P, waves=waves, rpg=rpg, elems=elems,
+               chunks=chunks, nnz=nnz_p, staged=staged, segments=n_seg, n_rows=n_rows, cnt_stride=stride,
+               rows=np.zeros(max(n_panels * R, 1), np.int32), cols=np.zeros(max(n_tiles * P, 1), np.int32),
+               width=np.zeros(max(n_tiles, 1), np.uint8),
+               cnt=np.zeros(max(n_tiles * stride, 1), np.uint8), pos=np.zeros(max(a.nnz, 1), np.uint8),
+               units=np.zeros((max(n_units, 1), 4), np.int32), panel_units=np.zeros(max(n_panels, 1), np.int32),
+               ustart=np.zeros(max(n_units * R, 1), np.int32), longrows=np.zeros((max(n_long, 1), 4), np.int32))
+    call("tca_plan_panels", *args, np_ptr(out["rows"], ctypes.c_int32), np_ptr(out["cols"], ctypes.c_int32),
+         out["width"].ctypes.data, out["cnt"].ctypes.data, out["pos"].ctypes.data, np_ptr(out["units"], ctypes.c_int32),
+         np_ptr(out["panel_units"], ctypes.c_int32), np_ptr(out["ustart"], ctypes.c_int32),
+         np_ptr(out["longrows"], ctypes.c_int32))
+    out["rows"] = out["rows"][:n_panels * R]
+    out["cols"] = out["cols"][:n_tiles * P]
+    out["width"] = out["width"][:n_tiles]
+    out["cnt"] = out["cnt"][:n_tiles * stride]
+    out["pos"] = out["pos"][:a.nnz]
+    out["units"] = out["units"][:n_units]
+    out["panel_units"] = out["panel_units"][:n_panels]
+    out["ustart"] = out["ustart"][:n_units * R]
+    out["longrows"] = out["longrows"][:n_long]
+    return out
+
+
 # ----------------------------------------------------------- generators
 def gen_dense(rows: int, cols: int, dist: int = 0, seed: int = 1, dtype: int = TCA_F16,
               sparsity: float = 0.0) -> np.ndarray:
@@ -464,13 +498,14 @@ class Plan:
              _addr(stream) if stream is not None else None, warmup, iters, ctypes.byref(ms))
         return ms.value
 
-    PHASES = ("pack", "tiles", "rows", "segments")
+    PHASES = ("pack", "tiles", "rows", "segments", "panels")
 
     def time_phases(self, val, b, c, stream=None, warmup: int = 5, iters: int = 10) -> dict:
         """Mean milliseconds of one launch of each phase (MFMA value pack, MFMA
-        tiles, row kernel, long-row segment sums): each phase launched alone
-        `iters` times back to back between hipEvents on the run's stream."""
-        ms = (ctypes.c_float * 4)()
+        tiles, row kernel, segment sums of split rows, panel kernel): each
+        phase launched alone `iters` times back to back between hipEvents on
+        the run's stream."""
+        ms = (ctypes.c_float * len(self.PHASES))()
         call("tca_spmm_time_phases", self._p, _addr(val), _addr(b), _addr(c),
              _addr(stream) if stream is not None else None, warmup, iters, ms)
         return {k: float(ms[i]) for i, k in enumerate(self.PHASES)}

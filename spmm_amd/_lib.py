@@ -22,6 +22,8 @@ TCA_PLAN_MFMA_DENSE = 16
 TCA_PLAN_MFMA_SPARSE = 32
 TCA_PLAN_MFMA_PAIR = 64
 TCA_PLAN_MFMA_COMPACT = 128
+TCA_PLAN_NO_PANELS = 256
+TCA_PLAN_FORCE_PANELS = 512
 # tile kernel of a plan (tca_plan_info.tile_kernel)
 TCA_TILES_NONE, TCA_TILES_REGS, TCA_TILES_DMA, TCA_TILES_PAIR = 0, 1, 2, 3
 TCA_TILES_DENSE, TCA_TILES_DENSE_K, TCA_TILES_SPARSE, TCA_TILES_COMPACT = 4, 5, 6, 7
@@ -55,7 +57,9 @@ class TcaPlanInfo(ctypes.Structure):
                 ("row_blocks", i32), ("row_blockdim", i32), ("mfma_blocks", i32), ("mfma_blockdim", i32),
                 ("mfma_lds_bytes", i32), ("seg_len", i32), ("scratch_bytes", i64), ("plan_ms", ctypes.c_double),
                 ("n_wide_tasks", i32), ("chunk_lanes", i32), ("row_len", i32), ("wide_len", i32),
-                ("tile_kernel", i32)]
+                ("tile_kernel", i32), ("n_panels", i32), ("n_panel_units", i32), ("rows_panels", i32),
+                ("panel_blocks", i32), ("nnz_panels", i64), ("staged_panels", i64), ("panel_blockdim", i32),
+                ("panel_lds_bytes", i32)]
 
     def as_dict(self):
         return {name: getattr(self, name) for name, _ in self._fields_}
@@ -97,6 +101,8 @@ SIGNATURES = {
     "tca_plan_row_tasks": (i32, [i32p, i32, i32, i32, i32, i32p, i32p, i32p, i32p, i32p, i32p, i32p]),
     "tca_plan_mfma_windows": (i32, [i32p, i32p, i32, i32, i32, u32, i32p, i32p, i64p, i32p, i32p, i32p,
                                     ctypes.POINTER(ctypes.c_uint32)]),
+    "tca_plan_panels": (i32, [i32p, i32p, i32, i32, i32, i32, u32, i64p, i32p, i32p, vp, vp, vp, i32p, i32p,
+                              i32p, i32p]),
     "tca_status_string": (ctypes.c_char_p, [i32]),
     "tca_last_error": (ctypes.c_char_p, []),
     "tca_device_count": (i32, [i32p]),

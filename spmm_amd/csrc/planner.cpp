@@ -399,6 +399,257 @@ void plan_mfma24(const MfmaPlan& m, const int32_t* rowptr, const int32_t* colidx
     for (auto& v : wpos) p->pos.insert(p->pos.end(), v.begin(), v.end());
 }
 
+int32_t panel_elems(int32_t N, int32_t es) {
+    for (int32_t e = 8; e >= 2; e >>= 1)
+        if (N % (16 * e) == 0 && e * es >= 8 && e * es <= 32) return e;
+    return 0;
+}
+
+bool panel_default_ok(int32_t N, int32_t es) {
+    // B rows of at least 256 bytes: with narrower rows the row kernel's
+    // gathers are cheap and win (measured on MI355X, configuration 4, fp16
+    // N = 64: 0.60 ms with panels, 0.44 ms on the row kernel alone).
+    const int32_t e = panel_elems(N, es);
+    return e > 0 && static_cast<int64_t>(N) * es >= 256;
+}
+
+int32_t panel_tile_cols(int32_t chunk_bytes) { return std::min<int32_t>(255, 65536 / chunk_bytes); }
+
+void plan_panels_routed(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_t K, int32_t N,
+                        int32_t dtype, uint32_t flags, const std::vector<uint8_t>& skip, PanelPlan* p) {
+    if ((flags & TCA_PLAN_NO_PANELS) ||
+        (!(flags & TCA_PLAN_FORCE_PANELS) && !panel_default_ok(N, static_cast<int32_t>(dtype_size(dtype))))) {
+        *p = PanelPlan{};
+        p->row_panel.assign(M, 0);
+        return;
+    }
+    double min_reuse = kPanelMinReuse;
+    int64_t unit = 0, min_nnz = kPanelMinNnz;
+    // Tuning overrides (not part of the interface).
+    if (const char* e = std::getenv("TCA_PANEL_MIN_REUSE")) min_reuse = std::atof(e);
+    if (const char* e = std::getenv("TCA_PANEL_MIN_NNZ")) min_nnz = std::atoll(e);
+    if (const char* e = std::getenv("TCA_PANEL_UNIT")) unit = std::atoll(e);
+    plan_panels(rowptr, colidx, M, K, N, static_cast<int32_t>(dtype_size(dtype)), skip,
+                (flags & TCA_PLAN_FORCE_PANELS) != 0, min_reuse, min_nnz, unit, p);
+}
+
+void plan_panels(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_t K, int32_t N, int32_t es,
+                 const std::vector<uint8_t>& skip, bool force, double min_reuse, int64_t min_nnz, int64_t unit_nnz,
+                 PanelPlan* p) {
+    *p = PanelPlan{};
+    p->row_panel.assign(M, 0);
+    const int32_t E = panel_elems(N, es);
+    if (E == 0 || M == 0) return;
+    p->elems = E;
+    p->chunks = N / (16 * E);
+    p->waves = kPanelWaves;
+    p->rpg = kPanelRpg;
+    p->R = p->waves * 4 * p->rpg;
+    p->P = panel_tile_cols(16 * E * es);
+    const int32_t R = p->R, P = p->P, G = p->waves * 4;
+    auto len = [&](int32_t r) { return rowptr[r + 1] - rowptr[r]; };
+
+    std::vector<int32_t> order;
+    order.reserve(M);
+    for (int32_t r = 0; r < M; r++)
+        if ((skip.empty() || !skip[r]) && len(r) > 0) order.push_back(r);
+    std::stable_sort(order.begin(), order.end(), [&](int32_t a, int32_t b) { return len(a) > len(b); });
+    const int32_t n_cand = static_cast<int32_t>((order.size() + R - 1) / R);
+    if (n_cand == 0) return;
+
+    // Pass 1 (parallel over candidate panels): slot assignment, sorted column
+    // union, and whether the panel is taken.
+    struct Cand {
+        std::vector<int32_t> slots;  // R entries: row id or -1
+        std::vector<int32_t> uni;
+        std::vector<int32_t> cuts;  // tile t = union positions [cuts[t], cuts[t + 1])
+        int64_t nnz = 0;
+        bool take = false;
+    };
+    std::vector<Cand> cand(n_cand);
+#pragma omp parallel
+    {
+        std::vector<int32_t> mark(K, -1), posmap(K, 0);
+#pragma omp for schedule(dynamic, 1)
+        for (int32_t q = 0; q < n_cand; q++) {
+            Cand& c = cand[q];
+            c.slots.assign(R, -1);
+            const size_t first = static_cast<size_t>(q) * R;
+            const size_t cnt = std::min<size_t>(R, order.size() - first);
+            for (size_t k = 0; k < cnt; k++) {
+                // k-th longest row of the panel -> group k % G, row entry k / G
+                const int32_t gi = static_cast<int32_t>(k % G), i = static_cast<int32_t>(k / G);
+                const int32_t wave = gi / 4, group = gi % 4;
+                const int32_t row = order[first + k];
+                c.slots[(wave * p->rpg + i) * 4 + group] = row;
+                c.nnz += len(row);
+                for (int32_t j = rowptr[row]; j < rowptr[row + 1]; j++)
+                    if (mark[colidx[j]] != q) {
+                        mark[colidx[j]] = q;
+                        c.uni.push_back(colidx[j]);
+                    }
+            }
+            std::sort(c.uni.begin(), c.uni.end());
+            c.take = !c.uni.empty() && (force || static_cast<double>(c.nnz) >= min_reuse * c.uni.size());
+            if (!c.take) {
+                c.uni.clear();
+                continue;
+            }
+            // Tiles: ranges of the union of at most P columns in which no row
+            // holds more than kPanelMaxRun nonzeros (one 16-lane batch).
+            const int32_t U = static_cast<int32_t>(c.uni.size());
+            for (int32_t u = 0; u < U; u++) posmap[c.uni[u]] = u;
+            std::vector<int32_t> head(U + 1, 0);  // slots holding union column u: colslot[head[u] .. head[u+1])
+            for (int32_t s = 0; s < R; s++) {
+                const int32_t row = c.slots[s];
+                if (row >= 0)
+                    for (int32_t j = rowptr[row]; j < rowptr[row + 1]; j++) head[posmap[colidx[j]] + 1]++;
+            }
+            for (int32_t u = 0; u < U; u++) head[u + 1] += head[u];
+            std::vector<uint16_t> colslot(head[U]);
+            {
+                std::vector<int32_t> fill(head.begin(), head.end() - 1);
+                for (int32_t s = 0; s < R; s++) {
+                    const int32_t row = c.slots[s];
+                    if (row >= 0)
+                        for (int32_t j = rowptr[row]; j < rowptr[row + 1]; j++)
+                            colslot[fill[posmap[colidx[j]]]++] = static_cast<uint16_t>(s);
+                }
+            }
+            std::vector<int32_t> run(R, 0);
+            c.cuts.assign(1, 0);
+            for (int32_t u = 0; u < U; u++) {
+                bool cut = u - c.cuts.back() == P;
+                for (int32_t h = head[u]; h < head[u + 1] && !cut; h++) cut = run[colslot[h]] == kPanelMaxRun;
+                if (cut) {
+                    for (int32_t v = c.cuts.back(); v < u; v++)
+                        for (int32_t h = head[v]; h < head[v + 1]; h++) run[colslot[h]] = 0;
+                    c.cuts.push_back(u);
+                }
+                for (int32_t h = head[u]; h < head[u + 1]; h++) run[colslot[h]]++;
+            }
+            c.cuts.push_back(U);
+        }
+    }
+
+    // Tile and unit layout (sequential: global offsets).
+    int64_t tot = 0;
+    for (const Cand& c : cand)
+        if (c.take) tot += c.nnz;
+    // Too few nonzeros for the panel kernel's workgroups to fill the GPU: the
+    // row kernel's short tasks do better (measured on the 2048 x 512
+    // configuration 0, 105k nonzeros: 52.6 us on panels, 5.6 us on rows).
+    if (tot == 0 || (!force && tot < min_nnz)) {
+        p->n_panels = 0;
+        p->rows.clear();
+        p->cols.clear();
+        p->width.clear();
+        p->cnt.clear();
+        p->pos.clear();
+        return;
+    }
+    if (unit_nnz <= 0) unit_nnz = std::min<int64_t>(262144, std::max<int64_t>(8192, tot / 2048));
+    std::vector<int32_t> panel_of(n_cand, -1), tile0(n_cand, 0);
+    int32_t n_tiles = 0;
+    for (int32_t q = 0; q < n_cand; q++) {
+        if (!cand[q].take) continue;
+        panel_of[q] = p->n_panels++;
+        tile0[q] = n_tiles;
+        n_tiles += static_cast<int32_t>(cand[q].cuts.size()) - 1;
+    }
+    p->rows.assign(static_cast<size_t>(p->n_panels) * R, -1);
+    p->cols.assign(static_cast<size_t>(n_tiles) * P, 0);
+    p->width.assign(n_tiles, 0);
+    const size_t cnt_stride = static_cast<size_t>(p->waves) * kPanelCntRows * 4;  // bytes per tile
+    p->cnt.assign(static_cast<size_t>(n_tiles) * cnt_stride, 0);
+    p->pos.assign((static_cast<size_t>(rowptr[M]) + 3) & ~size_t(3), 0);  // whole dwords (the kernel loads dwords)
+
+    // Pass 2 (parallel over taken panels): positions, counts.
+#pragma omp parallel
+    {
+        std::vector<int32_t> posmap(K, 0);
+#pragma omp for schedule(dynamic, 1)
+        for (int32_t q = 0; q < n_cand; q++) {
+            if (!cand[q].take) continue;
+            const Cand& c = cand[q];
+            const int32_t pid = panel_of[q], t0 = tile0[q];
+            const int32_t U = static_cast<int32_t>(c.uni.size());
+            const int32_t nt = static_cast<int32_t>(c.cuts.size()) - 1;
+            std::vector<int32_t> tile_of(U);
+            for (int32_t t = 0; t < nt; t++) {
+                p->width[t0 + t] = static_cast<uint8_t>(c.cuts[t + 1] - c.cuts[t]);
+                for (int32_t u = c.cuts[t]; u < c.cuts[t + 1]; u++) tile_of[u] = t;
+                for (int32_t j = 0; j < P; j++)  // padding repeats the tile's last column
+                    p->cols[static_cast<size_t>(t0 + t) * P + j] = c.uni[std::min(c.cuts[t] + j, c.cuts[t + 1] - 1)];
+            }
+            for (int32_t u = 0; u < U; u++) posmap[c.uni[u]] = u;
+            for (int32_t s = 0; s < R; s++) {
+                const int32_t row = c.slots[s];
+                p->rows[static_cast<size_t>(pid) * R + s] = row;
+                if (row < 0) continue;
+                const int32_t wave = s / (4 * p->rpg), i = (s / 4) % p->rpg, group = s % 4;
+                for (int32_t k = rowptr[row]; k < rowptr[row + 1]; k++) {
+                    const int32_t u = posmap[colidx[k]];
+                    const int32_t t = tile_of[u];
+                    p->pos[k] = static_cast<uint8_t>(u - c.cuts[t]);
+                    p->cnt[static_cast<size_t>(t0 + t) * cnt_stride + (wave * kPanelCntRows + i) * 4 + group]++;
+                }
+                p->row_panel[row] = 1;
+            }
+        }
+    }
+
+    // Units: each panel's tiles, split by nonzeros into units of ~unit_nnz.
+    int64_t seg = 0;
+    for (int32_t q = 0; q < n_cand; q++) {
+        if (!cand[q].take) continue;
+        const Cand& c = cand[q];
+        const int32_t pid = panel_of[q], t0 = tile0[q];
+        const int32_t nt = static_cast<int32_t>(c.cuts.size()) - 1;
+        const int32_t nu = static_cast<int32_t>(std::max<int64_t>(1, std::min<int64_t>(nt, (c.nnz + unit_nnz - 1) / unit_nnz)));
+        // tile nonzeros, then cut points at multiples of nnz / nu
+        std::vector<int64_t> tn(nt, 0);
+        for (int32_t t = 0; t < nt; t++) {
+            const uint8_t* cb = &p->cnt[static_cast<size_t>(t0 + t) * cnt_stride];
+            for (size_t b = 0; b < cnt_stride; b++) tn[t] += cb[b];
+        }
+        std::vector<int32_t> cut = {0};
+        int64_t acc = 0;
+        for (int32_t t = 0; t < nt; t++) {
+            acc += tn[t];
+            const int64_t want = c.nnz * static_cast<int64_t>(cut.size()) / nu;
+            if (acc >= want && static_cast<int32_t>(cut.size()) < nu && t + 1 < nt) cut.push_back(t + 1);
+        }
+        cut.push_back(nt);
+        const int32_t units = static_cast<int32_t>(cut.size()) - 1;
+        const int32_t first_seg = units > 1 ? static_cast<int32_t>(seg) : -1;
+        // per slot cursor walking the tiles
+        std::vector<int32_t> cur(R, 0);
+        for (int32_t s = 0; s < R; s++) cur[s] = c.slots[s] >= 0 ? rowptr[c.slots[s]] : 0;
+        for (int32_t k = 0; k < units; k++) {
+            p->units.push_back({pid, t0 + cut[k], cut[k + 1] - cut[k], units > 1 ? first_seg + k : -1});
+            for (int32_t s = 0; s < R; s++) p->ustart.push_back(cur[s]);
+            for (int32_t t = cut[k]; t < cut[k + 1]; t++) {
+                const uint8_t* cb = &p->cnt[static_cast<size_t>(t0 + t) * cnt_stride];
+                for (int32_t s = 0; s < R; s++) {
+                    const int32_t wave = s / (4 * p->rpg), i = (s / 4) % p->rpg, group = s % 4;
+                    cur[s] += cb[(wave * kPanelCntRows + i) * 4 + group];
+                }
+            }
+        }
+        p->panel_units.push_back(units);
+        if (units > 1) {
+            for (int32_t s = 0; s < R; s++)
+                if (c.slots[s] >= 0) p->longrows.push_back({c.slots[s], first_seg + s * units, units, 0});
+            seg += static_cast<int64_t>(R) * units;
+        }
+        p->nnz += c.nnz;
+        p->staged += static_cast<int64_t>(c.uni.size());
+        for (int32_t s = 0; s < R; s++) p->n_rows += c.slots[s] >= 0;
+    }
+    p->n_segments = seg;
+}
+
 }  // namespace tca
 
 extern "C" int tca_condense_windows(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_t nnz,
@@ -473,5 +724,49 @@ extern "C" int tca_plan_mfma_windows(const int32_t* rowptr, const int32_t* colid
     *n_windows = static_cast<int32_t>(p.windows.size());
     *n_steps = steps;
     *n_entries = static_cast<int64_t>(p.entries.size());
+    return TCA_OK;
+}
+
+extern "C" int tca_plan_panels(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_t K, int32_t N,
+                               int32_t dtype, uint32_t flags, int64_t* sizes, int32_t* rows, int32_t* cols,
+                               uint8_t* width, uint8_t* cnt, uint8_t* pos, int32_t* units, int32_t* panel_units,
+                               int32_t* ustart, int32_t* longrows) {
+    using namespace tca;
+    if (!rowptr || !colidx || M < 0 || K < 1 || N < 1 || !dtype_ok(dtype) || !sizes)
+        return fail(TCA_ERR_INVALID, "tca_plan_panels: bad argument");
+    MfmaPlan mp;
+    const char* md = std::getenv("TCA_MFMA_MIN_DENSITY");
+    plan_mfma(rowptr, colidx, M, N, dtype, (flags & TCA_PLAN_FORCE_MFMA) != 0, (flags & TCA_PLAN_NO_MFMA) != 0,
+              md ? std::atof(md) : kMfmaMinDensity, mfma_shape(flags), &mp);
+    PanelPlan p;
+    plan_panels_routed(rowptr, colidx, M, K, N, dtype, flags, mp.row_mfma, &p);
+    const int64_t stride = static_cast<int64_t>(p.waves) * kPanelCntRows * 4;
+    const int64_t sz[16] = {p.n_panels, p.n_tiles(), static_cast<int64_t>(p.units.size()),
+                            static_cast<int64_t>(p.longrows.size()), p.R, p.P, p.waves, p.rpg, p.elems, p.chunks,
+                            p.nnz, p.staged, p.n_segments, p.n_rows, stride, 0};
+    std::copy(sz, sz + 16, sizes);
+    if (!rows) return TCA_OK;
+    if (!cols || !width || !cnt || !pos || !units || !panel_units || !ustart || !longrows)
+        return fail(TCA_ERR_INVALID, "tca_plan_panels: missing output array");
+    std::copy(p.rows.begin(), p.rows.end(), rows);
+    std::copy(p.cols.begin(), p.cols.end(), cols);
+    std::copy(p.width.begin(), p.width.end(), width);
+    std::copy(p.cnt.begin(), p.cnt.end(), cnt);
+    if (!p.pos.empty()) std::copy(p.pos.begin(), p.pos.begin() + rowptr[M], pos);
+    else std::fill(pos, pos + rowptr[M], 0);
+    for (size_t u = 0; u < p.units.size(); u++) {
+        units[4 * u] = p.units[u].x;
+        units[4 * u + 1] = p.units[u].y;
+        units[4 * u + 2] = p.units[u].z;
+        units[4 * u + 3] = p.units[u].w;
+    }
+    std::copy(p.panel_units.begin(), p.panel_units.end(), panel_units);
+    std::copy(p.ustart.begin(), p.ustart.end(), ustart);
+    for (size_t u = 0; u < p.longrows.size(); u++) {
+        longrows[4 * u] = p.longrows[u].x;
+        longrows[4 * u + 1] = p.longrows[u].y;
+        longrows[4 * u + 2] = p.longrows[u].z;
+        longrows[4 * u + 3] = p.longrows[u].w;
+    }
     return TCA_OK;
 }

@@ -146,6 +146,79 @@ void plan_geometry(int32_t N, int32_t es, int32_t slices, RowPlan* p);
 // multi_max) of the row kernel for a matrix of nnz nonzeros.
 void plan_row_params(int64_t nnz, int32_t N, int32_t es, int32_t slices, RowPlan* p);
 
+// Row panels with B rows staged in LDS (the panel kernel).  Rows are taken
+// longest first (ties by row id) in panels of R = waves * 4 * rpg rows; the
+// sorted union of a panel's columns is cut into tiles of at most P columns
+// in which no row holds more than kPanelMaxRun nonzeros, and a
+// workgroup stages one tile's B rows (all N columns of a column chunk) into
+// LDS while its consumer wavefronts multiply the previous tile: every row of
+// the panel reads the staged rows of its nonzeros instead of gathering them
+// from L2.  Since the CSR columns of a row are sorted and a tile is a range
+// of the sorted union, a row's nonzeros in one tile are a contiguous CSR run.
+//   slot s of panel p (s = (wave * rpg + i) * 4 + group): rows[p * R + s]
+//     (-1 = empty slot); lane group `group` of consumer wave `wave` owns it as
+//     its i-th row;
+//   tile t (global index): cols[t * P + j] = the B row staged at position j
+//     for j < width[t] (padding repeats a valid column; never read);
+//   cnt[t * waves * 16 * 4 + (wave * 16 + i) * 4 + group] (bytes): nonzeros
+//     of slot s's row in tile t (16 row entries per wave, rpg used);
+//   pos[k] for a CSR nonzero k of a panel row: its position in its tile;
+//   units[u] = {panel, first tile, tiles, segment base or -1}: one
+//     workgroup; a panel whose nonzeros exceed the unit size is split into
+//     panel_units[panel] units by tiles, each writing partial rows that are
+//     summed in unit order: unit k of a panel whose first segment is f has
+//     segment base f + k, and slot s writes segment base + s * panel_units;
+//   ustart[u * R + s] = CSR index of slot s's first nonzero in unit u;
+//   longrows: {row, first segment, segments, 0} for split panels' rows.
+// A panel is taken when its reuse nnz / |union| is at least min_reuse (or
+// always with force).  Eligible: N % (16 * E) == 0 for the lane geometry of
+// panel_geometry.
+struct PanelPlan {
+    int32_t waves = 0, rpg = 0, R = 0, P = 0;  // consumer waves, rows per lane group, rows per panel, tile columns
+    int32_t elems = 0, chunks = 0;             // B elements per lane, column chunks of C
+    int32_t n_panels = 0;
+    std::vector<int32_t> rows;
+    std::vector<int32_t> cols;
+    std::vector<uint8_t> width;  // [tile]: columns of the tile (1..P)
+    std::vector<uint8_t> cnt;
+    std::vector<uint8_t> pos;  // indexed by CSR nonzero (0 outside panels)
+    std::vector<Int4> units;
+    std::vector<int32_t> panel_units;
+    std::vector<int32_t> ustart;
+    std::vector<Int4> longrows;
+    int64_t n_segments = 0;    // partial rows of split panels
+    std::vector<uint8_t> row_panel;  // per row: in a panel
+    int64_t nnz = 0;           // nonzeros in panels
+    int64_t staged = 0;        // union columns summed over panels
+    int32_t n_rows = 0;        // rows in panels
+    int32_t n_tiles() const { return P ? static_cast<int32_t>(cols.size() / P) : 0; }
+};
+constexpr int kPanelWaves = 8;    // consumer wavefronts per workgroup (plus one producer)
+constexpr int kPanelRpg = 10;     // rows per 16-lane group
+constexpr int kPanelCntRows = 16; // count entries per wave and tile (rpg <= 16)
+constexpr int kPanelMaxRun = 16;  // nonzeros of one row in one tile (one 16-lane batch)
+constexpr double kPanelMinReuse = 2.0;
+constexpr int64_t kPanelMinNnz = int64_t(1) << 21;  // fewer nonzeros in panels: none (unless forced)
+// Lane geometry: 16 lanes cover one column chunk of a B row, E elements each
+// (E = 8, 4 or 2 with E * elem_size in 8..32 bytes); 0 when N does not fit.
+int32_t panel_elems(int32_t N, int32_t es);
+// Default routing also needs B rows of at least 256 bytes (N * elem_size).
+bool panel_default_ok(int32_t N, int32_t es);
+// Tile width P for a chunk of `chunk_bytes` bytes: two LDS buffers of at most
+// 64 KiB, positions fit one byte (P <= 255).
+int32_t panel_tile_cols(int32_t chunk_bytes);
+// plan_panels with the routing of a plan: none with TCA_PLAN_NO_PANELS, every
+// eligible row with TCA_PLAN_FORCE_PANELS, else (B rows of >= 256 bytes)
+// panels of reuse >= 2 when they hold at least kPanelMinNnz nonzeros in all.
+void plan_panels_routed(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_t K, int32_t N,
+                        int32_t dtype, uint32_t flags, const std::vector<uint8_t>& skip, PanelPlan* p);
+// Builds the panel plan over the rows with skip[r] == 0 (skip may be empty).
+// unit_nnz: nonzeros per workgroup unit (0 = automatic).
+// Unless forced, panels are kept only when they hold at least min_nnz nonzeros in all.
+void plan_panels(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_t K, int32_t N, int32_t es,
+                 const std::vector<uint8_t>& skip, bool force, double min_reuse, int64_t min_nnz, int64_t unit_nnz,
+                 PanelPlan* p);
+
 // Builds the row-kernel task list for rows with skip[r] == 0 (skip may be
 // empty).  Rows are assigned longest first.  The categories, in task order:
 // wide rows (row_len < length <= wide_len, 4 tasks each), long rows

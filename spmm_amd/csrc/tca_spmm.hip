@@ -20,6 +20,7 @@
 #include "sparse24_kernel.hpp"
 #include "device_planner.hpp"
 #include "mfma_sparse_kernel.hpp"
+#include "panel_kernel.hpp"
 
 #include <hipcub/hipcub.hpp>
 #include "sddmm_kernel.hpp"
@@ -79,6 +80,18 @@ struct tca_spmm_plan {
     int32_t n_perm = 0;       // rows in multi tasks (entries of d_perm)
     bool device_planned = false;
     float* d_partials = nullptr;
+    // row panels (panel kernel)
+    PanelPlan panels;
+    int32_t n_units = 0;
+    int4* d_units = nullptr;
+    int* d_panel_units = nullptr;
+    int* d_prows = nullptr;
+    int* d_pcols = nullptr;  // panel tiles' staged B rows, as byte offsets into B
+    uint8_t* d_pwidth = nullptr;
+    uint32_t* d_pcnt = nullptr;
+    uint8_t* d_ppos = nullptr;
+    int* d_ustart = nullptr;
+    size_t n_pos_bytes = 0;  // d_ppos, whole dwords
     tca_plan_info info{};
 };
 
@@ -120,6 +133,14 @@ void free_plan_device(tca_spmm_plan* p) {
     (void)hipFree(p->d_amask);
     (void)hipFree(p->d_dn_src);
     (void)hipFree(p->d_dn_pos);
+    (void)hipFree(p->d_units);
+    (void)hipFree(p->d_panel_units);
+    (void)hipFree(p->d_prows);
+    (void)hipFree(p->d_pcols);
+    (void)hipFree(p->d_pwidth);
+    (void)hipFree(p->d_pcnt);
+    (void)hipFree(p->d_ppos);
+    (void)hipFree(p->d_ustart);
 }
 
 template <typename T, int E>
@@ -183,6 +204,8 @@ void launch_pack(const tca_spmm_plan* p, const void* val, hipStream_t s) {
                        static_cast<const uint16_t*>(val), p->d_packed);
 }
 
+static_assert(kPnWaves == kPanelWaves && kPnRpg == kPanelRpg && kPnCntRows == kPanelCntRows, "panel plan layout");
+static_assert(PanelGeom<float, 8>::kP == 128 && PanelGeom<float, 4>::kP == 255, "panel tile widths (panel_tile_cols)");
 static_assert(kMfmaDmaShape.max_step_entries == kDmaMaxStepEntries, "planner and LDS-DMA kernel agree on step size");
 static_assert(kMfmaDmaShape.win_rows == kDmaWinRows && kMfmaDmaShape.tile_cols == kDmaTileCols, "LDS-DMA tile shape");
 static_assert(kMfmaDmaShape.max_step_entries <= 8 * kPairGroup, "paired kernel: at most 8 entry groups per step");
@@ -303,10 +326,57 @@ int launch_rows(const tca_spmm_plan* p, const void* val, const void* B, float* C
     }
 }
 
-// One SpMM in stream order: pack, tile kernel, row kernel, segment sums.
+template <typename T, int E>
+void launch_panels_t(const tca_spmm_plan* p, const void* val, const void* B, float* C, hipStream_t s) {
+    PanelArgs a;
+    a.units = p->d_units;
+    a.panel_units = p->d_panel_units;
+    a.rows = p->d_prows;
+    a.boff = reinterpret_cast<const uint32_t*>(p->d_pcols);
+    a.width = p->d_pwidth;
+    a.cnt = p->d_pcnt;
+    a.pos = p->d_ppos;
+    a.ustart = p->d_ustart;
+    a.val = val;
+    a.B = B;
+    a.C = C;
+    a.partials = p->d_partials;
+    a.N = p->N;
+    a.chunks = p->panels.chunks;
+    a.pos_bytes = static_cast<uint32_t>(p->n_pos_bytes);
+    a.val_bytes = static_cast<uint32_t>(static_cast<uint64_t>(p->nnz) * sizeof(T));
+    hipLaunchKernelGGL((panel_kernel<T, E>), dim3(p->n_units * p->panels.chunks), dim3(kPnThreads), 0, s, a);
+}
+
+int launch_panels(const tca_spmm_plan* p, const void* val, const void* B, float* C, hipStream_t s) {
+    if (p->n_units == 0) return TCA_OK;
+    const int e = p->panels.elems;
+    switch (p->dtype) {
+        case TCA_F32:
+            if (e == 8) launch_panels_t<float, 8>(p, val, B, C, s);
+            else if (e == 4) launch_panels_t<float, 4>(p, val, B, C, s);
+            else if (e == 2) launch_panels_t<float, 2>(p, val, B, C, s);
+            else return fail(TCA_ERR_INVALID, "bad panel geometry");
+            return TCA_OK;
+        case TCA_F16:
+            if (e == 8) launch_panels_t<_Float16, 8>(p, val, B, C, s);
+            else if (e == 4) launch_panels_t<_Float16, 4>(p, val, B, C, s);
+            else return fail(TCA_ERR_INVALID, "bad panel geometry");
+            return TCA_OK;
+        default:
+            if (e == 8) launch_panels_t<bf16_t, 8>(p, val, B, C, s);
+            else if (e == 4) launch_panels_t<bf16_t, 4>(p, val, B, C, s);
+            else return fail(TCA_ERR_INVALID, "bad panel geometry");
+            return TCA_OK;
+    }
+}
+
+// One SpMM in stream order: pack, tile kernel, panel kernel, row kernel, segment sums.
 int run_phases(const tca_spmm_plan* p, const void* val, const void* B, float* C, hipStream_t s) {
     launch_pack(p, val, s);
     int st = launch_mfma(p, B, C, s);
+    if (st) return st;
+    st = launch_panels(p, val, B, C, s);
     if (st) return st;
     st = launch_rows(p, val, B, C, s);
     if (st) return st;
@@ -356,6 +426,16 @@ void fill_info(tca_spmm_plan* p) {
     else
         in.mfma_lds_bytes = p->mfma_slots == 1 ? mfma_lds_bytes<1>() : p->mfma_slots == 2 ? mfma_lds_bytes<2>() : mfma_lds_bytes<4>();
     in.scratch_bytes = static_cast<int64_t>(p->n_seg_total * p->N * sizeof(float));
+    in.n_panels = p->panels.n_panels;
+    in.n_panel_units = p->n_units;
+    in.rows_panels = p->panels.n_rows;
+    in.panel_blocks = p->n_units * p->panels.chunks;
+    in.nnz_panels = p->panels.nnz;
+    in.staged_panels = p->panels.staged;
+    in.panel_blockdim = kPnThreads;
+    in.panel_lds_bytes = p->n_units ? panel_lds_bytes(16 * p->panels.elems * static_cast<int>(dtype_size(p->dtype))) +
+                                          16 * p->panels.elems * static_cast<int>(dtype_size(p->dtype))
+                                    : 0;
     in.tile_kernel = p->mfma.windows.empty() ? TCA_TILES_NONE
                      : p->mfma_sparse       ? TCA_TILES_SPARSE
                      : p->mfma_compact      ? TCA_TILES_COMPACT
@@ -385,6 +465,7 @@ void print_launches(const tca_spmm_plan* p) {
                                       "mfma_compact_kernel"};
         line(in.mfma_blocks, in.mfma_blockdim, in.mfma_lds_bytes, names[in.tile_kernel]);
     }
+    if (p->n_units > 0) line(in.panel_blocks, in.panel_blockdim, in.panel_lds_bytes, "panel_kernel");
     if (p->ntasks > 0)  // static LDS of row_kernel: kRowWaves partial row chunks of 64 lanes x E floats
         line(in.row_blocks, in.row_blockdim, 4.0 * kRowWaves * 64 * p->rows.elems_per_lane, "row_kernel");
     if (p->n_longrows > 0)
@@ -514,11 +595,30 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
         p->mfma_slots = most <= 256 ? 1 : most <= 512 ? 2 : 4;
         p->mfma_groups = most <= 4 * kPairGroup ? 4 : 8;
     }
-    plan_rows(rowptr, M, N, static_cast<int32_t>(dtype_size(dtype)), p->mfma.row_mfma, default_slices(K, N, dtype),
+    // Row panels with B staged in LDS for the rows outside MFMA windows, then
+    // the row kernel for the rest.
+    plan_panels_routed(rowptr, colidx, M, K, N, dtype, flags, p->mfma.row_mfma, &p->panels);
+    std::vector<uint8_t> skip_rows(M, 0);
+    for (int32_t r = 0; r < M; r++)
+        skip_rows[r] = (!p->mfma.row_mfma.empty() && p->mfma.row_mfma[r]) || p->panels.row_panel[r];
+    plan_rows(rowptr, M, N, static_cast<int32_t>(dtype_size(dtype)), skip_rows, default_slices(K, N, dtype),
               &p->rows);
     p->ntasks = static_cast<int32_t>(p->rows.tasks.size());
-    const size_t n_seg_total =
+    const size_t n_seg_rows =
         p->rows.longrows.empty() ? 0 : static_cast<size_t>(p->rows.longrows.back().y + p->rows.longrows.back().z);
+    // One partial-row array and one segment-sum table for both kernels: the
+    // panels' segments follow the row kernel's.
+    {
+        const int32_t off = static_cast<int32_t>(n_seg_rows);
+        for (Int4& u : p->panels.units)
+            if (u.w >= 0) u.w += off;
+        for (Int4 lr : p->panels.longrows) {
+            lr.y += off;
+            p->rows.longrows.push_back(lr);
+        }
+    }
+    const size_t n_seg_total = n_seg_rows + static_cast<size_t>(p->panels.n_segments);
+    p->n_units = static_cast<int32_t>(p->panels.units.size());
     p->n_longrows = static_cast<int32_t>(p->rows.longrows.size());
     p->n_seg_total = n_seg_total;
     p->n_perm = static_cast<int32_t>(p->rows.perm.size());
@@ -535,6 +635,30 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
     if ((st = dev_upload(&p->d_perm, p->rows.perm.data(), p->rows.perm.size()))) return bail(st);
     if ((st = dev_upload(&p->d_longrows, p->rows.longrows.data(), p->rows.longrows.size()))) return bail(st);
     if ((st = dev_upload(&p->d_partials, nullptr, n_seg_total * N))) return bail(st);
+    if (p->n_units > 0) {
+        const PanelPlan& pp = p->panels;
+        if ((st = dev_upload(&p->d_units, pp.units.data(), pp.units.size()))) return bail(st);
+        if ((st = dev_upload(&p->d_panel_units, pp.panel_units.data(), pp.panel_units.size()))) return bail(st);
+        if ((st = dev_upload(&p->d_prows, pp.rows.data(), pp.rows.size()))) return bail(st);
+        {
+            // staged rows as byte offsets into B (B < 4 GiB, checked above)
+            std::vector<int32_t> boff(pp.cols.size());
+            const uint32_t rb = static_cast<uint32_t>(N) * static_cast<uint32_t>(dtype_size(dtype));
+            for (size_t j = 0; j < boff.size(); j++) boff[j] = static_cast<int32_t>(static_cast<uint32_t>(pp.cols[j]) * rb);
+            if ((st = dev_upload(&p->d_pcols, boff.data(), boff.size()))) return bail(st);
+        }
+        if ((st = dev_upload(&p->d_pwidth, pp.width.data(), pp.width.size()))) return bail(st);
+        if ((st = dev_upload(&p->d_pcnt, pp.cnt.data(), pp.cnt.size() / 4))) return bail(st);
+        if ((st = dev_upload(&p->d_ppos, pp.pos.data(), pp.pos.size()))) return bail(st);
+        p->n_pos_bytes = pp.pos.size();
+        if ((st = dev_upload(&p->d_ustart, pp.ustart.data(), pp.ustart.size()))) return bail(st);
+        // the kernel needs only the arrays on the device
+        p->panels.cols.clear(); p->panels.cols.shrink_to_fit();
+        p->panels.width.clear(); p->panels.width.shrink_to_fit();
+        p->panels.cnt.clear(); p->panels.cnt.shrink_to_fit();
+        p->panels.pos.clear(); p->panels.pos.shrink_to_fit();
+        p->panels.ustart.clear(); p->panels.ustart.shrink_to_fit();
+    }
     if ((st = dev_upload(&p->d_windows, p->mfma.windows.data(), p->mfma.windows.size()))) return bail(st);
     if (!p->mfma.windows.empty()) {
         // Device forms: B row byte offsets (padding 0xffffffff); per entry its
@@ -1299,7 +1423,7 @@ int tca_spmm_time_phases(const tca_spmm_plan* p, const void* d_val, const void* 
     int st = TCA_OK;
     const bool used[TCA_PHASES] = {!p->mfma.windows.empty() && (!p->mfma.entries.empty() || p->n_dn > 0),
                                    !p->mfma.windows.empty(),
-                                   p->ntasks > 0, p->n_longrows > 0};
+                                   p->ntasks > 0, p->n_longrows > 0, p->n_units > 0};
     for (int k = 0; k < TCA_PHASES && st == TCA_OK; k++) {
         if (!used[k]) continue;
         (void)hipEventRecord(e0, s);
@@ -1308,6 +1432,7 @@ int tca_spmm_time_phases(const tca_spmm_plan* p, const void* d_val, const void* 
                 case TCA_PHASE_PACK: launch_pack(p, d_val, s); break;
                 case TCA_PHASE_TILES: st = launch_mfma(p, d_B, d_C, s); break;
                 case TCA_PHASE_ROWS: st = launch_rows(p, d_val, d_B, d_C, s); break;
+                case TCA_PHASE_PANELS: st = launch_panels(p, d_val, d_B, d_C, s); break;
                 default: launch_finalize(p, d_C, s); break;
             }
         }

@@ -31,7 +31,7 @@ def test_device_plan_equals_host_plan(torch_cuda, name, a, n):
     torch = torch_cuda
     print(f"device plan {name}: M={a.nrow} K={a.ncol} nnz={a.nnz} N={n}", flush=True)
     drp, dci = _dev(torch, a.rowptr), _dev(torch, a.colidx)
-    with S.Plan(a, n, S.TCA_PLAN_NO_MFMA) as hp:
+    with S.Plan(a, n, S.TCA_PLAN_NO_MFMA | S.TCA_PLAN_NO_PANELS) as hp:
         dp = S.Plan.from_device(drp, dci, a.nrow, a.ncol, a.nnz, n, a.dtype, S.TCA_PLAN_NO_MFMA)
         try:
             ht, hperm, hl = hp.export_rows()
@@ -96,7 +96,7 @@ def test_device_mfma_plan_equals_host_plan(torch_cuda, name, a, n, flags):
     v = rng.choice(np.array([-2.0, -1.0, -0.5, 0.5, 1.0, 2.0], np.float32), size=a.nnz)
     a = S.CSR(a.nrow, a.ncol, a.rowptr, a.colidx, S.to_storage(v, a.dtype), a.dtype)
     b = S.to_storage(exact_dense(rng, (a.ncol, n)), a.dtype)
-    with S.Plan(a, n, flags) as hp:
+    with S.Plan(a, n, flags | S.TCA_PLAN_NO_PANELS) as hp:
         dp = S.Plan.from_device(_dev(torch, a.rowptr), _dev(torch, a.colidx), a.nrow, a.ncol, a.nnz, n, a.dtype, flags)
         try:
             hi, di = hp.info(), dp.info()

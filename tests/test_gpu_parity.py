@@ -232,7 +232,7 @@ def test_exact_long_rows_many_segments(torch_cuda):
     info = None
     for n in (64, 256, 512):
         b = S.to_storage(exact_dense(rng, (k, n)), S.TCA_F16)
-        with S.Plan(a, n, S.TCA_PLAN_NO_MFMA) as p:  # the segment path of the row kernel
+        with S.Plan(a, n, S.TCA_PLAN_NO_MFMA | S.TCA_PLAN_NO_PANELS) as p:  # the segment path of the row kernel
             info = p.info()
             got = run_gpu(torch_cuda, a, b, plan=p)
         assert info["n_long_rows"] >= 4
@@ -247,7 +247,7 @@ def test_exact_segments_ragged_widths(torch_cuda, n):
     k = 12000
     a = make_csr(rng, [11000, 7, 9000, 0, 11999], k, S.TCA_F32)
     b = S.to_storage(exact_dense(rng, (k, n)), S.TCA_F32)
-    with S.Plan(a, n, S.TCA_PLAN_NO_MFMA) as p:
+    with S.Plan(a, n, S.TCA_PLAN_NO_MFMA | S.TCA_PLAN_NO_PANELS) as p:
         info = p.info()
         got = run_gpu(torch_cuda, a, b, plan=p)
     assert info["n_long_rows"] >= 3, info
@@ -333,7 +333,8 @@ def test_config_full_size_small(torch_cuda, cfg):
     assert_close(oracle_c(a, b), got, f"config {cfg} vs fp32 oracle")
     assert_parity(a, b, got, f"config {cfg}")
     # both kernels on the whole matrix
-    for flags, what in ((S.TCA_PLAN_NO_MFMA, "row kernel only"), (S.TCA_PLAN_FORCE_MFMA, "MFMA tiles only")):
+    for flags, what in ((S.TCA_PLAN_NO_MFMA | S.TCA_PLAN_NO_PANELS, "row kernel only"),
+                        (S.TCA_PLAN_FORCE_MFMA, "MFMA tiles only")):
         with S.Plan(a, n, flags) as pl:
             info = pl.info()
             got_k = run_gpu(torch_cuda, a, b, plan=pl)
@@ -372,10 +373,13 @@ def test_phase_timing_reports_the_kernels_a_plan_uses(torch_cuda):
     bd = torch.from_numpy(b.view(np.int16)).to(dev)
     for flags, used in ((S.TCA_PLAN_FORCE_MFMA, {"pack", "tiles"}),
                         (S.TCA_PLAN_FORCE_MFMA | S.TCA_PLAN_MFMA_PAIR, {"pack", "tiles"}),
-                        (S.TCA_PLAN_NO_MFMA, {"rows"})):
+                        (S.TCA_PLAN_NO_MFMA | S.TCA_PLAN_NO_PANELS, {"rows"}),
+                        (S.TCA_PLAN_NO_MFMA | S.TCA_PLAN_FORCE_PANELS, {"panels"})):
         c = torch.zeros((a.nrow, 256), dtype=torch.float32, device=dev)
         with S.Plan(a, 256, flags) as pl:
             ph = pl.time_phases(val, bd, c, warmup=1, iters=3)
+            if pl.info()["n_long_rows"] > 0:  # rows split over several units or segments
+                used = used | {"segments"}
         torch.cuda.synchronize()
         assert {k for k, v in ph.items() if v > 0} == used, (flags, ph)
         assert np.array_equal(c.cpu().numpy(), oracle_c(a, b))
