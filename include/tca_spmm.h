@@ -69,6 +69,7 @@ typedef enum tca_status {
  * rows of at least 256 bytes and at least 2^21 nonzeros in panels. */
 #define TCA_PLAN_NO_PANELS 256u    /* no panels: rows outside MFMA windows go to the row kernel */
 #define TCA_PLAN_FORCE_PANELS 512u /* every eligible row in panels, whatever their reuse */
+#define TCA_PLAN_NO_SCRATCH 1024u  /* the plan keeps no partial-row scratch: run it with tca_spmm_run_static */
 
 typedef struct tca_spmm_plan tca_spmm_plan;
 
@@ -138,6 +139,20 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
  * streams at once: long-row partial sums live in plan-owned scratch. */
 int tca_spmm_run(const tca_spmm_plan* plan, const void* d_val, const void* d_B, float* d_C,
                  void* stream);
+
+/* Allocation-free variant of tca_spmm_run, for callers that cannot allocate
+ * device memory while they run (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc); no counterpart in the reference.
+ * The kernels are tca_spmm_run's; the partial rows of split rows (row-kernel
+ * segments, units of split panels) go to a file-scope device array of
+ * 64 MiB per GPU instead of plan-owned memory, so the plan may be created
+ * with TCA_PLAN_NO_SCRATCH.  Calls no hipMalloc or hipFree.  Plans whose
+ * partial rows exceed 64 MiB are rejected (TCA_ERR_UNSUPPORTED); the
+ * current device must be the plan's.  Every call on one GPU shares that
+ * GPU's array (each partial row is written before it is read, nothing needs
+ * clearing): calls that overlap on one GPU, on any streams, race. */
+int tca_spmm_run_static(const tca_spmm_plan* plan, const void* d_val, const void* d_B, float* d_C,
+                        void* stream);
 
 /* Times tca_spmm_run the way our_spmm_balanced does (src/our_spmm.cu:553-576):
  * `warmup` untimed launches, then `iters` launches between two hipEvents

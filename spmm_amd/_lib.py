@@ -24,6 +24,7 @@ TCA_PLAN_MFMA_PAIR = 64
 TCA_PLAN_MFMA_COMPACT = 128
 TCA_PLAN_NO_PANELS = 256
 TCA_PLAN_FORCE_PANELS = 512
+TCA_PLAN_NO_SCRATCH = 1024
 # tile kernel of a plan (tca_plan_info.tile_kernel)
 TCA_TILES_NONE, TCA_TILES_REGS, TCA_TILES_DMA, TCA_TILES_PAIR = 0, 1, 2, 3
 TCA_TILES_DENSE, TCA_TILES_DENSE_K, TCA_TILES_SPARSE, TCA_TILES_COMPACT = 4, 5, 6, 7
@@ -85,6 +86,7 @@ SIGNATURES = {
     "tca_spmm_run": (i32, [vp, vp, vp, vp, vp]),
     "tca_spmm_time": (i32, [vp, vp, vp, vp, vp, i32, i32, f32p]),
     "tca_spmm_time_phases": (i32, [vp, vp, vp, vp, vp, i32, i32, f32p]),
+    "tca_spmm_run_static": (i32, [vp, vp, vp, vp, vp]),
     "tca_sddmm": (i32, [vp, vp, vp, vp, vp]),
     "tca_launch_floor": (i32, [vp, i32, f32p]),
     "tca_gather_values": (i32, [vp, i32, vp, i32, vp, vp]),

@@ -6,6 +6,7 @@
 #include <chrono>
 #include <cstdio>
 #include <cstdlib>
+#include <mutex>
 #include <vector>
 
 #include "common.hpp"
@@ -95,7 +96,33 @@ struct tca_spmm_plan {
     tca_plan_info info{};
 };
 
+// The allocation-free run's partial rows (tca_spmm_run_static): one
+// file-scope device array per GPU, held until the process ends.  Its
+// host-side name is not a device address: host code uses only the address
+// hipGetSymbolAddress returns for the current device (kept per device).
+constexpr size_t kStaticScratchBytes = size_t(64) << 20;
+static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
 namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// This device's copy of `scratch` (looked up once per device, with that
+// device current).
+int static_scratch(int dev, float** out) {
+    if (dev < 0 || dev >= kMaxDevices) return fail(TCA_ERR_UNSUPPORTED, "device %d: too many devices", dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr) return fail(TCA_ERR_HIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+        g_scratch_ptr[dev] = ptr;
+    }
+    *out = static_cast<float*>(g_scratch_ptr[dev]);
+    return TCA_OK;
+}
 
 __global__ void warm_up_kernel() {}
 
@@ -144,13 +171,13 @@ void free_plan_device(tca_spmm_plan* p) {
 }
 
 template <typename T, int E>
-void launch_rows_t(const tca_spmm_plan* p, const void* val, const void* B, float* C, hipStream_t s) {
+void launch_rows_t(const tca_spmm_plan* p, const void* val, const void* B, float* C, float* W, hipStream_t s) {
     RowArgs a;
     a.tasks = p->d_tasks;
     a.ntasks = p->ntasks;
     a.rowptr = p->d_rowptr;
     a.perm = p->d_perm;
-    a.partials = p->d_partials;
+    a.partials = W;
     a.C = C;
     a.N = p->N;
     a.logG = p->rows.log_lanes;
@@ -168,21 +195,21 @@ void launch_rows_t(const tca_spmm_plan* p, const void* val, const void* B, float
 }
 
 // Adds the segments of long rows (after the row kernel, same stream).
-void launch_finalize(const tca_spmm_plan* p, float* C, hipStream_t s) {
+void launch_finalize(const tca_spmm_plan* p, float* C, const float* W, hipStream_t s) {
     if (p->n_longrows == 0) return;
     const dim3 fgrid(static_cast<unsigned>(p->n_longrows), (p->N + 255) / 256);
-    hipLaunchKernelGGL(seg_finalize_kernel, fgrid, dim3(64), 0, s, p->d_longrows, p->d_partials, C, p->N);
+    hipLaunchKernelGGL(seg_finalize_kernel, fgrid, dim3(64), 0, s, p->d_longrows, W, C, p->N);
 }
 
 template <typename T>
-int launch_rows_e(const tca_spmm_plan* p, const void* val, const void* B, float* C, hipStream_t s) {
+int launch_rows_e(const tca_spmm_plan* p, const void* val, const void* B, float* C, float* W, hipStream_t s) {
     switch (p->rows.elems_per_lane) {
-        case 1: launch_rows_t<T, 1>(p, val, B, C, s); return TCA_OK;
-        case 2: launch_rows_t<T, 2>(p, val, B, C, s); return TCA_OK;
-        case 4: launch_rows_t<T, 4>(p, val, B, C, s); return TCA_OK;
+        case 1: launch_rows_t<T, 1>(p, val, B, C, W, s); return TCA_OK;
+        case 2: launch_rows_t<T, 2>(p, val, B, C, W, s); return TCA_OK;
+        case 4: launch_rows_t<T, 4>(p, val, B, C, W, s); return TCA_OK;
         case 8:
             if constexpr (sizeof(T) == 2) {
-                launch_rows_t<T, 8>(p, val, B, C, s);
+                launch_rows_t<T, 8>(p, val, B, C, W, s);
                 return TCA_OK;
             }
             [[fallthrough]];
@@ -317,17 +344,17 @@ int launch_mfma(const tca_spmm_plan* p, const void* B, float* C, hipStream_t s) 
     }
 }
 
-int launch_rows(const tca_spmm_plan* p, const void* val, const void* B, float* C, hipStream_t s) {
+int launch_rows(const tca_spmm_plan* p, const void* val, const void* B, float* C, float* W, hipStream_t s) {
     if (p->ntasks == 0) return TCA_OK;
     switch (p->dtype) {
-        case TCA_F16: return launch_rows_e<_Float16>(p, val, B, C, s);
-        case TCA_BF16: return launch_rows_e<bf16_t>(p, val, B, C, s);
-        default: return launch_rows_e<float>(p, val, B, C, s);
+        case TCA_F16: return launch_rows_e<_Float16>(p, val, B, C, W, s);
+        case TCA_BF16: return launch_rows_e<bf16_t>(p, val, B, C, W, s);
+        default: return launch_rows_e<float>(p, val, B, C, W, s);
     }
 }
 
 template <typename T, int E>
-void launch_panels_t(const tca_spmm_plan* p, const void* val, const void* B, float* C, hipStream_t s) {
+void launch_panels_t(const tca_spmm_plan* p, const void* val, const void* B, float* C, float* W, hipStream_t s) {
     PanelArgs a;
     a.units = p->d_units;
     a.panel_units = p->d_panel_units;
@@ -340,7 +367,7 @@ void launch_panels_t(const tca_spmm_plan* p, const void* val, const void* B, flo
     a.val = val;
     a.B = B;
     a.C = C;
-    a.partials = p->d_partials;
+    a.partials = W;
     a.N = p->N;
     a.chunks = p->panels.chunks;
     a.pos_bytes = static_cast<uint32_t>(p->n_pos_bytes);
@@ -348,39 +375,40 @@ void launch_panels_t(const tca_spmm_plan* p, const void* val, const void* B, flo
     hipLaunchKernelGGL((panel_kernel<T, E>), dim3(p->n_units * p->panels.chunks), dim3(kPnThreads), 0, s, a);
 }
 
-int launch_panels(const tca_spmm_plan* p, const void* val, const void* B, float* C, hipStream_t s) {
+int launch_panels(const tca_spmm_plan* p, const void* val, const void* B, float* C, float* W, hipStream_t s) {
     if (p->n_units == 0) return TCA_OK;
     const int e = p->panels.elems;
     switch (p->dtype) {
         case TCA_F32:
-            if (e == 8) launch_panels_t<float, 8>(p, val, B, C, s);
-            else if (e == 4) launch_panels_t<float, 4>(p, val, B, C, s);
-            else if (e == 2) launch_panels_t<float, 2>(p, val, B, C, s);
+            if (e == 8) launch_panels_t<float, 8>(p, val, B, C, W, s);
+            else if (e == 4) launch_panels_t<float, 4>(p, val, B, C, W, s);
+            else if (e == 2) launch_panels_t<float, 2>(p, val, B, C, W, s);
             else return fail(TCA_ERR_INVALID, "bad panel geometry");
             return TCA_OK;
         case TCA_F16:
-            if (e == 8) launch_panels_t<_Float16, 8>(p, val, B, C, s);
-            else if (e == 4) launch_panels_t<_Float16, 4>(p, val, B, C, s);
+            if (e == 8) launch_panels_t<_Float16, 8>(p, val, B, C, W, s);
+            else if (e == 4) launch_panels_t<_Float16, 4>(p, val, B, C, W, s);
             else return fail(TCA_ERR_INVALID, "bad panel geometry");
             return TCA_OK;
         default:
-            if (e == 8) launch_panels_t<bf16_t, 8>(p, val, B, C, s);
-            else if (e == 4) launch_panels_t<bf16_t, 4>(p, val, B, C, s);
+            if (e == 8) launch_panels_t<bf16_t, 8>(p, val, B, C, W, s);
+            else if (e == 4) launch_panels_t<bf16_t, 4>(p, val, B, C, W, s);
             else return fail(TCA_ERR_INVALID, "bad panel geometry");
             return TCA_OK;
     }
 }
 
 // One SpMM in stream order: pack, tile kernel, panel kernel, row kernel, segment sums.
-int run_phases(const tca_spmm_plan* p, const void* val, const void* B, float* C, hipStream_t s) {
+// W: the partial rows of split rows (plan-owned, or the static scratch).
+int run_phases(const tca_spmm_plan* p, const void* val, const void* B, float* C, float* W, hipStream_t s) {
     launch_pack(p, val, s);
     int st = launch_mfma(p, B, C, s);
     if (st) return st;
-    st = launch_panels(p, val, B, C, s);
+    st = launch_panels(p, val, B, C, W, s);
     if (st) return st;
-    st = launch_rows(p, val, B, C, s);
+    st = launch_rows(p, val, B, C, W, s);
     if (st) return st;
-    launch_finalize(p, C, s);
+    launch_finalize(p, C, W, s);
     return TCA_OK;
 }
 
@@ -634,7 +662,7 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
     if ((st = dev_upload(&p->d_tasks, p->rows.tasks.data(), p->rows.tasks.size()))) return bail(st);
     if ((st = dev_upload(&p->d_perm, p->rows.perm.data(), p->rows.perm.size()))) return bail(st);
     if ((st = dev_upload(&p->d_longrows, p->rows.longrows.data(), p->rows.longrows.size()))) return bail(st);
-    if ((st = dev_upload(&p->d_partials, nullptr, n_seg_total * N))) return bail(st);
+    if (!(flags & TCA_PLAN_NO_SCRATCH) && (st = dev_upload(&p->d_partials, nullptr, n_seg_total * N))) return bail(st);
     if (p->n_units > 0) {
         const PanelPlan& pp = p->panels;
         if ((st = dev_upload(&p->d_units, pp.units.data(), pp.units.size()))) return bail(st);
@@ -1147,7 +1175,7 @@ int tca_spmm_plan_create_device(const int32_t* d_rowptr, const int32_t* d_colidx
     p->n_perm = n_short;
     if ((st = dev_upload(&p->d_tasks, nullptr, p->ntasks)) || (st = dev_upload(&p->d_perm, nullptr, n_short)) ||
         (st = dev_upload(&p->d_longrows, nullptr, n_long)) ||
-        (st = dev_upload(&p->d_partials, nullptr, p->n_seg_total * N)))
+        (!(flags & TCA_PLAN_NO_SCRATCH) && (st = dev_upload(&p->d_partials, nullptr, p->n_seg_total * N))))
         return bail(st);
     if (Mp > 0) {
         DpEmitArgs ea;
@@ -1238,8 +1266,42 @@ int tca_spmm_run(const tca_spmm_plan* p, const void* d_val, const void* d_B, flo
     if (reinterpret_cast<uintptr_t>(d_C) % 16 != 0) return fail(TCA_ERR_INVALID, "C must be aligned to 16 bytes");
     if (reinterpret_cast<uintptr_t>(d_val) % dtype_size(p->dtype) != 0)
         return fail(TCA_ERR_INVALID, "values misaligned");
+    if (p->n_seg_total > 0 && !p->d_partials)
+        return fail(TCA_ERR_INVALID, "plan was created with TCA_PLAN_NO_SCRATCH: run it with tca_spmm_run_static");
     hipStream_t s = static_cast<hipStream_t>(stream);
-    const int st = run_phases(p, d_val, d_B, d_C, s);
+    const int st = run_phases(p, d_val, d_B, d_C, p->d_partials, s);
+    if (st) return st;
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(TCA_ERR_HIP, "kernel launch: %s", hipGetErrorString(e));
+    return TCA_OK;
+}
+
+int tca_spmm_run_static(const tca_spmm_plan* p, const void* d_val, const void* d_B, float* d_C, void* stream) {
+    if (!p) return fail(TCA_ERR_INVALID, "plan is NULL");
+    if (p->M == 0) return TCA_OK;
+    if ((p->nnz > 0 && (!d_val || !d_B)) || !d_C) return fail(TCA_ERR_INVALID, "NULL device pointer");
+    const size_t vb = static_cast<size_t>(p->rows.elems_per_lane) * dtype_size(p->dtype);
+    if (reinterpret_cast<uintptr_t>(d_B) % vb != 0)
+        return fail(TCA_ERR_INVALID, "B must be aligned to %zu bytes", vb);
+    if (reinterpret_cast<uintptr_t>(d_C) % 16 != 0) return fail(TCA_ERR_INVALID, "C must be aligned to 16 bytes");
+    if (reinterpret_cast<uintptr_t>(d_val) % dtype_size(p->dtype) != 0)
+        return fail(TCA_ERR_INVALID, "values misaligned");
+    const size_t need = p->n_seg_total * static_cast<size_t>(p->N) * sizeof(float);
+    if (need > kStaticScratchBytes)
+        return fail(TCA_ERR_UNSUPPORTED,
+                    "tca_spmm_run_static: the plan's partial rows need %zu bytes, the static scratch holds %zu",
+                    need, static_cast<size_t>(kStaticScratchBytes));
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess) return fail(TCA_ERR_HIP, "hipGetDevice failed");
+    if (dev != p->device)
+        return fail(TCA_ERR_INVALID, "tca_spmm_run_static: current device %d, plan built on device %d", dev, p->device);
+    float* w = nullptr;
+    if (need > 0) {
+        const int st = static_scratch(dev, &w);
+        if (st) return st;
+    }
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int st = run_phases(p, d_val, d_B, d_C, w, s);
     if (st) return st;
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(TCA_ERR_HIP, "kernel launch: %s", hipGetErrorString(e));
@@ -1431,9 +1493,9 @@ int tca_spmm_time_phases(const tca_spmm_plan* p, const void* d_val, const void* 
             switch (k) {
                 case TCA_PHASE_PACK: launch_pack(p, d_val, s); break;
                 case TCA_PHASE_TILES: st = launch_mfma(p, d_B, d_C, s); break;
-                case TCA_PHASE_ROWS: st = launch_rows(p, d_val, d_B, d_C, s); break;
-                case TCA_PHASE_PANELS: st = launch_panels(p, d_val, d_B, d_C, s); break;
-                default: launch_finalize(p, d_C, s); break;
+                case TCA_PHASE_ROWS: st = launch_rows(p, d_val, d_B, d_C, p->d_partials, s); break;
+                case TCA_PHASE_PANELS: st = launch_panels(p, d_val, d_B, d_C, p->d_partials, s); break;
+                default: launch_finalize(p, d_C, p->d_partials, s); break;
             }
         }
         (void)hipEventRecord(e1, s);
