@@ -211,8 +211,7 @@ __global__ __launch_bounds__(kPnThreads, 1) void panel_kernel(PanelArgs a) {
         const int sub = lane / (G::kRowBytes / 16);  // row within one 1 KiB transfer
         constexpr int kRowsPerInstr = 1024 / G::kRowBytes;
         // B rows of this column chunk, addressed by 32-bit offsets from one
-        // scalar base (the offsets of a tile's rows come through scalar loads)
-        // The transfer's base, held in SGPRs.  readfirstlane returns a signed
+        // scalar base held in SGPRs.  readfirstlane returns a signed
         // int: each half goes through uint32_t before widening, so a low half
         // with bit 31 set is not sign-extended into the high half.
         const uint64_t bb = reinterpret_cast<uint64_t>(a.B) + static_cast<uint64_t>(chunk) * G::kRowBytes;
@@ -220,49 +219,67 @@ __global__ __launch_bounds__(kPnThreads, 1) void panel_kernel(PanelArgs a) {
         const uint32_t bb_lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(bb)));
         const char* bbase = reinterpret_cast<const char*>((static_cast<uint64_t>(bb_hi) << 32) | bb_lo);
         const uint32_t lds0 = pn_lds_addr(smem);
-        using CU32P = const __attribute__((address_space(4))) uint32_t;
-        using CU8P = const __attribute__((address_space(4))) uint8_t;
-        constexpr int kBatch = 16 / kRowsPerInstr;  // transfers per 16 scalar-loaded offsets
-        auto stage = [&](int tile, int buf) {
-            CU32P* bo = (CU32P*)(reinterpret_cast<uintptr_t>(a.boff)) + static_cast<size_t>(tile) * G::kP;
-            const int ninstr = (((CU8P*)(reinterpret_cast<uintptr_t>(a.width)))[tile] * G::kRowBytes + 1023) / 1024;
-            // 16 offsets at a time by scalar loads (readfirstlane keeps them
-            // uniform values, so the selects pick values, not addresses), the
-            // next 16 loaded before this batch's transfers are issued;
-            // positions past P clamp to P - 1 (never staged)
-            auto load16 = [&](int kb, uint32_t (&o)[16]) {
+        // A tile's P offsets come through coalesced vector loads, lane l
+        // holding position j * 64 + l in o[j]; each transfer takes its rows'
+        // offsets by readlane.  The offsets (and width) of tile t + 2 load
+        // while tile t + 1's transfers are in flight, so one wait per tile
+        // covers both.  Positions past P clamp to P - 1 (never staged).
+        constexpr int kOffRegs = (G::kP + 63) / 64;
+        auto load_offs = [&](int tile, uint32_t (&o)[kOffRegs]) {
+            const uint32_t* bo = a.boff + static_cast<size_t>(tile) * G::kP;
 #pragma unroll
-                for (int j = 0; j < 16; j++) {
-                    const int r = kb * kRowsPerInstr + j;
-                    o[j] = __builtin_amdgcn_readfirstlane(bo[r < G::kP ? r : G::kP - 1]);
-                }
-            };
-            uint32_t o[16], on[16];
-            load16(0, o);
-#pragma unroll
-            for (int kb = 0; kb < G::kInstrs; kb += kBatch) {
-                if (kb >= ninstr) break;
-                if (kb + kBatch < G::kInstrs) load16(kb + kBatch, on);
-#pragma unroll
-                for (int k = kb; k < kb + kBatch; k++) {
-                    if (k < ninstr) {
-                        uint32_t off = o[(k - kb) * kRowsPerInstr];
-#pragma unroll
-                        for (int j = 1; j < kRowsPerInstr; j++) off = sub == j ? o[(k - kb) * kRowsPerInstr + j] : off;
-                        pn_dma(bbase, off + 16 * piece, lds0 + buf * G::kBufBytes + k * 1024);
-                    }
-                }
-#pragma unroll
-                for (int j = 0; j < 16; j++) o[j] = on[j];
+            for (int j = 0; j < kOffRegs; j++) {
+                const int r = j * 64 + lane;
+                o[j] = bo[r < G::kP ? r : G::kP - 1];
             }
         };
-        stage(u.y, 0);
-        pn_wait_all();
+        auto n_instr = [&](int tile) { return (a.width[tile] * G::kRowBytes + 1023) / 1024; };
+        auto stage = [&](const uint32_t (&o)[kOffRegs], int ninstr, int buf) {
+#pragma unroll
+            for (int k = 0; k < G::kInstrs; k++) {
+                if (k < ninstr) {
+                    const int r0 = k * kRowsPerInstr;
+                    uint32_t off = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(o[r0 / 64]), r0 % 64));
+#pragma unroll
+                    for (int j = 1; j < kRowsPerInstr; j++) {
+                        const uint32_t oj = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(o[r0 / 64]), r0 % 64 + j));
+                        off = sub == j ? oj : off;
+                    }
+                    pn_dma(bbase, off + 16 * piece, lds0 + buf * G::kBufBytes + k * 1024);
+                }
+            }
+        };
+        // The compiler cannot see the transfers (inline asm), so it would
+        // wait on the offset loads with vmcnt counts that then also wait for
+        // the transfers issued before each readlane.  Passing the offsets
+        // through an empty asm after the explicit wait ends their load
+        // dependence there, where nothing else is in flight.
+        uint32_t o[kOffRegs];
+        auto settle = [&](int& nin) {
+            pn_wait_all();
+#pragma unroll
+            for (int j = 0; j < kOffRegs; j++) asm volatile("" : "+v"(o[j]));
+            nin = __builtin_amdgcn_readfirstlane(nin);
+            asm volatile("" : "+s"(nin));
+        };
+        int nin = n_instr(u.y);
+        load_offs(u.y, o);
+        settle(nin);
+        stage(o, nin, 0);
+        if (u.z > 1) {
+            nin = n_instr(u.y + 1);
+            load_offs(u.y + 1, o);
+        }
+        settle(nin);
         for (int t = 0; t < u.z; t++) {
             __syncthreads();
             if (t + 1 < u.z) {
-                stage(u.y + t + 1, (t + 1) & 1);
-                pn_wait_all();
+                stage(o, nin, (t + 1) & 1);
+                if (t + 2 < u.z) {
+                    nin = n_instr(u.y + t + 2);
+                    load_offs(u.y + t + 2, o);
+                }
+                settle(nin);
             }
         }
         return;
