@@ -49,15 +49,12 @@ typedef enum tca_status {
 /* Plan flags. */
 #define TCA_PLAN_DEFAULT 0u
 #define TCA_PLAN_NO_MFMA 1u    /* route every row to the wavefront-per-row kernel */
-#define TCA_PLAN_FORCE_MFMA 2u /* route every eligible 64-row window to the MFMA tile kernel (fp16/bf16, N % 8 == 0) */
-#define TCA_PLAN_MFMA_REGS 4u  /* register-staged 64 x 128 tile kernel instead of the default one */
-#define TCA_PLAN_MFMA_DMA 8u   /* LDS-DMA 128 x 64 tile kernel instead of the default one */
+#define TCA_PLAN_FORCE_MFMA 2u /* route every eligible 128-row window to the MFMA tile kernel (fp16/bf16, N % 8 == 0) */
 #define TCA_PLAN_MFMA_DENSE 16u /* dense-tile 128 x 64 kernel (plan keeps dense condensed windows) */
 /* Default tile kernel: dense tiles spanning all of K when the routed windows'
  * column unions cover on average >= 85 % of K (B rows then need no gather
  * table), compacted (TCA_TILES_COMPACT) when no step has more than 255
  * non-empty fragment cells, else the paired kernel. */
-#define TCA_PLAN_MFMA_SPARSE 32u /* 2:4-grouped windows on the sparse matrix cores (v_smfmac) */
 #define TCA_PLAN_MFMA_PAIR 64u  /* paired (MFMA + staging wavefront) 128 x 64 kernel, whatever the windows */
 #define TCA_PLAN_MFMA_COMPACT 128u /* dense-tile kernel on compacted steps (only the non-empty 16-byte
                                       fragment cells, at most 255 per step; else plain dense tiles) */
@@ -70,6 +67,11 @@ typedef enum tca_status {
 #define TCA_PLAN_NO_PANELS 256u    /* no panels: rows outside MFMA windows go to the row kernel */
 #define TCA_PLAN_FORCE_PANELS 512u /* every eligible row in panels, whatever their reuse */
 #define TCA_PLAN_NO_SCRATCH 1024u  /* the plan keeps no partial-row scratch: run it with tca_spmm_run_static */
+/* Every flag a plan accepts; other bits (4, 8 and 32 among them, once tile
+ * kernel selectors) give TCA_ERR_INVALID. */
+#define TCA_PLAN_KNOWN_FLAGS                                                                            \
+    (TCA_PLAN_NO_MFMA | TCA_PLAN_FORCE_MFMA | TCA_PLAN_MFMA_DENSE | TCA_PLAN_MFMA_PAIR |                \
+     TCA_PLAN_MFMA_COMPACT | TCA_PLAN_NO_PANELS | TCA_PLAN_FORCE_PANELS | TCA_PLAN_NO_SCRATCH)
 
 typedef struct tca_spmm_plan tca_spmm_plan;
 
@@ -84,7 +86,7 @@ typedef struct tca_plan_info {
     int32_t n_multi_tasks;    /* of which: several short rows per wavefront */
     int32_t n_seg_tasks;      /* of which: segments of split long rows */
     int32_t n_long_rows;      /* rows split across wavefronts */
-    int32_t n_windows_mfma;   /* 16-row windows routed to the MFMA tile kernel */
+    int32_t n_windows_mfma;   /* 128-row windows routed to the MFMA tile kernel */
     int32_t rows_mfma;        /* rows covered by those windows */
     int64_t nnz_mfma;         /* nonzeros covered by those windows */
     int64_t cond_cols_mfma;   /* sum over MFMA windows of the padded condensed width */
@@ -112,13 +114,10 @@ typedef struct tca_plan_info {
 } tca_plan_info;
 
 /* tca_plan_info.tile_kernel */
-#define TCA_TILES_NONE 0       /* no window routed to the matrix cores */
-#define TCA_TILES_REGS 1       /* register-staged 64 x 128 tiles (TCA_PLAN_MFMA_REGS) */
-#define TCA_TILES_DMA 2        /* LDS-DMA 128 x 64 tiles (TCA_PLAN_MFMA_DMA) */
+#define TCA_TILES_NONE 0       /* no window routed to the matrix cores (1, 2 and 6 are unused) */
 #define TCA_TILES_PAIR 3       /* paired MFMA + staging wavefronts (default when windows are narrow) */
 #define TCA_TILES_DENSE 4      /* dense condensed tiles (TCA_PLAN_MFMA_DENSE) */
 #define TCA_TILES_DENSE_K 5    /* dense tiles spanning all of K (default when the windows cover most of K) */
-#define TCA_TILES_SPARSE 6     /* 2:4-grouped tiles on the sparse matrix cores (TCA_PLAN_MFMA_SPARSE) */
 #define TCA_TILES_COMPACT 7    /* dense tiles with compacted steps (TCA_PLAN_MFMA_COMPACT) */
 
 /* Replaces reference workload_manager (src/our_spmm.cu:353-477) plus the
@@ -225,7 +224,7 @@ int tca_spmm_24(const void* d_vals, const uint16_t* d_meta, int32_t M, int32_t K
  * task emission).  With TCA_PLAN_NO_MFMA, TCA_PLAN_MFMA_DENSE (optionally
  * with TCA_PLAN_FORCE_MFMA), or by default when the windows cover most of K,
  * the plan equals the host planner's for the same flags, entry for entry.
- * TCA_PLAN_MFMA_REGS, _DMA, _PAIR and _SPARSE give TCA_ERR_UNSUPPORTED;
+ * TCA_PLAN_MFMA_PAIR gives TCA_ERR_UNSUPPORTED; panels are host-planned only;
  * window tables above 2^25 words (windows x ceil(K / 32)) leave every row on
  * the row kernel.  The structure is validated on the device
  * (TCA_ERR_INVALID as the host planner).  The plan copies the structure;

@@ -17,17 +17,18 @@ LIB_PATH = os.path.join(_HERE, "lib", "libtcaspmm.so")
 
 TCA_F16, TCA_F32, TCA_BF16 = 0, 1, 2
 DTYPE_NAMES = {TCA_F16: "f16", TCA_F32: "f32", TCA_BF16: "bf16"}
-TCA_PLAN_DEFAULT, TCA_PLAN_NO_MFMA, TCA_PLAN_FORCE_MFMA, TCA_PLAN_MFMA_REGS, TCA_PLAN_MFMA_DMA = 0, 1, 2, 4, 8
+TCA_PLAN_DEFAULT, TCA_PLAN_NO_MFMA, TCA_PLAN_FORCE_MFMA = 0, 1, 2
 TCA_PLAN_MFMA_DENSE = 16
-TCA_PLAN_MFMA_SPARSE = 32
 TCA_PLAN_MFMA_PAIR = 64
 TCA_PLAN_MFMA_COMPACT = 128
 TCA_PLAN_NO_PANELS = 256
 TCA_PLAN_FORCE_PANELS = 512
 TCA_PLAN_NO_SCRATCH = 1024
+TCA_PLAN_KNOWN_FLAGS = (TCA_PLAN_NO_MFMA | TCA_PLAN_FORCE_MFMA | TCA_PLAN_MFMA_DENSE | TCA_PLAN_MFMA_PAIR |
+                        TCA_PLAN_MFMA_COMPACT | TCA_PLAN_NO_PANELS | TCA_PLAN_FORCE_PANELS | TCA_PLAN_NO_SCRATCH)
 # tile kernel of a plan (tca_plan_info.tile_kernel)
-TCA_TILES_NONE, TCA_TILES_REGS, TCA_TILES_DMA, TCA_TILES_PAIR = 0, 1, 2, 3
-TCA_TILES_DENSE, TCA_TILES_DENSE_K, TCA_TILES_SPARSE, TCA_TILES_COMPACT = 4, 5, 6, 7
+TCA_TILES_NONE, TCA_TILES_PAIR = 0, 3
+TCA_TILES_DENSE, TCA_TILES_DENSE_K, TCA_TILES_COMPACT = 4, 5, 7
 
 i32 = ctypes.c_int32
 i64 = ctypes.c_int64

@@ -30,7 +30,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#include "mfma_dma_kernel.hpp"
+#include "mfma_common.hpp"
 
 namespace tca {
 

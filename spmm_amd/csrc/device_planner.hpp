@@ -27,7 +27,7 @@
 #include <stdint.h>
 
 #include "planner.hpp"
-#include "mfma_dma_kernel.hpp"
+#include "mfma_common.hpp"
 
 namespace tca {
 

@@ -2,7 +2,7 @@
 // dense A tiles: both operands reach LDS by global -> LDS transfers, so no
 // wavefront writes LDS during the main loop.
 //
-// Tiles and steps are those of the paired and LDS-DMA kernels: a workgroup
+// Tiles and steps are those of the paired kernel: a workgroup
 // owns a 128-row window of A and a 64-column block of C, a step is 32
 // condensed columns, an iteration is 4 steps, K-split over four consumers
 // (step 4 i + w of iteration i goes to consumer w), partial tiles added
@@ -39,7 +39,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#include "mfma_dma_kernel.hpp"
+#include "mfma_common.hpp"
 
 namespace tca {
 

@@ -1,11 +1,10 @@
 // mfma_pair_kernel.hpp -- condensed-tile SpMM on gfx950 matrix cores with one
 // MFMA wavefront and one staging wavefront per SIMD.
 //
-// Same tiles and steps as mfma_dma_kernel (mfma_dma_kernel.hpp): a workgroup
-// owns a 128-row window of A and a 64-column block of C and walks the
-// window's steps of 32 condensed columns, K-split over four consumers (step
-// 4 i + w of iteration i goes to consumer w), partial tiles added through LDS
-// at the end.  What differs is who does what:
+// Tiles and steps of mfma_common.hpp: a workgroup owns a 128-row window of A
+// and a 64-column block of C and walks the window's steps of 32 condensed
+// columns, K-split over four consumers (step 4 i + w of iteration i goes to
+// consumer w), partial tiles added through LDS at the end.  Who does what:
 //   * consumer wavefront w only reads fragments and issues MFMAs.  During the
 //     32 v_mfma_f32_16x16x32 of step i it issues the 16 fragment reads of its
 //     step i + 1 (8 A reads of 16 bytes, 8 transposing B reads), interleaved
@@ -47,7 +46,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#include "mfma_dma_kernel.hpp"
+#include "mfma_common.hpp"
 
 namespace tca {
 

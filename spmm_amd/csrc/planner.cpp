@@ -266,139 +266,6 @@ void plan_mfma(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_t 
     p->eoff.push_back(static_cast<int32_t>(p->entries.size()));
 }
 
-void plan_mfma24(const MfmaPlan& m, const int32_t* rowptr, const int32_t* colidx, Mfma24Plan* p) {
-    constexpr int kWin = 128, kStep64 = 64;
-    *p = Mfma24Plan();
-    const size_t nw = m.windows.size();
-    // per window: the grouped order of its condensed columns
-    std::vector<std::vector<int32_t>> order(nw);
-    std::vector<int64_t> pads(nw, 0);
-#pragma omp parallel for schedule(dynamic, 1)
-    for (size_t w = 0; w < nw; w++) {
-        const Int4 win = m.windows[w];
-        const int32_t r0 = win.x, r1 = std::min<int32_t>(r0 + kWin, static_cast<int32_t>(m.row_mfma.size()));
-        // the window's column union (the condensed columns, ascending) and,
-        // per column, the rows holding it
-        std::vector<int32_t> u;
-        for (int32_t s = 0; s < win.y; s++)
-            for (int32_t k = 0; k < 32; k++) {
-                const int32_t c = m.ucols[static_cast<size_t>(win.z + s) * 32 + k];
-                if (c >= 0) u.push_back(c);
-            }
-        std::vector<int32_t> first(u.size() + 1, 0), rowsof;
-        {
-            std::vector<int32_t> cnt(u.size(), 0);
-            for (int32_t r = r0; r < r1; r++)
-                for (int32_t j = rowptr[r]; j < rowptr[r + 1]; j++)
-                    cnt[std::lower_bound(u.begin(), u.end(), colidx[j]) - u.begin()]++;
-            for (size_t i = 0; i < u.size(); i++) first[i + 1] = first[i] + cnt[i];
-            rowsof.resize(first.back());
-            std::vector<int32_t> fill(first.begin(), first.end() - 1);
-            for (int32_t r = r0; r < r1; r++)
-                for (int32_t j = rowptr[r]; j < rowptr[r + 1]; j++)
-                    rowsof[fill[std::lower_bound(u.begin(), u.end(), colidx[j]) - u.begin()]++] = r - r0;
-        }
-        // Greedy: each column joins the first open group (of the most recent
-        // ones) in which none of its rows already has two entries; a group
-        // closes at 4 columns; a column fitting none opens a new group.
-        constexpr int kOpen = 16;
-        struct Group {
-            int32_t c[4];
-            int32_t n;
-            uint8_t cnt[kWin];
-        };
-        std::vector<Group> groups;
-        std::vector<int32_t> open;  // indices into groups, not yet full
-        for (size_t i = 0; i < u.size(); i++) {
-            int32_t g = -1;
-            for (int32_t o : open) {
-                bool ok = true;
-                for (int32_t t = first[i]; t < first[i + 1] && ok; t++) ok = groups[o].cnt[rowsof[t]] < 2;
-                if (ok) {
-                    g = o;
-                    break;
-                }
-            }
-            if (g < 0) {
-                groups.push_back(Group{});
-                std::memset(&groups.back(), 0, sizeof(Group));
-                g = static_cast<int32_t>(groups.size()) - 1;
-                open.push_back(g);
-                if (open.size() > kOpen) open.erase(open.begin());  // oldest stays partly empty (padding)
-            }
-            Group& G = groups[g];
-            G.c[G.n++] = static_cast<int32_t>(i);
-            for (int32_t t = first[i]; t < first[i + 1]; t++) G.cnt[rowsof[t]]++;
-            if (G.n == 4) open.erase(std::find(open.begin(), open.end(), g));
-        }
-        std::vector<int32_t>& ord = order[w];
-        for (const Group& G : groups)
-            for (int32_t k = 0; k < 4; k++) ord.push_back(k < G.n ? u[G.c[k]] : -1);
-        while (ord.size() % kStep64) ord.push_back(-1);
-        pads[w] = static_cast<int64_t>(ord.size() - u.size());
-    }
-    // global steps, B rows, compressed positions and index words
-    int32_t gstep = 0;
-    std::vector<std::vector<std::pair<uint32_t, int32_t>>> wpos(nw);
-    for (size_t w = 0; w < nw; w++) {
-        const Int4 win = m.windows[w];
-        const int32_t steps = static_cast<int32_t>(order[w].size() / kStep64);
-        p->windows.push_back({win.x, steps, gstep, win.w});
-        p->cols.insert(p->cols.end(), order[w].begin(), order[w].end());
-        p->pad_cols += pads[w];
-        gstep += steps;
-    }
-    p->idx.assign(static_cast<size_t>(gstep) * 8 * 64, 0x44444444u);
-#pragma omp parallel for schedule(dynamic, 1)
-    for (size_t w = 0; w < nw; w++) {
-        const Int4 win = p->windows[w];
-        const std::vector<int32_t>& ord = order[w];
-        // condensed position of each column of the window
-        std::vector<std::pair<int32_t, int32_t>> at;  // (column, position)
-        for (size_t q = 0; q < ord.size(); q++)
-            if (ord[q] >= 0) at.emplace_back(ord[q], static_cast<int32_t>(q));
-        std::sort(at.begin(), at.end());
-        const int32_t r1 = std::min<int32_t>(win.x + kWin, static_cast<int32_t>(m.row_mfma.size()));
-        for (int32_t r = win.x; r < r1; r++) {
-            // this row's entries by condensed position
-            std::vector<std::pair<int32_t, int32_t>> e;  // (position, nonzero)
-            for (int32_t j = rowptr[r]; j < rowptr[r + 1]; j++)
-                e.emplace_back(std::lower_bound(at.begin(), at.end(), std::make_pair(colidx[j], -1))->second, j);
-            std::sort(e.begin(), e.end());
-            const int32_t rr = r - win.x, rb = rr / 16;
-            for (size_t a = 0; a < e.size();) {
-                const int32_t grp = e[a].first / 4;
-                size_t b = a;
-                while (b < e.size() && e[b].first / 4 == grp) b++;
-                // b - a <= 2 by construction
-                int32_t p0, p1, slot0 = -1, slot1 = -1;
-                if (b - a == 2) {
-                    p0 = e[a].first % 4, p1 = e[a + 1].first % 4, slot0 = static_cast<int32_t>(a),
-                    slot1 = static_cast<int32_t>(a + 1);
-                } else {
-                    const int32_t q = e[a].first % 4;
-                    if (q == 3) p0 = 2, p1 = 3, slot1 = static_cast<int32_t>(a);
-                    else p0 = q, p1 = q + 1, slot0 = static_cast<int32_t>(a);
-                }
-                const int32_t pos = grp * 4;
-                const int32_t step = pos / kStep64, lc = pos % kStep64;
-                const int32_t lane = rr % 16 + 16 * (lc / 16), G = (lc % 16) / 4;
-                const size_t word = (static_cast<size_t>(win.z + step) * 8 + rb) * 64 + lane;
-                const uint32_t nib = static_cast<uint32_t>(p0 | (p1 << 2));
-                uint32_t v = p->idx[word] & 0xffffu;
-                v = (v & ~(0xfu << (4 * G))) | (nib << (4 * G));
-                p->idx[word] = v | (v << 16);
-                const size_t half = word * 8 + 2 * G;
-                if (slot0 >= 0) wpos[w].emplace_back(static_cast<uint32_t>(half), e[slot0].second);
-                if (slot1 >= 0) wpos[w].emplace_back(static_cast<uint32_t>(half + 1), e[slot1].second);
-                a = b;
-            }
-        }
-        std::sort(wpos[w].begin(), wpos[w].end());
-    }
-    for (auto& v : wpos) p->pos.insert(p->pos.end(), v.begin(), v.end());
-}
-
 int32_t panel_elems(int32_t N, int32_t es) {
     for (int32_t e = 8; e >= 2; e >>= 1)
         if (N % (16 * e) == 0 && e * es >= 8 && e * es <= 32) return e;

@@ -46,8 +46,7 @@ struct RowPlan {
     int32_t n_multi = 0, n_seg = 0, n_rowtasks = 0, n_wide = 0;
 };
 
-// Row windows routed to an MFMA tile kernel (64 rows each for the
-// register-staged kernel, 128 for the LDS-DMA kernel).  For window i:
+// Row windows of 128 rows routed to an MFMA tile kernel.  For window i:
 // windows[i] = {first row, steps, first global step, first nonzero}; step s
 // of the window has B rows ucols[(first global step + s) * 32 + 0..31]
 // (-1 = padding past the column union) and nonzeros
@@ -77,22 +76,18 @@ struct MfmaShape {
     double fixed_us, iter_us;  // cost model: launch + prologue, one 4-step iteration
     int32_t fill_iters;        // pipeline fill, in iterations
 };
-// Register-staged kernel: 64 x 128 tiles, up to 1024 nonzeros per step, a
-// 4-step iteration ~0.95 us.  LDS-DMA kernel: 128 x 64 tiles, up to 512.
-// Dense-tile kernel: 128 x 64 tiles, no per-step entry limit (a step is a
-// dense 128 x 32 tile), a 4-step iteration ~0.5 us.
-constexpr MfmaShape kMfmaRegsShape = {64, 128, 1024, 3.0, 0.95, 4};
-constexpr MfmaShape kMfmaDmaShape = {128, 64, 512, 3.0, 0.95, 3};
+// Paired kernel: 128 x 64 tiles, up to 512 nonzeros per step, a 4-step
+// iteration ~0.95 us.  Dense-tile kernels: 128 x 64 tiles, no per-step entry
+// limit (a step is a dense 128 x 32 tile), a 4-step iteration ~0.5 us.
+constexpr MfmaShape kMfmaPairShape = {128, 64, 512, 3.0, 0.95, 3};
 constexpr MfmaShape kMfmaDenseShape = {128, 64, 128 * 32, 3.0, 0.5, 3};
 inline const MfmaShape& mfma_shape(uint32_t flags) {
-    if (flags & TCA_PLAN_MFMA_REGS) return kMfmaRegsShape;
-    if (flags & TCA_PLAN_MFMA_DMA) return kMfmaDmaShape;
-    if (flags & (TCA_PLAN_MFMA_DENSE | TCA_PLAN_MFMA_SPARSE | TCA_PLAN_MFMA_COMPACT)) return kMfmaDenseShape;
-    return kMfmaDmaShape;
+    if (flags & (TCA_PLAN_MFMA_DENSE | TCA_PLAN_MFMA_COMPACT)) return kMfmaDenseShape;
+    return kMfmaPairShape;
 }
 
 struct MfmaPlan {
-    int32_t win_rows = 64;
+    int32_t win_rows = 128;
     std::vector<Int4> windows;
     std::vector<int32_t> ucols;
     std::vector<int32_t> eoff;
@@ -102,27 +97,6 @@ struct MfmaPlan {
     int64_t cond_cols = 0;          // padded condensed columns, summed over windows
     int32_t rows = 0;
 };
-
-// 2:4 form of the MFMA windows (the sparse-matrix-core tile kernel).  Each
-// window's condensed columns are reordered and padded so that every aligned
-// group of 4 condensed columns holds at most two nonzeros of any row (the
-// 2:4 structure v_smfmac needs); a step is 64 condensed columns.  For window
-// i: windows[i] = {first row, steps, first global step, first nonzero};
-// cols[(first global step + s) * 64 + j] = the A column (B row) at condensed
-// position 64 s + j, -1 for padding.  Per nonzero of the windows: the half
-// index of its value in the compressed tiles, with its CSR index (8 KiB
-// per step: [row block 8][lane 64][8 halves], lane L = row % 16 + 16 *
-// (column group of 16), halves 2 G + slot for group G of 4).  idx[step][row
-// block][lane] = the lane's v_smfmac index word (both 16-bit halves).
-struct Mfma24Plan {
-    std::vector<Int4> windows;
-    std::vector<int32_t> cols;
-    std::vector<std::pair<uint32_t, int32_t>> pos;  // (half index, CSR nonzero), sorted by half index
-    std::vector<uint32_t> idx;
-    int64_t pad_cols = 0;           // padding positions added by the grouping (all windows)
-};
-// Builds the 2:4 form of the windows of `m` (128-row windows, any step size).
-void plan_mfma24(const MfmaPlan& m, const int32_t* rowptr, const int32_t* colidx, Mfma24Plan* p);
 
 // Windows routed by the rule above (min_density replaces kMfmaMinDensity; with
 // force every qualifying window, with disable none).  Only for fp16 / bf16 and

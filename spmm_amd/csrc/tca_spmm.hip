@@ -12,19 +12,18 @@
 #include "common.hpp"
 #include "planner.hpp"
 #include "row_kernel.hpp"
-#include "mfma_kernel.hpp"
-#include "mfma_dma_kernel.hpp"
+#include "mfma_common.hpp"
 #include "mfma_pair_kernel.hpp"
 #include "mfma_dense_kernel.hpp"
 #include "mfma_compact_kernel.hpp"
 #include "bell_kernel.hpp"
 #include "sparse24_kernel.hpp"
 #include "device_planner.hpp"
-#include "mfma_sparse_kernel.hpp"
 #include "panel_kernel.hpp"
-
-#include <hipcub/hipcub.hpp>
 #include "sddmm_kernel.hpp"
+
+#include <rocprim/device/device_radix_sort.hpp>
+#include <rocprim/device/device_scan.hpp>
 
 using namespace tca;
 
@@ -42,17 +41,13 @@ struct tca_spmm_plan {
     RowPlan rows;
     MfmaPlan mfma;
     int32_t mfma_col_blocks = 0;
-    int32_t mfma_slots = 1;  // entries per thread and step in the MFMA kernel (1, 2 or 4)
-    bool mfma_dma = false;   // LDS-DMA tile kernel instead of the register-staged one
     bool mfma_pair = false;  // paired (MFMA + staging wavefront) tile kernel
     bool mfma_dense = false; // dense-tile kernel (plan keeps dense condensed windows)
-    bool mfma_sparse = false; // 2:4-grouped windows on the sparse matrix cores
     bool mfma_natural = false; // dense kernel: windows span all of K in column order (B rows contiguous)
     bool mfma_compact = false; // dense kernel on compacted steps (non-empty fragment cells only)
     bool mfma_compact_want = false; // compact the dense tiles if every step fits
     int mfma_compact_lb = 3;   // compact kernel: transfer lookahead in iterations (3, or 4 by TCA_COMPACT_LB)
     uint64_t* d_amask = nullptr;  // compact kernel: [global step][8] non-empty cells per row block
-    int32_t n_windows24 = 0;  // windows of the 2:4 plan
     uint16_t* d_adense = nullptr;  // dense kernel: [global step] 8 KiB A tile, then 1 KiB of zeros
     size_t adense_halves = 0;
     int32_t n_dn = 0;              // dense kernel: nonzeros the pack writes
@@ -69,7 +64,7 @@ struct tca_spmm_plan {
     int32_t n_pk_words = 0;         // words of d_packed that the pack kernel writes
     int* d_pk_src = nullptr;        // per packed word: CSR index of its nonzero, -1 for none
     uint16_t* d_pk_cell = nullptr;  // per packed word: its cell (low 16 bits)
-    uint32_t* d_packed = nullptr;   // cell | value << 16 per entry (rewritten each run) + sentinel
+    uint32_t* d_packed = nullptr;   // cell | value << 16 per entry word (rewritten each run), then 16 zero bytes
     int32_t ntasks = 0;
     int* d_rowptr = nullptr;
     int* d_colidx = nullptr;
@@ -219,7 +214,7 @@ int launch_rows_e(const tca_spmm_plan* p, const void* val, const void* B, float*
 
 // Pairs the MFMA entries with this run's values (before the tile kernel).
 void launch_pack(const tca_spmm_plan* p, const void* val, hipStream_t s) {
-    if (p->mfma_dense || p->mfma_sparse) {
+    if (p->mfma_dense) {
         if (p->n_dn > 0)
             hipLaunchKernelGGL(dense_pack_kernel, dim3((p->n_dn + 255) / 256), dim3(256), 0, s, p->d_dn_src,
                                p->d_dn_pos, p->n_dn, static_cast<const uint16_t*>(val), p->d_adense);
@@ -233,10 +228,11 @@ void launch_pack(const tca_spmm_plan* p, const void* val, hipStream_t s) {
 
 static_assert(kPnWaves == kPanelWaves && kPnRpg == kPanelRpg && kPnCntRows == kPanelCntRows, "panel plan layout");
 static_assert(PanelGeom<float, 8>::kP == 128 && PanelGeom<float, 4>::kP == 255, "panel tile widths (panel_tile_cols)");
-static_assert(kMfmaDmaShape.max_step_entries == kDmaMaxStepEntries, "planner and LDS-DMA kernel agree on step size");
-static_assert(kMfmaDmaShape.win_rows == kDmaWinRows && kMfmaDmaShape.tile_cols == kDmaTileCols, "LDS-DMA tile shape");
-static_assert(kMfmaDmaShape.max_step_entries <= 8 * kPairGroup, "paired kernel: at most 8 entry groups per step");
-static_assert(kMfmaRegsShape.win_rows == kWinRows && kMfmaRegsShape.tile_cols == kTileCols, "register tile shape");
+static_assert(kMfmaPairShape.max_step_entries == kDmaMaxStepEntries, "planner and paired kernel agree on step size");
+static_assert(kMfmaPairShape.win_rows == kDmaWinRows && kMfmaPairShape.tile_cols == kDmaTileCols, "paired tile shape");
+static_assert(kMfmaDenseShape.win_rows == kDmaWinRows && kMfmaDenseShape.tile_cols == kDmaTileCols, "dense tile shape");
+static_assert(kMfmaPairShape.max_step_entries <= 8 * kPairGroup, "paired kernel: at most 8 entry groups per step");
+static_assert(kPairThreads == kDnThreads, "tile kernels share one workgroup size");
 
 int launch_mfma(const tca_spmm_plan* p, const void* B, float* C, hipStream_t s) {
     if (p->mfma.windows.empty()) return TCA_OK;
@@ -252,25 +248,12 @@ int launch_mfma(const tca_spmm_plan* p, const void* B, float* C, hipStream_t s) 
     a.N = p->N;
     a.col_blocks = p->mfma_col_blocks;
     a.B_bytes = static_cast<uint32_t>(static_cast<uint64_t>(p->K) * p->N * 2);
-    // The packed entry array ends with one kNoEntry sentinel (set at plan time).
-    const int n_ent = static_cast<int>(p->mfma.entries.size());
-    a.sentinel = n_ent;
     a.zeros = p->d_packed + p->mfma_zeros_at;
     a.packed_bytes = static_cast<uint32_t>(p->n_packed * 4);
     a.ucols_bytes = static_cast<uint32_t>(p->mfma.ucols.size() * 4);
     a.eoff_bytes = static_cast<uint32_t>(p->mfma.eoff.size() * 4);
     const dim3 grid(static_cast<unsigned>(p->mfma.windows.size()) * p->mfma_col_blocks);
     const bool bf = p->dtype == TCA_BF16;
-    if (p->mfma_sparse) {
-        a.adense = p->d_adense;
-        a.packed = p->d_packed;  // index words
-        a.zeros = p->d_adense + (p->adense_halves - 512);
-        a.n_windows = p->n_windows24;
-        const dim3 sgrid(mfma_dense_grid(a.n_windows, p->mfma_col_blocks));
-        if (bf) hipLaunchKernelGGL((mfma_sparse_kernel<true>), sgrid, dim3(kSpThreads), 0, s, a);
-        else hipLaunchKernelGGL((mfma_sparse_kernel<false>), sgrid, dim3(kSpThreads), 0, s, a);
-        return TCA_OK;
-    }
     if (p->mfma_dense) {
         a.adense = p->d_adense;
         a.zeros = p->d_adense + (p->adense_halves - 512);
@@ -314,34 +297,7 @@ int launch_mfma(const tca_spmm_plan* p, const void* B, float* C, hipStream_t s) 
             default: return fail(TCA_ERR_INVALID, "bad MFMA entry group count %d", p->mfma_groups);
         }
     }
-    if (p->mfma_dma && p->mfma_slots <= 2) {
-        switch (p->mfma_slots) {
-            case 1:
-                if (bf) hipLaunchKernelGGL((mfma_dma_kernel<true, 1>), grid, dim3(kMfmaThreads), 0, s, a);
-                else hipLaunchKernelGGL((mfma_dma_kernel<false, 1>), grid, dim3(kMfmaThreads), 0, s, a);
-                return TCA_OK;
-            case 2:
-                if (bf) hipLaunchKernelGGL((mfma_dma_kernel<true, 2>), grid, dim3(kMfmaThreads), 0, s, a);
-                else hipLaunchKernelGGL((mfma_dma_kernel<false, 2>), grid, dim3(kMfmaThreads), 0, s, a);
-                return TCA_OK;
-            default: break;  // four slots per thread: register-staged kernel (LDS budget)
-        }
-    }
-    switch (p->mfma_slots) {
-        case 1:
-            if (bf) hipLaunchKernelGGL((mfma_tile_kernel<true, 1>), grid, dim3(kMfmaThreads), 0, s, a);
-            else hipLaunchKernelGGL((mfma_tile_kernel<false, 1>), grid, dim3(kMfmaThreads), 0, s, a);
-            return TCA_OK;
-        case 2:
-            if (bf) hipLaunchKernelGGL((mfma_tile_kernel<true, 2>), grid, dim3(kMfmaThreads), 0, s, a);
-            else hipLaunchKernelGGL((mfma_tile_kernel<false, 2>), grid, dim3(kMfmaThreads), 0, s, a);
-            return TCA_OK;
-        case 4:
-            if (bf) hipLaunchKernelGGL((mfma_tile_kernel<true, 4>), grid, dim3(kMfmaThreads), 0, s, a);
-            else hipLaunchKernelGGL((mfma_tile_kernel<false, 4>), grid, dim3(kMfmaThreads), 0, s, a);
-            return TCA_OK;
-        default: return fail(TCA_ERR_INVALID, "bad MFMA slot count %d", p->mfma_slots);
-    }
+    return fail(TCA_ERR_INVALID, "plan has MFMA windows but no tile kernel");
 }
 
 int launch_rows(const tca_spmm_plan* p, const void* val, const void* B, float* C, float* W, hipStream_t s) {
@@ -438,21 +394,15 @@ void fill_info(tca_spmm_plan* p) {
     in.rows_mfma = p->mfma.rows;
     in.nnz_mfma = p->mfma.nnz;
     in.cond_cols_mfma = p->mfma.cond_cols;
-    in.mfma_blocks = (p->mfma_dense || p->mfma_sparse) ? mfma_dense_grid(in.n_windows_mfma, p->mfma_col_blocks)
+    in.mfma_blocks = p->mfma_dense ? mfma_dense_grid(in.n_windows_mfma, p->mfma_col_blocks)
                                    : in.n_windows_mfma * p->mfma_col_blocks;
-    in.mfma_blockdim = kMfmaThreads;
-    if (p->mfma_sparse)
-        in.mfma_lds_bytes = mfma_sparse_lds_bytes();
-    else if (p->mfma_dense && p->mfma_compact)
+    in.mfma_blockdim = kPairThreads;
+    if (p->mfma_dense && p->mfma_compact)
         in.mfma_lds_bytes = p->mfma_compact_lb == 3 ? mfma_compact_lds_bytes<3>() : mfma_compact_lds_bytes<4>();
     else if (p->mfma_dense)
         in.mfma_lds_bytes = mfma_dense_lds_bytes();
     else if (p->mfma_pair)
         in.mfma_lds_bytes = mfma_pair_lds_bytes();
-    else if (p->mfma_dma && p->mfma_slots <= 2)
-        in.mfma_lds_bytes = mfma_dma_lds_bytes();
-    else
-        in.mfma_lds_bytes = p->mfma_slots == 1 ? mfma_lds_bytes<1>() : p->mfma_slots == 2 ? mfma_lds_bytes<2>() : mfma_lds_bytes<4>();
     in.scratch_bytes = static_cast<int64_t>(p->n_seg_total * p->N * sizeof(float));
     in.n_panels = p->panels.n_panels;
     in.n_panel_units = p->n_units;
@@ -465,12 +415,9 @@ void fill_info(tca_spmm_plan* p) {
                                           16 * p->panels.elems * static_cast<int>(dtype_size(p->dtype))
                                     : 0;
     in.tile_kernel = p->mfma.windows.empty() ? TCA_TILES_NONE
-                     : p->mfma_sparse       ? TCA_TILES_SPARSE
                      : p->mfma_compact      ? TCA_TILES_COMPACT
                      : p->mfma_dense        ? (p->mfma_natural ? TCA_TILES_DENSE_K : TCA_TILES_DENSE)
-                     : p->mfma_pair         ? TCA_TILES_PAIR
-                     : (p->mfma_dma && p->mfma_slots <= 2) ? TCA_TILES_DMA
-                                                           : TCA_TILES_REGS;
+                                            : TCA_TILES_PAIR;
 }
 
 // The reference prints its one kernel's grid, block and dynamic LDS
@@ -483,13 +430,12 @@ void print_launches(const tca_spmm_plan* p) {
         std::printf("num_block: %lld blockdim: %d shm: %fKB (%s)\n", blocks, dim, lds_bytes / 1024.0, name);
     };
     if (!p->mfma.windows.empty()) {
-        if (p->mfma_dense || p->mfma_sparse) {
+        if (p->mfma_dense) {
             if (p->n_dn > 0) line((p->n_dn + 255) / 256, 256, 0.0, "dense_pack_kernel");
         } else if (p->n_pk_words > 0) {
             line((p->n_pk_words + 1023) / 1024, 256, 0.0, "mfma_pack_kernel");
         }
-        static const char* names[] = {"", "mfma_tile_kernel", "mfma_dma_kernel", "mfma_pair_kernel",
-                                      "mfma_dense_kernel", "mfma_dense_kernel", "mfma_sparse_kernel",
+        static const char* names[] = {"", "", "", "mfma_pair_kernel", "mfma_dense_kernel", "mfma_dense_kernel", "",
                                       "mfma_compact_kernel"};
         line(in.mfma_blocks, in.mfma_blockdim, in.mfma_lds_bytes, names[in.tile_kernel]);
     }
@@ -549,6 +495,7 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
     *plan = nullptr;
     if (M < 0 || K < 1 || N < 1 || nnz < 0) return fail(TCA_ERR_INVALID, "bad shape M=%d K=%d N=%d nnz=%d", M, K, N, nnz);
     if (!dtype_ok(dtype)) return fail(TCA_ERR_INVALID, "unknown dtype %d", dtype);
+    if (flags & ~TCA_PLAN_KNOWN_FLAGS) return fail(TCA_ERR_INVALID, "unknown plan flags 0x%x", flags & ~TCA_PLAN_KNOWN_FLAGS);
     // The kernels address B, values and column indices through 32-bit buffer
     // offsets, with 0xfffffff0 reserved as the out-of-range marker.
     const uint64_t b_bytes = static_cast<uint64_t>(K) * static_cast<uint64_t>(N) * dtype_size(dtype);
@@ -570,20 +517,17 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
         delete p;
         return fail(TCA_ERR_HIP, "no HIP device");
     }
-    // Dense-enough row windows go to an MFMA tile kernel (fp16 / bf16): 64-row
-    // windows x 128 columns (register-staged) or 128 x 64 (paired or LDS-DMA kernel).
-    // TCA_MFMA_MIN_DENSITY (tuning only) overrides the routing threshold.
+    // Dense-enough 128-row windows go to an MFMA tile kernel (fp16 / bf16),
+    // 64 columns of C per workgroup: the paired kernel, or the dense-tile
+    // kernels (plain or compacted).  TCA_MFMA_MIN_DENSITY (tuning only)
+    // overrides the routing threshold.
     const char* md = std::getenv("TCA_MFMA_MIN_DENSITY");
     const MfmaShape* shape = &mfma_shape(flags);
     const double min_density = md ? std::atof(md) : kMfmaMinDensity;
     plan_mfma(rowptr, colidx, M, N, dtype, (flags & TCA_PLAN_FORCE_MFMA) != 0, (flags & TCA_PLAN_NO_MFMA) != 0,
               min_density, *shape, &p->mfma);
-    p->mfma_dma = (flags & TCA_PLAN_MFMA_REGS) == 0 && (flags & TCA_PLAN_MFMA_DMA) != 0;
-    p->mfma_dense = (flags & (TCA_PLAN_MFMA_REGS | TCA_PLAN_MFMA_DMA)) == 0 &&
-                    (flags & (TCA_PLAN_MFMA_DENSE | TCA_PLAN_MFMA_COMPACT)) != 0;
-    if ((flags & (TCA_PLAN_MFMA_REGS | TCA_PLAN_MFMA_DMA | TCA_PLAN_MFMA_DENSE | TCA_PLAN_MFMA_SPARSE |
-                  TCA_PLAN_MFMA_PAIR)) == 0 &&
-        !p->mfma.windows.empty() &&
+    p->mfma_dense = (flags & (TCA_PLAN_MFMA_DENSE | TCA_PLAN_MFMA_COMPACT)) != 0;
+    if ((flags & (TCA_PLAN_MFMA_DENSE | TCA_PLAN_MFMA_PAIR)) == 0 && !p->mfma.windows.empty() &&
         static_cast<double>(p->mfma.cond_cols) >= kNaturalCover * static_cast<double>(p->mfma.windows.size()) * K &&
         p->mfma.windows.size() * static_cast<size_t>((K + 31) / 32) * kDnATileBytes <= kDenseMaxBytes) {
         // Default kernel choice: windows that cover most of K run on the dense
@@ -598,29 +542,15 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
     if (p->mfma_dense && (p->mfma.eoff.size() - 1) * static_cast<size_t>(kDnATileBytes) > kDenseMaxBytes) {
         // Dense windows past the budget: the paired kernel, which keeps only the entries.
         p->mfma_dense = false;
-        shape = &kMfmaDmaShape;
+        shape = &kMfmaPairShape;
         plan_mfma(rowptr, colidx, M, N, dtype, (flags & TCA_PLAN_FORCE_MFMA) != 0, (flags & TCA_PLAN_NO_MFMA) != 0,
                   min_density, *shape, &p->mfma);
     }
-    p->mfma_sparse = (flags & (TCA_PLAN_MFMA_REGS | TCA_PLAN_MFMA_DMA | TCA_PLAN_MFMA_DENSE)) == 0 &&
-                     (flags & TCA_PLAN_MFMA_SPARSE) != 0;
-    Mfma24Plan m24;
-    if (p->mfma_sparse && !p->mfma.windows.empty()) {
-        plan_mfma24(p->mfma, rowptr, colidx, &m24);
-        const size_t steps24 = m24.windows.empty() ? 0 : static_cast<size_t>(m24.windows.back().z + m24.windows.back().y);
-        if (steps24 * (kSpATile + kSpITile) > kDenseMaxBytes) {
-            p->mfma_sparse = false;  // past the budget: the paired kernel
-            shape = &kMfmaDmaShape;
-            plan_mfma(rowptr, colidx, M, N, dtype, (flags & TCA_PLAN_FORCE_MFMA) != 0, (flags & TCA_PLAN_NO_MFMA) != 0,
-                      min_density, *shape, &p->mfma);
-        }
-    }
-    p->mfma_pair = (flags & (TCA_PLAN_MFMA_REGS | TCA_PLAN_MFMA_DMA)) == 0 && !p->mfma_dense && !p->mfma_sparse;
+    p->mfma_pair = !p->mfma_dense;
     p->mfma_col_blocks = (N + shape->tile_cols - 1) / shape->tile_cols;
     {
         int32_t most = 0;
         for (size_t i = 0; i + 1 < p->mfma.eoff.size(); i++) most = std::max(most, p->mfma.eoff[i + 1] - p->mfma.eoff[i]);
-        p->mfma_slots = most <= 256 ? 1 : most <= 512 ? 2 : 4;
         p->mfma_groups = most <= 4 * kPairGroup ? 4 : 8;
     }
     // Row panels with B staged in LDS for the rows outside MFMA windows, then
@@ -689,10 +619,9 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
     }
     if ((st = dev_upload(&p->d_windows, p->mfma.windows.data(), p->mfma.windows.size()))) return bail(st);
     if (!p->mfma.windows.empty()) {
-        // Device forms: B row byte offsets (padding 0xffffffff); per entry its
-        // fragment-order A-tile cell and nonzero index (the pack kernel pairs
-        // them with the run's values), and the packed array's kNoEntry sentinel.
-        // (Paired kernel: each step's 32 offsets permuted, word 4 r + k = column r + 8 k.)
+        // Device forms: B row byte offsets (padding 0xffffffff; paired kernel:
+        // each step's 32 offsets permuted, word 4 r + k = column r + 8 k) and
+        // the step entry ranges.
         std::vector<uint32_t> uoff(p->mfma.ucols.size());
         for (size_t i = 0; i < uoff.size(); i++) {
             const size_t src = p->mfma_pair ? (i & ~size_t(31)) + ((i & 31) >> 2) + 8 * (i & 3) : i;
@@ -703,37 +632,7 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
         p->n_ucols = uoff.size();
         if ((st = dev_upload(&p->d_eoff, p->mfma.eoff.data(), p->mfma.eoff.size()))) return bail(st);
     }
-    if (!p->mfma.windows.empty() && p->mfma_sparse) {
-        // 2:4 windows: their own window table and 64-column steps of B rows;
-        // compressed value tiles (zero, values written per run), fixed index
-        // words, 1 KiB of zeros after the value tiles.
-        (void)hipFree(p->d_windows);
-        (void)hipFree(p->d_ucols);
-        p->d_windows = nullptr;
-        p->d_ucols = nullptr;
-        p->n_windows24 = static_cast<int32_t>(m24.windows.size());
-        p->mfma.cond_cols = static_cast<int64_t>(m24.cols.size());  // padded 2:4 condensed columns
-        if ((st = dev_upload(&p->d_windows, m24.windows.data(), m24.windows.size()))) return bail(st);
-        std::vector<uint32_t> uoff(m24.cols.size());
-        for (size_t i = 0; i < uoff.size(); i++)
-            uoff[i] = m24.cols[i] < 0 ? kNoEntry : static_cast<uint32_t>(m24.cols[i]) * static_cast<uint32_t>(N) * 2u;
-        if ((st = dev_upload(&p->d_ucols, uoff.data(), uoff.size()))) return bail(st);
-        const size_t steps24 = m24.cols.size() / kSpStepK;
-        p->adense_halves = steps24 * (kSpATile / 2) + 512;
-        if ((st = dev_upload(&p->d_adense, nullptr, p->adense_halves))) return bail(st);
-        if (hipMemset(p->d_adense, 0, p->adense_halves * 2) != hipSuccess)
-            return bail(fail(TCA_ERR_HIP, "hipMemset of the compressed tiles failed"));
-        if ((st = dev_upload(&p->d_packed, m24.idx.data(), m24.idx.size()))) return bail(st);
-        std::vector<int32_t> dsrc(m24.pos.size());
-        std::vector<uint32_t> dpos(m24.pos.size());
-        for (size_t x = 0; x < m24.pos.size(); x++) {
-            dpos[x] = m24.pos[x].first;
-            dsrc[x] = m24.pos[x].second;
-        }
-        p->n_dn = static_cast<int32_t>(dsrc.size());
-        if ((st = dev_upload(&p->d_dn_src, dsrc.data(), dsrc.size()))) return bail(st);
-        if ((st = dev_upload(&p->d_dn_pos, dpos.data(), dpos.size()))) return bail(st);
-    } else if (!p->mfma.windows.empty() && p->mfma_dense) {
+    if (!p->mfma.windows.empty() && p->mfma_dense) {
         // Dense condensed windows: 8 KiB per global step (128 rows x 32
         // condensed columns in fragment order), zero except at the entries,
         // whose values the pack kernel writes each run; 1 KiB of zeros after
@@ -825,49 +724,36 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
         if (hipMemset(p->d_adense, 0, p->adense_halves * 2) != hipSuccess)
             return bail(fail(TCA_ERR_HIP, "hipMemset of the dense tiles failed"));
     } else if (!p->mfma.windows.empty()) {
-        // Packed entries.  Register-staged kernel: walk order, then one
-        // kNoEntry sentinel.  LDS-DMA kernel: step g's block at g * 256 * slots
-        // words (unused words kNoEntry).  Paired kernel: step g's block at
-        // ebase[g], whole chunks of 256 words (at least one), entries placed
-        // by pair_entry_word, unused words the dummy cell of the lane that
-        // loads them, with value 0.  Both tile kernels find 16 zero bytes
-        // (padding B source) after the blocks.
-        const size_t ne = p->mfma.entries.size();
+        // Packed entries of the paired kernel: step g's block at ebase[g],
+        // whole chunks of 256 words (at least one), entries placed by
+        // pair_entry_word, unused words the dummy cell of the lane that loads
+        // them, with value 0; 16 zero bytes (padding B source) after the blocks.
         const size_t nsteps_all = p->mfma.eoff.size() - 1;
-        const size_t ewords = 256u * static_cast<size_t>(p->mfma_slots);
-        std::vector<int> ebase;
-        std::vector<i32x2v> emeta;
-        if (p->mfma_pair) {
-            ebase.resize(nsteps_all + 1);
-            emeta.resize(nsteps_all);
-            ebase[0] = 0;
-            for (size_t g = 0; g < nsteps_all; g++) {
-                const int cnt = p->mfma.eoff[g + 1] - p->mfma.eoff[g];
-                const int chunks = std::max(1, (cnt + kPairChunk - 1) / kPairChunk);
-                ebase[g + 1] = ebase[g] + chunks * kPairChunk;
-                emeta[g] = i32x2v{ebase[g], std::max(1, (cnt + kPairGroup - 1) / kPairGroup)};
-            }
+        std::vector<int> ebase(nsteps_all + 1);
+        std::vector<i32x2v> emeta(nsteps_all);
+        ebase[0] = 0;
+        for (size_t g = 0; g < nsteps_all; g++) {
+            const int cnt = p->mfma.eoff[g + 1] - p->mfma.eoff[g];
+            const int chunks = std::max(1, (cnt + kPairChunk - 1) / kPairChunk);
+            ebase[g + 1] = ebase[g] + chunks * kPairChunk;
+            emeta[g] = i32x2v{ebase[g], std::max(1, (cnt + kPairGroup - 1) / kPairGroup)};
         }
-        const size_t nblocks = p->mfma_pair ? static_cast<size_t>(ebase.back()) : nsteps_all * ewords;
-        const bool tiles_lds = p->mfma_dma || p->mfma_pair;
-        const size_t npacked = tiles_lds ? nblocks + 4 : ne + 1;
-        p->mfma_zeros_at = tiles_lds ? nblocks : 0;
-        // pack kernel inputs, per word it writes (all words before the zeros /
-        // the sentinel): the nonzero's CSR index and the cell
-        const size_t nwords = tiles_lds ? nblocks : ne;
+        const size_t nwords = static_cast<size_t>(ebase.back());
+        const size_t npacked = nwords + 4;
+        p->mfma_zeros_at = nwords;
+        // pack kernel inputs, per word it writes (all words before the
+        // zeros): the nonzero's CSR index and the cell
         std::vector<int> src(nwords, -1);
         std::vector<uint16_t> cell(nwords, 0xffffu);
         std::vector<uint32_t> packed(npacked, kNoEntry);
-        if (tiles_lds) std::fill(packed.end() - 4, packed.end(), 0u);
-        if (p->mfma_pair) {
-            for (size_t w = 0; w < p->mfma.windows.size(); w++) {
-                const Int4 win = p->mfma.windows[w];
-                for (int32_t j = 0; j < win.y; j++)
-                    for (int32_t x = ebase[win.z + j]; x < ebase[win.z + j + 1]; x++) {
-                        packed[x] = pair_cell_addr(j % kPairSteps, kDmaATile + ((x - ebase[win.z + j]) % kPairChunk) / 4);
-                        cell[x] = static_cast<uint16_t>(packed[x]);
-                    }
-            }
+        std::fill(packed.end() - 4, packed.end(), 0u);
+        for (size_t w = 0; w < p->mfma.windows.size(); w++) {
+            const Int4 win = p->mfma.windows[w];
+            for (int32_t j = 0; j < win.y; j++)
+                for (int32_t x = ebase[win.z + j]; x < ebase[win.z + j + 1]; x++) {
+                    packed[x] = pair_cell_addr(j % kPairSteps, kDmaATile + ((x - ebase[win.z + j]) % kPairChunk) / 4);
+                    cell[x] = static_cast<uint16_t>(packed[x]);
+                }
         }
         const int row_mask = 127, k_shift = 7, idx_shift = 12;
         for (size_t w = 0, e = 0; w < p->mfma.windows.size(); w++) {
@@ -876,17 +762,9 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
                 for (; e < static_cast<size_t>(p->mfma.eoff[g + 1]); e++) {
                     const uint32_t en = p->mfma.entries[e];
                     const int acell = a_cell(static_cast<int>(en & row_mask), static_cast<int>((en >> k_shift) & 31u));
-                    size_t x;
-                    uint16_t c;
-                    if (p->mfma_pair) {
-                        x = static_cast<size_t>(ebase[g] + pair_entry_word(static_cast<int>(e - p->mfma.eoff[g])));
-                        c = static_cast<uint16_t>(pair_cell_addr((g - win.z) % kPairSteps, acell));
-                    } else {
-                        x = p->mfma_dma ? g * ewords + (e - p->mfma.eoff[g]) : e;
-                        c = static_cast<uint16_t>(acell);
-                    }
+                    const size_t x = static_cast<size_t>(ebase[g] + pair_entry_word(static_cast<int>(e - p->mfma.eoff[g])));
                     src[x] = win.w + static_cast<int>(en >> idx_shift);
-                    cell[x] = c;
+                    cell[x] = static_cast<uint16_t>(pair_cell_addr((g - win.z) % kPairSteps, acell));
                 }
         }
         p->n_pk_words = static_cast<int32_t>(nwords);
@@ -911,10 +789,10 @@ int tca_spmm_plan_create_device(const int32_t* d_rowptr, const int32_t* d_colidx
     if (M < 0 || K < 1 || N < 1 || nnz < 0) return fail(TCA_ERR_INVALID, "bad shape M=%d K=%d N=%d nnz=%d", M, K, N, nnz);
     if (!dtype_ok(dtype)) return fail(TCA_ERR_INVALID, "unknown dtype %d", dtype);
     if (!d_rowptr || (nnz > 0 && !d_colidx)) return fail(TCA_ERR_INVALID, "NULL device pointer");
-    if (flags & (TCA_PLAN_MFMA_REGS | TCA_PLAN_MFMA_DMA | TCA_PLAN_MFMA_PAIR | TCA_PLAN_MFMA_SPARSE))
+    if (flags & ~TCA_PLAN_KNOWN_FLAGS) return fail(TCA_ERR_INVALID, "unknown plan flags 0x%x", flags & ~TCA_PLAN_KNOWN_FLAGS);
+    if (flags & TCA_PLAN_MFMA_PAIR)
         return fail(TCA_ERR_UNSUPPORTED,
-                    "device planning builds row-kernel and dense-tile plans (TCA_PLAN_MFMA_REGS, _DMA, _PAIR and "
-                    "_SPARSE need the host planner)");
+                    "device planning builds row-kernel and dense-tile plans (TCA_PLAN_MFMA_PAIR needs the host planner)");
     const uint64_t b_bytes = static_cast<uint64_t>(K) * static_cast<uint64_t>(N) * dtype_size(dtype);
     if (b_bytes >= 0xfffffff0ull || static_cast<uint64_t>(nnz) * 4 >= 0xfffffff0ull)
         return fail(TCA_ERR_UNSUPPORTED, "B (%llu bytes) or the nonzeros exceed the 4 GiB buffer range",
@@ -1077,11 +955,11 @@ int tca_spmm_plan_create_device(const int32_t* d_rowptr, const int32_t* d_colidx
                 hipLaunchKernelGGL(dm_entries_kernel, rgrid, blk, 0, s, ea);
                 // ascending positions: the routed nonzeros first, in the host planner's order
                 size_t tmp_bytes = 0;
-                if (hipcub::DeviceRadixSort::SortPairs(nullptr, tmp_bytes, ekeys, ekeys_s, evals, evals_s, nnz, 0, 32, s) !=
-                        hipSuccess ||
+                if (rocprim::radix_sort_pairs(nullptr, tmp_bytes, ekeys, ekeys_s, evals, evals_s,
+                                              static_cast<size_t>(nnz), 0, 32, s) != hipSuccess ||
                     hipMalloc(&tmp, tmp_bytes) != hipSuccess ||
-                    hipcub::DeviceRadixSort::SortPairs(tmp, tmp_bytes, ekeys, ekeys_s, evals, evals_s, nnz, 0, 32, s) !=
-                        hipSuccess)
+                    rocprim::radix_sort_pairs(tmp, tmp_bytes, ekeys, ekeys_s, evals, evals_s, static_cast<size_t>(nnz),
+                                              0, 32, s) != hipSuccess)
                     return bail(fail(TCA_ERR_HIP, "entry sort failed"));
                 (void)hipFree(tmp);
                 tmp = nullptr;
@@ -1129,11 +1007,11 @@ int tca_spmm_plan_create_device(const int32_t* d_rowptr, const int32_t* d_colidx
         hipLaunchKernelGGL(dp_lengths_kernel, grid_for(M), blk, 0, s, p->d_rowptr, M,
                            p->mfma.windows.empty() ? nullptr : wmap, keys, rows);
         size_t tmp_bytes = 0;
-        if (hipcub::DeviceRadixSort::SortPairsDescending(nullptr, tmp_bytes, keys, keys_s, rows, rows_s, M, 0, 32, s) !=
-            hipSuccess)
+        if (rocprim::radix_sort_pairs_desc(nullptr, tmp_bytes, keys, keys_s, rows, rows_s, static_cast<size_t>(M), 0, 32,
+                                           s) != hipSuccess)
             return bail(fail(TCA_ERR_HIP, "radix sort sizing failed"));
         if (hipMalloc(&tmp, tmp_bytes) != hipSuccess) return bail(fail(TCA_ERR_ALLOC, "radix sort workspace"));
-        if (hipcub::DeviceRadixSort::SortPairsDescending(tmp, tmp_bytes, keys, keys_s, rows, rows_s, M, 0, 32, s) !=
+        if (rocprim::radix_sort_pairs_desc(tmp, tmp_bytes, keys, keys_s, rows, rows_s, static_cast<size_t>(M), 0, 32, s) !=
             hipSuccess)
             return bail(fail(TCA_ERR_HIP, "radix sort failed"));
         if (Mp > 0)
@@ -1156,9 +1034,11 @@ int tca_spmm_plan_create_device(const int32_t* d_rowptr, const int32_t* d_colidx
         (void)hipFree(tmp);
         tmp = nullptr;
         size_t tmp_bytes = 0;
-        if (hipcub::DeviceScan::ExclusiveSum(nullptr, tmp_bytes, nseg, segoff, n_long + 1, s) != hipSuccess ||
+        if (rocprim::exclusive_scan(nullptr, tmp_bytes, nseg, segoff, 0, static_cast<size_t>(n_long) + 1,
+                                    rocprim::plus<int>(), s) != hipSuccess ||
             hipMalloc(&tmp, tmp_bytes) != hipSuccess ||
-            hipcub::DeviceScan::ExclusiveSum(tmp, tmp_bytes, nseg, segoff, n_long + 1, s) != hipSuccess ||
+            rocprim::exclusive_scan(tmp, tmp_bytes, nseg, segoff, 0, static_cast<size_t>(n_long) + 1, rocprim::plus<int>(),
+                                    s) != hipSuccess ||
             hipMemcpyAsync(&seg_total, segoff + n_long, sizeof(int), hipMemcpyDeviceToHost, s) != hipSuccess ||
             hipStreamSynchronize(s) != hipSuccess)
             return bail(fail(TCA_ERR_HIP, "segment scan failed"));

@@ -77,11 +77,16 @@ def test_device_plan_argument_checks_need_no_gpu():
     import ctypes
     import spmm_amd as S
     p = ctypes.c_void_p()
-    # the kernels whose layouts only the host planner builds
-    for flags in (S.TCA_PLAN_MFMA_REGS, S.TCA_PLAN_MFMA_DMA, S.TCA_PLAN_MFMA_PAIR, S.TCA_PLAN_MFMA_SPARSE):
+    # the kernel whose layout only the host planner builds
+    with pytest.raises(S.TcaError) as ei:
+        S._lib.call("tca_spmm_plan_create_device", 16, 16, 4, 4, 4, 8, S.TCA_F16, S.TCA_PLAN_MFMA_PAIR, None,
+                    ctypes.byref(p))
+    assert ei.value.status == 4
+    # bits outside TCA_PLAN_KNOWN_FLAGS (4, 8 and 32 once selected tile kernels)
+    for flags in (4, 8, 32, 1 << 20):
         with pytest.raises(S.TcaError) as ei:
             S._lib.call("tca_spmm_plan_create_device", 16, 16, 4, 4, 4, 8, S.TCA_F16, flags, None, ctypes.byref(p))
-        assert ei.value.status == 4, flags
+        assert ei.value.status == 1 and b"unknown plan flags" in S._lib.lib.tca_last_error(), flags
     with pytest.raises(S.TcaError) as ei:
         S._lib.call("tca_spmm_plan_create_device", None, None, 4, 4, 4, 8, S.TCA_F32, 0, None, ctypes.byref(p))
     assert ei.value.status == 1
@@ -94,6 +99,14 @@ def test_python_constants_match_the_header():
     import spmm_amd as S
     head = open(os.path.join(ROOT, "include", "tca_spmm.h")).read()
     found = re.findall(r"#define (TCA_(?:PLAN|TILES)_\w+) (\d+)u?", head)
-    assert len(found) >= 15
+    assert len(found) >= 14
     for name, value in found:
         assert getattr(S, name) == int(value), name
+    # TCA_PLAN_KNOWN_FLAGS: the OR of the flags its definition names
+    m = re.search(r"#define TCA_PLAN_KNOWN_FLAGS\s*\\?\s*\(([^)]*)\)", head)
+    names = re.findall(r"TCA_PLAN_\w+", m.group(1))
+    assert len(names) == 8
+    want = 0
+    for name in names:
+        want |= getattr(S, name)
+    assert S.TCA_PLAN_KNOWN_FLAGS == want

@@ -137,20 +137,18 @@ def test_exact_bit_equal_all_widths(torch_cuda, dtype):
         assert np.array_equal(got, want), (dtype, n, np.abs(got - want).max())
 
 
-@pytest.mark.parametrize("variant", [S.TCA_PLAN_MFMA_REGS, S.TCA_PLAN_MFMA_DMA, S.TCA_PLAN_MFMA_PAIR, 0,
-                                     S.TCA_PLAN_MFMA_DENSE, S.TCA_PLAN_MFMA_SPARSE, S.TCA_PLAN_MFMA_COMPACT],
-                         ids=["regs", "dma", "pair", "default", "dense", "sparse", "compact"])
+@pytest.mark.parametrize("variant", [S.TCA_PLAN_MFMA_PAIR, 0, S.TCA_PLAN_MFMA_DENSE, S.TCA_PLAN_MFMA_COMPACT],
+                         ids=["pair", "default", "dense", "compact"])
 @pytest.mark.parametrize("dtype", [S.TCA_F16, S.TCA_BF16])
 def test_mfma_exact_bit_equal(torch_cuda, dtype, variant):
     """Condensed-tile MFMA path (forced on every eligible window) is bit-equal
     to the oracle on exact-arithmetic inputs, for partial windows, partial
-    column blocks and empty rows.  The cases cover one, two and four entry
-    slots per thread (up to 256, 512 and 1024 nonzeros in a step) and windows
-    whose steps span several pipeline blocks, for the three tile kernels
-    (register staging, global->LDS transfers, paired MFMA and staging
-    wavefronts).  The two 128-row kernels take at most 512 nonzeros per step:
-    the cases marked dense stay on the row kernel under them (still checked
-    against the oracle)."""
+    column blocks and empty rows.  The cases cover steps of up to 256, 512
+    and more than 512 nonzeros and windows whose steps span several pipeline
+    blocks, for the paired kernel (MFMA and staging wavefronts) and the dense
+    tiles (plain, natural column order, compacted).  The paired kernel takes
+    at most 512 nonzeros per step: the cases marked dense stay on the row
+    kernel under it (still checked against the oracle)."""
     rng = np.random.default_rng(71 + dtype)
     dense = {(200, 64, 0.45), (128, 2048, 0.2), (64, 1500, 0.4)}
     for m, k, p in [(64, 256, 0.1), (130, 700, 0.05), (200, 64, 0.45), (17, 40, 0.3), (96, 5000, 0.004),
@@ -163,9 +161,8 @@ def test_mfma_exact_bit_equal(torch_cuda, dtype, variant):
             with S.Plan(a, n, S.TCA_PLAN_FORCE_MFMA | variant) as pl:
                 info = pl.info()
                 got = run_gpu(torch_cuda, a, b, plan=pl)
-            assert info["n_windows_mfma"] > 0 or (variant != S.TCA_PLAN_MFMA_REGS and (m, k, p) in dense), (m, k, n)
-            want_kernel = {S.TCA_PLAN_MFMA_REGS: {1}, S.TCA_PLAN_MFMA_DMA: {2, 1}, S.TCA_PLAN_MFMA_PAIR: {3},
-                           0: {3, 5, 7}, S.TCA_PLAN_MFMA_DENSE: {4, 5}, S.TCA_PLAN_MFMA_SPARSE: {6},
+            assert info["n_windows_mfma"] > 0 or (m, k, p) in dense, (m, k, n)
+            want_kernel = {S.TCA_PLAN_MFMA_PAIR: {3}, 0: {3, 5, 7}, S.TCA_PLAN_MFMA_DENSE: {4, 5},
                            S.TCA_PLAN_MFMA_COMPACT: {7, 4, 5}}[variant]
             assert info["tile_kernel"] in want_kernel or info["n_windows_mfma"] == 0, (variant, info["tile_kernel"])
             want = oracle_c(a, b)

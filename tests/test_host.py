@@ -233,19 +233,20 @@ def test_condense_windows_bit_exact_with_oracle(m, k, p, win):
     assert np.array_equal(uoff, ou) and np.array_equal(ucols, oc) and np.array_equal(cpos, op)
 
 
-@pytest.mark.parametrize("m,k,n,p,flags", [(200, 700, 128, 0.06, S.TCA_PLAN_FORCE_MFMA | S.TCA_PLAN_MFMA_REGS),
-                                           (130, 300, 64, 0.02, S.TCA_PLAN_FORCE_MFMA | S.TCA_PLAN_MFMA_REGS),
-                                           (64, 2048, 256, 0.3, S.TCA_PLAN_FORCE_MFMA | S.TCA_PLAN_MFMA_REGS),
+@pytest.mark.parametrize("m,k,n,p,flags", [(200, 700, 128, 0.06, S.TCA_PLAN_FORCE_MFMA | S.TCA_PLAN_MFMA_DENSE),
+                                           (130, 300, 64, 0.02, S.TCA_PLAN_FORCE_MFMA | S.TCA_PLAN_MFMA_PAIR),
+                                           (64, 2048, 256, 0.3, S.TCA_PLAN_FORCE_MFMA | S.TCA_PLAN_MFMA_DENSE),
                                            (300, 700, 128, 0.06, S.TCA_PLAN_FORCE_MFMA),
                                            (129, 1500, 64, 0.1, S.TCA_PLAN_FORCE_MFMA)])
 def test_mfma_window_plan_decodes_to_the_csr(m, k, n, p, flags):
     """Every MFMA window's steps, B-row lists and entries reproduce the CSR
-    exactly, with the oracle's condensed positions (64-row windows for the
-    register-staged tile kernel, 128-row windows for the LDS-DMA kernel)."""
+    exactly, with the oracle's condensed positions (128-row windows; the
+    dense-tile shape admits any number of entries per step, the paired one at
+    most 512)."""
     a, _ = S.gen_bernoulli(m, k, p, seed=7, dtype=S.TCA_F16)
     windows, ucols, eoff, entries = S.plan_mfma_windows(a, n, flags=flags)
     assert len(windows) > 0
-    win = 64 if flags & S.TCA_PLAN_MFMA_REGS else 128
+    win = 128
     uo, uc, cp = oracle.condense_windows(a.rowptr, a.colidx, m, win)
     for row0, steps, gstep, nz0 in windows:
         w = row0 // win
@@ -270,15 +271,15 @@ def test_mfma_window_plan_decodes_to_the_csr(m, k, n, p, flags):
     assert len(S.plan_mfma_windows(a, 100, flags=S.TCA_PLAN_FORCE_MFMA)[0]) == 0  # N % 8 != 0
 
 
-@pytest.mark.parametrize("kernel", [0, S.TCA_PLAN_MFMA_REGS], ids=["128x64", "regs"])
+@pytest.mark.parametrize("kernel", [0, S.TCA_PLAN_MFMA_PAIR], ids=["default", "pair"])
 def test_mfma_default_routing_follows_the_cost_model(kernel):
-    """Default routing, for both tile shapes (128-row windows of the paired and
-    LDS-DMA kernels, 64-row windows of the register-staged one): the lognormal 4096 x 4096 layer
+    """Default routing of 128-row windows (whatever tile kernel then takes
+    them): the lognormal 4096 x 4096 layer
     (config 1) goes to the tile kernel, the small 2048 x 512 Bernoulli layer
     (config 0) stays on the row kernel (too few steps and workgroups to
     amortise the pipeline fill), and a very sparse matrix (density below
     0.04) stays on the row kernel."""
-    win = 64 if kernel else 128
+    win = 128
     a1, n1, _ = S.gen_config(1, seed=1)
     w1 = S.plan_mfma_windows(a1, n1, flags=kernel)[0]
     assert len(w1) == (a1.nrow + win - 1) // win
