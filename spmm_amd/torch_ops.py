@@ -3,8 +3,14 @@
     sm = SparseMatrix(a)                 # structure of A (host CSR), planned lazily per width
     c = spmm(sm, values, b)              # C = A * B, fp32, differentiable in values and B
 
-Forward runs the library's planned SpMM (tca_spmm_run) on the current torch
-stream.  Backward:
+The operator is registered with torch.library as torch.ops.spmm_amd.spmm
+(schema: spmm(int handle, Tensor values, Tensor b) -> Tensor), with a fake
+kernel (output shape and dtype only, for torch.compile and meta tracing)
+and its autograd formula registered through register_autograd; `handle`
+names a SparseMatrix (its structure and plans stay on the Python side, so
+the op's arguments are plain ints and tensors).  Forward runs the library's
+planned SpMM (tca_spmm_run) on the current torch stream.  Backward, through
+the two companion ops spmm_amd::spmm_t and spmm_amd::sddmm:
     dB      = A^T * dC     -- an SpMM with a plan of the transpose (fp32; A's
                               values reordered on the device by tca_gather_values),
     dvalues = SDDMM(dC, B) -- <dC[row(j), :], B[col(j), :]> per nonzero (tca_sddmm).
@@ -14,25 +20,39 @@ our_spmm_balanced (src/our_spmm.cuh:4) is forward-only; this is the operator
 a GCN / GraphSAGE aggregation (C = A * X with A the normalised adjacency)
 calls, forward and backward.
 
+A plan owns device scratch that every run rewrites (packed MFMA entries,
+partial rows of split rows), so one plan cannot serve two streams at once:
+running a SparseMatrix's plan on a stream while its previous run on another
+stream has not completed raises RuntimeError instead of racing.
+
 Errors follow the library: TcaError with the library's message.  There is no
 CPU fallback: the op needs the HIP library and a GPU.
 """
 from __future__ import annotations
 
 import ctypes
+import itertools
 
 import numpy as np
 import torch
 
 from . import (CSR, TCA_BF16, TCA_F16, TCA_F32, TCA_PLAN_DEFAULT, Plan, _addr, call, np_ptr)
 
-__all__ = ["SparseMatrix", "spmm", "GCNConv", "SAGEMeanConv", "TORCH_DTYPES"]
+__all__ = ["SparseMatrix", "spmm", "GCNConv", "SAGEMeanConv", "TORCH_DTYPES", "lookup"]
 
 TORCH_DTYPES = {torch.float16: TCA_F16, torch.bfloat16: TCA_BF16, torch.float32: TCA_F32}
 
 
-def _stream() -> int:
-    return torch.cuda.current_stream().cuda_stream
+# SparseMatrix objects by handle (the int the registered ops take)
+_REGISTRY: dict = {}
+_HANDLES = itertools.count(1)
+
+
+def lookup(handle: int) -> "SparseMatrix":
+    sm = _REGISTRY.get(int(handle))
+    if sm is None:
+        raise ValueError(f"spmm_amd: no open SparseMatrix with handle {handle}")
+    return sm
 
 
 class SparseMatrix:
@@ -60,6 +80,9 @@ class SparseMatrix:
         self.perm = torch.from_numpy(perm[:a.nnz].copy()).to(self.device)
         self._plans: dict = {}
         self._plans_t: dict = {}
+        self._inflight: dict = {}  # plan key -> (stream handle, event after its last run)
+        self.handle = next(_HANDLES)
+        _REGISTRY[self.handle] = self
 
     def plan(self, n: int) -> Plan:
         if n not in self._plans:
@@ -79,11 +102,39 @@ class SparseMatrix:
             v = v.view(torch.bfloat16)
         return v.to(self.device)
 
+    def guarded(self, key, device) -> "_Guard":
+        """Context for one run of the plan `key` on the current stream of
+        `device`: raises RuntimeError if the plan's previous run was on
+        another stream and has not completed; records its completion after."""
+        return _Guard(self, key, torch.cuda.current_stream(device))
+
     def close(self) -> None:
         for p in list(self._plans.values()) + list(self._plans_t.values()):
             p.close()
         self._plans.clear()
         self._plans_t.clear()
+        self._inflight.clear()
+        _REGISTRY.pop(self.handle, None)
+
+
+class _Guard:
+    def __init__(self, sm: SparseMatrix, key, stream: torch.cuda.Stream):
+        self.sm, self.key, self.stream = sm, key, stream
+
+    def __enter__(self) -> int:
+        prev = self.sm._inflight.get(self.key)
+        if prev is not None and prev[0] != self.stream.cuda_stream and not prev[1].query():
+            raise RuntimeError(f"spmm_amd: the plan {self.key} of SparseMatrix {self.sm.handle} is still running on "
+                               f"another stream; a plan's scratch serves one run at a time (synchronise that stream, "
+                               f"or use one SparseMatrix per stream)")
+        return self.stream.cuda_stream
+
+    def __exit__(self, exc_type, exc, tb) -> None:
+        if exc_type is None:
+            prev = self.sm._inflight.get(self.key)
+            ev = prev[1] if prev is not None else torch.cuda.Event()
+            ev.record(self.stream)
+            self.sm._inflight[self.key] = (self.stream.cuda_stream, ev)
 
 
 def _check(sm: SparseMatrix, values: torch.Tensor, b: torch.Tensor):
@@ -97,43 +148,91 @@ def _check(sm: SparseMatrix, values: torch.Tensor, b: torch.Tensor):
         raise ValueError(f"spmm: B must be {sm.shape[1]} x N, got {tuple(b.shape)}")
 
 
-class _SpMM(torch.autograd.Function):
-    @staticmethod
-    def forward(ctx, values, b, sm):
-        _check(sm, values, b)
-        values = values.contiguous()
-        b = b.contiguous()
-        n = b.shape[1]
-        c = torch.empty((sm.shape[0], n), dtype=torch.float32, device=b.device)
-        sm.plan(n).run(values, b, c, stream=_stream())
-        ctx.sm = sm
-        ctx.save_for_backward(values, b)
-        return c
+@torch.library.custom_op("spmm_amd::spmm", mutates_args=())
+def _spmm_op(handle: int, values: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """C = A * B in fp32, A = the structure of SparseMatrix `handle` with `values`."""
+    sm = lookup(handle)
+    _check(sm, values, b)
+    values = values.contiguous()
+    b = b.contiguous()
+    n = b.shape[1]
+    c = torch.empty((sm.shape[0], n), dtype=torch.float32, device=b.device)
+    with sm.guarded(("A", n), b.device) as stream:
+        sm.plan(n).run(values, b, c, stream=stream)
+    return c
 
-    @staticmethod
-    def backward(ctx, gc):
-        sm = ctx.sm
-        values, b = ctx.saved_tensors
-        gc = gc.contiguous().to(torch.float32)
-        n = b.shape[1]
-        grad_values = grad_b = None
-        if ctx.needs_input_grad[1]:
-            vt = torch.empty(sm.nnz, dtype=torch.float32, device=b.device)
-            call("tca_gather_values", _addr(sm.perm), sm.nnz, _addr(values), sm.dtype, _addr(vt), _stream())
-            gb = torch.empty((sm.shape[1], n), dtype=torch.float32, device=b.device)
-            sm.plan_t(n).run(vt, gc, gb, stream=_stream())
-            grad_b = gb.to(b.dtype)
-        if ctx.needs_input_grad[0]:
-            gv = torch.empty(sm.nnz, dtype=torch.float32, device=b.device)
-            call("tca_sddmm", sm.plan(n)._p, _addr(gc), _addr(b), _addr(gv), _stream())
-            grad_values = gv.to(values.dtype)
-        return grad_values, grad_b, None
+
+@_spmm_op.register_fake
+def _spmm_fake(handle: int, values: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    sm = lookup(handle)
+    return b.new_empty((sm.shape[0], b.shape[1]), dtype=torch.float32)
+
+
+@torch.library.custom_op("spmm_amd::spmm_t", mutates_args=())
+def _spmm_t_op(handle: int, values: torch.Tensor, g: torch.Tensor) -> torch.Tensor:
+    """A^T * G in fp32 (G fp32, M x N): A's values reordered to the
+    transpose's order on the device (tca_gather_values), then the planned
+    SpMM of the transpose structure."""
+    sm = lookup(handle)
+    g = g.contiguous()
+    n = g.shape[1]
+    vt = torch.empty(sm.nnz, dtype=torch.float32, device=g.device)
+    out = torch.empty((sm.shape[1], n), dtype=torch.float32, device=g.device)
+    with sm.guarded(("AT", n), g.device) as stream:
+        call("tca_gather_values", _addr(sm.perm), sm.nnz, _addr(values.contiguous()), sm.dtype, _addr(vt), stream)
+        sm.plan_t(n).run(vt, g, out, stream=stream)
+    return out
+
+
+@_spmm_t_op.register_fake
+def _spmm_t_fake(handle: int, values: torch.Tensor, g: torch.Tensor) -> torch.Tensor:
+    sm = lookup(handle)
+    return g.new_empty((sm.shape[1], g.shape[1]), dtype=torch.float32)
+
+
+@torch.library.custom_op("spmm_amd::sddmm", mutates_args=())
+def _sddmm_op(handle: int, g: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """Per nonzero j of A: <G[row(j), :], B[col(j), :]> in fp32 (tca_sddmm)."""
+    sm = lookup(handle)
+    g = g.contiguous()
+    b = b.contiguous()
+    n = b.shape[1]
+    gv = torch.empty(sm.nnz, dtype=torch.float32, device=b.device)
+    with sm.guarded(("A", n), b.device) as stream:
+        call("tca_sddmm", sm.plan(n)._p, _addr(g), _addr(b), _addr(gv), stream)
+    return gv
+
+
+@_sddmm_op.register_fake
+def _sddmm_fake(handle: int, g: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    sm = lookup(handle)
+    return b.new_empty((sm.nnz,), dtype=torch.float32)
+
+
+def _spmm_setup(ctx, inputs, output) -> None:
+    handle, values, b = inputs
+    ctx.handle = handle
+    ctx.save_for_backward(values, b)
+
+
+def _spmm_backward(ctx, gc):
+    values, b = ctx.saved_tensors
+    gc = gc.contiguous().to(torch.float32)
+    grad_values = grad_b = None
+    if ctx.needs_input_grad[1]:
+        grad_values = torch.ops.spmm_amd.sddmm(ctx.handle, gc, b).to(values.dtype)
+    if ctx.needs_input_grad[2]:
+        grad_b = torch.ops.spmm_amd.spmm_t(ctx.handle, values, gc).to(b.dtype)
+    return None, grad_values, grad_b
+
+
+_spmm_op.register_autograd(_spmm_backward, setup_context=_spmm_setup)
 
 
 def spmm(sm: SparseMatrix, values: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     """C = A * B (fp32 result) with A's structure from `sm` and its values
-    `values`; differentiable in `values` and `b`."""
-    return _SpMM.apply(values, b, sm)
+    `values`; differentiable in `values` and `b` (torch.ops.spmm_amd.spmm)."""
+    return torch.ops.spmm_amd.spmm(sm.handle, values, b)
 
 
 class GCNConv(torch.nn.Module):
