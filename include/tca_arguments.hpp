@@ -1,4 +1,7 @@
-// arg_parse.hpp -- command-line flags of the ./test harness.
+// tca_arguments.hpp -- the Arguments class: command-line flags of the ./test
+// harness, and the options the reference-signature readers of tca_compat.hpp
+// take (mtx_input_to_CSR, mtx_input_to_Dense, smtx_input_to_CSR read
+// pattern_only and input_is_zero_based).
 //
 // Same getopt letters, defaults and meanings as the reference's Arguments
 // class (src/arg_parse.h:15-161), which its main() never instantiated; here
@@ -11,7 +14,11 @@
 //   * the matrix file may also be given as the first positional argument
 //     (the reference's "./test {matrix.smtx}" usage, src/test.cu:38-43);
 //   * -f stores the full name (the reference under-allocates by one byte,
-//     src/arg_parse.h:79); -r sets the seed of B; -j prints a JSON summary.
+//     src/arg_parse.h:79) in a std::string; -r sets the seed of B; -j prints
+//     a JSON summary;
+//   * the constructor does not print; print() gives the reference's summary;
+//   * a default-constructed Arguments holds the defaults (for callers of the
+//     readers that build their options in code).
 #pragma once
 
 #include <unistd.h>
@@ -20,7 +27,7 @@
 #include <cstdlib>
 #include <string>
 
-#include "../../../include/tca_spmm.h"
+#include "tca_spmm.h"
 
 class Arguments {
   public:
@@ -40,7 +47,29 @@ class Arguments {
     bool json = false;
     bool n_given = false;
 
+    Arguments() = default;
     Arguments(int argc, char* argv[]) { ParseArgs(argc, argv); }
+
+    // The reference's summary of the options (src/arg_parse.h:130-158).
+    void print() const {
+        static const char* names[] = {"FP16", "FP32", "BF16"};
+        const char* ab = names[dtype == TCA_F32 ? 1 : dtype == TCA_BF16 ? 2 : 0];
+        std::printf("===================== Arguments ==========================\n");
+        std::printf("Tolerance : %f\n", tolerance);
+        std::printf("A type : %s, B type : %s, C type : %s\n", ab, ab, "FP32");
+        std::printf("N iter : %d\n", num_iter);
+        std::printf("Ell block size : %d \n", ell_block_size);
+        if (!input_file_exists) {
+            std::printf("No input file have been passed ... generate synthetic with random entries\n");
+            std::printf("The matrix size .. M: %d , N: %d, K: %d\n", M, N, K);
+            std::printf("Target Sparsity : %f\n", target_sparsity);
+        } else {
+            std::printf("Input file name : %s\n", input_fname.c_str());
+            if (pattern_only) std::printf("Matrix is specified as pattern only matrix\n");
+            if (!input_is_zero_based) std::printf("Input matrix is specified as one based index matrix\n");
+        }
+        std::printf("================== End of Arguments ======================\n");
+    }
 
     static void usage(const char* prog) {
         std::printf(

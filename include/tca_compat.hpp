@@ -13,9 +13,11 @@
 //   convert_csr_to_dense  src/miscalleneous.cu:66
 //   destroy_csr           src/miscalleneous.cu:82
 //   naive_gemm            src/miscalleneous.cu:114
+//   Arguments             src/arg_parse.h:15    Arguments (tca_arguments.hpp)
 //   smtx_input_to_Dense   src/file_input.cu:135
 //   smtx_input_to_CSR     src/file_input.cu:194 (an empty stub there; implemented here)
-//   mtx_input_to_CSR      src/file_input.cu:63
+//   mtx_input_to_CSR      src/file_input.cu:63  (reference signature and CSR order)
+//   mtx_input_to_Dense    src/file_input.cu:8
 //   our_spmm_balanced     src/our_spmm.cuh:4, src/our_spmm.cu:478
 //
 // Errors: like the reference's CHECK_CUDA (src/general.cuh:8-16), these
@@ -31,6 +33,7 @@
 #include <cstring>
 #include <fstream>
 
+#include "tca_arguments.hpp"
 #include "tca_host.h"
 #include "tca_spmm.h"
 
@@ -76,7 +79,19 @@ void naive_gemm(half* A, half* B, float* C, int M, int N, int K);
 void smtx_input_to_Dense(std::ifstream& fin, half** mat, char* filename, int* nRow, int* nCol, int* nnz);
 // .smtx -> CSR directly (no dense intermediate), values 1.0.
 void smtx_input_to_CSR(std::ifstream& fin, CSR** csr_mat, const char* filename = nullptr);
-// MatrixMarket coordinate -> CSR (pattern_only: values 1.0; one based unless zero_based).
+// The reference's signature of the same (arg is not consulted: .smtx has no options).
+void smtx_input_to_CSR(std::ifstream& fin, CSR** csr_mat, Arguments* arg);
+// MatrixMarket coordinate -> CSR with the reference's signature and result
+// (src/file_input.cu:63-134): arg->pattern_only (values 1.0, else a missing
+// value is 0), arg->input_is_zero_based; rows ascending, each row's entries
+// in file order, duplicates kept (tca_mtx_read_csr_file_order).
+void mtx_input_to_CSR(std::ifstream& fin, CSR** csr_mat, Arguments* arg);
+// MatrixMarket coordinate -> dense nRow x nCol halves, reference signature
+// and result (src/file_input.cu:8-62): a value read on every line (1.0 when
+// missing), a later duplicate overwriting an earlier one; the dimensions are
+// not returned (as in the reference).
+void mtx_input_to_Dense(std::ifstream& fin, half** mat, Arguments* arg);
+// From a path: CSR sorted by (row, col), duplicates rejected (tca_mtx_read_csr).
 void mtx_input_to_CSR(const char* filename, CSR** csr_mat, bool pattern_only, bool zero_based);
 
 // C = A * B on the GPU for host pointers; *elapsed = mean ms of n_iter

@@ -93,12 +93,31 @@ int tca_smtx_read_csr_values(const char* smtx_path, const char* values_path, int
 
 /* ---- MatrixMarket coordinate files (reference src/file_input.cu:8-134) ----
  * '%' lines are skipped, then "rows cols nnz", then one "r c [v]" per line.
- * pattern_only: values are 1.0; zero_based == 0: indices are one based.
- * Entries are sorted by (row, col); duplicate (row, col) pairs are rejected
- * (the reference keeps file order and does not check; unsorted columns would
- * break the CSR contract of tca_spmm). */
+ * pattern_only: values are 1.0 (only "r c" is read); otherwise a missing
+ * value reads as 0, as in the reference.  zero_based == 0: indices are one
+ * based.  Values are parsed like the reference's `stream >> float` (the
+ * decimal rounded once to fp32), then converted to dtype (RNE).  Blank lines
+ * are skipped; entries out of range and an entry count other than the
+ * header's give TCA_ERR_FORMAT (the reference asserts the count).
+ *
+ * tca_mtx_read_csr: entries sorted by (row, col), duplicate (row, col) pairs
+ * rejected -- the CSR contract of tca_spmm_plan_create. */
 int tca_mtx_read_csr(const char* path, int32_t pattern_only, int32_t zero_based, int32_t dtype,
                      tca_csr* out);
+/* The reference's CSR exactly (mtx_input_to_CSR, src/file_input.cu:63-134):
+ * rows ascending, each row's entries in file order, duplicates kept.  For
+ * files sorted column-major or row-major (MatrixMarket's usual orders) the
+ * columns of each row ascend and the result is a valid tca_spmm input;
+ * otherwise tca_spmm_plan_create rejects it (columns not ascending). */
+int tca_mtx_read_csr_file_order(const char* path, int32_t pattern_only, int32_t zero_based, int32_t dtype,
+                                tca_csr* out);
+/* The reference's dense reader (mtx_input_to_Dense, src/file_input.cu:8-62):
+ * a value is read on every line (1.0 when missing, whatever pattern_only),
+ * nRow x nCol row-major elements of dtype (release with tca_free),
+ * zero except at the entries, a later duplicate overwriting an earlier one;
+ * *nnz = entries read. */
+int tca_mtx_read_dense(const char* path, int32_t zero_based, int32_t dtype, void** dense, int32_t* nRow,
+                       int32_t* nCol, int32_t* nnz);
 
 /* ---- format conversion (reference src/miscalleneous.cu:29-81) ---- */
 /* Keeps entries whose fp32 value != 0 (so +-0 are dropped), row-major. */

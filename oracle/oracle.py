@@ -23,6 +23,13 @@ Each function names the reference lines it restates.  How each is pinned
   closed form), closed forms (identity, permutation, all-ones rows), scipy
   fixtures and dense brute force.
 * ``compare_mat``      -- hand-built cases for each branch of the verdict.
+* ``parse_mtx`` / ``mtx_to_csr_file_order`` / ``mtx_to_dense`` -- the
+  entries against scipy.io.mmread (an independent MatrixMarket parser that
+  keeps file order) on shuffled files with values; the CSR and the dense
+  matrix against scipy's dense form for unique entries; hand-built known
+  answers for what scipy does not fix (each row's entries in file order,
+  duplicates kept in the CSR, the last duplicate winning in the dense form,
+  a missing value read as 0 / 1, one-based indices).
 * ``dense_to_bell`` / ``bell_to_dense`` -- the round trip
   ``bell_to_dense(dense_to_bell(D)) == D`` (padded), hand-built cases (a
   block row with no blocks, zero-valued entries, ragged M and K), and the
@@ -336,3 +343,67 @@ def compare_mat(gold, cmp, tol: float = 1e-3):
     ok = lib.oracle_compare_mat(_ptr(g, ctypes.c_float), _ptr(c, ctypes.c_float), g.size, tol,
                                 ctypes.byref(fc), ctypes.byref(ff), ctypes.byref(mr))
     return bool(ok), fc.value, ff.value, mr.value
+
+
+# ------------------------------------------------ MatrixMarket coordinate
+def _strtof(tok: str) -> np.float32:
+    """A decimal rounded once to fp32, like the reference's `stream >> float`."""
+    libc = ctypes.CDLL(None)
+    libc.strtof.restype = ctypes.c_float
+    libc.strtof.argtypes = [ctypes.c_char_p, ctypes.POINTER(ctypes.c_char_p)]
+    return np.float32(libc.strtof(tok.encode(), None))
+
+
+def parse_mtx(text: str, zero_based: bool, read_value: bool, missing: float):
+    """(rows, cols, [(r, c, v), ...] in file order) of a MatrixMarket
+    coordinate text, as the reference reads it (src/file_input.cu:63-112):
+    '%' lines skipped, "rows cols nnz", then "r c [v]" per line, indices
+    shifted down by one unless zero based, v = `missing` when absent (and
+    not read at all unless read_value)."""
+    lines = text.splitlines()
+    i = 0
+    while lines[i].startswith("%"):
+        i += 1
+    rows, cols, nnz = (int(t) for t in lines[i].split()[:3])
+    ents = []
+    for line in lines[i + 1:]:
+        tok = line.split()
+        if not tok or tok[0].startswith("%"):
+            continue
+        r, c = int(tok[0]), int(tok[1])
+        v = _strtof(tok[2]) if read_value and len(tok) > 2 else np.float32(missing)
+        if not zero_based:
+            r, c = r - 1, c - 1
+        ents.append((r, c, v))
+    assert len(ents) == nnz
+    return rows, cols, ents
+
+
+def mtx_to_csr_file_order(text: str, pattern_only: bool, zero_based: bool):
+    """The reference's mtx_input_to_CSR (src/file_input.cu:63-134): rows in
+    ascending order, each row's entries in file order, duplicates kept;
+    pattern_only: value 1, else a missing value is 0.  Returns (nrow, ncol,
+    rowptr, colidx, values fp32)."""
+    rows, cols, ents = parse_mtx(text, zero_based, not pattern_only, 1.0 if pattern_only else 0.0)
+    per_row = [[] for _ in range(rows)]
+    for r, c, v in ents:
+        per_row[r].append((c, v))
+    rowptr = np.zeros(rows + 1, np.int32)
+    colidx, vals = [], []
+    for r in range(rows):
+        rowptr[r + 1] = rowptr[r] + len(per_row[r])
+        for c, v in per_row[r]:
+            colidx.append(c)
+            vals.append(v)
+    return rows, cols, rowptr, np.array(colidx, np.int32), np.array(vals, np.float32)
+
+
+def mtx_to_dense(text: str, zero_based: bool) -> np.ndarray:
+    """The reference's mtx_input_to_Dense (src/file_input.cu:8-62): a value
+    read on every line (1 when missing), entries written in file order (a
+    later duplicate overwrites an earlier one).  fp32 result."""
+    rows, cols, ents = parse_mtx(text, zero_based, True, 1.0)
+    d = np.zeros((rows, cols), np.float32)
+    for r, c, v in ents:
+        d[r, c] = v
+    return d

@@ -25,7 +25,7 @@ from ._lib import (TCA_BF16, TCA_F16, TCA_F32, TCA_PLAN_DEFAULT, TCA_PLAN_FORCE_
                    call, lib, np_ptr)
 
 __all__ = ["CSR", "Plan", "TcaError", "TCA_F16", "TCA_F32", "TCA_BF16", "TCA_PLAN_DEFAULT", "TCA_PLAN_NO_MFMA", "TCA_PLAN_NO_PANELS", "TCA_PLAN_FORCE_PANELS", "TCA_PLAN_NO_SCRATCH",
-           "TCA_PLAN_FORCE_MFMA", "TCA_PLAN_MFMA_DENSE", "TCA_PLAN_MFMA_PAIR", "TCA_PLAN_MFMA_COMPACT", "TCA_PLAN_KNOWN_FLAGS", "TCA_TILES_NONE", "TCA_TILES_PAIR", "TCA_TILES_DENSE", "TCA_TILES_DENSE_K", "TCA_TILES_COMPACT", "read_smtx", "read_smtx_dense", "write_smtx", "read_mtx", "write_values", "write_csr_binary",
+           "TCA_PLAN_FORCE_MFMA", "TCA_PLAN_MFMA_DENSE", "TCA_PLAN_MFMA_PAIR", "TCA_PLAN_MFMA_COMPACT", "TCA_PLAN_KNOWN_FLAGS", "TCA_TILES_NONE", "TCA_TILES_PAIR", "TCA_TILES_DENSE", "TCA_TILES_DENSE_K", "TCA_TILES_COMPACT", "read_smtx", "read_smtx_dense", "write_smtx", "read_mtx", "read_mtx_dense", "write_values", "write_csr_binary",
            "read_csr_binary", "launch_floor", "dense_to_csr", "csr_to_bell", "bell_spmm", "prune_24", "csr_to_24", "spmm_24",
            "csr_to_dense", "compare_mat", "gen_config", "gen_dense", "gen_bernoulli", "gen_lognormal_rows",
            "gen_rmat", "gen_zipf_rows", "naive_csr_spmm", "plan_row_tasks", "plan_mfma_windows", "our_spmm_balanced", "condense_windows", "np_dtype",
@@ -157,10 +157,33 @@ def write_smtx(path: str, a: CSR) -> None:
     call("tca_smtx_write", path.encode(), ctypes.byref(s))
 
 
-def read_mtx(path: str, pattern_only: bool = False, zero_based: bool = False, dtype: int = TCA_F16) -> CSR:
+def read_mtx(path: str, pattern_only: bool = False, zero_based: bool = False, dtype: int = TCA_F16,
+             file_order: bool = False) -> CSR:
+    """MatrixMarket coordinate file -> CSR.  Default: entries sorted by
+    (row, col), duplicates rejected (tca_mtx_read_csr).  file_order: the
+    reference's CSR -- rows ascending, each row's entries in file order,
+    duplicates kept (tca_mtx_read_csr_file_order, reference
+    src/file_input.cu:63-134)."""
     s = _lib.TcaCsr()
-    call("tca_mtx_read_csr", path.encode(), int(pattern_only), int(zero_based), dtype, ctypes.byref(s))
+    fn = "tca_mtx_read_csr_file_order" if file_order else "tca_mtx_read_csr"
+    call(fn, path.encode(), int(pattern_only), int(zero_based), dtype, ctypes.byref(s))
     return CSR.from_struct(s)
+
+
+def read_mtx_dense(path: str, zero_based: bool = False, dtype: int = TCA_F16) -> np.ndarray:
+    """MatrixMarket coordinate file -> dense matrix, the reference's
+    mtx_input_to_Dense (src/file_input.cu:8-62): a value on every line (1.0
+    when missing), a later duplicate overwriting an earlier one."""
+    p = ctypes.c_void_p()
+    m, k, nnz = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
+    call("tca_mtx_read_dense", path.encode(), int(zero_based), dtype, ctypes.byref(p), ctypes.byref(m),
+         ctypes.byref(k), ctypes.byref(nnz))
+    st = _STORAGE[dtype]
+    n = m.value * k.value
+    buf = (ctypes.c_char * max(n * np.dtype(st).itemsize, 1)).from_address(p.value)
+    out = np.frombuffer(buf, dtype=st, count=n).copy().reshape(m.value, k.value)
+    lib.tca_free(p)
+    return out
 
 
 def csr_to_bell(a: CSR, bsize: int):

@@ -120,6 +120,8 @@ SIGNATURES = {
     "tca_smtx_read_dense": (i32, [ctypes.c_char_p, i32, ctypes.POINTER(vp), i32p, i32p, i32p]),
     "tca_smtx_write": (i32, [ctypes.c_char_p, ctypes.POINTER(TcaCsr)]),
     "tca_mtx_read_csr": (i32, [ctypes.c_char_p, i32, i32, i32, ctypes.POINTER(TcaCsr)]),
+    "tca_mtx_read_csr_file_order": (i32, [ctypes.c_char_p, i32, i32, i32, ctypes.POINTER(TcaCsr)]),
+    "tca_mtx_read_dense": (i32, [ctypes.c_char_p, i32, i32, ctypes.POINTER(vp), i32p, i32p, i32p]),
     "tca_csr_write_binary": (i32, [ctypes.c_char_p, ctypes.POINTER(TcaCsr)]),
     "tca_csr_read_binary": (i32, [ctypes.c_char_p, ctypes.POINTER(TcaCsr)]),
     "tca_values_write": (i32, [ctypes.c_char_p, vp, i64, i32]),

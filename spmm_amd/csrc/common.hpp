@@ -24,6 +24,14 @@ void clear_error();
 int smtx_read_csr_file(FILE* f, const char* name, int32_t dtype, tca_csr* out);
 int smtx_read_dense_file(FILE* f, const char* name, int32_t dtype, void** dense, int32_t* nRow, int32_t* nCol,
                          int32_t* nnz);
+// MatrixMarket readers over an open stream: CSR sorted by (row, col) with
+// duplicates rejected, or (file_order) the reference's CSR -- rows ascending,
+// each row's entries in file order, duplicates kept; and the reference's
+// dense reader (later duplicates overwrite earlier ones).
+int mtx_read_csr_file(FILE* f, const char* name, bool pattern_only, bool zero_based, int32_t dtype, bool file_order,
+                      tca_csr* out);
+int mtx_read_dense_file(FILE* f, const char* name, bool zero_based, int32_t dtype, void** dense, int32_t* nRow,
+                        int32_t* nCol, int32_t* nnz);
 
 // Allocates the arrays of a host CSR (malloc; tca_csr_free releases them).
 int csr_alloc(tca_csr* out, int32_t nRow, int32_t nCol, int64_t nnz, int32_t dtype);

@@ -144,6 +144,48 @@ void smtx_input_to_CSR(std::ifstream& fin, CSR** csr_mat, const char* filename) 
     *csr_mat = to_csr(&s);
 }
 
+void smtx_input_to_CSR(std::ifstream& fin, CSR** csr_mat, Arguments* arg) {
+    (void)arg;
+    smtx_input_to_CSR(fin, csr_mat, static_cast<const char*>(nullptr));
+}
+
+void mtx_input_to_CSR(std::ifstream& fin, CSR** csr_mat, Arguments* arg) {
+    if (!arg) {
+        std::fprintf(stderr, "mtx_input_to_CSR: Arguments is NULL\n");
+        std::exit(EXIT_FAILURE);
+    }
+    std::string text = slurp(fin);
+    FILE* f = fmemopen(text.empty() ? nullptr : &text[0], text.size(), "rb");
+    if (!f) {
+        std::fprintf(stderr, "mtx_input_to_CSR: cannot read input stream\n");
+        std::exit(EXIT_FAILURE);
+    }
+    tca_csr s{};
+    const int st = tca::mtx_read_csr_file(f, "<stream>", arg->pattern_only, arg->input_is_zero_based, TCA_F16, true, &s);
+    std::fclose(f);
+    check(st, "mtx_input_to_CSR");
+    *csr_mat = to_csr(&s);
+}
+
+void mtx_input_to_Dense(std::ifstream& fin, half** mat, Arguments* arg) {
+    if (!arg) {
+        std::fprintf(stderr, "mtx_input_to_Dense: Arguments is NULL\n");
+        std::exit(EXIT_FAILURE);
+    }
+    std::string text = slurp(fin);
+    FILE* f = fmemopen(text.empty() ? nullptr : &text[0], text.size(), "rb");
+    if (!f) {
+        std::fprintf(stderr, "mtx_input_to_Dense: cannot read input stream\n");
+        std::exit(EXIT_FAILURE);
+    }
+    void* d = nullptr;
+    int32_t m = 0, k = 0, z = 0;
+    const int st = tca::mtx_read_dense_file(f, "<stream>", arg->input_is_zero_based, TCA_F16, &d, &m, &k, &z);
+    std::fclose(f);
+    check(st, "mtx_input_to_Dense");
+    *mat = static_cast<half*>(d);
+}
+
 void mtx_input_to_CSR(const char* filename, CSR** csr_mat, bool pattern_only, bool zero_based) {
     tca_csr s{};
     check(tca_mtx_read_csr(filename, pattern_only, zero_based, TCA_F16, &s), "mtx_input_to_CSR");

@@ -9,6 +9,7 @@
 // mis-read silently (token counts, offsets, column range).
 #include <algorithm>
 #include <cstdlib>
+#include <cstring>
 #include <vector>
 
 #include "common.hpp"
@@ -149,6 +150,140 @@ extern "C" {
 }  // extern "C"
 
 namespace tca {
+
+// MatrixMarket coordinate entries in file order (reference
+// src/file_input.cu:8-134): '%' lines are skipped, then "rows cols nnz",
+// then one "r c [v]" per line.  A value is read like the reference's
+// `stream >> float` (strtof: the decimal rounded once to fp32); a line
+// without one keeps `missing`.  Blank lines and later '%' lines are skipped
+// (the reference would count them as entries and fail its count assert);
+// entries outside the matrix and a count different from the header's are
+// errors (the reference asserts the count, and writes out-of-range entries
+// nowhere or out of bounds).
+static int mtx_parse(FILE* f, const char* path, bool zero_based, bool read_value, float missing, int64_t* rows,
+                     int64_t* cols, std::vector<int32_t>& ri, std::vector<int32_t>& ci, std::vector<float>& vv) {
+    std::vector<char> line(1 << 16);
+    int64_t m = -1, k = -1, meta = -1;
+    while (std::fgets(line.data(), static_cast<int>(line.size()), f)) {
+        if (line[0] == '%') continue;
+        long long a, b, c;
+        if (std::sscanf(line.data(), "%lld %lld %lld", &a, &b, &c) != 3)
+            return fail(TCA_ERR_FORMAT, "%s: bad size line", path);
+        m = a; k = b; meta = c;
+        break;
+    }
+    if (m < 0 || k < 0 || meta < 0 || m > INT32_MAX - 1 || k > INT32_MAX || meta > INT32_MAX)
+        return fail(TCA_ERR_FORMAT, "%s: missing or out-of-range size line", path);
+    ri.clear(); ci.clear(); vv.clear();
+    ri.reserve(meta);
+    ci.reserve(meta);
+    vv.reserve(meta);
+    while (std::fgets(line.data(), static_cast<int>(line.size()), f)) {
+        const char* p = line.data();
+        while (*p == ' ' || *p == '\t') p++;
+        if (*p == '%' || *p == '\n' || *p == '\r' || *p == '\0') continue;
+        long long r, c;
+        float v = missing;
+        int used = 0;
+        if (std::sscanf(p, "%lld %lld%n", &r, &c, &used) != 2) return fail(TCA_ERR_FORMAT, "%s: bad entry line", path);
+        if (read_value) {
+            const char* q = p + used;
+            while (*q == ' ' || *q == '\t') q++;
+            if (*q != '\n' && *q != '\r' && *q != '\0') {
+                char* end = nullptr;
+                v = std::strtof(q, &end);
+                if (end == q) return fail(TCA_ERR_FORMAT, "%s: bad value in entry line", path);
+            }
+        }
+        if (!zero_based) { r--; c--; }
+        if (r < 0 || r >= m || c < 0 || c >= k)
+            return fail(TCA_ERR_FORMAT, "%s: entry (%lld, %lld) out of range", path, r, c);
+        ri.push_back(static_cast<int32_t>(r));
+        ci.push_back(static_cast<int32_t>(c));
+        vv.push_back(v);
+    }
+    if (static_cast<int64_t>(ri.size()) != meta)
+        return fail(TCA_ERR_FORMAT, "%s: header says %lld entries, read %zu", path, (long long)meta, ri.size());
+    *rows = m;
+    *cols = k;
+    return TCA_OK;
+}
+
+int mtx_read_csr_file(FILE* f, const char* path, bool pattern_only, bool zero_based, int32_t dtype, bool file_order,
+                      tca_csr* out) {
+    if (!f || !out || !dtype_ok(dtype)) return fail(TCA_ERR_INVALID, "mtx_read_csr_file: bad argument");
+    std::vector<int32_t> ri, ci;
+    std::vector<float> vv;
+    int64_t rows = 0, cols = 0;
+    // pattern_only: "r c" only, value 1; else a missing value reads as 0
+    // (reference src/file_input.cu:84-95)
+    int st = mtx_parse(f, path, zero_based, !pattern_only, pattern_only ? 1.0f : 0.0f, &rows, &cols, ri, ci, vv);
+    if (st) return st;
+    std::vector<uint16_t> v16;
+    const void* vals = vv.data();
+    if (dtype != TCA_F32) {
+        v16.resize(vv.size());
+        tca_convert_array(vv.data(), TCA_F32, v16.data(), dtype, static_cast<int64_t>(vv.size()));
+        vals = v16.data();
+    }
+    if (!file_order) {
+        tca_coo coo{};
+        coo.nRow = static_cast<int32_t>(rows);
+        coo.nCol = static_cast<int32_t>(cols);
+        coo.nnz = static_cast<int32_t>(ri.size());
+        coo.dtype = dtype;
+        coo.row_idx = ri.data();
+        coo.col_idx = ci.data();
+        coo.value = const_cast<void*>(vals);
+        return tca_coo_to_csr(&coo, out);
+    }
+    // The reference's CSR: rows ascending, each row's entries in file order,
+    // duplicates kept (a per-row map of vectors, src/file_input.cu:103-134)
+    // -- here a stable counting sort by row.
+    st = csr_alloc(out, static_cast<int32_t>(rows), static_cast<int32_t>(cols), static_cast<int64_t>(ri.size()), dtype);
+    if (st) return st;
+    std::vector<int64_t> next(static_cast<size_t>(rows) + 1, 0);
+    for (int32_t r : ri) next[static_cast<size_t>(r) + 1]++;
+    for (int64_t r = 0; r < rows; r++) next[r + 1] += next[r];
+    for (int64_t r = 0; r <= rows; r++) out->row_offset[r] = static_cast<int32_t>(next[r]);
+    const size_t es = dtype_size(dtype);
+    for (size_t e = 0; e < ri.size(); e++) {
+        const int64_t d = next[ri[e]]++;
+        out->col_idx[d] = ci[e];
+        std::memcpy(static_cast<char*>(out->value) + d * es, static_cast<const char*>(vals) + e * es, es);
+    }
+    return TCA_OK;
+}
+
+int mtx_read_dense_file(FILE* f, const char* path, bool zero_based, int32_t dtype, void** dense, int32_t* nRow,
+                        int32_t* nCol, int32_t* nnz) {
+    if (!f || !dense || !nRow || !nCol || !nnz || !dtype_ok(dtype))
+        return fail(TCA_ERR_INVALID, "mtx_read_dense_file: bad argument");
+    std::vector<int32_t> ri, ci;
+    std::vector<float> vv;
+    int64_t rows = 0, cols = 0;
+    // the reference's dense reader always reads a value, 1 when missing
+    // (src/file_input.cu:20-30)
+    int st = mtx_parse(f, path, zero_based, true, 1.0f, &rows, &cols, ri, ci, vv);
+    if (st) return st;
+    const size_t total = static_cast<size_t>(rows) * static_cast<size_t>(cols);
+    const size_t es = dtype_size(dtype);
+    void* d = std::calloc(total > 0 ? total : 1, es);
+    if (!d) return fail(TCA_ERR_ALLOC, "tca_mtx_read_dense: %zu elements", total);
+    // entries in file order: a later duplicate overwrites an earlier one
+    std::vector<uint16_t> v16(dtype == TCA_F32 ? 0 : vv.size());
+    if (dtype != TCA_F32) tca_convert_array(vv.data(), TCA_F32, v16.data(), dtype, static_cast<int64_t>(vv.size()));
+    for (size_t e = 0; e < ri.size(); e++) {
+        const size_t at = static_cast<size_t>(ri[e]) * static_cast<size_t>(cols) + static_cast<size_t>(ci[e]);
+        if (dtype == TCA_F32) static_cast<float*>(d)[at] = vv[e];
+        else static_cast<uint16_t*>(d)[at] = v16[e];
+    }
+    *dense = d;
+    *nRow = static_cast<int32_t>(rows);
+    *nCol = static_cast<int32_t>(cols);
+    *nnz = static_cast<int32_t>(ri.size());
+    return TCA_OK;
+}
 
 int smtx_read_csr_file(FILE* f, const char* path, int32_t dtype, tca_csr* out) {
     if (!f || !out || !dtype_ok(dtype)) return fail(TCA_ERR_INVALID, "smtx_read_csr_file: bad argument");
@@ -377,63 +512,30 @@ int tca_mtx_read_csr(const char* path, int32_t pattern_only, int32_t zero_based,
     if (!path || !out || !dtype_ok(dtype)) return fail(TCA_ERR_INVALID, "tca_mtx_read_csr: bad argument");
     FILE* f = std::fopen(path, "rb");
     if (!f) return fail(TCA_ERR_IO, "cannot open '%s'", path);
-    // Skip '%' comment lines, then "rows cols nnz" (reference src/file_input.cu:64-76).
-    std::vector<char> line(1 << 16);
-    int64_t rows = -1, cols = -1, meta = -1;
-    while (std::fgets(line.data(), static_cast<int>(line.size()), f)) {
-        if (line[0] == '%') continue;
-        long long a, b, c;
-        if (std::sscanf(line.data(), "%lld %lld %lld", &a, &b, &c) != 3) {
-            std::fclose(f);
-            return fail(TCA_ERR_FORMAT, "%s: bad size line", path);
-        }
-        rows = a; cols = b; meta = c;
-        break;
-    }
-    if (rows < 0 || cols < 0 || meta < 0 || rows > INT32_MAX - 1 || cols > INT32_MAX || meta > INT32_MAX) {
-        std::fclose(f);
-        return fail(TCA_ERR_FORMAT, "%s: missing or out-of-range size line", path);
-    }
-    tca_coo coo{};
-    coo.nRow = static_cast<int32_t>(rows);
-    coo.nCol = static_cast<int32_t>(cols);
-    coo.dtype = dtype;
-    std::vector<int32_t> ri, ci;
-    std::vector<float> vv;
-    ri.reserve(meta);
-    ci.reserve(meta);
-    vv.reserve(meta);
-    while (std::fgets(line.data(), static_cast<int>(line.size()), f)) {
-        if (line[0] == '%' || line[0] == '\n' || line[0] == '\r') continue;
-        long long r, c;
-        double v = pattern_only ? 1.0 : 0.0;  // reference: v = 0 when a value is missing
-        const int got = std::sscanf(line.data(), "%lld %lld %lf", &r, &c, &v);
-        if (got < 2) { std::fclose(f); return fail(TCA_ERR_FORMAT, "%s: bad entry line", path); }
-        if (pattern_only) v = 1.0;
-        if (!zero_based) { r--; c--; }
-        if (r < 0 || r >= rows || c < 0 || c >= cols) {
-            std::fclose(f);
-            return fail(TCA_ERR_FORMAT, "%s: entry (%lld, %lld) out of range", path, r, c);
-        }
-        ri.push_back(static_cast<int32_t>(r));
-        ci.push_back(static_cast<int32_t>(c));
-        vv.push_back(static_cast<float>(v));
-    }
+    const int st = tca::mtx_read_csr_file(f, path, pattern_only != 0, zero_based != 0, dtype, false, out);
     std::fclose(f);
-    if (static_cast<int64_t>(ri.size()) != meta)  // reference asserts the count (src/file_input.cu:114)
-        return fail(TCA_ERR_FORMAT, "%s: header says %lld entries, read %zu", path, (long long)meta, ri.size());
-    coo.nnz = static_cast<int32_t>(ri.size());
-    coo.row_idx = ri.data();
-    coo.col_idx = ci.data();
-    std::vector<uint16_t> v16;
-    if (dtype == TCA_F32) {
-        coo.value = vv.data();
-    } else {
-        v16.resize(vv.size());
-        tca_convert_array(vv.data(), TCA_F32, v16.data(), dtype, static_cast<int64_t>(vv.size()));
-        coo.value = v16.data();
-    }
-    return tca_coo_to_csr(&coo, out);
+    return st;
+}
+
+int tca_mtx_read_csr_file_order(const char* path, int32_t pattern_only, int32_t zero_based, int32_t dtype,
+                                tca_csr* out) {
+    if (!path || !out || !dtype_ok(dtype)) return fail(TCA_ERR_INVALID, "tca_mtx_read_csr_file_order: bad argument");
+    FILE* f = std::fopen(path, "rb");
+    if (!f) return fail(TCA_ERR_IO, "cannot open '%s'", path);
+    const int st = tca::mtx_read_csr_file(f, path, pattern_only != 0, zero_based != 0, dtype, true, out);
+    std::fclose(f);
+    return st;
+}
+
+int tca_mtx_read_dense(const char* path, int32_t zero_based, int32_t dtype, void** dense, int32_t* nRow,
+                       int32_t* nCol, int32_t* nnz) {
+    if (!path || !dense || !nRow || !nCol || !nnz || !dtype_ok(dtype))
+        return fail(TCA_ERR_INVALID, "tca_mtx_read_dense: bad argument");
+    FILE* f = std::fopen(path, "rb");
+    if (!f) return fail(TCA_ERR_IO, "cannot open '%s'", path);
+    const int st = tca::mtx_read_dense_file(f, path, zero_based != 0, dtype, dense, nRow, nCol, nnz);
+    std::fclose(f);
+    return st;
 }
 
 }  // extern "C"

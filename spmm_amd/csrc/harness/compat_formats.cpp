@@ -5,9 +5,18 @@
 //                           "compat formats ok" and exits 0 on success
 //   ./compat_formats dup    a duplicate COO entry: coo_to_csr must exit
 //   ./compat_formats range  an out-of-range COO entry: coo_to_csr must exit
+//   ./compat_formats mtx FILE PATTERN ZERO_BASED
+//                           mtx_input_to_CSR(ifstream&, CSR**, Arguments*):
+//                           prints "nRow nCol nnz", then the row offsets, the
+//                           column indices and the values (as floats), one
+//                           line each
+//   ./compat_formats mtxdense FILE ZERO_BASED M K
+//                           mtx_input_to_Dense(ifstream&, half**, Arguments*):
+//                           prints the M x K values row by row
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <fstream>
 #include <vector>
 
 #include "../../../include/tca_compat.hpp"
@@ -38,6 +47,35 @@ COO* make_coo(int nrow, int ncol, const std::vector<int>& r, const std::vector<i
 }  // namespace
 
 int main(int argc, char* argv[]) {
+    if (argc == 5 && std::strcmp(argv[1], "mtx") == 0) {
+        Arguments arg;
+        arg.pattern_only = std::atoi(argv[3]) != 0;
+        arg.input_is_zero_based = std::atoi(argv[4]) != 0;
+        std::ifstream fin(argv[2]);
+        CSR* a = nullptr;
+        mtx_input_to_CSR(fin, &a, &arg);
+        std::printf("%d %d %d\n", a->nRow, a->nCol, a->nnz);
+        for (int r = 0; r <= a->nRow; r++) std::printf("%d ", a->row_offset[r]);
+        std::printf("\n");
+        for (int j = 0; j < a->nnz; j++) std::printf("%d ", a->col_idx[j]);
+        std::printf("\n");
+        for (int j = 0; j < a->nnz; j++) std::printf("%.9g ", static_cast<float>(a->value[j]));
+        std::printf("\n");
+        destroy_csr(a);
+        return EXIT_SUCCESS;
+    }
+    if (argc == 6 && std::strcmp(argv[1], "mtxdense") == 0) {
+        Arguments arg;
+        arg.input_is_zero_based = std::atoi(argv[3]) != 0;
+        const int M = std::atoi(argv[4]), K = std::atoi(argv[5]);
+        std::ifstream fin(argv[2]);
+        half* d = nullptr;
+        mtx_input_to_Dense(fin, &d, &arg);
+        for (int i = 0; i < M * K; i++) std::printf("%.9g ", static_cast<float>(d[i]));
+        std::printf("\n");
+        std::free(d);
+        return EXIT_SUCCESS;
+    }
     if (argc > 1) {  // rejection cases: coo_to_csr prints and exits
         const bool dup = std::strcmp(argv[1], "dup") == 0;
         COO* a = dup ? make_coo(3, 4, {0, 2, 0}, {1, 3, 1}) : make_coo(3, 4, {0, 2}, {1, 4});

@@ -15,7 +15,7 @@
 #include <vector>
 
 #include "../../../include/tca_compat.hpp"
-#include "arg_parse.hpp"
+#include "../../../include/tca_arguments.hpp"
 
 namespace {
 

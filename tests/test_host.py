@@ -474,3 +474,81 @@ def test_compat_coo_round_trip_binary():
     for mode in ("dup", "range"):
         r = subprocess.run([exe, mode], capture_output=True, text=True, timeout=60)
         assert r.returncode != 0 and "coo_to_csr" in r.stderr, (mode, r.stdout, r.stderr)
+
+
+# ------------------------------------------- reference-order MatrixMarket
+def _random_mtx(rng, m, k, n, dup, one_based, values):
+    r = rng.integers(0, m, n)
+    c = rng.integers(0, k, n)
+    if dup:
+        r = np.concatenate([r, r[:dup]])
+        c = np.concatenate([c, c[:dup]])
+    v = np.round(rng.uniform(-8, 8, len(r)), 4)
+    off = 1 if one_based else 0
+    lines = ["%%MatrixMarket matrix coordinate real general", f"{m} {k} {len(r)}"]
+    for i in range(len(r)):
+        lines.append(f"{r[i] + off} {c[i] + off} {v[i]:g}" if values else f"{r[i] + off} {c[i] + off}")
+    return "\n".join(lines) + "\n"
+
+
+@pytest.mark.parametrize("m,k,n,dup,one_based,pattern", [(30, 40, 200, 5, True, False), (7, 300, 60, 0, False, False),
+                                                         (50, 50, 300, 20, True, True), (1, 1, 3, 2, False, False),
+                                                         (10, 10, 0, 0, True, False)])
+@pytest.mark.parametrize("dtype", [S.TCA_F32, S.TCA_F16])
+def test_mtx_file_order_reader_matches_the_reference_oracle(tmp_path, m, k, n, dup, one_based, pattern, dtype):
+    """tca_mtx_read_csr_file_order and tca_mtx_read_dense reproduce the
+    reference's mtx_input_to_CSR / mtx_input_to_Dense (oracle): shuffled
+    entries, duplicates, one- and zero-based files, pattern files."""
+    rng = np.random.default_rng(m * 31 + n)
+    text = _random_mtx(rng, m, k, n, dup, one_based, not pattern)
+    p = tmp_path / "a.mtx"
+    p.write_text(text)
+    a = S.read_mtx(str(p), pattern_only=pattern, zero_based=not one_based, dtype=dtype, file_order=True)
+    om, ok, rp, ci, vals = oracle.mtx_to_csr_file_order(text, pattern, not one_based)
+    assert (a.nrow, a.ncol) == (om, ok)
+    assert np.array_equal(a.rowptr, rp) and np.array_equal(a.colidx, ci)
+    assert np.array_equal(S.from_storage(a.values, dtype), S.from_storage(S.to_storage(vals, dtype), dtype))
+    d = S.read_mtx_dense(str(p), zero_based=not one_based, dtype=dtype)
+    want = oracle.mtx_to_dense(text, not one_based)
+    assert np.array_equal(S.from_storage(d, dtype), S.from_storage(S.to_storage(want, dtype), dtype))
+
+
+@pytest.mark.parametrize("text", ["3 4 3\n1 1 1\n2 2 2\n",        # fewer entries than the header
+                                  "3 4 1\n4 1 1\n",                # row out of range (one based)
+                                  "3 4 1\n1 5 1\n",                # column out of range
+                                  "3 4 1\n1 1 x\n",                # bad value
+                                  "3 4\n1 1 1\n",                  # bad size line
+                                  "% only a comment\n"])
+def test_mtx_file_order_reader_rejects_malformed(tmp_path, text):
+    p = tmp_path / "bad.mtx"
+    p.write_text(text)
+    for fn in (lambda: S.read_mtx(str(p), file_order=True), lambda: S.read_mtx_dense(str(p))):
+        with pytest.raises(S.TcaError) as ei:
+            fn()
+        assert ei.value.status == 6
+
+
+def test_compat_reference_signature_mtx_readers(tmp_path):
+    """mtx_input_to_CSR(ifstream&, CSR**, Arguments*) and mtx_input_to_Dense
+    (tca_compat.hpp, Arguments from tca_arguments.hpp) give the reference's
+    CSR and dense matrix (oracle), in half precision."""
+    import subprocess
+    exe = os.path.join(ROOT, "spmm_amd", "bin", "compat_formats")
+    rng = np.random.default_rng(12)
+    text = _random_mtx(rng, 12, 9, 60, 7, True, True)
+    p = tmp_path / "c.mtx"
+    p.write_text(text)
+    for pattern in (0, 1):
+        r = subprocess.run([exe, "mtx", str(p), str(pattern), "0"], capture_output=True, text=True, timeout=60)
+        assert r.returncode == 0, r.stderr
+        lines = r.stdout.splitlines()
+        m, k, rp, ci, vals = oracle.mtx_to_csr_file_order(text, bool(pattern), False)
+        assert [int(x) for x in lines[0].split()] == [m, k, len(ci)]
+        assert [int(x) for x in lines[1].split()] == rp.tolist()
+        assert [int(x) for x in lines[2].split()] == ci.tolist()
+        got = np.array([float(x) for x in lines[3].split()], np.float32)
+        assert np.array_equal(got, vals.astype(np.float16).astype(np.float32))
+    r = subprocess.run([exe, "mtxdense", str(p), "0", "12", "9"], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0, r.stderr
+    got = np.array([float(x) for x in r.stdout.split()], np.float32).reshape(12, 9)
+    assert np.array_equal(got, oracle.mtx_to_dense(text, False).astype(np.float16).astype(np.float32))

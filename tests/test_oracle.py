@@ -229,3 +229,73 @@ def test_golden_manifest_lists_fixtures():
     for name in man["files"]:
         assert os.path.exists(os.path.join(GOLDEN, name)), name
     assert os.path.basename(FIXTURE_SMTX) in man["files"]
+
+
+# ------------------------------------------------ MatrixMarket readers
+def _mm_text(rng, m, k, n, one_based=True, banner=True, dup=0, values=True):
+    r = rng.integers(0, m, n)
+    c = rng.integers(0, k, n)
+    if dup:
+        r = np.concatenate([r, r[:dup]])
+        c = np.concatenate([c, c[:dup]])
+    v = np.round(rng.uniform(-4, 4, len(r)), 3)
+    lines = ["%%MatrixMarket matrix coordinate real general"] if banner else []
+    lines += ["% comment", f"{m} {k} {len(r)}"]
+    off = 1 if one_based else 0
+    for i in range(len(r)):
+        lines.append(f"{r[i] + off} {c[i] + off} {v[i]:g}" if values else f"{r[i] + off} {c[i] + off}")
+    return "\n".join(lines) + "\n", r, c, v
+
+
+def test_parse_mtx_entries_match_scipy_mmread():
+    """The oracle's entries, in file order, equal scipy.io.mmread's (an
+    independent MatrixMarket parser that keeps file order), duplicates included."""
+    import io
+    import scipy.io
+    rng = np.random.default_rng(3)
+    for m, k, n, dup in [(20, 30, 50, 0), (5, 5, 20, 6), (1, 40, 10, 2)]:
+        text, _, _, _ = _mm_text(rng, m, k, n, dup=dup)
+        rows, cols, ents = oracle.parse_mtx(text, zero_based=False, read_value=True, missing=0.0)
+        mm = scipy.io.mmread(io.BytesIO(text.encode()))
+        assert (rows, cols) == mm.shape
+        assert [e[0] for e in ents] == mm.row.tolist() and [e[1] for e in ents] == mm.col.tolist()
+        assert np.array_equal(np.array([e[2] for e in ents], np.float32), mm.data.astype(np.float32))
+
+
+def test_mtx_oracle_csr_and_dense_match_scipy_on_unique_entries():
+    """Unique entries: the file-order CSR, scattered to dense, and the dense
+    reader both equal scipy's dense form of the file."""
+    import io
+    import scipy.io
+    rng = np.random.default_rng(4)
+    text, r, c, v = _mm_text(rng, 40, 25, 400)
+    keep = {}
+    for i in range(len(r)):
+        keep.setdefault((r[i], c[i]), i)
+    lines = text.splitlines()
+    body = [lines[3 + i] for i in sorted(keep.values())]
+    text = "\n".join(lines[:2] + [f"40 25 {len(body)}"] + body) + "\n"
+    want = scipy.io.mmread(io.BytesIO(text.encode())).toarray().astype(np.float32)
+    m, k, rp, ci, vals = oracle.mtx_to_csr_file_order(text, pattern_only=False, zero_based=False)
+    assert np.array_equal(oracle.csr_to_dense(rp, ci, vals, k), want)
+    assert np.array_equal(oracle.mtx_to_dense(text, zero_based=False), want)
+
+
+def test_mtx_oracle_known_answers():
+    """What scipy does not fix: each row's entries in file order, duplicates
+    kept by the CSR reader and the last one winning in the dense reader, a
+    missing value read as 0 (CSR) or 1 (dense, pattern), zero-based indices."""
+    text = "%c\n3 4 6\n2 3 1.5\n1 4 2\n2 1 -1\n3 2 0.25\n1 1 7\n2 3 5\n"
+    m, k, rp, ci, v = oracle.mtx_to_csr_file_order(text, pattern_only=False, zero_based=False)
+    assert (m, k) == (3, 4)
+    assert rp.tolist() == [0, 2, 5, 6]
+    assert ci.tolist() == [3, 0, 2, 0, 2, 1]
+    assert v.tolist() == [2.0, 7.0, 1.5, -1.0, 5.0, 0.25]
+    d = oracle.mtx_to_dense(text, zero_based=False)
+    assert d[1, 2] == 5.0 and d[0, 0] == 7.0 and d[2, 1] == 0.25 and np.count_nonzero(d) == 5
+    pat = "2 2 2\n0 1\n1 0 3.5\n"
+    _, _, rp, ci, v = oracle.mtx_to_csr_file_order(pat, pattern_only=True, zero_based=True)
+    assert rp.tolist() == [0, 1, 2] and ci.tolist() == [1, 0] and v.tolist() == [1.0, 1.0]
+    _, _, _, _, v = oracle.mtx_to_csr_file_order(pat, pattern_only=False, zero_based=True)
+    assert v.tolist() == [0.0, 3.5]
+    assert oracle.mtx_to_dense(pat, zero_based=True).tolist() == [[0.0, 1.0], [3.5, 0.0]]
