@@ -51,6 +51,14 @@ void tca_csr_free(tca_csr* a);
 void tca_coo_free(tca_coo* a);
 void tca_free(void* p);
 
+/* Test hook: allocation-failure injection.  After host_after further host
+ * allocations of arrays the library hands out (CSR / COO / dense results),
+ * the next one fails; after device_after further device allocations (plan
+ * creation, the host driver), the next one fails; each counter then disarms.
+ * -1 disarms a counter.  The failing call returns TCA_ERR_ALLOC and releases
+ * what it had allocated.  No counterpart in the reference. */
+int tca_debug_fail_allocs(int64_t host_after, int64_t device_after);
+
 /* Checks rowptr[0] == 0, monotone, rowptr[nRow] == nnz, 0 <= col < nCol and
  * strictly ascending columns within each row.  TCA_OK or TCA_ERR_INVALID. */
 int tca_csr_validate(const int32_t* rowptr, const int32_t* colidx, int32_t nRow, int32_t nCol,

@@ -293,15 +293,15 @@ int tca_plan_row_tasks(const int32_t* rowptr, int32_t M, int32_t K, int32_t N, i
                        int32_t* geometry);
 
 /* ---- host-only view of the MFMA window plan (no device needed) ----
- * The 64-row windows tca_spmm_plan_create routes to the MFMA tile kernel for
+ * The 128-row windows tca_spmm_plan_create routes to the MFMA tile kernel for
  * this structure, width N, dtype and flags.  Call with windows == NULL to get
  * the counts, then with windows[4*n_windows], ucols[32*n_steps],
  * eoff[n_steps+1] and entries[n_entries].  windows[i] = {first row, steps,
  * first global step, first nonzero}; global step g gathers B rows
  * ucols[32g .. 32g+31] (-1 = padding) and holds entries eoff[g] ..
- * eoff[g+1]-1, each packing the row within the window (bits 0-5), the
- * column within the step (bits 6-10) and the nonzero index minus the
- * window's first nonzero (bits 11-31). */
+ * eoff[g+1]-1, each packing the row within the window (bits 0-6), the
+ * column within the step (bits 7-11) and the nonzero index minus the
+ * window's first nonzero (bits 12-31). */
 int tca_plan_mfma_windows(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_t N, int32_t dtype,
                           uint32_t flags, int32_t* n_windows, int32_t* n_steps, int64_t* n_entries,
                           int32_t* windows, int32_t* ucols, int32_t* eoff, uint32_t* entries);

@@ -121,6 +121,7 @@ SIGNATURES = {
     "tca_smtx_write": (i32, [ctypes.c_char_p, ctypes.POINTER(TcaCsr)]),
     "tca_mtx_read_csr": (i32, [ctypes.c_char_p, i32, i32, i32, ctypes.POINTER(TcaCsr)]),
     "tca_mtx_read_csr_file_order": (i32, [ctypes.c_char_p, i32, i32, i32, ctypes.POINTER(TcaCsr)]),
+    "tca_debug_fail_allocs": (i32, [i64, i64]),
     "tca_mtx_read_dense": (i32, [ctypes.c_char_p, i32, i32, ctypes.POINTER(vp), i32p, i32p, i32p]),
     "tca_csr_write_binary": (i32, [ctypes.c_char_p, ctypes.POINTER(TcaCsr)]),
     "tca_csr_read_binary": (i32, [ctypes.c_char_p, ctypes.POINTER(TcaCsr)]),

@@ -5,6 +5,7 @@
 
 #include <cstdarg>
 #include <cstdint>
+#include <new>
 #include <cstdio>
 #include <cstring>
 #include <cmath>
@@ -32,6 +33,25 @@ int mtx_read_csr_file(FILE* f, const char* name, bool pattern_only, bool zero_ba
                       tca_csr* out);
 int mtx_read_dense_file(FILE* f, const char* name, bool zero_based, int32_t dtype, void** dense, int32_t* nRow,
                         int32_t* nCol, int32_t* nnz);
+
+// Runs the body of a C ABI entry point, turning std::bad_alloc from its
+// containers into TCA_ERR_ALLOC (exceptions must not cross the C boundary).
+template <typename F>
+int api_guard(const char* name, F&& body) {
+    try {
+        return body();
+    } catch (const std::bad_alloc&) {
+        return fail(TCA_ERR_ALLOC, "%s: out of host memory", name);
+    }
+}
+
+// The library's host allocations that outlive a call (arrays handed to the
+// caller): malloc, or calloc when `zero`.  tca_debug_fail_allocs can make
+// the n-th one fail, to test the failure paths; free() releases them.
+void* host_alloc(size_t bytes, bool zero = false);
+// Whether the next device allocation is to fail (the device side of
+// tca_debug_fail_allocs; counts one allocation per call).
+bool device_alloc_fails();
 
 // Allocates the arrays of a host CSR (malloc; tca_csr_free releases them).
 int csr_alloc(tca_csr* out, int32_t nRow, int32_t nCol, int64_t nnz, int32_t dtype);

@@ -8,6 +8,7 @@
 // unique per row, value 1.0), and it rejects input the reference would
 // mis-read silently (token counts, offsets, column range).
 #include <algorithm>
+#include <cstdint>
 #include <cstdlib>
 #include <cstring>
 #include <vector>
@@ -100,15 +101,20 @@ int parse_smtx_stream(FILE* f, const char* path, SmtxRaw* raw) {
     raw->nrow = static_cast<int32_t>(h[0]);
     raw->ncol = static_cast<int32_t>(h[1]);
     raw->nnz = static_cast<int32_t>(h[2]);
-    // Line 2: nrow + 1 row offsets.
-    raw->rowptr.resize(static_cast<size_t>(raw->nrow) + 1);
+    // Line 2: nrow + 1 row offsets.  The arrays grow with what is read (at
+    // most 2^24 entries reserved up front), so a header alone cannot make
+    // the reader allocate gigabytes.
+    constexpr size_t kReserve = size_t(1) << 24;
+    raw->rowptr.clear();
+    raw->rowptr.reserve(std::min(static_cast<size_t>(raw->nrow) + 1, kReserve));
     int64_t v;
     size_t n = 0;
     while (rd.next_int(" \t", &v, &stop)) {
         if (n > static_cast<size_t>(raw->nrow)) {
             return fail(TCA_ERR_FORMAT, "%s: more than rows+1 = %d row offsets", path, raw->nrow + 1);
         }
-        raw->rowptr[n++] = static_cast<int32_t>(v);
+        raw->rowptr.push_back(static_cast<int32_t>(v));
+        n++;
     }
     if (stop == -2 || n != static_cast<size_t>(raw->nrow) + 1) {
         return fail(TCA_ERR_FORMAT, "%s: expected %d row offsets on line 2, read %zu", path, raw->nrow + 1, n);
@@ -121,7 +127,8 @@ int parse_smtx_stream(FILE* f, const char* path, SmtxRaw* raw) {
             return fail(TCA_ERR_FORMAT, "%s: row offsets decrease at row %d", path, r);
         }
     // Remaining lines: nnz column indices.
-    raw->colidx.resize(std::max<int32_t>(raw->nnz, 0));
+    raw->colidx.clear();
+    raw->colidx.reserve(std::min(static_cast<size_t>(raw->nnz), kReserve));
     n = 0;
     for (;;) {
         if (rd.next_int(" \t", &v, &stop)) {
@@ -131,7 +138,8 @@ int parse_smtx_stream(FILE* f, const char* path, SmtxRaw* raw) {
             if (v < 0 || v >= raw->ncol) {
                     return fail(TCA_ERR_FORMAT, "%s: column index %lld out of [0, %d)", path, (long long)v, raw->ncol);
             }
-            raw->colidx[n++] = static_cast<int32_t>(v);
+            raw->colidx.push_back(static_cast<int32_t>(v));
+            n++;
             continue;
         }
         if (stop == -2) { return fail(TCA_ERR_FORMAT, "%s: bad column token", path); }
@@ -175,9 +183,12 @@ static int mtx_parse(FILE* f, const char* path, bool zero_based, bool read_value
     if (m < 0 || k < 0 || meta < 0 || m > INT32_MAX - 1 || k > INT32_MAX || meta > INT32_MAX)
         return fail(TCA_ERR_FORMAT, "%s: missing or out-of-range size line", path);
     ri.clear(); ci.clear(); vv.clear();
-    ri.reserve(meta);
-    ci.reserve(meta);
-    vv.reserve(meta);
+    // reserve at most 2^24 entries up front: a header alone cannot make the
+    // reader allocate gigabytes (the vectors grow with the entries read)
+    const size_t want = static_cast<size_t>(std::min<int64_t>(meta, int64_t(1) << 24));
+    ri.reserve(want);
+    ci.reserve(want);
+    vv.reserve(want);
     while (std::fgets(line.data(), static_cast<int>(line.size()), f)) {
         const char* p = line.data();
         while (*p == ' ' || *p == '\t') p++;
@@ -268,7 +279,7 @@ int mtx_read_dense_file(FILE* f, const char* path, bool zero_based, int32_t dtyp
     if (st) return st;
     const size_t total = static_cast<size_t>(rows) * static_cast<size_t>(cols);
     const size_t es = dtype_size(dtype);
-    void* d = std::calloc(total > 0 ? total : 1, es);
+    void* d = total <= SIZE_MAX / es ? host_alloc(total * es, true) : nullptr;
     if (!d) return fail(TCA_ERR_ALLOC, "tca_mtx_read_dense: %zu elements", total);
     // entries in file order: a later duplicate overwrites an earlier one
     std::vector<uint16_t> v16(dtype == TCA_F32 ? 0 : vv.size());
@@ -306,9 +317,9 @@ int smtx_read_csr_file(FILE* f, const char* path, int32_t dtype, tca_csr* out) {
     out->nCol = raw.ncol;
     out->nnz = w;
     out->dtype = dtype;
-    out->row_offset = static_cast<int32_t*>(std::malloc(sizeof(int32_t) * rp.size()));
-    out->col_idx = static_cast<int32_t*>(std::malloc(sizeof(int32_t) * std::max(w, 1)));
-    out->value = std::malloc(dtype_size(dtype) * std::max(w, 1));
+    out->row_offset = static_cast<int32_t*>(host_alloc(sizeof(int32_t) * rp.size()));
+    out->col_idx = static_cast<int32_t*>(host_alloc(sizeof(int32_t) * std::max(w, 1)));
+    out->value = host_alloc(dtype_size(dtype) * std::max(w, 1));
     if (!out->row_offset || !out->col_idx || !out->value) {
         tca_csr_free(out);
         return fail(TCA_ERR_ALLOC, "tca_smtx_read_csr: allocation failed");
@@ -328,7 +339,7 @@ int smtx_read_dense_file(FILE* f, const char* path, int32_t dtype, void** dense,
     if (st) return st;
     const size_t es = dtype_size(dtype);
     const size_t total = static_cast<size_t>(raw.nrow) * raw.ncol;
-    void* d = std::calloc(std::max<size_t>(total, 1), es);
+    void* d = total <= SIZE_MAX / es ? host_alloc(total * es, true) : nullptr;
     if (!d) return fail(TCA_ERR_ALLOC, "tca_smtx_read_dense: %zu elements", total);
     // 1.0 at every listed (row, col) (reference src/file_input.cu:182-191).
     for (int32_t r = 0; r < raw.nrow; r++)
@@ -346,46 +357,52 @@ int smtx_read_dense_file(FILE* f, const char* path, int32_t dtype, void** dense,
 extern "C" {
 
 int tca_smtx_read_csr(const char* path, int32_t dtype, tca_csr* out) {
-    if (!path || !out || !dtype_ok(dtype)) return fail(TCA_ERR_INVALID, "tca_smtx_read_csr: bad argument");
-    FILE* f = std::fopen(path, "rb");
-    if (!f) return fail(TCA_ERR_IO, "cannot open '%s'", path);
-    const int st = smtx_read_csr_file(f, path, dtype, out);
-    std::fclose(f);
-    return st;
+    return api_guard("tca_smtx_read_csr", [&]() -> int {
+        if (!path || !out || !dtype_ok(dtype)) return fail(TCA_ERR_INVALID, "tca_smtx_read_csr: bad argument");
+        FILE* f = std::fopen(path, "rb");
+        if (!f) return fail(TCA_ERR_IO, "cannot open '%s'", path);
+        const int st = smtx_read_csr_file(f, path, dtype, out);
+        std::fclose(f);
+        return st;
+    });
 }
 
 int tca_smtx_read_dense(const char* path, int32_t dtype, void** dense, int32_t* nRow, int32_t* nCol,
                         int32_t* nnz) {
-    if (!path || !dense || !nRow || !nCol || !nnz || !dtype_ok(dtype))
-        return fail(TCA_ERR_INVALID, "tca_smtx_read_dense: bad argument");
-    FILE* f = std::fopen(path, "rb");
-    if (!f) return fail(TCA_ERR_IO, "cannot open '%s'", path);
-    const int st = smtx_read_dense_file(f, path, dtype, dense, nRow, nCol, nnz);
-    std::fclose(f);
-    return st;
+    return api_guard("tca_smtx_read_dense", [&]() -> int {
+        if (!path || !dense || !nRow || !nCol || !nnz || !dtype_ok(dtype))
+            return fail(TCA_ERR_INVALID, "tca_smtx_read_dense: bad argument");
+        FILE* f = std::fopen(path, "rb");
+        if (!f) return fail(TCA_ERR_IO, "cannot open '%s'", path);
+        const int st = smtx_read_dense_file(f, path, dtype, dense, nRow, nCol, nnz);
+        std::fclose(f);
+        return st;
+    });
 }
 
 int tca_smtx_write(const char* path, const tca_csr* a) {
-    if (!path || !a) return fail(TCA_ERR_INVALID, "tca_smtx_write: bad argument");
-    FILE* f = std::fopen(path, "wb");
-    if (!f) return fail(TCA_ERR_IO, "cannot create '%s'", path);
-    std::vector<char> buf(1 << 22);
-    std::setvbuf(f, buf.data(), _IOFBF, buf.size());
-    std::fprintf(f, "%d, %d, %d\n", a->nRow, a->nCol, a->nnz);
-    char tmp[16];
-    for (int32_t r = 0; r <= a->nRow; r++) {
-        const int k = std::snprintf(tmp, sizeof tmp, "%d ", a->row_offset[r]);
-        std::fwrite(tmp, 1, k, f);
-    }
-    std::fputc('\n', f);
-    for (int32_t j = 0; j < a->nnz; j++) {
-        const int k = std::snprintf(tmp, sizeof tmp, "%d ", a->col_idx[j]);
-        std::fwrite(tmp, 1, k, f);
-    }
-    std::fputc('\n', f);
-    const bool ok = std::ferror(f) == 0;
-    if (std::fclose(f) != 0 || !ok) return fail(TCA_ERR_IO, "write to '%s' failed", path);
-    return TCA_OK;
+    return api_guard("tca_smtx_write", [&]() -> int {
+        if (!path || !a) return fail(TCA_ERR_INVALID, "tca_smtx_write: bad argument");
+        FILE* f = std::fopen(path, "wb");
+        if (!f) return fail(TCA_ERR_IO, "cannot create '%s'", path);
+        std::vector<char> buf(1 << 22);
+        std::setvbuf(f, buf.data(), _IOFBF, buf.size());
+        std::fprintf(f, "%d, %d, %d\n", a->nRow, a->nCol, a->nnz);
+        char tmp[16];
+        for (int32_t r = 0; r <= a->nRow; r++) {
+            const int k = std::snprintf(tmp, sizeof tmp, "%d ", a->row_offset[r]);
+            std::fwrite(tmp, 1, k, f);
+        }
+        std::fputc('\n', f);
+        for (int32_t j = 0; j < a->nnz; j++) {
+            const int k = std::snprintf(tmp, sizeof tmp, "%d ", a->col_idx[j]);
+            std::fwrite(tmp, 1, k, f);
+        }
+        std::fputc('\n', f);
+        const bool ok = std::ferror(f) == 0;
+        if (std::fclose(f) != 0 || !ok) return fail(TCA_ERR_IO, "write to '%s' failed", path);
+        return TCA_OK;
+    });
 }
 
 // ---- binary CSR cache and values sidecar (no reference counterpart) ----
@@ -417,125 +434,139 @@ int64_t file_size(FILE* f) {
 }  // namespace
 
 int tca_csr_write_binary(const char* path, const tca_csr* a) {
-    if (!path || !a || !dtype_ok(a->dtype) || a->nRow < 0 || a->nCol < 0 || a->nnz < 0)
-        return fail(TCA_ERR_INVALID, "tca_csr_write_binary: bad argument");
-    FILE* f = std::fopen(path, "wb");
-    if (!f) return fail(TCA_ERR_IO, "cannot create '%s'", path);
-    const CsrHeader h{a->nRow, a->nCol, a->nnz, a->dtype, 0};
-    bool ok = write_all(f, kCsrMagic, 8) && write_all(f, &h, sizeof h) &&
-              write_all(f, a->row_offset, sizeof(int32_t) * (static_cast<size_t>(a->nRow) + 1)) &&
-              write_all(f, a->col_idx, sizeof(int32_t) * static_cast<size_t>(a->nnz)) &&
-              write_all(f, a->value, dtype_size(a->dtype) * static_cast<size_t>(a->nnz));
-    ok = std::fclose(f) == 0 && ok;
-    return ok ? TCA_OK : fail(TCA_ERR_IO, "write to '%s' failed", path);
+    return api_guard("tca_csr_write_binary", [&]() -> int {
+        if (!path || !a || !dtype_ok(a->dtype) || a->nRow < 0 || a->nCol < 0 || a->nnz < 0)
+            return fail(TCA_ERR_INVALID, "tca_csr_write_binary: bad argument");
+        FILE* f = std::fopen(path, "wb");
+        if (!f) return fail(TCA_ERR_IO, "cannot create '%s'", path);
+        const CsrHeader h{a->nRow, a->nCol, a->nnz, a->dtype, 0};
+        bool ok = write_all(f, kCsrMagic, 8) && write_all(f, &h, sizeof h) &&
+                  write_all(f, a->row_offset, sizeof(int32_t) * (static_cast<size_t>(a->nRow) + 1)) &&
+                  write_all(f, a->col_idx, sizeof(int32_t) * static_cast<size_t>(a->nnz)) &&
+                  write_all(f, a->value, dtype_size(a->dtype) * static_cast<size_t>(a->nnz));
+        ok = std::fclose(f) == 0 && ok;
+        return ok ? TCA_OK : fail(TCA_ERR_IO, "write to '%s' failed", path);
+    });
 }
 
 int tca_csr_read_binary(const char* path, tca_csr* out) {
-    if (!path || !out) return fail(TCA_ERR_INVALID, "tca_csr_read_binary: bad argument");
-    FILE* f = std::fopen(path, "rb");
-    if (!f) return fail(TCA_ERR_IO, "cannot open '%s'", path);
-    const int64_t size = file_size(f);
-    char magic[8];
-    CsrHeader h{};
-    if (!read_all(f, magic, 8) || std::memcmp(magic, kCsrMagic, 8) != 0 || !read_all(f, &h, sizeof h)) {
+    return api_guard("tca_csr_read_binary", [&]() -> int {
+        if (!path || !out) return fail(TCA_ERR_INVALID, "tca_csr_read_binary: bad argument");
+        FILE* f = std::fopen(path, "rb");
+        if (!f) return fail(TCA_ERR_IO, "cannot open '%s'", path);
+        const int64_t size = file_size(f);
+        char magic[8];
+        CsrHeader h{};
+        if (!read_all(f, magic, 8) || std::memcmp(magic, kCsrMagic, 8) != 0 || !read_all(f, &h, sizeof h)) {
+            std::fclose(f);
+            return fail(TCA_ERR_FORMAT, "'%s' is not a binary CSR file", path);
+        }
+        if (h.nRow < 0 || h.nCol < 0 || h.nnz < 0 || h.nnz > INT32_MAX || !dtype_ok(h.dtype) ||
+            size != static_cast<int64_t>(8 + sizeof h + 4 * (static_cast<int64_t>(h.nRow) + 1) + 4 * h.nnz +
+                                         static_cast<int64_t>(dtype_size(h.dtype)) * h.nnz)) {
+            std::fclose(f);
+            return fail(TCA_ERR_FORMAT, "'%s': header (%d x %d, nnz %lld, dtype %d) does not match the file size %lld",
+                        path, h.nRow, h.nCol, (long long)h.nnz, h.dtype, (long long)size);
+        }
+        int st = csr_alloc(out, h.nRow, h.nCol, h.nnz, h.dtype);
+        if (st) {
+            std::fclose(f);
+            return st;
+        }
+        const bool ok = read_all(f, out->row_offset, sizeof(int32_t) * (static_cast<size_t>(h.nRow) + 1)) &&
+                        read_all(f, out->col_idx, sizeof(int32_t) * static_cast<size_t>(h.nnz)) &&
+                        read_all(f, out->value, dtype_size(h.dtype) * static_cast<size_t>(h.nnz));
         std::fclose(f);
-        return fail(TCA_ERR_FORMAT, "'%s' is not a binary CSR file", path);
-    }
-    if (h.nRow < 0 || h.nCol < 0 || h.nnz < 0 || h.nnz > INT32_MAX || !dtype_ok(h.dtype) ||
-        size != static_cast<int64_t>(8 + sizeof h + 4 * (static_cast<int64_t>(h.nRow) + 1) + 4 * h.nnz +
-                                     static_cast<int64_t>(dtype_size(h.dtype)) * h.nnz)) {
-        std::fclose(f);
-        return fail(TCA_ERR_FORMAT, "'%s': header (%d x %d, nnz %lld, dtype %d) does not match the file size %lld",
-                    path, h.nRow, h.nCol, (long long)h.nnz, h.dtype, (long long)size);
-    }
-    int st = csr_alloc(out, h.nRow, h.nCol, h.nnz, h.dtype);
-    if (st) {
-        std::fclose(f);
+        if (!ok) {
+            tca_csr_free(out);
+            return fail(TCA_ERR_IO, "read of '%s' failed", path);
+        }
+        st = tca_csr_validate(out->row_offset, out->col_idx, out->nRow, out->nCol, out->nnz);
+        if (st) tca_csr_free(out);
         return st;
-    }
-    const bool ok = read_all(f, out->row_offset, sizeof(int32_t) * (static_cast<size_t>(h.nRow) + 1)) &&
-                    read_all(f, out->col_idx, sizeof(int32_t) * static_cast<size_t>(h.nnz)) &&
-                    read_all(f, out->value, dtype_size(h.dtype) * static_cast<size_t>(h.nnz));
-    std::fclose(f);
-    if (!ok) {
-        tca_csr_free(out);
-        return fail(TCA_ERR_IO, "read of '%s' failed", path);
-    }
-    st = tca_csr_validate(out->row_offset, out->col_idx, out->nRow, out->nCol, out->nnz);
-    if (st) tca_csr_free(out);
-    return st;
+    });
 }
 
 int tca_values_write(const char* path, const void* values, int64_t nnz, int32_t dtype) {
-    if (!path || (nnz > 0 && !values) || nnz < 0 || !dtype_ok(dtype))
-        return fail(TCA_ERR_INVALID, "tca_values_write: bad argument");
-    FILE* f = std::fopen(path, "wb");
-    if (!f) return fail(TCA_ERR_IO, "cannot create '%s'", path);
-    const ValHeader h{nnz, dtype, 0};
-    bool ok = write_all(f, kValMagic, 8) && write_all(f, &h, sizeof h) &&
-              write_all(f, values, dtype_size(dtype) * static_cast<size_t>(nnz));
-    ok = std::fclose(f) == 0 && ok;
-    return ok ? TCA_OK : fail(TCA_ERR_IO, "write to '%s' failed", path);
+    return api_guard("tca_values_write", [&]() -> int {
+        if (!path || (nnz > 0 && !values) || nnz < 0 || !dtype_ok(dtype))
+            return fail(TCA_ERR_INVALID, "tca_values_write: bad argument");
+        FILE* f = std::fopen(path, "wb");
+        if (!f) return fail(TCA_ERR_IO, "cannot create '%s'", path);
+        const ValHeader h{nnz, dtype, 0};
+        bool ok = write_all(f, kValMagic, 8) && write_all(f, &h, sizeof h) &&
+                  write_all(f, values, dtype_size(dtype) * static_cast<size_t>(nnz));
+        ok = std::fclose(f) == 0 && ok;
+        return ok ? TCA_OK : fail(TCA_ERR_IO, "write to '%s' failed", path);
+    });
 }
 
 int tca_smtx_read_csr_values(const char* smtx_path, const char* values_path, int32_t dtype, tca_csr* out) {
-    if (!smtx_path || !values_path || !out || !dtype_ok(dtype))
-        return fail(TCA_ERR_INVALID, "tca_smtx_read_csr_values: bad argument");
-    FILE* f = std::fopen(values_path, "rb");
-    if (!f) return fail(TCA_ERR_IO, "cannot open '%s'", values_path);
-    const int64_t size = file_size(f);
-    char magic[8];
-    ValHeader h{};
-    if (!read_all(f, magic, 8) || std::memcmp(magic, kValMagic, 8) != 0 || !read_all(f, &h, sizeof h) ||
-        h.nnz < 0 || !dtype_ok(h.dtype) ||
-        size != static_cast<int64_t>(8 + sizeof h + static_cast<int64_t>(dtype_size(h.dtype)) * h.nnz)) {
+    return api_guard("tca_smtx_read_csr_values", [&]() -> int {
+        if (!smtx_path || !values_path || !out || !dtype_ok(dtype))
+            return fail(TCA_ERR_INVALID, "tca_smtx_read_csr_values: bad argument");
+        FILE* f = std::fopen(values_path, "rb");
+        if (!f) return fail(TCA_ERR_IO, "cannot open '%s'", values_path);
+        const int64_t size = file_size(f);
+        char magic[8];
+        ValHeader h{};
+        if (!read_all(f, magic, 8) || std::memcmp(magic, kValMagic, 8) != 0 || !read_all(f, &h, sizeof h) ||
+            h.nnz < 0 || !dtype_ok(h.dtype) ||
+            size != static_cast<int64_t>(8 + sizeof h + static_cast<int64_t>(dtype_size(h.dtype)) * h.nnz)) {
+            std::fclose(f);
+            return fail(TCA_ERR_FORMAT, "'%s' is not a values file of its stated size", values_path);
+        }
+        std::vector<char> vals(dtype_size(h.dtype) * static_cast<size_t>(h.nnz) + 1);
+        const bool ok = read_all(f, vals.data(), dtype_size(h.dtype) * static_cast<size_t>(h.nnz));
         std::fclose(f);
-        return fail(TCA_ERR_FORMAT, "'%s' is not a values file of its stated size", values_path);
-    }
-    std::vector<char> vals(dtype_size(h.dtype) * static_cast<size_t>(h.nnz) + 1);
-    const bool ok = read_all(f, vals.data(), dtype_size(h.dtype) * static_cast<size_t>(h.nnz));
-    std::fclose(f);
-    if (!ok) return fail(TCA_ERR_IO, "read of '%s' failed", values_path);
-    int st = tca_smtx_read_csr(smtx_path, dtype, out);
-    if (st) return st;
-    if (out->nnz != h.nnz) {
-        const int32_t got = out->nnz;
-        tca_csr_free(out);
-        return fail(TCA_ERR_FORMAT, "'%s' holds %lld values, '%s' has %d nonzeros", values_path, (long long)h.nnz,
-                    smtx_path, got);
-    }
-    tca_convert_array(vals.data(), h.dtype, out->value, dtype, h.nnz);
-    return TCA_OK;
+        if (!ok) return fail(TCA_ERR_IO, "read of '%s' failed", values_path);
+        int st = tca_smtx_read_csr(smtx_path, dtype, out);
+        if (st) return st;
+        if (out->nnz != h.nnz) {
+            const int32_t got = out->nnz;
+            tca_csr_free(out);
+            return fail(TCA_ERR_FORMAT, "'%s' holds %lld values, '%s' has %d nonzeros", values_path, (long long)h.nnz,
+                        smtx_path, got);
+        }
+        tca_convert_array(vals.data(), h.dtype, out->value, dtype, h.nnz);
+        return TCA_OK;
+    });
 }
 
 int tca_mtx_read_csr(const char* path, int32_t pattern_only, int32_t zero_based, int32_t dtype, tca_csr* out) {
-    if (!path || !out || !dtype_ok(dtype)) return fail(TCA_ERR_INVALID, "tca_mtx_read_csr: bad argument");
-    FILE* f = std::fopen(path, "rb");
-    if (!f) return fail(TCA_ERR_IO, "cannot open '%s'", path);
-    const int st = tca::mtx_read_csr_file(f, path, pattern_only != 0, zero_based != 0, dtype, false, out);
-    std::fclose(f);
-    return st;
+    return api_guard("tca_mtx_read_csr", [&]() -> int {
+        if (!path || !out || !dtype_ok(dtype)) return fail(TCA_ERR_INVALID, "tca_mtx_read_csr: bad argument");
+        FILE* f = std::fopen(path, "rb");
+        if (!f) return fail(TCA_ERR_IO, "cannot open '%s'", path);
+        const int st = tca::mtx_read_csr_file(f, path, pattern_only != 0, zero_based != 0, dtype, false, out);
+        std::fclose(f);
+        return st;
+    });
 }
 
 int tca_mtx_read_csr_file_order(const char* path, int32_t pattern_only, int32_t zero_based, int32_t dtype,
                                 tca_csr* out) {
-    if (!path || !out || !dtype_ok(dtype)) return fail(TCA_ERR_INVALID, "tca_mtx_read_csr_file_order: bad argument");
-    FILE* f = std::fopen(path, "rb");
-    if (!f) return fail(TCA_ERR_IO, "cannot open '%s'", path);
-    const int st = tca::mtx_read_csr_file(f, path, pattern_only != 0, zero_based != 0, dtype, true, out);
-    std::fclose(f);
-    return st;
+    return api_guard("tca_mtx_read_csr_file_order", [&]() -> int {
+        if (!path || !out || !dtype_ok(dtype)) return fail(TCA_ERR_INVALID, "tca_mtx_read_csr_file_order: bad argument");
+        FILE* f = std::fopen(path, "rb");
+        if (!f) return fail(TCA_ERR_IO, "cannot open '%s'", path);
+        const int st = tca::mtx_read_csr_file(f, path, pattern_only != 0, zero_based != 0, dtype, true, out);
+        std::fclose(f);
+        return st;
+    });
 }
 
 int tca_mtx_read_dense(const char* path, int32_t zero_based, int32_t dtype, void** dense, int32_t* nRow,
                        int32_t* nCol, int32_t* nnz) {
-    if (!path || !dense || !nRow || !nCol || !nnz || !dtype_ok(dtype))
-        return fail(TCA_ERR_INVALID, "tca_mtx_read_dense: bad argument");
-    FILE* f = std::fopen(path, "rb");
-    if (!f) return fail(TCA_ERR_IO, "cannot open '%s'", path);
-    const int st = tca::mtx_read_dense_file(f, path, zero_based != 0, dtype, dense, nRow, nCol, nnz);
-    std::fclose(f);
-    return st;
+    return api_guard("tca_mtx_read_dense", [&]() -> int {
+        if (!path || !dense || !nRow || !nCol || !nnz || !dtype_ok(dtype))
+            return fail(TCA_ERR_INVALID, "tca_mtx_read_dense: bad argument");
+        FILE* f = std::fopen(path, "rb");
+        if (!f) return fail(TCA_ERR_IO, "cannot open '%s'", path);
+        const int st = tca::mtx_read_dense_file(f, path, zero_based != 0, dtype, dense, nRow, nCol, nnz);
+        std::fclose(f);
+        return st;
+    });
 }
 
 }  // extern "C"

@@ -521,119 +521,127 @@ void plan_panels(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_
 
 extern "C" int tca_condense_windows(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_t nnz,
                                     int32_t win, int64_t* uoff, int32_t* ucols, int32_t* cpos) {
-    using namespace tca;
-    if (!rowptr || (nnz > 0 && !colidx) || M < 0 || win < 1 || !uoff)
-        return fail(TCA_ERR_INVALID, "tca_condense_windows: bad argument");
-    if (rowptr[M] != nnz) return fail(TCA_ERR_INVALID, "tca_condense_windows: rowptr[M] != nnz");
-    std::vector<int64_t> off;
-    std::vector<int32_t> uc, cp;
-    if (cpos) cp.resize(nnz);
-    condense(rowptr, colidx, M, win, &off, ucols ? &uc : nullptr, cpos ? &cp : nullptr);
-    std::copy(off.begin(), off.end(), uoff);
-    if (ucols) std::copy(uc.begin(), uc.end(), ucols);
-    if (cpos) std::copy(cp.begin(), cp.end(), cpos);
-    return TCA_OK;
+    return tca::api_guard("tca_condense_windows", [&]() -> int {
+        using namespace tca;
+        if (!rowptr || (nnz > 0 && !colidx) || M < 0 || win < 1 || !uoff)
+            return fail(TCA_ERR_INVALID, "tca_condense_windows: bad argument");
+        if (rowptr[M] != nnz) return fail(TCA_ERR_INVALID, "tca_condense_windows: rowptr[M] != nnz");
+        std::vector<int64_t> off;
+        std::vector<int32_t> uc, cp;
+        if (cpos) cp.resize(nnz);
+        condense(rowptr, colidx, M, win, &off, ucols ? &uc : nullptr, cpos ? &cp : nullptr);
+        std::copy(off.begin(), off.end(), uoff);
+        if (ucols) std::copy(uc.begin(), uc.end(), ucols);
+        if (cpos) std::copy(cp.begin(), cp.end(), cpos);
+        return TCA_OK;
+    });
 }
 
 extern "C" int tca_plan_row_tasks(const int32_t* rowptr, int32_t M, int32_t K, int32_t N, int32_t dtype, int32_t* n_tasks,
                                   int32_t* n_perm, int32_t* n_long, int32_t* tasks, int32_t* perm, int32_t* longrows,
                                   int32_t* geometry) {
-    using namespace tca;
-    if (!rowptr || M < 0 || K < 1 || N < 1 || !dtype_ok(dtype) || !n_tasks || !n_perm || !n_long)
-        return fail(TCA_ERR_INVALID, "tca_plan_row_tasks: bad argument");
-    RowPlan p;
-    plan_rows(rowptr, M, N, static_cast<int32_t>(dtype_size(dtype)), {}, default_slices(K, N, dtype), &p);
-    if (tasks) {
-        if (*n_tasks < static_cast<int32_t>(p.tasks.size()) || *n_perm < static_cast<int32_t>(p.perm.size()) ||
-            *n_long < static_cast<int32_t>(p.longrows.size()) || !perm || !longrows)
-            return fail(TCA_ERR_INVALID, "tca_plan_row_tasks: output buffers too small");
-        if (!p.tasks.empty()) std::copy(&p.tasks[0].x, &p.tasks[0].x + 4 * p.tasks.size(), tasks);
-        std::copy(p.perm.begin(), p.perm.end(), perm);
-        if (!p.longrows.empty()) std::copy(&p.longrows[0].x, &p.longrows[0].x + 4 * p.longrows.size(), longrows);
-    }
-    *n_tasks = static_cast<int32_t>(p.tasks.size());
-    *n_perm = static_cast<int32_t>(p.perm.size());
-    *n_long = static_cast<int32_t>(p.longrows.size());
-    if (geometry) {
-        geometry[0] = p.elems_per_lane;
-        geometry[1] = 1 << p.log_lanes;
-        geometry[2] = p.col_chunks;
-        geometry[3] = p.seg_len;
-        geometry[4] = p.chunk_lanes;
-        geometry[5] = p.row_len;
-        geometry[6] = p.wide_len;
-        geometry[7] = p.multi_max;
-    }
-    return TCA_OK;
+    return tca::api_guard("tca_plan_row_tasks", [&]() -> int {
+        using namespace tca;
+        if (!rowptr || M < 0 || K < 1 || N < 1 || !dtype_ok(dtype) || !n_tasks || !n_perm || !n_long)
+            return fail(TCA_ERR_INVALID, "tca_plan_row_tasks: bad argument");
+        RowPlan p;
+        plan_rows(rowptr, M, N, static_cast<int32_t>(dtype_size(dtype)), {}, default_slices(K, N, dtype), &p);
+        if (tasks) {
+            if (*n_tasks < static_cast<int32_t>(p.tasks.size()) || *n_perm < static_cast<int32_t>(p.perm.size()) ||
+                *n_long < static_cast<int32_t>(p.longrows.size()) || !perm || !longrows)
+                return fail(TCA_ERR_INVALID, "tca_plan_row_tasks: output buffers too small");
+            if (!p.tasks.empty()) std::copy(&p.tasks[0].x, &p.tasks[0].x + 4 * p.tasks.size(), tasks);
+            std::copy(p.perm.begin(), p.perm.end(), perm);
+            if (!p.longrows.empty()) std::copy(&p.longrows[0].x, &p.longrows[0].x + 4 * p.longrows.size(), longrows);
+        }
+        *n_tasks = static_cast<int32_t>(p.tasks.size());
+        *n_perm = static_cast<int32_t>(p.perm.size());
+        *n_long = static_cast<int32_t>(p.longrows.size());
+        if (geometry) {
+            geometry[0] = p.elems_per_lane;
+            geometry[1] = 1 << p.log_lanes;
+            geometry[2] = p.col_chunks;
+            geometry[3] = p.seg_len;
+            geometry[4] = p.chunk_lanes;
+            geometry[5] = p.row_len;
+            geometry[6] = p.wide_len;
+            geometry[7] = p.multi_max;
+        }
+        return TCA_OK;
+    });
 }
 
 extern "C" int tca_plan_mfma_windows(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_t N,
                                      int32_t dtype, uint32_t flags, int32_t* n_windows, int32_t* n_steps,
                                      int64_t* n_entries, int32_t* windows, int32_t* ucols, int32_t* eoff,
                                      uint32_t* entries) {
-    using namespace tca;
-    if (!rowptr || M < 0 || N < 1 || !dtype_ok(dtype) || !n_windows || !n_steps || !n_entries)
-        return fail(TCA_ERR_INVALID, "tca_plan_mfma_windows: bad argument");
-    MfmaPlan p;
-    const char* md = std::getenv("TCA_MFMA_MIN_DENSITY");
-    plan_mfma(rowptr, colidx, M, N, dtype, (flags & TCA_PLAN_FORCE_MFMA) != 0, (flags & TCA_PLAN_NO_MFMA) != 0,
-              md ? std::atof(md) : kMfmaMinDensity, mfma_shape(flags), &p);
-    const int32_t steps = static_cast<int32_t>(p.eoff.size()) - 1;
-    if (windows) {
-        if (*n_windows < static_cast<int32_t>(p.windows.size()) || *n_steps < steps ||
-            *n_entries < static_cast<int64_t>(p.entries.size()) || !ucols || !eoff || !entries)
-            return fail(TCA_ERR_INVALID, "tca_plan_mfma_windows: output buffers too small");
-        if (!p.windows.empty()) std::copy(&p.windows[0].x, &p.windows[0].x + 4 * p.windows.size(), windows);
-        std::copy(p.ucols.begin(), p.ucols.end(), ucols);
-        std::copy(p.eoff.begin(), p.eoff.end(), eoff);
-        std::copy(p.entries.begin(), p.entries.end(), entries);
-    }
-    *n_windows = static_cast<int32_t>(p.windows.size());
-    *n_steps = steps;
-    *n_entries = static_cast<int64_t>(p.entries.size());
-    return TCA_OK;
+    return tca::api_guard("tca_plan_mfma_windows", [&]() -> int {
+        using namespace tca;
+        if (!rowptr || M < 0 || N < 1 || !dtype_ok(dtype) || !n_windows || !n_steps || !n_entries)
+            return fail(TCA_ERR_INVALID, "tca_plan_mfma_windows: bad argument");
+        MfmaPlan p;
+        const char* md = std::getenv("TCA_MFMA_MIN_DENSITY");
+        plan_mfma(rowptr, colidx, M, N, dtype, (flags & TCA_PLAN_FORCE_MFMA) != 0, (flags & TCA_PLAN_NO_MFMA) != 0,
+                  md ? std::atof(md) : kMfmaMinDensity, mfma_shape(flags), &p);
+        const int32_t steps = static_cast<int32_t>(p.eoff.size()) - 1;
+        if (windows) {
+            if (*n_windows < static_cast<int32_t>(p.windows.size()) || *n_steps < steps ||
+                *n_entries < static_cast<int64_t>(p.entries.size()) || !ucols || !eoff || !entries)
+                return fail(TCA_ERR_INVALID, "tca_plan_mfma_windows: output buffers too small");
+            if (!p.windows.empty()) std::copy(&p.windows[0].x, &p.windows[0].x + 4 * p.windows.size(), windows);
+            std::copy(p.ucols.begin(), p.ucols.end(), ucols);
+            std::copy(p.eoff.begin(), p.eoff.end(), eoff);
+            std::copy(p.entries.begin(), p.entries.end(), entries);
+        }
+        *n_windows = static_cast<int32_t>(p.windows.size());
+        *n_steps = steps;
+        *n_entries = static_cast<int64_t>(p.entries.size());
+        return TCA_OK;
+    });
 }
 
 extern "C" int tca_plan_panels(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_t K, int32_t N,
                                int32_t dtype, uint32_t flags, int64_t* sizes, int32_t* rows, int32_t* cols,
                                uint8_t* width, uint8_t* cnt, uint8_t* pos, int32_t* units, int32_t* panel_units,
                                int32_t* ustart, int32_t* longrows) {
-    using namespace tca;
-    if (!rowptr || !colidx || M < 0 || K < 1 || N < 1 || !dtype_ok(dtype) || !sizes)
-        return fail(TCA_ERR_INVALID, "tca_plan_panels: bad argument");
-    MfmaPlan mp;
-    const char* md = std::getenv("TCA_MFMA_MIN_DENSITY");
-    plan_mfma(rowptr, colidx, M, N, dtype, (flags & TCA_PLAN_FORCE_MFMA) != 0, (flags & TCA_PLAN_NO_MFMA) != 0,
-              md ? std::atof(md) : kMfmaMinDensity, mfma_shape(flags), &mp);
-    PanelPlan p;
-    plan_panels_routed(rowptr, colidx, M, K, N, dtype, flags, mp.row_mfma, &p);
-    const int64_t stride = static_cast<int64_t>(p.waves) * kPanelCntRows * 4;
-    const int64_t sz[16] = {p.n_panels, p.n_tiles(), static_cast<int64_t>(p.units.size()),
-                            static_cast<int64_t>(p.longrows.size()), p.R, p.P, p.waves, p.rpg, p.elems, p.chunks,
-                            p.nnz, p.staged, p.n_segments, p.n_rows, stride, 0};
-    std::copy(sz, sz + 16, sizes);
-    if (!rows) return TCA_OK;
-    if (!cols || !width || !cnt || !pos || !units || !panel_units || !ustart || !longrows)
-        return fail(TCA_ERR_INVALID, "tca_plan_panels: missing output array");
-    std::copy(p.rows.begin(), p.rows.end(), rows);
-    std::copy(p.cols.begin(), p.cols.end(), cols);
-    std::copy(p.width.begin(), p.width.end(), width);
-    std::copy(p.cnt.begin(), p.cnt.end(), cnt);
-    if (!p.pos.empty()) std::copy(p.pos.begin(), p.pos.begin() + rowptr[M], pos);
-    else std::fill(pos, pos + rowptr[M], 0);
-    for (size_t u = 0; u < p.units.size(); u++) {
-        units[4 * u] = p.units[u].x;
-        units[4 * u + 1] = p.units[u].y;
-        units[4 * u + 2] = p.units[u].z;
-        units[4 * u + 3] = p.units[u].w;
-    }
-    std::copy(p.panel_units.begin(), p.panel_units.end(), panel_units);
-    std::copy(p.ustart.begin(), p.ustart.end(), ustart);
-    for (size_t u = 0; u < p.longrows.size(); u++) {
-        longrows[4 * u] = p.longrows[u].x;
-        longrows[4 * u + 1] = p.longrows[u].y;
-        longrows[4 * u + 2] = p.longrows[u].z;
-        longrows[4 * u + 3] = p.longrows[u].w;
-    }
-    return TCA_OK;
+    return tca::api_guard("tca_plan_panels", [&]() -> int {
+        using namespace tca;
+        if (!rowptr || !colidx || M < 0 || K < 1 || N < 1 || !dtype_ok(dtype) || !sizes)
+            return fail(TCA_ERR_INVALID, "tca_plan_panels: bad argument");
+        MfmaPlan mp;
+        const char* md = std::getenv("TCA_MFMA_MIN_DENSITY");
+        plan_mfma(rowptr, colidx, M, N, dtype, (flags & TCA_PLAN_FORCE_MFMA) != 0, (flags & TCA_PLAN_NO_MFMA) != 0,
+                  md ? std::atof(md) : kMfmaMinDensity, mfma_shape(flags), &mp);
+        PanelPlan p;
+        plan_panels_routed(rowptr, colidx, M, K, N, dtype, flags, mp.row_mfma, &p);
+        const int64_t stride = static_cast<int64_t>(p.waves) * kPanelCntRows * 4;
+        const int64_t sz[16] = {p.n_panels, p.n_tiles(), static_cast<int64_t>(p.units.size()),
+                                static_cast<int64_t>(p.longrows.size()), p.R, p.P, p.waves, p.rpg, p.elems, p.chunks,
+                                p.nnz, p.staged, p.n_segments, p.n_rows, stride, 0};
+        std::copy(sz, sz + 16, sizes);
+        if (!rows) return TCA_OK;
+        if (!cols || !width || !cnt || !pos || !units || !panel_units || !ustart || !longrows)
+            return fail(TCA_ERR_INVALID, "tca_plan_panels: missing output array");
+        std::copy(p.rows.begin(), p.rows.end(), rows);
+        std::copy(p.cols.begin(), p.cols.end(), cols);
+        std::copy(p.width.begin(), p.width.end(), width);
+        std::copy(p.cnt.begin(), p.cnt.end(), cnt);
+        if (!p.pos.empty()) std::copy(p.pos.begin(), p.pos.begin() + rowptr[M], pos);
+        else std::fill(pos, pos + rowptr[M], 0);
+        for (size_t u = 0; u < p.units.size(); u++) {
+            units[4 * u] = p.units[u].x;
+            units[4 * u + 1] = p.units[u].y;
+            units[4 * u + 2] = p.units[u].z;
+            units[4 * u + 3] = p.units[u].w;
+        }
+        std::copy(p.panel_units.begin(), p.panel_units.end(), panel_units);
+        std::copy(p.ustart.begin(), p.ustart.end(), ustart);
+        for (size_t u = 0; u < p.longrows.size(); u++) {
+            longrows[4 * u] = p.longrows[u].x;
+            longrows[4 * u + 1] = p.longrows[u].y;
+            longrows[4 * u + 2] = p.longrows[u].z;
+            longrows[4 * u + 3] = p.longrows[u].w;
+        }
+        return TCA_OK;
+    });
 }

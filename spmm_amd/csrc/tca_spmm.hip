@@ -121,11 +121,21 @@ int static_scratch(int dev, float** out) {
 
 __global__ void warm_up_kernel() {}
 
+// Every device allocation of the library goes through here (so
+// tca_debug_fail_allocs can make one fail).
+static hipError_t dev_malloc(void** p, size_t bytes) {
+    if (device_alloc_fails()) {
+        *p = nullptr;
+        return hipErrorOutOfMemory;
+    }
+    return hipMalloc(p, bytes);
+}
+
 template <typename T>
 int dev_upload(T** dst, const void* src, size_t count) {
     *dst = nullptr;
     if (count == 0) return TCA_OK;
-    hipError_t e = hipMalloc(reinterpret_cast<void**>(dst), sizeof(T) * count);
+    hipError_t e = dev_malloc(reinterpret_cast<void**>(dst), sizeof(T) * count);
     if (e != hipSuccess) {
         *dst = nullptr;
         return fail(TCA_ERR_ALLOC, "hipMalloc(%zu bytes): %s", sizeof(T) * count, hipGetErrorString(e));
@@ -164,6 +174,24 @@ void free_plan_device(tca_spmm_plan* p) {
     (void)hipFree(p->d_ppos);
     (void)hipFree(p->d_ustart);
 }
+
+// Owns a plan under construction: frees it (device buffers included) unless
+// released, so every early return and every exception of plan creation
+// leaves nothing behind.
+struct PlanHolder {
+    tca_spmm_plan* p;
+    ~PlanHolder() {
+        if (p) {
+            free_plan_device(p);
+            delete p;
+        }
+    }
+    tca_spmm_plan* release() {
+        tca_spmm_plan* q = p;
+        p = nullptr;
+        return q;
+    }
+};
 
 template <typename T, int E>
 void launch_rows_t(const tca_spmm_plan* p, const void* val, const void* B, float* C, float* W, hipStream_t s) {
@@ -491,596 +519,589 @@ int tca_device_count(int32_t* count) {
 
 int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_t K, int32_t nnz,
                          int32_t N, int32_t dtype, uint32_t flags, tca_spmm_plan** plan) {
-    if (!plan) return fail(TCA_ERR_INVALID, "plan is NULL");
-    *plan = nullptr;
-    if (M < 0 || K < 1 || N < 1 || nnz < 0) return fail(TCA_ERR_INVALID, "bad shape M=%d K=%d N=%d nnz=%d", M, K, N, nnz);
-    if (!dtype_ok(dtype)) return fail(TCA_ERR_INVALID, "unknown dtype %d", dtype);
-    if (flags & ~TCA_PLAN_KNOWN_FLAGS) return fail(TCA_ERR_INVALID, "unknown plan flags 0x%x", flags & ~TCA_PLAN_KNOWN_FLAGS);
-    // The kernels address B, values and column indices through 32-bit buffer
-    // offsets, with 0xfffffff0 reserved as the out-of-range marker.
-    const uint64_t b_bytes = static_cast<uint64_t>(K) * static_cast<uint64_t>(N) * dtype_size(dtype);
-    if (b_bytes >= 0xfffffff0ull || static_cast<uint64_t>(nnz) * 4 >= 0xfffffff0ull)
-        return fail(TCA_ERR_UNSUPPORTED, "B (%llu bytes) or the nonzeros exceed the 4 GiB buffer range",
-                    (unsigned long long)b_bytes);
-    int st = tca_csr_validate(rowptr, colidx, M, K, nnz);
-    if (st) return st;
-    const auto t0 = std::chrono::steady_clock::now();
-    tca_spmm_plan* p = new (std::nothrow) tca_spmm_plan();
-    if (!p) return fail(TCA_ERR_ALLOC, "plan allocation failed");
-    p->M = M;
-    p->K = K;
-    p->N = N;
-    p->nnz = nnz;
-    p->dtype = dtype;
-    p->flags = flags;
-    if (hipGetDevice(&p->device) != hipSuccess) {
-        delete p;
-        return fail(TCA_ERR_HIP, "no HIP device");
-    }
-    // Dense-enough 128-row windows go to an MFMA tile kernel (fp16 / bf16),
-    // 64 columns of C per workgroup: the paired kernel, or the dense-tile
-    // kernels (plain or compacted).  TCA_MFMA_MIN_DENSITY (tuning only)
-    // overrides the routing threshold.
-    const char* md = std::getenv("TCA_MFMA_MIN_DENSITY");
-    const MfmaShape* shape = &mfma_shape(flags);
-    const double min_density = md ? std::atof(md) : kMfmaMinDensity;
-    plan_mfma(rowptr, colidx, M, N, dtype, (flags & TCA_PLAN_FORCE_MFMA) != 0, (flags & TCA_PLAN_NO_MFMA) != 0,
-              min_density, *shape, &p->mfma);
-    p->mfma_dense = (flags & (TCA_PLAN_MFMA_DENSE | TCA_PLAN_MFMA_COMPACT)) != 0;
-    if ((flags & (TCA_PLAN_MFMA_DENSE | TCA_PLAN_MFMA_PAIR)) == 0 && !p->mfma.windows.empty() &&
-        static_cast<double>(p->mfma.cond_cols) >= kNaturalCover * static_cast<double>(p->mfma.windows.size()) * K &&
-        p->mfma.windows.size() * static_cast<size_t>((K + 31) / 32) * kDnATileBytes <= kDenseMaxBytes) {
-        // Default kernel choice: windows that cover most of K run on the dense
-        // tiles in natural column order, compacted when every step fits
-        // (measured on MI355X, config 1: 32.4 us per SpMM against 34.5 us for
-        // the plain dense tiles and
-        // 34.5 us per SpMM against 36.8 us for the paired kernel).
-        p->mfma_dense = true;
-        p->mfma_compact_want = true;
-    }
-    if (flags & TCA_PLAN_MFMA_COMPACT) p->mfma_compact_want = true;
-    if (p->mfma_dense && (p->mfma.eoff.size() - 1) * static_cast<size_t>(kDnATileBytes) > kDenseMaxBytes) {
-        // Dense windows past the budget: the paired kernel, which keeps only the entries.
-        p->mfma_dense = false;
-        shape = &kMfmaPairShape;
+    return api_guard("tca_spmm_plan_create", [&]() -> int {
+        if (!plan) return fail(TCA_ERR_INVALID, "plan is NULL");
+        *plan = nullptr;
+        if (M < 0 || K < 1 || N < 1 || nnz < 0) return fail(TCA_ERR_INVALID, "bad shape M=%d K=%d N=%d nnz=%d", M, K, N, nnz);
+        if (!dtype_ok(dtype)) return fail(TCA_ERR_INVALID, "unknown dtype %d", dtype);
+        if (flags & ~TCA_PLAN_KNOWN_FLAGS) return fail(TCA_ERR_INVALID, "unknown plan flags 0x%x", flags & ~TCA_PLAN_KNOWN_FLAGS);
+        // The kernels address B, values and column indices through 32-bit buffer
+        // offsets, with 0xfffffff0 reserved as the out-of-range marker.
+        const uint64_t b_bytes = static_cast<uint64_t>(K) * static_cast<uint64_t>(N) * dtype_size(dtype);
+        if (b_bytes >= 0xfffffff0ull || static_cast<uint64_t>(nnz) * 4 >= 0xfffffff0ull)
+            return fail(TCA_ERR_UNSUPPORTED, "B (%llu bytes) or the nonzeros exceed the 4 GiB buffer range",
+                        (unsigned long long)b_bytes);
+        int st = tca_csr_validate(rowptr, colidx, M, K, nnz);
+        if (st) return st;
+        const auto t0 = std::chrono::steady_clock::now();
+        tca_spmm_plan* p = new (std::nothrow) tca_spmm_plan();
+        if (!p) return fail(TCA_ERR_ALLOC, "plan allocation failed");
+        PlanHolder hold{p};
+        p->M = M;
+        p->K = K;
+        p->N = N;
+        p->nnz = nnz;
+        p->dtype = dtype;
+        p->flags = flags;
+        if (hipGetDevice(&p->device) != hipSuccess) return fail(TCA_ERR_HIP, "no HIP device");
+        // Dense-enough 128-row windows go to an MFMA tile kernel (fp16 / bf16),
+        // 64 columns of C per workgroup: the paired kernel, or the dense-tile
+        // kernels (plain or compacted).  TCA_MFMA_MIN_DENSITY (tuning only)
+        // overrides the routing threshold.
+        const char* md = std::getenv("TCA_MFMA_MIN_DENSITY");
+        const MfmaShape* shape = &mfma_shape(flags);
+        const double min_density = md ? std::atof(md) : kMfmaMinDensity;
         plan_mfma(rowptr, colidx, M, N, dtype, (flags & TCA_PLAN_FORCE_MFMA) != 0, (flags & TCA_PLAN_NO_MFMA) != 0,
                   min_density, *shape, &p->mfma);
-    }
-    p->mfma_pair = !p->mfma_dense;
-    p->mfma_col_blocks = (N + shape->tile_cols - 1) / shape->tile_cols;
-    {
-        int32_t most = 0;
-        for (size_t i = 0; i + 1 < p->mfma.eoff.size(); i++) most = std::max(most, p->mfma.eoff[i + 1] - p->mfma.eoff[i]);
-        p->mfma_groups = most <= 4 * kPairGroup ? 4 : 8;
-    }
-    // Row panels with B staged in LDS for the rows outside MFMA windows, then
-    // the row kernel for the rest.
-    plan_panels_routed(rowptr, colidx, M, K, N, dtype, flags, p->mfma.row_mfma, &p->panels);
-    std::vector<uint8_t> skip_rows(M, 0);
-    for (int32_t r = 0; r < M; r++)
-        skip_rows[r] = (!p->mfma.row_mfma.empty() && p->mfma.row_mfma[r]) || p->panels.row_panel[r];
-    plan_rows(rowptr, M, N, static_cast<int32_t>(dtype_size(dtype)), skip_rows, default_slices(K, N, dtype),
-              &p->rows);
-    p->ntasks = static_cast<int32_t>(p->rows.tasks.size());
-    const size_t n_seg_rows =
-        p->rows.longrows.empty() ? 0 : static_cast<size_t>(p->rows.longrows.back().y + p->rows.longrows.back().z);
-    // One partial-row array and one segment-sum table for both kernels: the
-    // panels' segments follow the row kernel's.
-    {
-        const int32_t off = static_cast<int32_t>(n_seg_rows);
-        for (Int4& u : p->panels.units)
-            if (u.w >= 0) u.w += off;
-        for (Int4 lr : p->panels.longrows) {
-            lr.y += off;
-            p->rows.longrows.push_back(lr);
+        p->mfma_dense = (flags & (TCA_PLAN_MFMA_DENSE | TCA_PLAN_MFMA_COMPACT)) != 0;
+        if ((flags & (TCA_PLAN_MFMA_DENSE | TCA_PLAN_MFMA_PAIR)) == 0 && !p->mfma.windows.empty() &&
+            static_cast<double>(p->mfma.cond_cols) >= kNaturalCover * static_cast<double>(p->mfma.windows.size()) * K &&
+            p->mfma.windows.size() * static_cast<size_t>((K + 31) / 32) * kDnATileBytes <= kDenseMaxBytes) {
+            // Default kernel choice: windows that cover most of K run on the dense
+            // tiles in natural column order, compacted when every step fits
+            // (measured on MI355X, config 1: 32.4 us per SpMM against 34.5 us for
+            // the plain dense tiles and
+            // 34.5 us per SpMM against 36.8 us for the paired kernel).
+            p->mfma_dense = true;
+            p->mfma_compact_want = true;
         }
-    }
-    const size_t n_seg_total = n_seg_rows + static_cast<size_t>(p->panels.n_segments);
-    p->n_units = static_cast<int32_t>(p->panels.units.size());
-    p->n_longrows = static_cast<int32_t>(p->rows.longrows.size());
-    p->n_seg_total = n_seg_total;
-    p->n_perm = static_cast<int32_t>(p->rows.perm.size());
-    const auto t1 = std::chrono::steady_clock::now();
-
-    auto bail = [&](int s) {
-        free_plan_device(p);
-        delete p;
-        return s;
-    };
-    if ((st = dev_upload(&p->d_rowptr, rowptr, static_cast<size_t>(M) + 1))) return bail(st);
-    if ((st = dev_upload(&p->d_colidx, colidx, static_cast<size_t>(nnz)))) return bail(st);
-    if ((st = dev_upload(&p->d_tasks, p->rows.tasks.data(), p->rows.tasks.size()))) return bail(st);
-    if ((st = dev_upload(&p->d_perm, p->rows.perm.data(), p->rows.perm.size()))) return bail(st);
-    if ((st = dev_upload(&p->d_longrows, p->rows.longrows.data(), p->rows.longrows.size()))) return bail(st);
-    if (!(flags & TCA_PLAN_NO_SCRATCH) && (st = dev_upload(&p->d_partials, nullptr, n_seg_total * N))) return bail(st);
-    if (p->n_units > 0) {
-        const PanelPlan& pp = p->panels;
-        if ((st = dev_upload(&p->d_units, pp.units.data(), pp.units.size()))) return bail(st);
-        if ((st = dev_upload(&p->d_panel_units, pp.panel_units.data(), pp.panel_units.size()))) return bail(st);
-        if ((st = dev_upload(&p->d_prows, pp.rows.data(), pp.rows.size()))) return bail(st);
+        if (flags & TCA_PLAN_MFMA_COMPACT) p->mfma_compact_want = true;
+        if (p->mfma_dense && (p->mfma.eoff.size() - 1) * static_cast<size_t>(kDnATileBytes) > kDenseMaxBytes) {
+            // Dense windows past the budget: the paired kernel, which keeps only the entries.
+            p->mfma_dense = false;
+            shape = &kMfmaPairShape;
+            plan_mfma(rowptr, colidx, M, N, dtype, (flags & TCA_PLAN_FORCE_MFMA) != 0, (flags & TCA_PLAN_NO_MFMA) != 0,
+                      min_density, *shape, &p->mfma);
+        }
+        p->mfma_pair = !p->mfma_dense;
+        p->mfma_col_blocks = (N + shape->tile_cols - 1) / shape->tile_cols;
         {
-            // staged rows as byte offsets into B (B < 4 GiB, checked above)
-            std::vector<int32_t> boff(pp.cols.size());
-            const uint32_t rb = static_cast<uint32_t>(N) * static_cast<uint32_t>(dtype_size(dtype));
-            for (size_t j = 0; j < boff.size(); j++) boff[j] = static_cast<int32_t>(static_cast<uint32_t>(pp.cols[j]) * rb);
-            if ((st = dev_upload(&p->d_pcols, boff.data(), boff.size()))) return bail(st);
+            int32_t most = 0;
+            for (size_t i = 0; i + 1 < p->mfma.eoff.size(); i++) most = std::max(most, p->mfma.eoff[i + 1] - p->mfma.eoff[i]);
+            p->mfma_groups = most <= 4 * kPairGroup ? 4 : 8;
         }
-        if ((st = dev_upload(&p->d_pwidth, pp.width.data(), pp.width.size()))) return bail(st);
-        if ((st = dev_upload(&p->d_pcnt, pp.cnt.data(), pp.cnt.size() / 4))) return bail(st);
-        if ((st = dev_upload(&p->d_ppos, pp.pos.data(), pp.pos.size()))) return bail(st);
-        p->n_pos_bytes = pp.pos.size();
-        if ((st = dev_upload(&p->d_ustart, pp.ustart.data(), pp.ustart.size()))) return bail(st);
-        // the kernel needs only the arrays on the device
-        p->panels.cols.clear(); p->panels.cols.shrink_to_fit();
-        p->panels.width.clear(); p->panels.width.shrink_to_fit();
-        p->panels.cnt.clear(); p->panels.cnt.shrink_to_fit();
-        p->panels.pos.clear(); p->panels.pos.shrink_to_fit();
-        p->panels.ustart.clear(); p->panels.ustart.shrink_to_fit();
-    }
-    if ((st = dev_upload(&p->d_windows, p->mfma.windows.data(), p->mfma.windows.size()))) return bail(st);
-    if (!p->mfma.windows.empty()) {
-        // Device forms: B row byte offsets (padding 0xffffffff; paired kernel:
-        // each step's 32 offsets permuted, word 4 r + k = column r + 8 k) and
-        // the step entry ranges.
-        std::vector<uint32_t> uoff(p->mfma.ucols.size());
-        for (size_t i = 0; i < uoff.size(); i++) {
-            const size_t src = p->mfma_pair ? (i & ~size_t(31)) + ((i & 31) >> 2) + 8 * (i & 3) : i;
-            uoff[i] = p->mfma.ucols[src] < 0 ? kNoEntry
-                                              : static_cast<uint32_t>(p->mfma.ucols[src]) * static_cast<uint32_t>(N) * 2u;
-        }
-        if ((st = dev_upload(&p->d_ucols, uoff.data(), uoff.size()))) return bail(st);
-        p->n_ucols = uoff.size();
-        if ((st = dev_upload(&p->d_eoff, p->mfma.eoff.data(), p->mfma.eoff.size()))) return bail(st);
-    }
-    if (!p->mfma.windows.empty() && p->mfma_dense) {
-        // Dense condensed windows: 8 KiB per global step (128 rows x 32
-        // condensed columns in fragment order), zero except at the entries,
-        // whose values the pack kernel writes each run; 1 KiB of zeros after
-        // them (the B source for padding rows).  Entries sorted by position.
-        // Windows whose column unions cover most of K (on average >= 85 %) keep
-        // their columns in natural order instead: every window spans all of K,
-        // step j holds columns 32 j .. 32 j + 31, so the kernel's B rows are
-        // contiguous and need no row-offset table.
-        const int32_t ksteps = (K + 31) / 32;
-        const size_t nwin = p->mfma.windows.size();
-        p->mfma_natural = static_cast<double>(p->mfma.cond_cols) >= kNaturalCover * static_cast<double>(nwin) * K &&
-                          nwin * static_cast<size_t>(ksteps) * kDnATileBytes <= kDenseMaxBytes;
-        std::vector<std::pair<uint32_t, int32_t>> ent;
-        ent.reserve(p->mfma.entries.size());
-        if (p->mfma_natural) {
-            std::vector<Int4> wn(nwin);
-            for (size_t w = 0; w < nwin; w++) {
-                const Int4 win = p->mfma.windows[w];
-                wn[w] = {win.x, ksteps, static_cast<int32_t>(w) * ksteps, win.w};
-                const int32_t r1 = std::min(M, win.x + kDmaWinRows);
-                for (int32_t r = win.x; r < r1; r++)
-                    for (int32_t j = rowptr[r]; j < rowptr[r + 1]; j++) {
-                        const int32_t c = colidx[j];
-                        ent.emplace_back(static_cast<uint32_t>(wn[w].z + c / 32) * kDmaATile +
-                                             static_cast<uint32_t>(a_cell(r - win.x, c % 32)),
-                                         j);
-                    }
-            }
-            (void)hipFree(p->d_windows);
-            p->d_windows = nullptr;
-            if ((st = dev_upload(&p->d_windows, wn.data(), wn.size()))) return bail(st);
-            p->mfma.cond_cols = static_cast<int64_t>(nwin) * ksteps * 32;
-        }
-        const size_t nsteps_all = p->mfma_natural ? nwin * static_cast<size_t>(ksteps) : p->mfma.eoff.size() - 1;
-        p->adense_halves = nsteps_all * static_cast<size_t>(kDmaATile) + 512;
-        for (size_t w = 0, e = 0; w < p->mfma.windows.size() && !p->mfma_natural; w++) {
-            const Int4 win = p->mfma.windows[w];
-            for (int32_t g = win.z; g < win.z + win.y; g++)
-                for (; e < static_cast<size_t>(p->mfma.eoff[g + 1]); e++) {
-                    const uint32_t en = p->mfma.entries[e];
-                    const uint32_t pos = static_cast<uint32_t>(g) * kDmaATile +
-                                         static_cast<uint32_t>(a_cell(static_cast<int>(en & 127u),
-                                                                      static_cast<int>((en >> 7) & 31u)));
-                    ent.emplace_back(pos, win.w + static_cast<int32_t>(en >> 12));
-                }
-        }
-        std::sort(ent.begin(), ent.end());
-        if (p->mfma_compact_want) {
-            // Compacted steps: the non-empty 16-byte cells of each step in
-            // cell order (cell = dense half index / 8 within the step, i.e.
-            // row block * 64 + lane), at most kCpCells - 1 per step (the last
-            // cell stays zero for the empty lanes); else plain dense tiles.
-            std::vector<uint64_t> mask(nsteps_all * 8, 0);
-            std::vector<std::pair<uint32_t, int32_t>> cent(ent);
-            bool fits = true;
-            for (size_t x = 0; x < cent.size() && fits;) {
-                const uint32_t g = cent[x].first / kDmaATile;
-                int32_t rank = -1;
-                uint32_t last = ~0u;
-                for (; x < cent.size() && cent[x].first / kDmaATile == g; x++) {
-                    const uint32_t h = cent[x].first % kDmaATile, c = h / 8;
-                    if (c != last) {
-                        rank++;
-                        last = c;
-                        mask[static_cast<size_t>(g) * 8 + c / 64] |= uint64_t(1) << (c % 64);
-                    }
-                    if (rank >= kCpCells - 1) fits = false;
-                    cent[x].first = g * static_cast<uint32_t>(kCpCells * 8) + static_cast<uint32_t>(rank) * 8u + h % 8;
-                }
-            }
-            if (fits) {
-                ent.swap(cent);
-                p->mfma_compact = true;
-                p->adense_halves = nsteps_all * static_cast<size_t>(kCpCells * 8) + 512;
-                if (const char* lb = std::getenv("TCA_COMPACT_LB")) p->mfma_compact_lb = std::atoi(lb) == 4 ? 4 : 3;
-                if ((st = dev_upload(&p->d_amask, mask.data(), mask.size()))) return bail(st);
+        // Row panels with B staged in LDS for the rows outside MFMA windows, then
+        // the row kernel for the rest.
+        plan_panels_routed(rowptr, colidx, M, K, N, dtype, flags, p->mfma.row_mfma, &p->panels);
+        std::vector<uint8_t> skip_rows(M, 0);
+        for (int32_t r = 0; r < M; r++)
+            skip_rows[r] = (!p->mfma.row_mfma.empty() && p->mfma.row_mfma[r]) || p->panels.row_panel[r];
+        plan_rows(rowptr, M, N, static_cast<int32_t>(dtype_size(dtype)), skip_rows, default_slices(K, N, dtype),
+                  &p->rows);
+        p->ntasks = static_cast<int32_t>(p->rows.tasks.size());
+        const size_t n_seg_rows =
+            p->rows.longrows.empty() ? 0 : static_cast<size_t>(p->rows.longrows.back().y + p->rows.longrows.back().z);
+        // One partial-row array and one segment-sum table for both kernels: the
+        // panels' segments follow the row kernel's.
+        {
+            const int32_t off = static_cast<int32_t>(n_seg_rows);
+            for (Int4& u : p->panels.units)
+                if (u.w >= 0) u.w += off;
+            for (Int4 lr : p->panels.longrows) {
+                lr.y += off;
+                p->rows.longrows.push_back(lr);
             }
         }
-        std::vector<int32_t> dsrc(ent.size());
-        std::vector<uint32_t> dpos(ent.size());
-        for (size_t x = 0; x < ent.size(); x++) {
-            dpos[x] = ent[x].first;
-            dsrc[x] = ent[x].second;
-        }
-        p->n_dn = static_cast<int32_t>(ent.size());
-        if ((st = dev_upload(&p->d_dn_src, dsrc.data(), dsrc.size()))) return bail(st);
-        if ((st = dev_upload(&p->d_dn_pos, dpos.data(), dpos.size()))) return bail(st);
-        if ((st = dev_upload(&p->d_adense, nullptr, p->adense_halves))) return bail(st);
-        if (hipMemset(p->d_adense, 0, p->adense_halves * 2) != hipSuccess)
-            return bail(fail(TCA_ERR_HIP, "hipMemset of the dense tiles failed"));
-    } else if (!p->mfma.windows.empty()) {
-        // Packed entries of the paired kernel: step g's block at ebase[g],
-        // whole chunks of 256 words (at least one), entries placed by
-        // pair_entry_word, unused words the dummy cell of the lane that loads
-        // them, with value 0; 16 zero bytes (padding B source) after the blocks.
-        const size_t nsteps_all = p->mfma.eoff.size() - 1;
-        std::vector<int> ebase(nsteps_all + 1);
-        std::vector<i32x2v> emeta(nsteps_all);
-        ebase[0] = 0;
-        for (size_t g = 0; g < nsteps_all; g++) {
-            const int cnt = p->mfma.eoff[g + 1] - p->mfma.eoff[g];
-            const int chunks = std::max(1, (cnt + kPairChunk - 1) / kPairChunk);
-            ebase[g + 1] = ebase[g] + chunks * kPairChunk;
-            emeta[g] = i32x2v{ebase[g], std::max(1, (cnt + kPairGroup - 1) / kPairGroup)};
-        }
-        const size_t nwords = static_cast<size_t>(ebase.back());
-        const size_t npacked = nwords + 4;
-        p->mfma_zeros_at = nwords;
-        // pack kernel inputs, per word it writes (all words before the
-        // zeros): the nonzero's CSR index and the cell
-        std::vector<int> src(nwords, -1);
-        std::vector<uint16_t> cell(nwords, 0xffffu);
-        std::vector<uint32_t> packed(npacked, kNoEntry);
-        std::fill(packed.end() - 4, packed.end(), 0u);
-        for (size_t w = 0; w < p->mfma.windows.size(); w++) {
-            const Int4 win = p->mfma.windows[w];
-            for (int32_t j = 0; j < win.y; j++)
-                for (int32_t x = ebase[win.z + j]; x < ebase[win.z + j + 1]; x++) {
-                    packed[x] = pair_cell_addr(j % kPairSteps, kDmaATile + ((x - ebase[win.z + j]) % kPairChunk) / 4);
-                    cell[x] = static_cast<uint16_t>(packed[x]);
-                }
-        }
-        const int row_mask = 127, k_shift = 7, idx_shift = 12;
-        for (size_t w = 0, e = 0; w < p->mfma.windows.size(); w++) {
-            const Int4 win = p->mfma.windows[w];
-            for (int32_t g = win.z; g < win.z + win.y; g++)
-                for (; e < static_cast<size_t>(p->mfma.eoff[g + 1]); e++) {
-                    const uint32_t en = p->mfma.entries[e];
-                    const int acell = a_cell(static_cast<int>(en & row_mask), static_cast<int>((en >> k_shift) & 31u));
-                    const size_t x = static_cast<size_t>(ebase[g] + pair_entry_word(static_cast<int>(e - p->mfma.eoff[g])));
-                    src[x] = win.w + static_cast<int>(en >> idx_shift);
-                    cell[x] = static_cast<uint16_t>(pair_cell_addr((g - win.z) % kPairSteps, acell));
-                }
-        }
-        p->n_pk_words = static_cast<int32_t>(nwords);
-        p->n_packed = npacked;
-        if ((st = dev_upload(&p->d_pk_src, src.data(), nwords))) return bail(st);
-        if ((st = dev_upload(&p->d_pk_cell, cell.data(), nwords))) return bail(st);
-        if ((st = dev_upload(&p->d_packed, packed.data(), npacked))) return bail(st);
-        if ((st = dev_upload(&p->d_emeta, emeta.data(), emeta.size()))) return bail(st);
-    }
-    if (hipDeviceSynchronize() != hipSuccess) return bail(fail(TCA_ERR_HIP, "hipDeviceSynchronize failed"));
+        const size_t n_seg_total = n_seg_rows + static_cast<size_t>(p->panels.n_segments);
+        p->n_units = static_cast<int32_t>(p->panels.units.size());
+        p->n_longrows = static_cast<int32_t>(p->rows.longrows.size());
+        p->n_seg_total = n_seg_total;
+        p->n_perm = static_cast<int32_t>(p->rows.perm.size());
+        const auto t1 = std::chrono::steady_clock::now();
 
-    fill_info(p);
-    p->info.plan_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
-    *plan = p;
-    return TCA_OK;
+        auto bail = [&](int s) { return s; };  // `hold` frees the plan
+        if ((st = dev_upload(&p->d_rowptr, rowptr, static_cast<size_t>(M) + 1))) return bail(st);
+        if ((st = dev_upload(&p->d_colidx, colidx, static_cast<size_t>(nnz)))) return bail(st);
+        if ((st = dev_upload(&p->d_tasks, p->rows.tasks.data(), p->rows.tasks.size()))) return bail(st);
+        if ((st = dev_upload(&p->d_perm, p->rows.perm.data(), p->rows.perm.size()))) return bail(st);
+        if ((st = dev_upload(&p->d_longrows, p->rows.longrows.data(), p->rows.longrows.size()))) return bail(st);
+        if (!(flags & TCA_PLAN_NO_SCRATCH) && (st = dev_upload(&p->d_partials, nullptr, n_seg_total * N))) return bail(st);
+        if (p->n_units > 0) {
+            const PanelPlan& pp = p->panels;
+            if ((st = dev_upload(&p->d_units, pp.units.data(), pp.units.size()))) return bail(st);
+            if ((st = dev_upload(&p->d_panel_units, pp.panel_units.data(), pp.panel_units.size()))) return bail(st);
+            if ((st = dev_upload(&p->d_prows, pp.rows.data(), pp.rows.size()))) return bail(st);
+            {
+                // staged rows as byte offsets into B (B < 4 GiB, checked above)
+                std::vector<int32_t> boff(pp.cols.size());
+                const uint32_t rb = static_cast<uint32_t>(N) * static_cast<uint32_t>(dtype_size(dtype));
+                for (size_t j = 0; j < boff.size(); j++) boff[j] = static_cast<int32_t>(static_cast<uint32_t>(pp.cols[j]) * rb);
+                if ((st = dev_upload(&p->d_pcols, boff.data(), boff.size()))) return bail(st);
+            }
+            if ((st = dev_upload(&p->d_pwidth, pp.width.data(), pp.width.size()))) return bail(st);
+            if ((st = dev_upload(&p->d_pcnt, pp.cnt.data(), pp.cnt.size() / 4))) return bail(st);
+            if ((st = dev_upload(&p->d_ppos, pp.pos.data(), pp.pos.size()))) return bail(st);
+            p->n_pos_bytes = pp.pos.size();
+            if ((st = dev_upload(&p->d_ustart, pp.ustart.data(), pp.ustart.size()))) return bail(st);
+            // the kernel needs only the arrays on the device
+            p->panels.cols.clear(); p->panels.cols.shrink_to_fit();
+            p->panels.width.clear(); p->panels.width.shrink_to_fit();
+            p->panels.cnt.clear(); p->panels.cnt.shrink_to_fit();
+            p->panels.pos.clear(); p->panels.pos.shrink_to_fit();
+            p->panels.ustart.clear(); p->panels.ustart.shrink_to_fit();
+        }
+        if ((st = dev_upload(&p->d_windows, p->mfma.windows.data(), p->mfma.windows.size()))) return bail(st);
+        if (!p->mfma.windows.empty()) {
+            // Device forms: B row byte offsets (padding 0xffffffff; paired kernel:
+            // each step's 32 offsets permuted, word 4 r + k = column r + 8 k) and
+            // the step entry ranges.
+            std::vector<uint32_t> uoff(p->mfma.ucols.size());
+            for (size_t i = 0; i < uoff.size(); i++) {
+                const size_t src = p->mfma_pair ? (i & ~size_t(31)) + ((i & 31) >> 2) + 8 * (i & 3) : i;
+                uoff[i] = p->mfma.ucols[src] < 0 ? kNoEntry
+                                                  : static_cast<uint32_t>(p->mfma.ucols[src]) * static_cast<uint32_t>(N) * 2u;
+            }
+            if ((st = dev_upload(&p->d_ucols, uoff.data(), uoff.size()))) return bail(st);
+            p->n_ucols = uoff.size();
+            if ((st = dev_upload(&p->d_eoff, p->mfma.eoff.data(), p->mfma.eoff.size()))) return bail(st);
+        }
+        if (!p->mfma.windows.empty() && p->mfma_dense) {
+            // Dense condensed windows: 8 KiB per global step (128 rows x 32
+            // condensed columns in fragment order), zero except at the entries,
+            // whose values the pack kernel writes each run; 1 KiB of zeros after
+            // them (the B source for padding rows).  Entries sorted by position.
+            // Windows whose column unions cover most of K (on average >= 85 %) keep
+            // their columns in natural order instead: every window spans all of K,
+            // step j holds columns 32 j .. 32 j + 31, so the kernel's B rows are
+            // contiguous and need no row-offset table.
+            const int32_t ksteps = (K + 31) / 32;
+            const size_t nwin = p->mfma.windows.size();
+            p->mfma_natural = static_cast<double>(p->mfma.cond_cols) >= kNaturalCover * static_cast<double>(nwin) * K &&
+                              nwin * static_cast<size_t>(ksteps) * kDnATileBytes <= kDenseMaxBytes;
+            std::vector<std::pair<uint32_t, int32_t>> ent;
+            ent.reserve(p->mfma.entries.size());
+            if (p->mfma_natural) {
+                std::vector<Int4> wn(nwin);
+                for (size_t w = 0; w < nwin; w++) {
+                    const Int4 win = p->mfma.windows[w];
+                    wn[w] = {win.x, ksteps, static_cast<int32_t>(w) * ksteps, win.w};
+                    const int32_t r1 = std::min(M, win.x + kDmaWinRows);
+                    for (int32_t r = win.x; r < r1; r++)
+                        for (int32_t j = rowptr[r]; j < rowptr[r + 1]; j++) {
+                            const int32_t c = colidx[j];
+                            ent.emplace_back(static_cast<uint32_t>(wn[w].z + c / 32) * kDmaATile +
+                                                 static_cast<uint32_t>(a_cell(r - win.x, c % 32)),
+                                             j);
+                        }
+                }
+                (void)hipFree(p->d_windows);
+                p->d_windows = nullptr;
+                if ((st = dev_upload(&p->d_windows, wn.data(), wn.size()))) return bail(st);
+                p->mfma.cond_cols = static_cast<int64_t>(nwin) * ksteps * 32;
+            }
+            const size_t nsteps_all = p->mfma_natural ? nwin * static_cast<size_t>(ksteps) : p->mfma.eoff.size() - 1;
+            p->adense_halves = nsteps_all * static_cast<size_t>(kDmaATile) + 512;
+            for (size_t w = 0, e = 0; w < p->mfma.windows.size() && !p->mfma_natural; w++) {
+                const Int4 win = p->mfma.windows[w];
+                for (int32_t g = win.z; g < win.z + win.y; g++)
+                    for (; e < static_cast<size_t>(p->mfma.eoff[g + 1]); e++) {
+                        const uint32_t en = p->mfma.entries[e];
+                        const uint32_t pos = static_cast<uint32_t>(g) * kDmaATile +
+                                             static_cast<uint32_t>(a_cell(static_cast<int>(en & 127u),
+                                                                          static_cast<int>((en >> 7) & 31u)));
+                        ent.emplace_back(pos, win.w + static_cast<int32_t>(en >> 12));
+                    }
+            }
+            std::sort(ent.begin(), ent.end());
+            if (p->mfma_compact_want) {
+                // Compacted steps: the non-empty 16-byte cells of each step in
+                // cell order (cell = dense half index / 8 within the step, i.e.
+                // row block * 64 + lane), at most kCpCells - 1 per step (the last
+                // cell stays zero for the empty lanes); else plain dense tiles.
+                std::vector<uint64_t> mask(nsteps_all * 8, 0);
+                std::vector<std::pair<uint32_t, int32_t>> cent(ent);
+                bool fits = true;
+                for (size_t x = 0; x < cent.size() && fits;) {
+                    const uint32_t g = cent[x].first / kDmaATile;
+                    int32_t rank = -1;
+                    uint32_t last = ~0u;
+                    for (; x < cent.size() && cent[x].first / kDmaATile == g; x++) {
+                        const uint32_t h = cent[x].first % kDmaATile, c = h / 8;
+                        if (c != last) {
+                            rank++;
+                            last = c;
+                            mask[static_cast<size_t>(g) * 8 + c / 64] |= uint64_t(1) << (c % 64);
+                        }
+                        if (rank >= kCpCells - 1) fits = false;
+                        cent[x].first = g * static_cast<uint32_t>(kCpCells * 8) + static_cast<uint32_t>(rank) * 8u + h % 8;
+                    }
+                }
+                if (fits) {
+                    ent.swap(cent);
+                    p->mfma_compact = true;
+                    p->adense_halves = nsteps_all * static_cast<size_t>(kCpCells * 8) + 512;
+                    if (const char* lb = std::getenv("TCA_COMPACT_LB")) p->mfma_compact_lb = std::atoi(lb) == 4 ? 4 : 3;
+                    if ((st = dev_upload(&p->d_amask, mask.data(), mask.size()))) return bail(st);
+                }
+            }
+            std::vector<int32_t> dsrc(ent.size());
+            std::vector<uint32_t> dpos(ent.size());
+            for (size_t x = 0; x < ent.size(); x++) {
+                dpos[x] = ent[x].first;
+                dsrc[x] = ent[x].second;
+            }
+            p->n_dn = static_cast<int32_t>(ent.size());
+            if ((st = dev_upload(&p->d_dn_src, dsrc.data(), dsrc.size()))) return bail(st);
+            if ((st = dev_upload(&p->d_dn_pos, dpos.data(), dpos.size()))) return bail(st);
+            if ((st = dev_upload(&p->d_adense, nullptr, p->adense_halves))) return bail(st);
+            if (hipMemset(p->d_adense, 0, p->adense_halves * 2) != hipSuccess)
+                return bail(fail(TCA_ERR_HIP, "hipMemset of the dense tiles failed"));
+        } else if (!p->mfma.windows.empty()) {
+            // Packed entries of the paired kernel: step g's block at ebase[g],
+            // whole chunks of 256 words (at least one), entries placed by
+            // pair_entry_word, unused words the dummy cell of the lane that loads
+            // them, with value 0; 16 zero bytes (padding B source) after the blocks.
+            const size_t nsteps_all = p->mfma.eoff.size() - 1;
+            std::vector<int> ebase(nsteps_all + 1);
+            std::vector<i32x2v> emeta(nsteps_all);
+            ebase[0] = 0;
+            for (size_t g = 0; g < nsteps_all; g++) {
+                const int cnt = p->mfma.eoff[g + 1] - p->mfma.eoff[g];
+                const int chunks = std::max(1, (cnt + kPairChunk - 1) / kPairChunk);
+                ebase[g + 1] = ebase[g] + chunks * kPairChunk;
+                emeta[g] = i32x2v{ebase[g], std::max(1, (cnt + kPairGroup - 1) / kPairGroup)};
+            }
+            const size_t nwords = static_cast<size_t>(ebase.back());
+            const size_t npacked = nwords + 4;
+            p->mfma_zeros_at = nwords;
+            // pack kernel inputs, per word it writes (all words before the
+            // zeros): the nonzero's CSR index and the cell
+            std::vector<int> src(nwords, -1);
+            std::vector<uint16_t> cell(nwords, 0xffffu);
+            std::vector<uint32_t> packed(npacked, kNoEntry);
+            std::fill(packed.end() - 4, packed.end(), 0u);
+            for (size_t w = 0; w < p->mfma.windows.size(); w++) {
+                const Int4 win = p->mfma.windows[w];
+                for (int32_t j = 0; j < win.y; j++)
+                    for (int32_t x = ebase[win.z + j]; x < ebase[win.z + j + 1]; x++) {
+                        packed[x] = pair_cell_addr(j % kPairSteps, kDmaATile + ((x - ebase[win.z + j]) % kPairChunk) / 4);
+                        cell[x] = static_cast<uint16_t>(packed[x]);
+                    }
+            }
+            const int row_mask = 127, k_shift = 7, idx_shift = 12;
+            for (size_t w = 0, e = 0; w < p->mfma.windows.size(); w++) {
+                const Int4 win = p->mfma.windows[w];
+                for (int32_t g = win.z; g < win.z + win.y; g++)
+                    for (; e < static_cast<size_t>(p->mfma.eoff[g + 1]); e++) {
+                        const uint32_t en = p->mfma.entries[e];
+                        const int acell = a_cell(static_cast<int>(en & row_mask), static_cast<int>((en >> k_shift) & 31u));
+                        const size_t x = static_cast<size_t>(ebase[g] + pair_entry_word(static_cast<int>(e - p->mfma.eoff[g])));
+                        src[x] = win.w + static_cast<int>(en >> idx_shift);
+                        cell[x] = static_cast<uint16_t>(pair_cell_addr((g - win.z) % kPairSteps, acell));
+                    }
+            }
+            p->n_pk_words = static_cast<int32_t>(nwords);
+            p->n_packed = npacked;
+            if ((st = dev_upload(&p->d_pk_src, src.data(), nwords))) return bail(st);
+            if ((st = dev_upload(&p->d_pk_cell, cell.data(), nwords))) return bail(st);
+            if ((st = dev_upload(&p->d_packed, packed.data(), npacked))) return bail(st);
+            if ((st = dev_upload(&p->d_emeta, emeta.data(), emeta.size()))) return bail(st);
+        }
+        if (hipDeviceSynchronize() != hipSuccess) return bail(fail(TCA_ERR_HIP, "hipDeviceSynchronize failed"));
+
+        fill_info(p);
+        p->info.plan_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
+        *plan = hold.release();
+        return TCA_OK;
+    });
 }
 
 int tca_spmm_plan_create_device(const int32_t* d_rowptr, const int32_t* d_colidx, int32_t M, int32_t K, int32_t nnz,
                                 int32_t N, int32_t dtype, uint32_t flags, void* stream, tca_spmm_plan** plan) {
-    if (!plan) return fail(TCA_ERR_INVALID, "plan is NULL");
-    *plan = nullptr;
-    if (M < 0 || K < 1 || N < 1 || nnz < 0) return fail(TCA_ERR_INVALID, "bad shape M=%d K=%d N=%d nnz=%d", M, K, N, nnz);
-    if (!dtype_ok(dtype)) return fail(TCA_ERR_INVALID, "unknown dtype %d", dtype);
-    if (!d_rowptr || (nnz > 0 && !d_colidx)) return fail(TCA_ERR_INVALID, "NULL device pointer");
-    if (flags & ~TCA_PLAN_KNOWN_FLAGS) return fail(TCA_ERR_INVALID, "unknown plan flags 0x%x", flags & ~TCA_PLAN_KNOWN_FLAGS);
-    if (flags & TCA_PLAN_MFMA_PAIR)
-        return fail(TCA_ERR_UNSUPPORTED,
-                    "device planning builds row-kernel and dense-tile plans (TCA_PLAN_MFMA_PAIR needs the host planner)");
-    const uint64_t b_bytes = static_cast<uint64_t>(K) * static_cast<uint64_t>(N) * dtype_size(dtype);
-    if (b_bytes >= 0xfffffff0ull || static_cast<uint64_t>(nnz) * 4 >= 0xfffffff0ull)
-        return fail(TCA_ERR_UNSUPPORTED, "B (%llu bytes) or the nonzeros exceed the 4 GiB buffer range",
-                    (unsigned long long)b_bytes);
-    const auto t0 = std::chrono::steady_clock::now();
-    tca_spmm_plan* p = new (std::nothrow) tca_spmm_plan();
-    if (!p) return fail(TCA_ERR_ALLOC, "plan allocation failed");
-    p->M = M;
-    p->K = K;
-    p->N = N;
-    p->nnz = nnz;
-    p->dtype = dtype;
-    p->flags = flags;
-    p->device_planned = true;
-    p->mfma.row_mfma.clear();
-    if (hipGetDevice(&p->device) != hipSuccess) {
-        delete p;
-        return fail(TCA_ERR_HIP, "no HIP device");
-    }
-    plan_row_params(nnz, N, static_cast<int32_t>(dtype_size(dtype)), default_slices(K, N, dtype), &p->rows);
-    const int slots = 64 >> p->rows.log_lanes;
-    hipStream_t s = static_cast<hipStream_t>(stream);
+    return api_guard("tca_spmm_plan_create_device", [&]() -> int {
+        if (!plan) return fail(TCA_ERR_INVALID, "plan is NULL");
+        *plan = nullptr;
+        if (M < 0 || K < 1 || N < 1 || nnz < 0) return fail(TCA_ERR_INVALID, "bad shape M=%d K=%d N=%d nnz=%d", M, K, N, nnz);
+        if (!dtype_ok(dtype)) return fail(TCA_ERR_INVALID, "unknown dtype %d", dtype);
+        if (!d_rowptr || (nnz > 0 && !d_colidx)) return fail(TCA_ERR_INVALID, "NULL device pointer");
+        if (flags & ~TCA_PLAN_KNOWN_FLAGS) return fail(TCA_ERR_INVALID, "unknown plan flags 0x%x", flags & ~TCA_PLAN_KNOWN_FLAGS);
+        if (flags & TCA_PLAN_MFMA_PAIR)
+            return fail(TCA_ERR_UNSUPPORTED,
+                        "device planning builds row-kernel and dense-tile plans (TCA_PLAN_MFMA_PAIR needs the host planner)");
+        const uint64_t b_bytes = static_cast<uint64_t>(K) * static_cast<uint64_t>(N) * dtype_size(dtype);
+        if (b_bytes >= 0xfffffff0ull || static_cast<uint64_t>(nnz) * 4 >= 0xfffffff0ull)
+            return fail(TCA_ERR_UNSUPPORTED, "B (%llu bytes) or the nonzeros exceed the 4 GiB buffer range",
+                        (unsigned long long)b_bytes);
+        const auto t0 = std::chrono::steady_clock::now();
+        tca_spmm_plan* p = new (std::nothrow) tca_spmm_plan();
+        if (!p) return fail(TCA_ERR_ALLOC, "plan allocation failed");
+        PlanHolder hold{p};
+        p->M = M;
+        p->K = K;
+        p->N = N;
+        p->nnz = nnz;
+        p->dtype = dtype;
+        p->flags = flags;
+        p->device_planned = true;
+        p->mfma.row_mfma.clear();
+        if (hipGetDevice(&p->device) != hipSuccess) return fail(TCA_ERR_HIP, "no HIP device");
+        plan_row_params(nnz, N, static_cast<int32_t>(dtype_size(dtype)), default_slices(K, N, dtype), &p->rows);
+        const int slots = 64 >> p->rows.log_lanes;
+        hipStream_t s = static_cast<hipStream_t>(stream);
 
-    // temporaries of the planning, freed on every exit
-    uint32_t *keys = nullptr, *keys_s = nullptr, *bm = nullptr, *ekeys = nullptr, *ekeys_s = nullptr;
-    int *rows = nullptr, *rows_s = nullptr, *cnt = nullptr, *nseg = nullptr, *segoff = nullptr;
-    int *wordpre = nullptr, *scnt = nullptr, *wstat = nullptr, *wmap = nullptr, *wgbase = nullptr, *evals = nullptr,
-        *evals_s = nullptr;
-    uint8_t* start = nullptr;
-    void* tmp = nullptr;
-    auto bail = [&](int st) {
-        (void)hipStreamSynchronize(s);
-        for (void* q : {(void*)keys, (void*)keys_s, (void*)rows, (void*)rows_s, (void*)cnt, (void*)nseg, (void*)segoff,
-                        (void*)start, tmp, (void*)bm, (void*)ekeys, (void*)ekeys_s, (void*)wordpre, (void*)scnt,
-                        (void*)wstat, (void*)wmap, (void*)wgbase, (void*)evals, (void*)evals_s})
-            (void)hipFree(q);
-        if (st != TCA_OK) {
-            free_plan_device(p);
-            delete p;
-        }
-        return st;
-    };
-    int st;
-    // The plan owns its copy of the structure (row kernel and SDDMM read it).
-    if ((st = dev_upload(&p->d_rowptr, nullptr, static_cast<size_t>(M) + 1))) return bail(st);
-    if ((st = dev_upload(&p->d_colidx, nullptr, static_cast<size_t>(nnz)))) return bail(st);
-    if (hipMemcpyAsync(p->d_rowptr, d_rowptr, sizeof(int) * (static_cast<size_t>(M) + 1), hipMemcpyDeviceToDevice, s) !=
-            hipSuccess ||
-        (nnz > 0 && hipMemcpyAsync(p->d_colidx, d_colidx, sizeof(int) * static_cast<size_t>(nnz),
-                                   hipMemcpyDeviceToDevice, s) != hipSuccess))
-        return bail(fail(TCA_ERR_HIP, "structure copy failed"));
-    // CSR checks
-    if ((st = dev_upload(&cnt, nullptr, 4))) return bail(st);  // [0..2] bounds, [3] error bits
-    if ((st = dev_upload(&start, nullptr, static_cast<size_t>(nnz) + 1))) return bail(st);
-    if (hipMemsetAsync(cnt, 0, 4 * sizeof(int), s) != hipSuccess ||
-        hipMemsetAsync(start, 0, static_cast<size_t>(nnz) + 1, s) != hipSuccess)
-        return bail(fail(TCA_ERR_HIP, "hipMemsetAsync failed"));
-    const dim3 blk(256);
-    auto grid_for = [](int64_t n) { return dim3(static_cast<unsigned>(std::min<int64_t>((n + 255) / 256, 65536))); };
-    if (M > 0) {
-        hipLaunchKernelGGL(dp_check_rows_kernel, grid_for(M), blk, 0, s, p->d_rowptr, M, nnz, start, cnt + 3);
-        if (nnz > 0) hipLaunchKernelGGL(dp_check_cols_kernel, grid_for(nnz), blk, 0, s, p->d_colidx, nnz, K, start, cnt + 3);
-    }
-    int h_cnt[4] = {0, 0, 0, 0};
-    // the columns index the window bitmaps below: validate first
-    if (hipMemcpyAsync(h_cnt, cnt, sizeof h_cnt, hipMemcpyDeviceToHost, s) != hipSuccess ||
-        hipStreamSynchronize(s) != hipSuccess)
-        return bail(fail(TCA_ERR_HIP, "CSR checks failed"));
-    if (h_cnt[3] & 1) return bail(fail(TCA_ERR_INVALID, "CSR row offsets are not 0 .. nnz non-decreasing"));
-    if (h_cnt[3] & 2) return bail(fail(TCA_ERR_INVALID, "CSR columns out of range or not strictly ascending in a row"));
-
-    // MFMA windows: statistics on the GPU, the host planner's routing, then
-    // dense tiles (natural column order when the windows cover most of K,
-    // else condensed) built on the GPU.  Needs fp16 / bf16, N % 8 == 0 and
-    // window bitmaps of at most kDevBitmapWords words.
-    int32_t rows_mfma = 0;
-    {
-        constexpr size_t kDevBitmapWords = size_t(1) << 25;  // 128 MiB per table
-        const int nw = (M + kDmaWinRows - 1) / kDmaWinRows, kw = (K + 31) / 32;
-        if ((flags & TCA_PLAN_NO_MFMA) == 0 && dtype != TCA_F32 && N % 8 == 0 && M > 0 && nnz > 0 &&
-            static_cast<size_t>(nw) * kw <= kDevBitmapWords) {
-            const size_t nb = static_cast<size_t>(nw) * kw;
-            if ((st = dev_upload(&bm, nullptr, nb)) || (st = dev_upload(&wordpre, nullptr, nb)) ||
-                (st = dev_upload(&scnt, nullptr, nb)) || (st = dev_upload(&wstat, nullptr, 3 * static_cast<size_t>(nw) + 1)))
-                return bail(st);
-            if (hipMemsetAsync(bm, 0, nb * 4, s) != hipSuccess || hipMemsetAsync(scnt, 0, nb * 4, s) != hipSuccess)
-                return bail(fail(TCA_ERR_HIP, "hipMemsetAsync failed"));
-            int* const ucount = wstat;
-            int* const maxper = wstat + nw;
-            int* const wrow = wstat + 2 * nw;  // nw + 1
-            const dim3 rgrid(static_cast<unsigned>(std::min<int64_t>((static_cast<int64_t>(M) + 3) / 4, 65536)));
-            hipLaunchKernelGGL(dm_bitmap_kernel, rgrid, blk, 0, s, p->d_rowptr, p->d_colidx, M, kw, bm);
-            hipLaunchKernelGGL(dm_union_kernel, dim3(nw), blk, 0, s, p->d_rowptr, M, nw, kw, bm, wordpre, ucount, wrow);
-            hipLaunchKernelGGL(dm_stepcount_kernel, rgrid, blk, 0, s, p->d_rowptr, p->d_colidx, M, kw, bm, wordpre,
-                               scnt);
-            hipLaunchKernelGGL(dm_stepmax_kernel, dim3(nw), blk, 0, s, scnt, kw, ucount, maxper);
-            std::vector<int> h(3 * static_cast<size_t>(nw) + 1);
-            if (hipMemcpyAsync(h.data(), wstat, sizeof(int) * h.size(), hipMemcpyDeviceToHost, s) != hipSuccess ||
-                hipStreamSynchronize(s) != hipSuccess)
-                return bail(fail(TCA_ERR_HIP, "window statistics failed"));
-            std::vector<WinStat> ws(nw);
-            for (int w = 0; w < nw; w++)
-                ws[w] = {static_cast<int64_t>(h[2 * nw + w + 1]) - h[2 * nw + w], h[w], h[nw + w]};
-            const char* md = std::getenv("TCA_MFMA_MIN_DENSITY");
-            std::vector<uint8_t> take;
-            route_windows(ws, M, nnz, N, (flags & TCA_PLAN_FORCE_MFMA) != 0, md ? std::atof(md) : kMfmaMinDensity,
-                          mfma_shape(flags), &take);
-            // the host planner's choice between natural and condensed dense tiles
-            std::vector<int> h_wmap(nw, -1), h_base;
-            int64_t cond_cols = 0, steps_all = 0, nz_take = 0;
-            int n_take = 0;
-            for (int w = 0; w < nw; w++) {
-                if (!take[w]) continue;
-                h_wmap[w] = n_take++;
-                const int steps = (h[w] + 31) / 32;
-                h_base.push_back(static_cast<int>(steps_all));
-                steps_all += steps;
-                cond_cols += static_cast<int64_t>(steps) * 32;
-                nz_take += ws[w].nz;
-                rows_mfma += std::min(M, (w + 1) * kDmaWinRows) - w * kDmaWinRows;
-            }
-            const int32_t ksteps = (K + 31) / 32;
-            const bool natural = n_take > 0 &&
-                                 static_cast<double>(cond_cols) >= kNaturalCover * static_cast<double>(n_take) * K &&
-                                 static_cast<size_t>(n_take) * ksteps * kDnATileBytes <= kDenseMaxBytes;
-            if (natural) {
-                for (int t = 0; t < n_take; t++) h_base[t] = t * ksteps;
-                steps_all = static_cast<int64_t>(n_take) * ksteps;
-                cond_cols = steps_all * 32;
-            }
-            if (n_take > 0 && static_cast<size_t>(steps_all) * kDnATileBytes > kDenseMaxBytes) {
-                n_take = 0;  // past the dense-tile budget: every row on the row kernel
-                rows_mfma = 0;
-            }
-            if (n_take > 0) {
-                std::vector<Int4> win;
-                for (int w = 0; w < nw; w++)
-                    if (h_wmap[w] >= 0) {
-                        const int t = h_wmap[w];
-                        win.push_back({w * kDmaWinRows, natural ? ksteps : (h[w] + 31) / 32, h_base[t], h[2 * nw + w]});
-                    }
-                if ((st = dev_upload(&wmap, h_wmap.data(), h_wmap.size())) ||
-                    (st = dev_upload(&wgbase, h_base.data(), h_base.size())) ||
-                    (st = dev_upload(&p->d_windows, win.data(), win.size())) ||
-                    (st = dev_upload(&ekeys, nullptr, nnz)) || (st = dev_upload(&ekeys_s, nullptr, nnz)) ||
-                    (st = dev_upload(&evals, nullptr, nnz)) || (st = dev_upload(&evals_s, nullptr, nnz)))
-                    return bail(st);
-                DmEntryArgs ea;
-                ea.rowptr = p->d_rowptr;
-                ea.colidx = p->d_colidx;
-                ea.bm = bm;
-                ea.wordpre = wordpre;
-                ea.wmap = wmap;
-                ea.wgbase = wgbase;
-                ea.keys = ekeys;
-                ea.vals = evals;
-                ea.M = M;
-                ea.kw = kw;
-                ea.natural = natural ? 1 : 0;
-                hipLaunchKernelGGL(dm_entries_kernel, rgrid, blk, 0, s, ea);
-                // ascending positions: the routed nonzeros first, in the host planner's order
-                size_t tmp_bytes = 0;
-                if (rocprim::radix_sort_pairs(nullptr, tmp_bytes, ekeys, ekeys_s, evals, evals_s,
-                                              static_cast<size_t>(nnz), 0, 32, s) != hipSuccess ||
-                    hipMalloc(&tmp, tmp_bytes) != hipSuccess ||
-                    rocprim::radix_sort_pairs(tmp, tmp_bytes, ekeys, ekeys_s, evals, evals_s, static_cast<size_t>(nnz),
-                                              0, 32, s) != hipSuccess)
-                    return bail(fail(TCA_ERR_HIP, "entry sort failed"));
-                (void)hipFree(tmp);
-                tmp = nullptr;
-                p->n_dn = static_cast<int32_t>(nz_take);
-                if ((st = dev_upload(&p->d_dn_pos, nullptr, static_cast<size_t>(nz_take))) ||
-                    (st = dev_upload(&p->d_dn_src, nullptr, static_cast<size_t>(nz_take))))
-                    return bail(st);
-                if (hipMemcpyAsync(p->d_dn_pos, ekeys_s, 4 * static_cast<size_t>(nz_take), hipMemcpyDeviceToDevice, s) !=
-                        hipSuccess ||
-                    hipMemcpyAsync(p->d_dn_src, evals_s, 4 * static_cast<size_t>(nz_take), hipMemcpyDeviceToDevice, s) !=
-                        hipSuccess)
-                    return bail(fail(TCA_ERR_HIP, "entry copy failed"));
-                if (!natural) {
-                    if ((st = dev_upload(&p->d_ucols, nullptr, static_cast<size_t>(steps_all) * 32))) return bail(st);
-                    p->n_ucols = static_cast<size_t>(steps_all) * 32;
-                    if (hipMemsetAsync(p->d_ucols, 0xff, 4 * static_cast<size_t>(steps_all) * 32, s) != hipSuccess)
-                        return bail(fail(TCA_ERR_HIP, "hipMemsetAsync failed"));
-                    hipLaunchKernelGGL(dm_ucols_kernel, grid_for(static_cast<int64_t>(nw) * kw), blk, 0, s, nw, kw, bm,
-                                       wordpre, wmap, wgbase, N, p->d_ucols);
-                }
-                p->adense_halves = static_cast<size_t>(steps_all) * kDmaATile + 512;
-                if ((st = dev_upload(&p->d_adense, nullptr, p->adense_halves))) return bail(st);
-                if (hipMemsetAsync(p->d_adense, 0, p->adense_halves * 2, s) != hipSuccess)
-                    return bail(fail(TCA_ERR_HIP, "hipMemsetAsync of the dense tiles failed"));
-                p->mfma.win_rows = kDmaWinRows;
-                p->mfma.windows = std::move(win);
-                p->mfma.rows = rows_mfma;
-                p->mfma.nnz = nz_take;
-                p->mfma.cond_cols = cond_cols;
-                p->mfma_dense = true;
-                p->mfma_natural = natural;
-                p->mfma_col_blocks = (N + kDmaTileCols - 1) / kDmaTileCols;
-            }
-        }
-    }
-    if (p->mfma.windows.empty()) p->flags |= TCA_PLAN_NO_MFMA;
-    const int Mp = M - rows_mfma;  // rows of the row kernel
-
-    // rows longest first (stable descending radix sort of length + 1; rows of
-    // the routed windows have key 0 and sort last)
-    if (M > 0) {
-        if ((st = dev_upload(&keys, nullptr, M)) || (st = dev_upload(&keys_s, nullptr, M)) ||
-            (st = dev_upload(&rows, nullptr, M)) || (st = dev_upload(&rows_s, nullptr, M)))
-            return bail(st);
-        hipLaunchKernelGGL(dp_lengths_kernel, grid_for(M), blk, 0, s, p->d_rowptr, M,
-                           p->mfma.windows.empty() ? nullptr : wmap, keys, rows);
-        size_t tmp_bytes = 0;
-        if (rocprim::radix_sort_pairs_desc(nullptr, tmp_bytes, keys, keys_s, rows, rows_s, static_cast<size_t>(M), 0, 32,
-                                           s) != hipSuccess)
-            return bail(fail(TCA_ERR_HIP, "radix sort sizing failed"));
-        if (hipMalloc(&tmp, tmp_bytes) != hipSuccess) return bail(fail(TCA_ERR_ALLOC, "radix sort workspace"));
-        if (rocprim::radix_sort_pairs_desc(tmp, tmp_bytes, keys, keys_s, rows, rows_s, static_cast<size_t>(M), 0, 32, s) !=
-            hipSuccess)
-            return bail(fail(TCA_ERR_HIP, "radix sort failed"));
-        if (Mp > 0)
-            hipLaunchKernelGGL(dp_bounds_kernel, dim3(1), dim3(64), 0, s, keys_s, Mp, p->rows.wide_len, p->rows.row_len,
-                               p->rows.multi_max, cnt);
-    }
-    if (hipMemcpyAsync(h_cnt, cnt, sizeof h_cnt, hipMemcpyDeviceToHost, s) != hipSuccess ||
-        hipStreamSynchronize(s) != hipSuccess)
-        return bail(fail(TCA_ERR_HIP, "planning kernels failed"));
-    const int n_long = h_cnt[0], end_wide = h_cnt[1], end_row = h_cnt[2];
-    // segment slots of the long rows: exclusive sum of their segment counts
-    int seg_total = 0;
-    if (n_long > 0) {
-        if ((st = dev_upload(&nseg, nullptr, static_cast<size_t>(n_long) + 1)) ||
-            (st = dev_upload(&segoff, nullptr, static_cast<size_t>(n_long) + 1)))
-            return bail(st);
-        if (hipMemsetAsync(nseg, 0, sizeof(int) * (static_cast<size_t>(n_long) + 1), s) != hipSuccess)
+        // temporaries of the planning, freed on every exit
+        uint32_t *keys = nullptr, *keys_s = nullptr, *bm = nullptr, *ekeys = nullptr, *ekeys_s = nullptr;
+        int *rows = nullptr, *rows_s = nullptr, *cnt = nullptr, *nseg = nullptr, *segoff = nullptr;
+        int *wordpre = nullptr, *scnt = nullptr, *wstat = nullptr, *wmap = nullptr, *wgbase = nullptr, *evals = nullptr,
+            *evals_s = nullptr;
+        uint8_t* start = nullptr;
+        void* tmp = nullptr;
+        auto bail = [&](int st) {
+            (void)hipStreamSynchronize(s);
+            for (void* q : {(void*)keys, (void*)keys_s, (void*)rows, (void*)rows_s, (void*)cnt, (void*)nseg, (void*)segoff,
+                            (void*)start, tmp, (void*)bm, (void*)ekeys, (void*)ekeys_s, (void*)wordpre, (void*)scnt,
+                            (void*)wstat, (void*)wmap, (void*)wgbase, (void*)evals, (void*)evals_s})
+                (void)hipFree(q);
+            return st;  // on failure `hold` frees the plan
+        };
+        int st;
+        // The plan owns its copy of the structure (row kernel and SDDMM read it).
+        if ((st = dev_upload(&p->d_rowptr, nullptr, static_cast<size_t>(M) + 1))) return bail(st);
+        if ((st = dev_upload(&p->d_colidx, nullptr, static_cast<size_t>(nnz)))) return bail(st);
+        if (hipMemcpyAsync(p->d_rowptr, d_rowptr, sizeof(int) * (static_cast<size_t>(M) + 1), hipMemcpyDeviceToDevice, s) !=
+                hipSuccess ||
+            (nnz > 0 && hipMemcpyAsync(p->d_colidx, d_colidx, sizeof(int) * static_cast<size_t>(nnz),
+                                       hipMemcpyDeviceToDevice, s) != hipSuccess))
+            return bail(fail(TCA_ERR_HIP, "structure copy failed"));
+        // CSR checks
+        if ((st = dev_upload(&cnt, nullptr, 4))) return bail(st);  // [0..2] bounds, [3] error bits
+        if ((st = dev_upload(&start, nullptr, static_cast<size_t>(nnz) + 1))) return bail(st);
+        if (hipMemsetAsync(cnt, 0, 4 * sizeof(int), s) != hipSuccess ||
+            hipMemsetAsync(start, 0, static_cast<size_t>(nnz) + 1, s) != hipSuccess)
             return bail(fail(TCA_ERR_HIP, "hipMemsetAsync failed"));
-        hipLaunchKernelGGL(dp_nseg_kernel, grid_for(n_long), blk, 0, s, keys_s, n_long, p->rows.seg_len, nseg);
-        (void)hipFree(tmp);
-        tmp = nullptr;
-        size_t tmp_bytes = 0;
-        if (rocprim::exclusive_scan(nullptr, tmp_bytes, nseg, segoff, 0, static_cast<size_t>(n_long) + 1,
-                                    rocprim::plus<int>(), s) != hipSuccess ||
-            hipMalloc(&tmp, tmp_bytes) != hipSuccess ||
-            rocprim::exclusive_scan(tmp, tmp_bytes, nseg, segoff, 0, static_cast<size_t>(n_long) + 1, rocprim::plus<int>(),
-                                    s) != hipSuccess ||
-            hipMemcpyAsync(&seg_total, segoff + n_long, sizeof(int), hipMemcpyDeviceToHost, s) != hipSuccess ||
+        const dim3 blk(256);
+        auto grid_for = [](int64_t n) { return dim3(static_cast<unsigned>(std::min<int64_t>((n + 255) / 256, 65536))); };
+        if (M > 0) {
+            hipLaunchKernelGGL(dp_check_rows_kernel, grid_for(M), blk, 0, s, p->d_rowptr, M, nnz, start, cnt + 3);
+            if (nnz > 0) hipLaunchKernelGGL(dp_check_cols_kernel, grid_for(nnz), blk, 0, s, p->d_colidx, nnz, K, start, cnt + 3);
+        }
+        int h_cnt[4] = {0, 0, 0, 0};
+        // the columns index the window bitmaps below: validate first
+        if (hipMemcpyAsync(h_cnt, cnt, sizeof h_cnt, hipMemcpyDeviceToHost, s) != hipSuccess ||
             hipStreamSynchronize(s) != hipSuccess)
-            return bail(fail(TCA_ERR_HIP, "segment scan failed"));
-    }
-    const int n_wide = end_wide - n_long, n_row = end_row - end_wide, n_short = Mp - end_row;
-    const int n_multi = (n_short + slots - 1) / slots;
-    p->ntasks = 4 * n_wide + seg_total + n_row + n_multi;
-    p->rows.n_wide = 4 * n_wide;
-    p->rows.n_seg = seg_total;
-    p->rows.n_rowtasks = n_row;
-    p->rows.n_multi = n_multi;
-    p->n_longrows = n_long;
-    p->n_seg_total = static_cast<size_t>(seg_total);
-    p->n_perm = n_short;
-    if ((st = dev_upload(&p->d_tasks, nullptr, p->ntasks)) || (st = dev_upload(&p->d_perm, nullptr, n_short)) ||
-        (st = dev_upload(&p->d_longrows, nullptr, n_long)) ||
-        (!(flags & TCA_PLAN_NO_SCRATCH) && (st = dev_upload(&p->d_partials, nullptr, p->n_seg_total * N))))
-        return bail(st);
-    if (Mp > 0) {
-        DpEmitArgs ea;
-        ea.rowptr = p->d_rowptr;
-        ea.len = keys_s;
-        ea.rows = rows_s;
-        ea.segoff = segoff;
-        ea.tasks = p->d_tasks;
-        ea.perm = p->d_perm;
-        ea.longrows = p->d_longrows;
-        ea.M = Mp;
-        ea.n_long = n_long;
-        ea.end_wide = end_wide;
-        ea.end_row = end_row;
-        ea.slots = slots;
-        ea.seg_total = seg_total;
-        hipLaunchKernelGGL(dp_emit_kernel, grid_for(Mp), blk, 0, s, ea);
-    }
-    if (hipGetLastError() != hipSuccess || hipStreamSynchronize(s) != hipSuccess)
-        return bail(fail(TCA_ERR_HIP, "task emission failed"));
-    st = bail(TCA_OK);  // frees the temporaries only
-    fill_info(p);
-    p->info.plan_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
-    *plan = p;
-    return TCA_OK;
+            return bail(fail(TCA_ERR_HIP, "CSR checks failed"));
+        if (h_cnt[3] & 1) return bail(fail(TCA_ERR_INVALID, "CSR row offsets are not 0 .. nnz non-decreasing"));
+        if (h_cnt[3] & 2) return bail(fail(TCA_ERR_INVALID, "CSR columns out of range or not strictly ascending in a row"));
+
+        // MFMA windows: statistics on the GPU, the host planner's routing, then
+        // dense tiles (natural column order when the windows cover most of K,
+        // else condensed) built on the GPU.  Needs fp16 / bf16, N % 8 == 0 and
+        // window bitmaps of at most kDevBitmapWords words.
+        int32_t rows_mfma = 0;
+        {
+            constexpr size_t kDevBitmapWords = size_t(1) << 25;  // 128 MiB per table
+            const int nw = (M + kDmaWinRows - 1) / kDmaWinRows, kw = (K + 31) / 32;
+            if ((flags & TCA_PLAN_NO_MFMA) == 0 && dtype != TCA_F32 && N % 8 == 0 && M > 0 && nnz > 0 &&
+                static_cast<size_t>(nw) * kw <= kDevBitmapWords) {
+                const size_t nb = static_cast<size_t>(nw) * kw;
+                if ((st = dev_upload(&bm, nullptr, nb)) || (st = dev_upload(&wordpre, nullptr, nb)) ||
+                    (st = dev_upload(&scnt, nullptr, nb)) || (st = dev_upload(&wstat, nullptr, 3 * static_cast<size_t>(nw) + 1)))
+                    return bail(st);
+                if (hipMemsetAsync(bm, 0, nb * 4, s) != hipSuccess || hipMemsetAsync(scnt, 0, nb * 4, s) != hipSuccess)
+                    return bail(fail(TCA_ERR_HIP, "hipMemsetAsync failed"));
+                int* const ucount = wstat;
+                int* const maxper = wstat + nw;
+                int* const wrow = wstat + 2 * nw;  // nw + 1
+                const dim3 rgrid(static_cast<unsigned>(std::min<int64_t>((static_cast<int64_t>(M) + 3) / 4, 65536)));
+                hipLaunchKernelGGL(dm_bitmap_kernel, rgrid, blk, 0, s, p->d_rowptr, p->d_colidx, M, kw, bm);
+                hipLaunchKernelGGL(dm_union_kernel, dim3(nw), blk, 0, s, p->d_rowptr, M, nw, kw, bm, wordpre, ucount, wrow);
+                hipLaunchKernelGGL(dm_stepcount_kernel, rgrid, blk, 0, s, p->d_rowptr, p->d_colidx, M, kw, bm, wordpre,
+                                   scnt);
+                hipLaunchKernelGGL(dm_stepmax_kernel, dim3(nw), blk, 0, s, scnt, kw, ucount, maxper);
+                std::vector<int> h(3 * static_cast<size_t>(nw) + 1);
+                if (hipMemcpyAsync(h.data(), wstat, sizeof(int) * h.size(), hipMemcpyDeviceToHost, s) != hipSuccess ||
+                    hipStreamSynchronize(s) != hipSuccess)
+                    return bail(fail(TCA_ERR_HIP, "window statistics failed"));
+                std::vector<WinStat> ws(nw);
+                for (int w = 0; w < nw; w++)
+                    ws[w] = {static_cast<int64_t>(h[2 * nw + w + 1]) - h[2 * nw + w], h[w], h[nw + w]};
+                const char* md = std::getenv("TCA_MFMA_MIN_DENSITY");
+                std::vector<uint8_t> take;
+                route_windows(ws, M, nnz, N, (flags & TCA_PLAN_FORCE_MFMA) != 0, md ? std::atof(md) : kMfmaMinDensity,
+                              mfma_shape(flags), &take);
+                // the host planner's choice between natural and condensed dense tiles
+                std::vector<int> h_wmap(nw, -1), h_base;
+                int64_t cond_cols = 0, steps_all = 0, nz_take = 0;
+                int n_take = 0;
+                for (int w = 0; w < nw; w++) {
+                    if (!take[w]) continue;
+                    h_wmap[w] = n_take++;
+                    const int steps = (h[w] + 31) / 32;
+                    h_base.push_back(static_cast<int>(steps_all));
+                    steps_all += steps;
+                    cond_cols += static_cast<int64_t>(steps) * 32;
+                    nz_take += ws[w].nz;
+                    rows_mfma += std::min(M, (w + 1) * kDmaWinRows) - w * kDmaWinRows;
+                }
+                const int32_t ksteps = (K + 31) / 32;
+                const bool natural = n_take > 0 &&
+                                     static_cast<double>(cond_cols) >= kNaturalCover * static_cast<double>(n_take) * K &&
+                                     static_cast<size_t>(n_take) * ksteps * kDnATileBytes <= kDenseMaxBytes;
+                if (natural) {
+                    for (int t = 0; t < n_take; t++) h_base[t] = t * ksteps;
+                    steps_all = static_cast<int64_t>(n_take) * ksteps;
+                    cond_cols = steps_all * 32;
+                }
+                if (n_take > 0 && static_cast<size_t>(steps_all) * kDnATileBytes > kDenseMaxBytes) {
+                    n_take = 0;  // past the dense-tile budget: every row on the row kernel
+                    rows_mfma = 0;
+                }
+                if (n_take > 0) {
+                    std::vector<Int4> win;
+                    for (int w = 0; w < nw; w++)
+                        if (h_wmap[w] >= 0) {
+                            const int t = h_wmap[w];
+                            win.push_back({w * kDmaWinRows, natural ? ksteps : (h[w] + 31) / 32, h_base[t], h[2 * nw + w]});
+                        }
+                    if ((st = dev_upload(&wmap, h_wmap.data(), h_wmap.size())) ||
+                        (st = dev_upload(&wgbase, h_base.data(), h_base.size())) ||
+                        (st = dev_upload(&p->d_windows, win.data(), win.size())) ||
+                        (st = dev_upload(&ekeys, nullptr, nnz)) || (st = dev_upload(&ekeys_s, nullptr, nnz)) ||
+                        (st = dev_upload(&evals, nullptr, nnz)) || (st = dev_upload(&evals_s, nullptr, nnz)))
+                        return bail(st);
+                    DmEntryArgs ea;
+                    ea.rowptr = p->d_rowptr;
+                    ea.colidx = p->d_colidx;
+                    ea.bm = bm;
+                    ea.wordpre = wordpre;
+                    ea.wmap = wmap;
+                    ea.wgbase = wgbase;
+                    ea.keys = ekeys;
+                    ea.vals = evals;
+                    ea.M = M;
+                    ea.kw = kw;
+                    ea.natural = natural ? 1 : 0;
+                    hipLaunchKernelGGL(dm_entries_kernel, rgrid, blk, 0, s, ea);
+                    // ascending positions: the routed nonzeros first, in the host planner's order
+                    size_t tmp_bytes = 0;
+                    if (rocprim::radix_sort_pairs(nullptr, tmp_bytes, ekeys, ekeys_s, evals, evals_s,
+                                                  static_cast<size_t>(nnz), 0, 32, s) != hipSuccess ||
+                        dev_malloc(reinterpret_cast<void**>(&tmp), tmp_bytes) != hipSuccess ||
+                        rocprim::radix_sort_pairs(tmp, tmp_bytes, ekeys, ekeys_s, evals, evals_s, static_cast<size_t>(nnz),
+                                                  0, 32, s) != hipSuccess)
+                        return bail(fail(TCA_ERR_HIP, "entry sort failed"));
+                    (void)hipFree(tmp);
+                    tmp = nullptr;
+                    p->n_dn = static_cast<int32_t>(nz_take);
+                    if ((st = dev_upload(&p->d_dn_pos, nullptr, static_cast<size_t>(nz_take))) ||
+                        (st = dev_upload(&p->d_dn_src, nullptr, static_cast<size_t>(nz_take))))
+                        return bail(st);
+                    if (hipMemcpyAsync(p->d_dn_pos, ekeys_s, 4 * static_cast<size_t>(nz_take), hipMemcpyDeviceToDevice, s) !=
+                            hipSuccess ||
+                        hipMemcpyAsync(p->d_dn_src, evals_s, 4 * static_cast<size_t>(nz_take), hipMemcpyDeviceToDevice, s) !=
+                            hipSuccess)
+                        return bail(fail(TCA_ERR_HIP, "entry copy failed"));
+                    if (!natural) {
+                        if ((st = dev_upload(&p->d_ucols, nullptr, static_cast<size_t>(steps_all) * 32))) return bail(st);
+                        p->n_ucols = static_cast<size_t>(steps_all) * 32;
+                        if (hipMemsetAsync(p->d_ucols, 0xff, 4 * static_cast<size_t>(steps_all) * 32, s) != hipSuccess)
+                            return bail(fail(TCA_ERR_HIP, "hipMemsetAsync failed"));
+                        hipLaunchKernelGGL(dm_ucols_kernel, grid_for(static_cast<int64_t>(nw) * kw), blk, 0, s, nw, kw, bm,
+                                           wordpre, wmap, wgbase, N, p->d_ucols);
+                    }
+                    p->adense_halves = static_cast<size_t>(steps_all) * kDmaATile + 512;
+                    if ((st = dev_upload(&p->d_adense, nullptr, p->adense_halves))) return bail(st);
+                    if (hipMemsetAsync(p->d_adense, 0, p->adense_halves * 2, s) != hipSuccess)
+                        return bail(fail(TCA_ERR_HIP, "hipMemsetAsync of the dense tiles failed"));
+                    p->mfma.win_rows = kDmaWinRows;
+                    p->mfma.windows = std::move(win);
+                    p->mfma.rows = rows_mfma;
+                    p->mfma.nnz = nz_take;
+                    p->mfma.cond_cols = cond_cols;
+                    p->mfma_dense = true;
+                    p->mfma_natural = natural;
+                    p->mfma_col_blocks = (N + kDmaTileCols - 1) / kDmaTileCols;
+                }
+            }
+        }
+        if (p->mfma.windows.empty()) p->flags |= TCA_PLAN_NO_MFMA;
+        const int Mp = M - rows_mfma;  // rows of the row kernel
+
+        // rows longest first (stable descending radix sort of length + 1; rows of
+        // the routed windows have key 0 and sort last)
+        if (M > 0) {
+            if ((st = dev_upload(&keys, nullptr, M)) || (st = dev_upload(&keys_s, nullptr, M)) ||
+                (st = dev_upload(&rows, nullptr, M)) || (st = dev_upload(&rows_s, nullptr, M)))
+                return bail(st);
+            hipLaunchKernelGGL(dp_lengths_kernel, grid_for(M), blk, 0, s, p->d_rowptr, M,
+                               p->mfma.windows.empty() ? nullptr : wmap, keys, rows);
+            size_t tmp_bytes = 0;
+            if (rocprim::radix_sort_pairs_desc(nullptr, tmp_bytes, keys, keys_s, rows, rows_s, static_cast<size_t>(M), 0, 32,
+                                               s) != hipSuccess)
+                return bail(fail(TCA_ERR_HIP, "radix sort sizing failed"));
+            if (dev_malloc(reinterpret_cast<void**>(&tmp), tmp_bytes) != hipSuccess)
+            return bail(fail(TCA_ERR_ALLOC, "radix sort workspace"));
+            if (rocprim::radix_sort_pairs_desc(tmp, tmp_bytes, keys, keys_s, rows, rows_s, static_cast<size_t>(M), 0, 32, s) !=
+                hipSuccess)
+                return bail(fail(TCA_ERR_HIP, "radix sort failed"));
+            if (Mp > 0)
+                hipLaunchKernelGGL(dp_bounds_kernel, dim3(1), dim3(64), 0, s, keys_s, Mp, p->rows.wide_len, p->rows.row_len,
+                                   p->rows.multi_max, cnt);
+        }
+        if (hipMemcpyAsync(h_cnt, cnt, sizeof h_cnt, hipMemcpyDeviceToHost, s) != hipSuccess ||
+            hipStreamSynchronize(s) != hipSuccess)
+            return bail(fail(TCA_ERR_HIP, "planning kernels failed"));
+        const int n_long = h_cnt[0], end_wide = h_cnt[1], end_row = h_cnt[2];
+        // segment slots of the long rows: exclusive sum of their segment counts
+        int seg_total = 0;
+        if (n_long > 0) {
+            if ((st = dev_upload(&nseg, nullptr, static_cast<size_t>(n_long) + 1)) ||
+                (st = dev_upload(&segoff, nullptr, static_cast<size_t>(n_long) + 1)))
+                return bail(st);
+            if (hipMemsetAsync(nseg, 0, sizeof(int) * (static_cast<size_t>(n_long) + 1), s) != hipSuccess)
+                return bail(fail(TCA_ERR_HIP, "hipMemsetAsync failed"));
+            hipLaunchKernelGGL(dp_nseg_kernel, grid_for(n_long), blk, 0, s, keys_s, n_long, p->rows.seg_len, nseg);
+            (void)hipFree(tmp);
+            tmp = nullptr;
+            size_t tmp_bytes = 0;
+            if (rocprim::exclusive_scan(nullptr, tmp_bytes, nseg, segoff, 0, static_cast<size_t>(n_long) + 1,
+                                        rocprim::plus<int>(), s) != hipSuccess ||
+                dev_malloc(reinterpret_cast<void**>(&tmp), tmp_bytes) != hipSuccess ||
+                rocprim::exclusive_scan(tmp, tmp_bytes, nseg, segoff, 0, static_cast<size_t>(n_long) + 1, rocprim::plus<int>(),
+                                        s) != hipSuccess ||
+                hipMemcpyAsync(&seg_total, segoff + n_long, sizeof(int), hipMemcpyDeviceToHost, s) != hipSuccess ||
+                hipStreamSynchronize(s) != hipSuccess)
+                return bail(fail(TCA_ERR_HIP, "segment scan failed"));
+        }
+        const int n_wide = end_wide - n_long, n_row = end_row - end_wide, n_short = Mp - end_row;
+        const int n_multi = (n_short + slots - 1) / slots;
+        p->ntasks = 4 * n_wide + seg_total + n_row + n_multi;
+        p->rows.n_wide = 4 * n_wide;
+        p->rows.n_seg = seg_total;
+        p->rows.n_rowtasks = n_row;
+        p->rows.n_multi = n_multi;
+        p->n_longrows = n_long;
+        p->n_seg_total = static_cast<size_t>(seg_total);
+        p->n_perm = n_short;
+        if ((st = dev_upload(&p->d_tasks, nullptr, p->ntasks)) || (st = dev_upload(&p->d_perm, nullptr, n_short)) ||
+            (st = dev_upload(&p->d_longrows, nullptr, n_long)) ||
+            (!(flags & TCA_PLAN_NO_SCRATCH) && (st = dev_upload(&p->d_partials, nullptr, p->n_seg_total * N))))
+            return bail(st);
+        if (Mp > 0) {
+            DpEmitArgs ea;
+            ea.rowptr = p->d_rowptr;
+            ea.len = keys_s;
+            ea.rows = rows_s;
+            ea.segoff = segoff;
+            ea.tasks = p->d_tasks;
+            ea.perm = p->d_perm;
+            ea.longrows = p->d_longrows;
+            ea.M = Mp;
+            ea.n_long = n_long;
+            ea.end_wide = end_wide;
+            ea.end_row = end_row;
+            ea.slots = slots;
+            ea.seg_total = seg_total;
+            hipLaunchKernelGGL(dp_emit_kernel, grid_for(Mp), blk, 0, s, ea);
+        }
+        if (hipGetLastError() != hipSuccess || hipStreamSynchronize(s) != hipSuccess)
+            return bail(fail(TCA_ERR_HIP, "task emission failed"));
+        st = bail(TCA_OK);  // frees the temporaries only
+        fill_info(p);
+        p->info.plan_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+        *plan = hold.release();
+        return TCA_OK;
+    });
 }
 
 int tca_spmm_plan_export_rows(const tca_spmm_plan* p, int32_t* n_tasks, int32_t* n_perm, int32_t* n_long,
@@ -1396,48 +1417,50 @@ int tca_spmm_time_phases(const tca_spmm_plan* p, const void* d_val, const void* 
 int tca_spmm_host(const int32_t* rowptr, const int32_t* colidx, const void* val, int32_t M, int32_t K, int32_t nnz,
                   const void* B, float* C, int32_t N, int32_t dtype, int32_t n_iter, int32_t verbose,
                   double* elapsed_ms) {
-    if (!rowptr || (nnz > 0 && (!colidx || !val)) || !B || !C || n_iter < 1)
-        return fail(TCA_ERR_INVALID, "tca_spmm_host: bad argument");
-    if (!dtype_ok(dtype)) return fail(TCA_ERR_INVALID, "unknown dtype %d", dtype);
-    const size_t es = dtype_size(dtype);
-    void *dval = nullptr, *dB = nullptr;
-    float* dC = nullptr;
-    tca_spmm_plan* plan = nullptr;
-    int st = TCA_OK;
-    auto cleanup = [&](int s) {
-        (void)hipFree(dval);
-        (void)hipFree(dB);
-        (void)hipFree(dC);
-        tca_spmm_plan_destroy(plan);
-        return s;
-    };
-    // Device copies of the operands (reference src/our_spmm.cu:503-525; C is
-    // not copied in: every row of C is written).
-    if (hipMalloc(&dval, es * std::max(nnz, 1)) != hipSuccess ||
-        hipMalloc(&dB, es * static_cast<size_t>(K) * N) != hipSuccess ||
-        hipMalloc(reinterpret_cast<void**>(&dC), sizeof(float) * std::max<size_t>(static_cast<size_t>(M) * N, 1)) !=
-            hipSuccess)
-        return cleanup(fail(TCA_ERR_ALLOC, "tca_spmm_host: device allocation failed"));
-    if ((nnz > 0 && hipMemcpy(dval, val, es * nnz, hipMemcpyHostToDevice) != hipSuccess) ||
-        hipMemcpy(dB, B, es * static_cast<size_t>(K) * N, hipMemcpyHostToDevice) != hipSuccess)
-        return cleanup(fail(TCA_ERR_HIP, "tca_spmm_host: H2D copy failed"));
-    const auto t0 = std::chrono::steady_clock::now();
-    st = tca_spmm_plan_create(rowptr, colidx, M, K, nnz, N, dtype, TCA_PLAN_DEFAULT, &plan);
-    const auto t1 = std::chrono::steady_clock::now();
-    if (st) return cleanup(st);
-    if (verbose) {
-        // Same two lines as reference our_spmm_balanced (src/our_spmm.cu:549,552),
-        // describing this build's plan: the row kernel's grid, block and LDS.
-        std::printf("preprocess %fms taken\n", std::chrono::duration<float, std::milli>(t1 - t0).count());
-        print_launches(plan);
-    }
-    float ms = 0.f;
-    st = tca_spmm_time(plan, dval, dB, dC, nullptr, 5, n_iter, &ms);
-    if (st) return cleanup(st);
-    if (hipMemcpy(C, dC, sizeof(float) * static_cast<size_t>(M) * N, hipMemcpyDeviceToHost) != hipSuccess)
-        return cleanup(fail(TCA_ERR_HIP, "tca_spmm_host: D2H copy failed"));
-    if (elapsed_ms) *elapsed_ms = ms;
-    return cleanup(TCA_OK);
+    return api_guard("tca_spmm_host", [&]() -> int {
+        if (!rowptr || (nnz > 0 && (!colidx || !val)) || !B || !C || n_iter < 1)
+            return fail(TCA_ERR_INVALID, "tca_spmm_host: bad argument");
+        if (!dtype_ok(dtype)) return fail(TCA_ERR_INVALID, "unknown dtype %d", dtype);
+        const size_t es = dtype_size(dtype);
+        void *dval = nullptr, *dB = nullptr;
+        float* dC = nullptr;
+        tca_spmm_plan* plan = nullptr;
+        int st = TCA_OK;
+        auto cleanup = [&](int s) {
+            (void)hipFree(dval);
+            (void)hipFree(dB);
+            (void)hipFree(dC);
+            tca_spmm_plan_destroy(plan);
+            return s;
+        };
+        // Device copies of the operands (reference src/our_spmm.cu:503-525; C is
+        // not copied in: every row of C is written).
+        if (dev_malloc(reinterpret_cast<void**>(&dval), es * std::max(nnz, 1)) != hipSuccess ||
+            dev_malloc(reinterpret_cast<void**>(&dB), es * static_cast<size_t>(K) * N) != hipSuccess ||
+            dev_malloc(reinterpret_cast<void**>(&dC), sizeof(float) * std::max<size_t>(static_cast<size_t>(M) * N, 1)) !=
+                hipSuccess)
+            return cleanup(fail(TCA_ERR_ALLOC, "tca_spmm_host: device allocation failed"));
+        if ((nnz > 0 && hipMemcpy(dval, val, es * nnz, hipMemcpyHostToDevice) != hipSuccess) ||
+            hipMemcpy(dB, B, es * static_cast<size_t>(K) * N, hipMemcpyHostToDevice) != hipSuccess)
+            return cleanup(fail(TCA_ERR_HIP, "tca_spmm_host: H2D copy failed"));
+        const auto t0 = std::chrono::steady_clock::now();
+        st = tca_spmm_plan_create(rowptr, colidx, M, K, nnz, N, dtype, TCA_PLAN_DEFAULT, &plan);
+        const auto t1 = std::chrono::steady_clock::now();
+        if (st) return cleanup(st);
+        if (verbose) {
+            // Same two lines as reference our_spmm_balanced (src/our_spmm.cu:549,552),
+            // describing this build's plan: the row kernel's grid, block and LDS.
+            std::printf("preprocess %fms taken\n", std::chrono::duration<float, std::milli>(t1 - t0).count());
+            print_launches(plan);
+        }
+        float ms = 0.f;
+        st = tca_spmm_time(plan, dval, dB, dC, nullptr, 5, n_iter, &ms);
+        if (st) return cleanup(st);
+        if (hipMemcpy(C, dC, sizeof(float) * static_cast<size_t>(M) * N, hipMemcpyDeviceToHost) != hipSuccess)
+            return cleanup(fail(TCA_ERR_HIP, "tca_spmm_host: D2H copy failed"));
+        if (elapsed_ms) *elapsed_ms = ms;
+        return cleanup(TCA_OK);
+    });
 }
 
 }  // extern "C"
