@@ -32,7 +32,8 @@ WORKLOADS = {
 
 # Kernels of each phase (tca_spmm_time_phases order); the tile and pack
 # kernels depend on the plan (tca_plan_info.tile_kernel).
-TILE_KERNELS = {3: "mfma_pair_kernel", 4: "mfma_dense_kernel", 5: "mfma_dense_kernel", 7: "mfma_compact_kernel"}
+TILE_KERNELS = {3: "mfma_pair_kernel", 4: "mfma_dense_kernel", 5: "mfma_dense_kernel", 7: "mfma_compact_kernel",
+                8: "mfma_short_kernel"}
 
 
 def phase_kernel(phase: str, tile_kernel: int) -> str:

@@ -67,11 +67,19 @@ typedef enum tca_status {
 #define TCA_PLAN_NO_PANELS 256u    /* no panels: rows outside MFMA windows go to the row kernel */
 #define TCA_PLAN_FORCE_PANELS 512u /* every eligible row in panels, whatever their reuse */
 #define TCA_PLAN_NO_SCRATCH 1024u  /* the plan keeps no partial-row scratch: run it with tca_spmm_run_static */
+/* Short-K matrix-core kernel (TCA_TILES_SHORT): fp16 / bf16, N % 8 == 0 and
+ * K <= 640: every row, in windows of 64 rows x 64 columns built in LDS from
+ * the CSR each run (no plan-time tiles, no pack kernel, one launch).  The
+ * default for such matrices whose rows hold at least max(8, 0.08 K)
+ * nonzeros on average; this flag asks for it whatever the row lengths.  TCA_PLAN_NO_MFMA and the
+ * other tile-kernel flags keep it off; on ineligible inputs it is ignored. */
+#define TCA_PLAN_MFMA_SHORT 2048u
 /* Every flag a plan accepts; other bits (4, 8 and 32 among them, once tile
  * kernel selectors) give TCA_ERR_INVALID. */
 #define TCA_PLAN_KNOWN_FLAGS                                                                            \
     (TCA_PLAN_NO_MFMA | TCA_PLAN_FORCE_MFMA | TCA_PLAN_MFMA_DENSE | TCA_PLAN_MFMA_PAIR |                \
-     TCA_PLAN_MFMA_COMPACT | TCA_PLAN_NO_PANELS | TCA_PLAN_FORCE_PANELS | TCA_PLAN_NO_SCRATCH)
+     TCA_PLAN_MFMA_COMPACT | TCA_PLAN_NO_PANELS | TCA_PLAN_FORCE_PANELS | TCA_PLAN_NO_SCRATCH |            \
+     TCA_PLAN_MFMA_SHORT)
 
 typedef struct tca_spmm_plan tca_spmm_plan;
 
@@ -119,6 +127,7 @@ typedef struct tca_plan_info {
 #define TCA_TILES_DENSE 4      /* dense condensed tiles (TCA_PLAN_MFMA_DENSE) */
 #define TCA_TILES_DENSE_K 5    /* dense tiles spanning all of K (default when the windows cover most of K) */
 #define TCA_TILES_COMPACT 7    /* dense tiles with compacted steps (TCA_PLAN_MFMA_COMPACT) */
+#define TCA_TILES_SHORT 8      /* short-K kernel over every row (TCA_PLAN_MFMA_SHORT; default when K <= 640) */
 
 /* Replaces reference workload_manager (src/our_spmm.cu:353-477) plus the
  * device uploads of our_spmm_balanced (src/our_spmm.cu:503-525).

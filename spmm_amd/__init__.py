@@ -20,12 +20,12 @@ from dataclasses import dataclass
 import numpy as np
 
 from . import _lib
-from ._lib import (TCA_BF16, TCA_F16, TCA_F32, TCA_PLAN_DEFAULT, TCA_PLAN_FORCE_MFMA, TCA_PLAN_MFMA_DENSE, TCA_PLAN_MFMA_PAIR, TCA_PLAN_MFMA_COMPACT, TCA_PLAN_NO_MFMA, TCA_PLAN_NO_PANELS, TCA_PLAN_FORCE_PANELS, TCA_PLAN_NO_SCRATCH, TCA_PLAN_KNOWN_FLAGS, TCA_TILES_NONE, TCA_TILES_PAIR, TCA_TILES_DENSE, TCA_TILES_DENSE_K, TCA_TILES_COMPACT,
+from ._lib import (TCA_BF16, TCA_F16, TCA_F32, TCA_PLAN_DEFAULT, TCA_PLAN_FORCE_MFMA, TCA_PLAN_MFMA_DENSE, TCA_PLAN_MFMA_PAIR, TCA_PLAN_MFMA_COMPACT, TCA_PLAN_NO_MFMA, TCA_PLAN_NO_PANELS, TCA_PLAN_FORCE_PANELS, TCA_PLAN_NO_SCRATCH, TCA_PLAN_KNOWN_FLAGS, TCA_PLAN_MFMA_SHORT, TCA_TILES_NONE, TCA_TILES_PAIR, TCA_TILES_DENSE, TCA_TILES_DENSE_K, TCA_TILES_COMPACT, TCA_TILES_SHORT,
                    TcaError,
                    call, lib, np_ptr)
 
 __all__ = ["CSR", "Plan", "TcaError", "TCA_F16", "TCA_F32", "TCA_BF16", "TCA_PLAN_DEFAULT", "TCA_PLAN_NO_MFMA", "TCA_PLAN_NO_PANELS", "TCA_PLAN_FORCE_PANELS", "TCA_PLAN_NO_SCRATCH",
-           "TCA_PLAN_FORCE_MFMA", "TCA_PLAN_MFMA_DENSE", "TCA_PLAN_MFMA_PAIR", "TCA_PLAN_MFMA_COMPACT", "TCA_PLAN_KNOWN_FLAGS", "TCA_TILES_NONE", "TCA_TILES_PAIR", "TCA_TILES_DENSE", "TCA_TILES_DENSE_K", "TCA_TILES_COMPACT", "read_smtx", "read_smtx_dense", "write_smtx", "read_mtx", "read_mtx_dense", "write_values", "write_csr_binary",
+           "TCA_PLAN_FORCE_MFMA", "TCA_PLAN_MFMA_DENSE", "TCA_PLAN_MFMA_PAIR", "TCA_PLAN_MFMA_COMPACT", "TCA_PLAN_KNOWN_FLAGS", "TCA_PLAN_MFMA_SHORT", "TCA_TILES_NONE", "TCA_TILES_PAIR", "TCA_TILES_DENSE", "TCA_TILES_DENSE_K", "TCA_TILES_COMPACT", "TCA_TILES_SHORT", "read_smtx", "read_smtx_dense", "write_smtx", "read_mtx", "read_mtx_dense", "write_values", "write_csr_binary",
            "read_csr_binary", "launch_floor", "dense_to_csr", "csr_to_bell", "bell_spmm", "prune_24", "csr_to_24", "spmm_24",
            "csr_to_dense", "compare_mat", "gen_config", "gen_dense", "gen_bernoulli", "gen_lognormal_rows",
            "gen_rmat", "gen_zipf_rows", "naive_csr_spmm", "plan_row_tasks", "plan_mfma_windows", "our_spmm_balanced", "condense_windows", "np_dtype",

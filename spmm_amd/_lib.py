@@ -24,11 +24,13 @@ TCA_PLAN_MFMA_COMPACT = 128
 TCA_PLAN_NO_PANELS = 256
 TCA_PLAN_FORCE_PANELS = 512
 TCA_PLAN_NO_SCRATCH = 1024
+TCA_PLAN_MFMA_SHORT = 2048
 TCA_PLAN_KNOWN_FLAGS = (TCA_PLAN_NO_MFMA | TCA_PLAN_FORCE_MFMA | TCA_PLAN_MFMA_DENSE | TCA_PLAN_MFMA_PAIR |
-                        TCA_PLAN_MFMA_COMPACT | TCA_PLAN_NO_PANELS | TCA_PLAN_FORCE_PANELS | TCA_PLAN_NO_SCRATCH)
+                        TCA_PLAN_MFMA_COMPACT | TCA_PLAN_NO_PANELS | TCA_PLAN_FORCE_PANELS | TCA_PLAN_NO_SCRATCH |
+                        TCA_PLAN_MFMA_SHORT)
 # tile kernel of a plan (tca_plan_info.tile_kernel)
 TCA_TILES_NONE, TCA_TILES_PAIR = 0, 3
-TCA_TILES_DENSE, TCA_TILES_DENSE_K, TCA_TILES_COMPACT = 4, 5, 7
+TCA_TILES_DENSE, TCA_TILES_DENSE_K, TCA_TILES_COMPACT, TCA_TILES_SHORT = 4, 5, 7, 8
 
 i32 = ctypes.c_int32
 i64 = ctypes.c_int64

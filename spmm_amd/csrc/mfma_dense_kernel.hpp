@@ -52,7 +52,6 @@ constexpr int kDnSlots = 3;                                   // ring slots
 constexpr int kDnLB = 3;                                      // transfer lookahead (iterations)
 constexpr int kDnOps = 3 * kDnSteps;                          // transfers per producer and iteration
 constexpr int kDnWait = (kDnLB - 2) * kDnOps;                 // tile i + 2 lands in iteration i
-constexpr int kXcds = 8;                                      // XCDs of the MI355X
 constexpr size_t kDenseMaxBytes = size_t(2) << 30;            // dense tiles a plan may keep
 constexpr double kNaturalCover = 0.85;  // windows covering this share of K keep all of K in column order
 

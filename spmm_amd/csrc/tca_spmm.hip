@@ -16,6 +16,7 @@
 #include "mfma_pair_kernel.hpp"
 #include "mfma_dense_kernel.hpp"
 #include "mfma_compact_kernel.hpp"
+#include "mfma_short_kernel.hpp"
 #include "bell_kernel.hpp"
 #include "sparse24_kernel.hpp"
 #include "device_planner.hpp"
@@ -42,6 +43,12 @@ struct tca_spmm_plan {
     MfmaPlan mfma;
     int32_t mfma_col_blocks = 0;
     bool mfma_pair = false;  // paired (MFMA + staging wavefront) tile kernel
+    bool mfma_short = false; // short-K kernel: every row, windows built in LDS (no pack, no windows table)
+    int32_t short_nwin = 0, short_col_blocks = 0, short_steps = 0;
+    uint32_t* d_zeros = nullptr;  // 16 zero bytes (short-K kernel: B rows past K, columns past N)
+    uint16_t* d_soff = nullptr;   // short-K kernel: per nonzero its half index in its window's A tiles
+    int32_t* d_wstart = nullptr;  // short-K kernel: [windows + 1] first nonzero of each window
+    std::vector<int32_t> short_wstart;  // the same on the host (kernel arguments when few windows)
     bool mfma_dense = false; // dense-tile kernel (plan keeps dense condensed windows)
     bool mfma_natural = false; // dense kernel: windows span all of K in column order (B rows contiguous)
     bool mfma_compact = false; // dense kernel on compacted steps (non-empty fragment cells only)
@@ -148,6 +155,9 @@ int dev_upload(T** dst, const void* src, size_t count) {
 }
 
 void free_plan_device(tca_spmm_plan* p) {
+    (void)hipFree(p->d_zeros);
+    (void)hipFree(p->d_soff);
+    (void)hipFree(p->d_wstart);
     (void)hipFree(p->d_rowptr);
     (void)hipFree(p->d_colidx);
     (void)hipFree(p->d_tasks);
@@ -262,7 +272,30 @@ static_assert(kMfmaDenseShape.win_rows == kDmaWinRows && kMfmaDenseShape.tile_co
 static_assert(kMfmaPairShape.max_step_entries <= 8 * kPairGroup, "paired kernel: at most 8 entry groups per step");
 static_assert(kPairThreads == kDnThreads, "tile kernels share one workgroup size");
 
-int launch_mfma(const tca_spmm_plan* p, const void* B, float* C, hipStream_t s) {
+int launch_short(const tca_spmm_plan* p, const void* val, const void* B, float* C, hipStream_t s) {
+    ShortArgs a;
+    a.wstart = p->d_wstart;
+    a.soff = p->d_soff;
+    a.val = static_cast<const uint16_t*>(val);
+    a.B = B;
+    a.C = C;
+    a.zeros = p->d_zeros;
+    a.M = p->M;
+    a.K = p->K;
+    a.N = p->N;
+    a.nwin = p->short_nwin;
+    a.col_blocks = p->short_col_blocks;
+    a.steps = p->short_steps;
+    if (a.nwin <= kShArgWindows)
+        for (int w = 0; w <= a.nwin; w++) a.wstart_arg[w] = p->short_wstart[w];
+    const dim3 grid(mfma_short_grid(a.nwin, a.col_blocks));
+    if (p->dtype == TCA_BF16) hipLaunchKernelGGL(mfma_short_kernel<true>, grid, dim3(kShThreads), 0, s, a);
+    else hipLaunchKernelGGL(mfma_short_kernel<false>, grid, dim3(kShThreads), 0, s, a);
+    return TCA_OK;
+}
+
+int launch_mfma(const tca_spmm_plan* p, const void* val, const void* B, float* C, hipStream_t s) {
+    if (p->mfma_short) return launch_short(p, val, B, C, s);
     if (p->mfma.windows.empty()) return TCA_OK;
     MfmaArgs a;
     a.windows = p->d_windows;
@@ -386,7 +419,7 @@ int launch_panels(const tca_spmm_plan* p, const void* val, const void* B, float*
 // W: the partial rows of split rows (plan-owned, or the static scratch).
 int run_phases(const tca_spmm_plan* p, const void* val, const void* B, float* C, float* W, hipStream_t s) {
     launch_pack(p, val, s);
-    int st = launch_mfma(p, B, C, s);
+    int st = launch_mfma(p, val, B, C, s);
     if (st) return st;
     st = launch_panels(p, val, B, C, W, s);
     if (st) return st;
@@ -442,7 +475,17 @@ void fill_info(tca_spmm_plan* p) {
     in.panel_lds_bytes = p->n_units ? panel_lds_bytes(16 * p->panels.elems * static_cast<int>(dtype_size(p->dtype))) +
                                           16 * p->panels.elems * static_cast<int>(dtype_size(p->dtype))
                                     : 0;
-    in.tile_kernel = p->mfma.windows.empty() ? TCA_TILES_NONE
+    if (p->mfma_short) {
+        in.n_windows_mfma = p->short_nwin;
+        in.rows_mfma = p->M;
+        in.nnz_mfma = p->nnz;
+        in.cond_cols_mfma = static_cast<int64_t>(p->short_nwin) * p->short_steps * kStepK;
+        in.mfma_blocks = mfma_short_grid(p->short_nwin, p->short_col_blocks);
+        in.mfma_blockdim = kShThreads;
+        in.mfma_lds_bytes = kShLdsBytes;
+    }
+    in.tile_kernel = p->mfma_short          ? TCA_TILES_SHORT
+                     : p->mfma.windows.empty() ? TCA_TILES_NONE
                      : p->mfma_compact      ? TCA_TILES_COMPACT
                      : p->mfma_dense        ? (p->mfma_natural ? TCA_TILES_DENSE_K : TCA_TILES_DENSE)
                                             : TCA_TILES_PAIR;
@@ -457,6 +500,7 @@ void print_launches(const tca_spmm_plan* p) {
     auto line = [](long long blocks, int dim, double lds_bytes, const char* name) {
         std::printf("num_block: %lld blockdim: %d shm: %fKB (%s)\n", blocks, dim, lds_bytes / 1024.0, name);
     };
+    if (p->mfma_short) line(in.mfma_blocks, in.mfma_blockdim, in.mfma_lds_bytes, "mfma_short_kernel");
     if (!p->mfma.windows.empty()) {
         if (p->mfma_dense) {
             if (p->n_dn > 0) line((p->n_dn + 255) / 256, 256, 0.0, "dense_pack_kernel");
@@ -464,7 +508,7 @@ void print_launches(const tca_spmm_plan* p) {
             line((p->n_pk_words + 1023) / 1024, 256, 0.0, "mfma_pack_kernel");
         }
         static const char* names[] = {"", "", "", "mfma_pair_kernel", "mfma_dense_kernel", "mfma_dense_kernel", "",
-                                      "mfma_compact_kernel"};
+                                      "mfma_compact_kernel", "mfma_short_kernel"};
         line(in.mfma_blocks, in.mfma_blockdim, in.mfma_lds_bytes, names[in.tile_kernel]);
     }
     if (p->n_units > 0) line(in.panel_blocks, in.panel_blockdim, in.panel_lds_bytes, "panel_kernel");
@@ -517,6 +561,58 @@ int tca_device_count(int32_t* count) {
     return TCA_OK;
 }
 
+// Routing of the short-K kernel: fp16 / bf16, N % 8 == 0, K <= 640, and by
+// default rows at least kShMinDensity full on average (and 8 nonzeros).  Its
+// cost per window grows with K (B staged, A zeroed, K / 32 MFMA steps), the
+// row kernel's with the nonzeros (one B-row gather each).  Measured on the
+// MI355X, fp16, N = 256 (short vs row kernel, per SpMM): 65536 x 512 at
+// 10 %: 71 vs 166 us; 16384 x 512 at 10 %: 19.2 vs 21.5; 2048 x 512 at
+// 10 %: 5.53 vs 5.51; 65536 x 256 at 5 % (N = 128): 27.3 vs 27.1;
+// 65536 x 640 at 2 %: 74 vs 38.  TCA_PLAN_MFMA_SHORT asks for it whatever
+// the density; the other tile-kernel flags and TCA_PLAN_NO_MFMA keep it off.
+constexpr double kShMinDensity = 0.08;
+static bool short_route(int32_t M, int32_t K, int32_t nnz, int32_t N, int32_t dtype, uint32_t flags) {
+    if (dtype == TCA_F32 || N % 8 != 0 || K > kShMaxSteps * kStepK || M == 0 || (flags & TCA_PLAN_NO_MFMA))
+        return false;
+    if (flags & TCA_PLAN_MFMA_SHORT) return true;
+    if (flags & (TCA_PLAN_MFMA_DENSE | TCA_PLAN_MFMA_PAIR | TCA_PLAN_MFMA_COMPACT)) return false;
+    const double per_row = static_cast<double>(nnz) / M;
+    return per_row >= 8.0 && per_row >= kShMinDensity * K;
+}
+
+// Half index of nonzero (row, col) in its window's A tiles (mfma_short_kernel.hpp).
+__host__ __device__ inline uint16_t short_soff(int32_t row, int32_t col) {
+    return static_cast<uint16_t>((col >> 5) * (kShATileBytes / 2) + a_cell(row % kShRows, col & 31));
+}
+
+// The short-K kernel's plan: sizes, zero bytes, per-nonzero tile offsets and
+// window starts (from the host structure).
+static int setup_short(tca_spmm_plan* p, const int32_t* rowptr, const int32_t* colidx) {
+    p->short_nwin = (p->M + kShRows - 1) / kShRows;
+    p->short_col_blocks = (p->N + kDmaTileCols - 1) / kDmaTileCols;
+    p->short_steps = (p->K + kStepK - 1) / kStepK;
+    const uint32_t z[4] = {0, 0, 0, 0};
+    int st = dev_upload(&p->d_zeros, z, 4);
+    if (st) return st;
+    std::vector<uint16_t> so(static_cast<size_t>(p->nnz));
+    for (int32_t r = 0; r < p->M; r++)
+        for (int32_t j = rowptr[r]; j < rowptr[r + 1]; j++) so[j] = short_soff(r, colidx[j]);
+    p->short_wstart.resize(static_cast<size_t>(p->short_nwin) + 1);
+    for (int32_t w = 0; w <= p->short_nwin; w++) p->short_wstart[w] = rowptr[std::min(w * kShRows, p->M)];
+    if ((st = dev_upload(&p->d_soff, so.data(), so.size()))) return st;
+    return dev_upload(&p->d_wstart, p->short_wstart.data(), p->short_wstart.size());
+}
+
+// Device planning of the same: one thread per row.
+__global__ void dp_short_kernel(const int32_t* __restrict__ rowptr, const int32_t* __restrict__ colidx, int32_t M,
+                                uint16_t* __restrict__ soff, int32_t* __restrict__ wstart) {
+    const int32_t r = blockIdx.x * 256 + threadIdx.x;
+    if (r > M) return;
+    if (r % kShRows == 0 || r == M) wstart[(r + kShRows - 1) / kShRows] = rowptr[r];
+    if (r == M) return;
+    for (int32_t j = rowptr[r]; j < rowptr[r + 1]; j++) soff[j] = short_soff(r, colidx[j]);
+}
+
 int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_t K, int32_t nnz,
                          int32_t N, int32_t dtype, uint32_t flags, tca_spmm_plan** plan) {
     return api_guard("tca_spmm_plan_create", [&]() -> int {
@@ -551,8 +647,11 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
         const char* md = std::getenv("TCA_MFMA_MIN_DENSITY");
         const MfmaShape* shape = &mfma_shape(flags);
         const double min_density = md ? std::atof(md) : kMfmaMinDensity;
-        plan_mfma(rowptr, colidx, M, N, dtype, (flags & TCA_PLAN_FORCE_MFMA) != 0, (flags & TCA_PLAN_NO_MFMA) != 0,
-                  min_density, *shape, &p->mfma);
+        // Short K (<= 640): every row on the short-K kernel (mfma_short_kernel.hpp).
+        p->mfma_short = short_route(M, K, nnz, N, dtype, flags);
+        if (!p->mfma_short)
+            plan_mfma(rowptr, colidx, M, N, dtype, (flags & TCA_PLAN_FORCE_MFMA) != 0, (flags & TCA_PLAN_NO_MFMA) != 0,
+                      min_density, *shape, &p->mfma);
         p->mfma_dense = (flags & (TCA_PLAN_MFMA_DENSE | TCA_PLAN_MFMA_COMPACT)) != 0;
         if ((flags & (TCA_PLAN_MFMA_DENSE | TCA_PLAN_MFMA_PAIR)) == 0 && !p->mfma.windows.empty() &&
             static_cast<double>(p->mfma.cond_cols) >= kNaturalCover * static_cast<double>(p->mfma.windows.size()) * K &&
@@ -582,9 +681,10 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
         }
         // Row panels with B staged in LDS for the rows outside MFMA windows, then
         // the row kernel for the rest.
-        plan_panels_routed(rowptr, colidx, M, K, N, dtype, flags, p->mfma.row_mfma, &p->panels);
-        std::vector<uint8_t> skip_rows(M, 0);
-        for (int32_t r = 0; r < M; r++)
+        if (!p->mfma_short) plan_panels_routed(rowptr, colidx, M, K, N, dtype, flags, p->mfma.row_mfma, &p->panels);
+        else p->panels.row_panel.assign(M, 0);
+        std::vector<uint8_t> skip_rows(M, p->mfma_short ? 1 : 0);
+        for (int32_t r = 0; r < M && !p->mfma_short; r++)
             skip_rows[r] = (!p->mfma.row_mfma.empty() && p->mfma.row_mfma[r]) || p->panels.row_panel[r];
         plan_rows(rowptr, M, N, static_cast<int32_t>(dtype_size(dtype)), skip_rows, default_slices(K, N, dtype),
                   &p->rows);
@@ -611,6 +711,7 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
 
         auto bail = [&](int s) { return s; };  // `hold` frees the plan
         if ((st = dev_upload(&p->d_rowptr, rowptr, static_cast<size_t>(M) + 1))) return bail(st);
+        if (p->mfma_short && (st = setup_short(p, rowptr, colidx))) return bail(st);
         if ((st = dev_upload(&p->d_colidx, colidx, static_cast<size_t>(nnz)))) return bail(st);
         if ((st = dev_upload(&p->d_tasks, p->rows.tasks.data(), p->rows.tasks.size()))) return bail(st);
         if ((st = dev_upload(&p->d_perm, p->rows.perm.data(), p->rows.perm.size()))) return bail(st);
@@ -882,6 +983,30 @@ int tca_spmm_plan_create_device(const int32_t* d_rowptr, const int32_t* d_colidx
             return bail(fail(TCA_ERR_HIP, "CSR checks failed"));
         if (h_cnt[3] & 1) return bail(fail(TCA_ERR_INVALID, "CSR row offsets are not 0 .. nnz non-decreasing"));
         if (h_cnt[3] & 2) return bail(fail(TCA_ERR_INVALID, "CSR columns out of range or not strictly ascending in a row"));
+        if (short_route(M, K, nnz, N, dtype, flags)) {
+            // short K: every row on the short-K kernel, which needs only the structure
+            p->mfma_short = true;
+            p->short_nwin = (M + kShRows - 1) / kShRows;
+            p->short_col_blocks = (N + kDmaTileCols - 1) / kDmaTileCols;
+            p->short_steps = (K + kStepK - 1) / kStepK;
+            const uint32_t z[4] = {0, 0, 0, 0};
+            if ((st = dev_upload(&p->d_zeros, z, 4)) ||
+                (st = dev_upload(&p->d_soff, nullptr, static_cast<size_t>(nnz))) ||
+                (st = dev_upload(&p->d_wstart, nullptr, static_cast<size_t>(p->short_nwin) + 1)))
+                return bail(st);
+            hipLaunchKernelGGL(dp_short_kernel, dim3((M + 256) / 256), dim3(256), 0, s, p->d_rowptr, p->d_colidx, M,
+                               p->d_soff, p->d_wstart);
+            p->short_wstart.resize(static_cast<size_t>(p->short_nwin) + 1);
+            if (hipMemcpyAsync(p->short_wstart.data(), p->d_wstart, sizeof(int32_t) * p->short_wstart.size(),
+                               hipMemcpyDeviceToHost, s) != hipSuccess ||
+                hipStreamSynchronize(s) != hipSuccess)
+                return bail(fail(TCA_ERR_HIP, "short-K planning failed"));
+            st = bail(TCA_OK);  // frees the temporaries only
+            fill_info(p);
+            p->info.plan_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+            *plan = hold.release();
+            return TCA_OK;
+        }
 
         // MFMA windows: statistics on the GPU, the host planner's routing, then
         // dense tiles (natural column order when the windows cover most of K,
@@ -1385,7 +1510,7 @@ int tca_spmm_time_phases(const tca_spmm_plan* p, const void* d_val, const void* 
     }
     int st = TCA_OK;
     const bool used[TCA_PHASES] = {!p->mfma.windows.empty() && (!p->mfma.entries.empty() || p->n_dn > 0),
-                                   !p->mfma.windows.empty(),
+                                   !p->mfma.windows.empty() || p->mfma_short,
                                    p->ntasks > 0, p->n_longrows > 0, p->n_units > 0};
     for (int k = 0; k < TCA_PHASES && st == TCA_OK; k++) {
         if (!used[k]) continue;
@@ -1393,7 +1518,7 @@ int tca_spmm_time_phases(const tca_spmm_plan* p, const void* d_val, const void* 
         for (int i = 0; i < iters && st == TCA_OK; i++) {
             switch (k) {
                 case TCA_PHASE_PACK: launch_pack(p, d_val, s); break;
-                case TCA_PHASE_TILES: st = launch_mfma(p, d_B, d_C, s); break;
+                case TCA_PHASE_TILES: st = launch_mfma(p, d_val, d_B, d_C, s); break;
                 case TCA_PHASE_ROWS: st = launch_rows(p, d_val, d_B, d_C, p->d_partials, s); break;
                 case TCA_PHASE_PANELS: st = launch_panels(p, d_val, d_B, d_C, p->d_partials, s); break;
                 default: launch_finalize(p, d_C, p->d_partials, s); break;

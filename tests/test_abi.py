@@ -105,7 +105,7 @@ def test_python_constants_match_the_header():
     # TCA_PLAN_KNOWN_FLAGS: the OR of the flags its definition names
     m = re.search(r"#define TCA_PLAN_KNOWN_FLAGS\s*\\?\s*\(([^)]*)\)", head)
     names = re.findall(r"TCA_PLAN_\w+", m.group(1))
-    assert len(names) == 8
+    assert len(names) == 9
     want = 0
     for name in names:
         want |= getattr(S, name)

@@ -161,3 +161,35 @@ def test_device_plan_rejects_invalid_structure(torch_cuda, bad):
     with pytest.raises(S.TcaError) as ei:
         S.Plan.from_device(_dev(torch, rowptr), _dev(torch, colidx), 3, 5, 5, 64, S.TCA_F32)
     assert ei.value.status == 1
+
+
+@pytest.mark.parametrize("m,k,p,n", [(2048, 512, 0.1, 256), (1000, 97, 0.3, 136), (70, 640, 0.2, 8)])
+def test_device_short_k_plan_equals_host_plan(torch_cuda, m, k, p, n):
+    """Short K: host and device planners both route every row to the short-K
+    kernel (the same windows and launch), and the products are bit-identical
+    and equal to the oracle on exact inputs."""
+    torch = torch_cuda
+    print(f"device short-K plan: M={m} K={k} p={p} N={n}", flush=True)
+    rng = np.random.default_rng(m + k)
+    a = S.gen_bernoulli(m, k, p, seed=m, dtype=S.TCA_F16)[0]
+    v = rng.choice(np.array([-2.0, -1.0, -0.5, 0.5, 1.0, 2.0], np.float32), size=a.nnz)
+    a = S.CSR(a.nrow, a.ncol, a.rowptr, a.colidx, S.to_storage(v, a.dtype), a.dtype)
+    b = S.to_storage(exact_dense(rng, (k, n)), a.dtype)
+    with S.Plan(a, n) as hp:
+        dp = S.Plan.from_device(_dev(torch, a.rowptr), _dev(torch, a.colidx), m, k, a.nnz, n, a.dtype)
+        try:
+            hi, di = hp.info(), dp.info()
+            for key in ("tile_kernel", "n_windows_mfma", "rows_mfma", "nnz_mfma", "mfma_blocks", "n_row_tasks"):
+                assert hi[key] == di[key], (key, hi[key], di[key])
+            assert hi["tile_kernel"] == S.TCA_TILES_SHORT
+            val, bd = _dev(torch, a.values), _dev(torch, b)
+            outs = []
+            for pl in (hp, dp):
+                c = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda:0")
+                pl.run(val, bd, c)
+                torch.cuda.synchronize()
+                outs.append(c.cpu().numpy())
+            want = oracle.csr_spmm(a.rowptr, a.colidx, a.values_f32(), S.from_storage(b, a.dtype))
+            assert np.array_equal(outs[0], want) and np.array_equal(outs[1], want)
+        finally:
+            dp.close()

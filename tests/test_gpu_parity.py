@@ -162,11 +162,47 @@ def test_mfma_exact_bit_equal(torch_cuda, dtype, variant):
                 info = pl.info()
                 got = run_gpu(torch_cuda, a, b, plan=pl)
             assert info["n_windows_mfma"] > 0 or (m, k, p) in dense, (m, k, n)
-            want_kernel = {S.TCA_PLAN_MFMA_PAIR: {3}, 0: {3, 5, 7}, S.TCA_PLAN_MFMA_DENSE: {4, 5},
+            want_kernel = {S.TCA_PLAN_MFMA_PAIR: {3}, 0: {3, 5, 7, 8}, S.TCA_PLAN_MFMA_DENSE: {4, 5},
                            S.TCA_PLAN_MFMA_COMPACT: {7, 4, 5}}[variant]
             assert info["tile_kernel"] in want_kernel or info["n_windows_mfma"] == 0, (variant, info["tile_kernel"])
             want = oracle_c(a, b)
             assert np.array_equal(got, want), (m, k, p, n, np.abs(got - want).max())
+
+
+@pytest.mark.parametrize("dtype", [S.TCA_F16, S.TCA_BF16])
+def test_short_k_kernel_bit_exact(torch_cuda, dtype):
+    """The short-K kernel (every row; 32-row windows built in LDS from the
+    CSR each run) is bit-equal to the oracle on exact-arithmetic inputs:
+    partial windows and column blocks, K not a multiple of 32, K = 1 and
+    640, empty rows and rows holding all of K.  Routing: the flag forces it
+    at any row length; by default it takes K <= 640 at >= max(8, 0.08 K)
+    nonzeros per row; K = 641, fp32, TCA_PLAN_NO_MFMA and sparser rows stay
+    off it."""
+    rng = np.random.default_rng(131 + dtype)
+    for m, k, p in [(2048, 512, 0.1), (37, 40, 0.5), (64, 640, 0.05), (100, 1, 1.0), (33, 100, 1.0),
+                    (5, 600, 0.02), (300, 33, 0.3), (1, 64, 0.0), (200, 97, 0.2)]:
+        lens = rng.binomial(k, p, m)
+        lens[rng.random(m) < 0.1] = 0
+        if m > 3:
+            lens[3] = k  # a row holding all of K
+        a = make_csr(rng, lens, k, dtype)
+        for n in (8, 16, 64, 136, 256):
+            b = S.to_storage(exact_dense(rng, (k, n)), dtype)
+            with S.Plan(a, n, S.TCA_PLAN_MFMA_SHORT) as pl:
+                info = pl.info()
+                got = run_gpu(torch_cuda, a, b, plan=pl)
+            assert info["tile_kernel"] == S.TCA_TILES_SHORT and info["n_row_tasks"] == 0, (m, k, n, info)
+            want = oracle_c(a, b)
+            assert np.array_equal(got, want), (m, k, p, n, np.abs(got - want).max())
+    a0, n0, _ = S.gen_config(0, seed=1)
+    with S.Plan(a0, n0) as pl:
+        assert pl.info()["tile_kernel"] == S.TCA_TILES_SHORT
+    sparse, _ = S.gen_bernoulli(256, 512, 0.05, seed=2, dtype=S.TCA_F16)       # ~26 per row, 5 %
+    wide, _ = S.gen_bernoulli(256, 641, 0.1, seed=3, dtype=S.TCA_F16)
+    for mat, flags in ((sparse, 0), (wide, S.TCA_PLAN_MFMA_SHORT), (a0, S.TCA_PLAN_NO_MFMA),
+                       (a0.astype(S.TCA_F32), S.TCA_PLAN_MFMA_SHORT), (a0, S.TCA_PLAN_MFMA_PAIR)):
+        with S.Plan(mat, 64, flags) as pl:
+            assert pl.info()["tile_kernel"] != S.TCA_TILES_SHORT, flags
 
 
 def test_mfma_and_row_paths_agree(torch_cuda):
@@ -358,8 +394,9 @@ def test_config_full_size_large(torch_cuda, cfg):
 
 def test_phase_timing_reports_the_kernels_a_plan_uses(torch_cuda):
     """tca_spmm_time_phases: a phase the plan does not use reads 0, the used
-    ones are positive, and C holds the exact product afterwards (default
-    MFMA plan, paired-kernel plan, row-kernel plan)."""
+    ones are positive, and C holds the exact product afterwards (short-K
+    plan: one launch, no pack; dense-tile and paired-kernel plans; row-kernel
+    and panel plans)."""
     torch = torch_cuda
     rng = np.random.default_rng(97)
     a, _ = S.gen_bernoulli(256, 512, 0.08, seed=9, dtype=S.TCA_F16)
@@ -368,7 +405,8 @@ def test_phase_timing_reports_the_kernels_a_plan_uses(torch_cuda):
     dev = torch.device("cuda:0")
     val = torch.from_numpy(a.values.view(np.int16)).to(dev)
     bd = torch.from_numpy(b.view(np.int16)).to(dev)
-    for flags, used in ((S.TCA_PLAN_FORCE_MFMA, {"pack", "tiles"}),
+    for flags, used in ((S.TCA_PLAN_FORCE_MFMA, {"tiles"}),
+                        (S.TCA_PLAN_FORCE_MFMA | S.TCA_PLAN_MFMA_DENSE, {"pack", "tiles"}),
                         (S.TCA_PLAN_FORCE_MFMA | S.TCA_PLAN_MFMA_PAIR, {"pack", "tiles"}),
                         (S.TCA_PLAN_NO_MFMA | S.TCA_PLAN_NO_PANELS, {"rows"}),
                         (S.TCA_PLAN_NO_MFMA | S.TCA_PLAN_FORCE_PANELS, {"panels"})):
