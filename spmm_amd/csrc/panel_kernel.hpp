@@ -13,9 +13,13 @@
 // rows' accumulators.  For row entry i of its rows the group walks the CSR
 // run of the row inside the tile (contiguous: the row's columns are sorted
 // and the tile is a column range); 16 positions and values are fetched with
-// one load per lane and broadcast to the group one at a time (DPP
-// row_newbcast), and each nonzero costs one or two conflict-free LDS reads
-// (16 lanes read 256 contiguous bytes of one staged row) and E FMAs.  The
+// one load per lane, and step U of the run takes lane U's through DPP
+// row_newbcast folded into the address add and the FMAs: one VALU
+// instruction for the address, one or two conflict-free LDS reads (16 lanes
+// read 256 contiguous bytes of one staged row) and E FMAs per step, the next
+// step's reads issued before the current step's FMAs.  The wavefront steps
+// through the longest run of its four groups; lanes past their run read a
+// zero row (position 0) and multiply by 0.  The
 // accumulation order of a row is its CSR order inside a unit, and units of a
 // split panel are summed in unit order by seg_finalize_kernel: results do
 // not depend on the schedule.
@@ -40,7 +44,8 @@ namespace tca {
 
 constexpr int kPnWaves = 8;     // consumer wavefronts (planner: kPanelWaves)
 constexpr int kPnRpg = 10;      // rows per 16-lane group (planner: kPanelRpg)
-constexpr int kPnCntRows = 16;  // count entries per wavefront and tile (planner: kPanelCntRows)
+constexpr int kPnCntRows = 16;  // count dwords per wavefront and tile (planner: kPanelCntRows)
+constexpr int kPnMaxDword = 12; // first dword of the entries' longest counts (planner: kPanelMaxDword)
 constexpr int kPnThreads = (kPnWaves + 1) * 64;
 
 struct PanelArgs {
@@ -69,10 +74,12 @@ struct PanelGeom {
     static constexpr int kInstrs = (kP * kRowBytes + 1023) / 1024;  // 1 KiB transfers per tile
     static constexpr int kBufBytes = kInstrs * 1024;                 // one tile buffer (whole transfers)
     static_assert(kLaneBytes == 8 || kLaneBytes == 16 || kLaneBytes == 32, "lane geometry");
+    static_assert(kP <= 255, "1-based positions fit a byte");
 };
 
+// LDS of the panel kernel: two tile buffers and their zero rows.
 constexpr int panel_lds_bytes(int row_bytes) {
-    return 2 * ((((65536 / row_bytes) < 255 ? (65536 / row_bytes) : 255) * row_bytes + 1023) / 1024) * 1024;
+    return 2 * (((((65536 / row_bytes) < 255 ? (65536 / row_bytes) : 255) * row_bytes + 1023) / 1024) * 1024 + row_bytes);
 }
 
 template <int U>
@@ -93,21 +100,32 @@ __device__ __forceinline__ uint32_t pn_lds_addr(P* p) {
     return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) char*)p));
 }
 
-// E elements of staged row `p` for lane g, widened to fp32 (layout: see the
-// column mapping in panel_store).
-// lbuf: the tile buffer plus this lane's offset in a staged row (one
-// shift-add per step then forms the address).
+// LDS layout of a workgroup: two tile buffers, each preceded by one zero row
+// (the target of positions 0: lanes past a run):
+//   [zero row | buffer 0 (kBufBytes) | zero row | buffer 1 (kBufBytes)]
+// Staged row q (1-based) of tile t starts at zrow_off(t & 1) + q * kRowBytes.
 template <typename T, int E>
-__device__ __forceinline__ void pn_read(const char* lbuf, int p, float (&b)[E]) {
+constexpr int pn_zrow_off(int buf) {
+    return buf * (PanelGeom<T, E>::kBufBytes + PanelGeom<T, E>::kRowBytes);
+}
+
+// E elements of the staged row at LDS byte address `addr` (the row's address
+// plus this lane's offset in it), widened to fp32; layout: see the column
+// mapping in panel_store.
+template <typename T, int E>
+__device__ __forceinline__ void pn_read_at(uint32_t addr, float (&b)[E]) {
     using G = PanelGeom<T, E>;
-    const char* row = lbuf + p * G::kRowBytes;
+    using LC = const __attribute__((address_space(3))) char;
+    LC* row = reinterpret_cast<LC*>(static_cast<uintptr_t>(addr));
     if constexpr (G::kLaneBytes == 32) {  // fp32, E = 8: two 256-byte halves
-        const f32x4 lo = *reinterpret_cast<const f32x4*>(row);
-        const f32x4 hi = *reinterpret_cast<const f32x4*>(row + 256);
+        const f32x4 lo = *reinterpret_cast<const __attribute__((address_space(3))) f32x4*>(row);
+        const f32x4 hi = *reinterpret_cast<const __attribute__((address_space(3))) f32x4*>(row + 256);
         b[0] = lo.x; b[1] = lo.y; b[2] = lo.z; b[3] = lo.w;
         b[4] = hi.x; b[5] = hi.y; b[6] = hi.z; b[7] = hi.w;
     } else {
-        const Pack<T, E> v = *reinterpret_cast<const Pack<T, E>*>(row);
+        typedef int w_t __attribute__((ext_vector_type(G::kLaneBytes / 4)));
+        const w_t w = *reinterpret_cast<const __attribute__((address_space(3))) w_t*>(row);
+        const Pack<T, E> v = __builtin_bit_cast(Pack<T, E>, w);
 #pragma unroll
         for (int e = 0; e < E; e++) b[e] = to_f32(v.v[e]);
     }
@@ -134,71 +152,81 @@ __device__ __forceinline__ void panel_store(float* dst, int g, const float (&acc
     }
 }
 
-// Step U of a batch: nonzero j + U of the group's run.  Lanes past the run
-// hold value 0 and the zero row's position (the batch loads are masked), so
-// the step needs no branch and its LDS reads can be issued ahead of earlier
-// steps' FMAs.
-template <typename T, int E, int U>
-__device__ __forceinline__ void pn_step(float (&acc)[E], int pv, float vv, const char* lbuf) {
-    const int p = pn_bcast<U>(pv);
-    const float v = __builtin_bit_cast(float, pn_bcast<U>(__builtin_bit_cast(int, vv)));
-    float b[E];
-    pn_read<T, E>(lbuf, p, b);
-#pragma unroll
-    for (int e = 0; e < E; e++) acc[e] = __builtin_fmaf(v, b[e], acc[e]);
+// Step U of a run (nonzero U of each group's run, held by lane U of the
+// group) in two DPP instructions: the address of the staged row is lane U's
+// row address broadcast to the group plus the lane's own offset in the row
+// (v_add_u32 with row_newbcast:U), and each FMA takes lane U's value through
+// the same broadcast (v_fmac_f32 with row_newbcast:U), so a step costs no
+// separate broadcast moves.  The compiler does not see the DPP inside these
+// statements: a DPP source written by a VALU instruction needs two wait
+// states before it is read, so the first statements of a run (whose
+// sources are computed just before) start with s_nop 1; later steps read
+// the same registers, which nothing writes in between.
+template <int U, bool kNop>
+__device__ __forceinline__ uint32_t pn_addr(uint32_t pa, uint32_t lanepart) {
+    uint32_t r;
+    if constexpr (kNop)
+        asm("s_nop 1\n\tv_add_u32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf bound_ctrl:1"
+            : "=v"(r) : "v"(pa), "v"(lanepart), "n"(U));
+    else
+        asm("v_add_u32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf bound_ctrl:1"
+            : "=v"(r) : "v"(pa), "v"(lanepart), "n"(U));
+    return r;
 }
-
-// Steps 2C and 2C + 1 when the wavefront's longest run reaches them (two
-// steps per uniform branch: fewer wasted steps than four, and the second
-// step's LDS reads can still be issued ahead of the first step's FMAs).
-template <typename T, int E, int C>
-__device__ __forceinline__ void pn_chunk(float (&acc)[E], int pv, float vv, int m, const char* lbuf) {
-    if (2 * C < m) {
-        pn_step<T, E, 2 * C + 0>(acc, pv, vv, lbuf);
-        pn_step<T, E, 2 * C + 1>(acc, pv, vv, lbuf);
+template <int E, int U>
+__device__ __forceinline__ void pn_fmas(float (&acc)[E], float vv, const float (&b)[E]) {
+#pragma unroll
+    for (int e = 0; e < E; e++) {
+        if (U == 0 && e == 0)
+            asm("s_nop 1\n\tv_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf bound_ctrl:1"
+                : "+v"(acc[e]) : "v"(vv), "v"(b[e]), "n"(U));
+        else
+            asm("v_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf bound_ctrl:1"
+                : "+v"(acc[e]) : "v"(vv), "v"(b[e]), "n"(U));
     }
 }
 
-// The run of a group in one tile holds at most 16 nonzeros (the planner cuts
-// tiles so), fetched with one load per lane: lane g takes nonzero cur + g
-// when g < n (masked buffer loads return 0 for the others).  The position
-// byte arrives inside the aligned dword that holds it, as a plain 32-bit
-// value, and is extracted only when the run is multiplied: no instruction
-// between the load and the next tile waits for it.
-template <typename T>
-__device__ __forceinline__ void pn_fetch(int cur, int n, int g, __amdgpu_buffer_rsrc_t rpos,
-                                         __amdgpu_buffer_rsrc_t rval, int& pl, float& vv) {
-    const bool ok = g < n;
-    const uint32_t k = static_cast<uint32_t>(cur + g);
-    pl = __builtin_amdgcn_raw_buffer_load_b32(rpos, ok ? (k & ~3u) : kOob, 0, 0);
-    vv = load_val<T>(rval, k, ok);
+// Steps U.. of a run: x holds step U's B row (read one step earlier).  Step
+// U + 1's row is read before step U's FMAs (also when the run ends at U: one
+// read that is not used), so its LDS latency hides behind them, and the run
+// leaves after the FMAs of its last step: every exit comes after the same
+// in-place accumulation (no join of differently-allocated results), and the
+// compiler's LDS waits count exactly the reads issued after the one they wait
+// for.  A uniform branch per step: m is the longest run of the wavefront's
+// four groups.
+template <typename T, int E, int U>
+__device__ __forceinline__ void pn_steps(float (&acc)[E], uint32_t pa, float vv, uint32_t lanepart, int m,
+                                         float (&x)[E], float (&y)[E]) {
+    if constexpr (U < 15) {
+        pn_read_at<T, E>(pn_addr<U + 1, false>(pa, lanepart), y);
+        // keeps the read here (otherwise it sinks into the branch that uses it)
+        asm volatile("" ::: "memory");
+    }
+    pn_fmas<E, U>(acc, vv, x);
+    if constexpr (U < 15) {
+        if (U + 1 < m) pn_steps<T, E, U + 1>(acc, pa, vv, lanepart, m, y, x);
+    }
 }
 
-// One group's run of n nonzeros from CSR index `cur` in the current tile;
-// nmax is the longest run of the wavefront's four groups (the wavefront
-// steps through nmax nonzeros in chunks of 2).  Lanes past the run use the
-// zero row (position zrow, relative to `buf`) and value 0.
+// One group's run in the current tile: lane g holds nonzero g of the run
+// (value vv, 1-based tile position q; lanes past the run hold 0 and 0, so
+// they multiply the zero row by 0).  zb: LDS address of the tile buffer's
+// zero row; nmax: the longest run of the wavefront's four groups (>= 1).
 template <typename T, int E>
-__device__ __forceinline__ void pn_run(float (&acc)[E], int cur, int n, int nmax, int pl, float vv, const char* lbuf,
-                                       int zrow, int g) {
-    const uint32_t k = static_cast<uint32_t>(cur + g);
-    const int pv = g < n ? static_cast<int>((static_cast<uint32_t>(pl) >> (8 * (k & 3))) & 255u) : zrow;
-    pn_chunk<T, E, 0>(acc, pv, vv, nmax, lbuf);
-    pn_chunk<T, E, 1>(acc, pv, vv, nmax, lbuf);
-    pn_chunk<T, E, 2>(acc, pv, vv, nmax, lbuf);
-    pn_chunk<T, E, 3>(acc, pv, vv, nmax, lbuf);
-    pn_chunk<T, E, 4>(acc, pv, vv, nmax, lbuf);
-    pn_chunk<T, E, 5>(acc, pv, vv, nmax, lbuf);
-    pn_chunk<T, E, 6>(acc, pv, vv, nmax, lbuf);
-    pn_chunk<T, E, 7>(acc, pv, vv, nmax, lbuf);
+__device__ __forceinline__ void pn_run(float (&acc)[E], uint32_t q, float vv, int nmax, uint32_t zb,
+                                       uint32_t lanepart) {
+    const uint32_t pa = q * static_cast<uint32_t>(PanelGeom<T, E>::kRowBytes) + zb;
+    float b0[E], b1[E];
+    pn_read_at<T, E>(pn_addr<0, true>(pa, lanepart), b0);
+    pn_steps<T, E, 0>(acc, pa, vv, lanepart, nmax, b0, b1);
 }
 
 template <typename T, int E>
 __global__ __launch_bounds__(kPnThreads, 1) void panel_kernel(PanelArgs a) {
     using G = PanelGeom<T, E>;
     constexpr int R = kPnWaves * 4 * kPnRpg;
-    // two tile buffers, then one zero row (the target of masked steps)
-    __shared__ __attribute__((aligned(16))) char smem[2 * G::kBufBytes + G::kRowBytes];
+    // two tile buffers, each after its zero row (pn_zrow_off)
+    __shared__ __attribute__((aligned(16))) char smem[2 * (G::kBufBytes + G::kRowBytes)];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int chunk = blockIdx.x % a.chunks;
@@ -245,7 +273,7 @@ __global__ __launch_bounds__(kPnThreads, 1) void panel_kernel(PanelArgs a) {
                         const uint32_t oj = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(o[r0 / 64]), r0 % 64 + j));
                         off = sub == j ? oj : off;
                     }
-                    pn_dma(bbase, off + 16 * piece, lds0 + buf * G::kBufBytes + k * 1024);
+                    pn_dma(bbase, off + 16 * piece, lds0 + pn_zrow_off<T, E>(buf) + G::kRowBytes + k * 1024);
                 }
             }
         };
@@ -299,51 +327,66 @@ __global__ __launch_bounds__(kPnThreads, 1) void panel_kernel(PanelArgs a) {
         for (int e = 0; e < E; e++) acc[i][e] = 0.f;
     }
     if (wave == 0)
-        for (int o = 16 * lane; o < G::kRowBytes; o += 1024)
-            *reinterpret_cast<f32x4*>(smem + 2 * G::kBufBytes + o) = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int o = 16 * lane; o < G::kRowBytes; o += 1024) {
+            *reinterpret_cast<f32x4*>(smem + pn_zrow_off<T, E>(0) + o) = f32x4{0.f, 0.f, 0.f, 0.f};
+            *reinterpret_cast<f32x4*>(smem + pn_zrow_off<T, E>(1) + o) = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
     const int shift = 8 * group;
-    // counts through the constant address space: scalar loads, counted by
-    // lgkmcnt, so using them never waits for the vector loads in flight
+    const uint32_t lds0 = pn_lds_addr(smem);
+    const uint32_t lanepart = static_cast<uint32_t>((G::kLaneBytes == 32 ? 16 : G::kLaneBytes) * g);
+    // Counts through the constant address space: scalar loads, counted by
+    // lgkmcnt, so using them never waits for the vector loads in flight.
+    // Per tile and wavefront 16 dwords: dword i (i < rpg) holds entry i's four
+    // group counts, byte i % 4 of dword kPnMaxDword + i / 4 entry i's longest.
     using CU32 = const __attribute__((address_space(4))) uint32_t;
     CU32* const cbase = (CU32*)(reinterpret_cast<uintptr_t>(a.cnt)) + (static_cast<size_t>(u.y) * kPnWaves + wave) * kPnCntRows;
     auto counts = [&](int t) { return cbase + static_cast<size_t>(t) * (kPnWaves * kPnCntRows); };
-    auto zero_row = [&](int t) { return (2 - (t & 1)) * G::kBufBytes / G::kRowBytes; };  // (t = -1: unused)
+    constexpr int kMaxWords = (kPnRpg + 3) / 4;
     // Entry i's run of tile t + 1 is fetched right after entry i is done with
-    // tile t, so its latency hides behind the rest of the tile.  Iteration -1
-    // only fetches tile 0, with the same instructions in the same order as
-    // every later iteration: the compiler's vmcnt waits then count exactly the
-    // loads issued after the one they wait for.  The fetch after the last
-    // tile has n = 0 (every lane masked).
-    uint32_t cn[kPnRpg];
-    int plq[kPnRpg];
+    // tile t, so its latency hides behind the rest of the tile: lane g loads
+    // the run's nonzero g (its 1-based position byte and its value; masked
+    // loads give 0 and 0 past the run).  Iteration -1 only fetches tile 0,
+    // with the same instructions in the same order as every later iteration:
+    // the compiler's vmcnt waits then count exactly the loads issued after
+    // the one they wait for.  The fetch after the last tile has n = 0.
+    uint32_t cn[kPnRpg], mx[kMaxWords];
+    uint32_t q[kPnRpg];
     float vvq[kPnRpg];
 #pragma unroll
     for (int i = 0; i < kPnRpg; i++) {
         cn[i] = 0;
-        plq[i] = 0;
+        q[i] = 0;
         vvq[i] = 0.f;
     }
+#pragma unroll
+    for (int w = 0; w < kMaxWords; w++) mx[w] = 0;
     for (int t = -1; t < u.z; t++) {
         if (t >= 0) __syncthreads();
-        const char* lbuf = smem + (t & 1) * G::kBufBytes + (G::kLaneBytes == 32 ? 16 : G::kLaneBytes) * g;
-        const int zrow = zero_row(t);
+        const uint32_t zb = lds0 + pn_zrow_off<T, E>(t & 1);
         const bool more = t + 1 < u.z;
-        uint32_t cnx[kPnRpg];
+        uint32_t cnx[kPnRpg], mxx[kMaxWords];
         {
             CU32* cw = counts(more ? t + 1 : t);
 #pragma unroll
             for (int i = 0; i < kPnRpg; i++) cnx[i] = cw[i];
+#pragma unroll
+            for (int w = 0; w < kMaxWords; w++) mxx[w] = cw[kPnMaxDword + w];
         }
 #pragma unroll
         for (int i = 0; i < kPnRpg; i++) {
-            const uint32_t c4 = cn[i];
-            const int n = (c4 >> shift) & 255;
-            const int nmax = max(max(c4 & 255, (c4 >> 8) & 255), max((c4 >> 16) & 255, c4 >> 24));
-            if (nmax > 0) pn_run<T, E>(acc[i], cur[i], n, nmax, plq[i], vvq[i], lbuf, zrow, g);
+            const int n = (cn[i] >> shift) & 255;
+            const int nmax = (mx[i / 4] >> (8 * (i % 4))) & 255;
+            if (nmax > 0) pn_run<T, E>(acc[i], q[i], vvq[i], nmax, zb, lanepart);
             cur[i] += n;
-            pn_fetch<T>(cur[i], more ? (cnx[i] >> shift) & 255 : 0, g, rpos, rval, plq[i], vvq[i]);
+            const int nn = more ? static_cast<int>((cnx[i] >> shift) & 255) : 0;
+            const bool ok = g < nn;
+            const uint32_t k = static_cast<uint32_t>(cur[i] + g);
+            q[i] = __builtin_amdgcn_raw_buffer_load_b8(rpos, ok ? k : kOob, 0, 0);
+            vvq[i] = load_val<T>(rval, k, ok);
             cn[i] = cnx[i];
         }
+#pragma unroll
+        for (int w = 0; w < kMaxWords; w++) mx[w] = mxx[w];
     }
     // ---- results: C rows, or this unit's partial rows of a split panel
     const int nu = u.w >= 0 ? a.panel_units[u.x] : 0;

@@ -458,10 +458,20 @@ void plan_panels(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_
                 for (int32_t k = rowptr[row]; k < rowptr[row + 1]; k++) {
                     const int32_t u = posmap[colidx[k]];
                     const int32_t t = tile_of[u];
-                    p->pos[k] = static_cast<uint8_t>(u - c.cuts[t]);
+                    p->pos[k] = static_cast<uint8_t>(u - c.cuts[t] + 1);
                     p->cnt[static_cast<size_t>(t0 + t) * cnt_stride + (wave * kPanelCntRows + i) * 4 + group]++;
                 }
                 p->row_panel[row] = 1;
+            }
+            // per wave and entry: the longest of the four group counts
+            for (int32_t t = 0; t < nt; t++) {
+                uint8_t* cb = &p->cnt[static_cast<size_t>(t0 + t) * cnt_stride];
+                for (int32_t wave = 0; wave < p->waves; wave++)
+                    for (int32_t i = 0; i < p->rpg; i++) {
+                        const uint8_t* c4 = cb + (wave * kPanelCntRows + i) * 4;
+                        cb[(wave * kPanelCntRows + kPanelMaxDword + i / 4) * 4 + i % 4] =
+                            std::max(std::max(c4[0], c4[1]), std::max(c4[2], c4[3]));
+                    }
             }
         }
     }
@@ -478,7 +488,8 @@ void plan_panels(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_
         std::vector<int64_t> tn(nt, 0);
         for (int32_t t = 0; t < nt; t++) {
             const uint8_t* cb = &p->cnt[static_cast<size_t>(t0 + t) * cnt_stride];
-            for (size_t b = 0; b < cnt_stride; b++) tn[t] += cb[b];
+            for (int32_t wave = 0; wave < p->waves; wave++)
+                for (int32_t b = 0; b < p->rpg * 4; b++) tn[t] += cb[wave * kPanelCntRows * 4 + b];
         }
         std::vector<int32_t> cut = {0};
         int64_t acc = 0;

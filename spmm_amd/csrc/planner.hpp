@@ -135,8 +135,11 @@ void plan_row_params(int64_t nnz, int32_t N, int32_t es, int32_t slices, RowPlan
 //   tile t (global index): cols[t * P + j] = the B row staged at position j
 //     for j < width[t] (padding repeats a valid column; never read);
 //   cnt[t * waves * 16 * 4 + (wave * 16 + i) * 4 + group] (bytes): nonzeros
-//     of slot s's row in tile t (16 row entries per wave, rpg used);
-//   pos[k] for a CSR nonzero k of a panel row: its position in its tile;
+//     of slot s's row in tile t (16 dwords per wave and tile: entries
+//     i < rpg), and byte i % 4 of dword kPanelMaxDword + i / 4 the longest
+//     of entry i's four counts (the steps the wave takes for entry i);
+//   pos[k] for a CSR nonzero k of a panel row: 1 + its position in its tile
+//     (the kernel's position 0 is a zero row);
 //   units[u] = {panel, first tile, tiles, segment base or -1}: one
 //     workgroup; a panel whose nonzeros exceed the unit size is split into
 //     panel_units[panel] units by tiles, each writing partial rows that are
@@ -169,7 +172,9 @@ struct PanelPlan {
 };
 constexpr int kPanelWaves = 8;    // consumer wavefronts per workgroup (plus one producer)
 constexpr int kPanelRpg = 10;     // rows per 16-lane group
-constexpr int kPanelCntRows = 16; // count entries per wave and tile (rpg <= 16)
+constexpr int kPanelCntRows = 16; // count dwords per wave and tile
+constexpr int kPanelMaxDword = 12; // first dword of the entries' longest counts
+static_assert(kPanelRpg <= kPanelMaxDword && kPanelMaxDword + (kPanelRpg + 3) / 4 <= kPanelCntRows, "cnt layout");
 constexpr int kPanelMaxRun = 16;  // nonzeros of one row in one tile (one 16-lane batch)
 constexpr double kPanelMinReuse = 2.0;
 constexpr int64_t kPanelMinNnz = int64_t(1) << 21;  // fewer nonzeros in panels: none (unless forced)

@@ -264,7 +264,8 @@ void launch_pack(const tca_spmm_plan* p, const void* val, hipStream_t s) {
                        static_cast<const uint16_t*>(val), p->d_packed);
 }
 
-static_assert(kPnWaves == kPanelWaves && kPnRpg == kPanelRpg && kPnCntRows == kPanelCntRows, "panel plan layout");
+static_assert(kPnWaves == kPanelWaves && kPnRpg == kPanelRpg && kPnCntRows == kPanelCntRows &&
+                  kPnMaxDword == kPanelMaxDword, "panel plan layout");
 static_assert(PanelGeom<float, 8>::kP == 128 && PanelGeom<float, 4>::kP == 255, "panel tile widths (panel_tile_cols)");
 static_assert(kMfmaPairShape.max_step_entries == kDmaMaxStepEntries, "planner and paired kernel agree on step size");
 static_assert(kMfmaPairShape.win_rows == kDmaWinRows && kMfmaPairShape.tile_cols == kDmaTileCols, "paired tile shape");
@@ -472,9 +473,8 @@ void fill_info(tca_spmm_plan* p) {
     in.nnz_panels = p->panels.nnz;
     in.staged_panels = p->panels.staged;
     in.panel_blockdim = kPnThreads;
-    in.panel_lds_bytes = p->n_units ? panel_lds_bytes(16 * p->panels.elems * static_cast<int>(dtype_size(p->dtype))) +
-                                          16 * p->panels.elems * static_cast<int>(dtype_size(p->dtype))
-                                    : 0;
+    in.panel_lds_bytes =
+        p->n_units ? panel_lds_bytes(16 * p->panels.elems * static_cast<int>(dtype_size(p->dtype))) : 0;
     if (p->mfma_short) {
         in.n_windows_mfma = p->short_nwin;
         in.rows_mfma = p->M;

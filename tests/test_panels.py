@@ -32,9 +32,13 @@ def emulate(a: S.CSR, b: np.ndarray, pp: dict, n: int):
                 if row < 0:
                     assert c == 0
                     continue
+                # the longest run of the entry's four groups: the steps the wave takes
+                c4 = pp["cnt"][t * stride + (wave * 16 + i) * 4:][:4]
+                assert int(pp["cnt"][t * stride + (wave * 16 + 12 + i // 4) * 4 + i % 4]) == int(c4.max())
                 for k in range(cur, cur + c):
-                    assert int(pp["pos"][k]) < int(pp["width"][t]) <= P
-                    col = pp["cols"][t * P + int(pp["pos"][k])]
+                    # positions are 1-based (0 is the kernel's zero row)
+                    assert 1 <= int(pp["pos"][k]) <= int(pp["width"][t]) <= P
+                    col = pp["cols"][t * P + int(pp["pos"][k]) - 1]
                     assert col == a.colidx[k], (u, s, t, k)
                     seen[k] += 1
                     acc = acc + np.float32(vals[k]) * bf[col]
@@ -60,7 +64,7 @@ def check_plan(a, n, flags=S.TCA_PLAN_FORCE_PANELS):
     assert pp["panels"] > 0, pp
     # a row holds at most 16 nonzeros of a tile (one 16-lane batch), a tile at most P columns
     assert int(pp["cnt"].max()) <= 16
-    assert int(pp["pos"].max()) < pp["P"]
+    assert int(pp["pos"].max()) <= pp["P"]
     got, seen = emulate(a, b, pp, n)
     panel_rows = np.array(sorted(got), np.int64)
     # every nonzero of a panel row visited once, nothing else
