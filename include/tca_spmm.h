@@ -321,7 +321,7 @@ int tca_plan_mfma_windows(const int32_t* rowptr, const int32_t* colidx, int32_t 
  * rows == NULL to get sizes[16] = {panels, tiles, units, long rows, R, P,
  * consumer waves, rows per lane group, elements per lane, column chunks,
  * nonzeros in panels, staged columns, partial segments, rows in panels,
- * count bytes per tile, 0}; then with rows[panels*R], cols[tiles*P],
+ * count bytes per tile, first dword of the longest runs in a wave's counts}; then with rows[panels*R], cols[tiles*P],
  * width[tiles], cnt[tiles * sizes[14]], pos[nnz], units[4*units], panel_units[panels],
  * ustart[units*R], longrows[4*long rows].  Layouts: see PanelPlan in
  * spmm_amd/csrc/planner.hpp.  No counterpart in the reference. */

@@ -375,9 +375,10 @@ def plan_panels(a: CSR, n: int, flags: int = TCA_PLAN_DEFAULT, dtype: int = None
             np_ptr(sizes, ctypes.c_int64))
     call("tca_plan_panels", *args, None, None, None, None, None, None, None, None, None)
     (n_panels, n_tiles, n_units, n_long, R, P, waves, rpg, elems, chunks, nnz_p, staged, n_seg, n_rows,
-     stride, _) = (int(x) for x in sizes)
+     stride, max_dword) = (int(x) for x in sizes)
     out = dict(panels=n_panels, tiles=n_tiles, n_units=n_units, R=R, P=P, waves=waves, rpg=rpg, elems=elems,
                chunks=chunks, nnz=nnz_p, staged=staged, segments=n_seg, n_rows=n_rows, cnt_stride=stride,
+               cnt_rows=stride // (4 * waves) if waves else 0, max_dword=max_dword,
                rows=np.zeros(max(n_panels * R, 1), np.int32), cols=np.zeros(max(n_tiles * P, 1), np.int32),
                width=np.zeros(max(n_tiles, 1), np.uint8),
                cnt=np.zeros(max(n_tiles * stride, 1), np.uint8), pos=np.zeros(max(a.nnz, 1), np.uint8),

@@ -6,7 +6,8 @@
 // tiles -- ranges of the panel's sorted column union, P columns each -- are
 // staged one after another into two LDS buffers by one producer wavefront.
 // While the consumers multiply tile t, the producer's global -> LDS
-// transfers bring tile t + 1; one barrier per tile separates the two.
+// transfers bring tile t + 1; one barrier per tile separates the two.  1024
+// threads, one workgroup per CU (LDS), four wavefronts per SIMD.
 //
 // Consumers.  A 16-lane group owns one B-row chunk of 16 * E elements (all
 // of N, or one column chunk of it): lane g holds E elements of each of its
@@ -14,21 +15,22 @@
 // run of the row inside the tile (contiguous: the row's columns are sorted
 // and the tile is a column range); 16 positions and values are fetched with
 // one load per lane, and step U of the run takes lane U's through DPP
-// row_newbcast folded into the address add and the FMAs: one VALU
-// instruction for the address, one or two conflict-free LDS reads (16 lanes
-// read 256 contiguous bytes of one staged row) and E FMAs per step, the next
-// step's reads issued before the current step's FMAs.  The wavefront steps
-// through the longest run of its four groups; lanes past their run read a
-// zero row (position 0) and multiply by 0.  The
-// accumulation order of a row is its CSR order inside a unit, and units of a
-// split panel are summed in unit order by seg_finalize_kernel: results do
-// not depend on the schedule.
+// row_newbcast: one VALU instruction for the address, one or two
+// conflict-free LDS reads (16 lanes read 256 contiguous bytes of one staged
+// row), one broadcast of the value and E FMAs per step, the next step's
+// reads issued before the current step's FMAs.  The wavefront steps through
+// the longest run of its four groups; lanes past their run read a zero row
+// (position 0) and multiply by 0.  The accumulation order of a row is its
+// CSR order inside a unit, and units of a split panel are summed in unit
+// order by seg_finalize_kernel: results do not depend on the schedule.
 //
 // Producer.  It issues only global_load_lds_dwordx4 transfers (16 bytes per
 // lane land at M0 + 16 * lane) and waits for its own transfers before the
 // barrier; it executes no LDS instruction (an LDS instruction of a wavefront
 // waits for that wavefront's in-flight transfers).  The byte offsets of the
-// tile's B rows come through scalar loads; a transfer's lanes select theirs.
+// tile's B rows come through vector loads; a transfer's lanes select theirs
+// by readlane.  With each tile the producer also stages the next tile's
+// per-wavefront run counts.
 //
 // Functionally replaces the reference's multirow_per_tb / multitb_per_row
 // (src/our_spmm.cu:24-295) for the rows routed to panels: each output row is
@@ -42,10 +44,10 @@
 
 namespace tca {
 
-constexpr int kPnWaves = 8;     // consumer wavefronts (planner: kPanelWaves)
-constexpr int kPnRpg = 10;      // rows per 16-lane group (planner: kPanelRpg)
-constexpr int kPnCntRows = 16;  // count dwords per wavefront and tile (planner: kPanelCntRows)
-constexpr int kPnMaxDword = 12; // first dword of the entries' longest counts (planner: kPanelMaxDword)
+constexpr int kPnWaves = 15;    // consumer wavefronts (planner: kPanelWaves)
+constexpr int kPnRpg = 5;       // rows per 16-lane group (planner: kPanelRpg)
+constexpr int kPnCntRows = 8;   // count dwords per wavefront and tile (planner: kPanelCntRows)
+constexpr int kPnMaxDword = 5;  // first dword of the entries' longest counts (planner: kPanelMaxDword)
 constexpr int kPnThreads = (kPnWaves + 1) * 64;
 
 struct PanelArgs {
@@ -77,9 +79,16 @@ struct PanelGeom {
     static_assert(kP <= 255, "1-based positions fit a byte");
 };
 
-// LDS of the panel kernel: two tile buffers and their zero rows.
+// Counts of one tile (all consumer wavefronts) and their LDS slot: one
+// 1 KiB transfer per tile.
+constexpr int kPnCntTileBytes = kPnWaves * kPnCntRows * 4;
+constexpr int kPnCntSlot = 1024;
+static_assert(kPnCntTileBytes <= kPnCntSlot && kPnCntTileBytes % 16 == 0, "counts of a tile in one transfer");
+
+// LDS of the panel kernel: two tile buffers and their zero rows, two count slots.
 constexpr int panel_lds_bytes(int row_bytes) {
-    return 2 * (((((65536 / row_bytes) < 255 ? (65536 / row_bytes) : 255) * row_bytes + 1023) / 1024) * 1024 + row_bytes);
+    return 2 * (((((65536 / row_bytes) < 255 ? (65536 / row_bytes) : 255) * row_bytes + 1023) / 1024) * 1024 + row_bytes) +
+           2 * kPnCntSlot;
 }
 
 template <int U>
@@ -95,18 +104,34 @@ __device__ __forceinline__ void pn_dma(const void* base, uint32_t off, uint32_t 
 }
 __device__ __forceinline__ void pn_wait_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// The tile hand-off: every LDS access of the wavefront done, then the
+// workgroup barrier, with compiler barriers on both sides.  Unlike
+// __syncthreads() it does not wait for the wavefront's vector loads (the
+// consumers' run fetches for the next tile stay in flight across it; the
+// producer waits for its transfers itself before arriving).
+__device__ __forceinline__ void pn_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 template <typename P>
 __device__ __forceinline__ uint32_t pn_lds_addr(P* p) {
     return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) char*)p));
 }
 
 // LDS layout of a workgroup: two tile buffers, each preceded by one zero row
-// (the target of positions 0: lanes past a run):
-//   [zero row | buffer 0 (kBufBytes) | zero row | buffer 1 (kBufBytes)]
-// Staged row q (1-based) of tile t starts at zrow_off(t & 1) + q * kRowBytes.
+// (the target of positions 0: lanes past a run), then two count slots:
+//   [zero row | buffer 0 (kBufBytes) | zero row | buffer 1 (kBufBytes) | counts 0 | counts 1]
+// Staged row q (1-based) of tile t starts at zrow_off(t & 1) + q * kRowBytes;
+// count slot t & 1 holds the counts of tile t + 1, staged with tile t.
 template <typename T, int E>
 constexpr int pn_zrow_off(int buf) {
     return buf * (PanelGeom<T, E>::kBufBytes + PanelGeom<T, E>::kRowBytes);
+}
+template <typename T, int E>
+constexpr int pn_cnt_off(int buf) {
+    return pn_zrow_off<T, E>(2) + buf * kPnCntSlot;
 }
 
 // E elements of the staged row at LDS byte address `addr` (the row's address
@@ -153,37 +178,35 @@ __device__ __forceinline__ void panel_store(float* dst, int g, const float (&acc
 }
 
 // Step U of a run (nonzero U of each group's run, held by lane U of the
-// group) in two DPP instructions: the address of the staged row is lane U's
-// row address broadcast to the group plus the lane's own offset in the row
-// (v_add_u32 with row_newbcast:U), and each FMA takes lane U's value through
-// the same broadcast (v_fmac_f32 with row_newbcast:U), so a step costs no
-// separate broadcast moves.  The compiler does not see the DPP inside these
-// statements: a DPP source written by a VALU instruction needs two wait
-// states before it is read, so the first statements of a run (whose
-// sources are computed just before) start with s_nop 1; later steps read
-// the same registers, which nothing writes in between.
+// group) in two DPP instructions and E plain FMAs: the address of the
+// staged row is lane U's row address broadcast to the group plus the lane's
+// own offset in the row (v_add_u32 with row_newbcast:U), and lane U's value
+// is broadcast once (v_mov_b32 with row_newbcast:U) for the E FMAs.  (A DPP
+// VALU instruction issues at about 5.4 cycles per SIMD against 3.1 for a
+// plain one, measured on MI355X with four wavefronts per SIMD, so the FMAs
+// do not take the broadcast themselves.)  The compiler does not see the DPP
+// inside the address statement: a DPP source written by a VALU instruction
+// needs two wait states before it is read, so the first statement of a run
+// (whose source is computed just before) starts with s_nop 1; later steps
+// read the same registers, which nothing writes in between.  The statements
+// are volatile so that they keep their program order (otherwise the
+// compiler may move a later step's statement above the first one's s_nop).
 template <int U, bool kNop>
 __device__ __forceinline__ uint32_t pn_addr(uint32_t pa, uint32_t lanepart) {
     uint32_t r;
     if constexpr (kNop)
-        asm("s_nop 1\n\tv_add_u32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf bound_ctrl:1"
+        asm volatile("s_nop 1\n\tv_add_u32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf bound_ctrl:1"
             : "=v"(r) : "v"(pa), "v"(lanepart), "n"(U));
     else
-        asm("v_add_u32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf bound_ctrl:1"
+        asm volatile("v_add_u32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf bound_ctrl:1"
             : "=v"(r) : "v"(pa), "v"(lanepart), "n"(U));
     return r;
 }
 template <int E, int U>
 __device__ __forceinline__ void pn_fmas(float (&acc)[E], float vv, const float (&b)[E]) {
+    const float v = __builtin_bit_cast(float, pn_bcast<U>(__builtin_bit_cast(int, vv)));
 #pragma unroll
-    for (int e = 0; e < E; e++) {
-        if (U == 0 && e == 0)
-            asm("s_nop 1\n\tv_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf bound_ctrl:1"
-                : "+v"(acc[e]) : "v"(vv), "v"(b[e]), "n"(U));
-        else
-            asm("v_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf bound_ctrl:1"
-                : "+v"(acc[e]) : "v"(vv), "v"(b[e]), "n"(U));
-    }
+    for (int e = 0; e < E; e++) acc[e] = __builtin_fmaf(v, b[e], acc[e]);
 }
 
 // Steps U.. of a run: x holds step U's B row (read one step earlier).  Step
@@ -221,12 +244,25 @@ __device__ __forceinline__ void pn_run(float (&acc)[E], uint32_t q, float vv, in
     pn_steps<T, E, 0>(acc, pa, vv, lanepart, nmax, b0, b1);
 }
 
+// Calls f(PnIndex<I>{}) for I = B .. N - 1 (compile-time indices for register arrays).
+template <int V>
+struct PnIndex {
+    static constexpr int value = V;
+};
+template <int B, int N, typename F>
+__device__ __forceinline__ void pn_static_for(F&& f) {
+    if constexpr (B < N) {
+        f(PnIndex<B>{});
+        pn_static_for<B + 1, N>(f);
+    }
+}
+
 template <typename T, int E>
 __global__ __launch_bounds__(kPnThreads, 1) void panel_kernel(PanelArgs a) {
     using G = PanelGeom<T, E>;
     constexpr int R = kPnWaves * 4 * kPnRpg;
-    // two tile buffers, each after its zero row (pn_zrow_off)
-    __shared__ __attribute__((aligned(16))) char smem[2 * (G::kBufBytes + G::kRowBytes)];
+    // two tile buffers, each after its zero row (pn_zrow_off), two count slots
+    __shared__ __attribute__((aligned(16))) char smem[2 * (G::kBufBytes + G::kRowBytes) + 2 * kPnCntSlot];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int chunk = blockIdx.x % a.chunks;
@@ -262,7 +298,12 @@ __global__ __launch_bounds__(kPnThreads, 1) void panel_kernel(PanelArgs a) {
             }
         };
         auto n_instr = [&](int tile) { return (a.width[tile] * G::kRowBytes + 1023) / 1024; };
-        auto stage = [&](const uint32_t (&o)[kOffRegs], int ninstr, int buf) {
+        // counts of tile rel + 1 (clamped to the unit's last tile) into count
+        // slot buf; lanes past the counts re-read the first 16 bytes
+        const uint32_t cnt_lane = 16u * static_cast<uint32_t>(lane < kPnCntTileBytes / 16 ? lane : 0);
+        auto stage = [&](const uint32_t (&o)[kOffRegs], int ninstr, int buf, int rel) {
+            const int tn = u.y + (rel + 1 < u.z ? rel + 1 : rel);
+            pn_dma(a.cnt, static_cast<uint32_t>(tn) * kPnCntTileBytes + cnt_lane, lds0 + pn_cnt_off<T, E>(buf));
 #pragma unroll
             for (int k = 0; k < G::kInstrs; k++) {
                 if (k < ninstr) {
@@ -293,16 +334,16 @@ __global__ __launch_bounds__(kPnThreads, 1) void panel_kernel(PanelArgs a) {
         int nin = n_instr(u.y);
         load_offs(u.y, o);
         settle(nin);
-        stage(o, nin, 0);
+        stage(o, nin, 0, 0);
         if (u.z > 1) {
             nin = n_instr(u.y + 1);
             load_offs(u.y + 1, o);
         }
         settle(nin);
         for (int t = 0; t < u.z; t++) {
-            __syncthreads();
+            pn_barrier();
             if (t + 1 < u.z) {
-                stage(o, nin, (t + 1) & 1);
+                stage(o, nin, (t + 1) & 1, t + 1);
                 if (t + 2 < u.z) {
                     nin = n_instr(u.y + t + 2);
                     load_offs(u.y + t + 2, o);
@@ -334,59 +375,76 @@ __global__ __launch_bounds__(kPnThreads, 1) void panel_kernel(PanelArgs a) {
     const int shift = 8 * group;
     const uint32_t lds0 = pn_lds_addr(smem);
     const uint32_t lanepart = static_cast<uint32_t>((G::kLaneBytes == 32 ? 16 : G::kLaneBytes) * g);
-    // Counts through the constant address space: scalar loads, counted by
-    // lgkmcnt, so using them never waits for the vector loads in flight.
-    // Per tile and wavefront 16 dwords: dword i (i < rpg) holds entry i's four
-    // group counts, byte i % 4 of dword kPnMaxDword + i / 4 entry i's longest.
-    using CU32 = const __attribute__((address_space(4))) uint32_t;
-    CU32* const cbase = (CU32*)(reinterpret_cast<uintptr_t>(a.cnt)) + (static_cast<size_t>(u.y) * kPnWaves + wave) * kPnCntRows;
-    auto counts = [&](int t) { return cbase + static_cast<size_t>(t) * (kPnWaves * kPnCntRows); };
-    constexpr int kMaxWords = (kPnRpg + 3) / 4;
+    // Counts: per tile and wavefront 8 dwords; dword i (i < rpg) holds entry
+    // i's four group counts, byte i % 4 of dword kPnMaxDword + i / 4 entry
+    // i's longest.  Tile 0's come through one vector load before the loop;
+    // tile t + 1's are read from the count slot the producer staged with tile
+    // t (LDS reads, ordered with the B-row reads: no scalar loads, which
+    // share lgkmcnt with the LDS reads and return out of order, and no
+    // loop-carried vector loads, whose copies between iterations would wait
+    // for every load in flight).
+    // (dword 7 is not used: the second read takes dwords 4..6)
+    static_assert(kPnCntRows == 8 && kPnMaxDword + (kPnRpg + 3) / 4 <= 7, "count reads of 16 + 12 bytes per tile");
+    typedef int i32x3v __attribute__((ext_vector_type(3)));
+    auto to_counts = [&](const i32x4v lo, const i32x3v hi, uint32_t (&c)[kPnCntRows]) {
+        c[0] = lo.x; c[1] = lo.y; c[2] = lo.z; c[3] = lo.w;
+        c[4] = hi.x; c[5] = hi.y; c[6] = hi.z; c[7] = 0;
+    };
     // Entry i's run of tile t + 1 is fetched right after entry i is done with
     // tile t, so its latency hides behind the rest of the tile: lane g loads
     // the run's nonzero g (its 1-based position byte and its value; masked
-    // loads give 0 and 0 past the run).  Iteration -1 only fetches tile 0,
-    // with the same instructions in the same order as every later iteration:
-    // the compiler's vmcnt waits then count exactly the loads issued after
-    // the one they wait for.  The fetch after the last tile has n = 0.
-    uint32_t cn[kPnRpg], mx[kMaxWords];
+    // loads give 0 and 0 past the run).  Tile 0's runs are fetched before
+    // the loop, with the same instructions in the same order as every later
+    // fetch: the compiler's vmcnt waits then count exactly the loads issued
+    // after the one they wait for.  The fetch after the last tile has n = 0.
+    // cn: counts of tile t (cursor advance, longest runs); cnx: of tile t + 1
+    // (masks of the fetches for t + 1).
+    uint32_t cn[kPnCntRows], cnx[kPnCntRows];
     uint32_t q[kPnRpg];
     float vvq[kPnRpg];
-#pragma unroll
-    for (int i = 0; i < kPnRpg; i++) {
-        cn[i] = 0;
-        q[i] = 0;
-        vvq[i] = 0.f;
+    {
+        const i32x4v* cw = reinterpret_cast<const i32x4v*>(a.cnt) +
+                           (static_cast<size_t>(u.y) * kPnWaves + wave) * (kPnCntRows / 4);
+        const i32x4v hi = cw[1];
+        to_counts(cw[0], i32x3v{hi.x, hi.y, hi.z}, cn);
     }
 #pragma unroll
-    for (int w = 0; w < kMaxWords; w++) mx[w] = 0;
-    for (int t = -1; t < u.z; t++) {
-        if (t >= 0) __syncthreads();
-        const uint32_t zb = lds0 + pn_zrow_off<T, E>(t & 1);
+    for (int i = 0; i < kPnRpg; i++) {
+        const int nn = static_cast<int>((cn[i] >> shift) & 255);
+        const bool ok = g < nn;
+        const uint32_t k = static_cast<uint32_t>(cur[i] + g);
+        q[i] = __builtin_amdgcn_raw_buffer_load_b8(rpos, ok ? k : kOob, 0, 0);
+        vvq[i] = load_val<T>(rval, k, ok);
+        // loads in the loop's order (no reordering across entries)
+        asm volatile("" ::: "memory");
+    }
+    for (int t = 0; t < u.z; t++) {
+        pn_barrier();
         const bool more = t + 1 < u.z;
-        uint32_t cnx[kPnRpg], mxx[kMaxWords];
+        const uint32_t zb = lds0 + pn_zrow_off<T, E>(t & 1);
         {
-            CU32* cw = counts(more ? t + 1 : t);
-#pragma unroll
-            for (int i = 0; i < kPnRpg; i++) cnx[i] = cw[i];
-#pragma unroll
-            for (int w = 0; w < kMaxWords; w++) mxx[w] = cw[kPnMaxDword + w];
+            const char* cs = smem + pn_cnt_off<T, E>(t & 1) + wave * (kPnCntRows * 4);
+            to_counts(*reinterpret_cast<const i32x4v*>(cs), *reinterpret_cast<const i32x3v*>(cs + 16), cnx);
         }
+        // entries' longest runs (uniform)
+        uint32_t mxw[(kPnRpg + 3) / 4];
 #pragma unroll
-        for (int i = 0; i < kPnRpg; i++) {
-            const int n = (cn[i] >> shift) & 255;
-            const int nmax = (mx[i / 4] >> (8 * (i % 4))) & 255;
+        for (int w = 0; w < (kPnRpg + 3) / 4; w++)
+            mxw[w] = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(cn[kPnMaxDword + w])));
+        pn_static_for<0, kPnRpg>([&](auto ic) {
+            constexpr int i = decltype(ic)::value;
+            const int nmax = static_cast<int>((mxw[i / 4] >> (8 * (i % 4))) & 255);
             if (nmax > 0) pn_run<T, E>(acc[i], q[i], vvq[i], nmax, zb, lanepart);
-            cur[i] += n;
+            cur[i] += static_cast<int>((cn[i] >> shift) & 255);
             const int nn = more ? static_cast<int>((cnx[i] >> shift) & 255) : 0;
             const bool ok = g < nn;
             const uint32_t k = static_cast<uint32_t>(cur[i] + g);
             q[i] = __builtin_amdgcn_raw_buffer_load_b8(rpos, ok ? k : kOob, 0, 0);
             vvq[i] = load_val<T>(rval, k, ok);
-            cn[i] = cnx[i];
-        }
+            asm volatile("" ::: "memory");
+        });
 #pragma unroll
-        for (int w = 0; w < kMaxWords; w++) mx[w] = mxx[w];
+        for (int j = 0; j < kPnCntRows; j++) cn[j] = cnx[j];
     }
     // ---- results: C rows, or this unit's partial rows of a split panel
     const int nu = u.w >= 0 ? a.panel_units[u.x] : 0;

@@ -628,7 +628,7 @@ extern "C" int tca_plan_panels(const int32_t* rowptr, const int32_t* colidx, int
         const int64_t stride = static_cast<int64_t>(p.waves) * kPanelCntRows * 4;
         const int64_t sz[16] = {p.n_panels, p.n_tiles(), static_cast<int64_t>(p.units.size()),
                                 static_cast<int64_t>(p.longrows.size()), p.R, p.P, p.waves, p.rpg, p.elems, p.chunks,
-                                p.nnz, p.staged, p.n_segments, p.n_rows, stride, 0};
+                                p.nnz, p.staged, p.n_segments, p.n_rows, stride, kPanelMaxDword};
         std::copy(sz, sz + 16, sizes);
         if (!rows) return TCA_OK;
         if (!cols || !width || !cnt || !pos || !units || !panel_units || !ustart || !longrows)

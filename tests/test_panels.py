@@ -15,6 +15,7 @@ def emulate(a: S.CSR, b: np.ndarray, pp: dict, n: int):
     """The panel kernel's traversal (units -> slots -> tiles -> CSR runs) in
     numpy; returns {row: C row} for the rows in panels and the visit mask."""
     R, P, rpg, stride = pp["R"], pp["P"], pp["rpg"], pp["cnt_stride"]
+    crow, mxd = pp["cnt_rows"], pp["max_dword"]
     vals = a.values_f32()
     bf = S.from_storage(b, a.dtype).astype(np.float32)
     seen = np.zeros(a.nnz, np.int32)
@@ -28,13 +29,13 @@ def emulate(a: S.CSR, b: np.ndarray, pp: dict, n: int):
             cur = pp["ustart"][u * R + s]
             acc = np.zeros(n, np.float32)
             for t in range(t0, t0 + nt):
-                c = int(pp["cnt"][t * stride + (wave * 16 + i) * 4 + g])
+                c = int(pp["cnt"][t * stride + (wave * crow + i) * 4 + g])
                 if row < 0:
                     assert c == 0
                     continue
                 # the longest run of the entry's four groups: the steps the wave takes
-                c4 = pp["cnt"][t * stride + (wave * 16 + i) * 4:][:4]
-                assert int(pp["cnt"][t * stride + (wave * 16 + 12 + i // 4) * 4 + i % 4]) == int(c4.max())
+                c4 = pp["cnt"][t * stride + (wave * crow + i) * 4:][:4]
+                assert int(pp["cnt"][t * stride + (wave * crow + mxd + i // 4) * 4 + i % 4]) == int(c4.max())
                 for k in range(cur, cur + c):
                     # positions are 1-based (0 is the kernel's zero row)
                     assert 1 <= int(pp["pos"][k]) <= int(pp["width"][t]) <= P
