@@ -49,6 +49,7 @@ constexpr int kPnRpg = 5;       // rows per 16-lane group (planner: kPanelRpg)
 constexpr int kPnCntRows = 8;   // count dwords per wavefront and tile (planner: kPanelCntRows)
 constexpr int kPnMaxDword = 5;  // first dword of the entries' longest counts (planner: kPanelMaxDword)
 constexpr int kPnThreads = (kPnWaves + 1) * 64;
+constexpr int kPnBufLimit = 77824;  // bytes of one tile buffer at most (two, with zero rows and count slots, fit 160 KiB)
 
 struct PanelArgs {
     const int4* units;       // {panel, first tile, tiles, segment base or -1}
@@ -72,7 +73,7 @@ template <typename T, int E>
 struct PanelGeom {
     static constexpr int kLaneBytes = E * static_cast<int>(sizeof(T));  // bytes per lane per staged row
     static constexpr int kRowBytes = 16 * kLaneBytes;                   // bytes per staged row chunk
-    static constexpr int kP = (65536 / kRowBytes) < 255 ? (65536 / kRowBytes) : 255;  // tile columns
+    static constexpr int kP = (kPnBufLimit / kRowBytes) < 255 ? (kPnBufLimit / kRowBytes) : 255;  // tile columns
     static constexpr int kInstrs = (kP * kRowBytes + 1023) / 1024;  // 1 KiB transfers per tile
     static constexpr int kBufBytes = kInstrs * 1024;                 // one tile buffer (whole transfers)
     static_assert(kLaneBytes == 8 || kLaneBytes == 16 || kLaneBytes == 32, "lane geometry");
@@ -87,7 +88,7 @@ static_assert(kPnCntTileBytes <= kPnCntSlot && kPnCntTileBytes % 16 == 0, "count
 
 // LDS of the panel kernel: two tile buffers and their zero rows, two count slots.
 constexpr int panel_lds_bytes(int row_bytes) {
-    return 2 * (((((65536 / row_bytes) < 255 ? (65536 / row_bytes) : 255) * row_bytes + 1023) / 1024) * 1024 + row_bytes) +
+    return 2 * (((((kPnBufLimit / row_bytes) < 255 ? (kPnBufLimit / row_bytes) : 255) * row_bytes + 1023) / 1024) * 1024 + row_bytes) +
            2 * kPnCntSlot;
 }
 

@@ -280,7 +280,7 @@ bool panel_default_ok(int32_t N, int32_t es) {
     return e > 0 && static_cast<int64_t>(N) * es >= 256;
 }
 
-int32_t panel_tile_cols(int32_t chunk_bytes) { return std::min<int32_t>(255, 65536 / chunk_bytes); }
+int32_t panel_tile_cols(int32_t chunk_bytes) { return std::min<int32_t>(255, 77824 / chunk_bytes); }
 
 void plan_panels_routed(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_t K, int32_t N,
                         int32_t dtype, uint32_t flags, const std::vector<uint8_t>& skip, PanelPlan* p) {

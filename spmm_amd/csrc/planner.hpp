@@ -184,7 +184,7 @@ int32_t panel_elems(int32_t N, int32_t es);
 // Default routing also needs B rows of at least 256 bytes (N * elem_size).
 bool panel_default_ok(int32_t N, int32_t es);
 // Tile width P for a chunk of `chunk_bytes` bytes: two LDS buffers of at most
-// 64 KiB, positions fit one byte (P <= 255).
+// 76 KiB, positions fit one byte (P <= 255).
 int32_t panel_tile_cols(int32_t chunk_bytes);
 // plan_panels with the routing of a plan: none with TCA_PLAN_NO_PANELS, every
 // eligible row with TCA_PLAN_FORCE_PANELS, else (B rows of >= 256 bytes)

@@ -266,7 +266,9 @@ void launch_pack(const tca_spmm_plan* p, const void* val, hipStream_t s) {
 
 static_assert(kPnWaves == kPanelWaves && kPnRpg == kPanelRpg && kPnCntRows == kPanelCntRows &&
                   kPnMaxDword == kPanelMaxDword, "panel plan layout");
-static_assert(PanelGeom<float, 8>::kP == 128 && PanelGeom<float, 4>::kP == 255, "panel tile widths (panel_tile_cols)");
+static_assert(PanelGeom<float, 8>::kP == 152 && PanelGeom<float, 4>::kP == 255 && PanelGeom<float, 2>::kP == 255,
+              "panel tile widths (panel_tile_cols)");
+static_assert(panel_lds_bytes(512) <= 160 * 1024, "panel LDS budget");
 static_assert(kMfmaPairShape.max_step_entries == kDmaMaxStepEntries, "planner and paired kernel agree on step size");
 static_assert(kMfmaPairShape.win_rows == kDmaWinRows && kMfmaPairShape.tile_cols == kDmaTileCols, "paired tile shape");
 static_assert(kMfmaDenseShape.win_rows == kDmaWinRows && kMfmaDenseShape.tile_cols == kDmaTileCols, "dense tile shape");
