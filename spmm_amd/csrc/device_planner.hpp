@@ -289,4 +289,43 @@ __global__ void dm_ucols_kernel(int nw, int kw, const uint32_t* __restrict__ bm,
     }
 }
 
+// Compaction of the dense tiles (the host planner's rule, tca_spmm.hip):
+// per global step, bit L of mask[step * 8 + b] is set when fragment cell
+// (row block b, lane L) holds an entry.  `pos` are the sorted dense-tile half
+// indices of the routed nonzeros (step * kDmaATile + a_cell).
+__global__ void dm_cmask_kernel(const uint32_t* __restrict__ pos, int n, unsigned long long* __restrict__ mask) {
+    for (int x = blockIdx.x * blockDim.x + threadIdx.x; x < n; x += gridDim.x * blockDim.x) {
+        const uint32_t g = pos[x] / kDmaATile, c = (pos[x] % kDmaATile) / 8;
+        atomicOr(&mask[static_cast<size_t>(g) * 8 + c / 64], 1ull << (c % 64));
+    }
+}
+
+// flag |= 1 when a step has more non-empty cells than a compacted step holds
+// (cells - 1: the last cell stays zero for the empty lanes).
+__global__ void dm_cfit_kernel(const unsigned long long* __restrict__ mask, int64_t steps, int cells,
+                               int* __restrict__ flag) {
+    for (int64_t g = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; g < steps;
+         g += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        int tot = 0;
+#pragma unroll
+        for (int b = 0; b < 8; b++) tot += __popcll(mask[g * 8 + b]);
+        if (tot > cells - 1) atomicOr(flag, 1);
+    }
+}
+
+// Compacted position of every entry, in place: the step's base, the rank of
+// its cell among the step's non-empty cells (in cell order), the half within
+// the cell.  Ranks grow with the cell, so the positions stay sorted.
+__global__ void dm_cpos_kernel(uint32_t* __restrict__ pos, int n, const unsigned long long* __restrict__ mask,
+                               int cells) {
+    for (int x = blockIdx.x * blockDim.x + threadIdx.x; x < n; x += gridDim.x * blockDim.x) {
+        const uint32_t g = pos[x] / kDmaATile, h = pos[x] % kDmaATile, c = h / 8;
+        const unsigned long long* m = mask + static_cast<size_t>(g) * 8;
+        uint32_t rank = 0;
+        for (uint32_t b = 0; b < c / 64; b++) rank += static_cast<uint32_t>(__popcll(m[b]));
+        rank += static_cast<uint32_t>(__popcll(m[c / 64] & ((1ull << (c % 64)) - 1ull)));
+        pos[x] = g * static_cast<uint32_t>(cells * 8) + rank * 8u + h % 8;
+    }
+}
+
 }  // namespace tca

@@ -1127,6 +1127,37 @@ int tca_spmm_plan_create_device(const int32_t* d_rowptr, const int32_t* d_colidx
                                            wordpre, wmap, wgbase, N, p->d_ucols);
                     }
                     p->adense_halves = static_cast<size_t>(steps_all) * kDmaATile + 512;
+                    // Compacted steps under the host planner's rule: by default for
+                    // natural-order tiles (unless TCA_PLAN_MFMA_DENSE), always with
+                    // TCA_PLAN_MFMA_COMPACT, when every step fits.
+                    const bool compact_want = (flags & TCA_PLAN_MFMA_COMPACT) != 0 ||
+                                              (natural && (flags & TCA_PLAN_MFMA_DENSE) == 0);
+                    if (compact_want && nz_take > 0) {
+                        const size_t nmask = static_cast<size_t>(steps_all) * 8;
+                        if ((st = dev_upload(&p->d_amask, nullptr, nmask))) return bail(st);
+                        if (hipMemsetAsync(p->d_amask, 0, nmask * 8, s) != hipSuccess ||
+                            hipMemsetAsync(cnt + 3, 0, sizeof(int), s) != hipSuccess)
+                            return bail(fail(TCA_ERR_HIP, "hipMemsetAsync failed"));
+                        auto* mk = reinterpret_cast<unsigned long long*>(p->d_amask);
+                        hipLaunchKernelGGL(dm_cmask_kernel, grid_for(nz_take), blk, 0, s, p->d_dn_pos,
+                                           static_cast<int>(nz_take), mk);
+                        hipLaunchKernelGGL(dm_cfit_kernel, grid_for(steps_all), blk, 0, s, mk, steps_all, kCpCells,
+                                           cnt + 3);
+                        int over = 0;
+                        if (hipMemcpyAsync(&over, cnt + 3, sizeof(int), hipMemcpyDeviceToHost, s) != hipSuccess ||
+                            hipStreamSynchronize(s) != hipSuccess)
+                            return bail(fail(TCA_ERR_HIP, "compaction check failed"));
+                        if (over == 0) {
+                            hipLaunchKernelGGL(dm_cpos_kernel, grid_for(nz_take), blk, 0, s, p->d_dn_pos,
+                                               static_cast<int>(nz_take), mk, kCpCells);
+                            p->mfma_compact = true;
+                            p->adense_halves = static_cast<size_t>(steps_all) * (kCpCells * 8) + 512;
+                            if (const char* lb = std::getenv("TCA_COMPACT_LB")) p->mfma_compact_lb = std::atoi(lb) == 4 ? 4 : 3;
+                        } else {
+                            (void)hipFree(p->d_amask);
+                            p->d_amask = nullptr;
+                        }
+                    }
                     if ((st = dev_upload(&p->d_adense, nullptr, p->adense_halves))) return bail(st);
                     if (hipMemsetAsync(p->d_adense, 0, p->adense_halves * 2, s) != hipSuccess)
                         return bail(fail(TCA_ERR_HIP, "hipMemsetAsync of the dense tiles failed"));

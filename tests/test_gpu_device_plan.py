@@ -79,17 +79,16 @@ def _mfma_cases():
 
 
 @pytest.mark.parametrize("flags", [S.TCA_PLAN_DEFAULT, S.TCA_PLAN_MFMA_DENSE,
-                                   S.TCA_PLAN_FORCE_MFMA | S.TCA_PLAN_MFMA_DENSE],
-                         ids=["default", "dense", "force-dense"])
+                                   S.TCA_PLAN_FORCE_MFMA | S.TCA_PLAN_MFMA_DENSE, S.TCA_PLAN_MFMA_COMPACT],
+                         ids=["default", "dense", "force-dense", "compact"])
 @pytest.mark.parametrize("name,a,n", list(_mfma_cases()), ids=[c[0] for c in _mfma_cases()])
 def test_device_mfma_plan_equals_host_plan(torch_cuda, name, a, n, flags):
-    """Windows, dense-tile positions, B row offsets and row tasks equal the
-    host planner's; products bit-identical and equal to the oracle on exact
-    inputs.  (By default, windows that do not cover most of K run on the
-    paired kernel when planned on the host and on condensed dense tiles when
-    planned on the GPU, and windows that do run on compacted dense tiles
-    when planned on the host and on plain dense tiles when planned on the
-    GPU: there only the products are compared.)"""
+    """Windows, dense-tile positions (compacted or not), B row offsets and
+    row tasks equal the host planner's; products bit-identical and equal to
+    the oracle on exact inputs.  (By default, windows that do not cover most
+    of K run on the paired kernel when planned on the host and on condensed
+    dense tiles when planned on the GPU: there only the products are
+    compared.)"""
     torch = torch_cuda
     print(f"device mfma plan {name} flags={flags}: M={a.nrow} K={a.ncol} nnz={a.nnz} N={n}", flush=True)
     rng = np.random.default_rng(11)
@@ -100,9 +99,9 @@ def test_device_mfma_plan_equals_host_plan(torch_cuda, name, a, n, flags):
         dp = S.Plan.from_device(_dev(torch, a.rowptr), _dev(torch, a.colidx), a.nrow, a.ncol, a.nnz, n, a.dtype, flags)
         try:
             hi, di = hp.info(), dp.info()
-            # host default tiles the device planner does not build: paired (3),
-            # compacted dense tiles (7); the device plans plain dense tiles
-            same = not (flags == S.TCA_PLAN_DEFAULT and hi["tile_kernel"] in (3, 7))
+            # host default tiles the device planner does not build: paired (3);
+            # the device plans condensed dense tiles there
+            same = not (flags == S.TCA_PLAN_DEFAULT and hi["tile_kernel"] == 3)
             for key in ("n_windows_mfma", "rows_mfma", "nnz_mfma"):
                 assert hi[key] == di[key], (name, key, hi[key], di[key])
             if same:
@@ -114,7 +113,9 @@ def test_device_mfma_plan_equals_host_plan(torch_cuda, name, a, n, flags):
                 for x, y in zip(hp.export_tiles(), dp.export_tiles()):
                     assert np.array_equal(x, y), name
             else:
-                assert di["tile_kernel"] == (4 if hi["tile_kernel"] == 3 else 5), (hi["tile_kernel"], di["tile_kernel"])
+                assert di["tile_kernel"] == 4, (hi["tile_kernel"], di["tile_kernel"])
+            if flags == S.TCA_PLAN_DEFAULT and name.endswith("-natural") and hi["n_windows_mfma"] > 0:
+                assert hi["tile_kernel"] == di["tile_kernel"] == S.TCA_TILES_COMPACT, (hi, di)
             val, bd = _dev(torch, a.values), _dev(torch, b)
             outs = []
             for pl in (hp, dp):
