@@ -4,10 +4,11 @@
 // panel's rows are spread over the 16-lane groups of kPanelWaves consumer
 // wavefronts (four groups per wavefront, rpg rows per group), and the unit's
 // tiles -- ranges of the panel's sorted column union, P columns each -- are
-// staged one after another into two LDS buffers by one producer wavefront.
-// While the consumers multiply tile t, the producer's global -> LDS
-// transfers bring tile t + 1; one barrier per tile separates the two.  1024
-// threads, one workgroup per CU (LDS), four wavefronts per SIMD.
+// staged one after another into two LDS buffers by kPnProducers producer
+// wavefronts, each issuing every kPnProducers-th transfer of a tile.  While
+// the consumers multiply tile t, the producers' global -> LDS transfers bring
+// tile t + 1; one barrier per tile separates the two.  1024 threads, one
+// workgroup per CU (LDS), four wavefronts per SIMD.
 //
 // Consumers.  A 16-lane group owns one B-row chunk of 16 * E elements (all
 // of N, or one column chunk of it): lane g holds E elements of each of its
@@ -24,10 +25,12 @@
 // CSR order inside a unit, and units of a split panel are summed in unit
 // order by seg_finalize_kernel: results do not depend on the schedule.
 //
-// Producer.  It issues only global_load_lds_dwordx4 transfers (16 bytes per
-// lane land at M0 + 16 * lane) and waits for its own transfers before the
-// barrier; it executes no LDS instruction (an LDS instruction of a wavefront
-// waits for that wavefront's in-flight transfers).  The byte offsets of the
+// Producers.  They issue only global_load_lds_dwordx4 transfers (16 bytes
+// per lane land at M0 + 16 * lane) and wait for their own transfers before
+// the barrier; they execute no LDS instruction (an LDS instruction of a
+// wavefront waits for that wavefront's in-flight transfers).  Several
+// producers because the staging is latency-bound: with one, the consumers
+// waited 57 % of their time at the barriers and the producer 4 %.  The byte offsets of the
 // tile's B rows come through vector loads; a transfer's lanes select theirs
 // by readlane.  With each tile the producer also stages the next tile's
 // per-wavefront run counts.
@@ -44,11 +47,13 @@
 
 namespace tca {
 
-constexpr int kPnWaves = 15;    // consumer wavefronts (planner: kPanelWaves)
-constexpr int kPnRpg = 5;       // rows per 16-lane group (planner: kPanelRpg)
-constexpr int kPnCntRows = 8;   // count dwords per wavefront and tile (planner: kPanelCntRows)
-constexpr int kPnMaxDword = 5;  // first dword of the entries' longest counts (planner: kPanelMaxDword)
-constexpr int kPnThreads = (kPnWaves + 1) * 64;
+constexpr int kPnProducers = 8;  // producer wavefronts: each issues every kPnProducers-th transfer of a tile
+constexpr int kPnWaves = 16 - kPnProducers;  // consumer wavefronts (planner: kPanelWaves)
+constexpr int kPnRpg = 8;       // rows per 16-lane group (planner: kPanelRpg)
+constexpr int kPnMaxDword = kPnRpg;  // first dword of the entries' longest counts (planner: kPanelMaxDword)
+constexpr int kPnCntUsed = kPnMaxDword + (kPnRpg + 3) / 4;  // count dwords a wavefront reads per tile
+constexpr int kPnCntRows = (kPnCntUsed + 3) / 4 * 4;  // count dwords per wavefront and tile (planner: kPanelCntRows)
+constexpr int kPnThreads = (kPnWaves + kPnProducers) * 64;
 constexpr int kPnBufLimit = 77824;  // bytes of one tile buffer at most (two, with zero rows and count slots, fit 160 KiB)
 
 struct PanelArgs {
@@ -270,8 +275,12 @@ __global__ __launch_bounds__(kPnThreads, 1) void panel_kernel(PanelArgs a) {
     const int unit = blockIdx.x / a.chunks;
     const int4 u = a.units[unit];
 
-    if (wave == kPnWaves) {
-        // ---- producer: tile t + 1 into buffer (t + 1) & 1 while tile t is used
+    if (wave >= kPnWaves) {
+        // ---- producers: tile t + 1 into buffer (t + 1) & 1 while tile t is used;
+        // producer pid issues transfers pid, pid + kPnProducers, ... of a tile (and
+        // producer 0 the counts), so each has at most kInstrs / kPnProducers + 1
+        // transfers in flight (a wavefront's vmcnt counts 63 at most)
+        const int pid = wave - kPnWaves;
         const int piece = lane % (G::kRowBytes / 16);
         const int sub = lane / (G::kRowBytes / 16);  // row within one 1 KiB transfer
         constexpr int kRowsPerInstr = 1024 / G::kRowBytes;
@@ -304,10 +313,10 @@ __global__ __launch_bounds__(kPnThreads, 1) void panel_kernel(PanelArgs a) {
         const uint32_t cnt_lane = 16u * static_cast<uint32_t>(lane < kPnCntTileBytes / 16 ? lane : 0);
         auto stage = [&](const uint32_t (&o)[kOffRegs], int ninstr, int buf, int rel) {
             const int tn = u.y + (rel + 1 < u.z ? rel + 1 : rel);
-            pn_dma(a.cnt, static_cast<uint32_t>(tn) * kPnCntTileBytes + cnt_lane, lds0 + pn_cnt_off<T, E>(buf));
+            if (pid == 0) pn_dma(a.cnt, static_cast<uint32_t>(tn) * kPnCntTileBytes + cnt_lane, lds0 + pn_cnt_off<T, E>(buf));
 #pragma unroll
             for (int k = 0; k < G::kInstrs; k++) {
-                if (k < ninstr) {
+                if (k % kPnProducers == pid && k < ninstr) {
                     const int r0 = k * kRowsPerInstr;
                     uint32_t off = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(o[r0 / 64]), r0 % 64));
 #pragma unroll
@@ -376,20 +385,35 @@ __global__ __launch_bounds__(kPnThreads, 1) void panel_kernel(PanelArgs a) {
     const int shift = 8 * group;
     const uint32_t lds0 = pn_lds_addr(smem);
     const uint32_t lanepart = static_cast<uint32_t>((G::kLaneBytes == 32 ? 16 : G::kLaneBytes) * g);
-    // Counts: per tile and wavefront 8 dwords; dword i (i < rpg) holds entry
-    // i's four group counts, byte i % 4 of dword kPnMaxDword + i / 4 entry
-    // i's longest.  Tile 0's come through one vector load before the loop;
+    // Counts: per tile and wavefront kPnCntRows dwords; dword i (i < rpg)
+    // holds entry i's four group counts, byte i % 4 of dword kPnMaxDword + i / 4
+    // entry i's longest.  Tile 0's come through one vector load before the loop;
     // tile t + 1's are read from the count slot the producer staged with tile
     // t (LDS reads, ordered with the B-row reads: no scalar loads, which
     // share lgkmcnt with the LDS reads and return out of order, and no
     // loop-carried vector loads, whose copies between iterations would wait
     // for every load in flight).
-    // (dword 7 is not used: the second read takes dwords 4..6)
-    static_assert(kPnCntRows == 8 && kPnMaxDword + (kPnRpg + 3) / 4 <= 7, "count reads of 16 + 12 bytes per tile");
-    typedef int i32x3v __attribute__((ext_vector_type(3)));
-    auto to_counts = [&](const i32x4v lo, const i32x3v hi, uint32_t (&c)[kPnCntRows]) {
-        c[0] = lo.x; c[1] = lo.y; c[2] = lo.z; c[3] = lo.w;
-        c[4] = hi.x; c[5] = hi.y; c[6] = hi.z; c[7] = 0;
+    // Only the kPnCntUsed dwords in use are read (16-byte reads, then one of
+    // 4, 8 or 12 bytes): a register loaded and never used would be reused by
+    // the compiler while its read is in flight, which costs a wait.
+    auto read_counts = [&](const char* p, uint32_t (&c)[kPnCntUsed]) {
+        pn_static_for<0, kPnCntUsed / 4>([&](auto jc) {
+            constexpr int j = decltype(jc)::value;
+            const i32x4v v = *reinterpret_cast<const i32x4v*>(p + 16 * j);
+            c[4 * j] = v.x; c[4 * j + 1] = v.y; c[4 * j + 2] = v.z; c[4 * j + 3] = v.w;
+        });
+        constexpr int b = kPnCntUsed / 4 * 4, rem = kPnCntUsed % 4;
+        if constexpr (rem == 1) {
+            c[b] = *reinterpret_cast<const uint32_t*>(p + 4 * b);
+        } else if constexpr (rem == 2) {
+            typedef int i32x2t __attribute__((ext_vector_type(2)));
+            const i32x2t v = *reinterpret_cast<const i32x2t*>(p + 4 * b);
+            c[b] = v.x; c[b + 1] = v.y;
+        } else if constexpr (rem == 3) {
+            typedef int i32x3t __attribute__((ext_vector_type(3)));
+            const i32x3t v = *reinterpret_cast<const i32x3t*>(p + 4 * b);
+            c[b] = v.x; c[b + 1] = v.y; c[b + 2] = v.z;
+        }
     };
     // Entry i's run of tile t + 1 is fetched right after entry i is done with
     // tile t, so its latency hides behind the rest of the tile: lane g loads
@@ -400,15 +424,11 @@ __global__ __launch_bounds__(kPnThreads, 1) void panel_kernel(PanelArgs a) {
     // after the one they wait for.  The fetch after the last tile has n = 0.
     // cn: counts of tile t (cursor advance, longest runs); cnx: of tile t + 1
     // (masks of the fetches for t + 1).
-    uint32_t cn[kPnCntRows], cnx[kPnCntRows];
+    uint32_t cn[kPnCntUsed], cnx[kPnCntUsed];
     uint32_t q[kPnRpg];
     float vvq[kPnRpg];
-    {
-        const i32x4v* cw = reinterpret_cast<const i32x4v*>(a.cnt) +
-                           (static_cast<size_t>(u.y) * kPnWaves + wave) * (kPnCntRows / 4);
-        const i32x4v hi = cw[1];
-        to_counts(cw[0], i32x3v{hi.x, hi.y, hi.z}, cn);
-    }
+    read_counts(reinterpret_cast<const char*>(a.cnt) + (static_cast<size_t>(u.y) * kPnWaves + wave) * (kPnCntRows * 4),
+                cn);
 #pragma unroll
     for (int i = 0; i < kPnRpg; i++) {
         const int nn = static_cast<int>((cn[i] >> shift) & 255);
@@ -424,8 +444,7 @@ __global__ __launch_bounds__(kPnThreads, 1) void panel_kernel(PanelArgs a) {
         const bool more = t + 1 < u.z;
         const uint32_t zb = lds0 + pn_zrow_off<T, E>(t & 1);
         {
-            const char* cs = smem + pn_cnt_off<T, E>(t & 1) + wave * (kPnCntRows * 4);
-            to_counts(*reinterpret_cast<const i32x4v*>(cs), *reinterpret_cast<const i32x3v*>(cs + 16), cnx);
+            read_counts(smem + pn_cnt_off<T, E>(t & 1) + wave * (kPnCntRows * 4), cnx);
         }
         // entries' longest runs (uniform)
         uint32_t mxw[(kPnRpg + 3) / 4];
@@ -445,7 +464,7 @@ __global__ __launch_bounds__(kPnThreads, 1) void panel_kernel(PanelArgs a) {
             asm volatile("" ::: "memory");
         });
 #pragma unroll
-        for (int j = 0; j < kPnCntRows; j++) cn[j] = cnx[j];
+        for (int j = 0; j < kPnCntUsed; j++) cn[j] = cnx[j];
     }
     // ---- results: C rows, or this unit's partial rows of a split panel
     const int nu = u.w >= 0 ? a.panel_units[u.x] : 0;

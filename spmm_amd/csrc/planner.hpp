@@ -170,10 +170,10 @@ struct PanelPlan {
     int32_t n_rows = 0;        // rows in panels
     int32_t n_tiles() const { return P ? static_cast<int32_t>(cols.size() / P) : 0; }
 };
-constexpr int kPanelWaves = 15;   // consumer wavefronts per workgroup (plus one producer: 1024 threads)
-constexpr int kPanelRpg = 5;      // rows per 16-lane group
-constexpr int kPanelCntRows = 8;  // count dwords per wave and tile
-constexpr int kPanelMaxDword = 5; // first dword of the entries' longest counts
+constexpr int kPanelWaves = 8;    // consumer wavefronts per workgroup (plus eight producers: 1024 threads)
+constexpr int kPanelRpg = 8;      // rows per 16-lane group
+constexpr int kPanelMaxDword = kPanelRpg;  // first dword of the entries' longest counts
+constexpr int kPanelCntRows = (kPanelMaxDword + (kPanelRpg + 3) / 4 + 3) / 4 * 4;  // count dwords per wave and tile
 static_assert(kPanelRpg <= kPanelMaxDword && kPanelMaxDword + (kPanelRpg + 3) / 4 <= kPanelCntRows, "cnt layout");
 constexpr int kPanelMaxRun = 16;  // nonzeros of one row in one tile (one 16-lane batch)
 constexpr double kPanelMinReuse = 2.0;
