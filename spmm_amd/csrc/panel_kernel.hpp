@@ -30,10 +30,10 @@
 // the barrier; they execute no LDS instruction (an LDS instruction of a
 // wavefront waits for that wavefront's in-flight transfers).  Several
 // producers because the staging is latency-bound: with one, the consumers
-// waited 57 % of their time at the barriers and the producer 4 %.  The byte offsets of the
-// tile's B rows come through vector loads; a transfer's lanes select theirs
-// by readlane.  With each tile the producer also stages the next tile's
-// per-wavefront run counts.
+// waited 57 % of their time at the barriers and the producer 4 %.  The byte
+// offsets of a tile's B rows come through vector loads; a transfer's lanes
+// select theirs by readlane.  With each tile producer 0 also stages the next
+// tile's per-wavefront run counts.
 //
 // Functionally replaces the reference's multirow_per_tb / multitb_per_row
 // (src/our_spmm.cu:24-295) for the rows routed to panels: each output row is
@@ -61,7 +61,6 @@ struct PanelArgs {
     const int* panel_units;  // units per panel
     const int* rows;         // [panel * R + slot]
     const uint32_t* boff;    // [tile * P + position]: byte offset in B of the staged row
-    const uint8_t* width;    // [tile]: columns of the tile (1..P)
     const uint32_t* cnt;     // [tile][wave][16 entries] dwords: byte g = group g's count
     const void* pos;         // [nnz] bytes, padded to whole dwords (pos_bytes)
     const int* ustart;       // [unit * R + slot]
@@ -295,9 +294,7 @@ __global__ __launch_bounds__(kPnThreads, 1) void panel_kernel(PanelArgs a) {
         const uint32_t lds0 = pn_lds_addr(smem);
         // A tile's P offsets come through coalesced vector loads, lane l
         // holding position j * 64 + l in o[j]; each transfer takes its rows'
-        // offsets by readlane.  The offsets (and width) of tile t + 2 load
-        // while tile t + 1's transfers are in flight, so one wait per tile
-        // covers both.  Positions past P clamp to P - 1 (never staged).
+        // offsets by readlane.  Positions past P clamp to P - 1 (never staged).
         constexpr int kOffRegs = (G::kP + 63) / 64;
         auto load_offs = [&](int tile, uint32_t (&o)[kOffRegs]) {
             const uint32_t* bo = a.boff + static_cast<size_t>(tile) * G::kP;
@@ -307,16 +304,19 @@ __global__ __launch_bounds__(kPnThreads, 1) void panel_kernel(PanelArgs a) {
                 o[j] = bo[r < G::kP ? r : G::kP - 1];
             }
         };
-        auto n_instr = [&](int tile) { return (a.width[tile] * G::kRowBytes + 1023) / 1024; };
         // counts of tile rel + 1 (clamped to the unit's last tile) into count
         // slot buf; lanes past the counts re-read the first 16 bytes
         const uint32_t cnt_lane = 16u * static_cast<uint32_t>(lane < kPnCntTileBytes / 16 ? lane : 0);
-        auto stage = [&](const uint32_t (&o)[kOffRegs], int ninstr, int buf, int rel) {
+        // Every transfer of the tile, whatever its width: columns past the
+        // width repeat the tile's last B row (plan padding) into rows that no
+        // consumer reads, so each producer issues the same number of memory
+        // operations every tile and its waits below are compile-time counts.
+        auto stage = [&](const uint32_t (&o)[kOffRegs], int buf, int rel) {
             const int tn = u.y + (rel + 1 < u.z ? rel + 1 : rel);
             if (pid == 0) pn_dma(a.cnt, static_cast<uint32_t>(tn) * kPnCntTileBytes + cnt_lane, lds0 + pn_cnt_off<T, E>(buf));
 #pragma unroll
             for (int k = 0; k < G::kInstrs; k++) {
-                if (k % kPnProducers == pid && k < ninstr) {
+                if (k % kPnProducers == pid) {
                     const int r0 = k * kRowsPerInstr;
                     uint32_t off = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(o[r0 / 64]), r0 % 64));
 #pragma unroll
@@ -328,37 +328,35 @@ __global__ __launch_bounds__(kPnThreads, 1) void panel_kernel(PanelArgs a) {
                 }
             }
         };
-        // The compiler cannot see the transfers (inline asm), so it would
-        // wait on the offset loads with vmcnt counts that then also wait for
-        // the transfers issued before each readlane.  Passing the offsets
-        // through an empty asm after the explicit wait ends their load
-        // dependence there, where nothing else is in flight.
+        // Per tile: the transfers of tile t + 1, then the offsets of tile t + 2
+        // (loaded unconditionally, clamped), then a wait that leaves only
+        // those kOffRegs loads in flight (land): the tile has landed, while
+        // the offsets' latency runs on into the next tile period.  After the
+        // barrier only those loads can be in flight: a full wait there, and
+        // the offsets pass through an empty asm (ready), which ends their load
+        // dependence for the compiler -- it cannot see the transfers (inline
+        // asm), and its own wait before each readlane would otherwise also
+        // wait for the transfers issued before it.
+        auto land = [&]() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kOffRegs) : "memory"); };
+        static_assert(kOffRegs <= 15, "vmcnt immediate");
         uint32_t o[kOffRegs];
-        auto settle = [&](int& nin) {
+        auto ready = [&]() {
             pn_wait_all();
 #pragma unroll
             for (int j = 0; j < kOffRegs; j++) asm volatile("" : "+v"(o[j]));
-            nin = __builtin_amdgcn_readfirstlane(nin);
-            asm volatile("" : "+s"(nin));
         };
-        int nin = n_instr(u.y);
         load_offs(u.y, o);
-        settle(nin);
-        stage(o, nin, 0, 0);
-        if (u.z > 1) {
-            nin = n_instr(u.y + 1);
-            load_offs(u.y + 1, o);
-        }
-        settle(nin);
+        ready();
+        stage(o, 0, 0);
+        load_offs(u.y + (u.z > 1 ? 1 : 0), o);
+        land();
         for (int t = 0; t < u.z; t++) {
             pn_barrier();
             if (t + 1 < u.z) {
-                stage(o, nin, (t + 1) & 1, t + 1);
-                if (t + 2 < u.z) {
-                    nin = n_instr(u.y + t + 2);
-                    load_offs(u.y + t + 2, o);
-                }
-                settle(nin);
+                ready();
+                stage(o, (t + 1) & 1, t + 1);
+                load_offs(u.y + (t + 2 < u.z ? t + 2 : t + 1), o);
+                land();
             }
         }
         return;

@@ -90,7 +90,6 @@ struct tca_spmm_plan {
     int* d_panel_units = nullptr;
     int* d_prows = nullptr;
     int* d_pcols = nullptr;  // panel tiles' staged B rows, as byte offsets into B
-    uint8_t* d_pwidth = nullptr;
     uint32_t* d_pcnt = nullptr;
     uint8_t* d_ppos = nullptr;
     int* d_ustart = nullptr;
@@ -179,7 +178,6 @@ void free_plan_device(tca_spmm_plan* p) {
     (void)hipFree(p->d_panel_units);
     (void)hipFree(p->d_prows);
     (void)hipFree(p->d_pcols);
-    (void)hipFree(p->d_pwidth);
     (void)hipFree(p->d_pcnt);
     (void)hipFree(p->d_ppos);
     (void)hipFree(p->d_ustart);
@@ -380,7 +378,6 @@ void launch_panels_t(const tca_spmm_plan* p, const void* val, const void* B, flo
     a.panel_units = p->d_panel_units;
     a.rows = p->d_prows;
     a.boff = reinterpret_cast<const uint32_t*>(p->d_pcols);
-    a.width = p->d_pwidth;
     a.cnt = p->d_pcnt;
     a.pos = p->d_ppos;
     a.ustart = p->d_ustart;
@@ -731,7 +728,6 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
                 for (size_t j = 0; j < boff.size(); j++) boff[j] = static_cast<int32_t>(static_cast<uint32_t>(pp.cols[j]) * rb);
                 if ((st = dev_upload(&p->d_pcols, boff.data(), boff.size()))) return bail(st);
             }
-            if ((st = dev_upload(&p->d_pwidth, pp.width.data(), pp.width.size()))) return bail(st);
             if ((st = dev_upload(&p->d_pcnt, pp.cnt.data(), pp.cnt.size() / 4))) return bail(st);
             if ((st = dev_upload(&p->d_ppos, pp.pos.data(), pp.pos.size()))) return bail(st);
             p->n_pos_bytes = pp.pos.size();
