@@ -176,7 +176,9 @@ constexpr int kPanelMaxDword = kPanelRpg;  // first dword of the entries' longes
 constexpr int kPanelCntRows = (kPanelMaxDword + (kPanelRpg + 3) / 4 + 3) / 4 * 4;  // count dwords per wave and tile
 static_assert(kPanelRpg <= kPanelMaxDword && kPanelMaxDword + (kPanelRpg + 3) / 4 <= kPanelCntRows, "cnt layout");
 constexpr int kPanelMaxRun = 16;  // nonzeros of one row in one tile (one 16-lane batch)
-constexpr double kPanelMinReuse = 2.0;
+// nnz / |union| a panel needs to be kept (measured on MI355X: config 2 1.94 ms
+// per SpMM at 1.2 against 2.00 at 2.0, config 3 3.73 against 4.09)
+constexpr double kPanelMinReuse = 1.2;
 constexpr int64_t kPanelMinNnz = int64_t(1) << 21;  // fewer nonzeros in panels: none (unless forced)
 // Lane geometry: 16 lanes cover one column chunk of a B row, E elements each
 // (E = 8, 4 or 2 with E * elem_size in 8..32 bytes); 0 when N does not fit.
@@ -188,7 +190,7 @@ bool panel_default_ok(int32_t N, int32_t es);
 int32_t panel_tile_cols(int32_t chunk_bytes);
 // plan_panels with the routing of a plan: none with TCA_PLAN_NO_PANELS, every
 // eligible row with TCA_PLAN_FORCE_PANELS, else (B rows of >= 256 bytes)
-// panels of reuse >= 2 when they hold at least kPanelMinNnz nonzeros in all.
+// panels of reuse >= kPanelMinReuse when they hold at least kPanelMinNnz nonzeros in all.
 void plan_panels_routed(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_t K, int32_t N,
                         int32_t dtype, uint32_t flags, const std::vector<uint8_t>& skip, PanelPlan* p);
 // Builds the panel plan over the rows with skip[r] == 0 (skip may be empty).
