@@ -289,7 +289,8 @@ int tca_condense_windows(const int32_t* rowptr, const int32_t* colidx, int32_t M
  * (M x K, width N) and dtype, with no rows routed to the MFMA kernel.  Call with tasks == NULL
  * to get the counts, then again with tasks[4*n_tasks], perm[n_perm] and
  * longrows[4*n_long].  Task int4 {x,y,z,w}: w == 0 row task (x row, [y,z)
- * nonzeros); w == 1 multi task (x offset into perm, y rows, z longest row);
+ * nonzeros); w == 1 multi task (x offset into perm, y rows, z longest row;
+ * z == 0: up to 64 empty rows whose C rows are cleared);
  * w & 3 == 2 segment task (x long-row id, [y,z) nonzeros, w >> 2 segment
  * slot); w & 3 == 3 quarter of a wide row (x row, [y,z) nonzeros, w >> 2
  * quarter), four consecutive 4-aligned tasks per wide row.  longrows entry

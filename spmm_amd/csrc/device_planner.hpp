@@ -68,16 +68,12 @@ __global__ void dp_lengths_kernel(const int* __restrict__ rowptr, int M, const i
 
 // Boundaries in the first M descending keys (length + 1): out[0] = rows
 // longer than wide_len, out[1] = longer than row_len, out[2] = longer than
-// multi_max.
+// max(multi_max, 0), out[3] = non-empty rows.
 __global__ void dp_bounds_kernel(const uint32_t* __restrict__ len, int M, int wide_len, int row_len, int multi_max,
                                  int* __restrict__ out) {
-    const int th[3] = {wide_len, row_len, multi_max};
+    const int th[4] = {wide_len, row_len, max(multi_max, 0), 0};
     const int k = threadIdx.x;
-    if (k >= 3) return;
-    if (th[k] < 0) {
-        out[k] = M;
-        return;
-    }
+    if (k >= 4) return;
     int lo = 0, hi = M;  // first index whose length <= th[k]
     while (lo < hi) {
         const int mid = lo + (hi - lo) / 2;
@@ -101,7 +97,7 @@ struct DpEmitArgs {
     int4* tasks;
     int* perm;
     int4* longrows;
-    int M, n_long, end_wide, end_row, slots, seg_total;  // M: the rows planned (Mp)
+    int M, n_long, end_wide, end_row, end_nz, slots, seg_total;  // M: the rows planned (Mp)
 };
 
 // Every row of the order writes its own tasks (see the file comment).
@@ -128,13 +124,18 @@ __global__ void dp_emit_kernel(DpEmitArgs a) {
         } else if (i < a.end_row) {
             a.tasks[4 * n_wide + a.seg_total + (i - a.end_wide)] = make_int4(r, beg, beg + static_cast<int>(L), kTaskRow);
         } else {
+            // short rows in groups of `slots`, then empty rows in groups of kZeroRows
             const int k = i - a.end_row;
             a.perm[k] = r;
-            if (k % a.slots == 0) {
-                const int g = k / a.slots;
-                const int cnt = min(a.slots, a.M - i);
-                a.tasks[4 * n_wide + a.seg_total + (a.end_row - a.end_wide) + g] =
-                    make_int4(k, cnt, static_cast<int>(L), kTaskMulti);
+            const int base = 4 * n_wide + a.seg_total + (a.end_row - a.end_wide);
+            if (i < a.end_nz) {
+                if (k % a.slots == 0)
+                    a.tasks[base + k / a.slots] = make_int4(k, min(a.slots, a.end_nz - i), static_cast<int>(L), kTaskMulti);
+            } else {
+                const int k0 = i - a.end_nz;
+                if (k0 % kZeroRows == 0)
+                    a.tasks[base + (a.end_nz - a.end_row + a.slots - 1) / a.slots + k0 / kZeroRows] =
+                        make_int4(k, min(kZeroRows, a.M - i), 0, kTaskMulti);
             }
         }
     }

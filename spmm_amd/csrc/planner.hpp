@@ -18,13 +18,17 @@
 
 namespace tca {
 
-// Task kinds of the row kernel (int4 {x, y, z, w}).
+// Task kinds of the row kernel (int4 {x, y, z, w}).  Multi tasks hold at most
+// `slots` rows, except zero tasks (z == 0), which hold up to kZeroRows empty
+// rows whose C rows the wavefront only clears.
 enum TaskKind : int32_t {
     kTaskRow = 0,    // x = row, y = nnz begin, z = nnz end: all slots split one row
-    kTaskMulti = 1,  // x = offset into perm, y = rows in group (<= slots), z = longest row
+    kTaskMulti = 1,  // x = offset into perm, y = rows in group, z = longest row; z == 0: empty rows
     kTaskSeg = 2,    // x = long-row id, y = nnz begin, z = nnz end, w = 2 | (segment slot << 2)
     kTaskWide = 3,   // x = row, y = nnz begin, z = nnz end of this quarter; all 4 waves of a workgroup
 };
+
+constexpr int32_t kZeroRows = 64;
 
 struct Int4 {
     int32_t x, y, z, w;
@@ -204,8 +208,8 @@ void plan_panels(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_
 // empty).  Rows are assigned longest first.  The categories, in task order:
 // wide rows (row_len < length <= wide_len, 4 tasks each), long rows
 // (length > wide_len, segments of at most seg_len, summed in segment order),
-// row tasks (multi_max < length <= row_len), then groups of `slots` short
-// rows (length <= multi_max).
+// row tasks (max(multi_max, 0) < length <= row_len), groups of `slots` short
+// rows (0 < length <= multi_max), then groups of up to kZeroRows empty rows.
 // Per-window statistics the MFMA routing decides on: nonzeros, size of the
 // column union, most nonzeros in one 32-column condensed step.
 struct WinStat {

@@ -7,7 +7,8 @@
 //   row   -- the S slots take every S-th nonzero of one row, 8 loads in flight
 //            per lane; the slots' fp32 partial rows are then summed with
 //            xor shuffles (identical order on every run) and written once.
-//   multi -- each slot walks its own short row (rows grouped by length).
+//   multi -- each slot walks its own short row (rows grouped by length);
+//            a group of empty rows (z == 0) only clears their C rows.
 //   seg   -- like row over one segment of a long row; the segment's partial
 //            row goes to plan scratch and seg_finalize_kernel, launched next
 //            on the same stream, adds the segments in segment order.
@@ -194,6 +195,12 @@ __global__ __launch_bounds__(256) void row_kernel(RowArgs a) {
 #pragma unroll
     for (int e = 0; e < E; e++) acc[e] = 0.f;
 
+    if (t.w == 1 && t.z == 0) {  // zero task: clear the C rows of up to kZeroRows empty rows
+        if (colok)
+            for (int r = slot; r < t.y; r += 1 << logS)
+                store_row<E>(a.C + static_cast<size_t>(a.perm[t.x + r]) * a.N + col, acc);
+        return;
+    }
     if (t.w == 1) {  // multi: slot s walks row perm[t.x + s]
         int row = -1, beg = 0, len = 0;
         if (slot < t.y) {

@@ -1195,7 +1195,9 @@ int tca_spmm_plan_create_device(const int32_t* d_rowptr, const int32_t* d_colidx
         if (hipMemcpyAsync(h_cnt, cnt, sizeof h_cnt, hipMemcpyDeviceToHost, s) != hipSuccess ||
             hipStreamSynchronize(s) != hipSuccess)
             return bail(fail(TCA_ERR_HIP, "planning kernels failed"));
-        const int n_long = h_cnt[0], end_wide = h_cnt[1], end_row = h_cnt[2];
+        // (cnt[3] held flags before the bounds kernel wrote it; with Mp == 0 it did not run)
+        if (Mp == 0) h_cnt[0] = h_cnt[1] = h_cnt[2] = h_cnt[3] = 0;
+        const int n_long = h_cnt[0], end_wide = h_cnt[1], end_row = h_cnt[2], end_nz = h_cnt[3];
         // segment slots of the long rows: exclusive sum of their segment counts
         int seg_total = 0;
         if (n_long > 0) {
@@ -1218,7 +1220,7 @@ int tca_spmm_plan_create_device(const int32_t* d_rowptr, const int32_t* d_colidx
                 return bail(fail(TCA_ERR_HIP, "segment scan failed"));
         }
         const int n_wide = end_wide - n_long, n_row = end_row - end_wide, n_short = Mp - end_row;
-        const int n_multi = (n_short + slots - 1) / slots;
+        const int n_multi = (end_nz - end_row + slots - 1) / slots + (Mp - end_nz + kZeroRows - 1) / kZeroRows;
         p->ntasks = 4 * n_wide + seg_total + n_row + n_multi;
         p->rows.n_wide = 4 * n_wide;
         p->rows.n_seg = seg_total;
@@ -1244,6 +1246,7 @@ int tca_spmm_plan_create_device(const int32_t* d_rowptr, const int32_t* d_colidx
             ea.n_long = n_long;
             ea.end_wide = end_wide;
             ea.end_row = end_row;
+            ea.end_nz = end_nz;
             ea.slots = slots;
             ea.seg_total = seg_total;
             hipLaunchKernelGGL(dp_emit_kernel, grid_for(Mp), blk, 0, s, ea);

@@ -373,12 +373,15 @@ def test_plan_covers_every_row_once(n, dtype):
     parts = {}
     for i, (x, y, z, w) in enumerate(tasks):
         if w == 0:
-            assert (y, z) == (rowptr[x], rowptr[x + 1]) and z - y <= geo["row_len"]
+            assert (y, z) == (rowptr[x], rowptr[x + 1]) and 0 < z - y <= geo["row_len"]
             covered[x] += 1
         elif w == 1:
-            assert 1 <= y <= 64 // g
             rows = perm[x:x + y]
-            assert z == lens[rows].max() and z <= geo["multi_max"]
+            if z == 0:  # zero task: empty rows only
+                assert 1 <= y <= 64 and np.all(lens[rows] == 0)
+            else:
+                assert 1 <= y <= 64 // g and np.all(lens[rows] > 0)
+                assert z == lens[rows].max() and z <= geo["multi_max"]
             covered[rows] += 1
         elif w & 3 == 2:
             row, first, nseg, _ = longrows[x]
@@ -402,6 +405,8 @@ def test_plan_covers_every_row_once(n, dtype):
     # wide groups first, then segments, rows and multi groups
     kinds = [w & 3 for *_, w in tasks]
     assert kinds == sorted(kinds, key=lambda k: {3: 0, 2: 1, 0: 2, 1: 3}[k])
+    zero = [w == 1 and z == 0 for _, _, z, w in tasks]
+    assert zero == sorted(zero)  # zero tasks last
 
 
 # ------------------------------------------------------------------ COO
