@@ -23,6 +23,7 @@
 
 #include <type_traits>
 
+#include "planner.hpp"
 #include "row_kernel.hpp"
 
 namespace tca {
@@ -33,7 +34,6 @@ constexpr int kDmaTileCols = 64;                      // columns of C per workgr
 constexpr int kDmaBRow = kDmaTileCols;                // halves per B-tile row in LDS (128 bytes)
 constexpr int kDmaATile = kDmaWinRows * kStepK;       // halves of one A tile (fragment order)
 constexpr int kDmaMaxStepEntries = 2 * 256;           // nonzeros a step of the paired kernel may hold
-constexpr int kXcds = 8;                              // XCDs of the MI355X (workgroup x runs on XCD x % 8)
 
 // A-tile cell of (row, step column) in MFMA fragment order: row block,
 // 8-column group, row, column (each fragment read is one contiguous 1 KiB).

@@ -58,6 +58,7 @@ constexpr int kPnBufLimit = 77824;  // bytes of one tile buffer at most (two, wi
 
 struct PanelArgs {
     const int4* units;       // {panel, first tile, tiles, segment base or -1}
+    const int* order;        // [workgroup]: unit, or -1 for an idle workgroup
     const int* panel_units;  // units per panel
     const int* rows;         // [panel * R + slot]
     const uint32_t* boff;    // [tile * P + position]: byte offset in B of the staged row
@@ -271,7 +272,8 @@ __global__ __launch_bounds__(kPnThreads, 1) void panel_kernel(PanelArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int chunk = blockIdx.x % a.chunks;
-    const int unit = blockIdx.x / a.chunks;
+    const int unit = a.order[blockIdx.x / a.chunks];
+    if (unit < 0) return;  // idle: every wavefront leaves before the first barrier
     const int4 u = a.units[unit];
 
     if (wave >= kPnWaves) {

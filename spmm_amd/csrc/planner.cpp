@@ -529,6 +529,61 @@ void plan_panels(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_
         for (int32_t s = 0; s < R; s++) p->n_rows += c.slots[s] >= 0;
     }
     p->n_segments = seg;
+    order_units(K, p);
+}
+
+void order_units(int32_t K, PanelPlan* p) {
+    const int32_t nu = static_cast<int32_t>(p->units.size());
+    p->order.clear();
+    const char* e = std::getenv("TCA_PANEL_ORDER");  // tuning override: 0 = natural order
+    if (p->chunks != 1 || (e && std::atoi(e) == 0)) {
+        for (int32_t u = 0; u < nu; u++) p->order.push_back(u);
+        return;
+    }
+    // The hardware deals workgroups to the XCDs round robin (workgroup b on
+    // XCD b % 8), each XCD with its own L2.  A unit stages the B rows of one
+    // range of its panel's sorted column union.  Units whose columns span at
+    // most K / 8 are sorted by the middle of that span and cut into 8 runs of
+    // equal tiles; run x goes to XCD x in column order, so the units resident
+    // together on one XCD stage nearby B rows and meet them in its L2.  Wider
+    // units follow, each on the XCD with the fewest tiles so far; shorter
+    // queues end in idle workgroups.
+    const int32_t P = p->P;
+    std::vector<std::pair<int64_t, int32_t>> local;
+    std::vector<int32_t> wide;
+    int64_t local_tiles = 0;
+    for (int32_t u = 0; u < nu; u++) {
+        const Int4& t = p->units[u];
+        const int64_t lo = p->cols[static_cast<size_t>(t.y) * P];
+        const int64_t hi = p->cols[static_cast<size_t>(t.y + t.z) * P - 1];  // padding repeats the last column
+        if ((hi - lo) * kXcds <= K) {
+            local.push_back({lo + hi, u});
+            local_tiles += t.z;
+        } else {
+            wide.push_back(u);
+        }
+    }
+    std::stable_sort(local.begin(), local.end());
+    std::vector<std::vector<int32_t>> q(kXcds);
+    std::vector<int64_t> load(kXcds, 0);
+    int64_t cum = 0;
+    for (const auto& l : local) {
+        const int32_t z = p->units[l.second].z;
+        const int32_t x = static_cast<int32_t>(std::min<int64_t>(kXcds - 1, (2 * cum + z) * kXcds / (2 * local_tiles)));
+        q[x].push_back(l.second);
+        load[x] += z;
+        cum += z;
+    }
+    for (int32_t u : wide) {
+        const int32_t x = static_cast<int32_t>(std::min_element(load.begin(), load.end()) - load.begin());
+        q[x].push_back(u);
+        load[x] += p->units[u].z;
+    }
+    size_t len = 0;
+    for (const auto& v : q) len = std::max(len, v.size());
+    p->order.assign(len * kXcds, -1);
+    for (int32_t x = 0; x < kXcds; x++)
+        for (size_t k = 0; k < q[x].size(); k++) p->order[k * kXcds + x] = q[x][k];
 }
 
 }  // namespace tca

@@ -18,6 +18,8 @@
 
 namespace tca {
 
+constexpr int kXcds = 8;  // XCDs of the MI355X: the hardware deals workgroup b to XCD b % 8
+
 // Task kinds of the row kernel (int4 {x, y, z, w}).  Multi tasks hold at most
 // `slots` rows, except zero tasks (z == 0), which hold up to kZeroRows empty
 // rows whose C rows the wavefront only clears.
@@ -164,6 +166,7 @@ struct PanelPlan {
     std::vector<uint8_t> cnt;
     std::vector<uint8_t> pos;  // indexed by CSR nonzero (0 outside panels)
     std::vector<Int4> units;
+    std::vector<int32_t> order;  // [workgroup]: unit it runs, -1 = idle (see order_units)
     std::vector<int32_t> panel_units;
     std::vector<int32_t> ustart;
     std::vector<Int4> longrows;
@@ -184,6 +187,8 @@ constexpr int kPanelMaxRun = 16;  // nonzeros of one row in one tile (one 16-lan
 // per SpMM at 1.2 against 2.00 at 2.0, config 3 3.73 against 4.09)
 constexpr double kPanelMinReuse = 1.2;
 constexpr int64_t kPanelMinNnz = int64_t(1) << 21;  // fewer nonzeros in panels: none (unless forced)
+// Launch order of the units (PanelPlan::order).
+void order_units(int32_t K, PanelPlan* p);
 // Lane geometry: 16 lanes cover one column chunk of a B row, E elements each
 // (E = 8, 4 or 2 with E * elem_size in 8..32 bytes); 0 when N does not fit.
 int32_t panel_elems(int32_t N, int32_t es);

@@ -85,8 +85,9 @@ struct tca_spmm_plan {
     float* d_partials = nullptr;
     // row panels (panel kernel)
     PanelPlan panels;
-    int32_t n_units = 0;
+    int32_t n_units = 0, n_pblocks = 0;  // panel units; panel workgroups (units and idle ones)
     int4* d_units = nullptr;
+    int32_t* d_porder = nullptr;
     int* d_panel_units = nullptr;
     int* d_prows = nullptr;
     int* d_pcols = nullptr;  // panel tiles' staged B rows, as byte offsets into B
@@ -175,6 +176,7 @@ void free_plan_device(tca_spmm_plan* p) {
     (void)hipFree(p->d_dn_src);
     (void)hipFree(p->d_dn_pos);
     (void)hipFree(p->d_units);
+    (void)hipFree(p->d_porder);
     (void)hipFree(p->d_panel_units);
     (void)hipFree(p->d_prows);
     (void)hipFree(p->d_pcols);
@@ -375,6 +377,7 @@ template <typename T, int E>
 void launch_panels_t(const tca_spmm_plan* p, const void* val, const void* B, float* C, float* W, hipStream_t s) {
     PanelArgs a;
     a.units = p->d_units;
+    a.order = p->d_porder;
     a.panel_units = p->d_panel_units;
     a.rows = p->d_prows;
     a.boff = reinterpret_cast<const uint32_t*>(p->d_pcols);
@@ -389,7 +392,7 @@ void launch_panels_t(const tca_spmm_plan* p, const void* val, const void* B, flo
     a.chunks = p->panels.chunks;
     a.pos_bytes = static_cast<uint32_t>(p->n_pos_bytes);
     a.val_bytes = static_cast<uint32_t>(static_cast<uint64_t>(p->nnz) * sizeof(T));
-    hipLaunchKernelGGL((panel_kernel<T, E>), dim3(p->n_units * p->panels.chunks), dim3(kPnThreads), 0, s, a);
+    hipLaunchKernelGGL((panel_kernel<T, E>), dim3(p->n_pblocks * p->panels.chunks), dim3(kPnThreads), 0, s, a);
 }
 
 int launch_panels(const tca_spmm_plan* p, const void* val, const void* B, float* C, float* W, hipStream_t s) {
@@ -468,7 +471,7 @@ void fill_info(tca_spmm_plan* p) {
     in.n_panels = p->panels.n_panels;
     in.n_panel_units = p->n_units;
     in.rows_panels = p->panels.n_rows;
-    in.panel_blocks = p->n_units * p->panels.chunks;
+    in.panel_blocks = p->n_pblocks * p->panels.chunks;
     in.nnz_panels = p->panels.nnz;
     in.staged_panels = p->panels.staged;
     in.panel_blockdim = kPnThreads;
@@ -719,6 +722,8 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
         if (p->n_units > 0) {
             const PanelPlan& pp = p->panels;
             if ((st = dev_upload(&p->d_units, pp.units.data(), pp.units.size()))) return bail(st);
+            if ((st = dev_upload(&p->d_porder, pp.order.data(), pp.order.size()))) return bail(st);
+            p->n_pblocks = static_cast<int32_t>(pp.order.size());
             if ((st = dev_upload(&p->d_panel_units, pp.panel_units.data(), pp.panel_units.size()))) return bail(st);
             if ((st = dev_upload(&p->d_prows, pp.rows.data(), pp.rows.size()))) return bail(st);
             {

@@ -42,9 +42,12 @@ def test_panels_exact_all_geometries(torch_cuda, dtype, widths):
 
 
 @pytest.mark.parametrize("unit", ["1500", "40000"])
-def test_panels_split_into_units(torch_cuda, monkeypatch, unit):
-    """Small units split panels by tiles; the partial rows are summed in unit order."""
+@pytest.mark.parametrize("order", ["0", "1"])
+def test_panels_split_into_units(torch_cuda, monkeypatch, unit, order):
+    """Small units split panels by tiles; the partial rows are summed in unit order.  The
+    launch order (natural, or XCD queues padded with idle workgroups) changes no result."""
     monkeypatch.setenv("TCA_PANEL_UNIT", unit)
+    monkeypatch.setenv("TCA_PANEL_ORDER", order)
     rng = np.random.default_rng(17)
     base, _ = S.gen_zipf_rows(3000, 6000, 200000, s=1.5, cap=5000, seed=5)
     a = exact(base, S.TCA_F32)
@@ -53,6 +56,10 @@ def test_panels_split_into_units(torch_cuda, monkeypatch, unit):
         info = pl.info()
         got = run_gpu(torch_cuda, a, b, plan=pl)
     assert info["n_panel_units"] > info["n_panels"] and info["n_long_rows"] > 0, info
+    if order == "0":
+        assert info["panel_blocks"] == info["n_panel_units"], info
+    else:
+        assert info["panel_blocks"] % 8 == 0 and info["panel_blocks"] >= info["n_panel_units"], info
     assert np.array_equal(got, oracle_c(a, b))
 
 
