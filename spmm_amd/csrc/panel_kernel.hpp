@@ -47,9 +47,9 @@
 
 namespace tca {
 
-constexpr int kPnProducers = 8;  // producer wavefronts: each issues every kPnProducers-th transfer of a tile
+constexpr int kPnProducers = 4;  // producer wavefronts: each issues every kPnProducers-th transfer of a tile
 constexpr int kPnWaves = 16 - kPnProducers;  // consumer wavefronts (planner: kPanelWaves)
-constexpr int kPnRpg = 8;       // rows per 16-lane group (planner: kPanelRpg)
+constexpr int kPnRpg = 4;       // rows per 16-lane group (planner: kPanelRpg)
 constexpr int kPnMaxDword = kPnRpg;  // first dword of the entries' longest counts (planner: kPanelMaxDword)
 constexpr int kPnCntUsed = kPnMaxDword + (kPnRpg + 3) / 4;  // count dwords a wavefront reads per tile
 constexpr int kPnCntRows = (kPnCntUsed + 3) / 4 * 4;  // count dwords per wavefront and tile (planner: kPanelCntRows)

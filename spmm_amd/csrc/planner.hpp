@@ -177,8 +177,8 @@ struct PanelPlan {
     int32_t n_rows = 0;        // rows in panels
     int32_t n_tiles() const { return P ? static_cast<int32_t>(cols.size() / P) : 0; }
 };
-constexpr int kPanelWaves = 8;    // consumer wavefronts per workgroup (plus eight producers: 1024 threads)
-constexpr int kPanelRpg = 8;      // rows per 16-lane group
+constexpr int kPanelWaves = 12;   // consumer wavefronts per workgroup (plus four producers: 1024 threads)
+constexpr int kPanelRpg = 4;      // rows per 16-lane group
 constexpr int kPanelMaxDword = kPanelRpg;  // first dword of the entries' longest counts
 constexpr int kPanelCntRows = (kPanelMaxDword + (kPanelRpg + 3) / 4 + 3) / 4 * 4;  // count dwords per wave and tile
 static_assert(kPanelRpg <= kPanelMaxDword && kPanelMaxDword + (kPanelRpg + 3) / 4 <= kPanelCntRows, "cnt layout");
