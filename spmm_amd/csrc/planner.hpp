@@ -183,9 +183,11 @@ constexpr int kPanelMaxDword = kPanelRpg;  // first dword of the entries' longes
 constexpr int kPanelCntRows = (kPanelMaxDword + (kPanelRpg + 3) / 4 + 3) / 4 * 4;  // count dwords per wave and tile
 static_assert(kPanelRpg <= kPanelMaxDword && kPanelMaxDword + (kPanelRpg + 3) / 4 <= kPanelCntRows, "cnt layout");
 constexpr int kPanelMaxRun = 16;  // nonzeros of one row in one tile (one 16-lane batch)
-// nnz / |union| a panel needs to be kept (measured on MI355X: config 2 1.94 ms
-// per SpMM at 1.2 against 2.00 at 2.0, config 3 3.73 against 4.09)
-constexpr double kPanelMinReuse = 1.2;
+// nnz / |union| a panel needs to be kept.  Measured on MI355X (per SpMM,
+// config 2 / config 3): 1.2 1.77 / 3.50 ms, 1.05 - / 3.50, 1.02 1.73 / 3.39,
+// 1.0 1.75 / 3.39: staged once per panel, even rows that share few columns
+// cost less than the row kernel's gathers; rows that share none stay there.
+constexpr double kPanelMinReuse = 1.02;
 constexpr int64_t kPanelMinNnz = int64_t(1) << 21;  // fewer nonzeros in panels: none (unless forced)
 // Launch order of the units (PanelPlan::order).
 void order_units(int32_t K, PanelPlan* p);

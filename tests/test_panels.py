@@ -106,7 +106,7 @@ def test_panel_plan_split_panels(monkeypatch):
 
 def test_panel_plan_routing_by_reuse(monkeypatch):
     """Default routing keeps a panel only when its nonzeros reuse its column
-    union at least 1.2 times; uniform short rows over a wide K do not.  (The
+    union at least 1.02 times; uniform short rows over a wide K do not.  (The
     minimum of nonzeros in panels is lowered for these small matrices.)"""
     monkeypatch.setenv("TCA_PANEL_MIN_NNZ", "1000")
     rng = np.random.default_rng(11)
