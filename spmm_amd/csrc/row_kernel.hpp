@@ -196,9 +196,25 @@ __global__ __launch_bounds__(256) void row_kernel(RowArgs a) {
     for (int e = 0; e < E; e++) acc[e] = 0.f;
 
     if (t.w == 1 && t.z == 0) {  // zero task: clear the C rows of up to kZeroRows empty rows
-        if (colok)
-            for (int r = slot; r < t.y; r += 1 << logS)
+        const int step = 1 << logS;
+        if constexpr (E == 8) {
+            // 32 bytes per lane: lane g clears 16-byte pieces g and g + chunk
+            // lanes of the chunk, so each store instruction covers whole
+            // 128-byte lines (store_row's two halves per lane would leave
+            // every line half written by each instruction)
+            const int c0 = chunk * a.chunk_lanes * 8;
+            const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+            if (g < a.chunk_lanes)
+                for (int r = slot; r < t.y; r += step) {
+                    float* dst = a.C + static_cast<size_t>(a.perm[t.x + r]) * a.N + c0;
+                    if (c0 + 4 * g < a.N) __builtin_nontemporal_store(z, reinterpret_cast<f32x4*>(dst + 4 * g));
+                    if (c0 + 4 * (g + a.chunk_lanes) < a.N)
+                        __builtin_nontemporal_store(z, reinterpret_cast<f32x4*>(dst + 4 * (g + a.chunk_lanes)));
+                }
+        } else if (colok) {
+            for (int r = slot; r < t.y; r += step)
                 store_row<E>(a.C + static_cast<size_t>(a.perm[t.x + r]) * a.N + col, acc);
+        }
         return;
     }
     if (t.w == 1) {  // multi: slot s walks row perm[t.x + s]
