@@ -22,7 +22,7 @@
 // reads issued before the current step's FMAs.  The wavefront steps through
 // the longest run of its four groups; lanes past their run read a zero row
 // (position 0) and multiply by 0.  The accumulation order of a row is its
-// CSR order inside a unit, and units of a split panel are summed in unit
+// CSR order inside a unit, and units of a split panel are summed in a fixed
 // order by seg_finalize_kernel: results do not depend on the schedule.
 //
 // Producers.  They issue only global_load_lds_dwordx4 transfers (16 bytes

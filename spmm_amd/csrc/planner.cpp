@@ -55,14 +55,16 @@ void plan_geometry(int32_t N, int32_t es, int32_t slices, RowPlan* p) {
 void plan_row_params(int64_t nnz, int32_t N, int32_t es, int32_t slices, RowPlan* p) {
     plan_geometry(N, es, slices, p);
     const int32_t slots = 64 >> p->log_lanes;
-    // Work per wavefront task: about nnz / 16384 nonzeros (two resident
+    // Work per wavefront task: about nnz / 32768 nonzeros (four resident
     // wavefronts on each of 256 CUs x 4 SIMDs x 8 slots, so long rows do
     // not leave a latency tail), a power of two of at least 256 nonzeros and
     // 2 rounds of slots * kUnroll loads, at most 32 rounds.  (Shorter tasks
     // cost more in partial sums than they gain in balance: on MI355X the
-    // 4096 x 4096 config-1 matrix runs 44 us at 256 and 47 us at 64.)
+    // 4096 x 4096 config-1 matrix runs 44 us at 256 and 47 us at 64;
+    // config 4, 20M nonzeros mostly in long rows' segments: 251 us at 2048,
+    // 212 at 1024, 217 at 512, 250 at 256.)
     const int64_t round = static_cast<int64_t>(slots) * kUnroll;
-    int64_t target = next_pow2(std::max<int64_t>(nnz / 16384, 1));
+    int64_t target = next_pow2(std::max<int64_t>(nnz / 32768, 1));
     target = std::min<int64_t>(std::max<int64_t>(32 * round, 256), std::max<int64_t>({2 * round, 256, target}));
     // Tuning overrides (not part of the interface): TCA_TARGET sets the
     // per-task length, TCA_WIDE=0 disables workgroup-shared rows,
@@ -589,6 +591,42 @@ void order_units(int32_t K, PanelPlan* p) {
     p->order.assign(len * kXcds, -1);
     for (int32_t x = 0; x < kXcds; x++)
         for (size_t k = 0; k < q[x].size(); k++) p->order[k * kXcds + x] = q[x][k];
+}
+
+void order_row_tasks(const int32_t* colidx, RowPlan* p) {
+    p->order.clear();
+    const char* e = std::getenv("TCA_ROW_ORDER");  // tuning override: 0 = task order
+    constexpr int32_t W = 4;                       // wavefronts per row-kernel workgroup (kRowWaves)
+    if (p->col_chunks != 1 || p->n_seg < kXcds * W || (e && std::atoi(e) == 0)) return;
+    // Workgroup b runs on XCD b % 8.  A long row's segments are column
+    // ranges of it (columns ascend within a row); sorted by the column of
+    // their middle nonzero and cut into 8 runs of equal count, run x goes to
+    // XCD x in column order, so the segments resident together on one XCD
+    // gather nearby B rows and meet them in its L2.  Wide rows' quarter
+    // groups (one workgroup each) keep their places before them, row and
+    // multi tasks follow in task order.
+    const int32_t nw = p->n_wide, ns = p->n_seg;
+    std::vector<std::pair<int32_t, int32_t>> seg(ns);
+    for (int32_t i = 0; i < ns; i++) {
+        const Int4& t = p->tasks[nw + i];
+        seg[i] = {colidx[t.y + (t.z - t.y) / 2], nw + i};
+    }
+    std::stable_sort(seg.begin(), seg.end());
+    for (int32_t i = 0; i < nw; i++) p->order.push_back(i);
+    std::vector<size_t> next(kXcds), end(kXcds);
+    for (int32_t x = 0; x < kXcds; x++) {
+        next[x] = static_cast<size_t>(ns) * x / kXcds;
+        end[x] = static_cast<size_t>(ns) * (x + 1) / kXcds;
+    }
+    for (size_t b = static_cast<size_t>(nw) / W;; b++) {
+        bool left = false;
+        for (int32_t x = 0; x < kXcds; x++) left = left || next[x] < end[x];
+        if (!left) break;
+        const size_t x = b % kXcds;
+        for (int32_t k = 0; k < W; k++) p->order.push_back(next[x] < end[x] ? seg[next[x]++].second : -1);
+    }
+    for (int32_t i = nw + ns; i < static_cast<int32_t>(p->tasks.size()); i++) p->order.push_back(i);
+    while (p->order.size() % W) p->order.push_back(-1);
 }
 
 }  // namespace tca

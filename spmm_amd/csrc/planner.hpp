@@ -49,6 +49,7 @@ struct RowPlan {
     std::vector<Int4> tasks;     // wide groups first (4-aligned), then seg, row, multi
     std::vector<int32_t> perm;   // row ids of multi tasks
     std::vector<Int4> longrows;  // {row, first segment slot, segments, 0}
+    std::vector<int32_t> order;  // [wavefront slot]: task it runs, -1 idle; empty = task order
     int32_t n_multi = 0, n_seg = 0, n_rowtasks = 0, n_wide = 0;
 };
 
@@ -149,7 +150,7 @@ void plan_row_params(int64_t nnz, int32_t N, int32_t es, int32_t slices, RowPlan
 //   units[u] = {panel, first tile, tiles, segment base or -1}: one
 //     workgroup; a panel whose nonzeros exceed the unit size is split into
 //     panel_units[panel] units by tiles, each writing partial rows that are
-//     summed in unit order: unit k of a panel whose first segment is f has
+//     summed in a fixed order: unit k of a panel whose first segment is f has
 //     segment base f + k, and slot s writes segment base + s * panel_units;
 //   ustart[u * R + s] = CSR index of slot s's first nonzero in unit u;
 //   longrows: {row, first segment, segments, 0} for split panels' rows.
@@ -191,6 +192,9 @@ constexpr double kPanelMinReuse = 1.02;
 constexpr int64_t kPanelMinNnz = int64_t(1) << 21;  // fewer nonzeros in panels: none (unless forced)
 // Launch order of the units (PanelPlan::order).
 void order_units(int32_t K, PanelPlan* p);
+// Launch order of the row kernel's tasks (RowPlan::order): segments of long
+// rows by column range, one range per XCD.
+void order_row_tasks(const int32_t* colidx, RowPlan* p);
 // Lane geometry: 16 lanes cover one column chunk of a B row, E elements each
 // (E = 8, 4 or 2 with E * elem_size in 8..32 bytes); 0 when N does not fit.
 int32_t panel_elems(int32_t N, int32_t es);
@@ -214,7 +218,7 @@ void plan_panels(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_
 // Builds the row-kernel task list for rows with skip[r] == 0 (skip may be
 // empty).  Rows are assigned longest first.  The categories, in task order:
 // wide rows (row_len < length <= wide_len, 4 tasks each), long rows
-// (length > wide_len, segments of at most seg_len, summed in segment order),
+// (length > wide_len, segments of at most seg_len, summed in a fixed order),
 // row tasks (max(multi_max, 0) < length <= row_len), groups of `slots` short
 // rows (0 < length <= multi_max), then groups of up to kZeroRows empty rows.
 // Per-window statistics the MFMA routing decides on: nonzeros, size of the

@@ -11,7 +11,7 @@
 //            a group of empty rows (z == 0) only clears their C rows.
 //   seg   -- like row over one segment of a long row; the segment's partial
 //            row goes to plan scratch and seg_finalize_kernel, launched next
-//            on the same stream, adds the segments in segment order.
+//            on the same stream, adds the segments in a fixed order.
 // Every row of C is written exactly once, so results do not depend on the
 // schedule, and C needs no zeroing.
 //
@@ -106,6 +106,7 @@ __device__ __forceinline__ void fma_pack(float (&acc)[E], float a, const Pack<T,
 
 struct RowArgs {
     const int4* tasks;
+    const int* order;  // [wavefront slot]: task, -1 idle; null: slot = task
     int ntasks;
     const int* rowptr;
     const int* perm;
@@ -180,8 +181,9 @@ __global__ __launch_bounds__(256) void row_kernel(RowArgs a) {
     // deals workgroups to the 8 XCDs round robin, so with 8 (or 4, 2) chunks
     // every XCD reads one fixed slice of B and keeps it in its own L2.
     const int chunk = blockIdx.x % a.col_chunks;
-    const int tid = (blockIdx.x / a.col_chunks) * kRowWaves + wave;
-    if (tid >= a.ntasks) return;
+    const int sid = (blockIdx.x / a.col_chunks) * kRowWaves + wave;
+    const int tid = a.order ? a.order[sid] : sid;
+    if (tid < 0 || tid >= a.ntasks) return;
     const __amdgpu_buffer_rsrc_t rcol = make_rsrc(a.colidx, a.colidx_bytes);
     const __amdgpu_buffer_rsrc_t rval = make_rsrc(a.val, a.val_bytes);
     const __amdgpu_buffer_rsrc_t rB = make_rsrc(a.B, a.B_bytes);
@@ -277,35 +279,70 @@ __global__ __launch_bounds__(256) void row_kernel(RowArgs a) {
         store_row<E>(a.partials + static_cast<size_t>(t.w >> 2) * a.N + col, acc);
 }
 
-// C[row, :] = sum over the row's segments, in segment order.  One wavefront
-// per (long row, chunk of 256 columns).
-__global__ __launch_bounds__(64) void seg_finalize_kernel(const int4* __restrict__ longrows,
-                                                          const float* __restrict__ partials, float* __restrict__ C,
-                                                          int N) {
-    const int4 lr = longrows[blockIdx.x];  // {row, first segment, segments, 0}
-    const int col = (blockIdx.y * 64 + threadIdx.x) * 4;
-    if (col >= N) return;
-    if ((N & 3) == 0) {  // rows 16-byte aligned
-        f32x4 s = {0.f, 0.f, 0.f, 0.f};
-        const f32x4* src = reinterpret_cast<const f32x4*>(partials + static_cast<size_t>(lr.y) * N + col);
-        const size_t stride = static_cast<size_t>(N) / 4;
-        int k = 0;
-        for (; k + 8 <= lr.z; k += 8) {  // eight loads in flight, added in segment order
-            f32x4 v[8];
+// Lanes of seg_finalize_kernel per partial row: four columns each, a power
+// of two up to 64 covering N; the 256 threads of a workgroup form 256 / L
+// groups of L lanes.
+__host__ __device__ inline int fin_lanes(int N) {
+    const int q = (N + 3) / 4;
+    int l = 1;
+    while (l < q && l < 64) l <<= 1;
+    return l;
+}
+
+// C[row, :] = sum of the row's partial rows (segments or panel units).  One
+// workgroup per (long row, 4L columns): group j of the 256 / L groups adds
+// the j-th contiguous block of the partial rows in order, eight loads in
+// flight, and group 0 adds the blocks' sums in block order.  The order is
+// fixed by N and the number of partial rows, so results do not depend on
+// the schedule.
+__global__ __launch_bounds__(256) void seg_finalize_kernel(const int4* __restrict__ longrows,
+                                                           const float* __restrict__ partials, float* __restrict__ C,
+                                                           int N) {
+    __shared__ f32x4 red[256];
+    const int4 lr = longrows[blockIdx.x];  // {row, first partial row, partial rows, 0}
+    const int L = fin_lanes(N), P = 256 / L;
+    const int grp = threadIdx.x / L, l = threadIdx.x % L;
+    const int col = (blockIdx.y * L + l) * 4;
+    const int k0 = static_cast<int>(static_cast<int64_t>(lr.z) * grp / P);
+    const int k1 = static_cast<int>(static_cast<int64_t>(lr.z) * (grp + 1) / P);
+    f32x4 s = {0.f, 0.f, 0.f, 0.f};
+    if (col < N) {
+        if ((N & 3) == 0) {  // rows 16-byte aligned
+            const f32x4* src = reinterpret_cast<const f32x4*>(partials + static_cast<size_t>(lr.y) * N + col);
+            const size_t stride = static_cast<size_t>(N) / 4;
+            int k = k0;
+            for (; k + 8 <= k1; k += 8) {
+                f32x4 v[8];
 #pragma unroll
-            for (int u = 0; u < 8; u++) v[u] = src[(k + u) * stride];
+                for (int u = 0; u < 8; u++) v[u] = src[(k + u) * stride];
 #pragma unroll
-            for (int u = 0; u < 8; u++) s += v[u];
+                for (int u = 0; u < 8; u++) s += v[u];
+            }
+            for (; k < k1; k++) s += src[k * stride];
+        } else {  // this thread's columns [col, col + 4) only
+            const float* src = partials + static_cast<size_t>(lr.y) * N + col;
+            for (int k = k0; k < k1; k++) {
+                const float* r = src + static_cast<size_t>(k) * N;
+                s.x += r[0];
+                if (col + 1 < N) s.y += r[1];
+                if (col + 2 < N) s.z += r[2];
+                if (col + 3 < N) s.w += r[3];
+            }
         }
-        for (; k < lr.z; k++) s += src[k * stride];
-        *reinterpret_cast<f32x4*>(C + static_cast<size_t>(lr.x) * N + col) = s;
-    } else {  // this thread's columns [col, col + 4) only
-        const int cend = min(col + 4, N);
-        for (int c = col; c < cend; c++) {
-            float s = 0.f;
-            for (int k = 0; k < lr.z; k++) s += partials[static_cast<size_t>(lr.y + k) * N + c];
-            C[static_cast<size_t>(lr.x) * N + c] = s;
-        }
+    }
+    red[threadIdx.x] = s;
+    __syncthreads();
+    if (grp != 0 || col >= N) return;
+    f32x4 t = red[l];
+    for (int j = 1; j < P; j++) t += red[j * L + l];
+    float* dst = C + static_cast<size_t>(lr.x) * N + col;
+    if ((N & 3) == 0) {
+        *reinterpret_cast<f32x4*>(dst) = t;
+    } else {
+        dst[0] = t.x;
+        if (col + 1 < N) dst[1] = t.y;
+        if (col + 2 < N) dst[2] = t.z;
+        if (col + 3 < N) dst[3] = t.w;
     }
 }
 

@@ -76,6 +76,8 @@ struct tca_spmm_plan {
     int* d_rowptr = nullptr;
     int* d_colidx = nullptr;
     int4* d_tasks = nullptr;
+    int32_t* d_torder = nullptr;  // row-kernel launch order (null: task order)
+    int32_t n_torder = 0;
     int* d_perm = nullptr;
     int4* d_longrows = nullptr;
     int32_t n_longrows = 0;   // rows split into segments (entries of d_longrows)
@@ -161,6 +163,7 @@ void free_plan_device(tca_spmm_plan* p) {
     (void)hipFree(p->d_rowptr);
     (void)hipFree(p->d_colidx);
     (void)hipFree(p->d_tasks);
+    (void)hipFree(p->d_torder);
     (void)hipFree(p->d_perm);
     (void)hipFree(p->d_longrows);
     (void)hipFree(p->d_partials);
@@ -203,10 +206,18 @@ struct PlanHolder {
     }
 };
 
+// Row-kernel workgroups: kRowWaves task slots each (the launch order's
+// slots, or the tasks), times the column chunks.
+int row_blocks(const tca_spmm_plan* p) {
+    const int slots = p->n_torder > 0 ? p->n_torder : p->ntasks;
+    return ((slots + kRowWaves - 1) / kRowWaves) * p->rows.col_chunks;
+}
+
 template <typename T, int E>
 void launch_rows_t(const tca_spmm_plan* p, const void* val, const void* B, float* C, float* W, hipStream_t s) {
     RowArgs a;
     a.tasks = p->d_tasks;
+    a.order = p->d_torder;
     a.ntasks = p->ntasks;
     a.rowptr = p->d_rowptr;
     a.perm = p->d_perm;
@@ -223,15 +234,14 @@ void launch_rows_t(const tca_spmm_plan* p, const void* val, const void* B, float
     a.colidx_bytes = static_cast<uint32_t>(static_cast<uint64_t>(p->nnz) * 4);
     a.val_bytes = static_cast<uint32_t>(static_cast<uint64_t>(p->nnz) * sizeof(T));
     a.B_bytes = static_cast<uint32_t>(static_cast<uint64_t>(p->K) * p->N * sizeof(T));
-    const dim3 grid(((p->ntasks + kRowWaves - 1) / kRowWaves) * p->rows.col_chunks);
-    hipLaunchKernelGGL((row_kernel<T, E>), grid, dim3(64 * kRowWaves), 0, s, a);
+    hipLaunchKernelGGL((row_kernel<T, E>), dim3(row_blocks(p)), dim3(64 * kRowWaves), 0, s, a);
 }
 
 // Adds the segments of long rows (after the row kernel, same stream).
 void launch_finalize(const tca_spmm_plan* p, float* C, const float* W, hipStream_t s) {
     if (p->n_longrows == 0) return;
-    const dim3 fgrid(static_cast<unsigned>(p->n_longrows), (p->N + 255) / 256);
-    hipLaunchKernelGGL(seg_finalize_kernel, fgrid, dim3(64), 0, s, p->d_longrows, W, C, p->N);
+    const dim3 fgrid(static_cast<unsigned>(p->n_longrows), (p->N + 4 * fin_lanes(p->N) - 1) / (4 * fin_lanes(p->N)));
+    hipLaunchKernelGGL(seg_finalize_kernel, fgrid, dim3(256), 0, s, p->d_longrows, W, C, p->N);
 }
 
 template <typename T>
@@ -451,7 +461,7 @@ void fill_info(tca_spmm_plan* p) {
     in.chunk_lanes = p->rows.chunk_lanes;
     in.row_len = p->rows.row_len;
     in.wide_len = p->rows.wide_len;
-    in.row_blocks = ((p->ntasks + kRowWaves - 1) / kRowWaves) * p->rows.col_chunks;
+    in.row_blocks = row_blocks(p);
     in.row_blockdim = 64 * kRowWaves;
     in.seg_len = p->rows.seg_len;
     in.n_windows_mfma = static_cast<int32_t>(p->mfma.windows.size());
@@ -517,7 +527,8 @@ void print_launches(const tca_spmm_plan* p) {
     if (p->ntasks > 0)  // static LDS of row_kernel: kRowWaves partial row chunks of 64 lanes x E floats
         line(in.row_blocks, in.row_blockdim, 4.0 * kRowWaves * 64 * p->rows.elems_per_lane, "row_kernel");
     if (p->n_longrows > 0)
-        line(static_cast<long long>(p->n_longrows) * ((p->N + 255) / 256), 64, 0.0, "seg_finalize_kernel");
+        line(static_cast<long long>(p->n_longrows) * ((p->N + 4 * fin_lanes(p->N) - 1) / (4 * fin_lanes(p->N))), 256, 0.0,
+             "seg_finalize_kernel");
 }
 
 }  // namespace
@@ -690,6 +701,7 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
             skip_rows[r] = (!p->mfma.row_mfma.empty() && p->mfma.row_mfma[r]) || p->panels.row_panel[r];
         plan_rows(rowptr, M, N, static_cast<int32_t>(dtype_size(dtype)), skip_rows, default_slices(K, N, dtype),
                   &p->rows);
+        order_row_tasks(colidx, &p->rows);
         p->ntasks = static_cast<int32_t>(p->rows.tasks.size());
         const size_t n_seg_rows =
             p->rows.longrows.empty() ? 0 : static_cast<size_t>(p->rows.longrows.back().y + p->rows.longrows.back().z);
@@ -716,6 +728,8 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
         if (p->mfma_short && (st = setup_short(p, rowptr, colidx))) return bail(st);
         if ((st = dev_upload(&p->d_colidx, colidx, static_cast<size_t>(nnz)))) return bail(st);
         if ((st = dev_upload(&p->d_tasks, p->rows.tasks.data(), p->rows.tasks.size()))) return bail(st);
+        if ((st = dev_upload(&p->d_torder, p->rows.order.data(), p->rows.order.size()))) return bail(st);
+        p->n_torder = static_cast<int32_t>(p->rows.order.size());
         if ((st = dev_upload(&p->d_perm, p->rows.perm.data(), p->rows.perm.size()))) return bail(st);
         if ((st = dev_upload(&p->d_longrows, p->rows.longrows.data(), p->rows.longrows.size()))) return bail(st);
         if (!(flags & TCA_PLAN_NO_SCRATCH) && (st = dev_upload(&p->d_partials, nullptr, n_seg_total * N))) return bail(st);

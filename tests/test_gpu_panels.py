@@ -1,7 +1,7 @@
 """GPU parity of the panel kernel (row panels with B rows staged in LDS):
 bit-exact against the oracle on exact-arithmetic inputs for every lane
 geometry (fp32 E = 8/4/2, fp16 and bf16 E = 8/4, several column chunks),
-split panels (partial rows summed in unit order), panels beside MFMA windows
+split panels (partial rows summed in a fixed order), panels beside MFMA windows
 and the row kernel, determinism, and exactness of the masked steps with
 non-finite B rows."""
 import numpy as np
@@ -44,7 +44,7 @@ def test_panels_exact_all_geometries(torch_cuda, dtype, widths):
 @pytest.mark.parametrize("unit", ["1500", "40000"])
 @pytest.mark.parametrize("order", ["0", "1"])
 def test_panels_split_into_units(torch_cuda, monkeypatch, unit, order):
-    """Small units split panels by tiles; the partial rows are summed in unit order.  The
+    """Small units split panels by tiles; the partial rows are summed in a fixed order.  The
     launch order (natural, or XCD queues padded with idle workgroups) changes no result."""
     monkeypatch.setenv("TCA_PANEL_UNIT", unit)
     monkeypatch.setenv("TCA_PANEL_ORDER", order)

@@ -256,8 +256,11 @@ def test_compact_tiles_equal_dense_tiles(torch_cuda, lookahead, monkeypatch):
     assert np.array_equal(got, oracle_c(a, b))
 
 
-def test_exact_long_rows_many_segments(torch_cuda):
-    """Rows far above the segment length; every output element exact."""
+@pytest.mark.parametrize("order", ["0", "1"])
+def test_exact_long_rows_many_segments(torch_cuda, monkeypatch, order):
+    """Rows far above the segment length; every output element exact, with the
+    segments launched in task order or by column range per XCD."""
+    monkeypatch.setenv("TCA_ROW_ORDER", order)
     rng = np.random.default_rng(21)
     k = 16000
     lens = [15000, 9000, 12000, 0, 3, 16000 - 1]
@@ -269,6 +272,11 @@ def test_exact_long_rows_many_segments(torch_cuda):
             info = p.info()
             got = run_gpu(torch_cuda, a, b, plan=p)
         assert info["n_long_rows"] >= 4
+        slots = (info["n_row_tasks"] + 3) // 4 * info["col_chunks"]
+        if order == "1" and info["col_chunks"] == 1:  # segments reordered (idle slots pad the XCD queues)
+            assert info["row_blocks"] >= slots, info
+        else:
+            assert info["row_blocks"] == slots, info
         assert np.array_equal(got, oracle_c(a, b)), n
 
 
