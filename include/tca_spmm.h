@@ -250,6 +250,12 @@ int tca_spmm_plan_create_device(const int32_t* d_rowptr, const int32_t* d_colidx
 int tca_spmm_plan_export_rows(const tca_spmm_plan* plan, int32_t* n_tasks, int32_t* n_perm, int32_t* n_long,
                               int32_t* tasks, int32_t* perm, int32_t* longrows);
 
+/* The row kernel's launch order (wavefront slot -> task, -1 an idle slot;
+ * long rows' segments grouped by column range per XCD), copied to the host;
+ * with order == NULL only the count, 0 when the tasks run in task order.  No
+ * counterpart in the reference: for tests comparing host and GPU plans. */
+int tca_spmm_plan_export_order(const tca_spmm_plan* plan, int32_t* n_slots, int32_t* order);
+
 /* The dense-tile data of a plan whose tile kernel is TCA_TILES_DENSE or
  * TCA_TILES_DENSE_K, copied to the host: the windows ({first row, steps,
  * first global step, first nonzero} as 4 int32 each), per routed nonzero its

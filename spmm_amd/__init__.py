@@ -492,6 +492,14 @@ class Plan:
              np_ptr(tasks, ctypes.c_int32), np_ptr(perm, ctypes.c_int32), np_ptr(longrows, ctypes.c_int32))
         return tasks[:nt.value], perm[:npm.value], longrows[:nl.value]
 
+    def export_order(self):
+        """The row kernel's launch order (slot -> task, -1 idle); empty in task order."""
+        ns = ctypes.c_int32()
+        call("tca_spmm_plan_export_order", self._p, ctypes.byref(ns), None)
+        order = np.zeros(max(ns.value, 1), np.int32)
+        call("tca_spmm_plan_export_order", self._p, ctypes.byref(ns), np_ptr(order, ctypes.c_int32))
+        return order[:ns.value]
+
     def export_tiles(self):
         """The dense-tile data (windows [W, 4], entry positions, entry CSR
         indices, B row offsets of condensed columns) as numpy arrays."""

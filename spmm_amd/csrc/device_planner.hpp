@@ -141,6 +141,43 @@ __global__ void dp_emit_kernel(DpEmitArgs a) {
     }
 }
 
+// ---------------- launch order of the segments (order_row_tasks) ----------------
+
+// Key of segment task i: the column of its middle nonzero (the host's sort key).
+__global__ void dp_segkey_kernel(const int4* __restrict__ tasks, int first, int ns, const int* __restrict__ colidx,
+                                 uint32_t* __restrict__ key, int* __restrict__ idx) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < ns; i += gridDim.x * blockDim.x) {
+        const int4 t = tasks[first + i];
+        key[i] = static_cast<uint32_t>(colidx[t.y + (t.z - t.y) / 2]);
+        idx[i] = first + i;
+    }
+}
+
+// Slots outside the segment queues: wide tasks in place ([0, nw)), idle
+// slots where the queues' blocks go ([nw, 4 b_end)), then the row and multi
+// tasks in order, idle slots to a whole workgroup.
+__global__ void dp_order_fill_kernel(int* __restrict__ order, int n_slots, int nw, int ns, int rest, int b_end) {
+    for (int k = blockIdx.x * blockDim.x + threadIdx.x; k < n_slots; k += gridDim.x * blockDim.x) {
+        int v = -1;
+        if (k < nw) v = k;
+        else if (k >= 4 * b_end && k - 4 * b_end < rest) v = nw + ns + (k - 4 * b_end);
+        order[k] = v;
+    }
+}
+
+// Segment j of the column order: queue x holds [ns x / 8, ns (x + 1) / 8);
+// its k-th entry goes to slot k % 4 of the (k / 4)-th workgroup on XCD x
+// after the wide rows' workgroups (workgroup b runs on XCD b % 8).
+__global__ void dp_order_seg_kernel(const int* __restrict__ sorted_idx, int ns, int b0, int* __restrict__ order) {
+    for (int j = blockIdx.x * blockDim.x + threadIdx.x; j < ns; j += gridDim.x * blockDim.x) {
+        int x = kXcds - 1;
+        while (static_cast<int64_t>(ns) * x / kXcds > j) x--;
+        const int k = j - static_cast<int>(static_cast<int64_t>(ns) * x / kXcds);
+        const int b = b0 + ((x - b0) % kXcds + kXcds) % kXcds + kXcds * (k / 4);
+        order[4 * b + k % 4] = sorted_idx[j];
+    }
+}
+
 // ---------------- MFMA windows ----------------
 
 // Column-union bitmaps: bit c % 32 of bm[w * kw + c / 32] for every column c

@@ -593,11 +593,15 @@ void order_units(int32_t K, PanelPlan* p) {
         for (size_t k = 0; k < q[x].size(); k++) p->order[k * kXcds + x] = q[x][k];
 }
 
+bool row_order_on(const RowPlan& p) {
+    const char* e = std::getenv("TCA_ROW_ORDER");  // tuning override: 0 = task order
+    return p.col_chunks == 1 && p.n_seg >= kXcds * kRowOrderSlots && !(e && std::atoi(e) == 0);
+}
+
 void order_row_tasks(const int32_t* colidx, RowPlan* p) {
     p->order.clear();
-    const char* e = std::getenv("TCA_ROW_ORDER");  // tuning override: 0 = task order
-    constexpr int32_t W = 4;                       // wavefronts per row-kernel workgroup (kRowWaves)
-    if (p->col_chunks != 1 || p->n_seg < kXcds * W || (e && std::atoi(e) == 0)) return;
+    constexpr int32_t W = kRowOrderSlots;
+    if (!row_order_on(*p)) return;
     // Workgroup b runs on XCD b % 8.  A long row's segments are column
     // ranges of it (columns ascend within a row); sorted by the column of
     // their middle nonzero and cut into 8 runs of equal count, run x goes to

@@ -193,7 +193,11 @@ constexpr int64_t kPanelMinNnz = int64_t(1) << 21;  // fewer nonzeros in panels:
 // Launch order of the units (PanelPlan::order).
 void order_units(int32_t K, PanelPlan* p);
 // Launch order of the row kernel's tasks (RowPlan::order): segments of long
-// rows by column range, one range per XCD.
+// rows by column range, one range per XCD.  row_order_on: whether a plan
+// gets one (one column chunk, at least 32 segments; TCA_ROW_ORDER=0 turns it
+// off); the GPU planner builds the same order.
+constexpr int32_t kRowOrderSlots = 4;  // wavefronts per row-kernel workgroup (kRowWaves)
+bool row_order_on(const RowPlan& p);
 void order_row_tasks(const int32_t* colidx, RowPlan* p);
 // Lane geometry: 16 lanes cover one column chunk of a B row, E elements each
 // (E = 8, 4 or 2 with E * elem_size in 8..32 bytes); 0 when N does not fit.

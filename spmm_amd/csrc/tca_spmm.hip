@@ -964,11 +964,14 @@ int tca_spmm_plan_create_device(const int32_t* d_rowptr, const int32_t* d_colidx
             *evals_s = nullptr;
         uint8_t* start = nullptr;
         void* tmp = nullptr;
+        uint32_t *skey = nullptr, *skey_s = nullptr;  // segment launch order
+        int *sidx = nullptr, *sidx_s = nullptr;
         auto bail = [&](int st) {
             (void)hipStreamSynchronize(s);
             for (void* q : {(void*)keys, (void*)keys_s, (void*)rows, (void*)rows_s, (void*)cnt, (void*)nseg, (void*)segoff,
                             (void*)start, tmp, (void*)bm, (void*)ekeys, (void*)ekeys_s, (void*)wordpre, (void*)scnt,
-                            (void*)wstat, (void*)wmap, (void*)wgbase, (void*)evals, (void*)evals_s})
+                            (void*)wstat, (void*)wmap, (void*)wgbase, (void*)evals, (void*)evals_s, (void*)skey,
+                            (void*)skey_s, (void*)sidx, (void*)sidx_s})
                 (void)hipFree(q);
             return st;  // on failure `hold` frees the plan
         };
@@ -1270,6 +1273,38 @@ int tca_spmm_plan_create_device(const int32_t* d_rowptr, const int32_t* d_colidx
             ea.seg_total = seg_total;
             hipLaunchKernelGGL(dp_emit_kernel, grid_for(Mp), blk, 0, s, ea);
         }
+        if (row_order_on(p->rows)) {
+            // the host planner's segment launch order (order_row_tasks):
+            // segments stably sorted by the column of their middle nonzero,
+            // cut into kXcds queues of equal count, queue x on XCD x
+            const int nw = p->rows.n_wide, ns = seg_total, rest = p->ntasks - nw - ns;
+            const int b0 = nw / kRowOrderSlots;
+            int b_end = b0;
+            for (int x = 0; x < kXcds; x++) {
+                const int len = static_cast<int>(static_cast<int64_t>(ns) * (x + 1) / kXcds - static_cast<int64_t>(ns) * x / kXcds);
+                if (len > 0)
+                    b_end = std::max(b_end, b0 + ((x - b0) % kXcds + kXcds) % kXcds +
+                                                kXcds * ((len + kRowOrderSlots - 1) / kRowOrderSlots - 1) + 1);
+            }
+            const int n_slots = (kRowOrderSlots * b_end + rest + kRowOrderSlots - 1) / kRowOrderSlots * kRowOrderSlots;
+            if ((st = dev_upload(&skey, nullptr, ns)) || (st = dev_upload(&skey_s, nullptr, ns)) ||
+                (st = dev_upload(&sidx, nullptr, ns)) || (st = dev_upload(&sidx_s, nullptr, ns)) ||
+                (st = dev_upload(&p->d_torder, nullptr, n_slots)))
+                return bail(st);
+            hipLaunchKernelGGL(dp_segkey_kernel, grid_for(ns), blk, 0, s, p->d_tasks, nw, ns, p->d_colidx, skey, sidx);
+            (void)hipFree(tmp);
+            tmp = nullptr;
+            size_t tmp_bytes = 0;
+            if (rocprim::radix_sort_pairs(nullptr, tmp_bytes, skey, skey_s, sidx, sidx_s, static_cast<size_t>(ns), 0, 32, s) !=
+                    hipSuccess ||
+                dev_malloc(reinterpret_cast<void**>(&tmp), std::max<size_t>(tmp_bytes, 4)) != hipSuccess ||
+                rocprim::radix_sort_pairs(tmp, tmp_bytes, skey, skey_s, sidx, sidx_s, static_cast<size_t>(ns), 0, 32, s) !=
+                    hipSuccess)
+                return bail(fail(TCA_ERR_HIP, "segment order sort failed"));
+            hipLaunchKernelGGL(dp_order_fill_kernel, grid_for(n_slots), blk, 0, s, p->d_torder, n_slots, nw, ns, rest, b_end);
+            hipLaunchKernelGGL(dp_order_seg_kernel, grid_for(ns), blk, 0, s, sidx_s, ns, b0, p->d_torder);
+            p->n_torder = n_slots;
+        }
         if (hipGetLastError() != hipSuccess || hipStreamSynchronize(s) != hipSuccess)
             return bail(fail(TCA_ERR_HIP, "task emission failed"));
         st = bail(TCA_OK);  // frees the temporaries only
@@ -1295,6 +1330,17 @@ int tca_spmm_plan_export_rows(const tca_spmm_plan* p, int32_t* n_tasks, int32_t*
     *n_tasks = p->ntasks;
     *n_perm = p->n_perm;
     *n_long = p->n_longrows;
+    return TCA_OK;
+}
+
+int tca_spmm_plan_export_order(const tca_spmm_plan* p, int32_t* n_slots, int32_t* order) {
+    if (!p || !n_slots) return fail(TCA_ERR_INVALID, "tca_spmm_plan_export_order: bad argument");
+    if (order) {
+        if (*n_slots < p->n_torder) return fail(TCA_ERR_INVALID, "tca_spmm_plan_export_order: output buffer too small");
+        if (p->n_torder && hipMemcpy(order, p->d_torder, sizeof(int) * p->n_torder, hipMemcpyDeviceToHost) != hipSuccess)
+            return fail(TCA_ERR_HIP, "tca_spmm_plan_export_order: copy failed");
+    }
+    *n_slots = p->n_torder;
     return TCA_OK;
 }
 

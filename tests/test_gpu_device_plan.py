@@ -37,8 +37,15 @@ def test_device_plan_equals_host_plan(torch_cuda, name, a, n):
             ht, hperm, hl = hp.export_rows()
             dt, dperm, dl = dp.export_rows()
             assert np.array_equal(ht, dt) and np.array_equal(hperm, dperm) and np.array_equal(hl, dl), name
+            ho, do = hp.export_order(), dp.export_order()
+            assert np.array_equal(ho, do), name  # the same launch order (segments by column range per XCD)
+            if len(ho):
+                assert sorted(ho[ho >= 0].tolist()) == list(range(len(ht))), name  # every task once
+            if name == "zipf":
+                assert len(ho) > 0, name  # long rows in segments, one column chunk: ordered
             hi, di = hp.info(), dp.info()
-            for key in ("n_row_tasks", "n_multi_tasks", "n_seg_tasks", "n_long_rows", "n_wide_tasks", "scratch_bytes"):
+            for key in ("n_row_tasks", "n_multi_tasks", "n_seg_tasks", "n_long_rows", "n_wide_tasks", "scratch_bytes",
+                        "row_blocks"):  # row_blocks: the same launch order length (segments by column range)
                 assert hi[key] == di[key], (name, key)
             rng = np.random.default_rng(7)
             b = S.to_storage(exact_dense(rng, (a.ncol, n)), a.dtype)
