@@ -337,6 +337,19 @@ int tca_plan_panels(const int32_t* rowptr, const int32_t* colidx, int32_t M, int
                     uint8_t* width, uint8_t* cnt, uint8_t* pos, int32_t* units, int32_t* panel_units,
                     int32_t* ustart, int32_t* longrows);
 
+/* ---- host-only view of the launch orders (no device needed) ----
+ * Workgroup b of a launch runs on XCD b % 8.  For this structure, width N,
+ * dtype and flags (MFMA routing as tca_plan_panels; the short-K kernel is
+ * not considered): the panel kernel's workgroup -> unit order (-1 an idle
+ * workgroup; units as tca_plan_panels returns them), and the row kernel's
+ * task list (int4 tasks as 4 int32, for the rows outside MFMA windows and
+ * panels) with its wavefront slot -> task order (-1 an idle slot; empty
+ * when the tasks run in task order).  Call with panel_order == NULL for
+ * the counts.  No counterpart in the reference: for tests of the planner. */
+int tca_plan_launch_orders(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_t K, int32_t N,
+                           int32_t dtype, uint32_t flags, int32_t* n_blocks, int32_t* panel_order, int32_t* n_tasks,
+                           int32_t* tasks, int32_t* n_slots, int32_t* row_order);
+
 /* Launches a trivial kernel on the current device and synchronises
  * (reference warm_up_gpu_kernel, src/miscalleneous.cu:158-164, launched
  * <<<1,32>>> ten times by src/test.cu:50-52). */

@@ -400,6 +400,22 @@ def plan_panels(a: CSR, n: int, flags: int = TCA_PLAN_DEFAULT, dtype: int = None
     return out
 
 
+def plan_launch_orders(a: CSR, n: int, flags: int = TCA_PLAN_DEFAULT) -> dict:
+    """Host view of the launch orders (tca_plan_launch_orders): panel workgroup ->
+    unit, the row tasks [T, 4] and wavefront slot -> task (-1 idle)."""
+    rp = np.ascontiguousarray(a.rowptr, np.int32)
+    ci = np.ascontiguousarray(a.colidx, np.int32)
+    nb, nt, ns = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
+    args = (np_ptr(rp, ctypes.c_int32), np_ptr(ci, ctypes.c_int32), a.nrow, a.ncol, n, a.dtype, flags)
+    call("tca_plan_launch_orders", *args, ctypes.byref(nb), None, ctypes.byref(nt), None, ctypes.byref(ns), None)
+    po = np.zeros(max(nb.value, 1), np.int32)
+    tasks = np.zeros((max(nt.value, 1), 4), np.int32)
+    ro = np.zeros(max(ns.value, 1), np.int32)
+    call("tca_plan_launch_orders", *args, ctypes.byref(nb), np_ptr(po, ctypes.c_int32), ctypes.byref(nt),
+         np_ptr(tasks, ctypes.c_int32), ctypes.byref(ns), np_ptr(ro, ctypes.c_int32))
+    return dict(panel_order=po[:nb.value], tasks=tasks[:nt.value], row_order=ro[:ns.value])
+
+
 # ----------------------------------------------------------- generators
 def gen_dense(rows: int, cols: int, dist: int = 0, seed: int = 1, dtype: int = TCA_F16,
               sparsity: float = 0.0) -> np.ndarray:

@@ -98,6 +98,7 @@ SIGNATURES = {
     "tca_spmm_plan_create_device": (i32, [vp, vp, i32, i32, i32, i32, i32, u32, vp, ctypes.POINTER(vp)]),
     "tca_spmm_plan_export_rows": (i32, [vp, i32p, i32p, i32p, i32p, i32p, i32p]),
     "tca_spmm_plan_export_order": (i32, [vp, i32p, i32p]),
+    "tca_plan_launch_orders": (i32, [i32p, i32p, i32, i32, i32, i32, u32, i32p, i32p, i32p, i32p, i32p, i32p]),
     "tca_spmm_plan_export_tiles": (i32, [vp, i32p, i32p, i32p, i32p, u32p, i32p, u32p]),
     "tca_spmm_plan_info": (i32, [vp, ctypes.POINTER(TcaPlanInfo)]),
     "tca_spmm_plan_destroy": (i32, [vp]),

@@ -716,6 +716,44 @@ extern "C" int tca_plan_mfma_windows(const int32_t* rowptr, const int32_t* colid
     });
 }
 
+extern "C" int tca_plan_launch_orders(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_t K, int32_t N,
+                                      int32_t dtype, uint32_t flags, int32_t* n_blocks, int32_t* panel_order,
+                                      int32_t* n_tasks, int32_t* tasks, int32_t* n_slots, int32_t* row_order) {
+    return tca::api_guard("tca_plan_launch_orders", [&]() -> int {
+        using namespace tca;
+        if (!rowptr || !colidx || M < 0 || K < 1 || N < 1 || !dtype_ok(dtype) || !n_blocks || !n_tasks || !n_slots)
+            return fail(TCA_ERR_INVALID, "tca_plan_launch_orders: bad argument");
+        MfmaPlan mp;
+        const char* md = std::getenv("TCA_MFMA_MIN_DENSITY");
+        plan_mfma(rowptr, colidx, M, N, dtype, (flags & TCA_PLAN_FORCE_MFMA) != 0, (flags & TCA_PLAN_NO_MFMA) != 0,
+                  md ? std::atof(md) : kMfmaMinDensity, mfma_shape(flags), &mp);
+        PanelPlan pp;
+        plan_panels_routed(rowptr, colidx, M, K, N, dtype, flags, mp.row_mfma, &pp);
+        std::vector<uint8_t> skip(M, 0);
+        for (int32_t r = 0; r < M; r++) skip[r] = (!mp.row_mfma.empty() && mp.row_mfma[r]) || pp.row_panel[r];
+        RowPlan rp;
+        plan_rows(rowptr, M, N, static_cast<int32_t>(dtype_size(dtype)), skip, default_slices(K, N, dtype), &rp);
+        order_row_tasks(colidx, &rp);
+        if (panel_order) {
+            if (*n_blocks < static_cast<int32_t>(pp.order.size()) || *n_tasks < static_cast<int32_t>(rp.tasks.size()) ||
+                *n_slots < static_cast<int32_t>(rp.order.size()) || !tasks || !row_order)
+                return fail(TCA_ERR_INVALID, "tca_plan_launch_orders: output buffers too small");
+            std::copy(pp.order.begin(), pp.order.end(), panel_order);
+            for (size_t t = 0; t < rp.tasks.size(); t++) {
+                tasks[4 * t] = rp.tasks[t].x;
+                tasks[4 * t + 1] = rp.tasks[t].y;
+                tasks[4 * t + 2] = rp.tasks[t].z;
+                tasks[4 * t + 3] = rp.tasks[t].w;
+            }
+            std::copy(rp.order.begin(), rp.order.end(), row_order);
+        }
+        *n_blocks = static_cast<int32_t>(pp.order.size());
+        *n_tasks = static_cast<int32_t>(rp.tasks.size());
+        *n_slots = static_cast<int32_t>(rp.order.size());
+        return TCA_OK;
+    });
+}
+
 extern "C" int tca_plan_panels(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_t K, int32_t N,
                                int32_t dtype, uint32_t flags, int64_t* sizes, int32_t* rows, int32_t* cols,
                                uint8_t* width, uint8_t* cnt, uint8_t* pos, int32_t* units, int32_t* panel_units,
