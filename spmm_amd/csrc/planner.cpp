@@ -420,12 +420,14 @@ void plan_panels(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_
         p->pos.clear();
         return;
     }
-    // Units of ~1/256 of the panels' nonzeros: about one per CU, so each CU
+    // Units of ~1/320 of the panels' nonzeros: about one per CU, so each CU
     // works through one contiguous column range of a panel and the partial
     // rows stay few (measured on MI355X, per SpMM, config 2 / config 3:
     // tot / 2048 1.87 / 3.34 ms, / 1024 1.69 / 3.23, / 512 1.65 / 3.24,
-    // / 256 1.63 / 3.07, / 128 - / 3.67, one box).
-    if (unit_nnz <= 0) unit_nnz = std::max<int64_t>(8192, tot / 256);
+    // / 256 1.63 / 3.07, / 128 - / 3.67, one box; then on another, config 3:
+    // / 256 3.15, / 320 3.03-3.04, / 192 3.08-3.13, config 2 level within
+    // the box's 5 % noise).
+    if (unit_nnz <= 0) unit_nnz = std::max<int64_t>(8192, tot / 320);
     std::vector<int32_t> panel_of(n_cand, -1), tile0(n_cand, 0);
     int32_t n_tiles = 0;
     for (int32_t q = 0; q < n_cand; q++) {
