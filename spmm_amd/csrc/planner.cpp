@@ -552,7 +552,7 @@ void order_units(int32_t K, PanelPlan* p) {
     // The hardware deals workgroups to the XCDs round robin (workgroup b on
     // XCD b % 8), each XCD with its own L2.  A unit stages the B rows of one
     // range of its panel's sorted column union.  Units whose columns span at
-    // most K / 8 are sorted by the middle of that span and cut into 8 runs of
+    // most K / 4 are sorted by the middle of that span and cut into 8 runs of
     // equal tiles; run x goes to XCD x in column order, so the units resident
     // together on one XCD stage nearby B rows and meet them in its L2.  Wider
     // units follow, each on the XCD with the fewest tiles so far; shorter
@@ -565,7 +565,7 @@ void order_units(int32_t K, PanelPlan* p) {
         const Int4& t = p->units[u];
         const int64_t lo = p->cols[static_cast<size_t>(t.y) * P];
         const int64_t hi = p->cols[static_cast<size_t>(t.y + t.z) * P - 1];  // padding repeats the last column
-        if ((hi - lo) * kXcds <= K) {
+        if ((hi - lo) * (kXcds / 2) <= K) {
             local.push_back({lo + hi, u});
             local_tiles += t.z;
         } else {

@@ -73,14 +73,14 @@ def test_panel_order_units_once_xcd_queues(monkeypatch):
         q = order[x::XCDS]
         idle = np.nonzero(q < 0)[0]
         assert len(idle) == 0 or np.all(q[idle[0]:] < 0), x
-    # local units (column span <= K / 8) reach each XCD in column order, queue x below queue x + 1
+    # local units (column span <= K / 4) reach each XCD in column order, queue x below queue x + 1
     P, K = pp["P"], a.ncol
     def span(u):
         t0, nt = pp["units"][u, 1], pp["units"][u, 2]
         return int(pp["cols"][t0 * P]), int(pp["cols"][(t0 + nt) * P - 1])
     mids = []
     for x in range(XCDS):
-        loc = [span(u) for u in order[x::XCDS] if u >= 0 and (span(u)[1] - span(u)[0]) * XCDS <= K]
+        loc = [span(u) for u in order[x::XCDS] if u >= 0 and (span(u)[1] - span(u)[0]) * (XCDS // 2) <= K]
         m = [lo_ + hi for lo_, hi in loc]
         assert m == sorted(m), x
         mids.append(m)
