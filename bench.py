@@ -108,9 +108,9 @@ def main():
     ap.add_argument("--no-others", action="store_true",
                     help="skip the other four configurations (reported under config.other_configs)")
     ap.add_argument("--flags", type=int, default=0,
-                    help="plan flags (1 = no MFMA, 2 = force MFMA, 4 = register-staged tile kernel, "
-                         "8 = LDS-DMA tile kernel, 16 = dense-tile kernel, 32 = 2:4 sparse-core tiles, "
-                         "64 = paired tile kernel)")
+                    help="plan flags, TCA_PLAN_KNOWN_FLAGS of include/tca_spmm.h (1 = no MFMA, 2 = force MFMA, "
+                         "16 = dense-tile kernel, 64 = paired tile kernel, 128 = compacted dense tiles, "
+                         "256 = no panels, 512 = force panels, 1024 = no scratch, 2048 = short-K kernel)")
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
                     help="before timing, run one device-to-device copy of MIB MiB (a known-size kernel to "
                          "scale rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
@@ -209,20 +209,24 @@ def measure(cfg: int, args, sha: str, headline: bool) -> dict:
         del src, dst
     torch.cuda.synchronize()
 
-    # Timed region: W warm-up steps, then K steps between hipEvents recorded on
-    # the launch stream (tca_spmm_time); wall clock around it as a cross-check.
+    # Timed region: W warm-up steps, then K steps back to back on the launch
+    # stream, between hipEvents before the first and after the last
+    # (tca_spmm_time_phases, the reference's protocol, src/our_spmm.cu:553-576);
+    # each kernel of those same steps carries its own start / stop timestamps,
+    # so the per-kernel durations of the roofline lie inside the step time.
+    # Wall clock around it as a cross-check.
     wall0 = time.perf_counter()
-    ms_per_step = plan.time(val, bd, c, stream=stream.cuda_stream, warmup=args.warmup, iters=args.steps)
+    ms_per_step, phases = plan.time_run_phases(val, bd, c, stream=stream.cuda_stream, warmup=args.warmup,
+                                               iters=args.steps)
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - wall0) * 1e3
     if not torch.isfinite(c).all().item():
         sys.exit(f"config {cfg}: non-finite output")
-    # Per-kernel durations (hipEvents between the kernels on the launch stream)
-    # for the roofline of the dominant kernel.
-    phases = plan.time_phases(val, bd, c, stream=stream.cuda_stream, warmup=1, iters=args.steps)
+    # Cross-check: K more steps with plain launches (tca_spmm_time).
+    ms_plain = plan.time(val, bd, c, stream=stream.cuda_stream, warmup=1, iters=args.steps)
     torch.cuda.synchronize()
+    log("phases (ms):", json.dumps(phases), "run", ms_per_step, "plain", ms_plain)
     dominant = max(phases, key=phases.get)
-    log("phases (ms):", json.dumps(phases))
 
     s_a = 4 if a.dtype == S.TCA_F32 else 2
     m, k, nnz = a.nrow, a.ncol, a.nnz
@@ -257,7 +261,8 @@ def measure(cfg: int, args, sha: str, headline: bool) -> dict:
     if not headline:
         plan.close()
         return {"workload": WORKLOADS[cfg], "M": m, "K": k, "N": n, "nnz": nnz, "dtype": dtype,
-                "ms_per_step": round(ms_per_step, 6), "gflops": round(gflops, 3), "bytes_alg": bytes_alg,
+                "ms_per_step": round(ms_per_step, 6), "ms_per_step_plain": round(ms_plain, 6),
+                "gflops": round(gflops, 3), "bytes_alg": bytes_alg,
                 "hbm_gbs_whole_step": round(hbm_gbs, 2),
                 "phases_us": {kk: round(v * 1e3, 3) for kk, v in phases.items()},
                 "tile_kernel": TILE_KERNELS.get(info["tile_kernel"], "none"), "roofline": roofline}
@@ -330,6 +335,7 @@ def measure(cfg: int, args, sha: str, headline: bool) -> dict:
         "data": "synthetic (seeded generators, seed %d)" % args.seed,
         "config": {"workload": WORKLOADS[cfg], "config_index": cfg, "M": m, "K": k, "N": n, "nnz": nnz,
                    "bytes_alg": bytes_alg, "hbm_gbs_whole_step": round(hbm_gbs, 2),
+                   "ms_per_step_plain": round(ms_plain, 6),
                    "plan_ms": round(info["plan_ms"], 3),
                    **({"plan_on_gpu": True, "plan_first_ms": round(plan_first_ms, 3)} if plan_first_ms is not None
                       else {}),

@@ -42,7 +42,8 @@ class Arguments {
     float tolerance = 1e-3f;
     int dtype = TCA_F16;  // A and B; C is fp32
     std::string input_fname;
-    int ell_block_size = 32;  // accepted for compatibility; Blocked-ELL is not built
+    int ell_block_size = 32;  // -e: Blocked-ELL block size (printed; the harness runs the CSR SpMM,
+                              // the Blocked-ELL kernel is tca_bell_spmm / bench.py --bell)
     unsigned long long seed = 1;
     bool json = false;
     bool n_given = false;

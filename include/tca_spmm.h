@@ -173,16 +173,25 @@ int tca_spmm_time(const tca_spmm_plan* plan, const void* d_val, const void* d_B,
  * panel phase has index 4 so the older indices stay as they were). */
 #define TCA_PHASES 5
 enum { TCA_PHASE_PACK = 0, TCA_PHASE_TILES = 1, TCA_PHASE_ROWS = 2, TCA_PHASE_SEGMENTS = 3, TCA_PHASE_PANELS = 4 };
+/* Slot after the phases in tca_spmm_time_phases' output: the whole run. */
+#define TCA_PHASE_RUN TCA_PHASES
 
-/* Per-phase timing: `warmup` + 1 full runs, then each phase the plan uses is
- * launched alone `iters` times back to back between two hipEvents on
- * `stream` (every phase is idempotent once a full run has produced its
- * inputs): phase_ms[k] = mean milliseconds of one launch of phase k, 0 for a
- * phase the plan does not use.  No counterpart in the reference, which times
- * whole runs only (src/our_spmm.cu:553-576); this is the per-kernel figure a
- * roofline needs. */
+/* Per-phase timing inside whole runs: `warmup` runs, then `iters` runs back
+ * to back on `stream`; each phase's kernel is dispatched with a start and a
+ * stop hipEvent of its own (hipExtLaunchKernelGGL: the kernel's span, as a
+ * kernel trace reports it, with nothing inserted between the kernels).
+ * phase_ms[k] = mean milliseconds of phase k's kernel over the runs, 0 for a
+ * phase the plan does not use.  phase_ms holds n_phase_ms floats: the first
+ * min(n_phase_ms, TCA_PHASES) entries are written (TCA_PHASES grew from 4 to
+ * 5 when the panel phase was added; the length argument keeps an older,
+ * shorter buffer in bounds), and when n_phase_ms > TCA_PHASE_RUN also
+ * phase_ms[TCA_PHASE_RUN] = mean milliseconds of one whole run of the same
+ * runs (hipEvents before the first and after the last, as tca_spmm_time), so
+ * every phase of the output lies within its run time.  iters <= 100000.  No counterpart in the
+ * reference, which times whole runs only (src/our_spmm.cu:553-576); this is
+ * the per-kernel figure a roofline needs. */
 int tca_spmm_time_phases(const tca_spmm_plan* plan, const void* d_val, const void* d_B, float* d_C, void* stream,
-                         int32_t warmup, int32_t iters, float* phase_ms);
+                         int32_t warmup, int32_t iters, float* phase_ms, int32_t n_phase_ms);
 
 /* Backward-pass kernels of the PyTorch op (no counterpart in the reference,
  * which has no backward pass).

@@ -554,14 +554,24 @@ class Plan:
     PHASES = ("pack", "tiles", "rows", "segments", "panels")
 
     def time_phases(self, val, b, c, stream=None, warmup: int = 5, iters: int = 10) -> dict:
-        """Mean milliseconds of one launch of each phase (MFMA value pack, MFMA
-        tiles, row kernel, segment sums of split rows, panel kernel): each
-        phase launched alone `iters` times back to back between hipEvents on
-        the run's stream."""
-        ms = (ctypes.c_float * len(self.PHASES))()
+        """Mean milliseconds of each phase (MFMA value pack, MFMA tiles, row
+        kernel, segment sums of split rows, panel kernel) inside whole runs:
+        `iters` runs back to back on the stream, hipEvents recorded between
+        their kernels."""
+        ms = (ctypes.c_float * (len(self.PHASES) + 1))()
         call("tca_spmm_time_phases", self._p, _addr(val), _addr(b), _addr(c),
-             _addr(stream) if stream is not None else None, warmup, iters, ms)
+             _addr(stream) if stream is not None else None, warmup, iters, ms, len(self.PHASES))
         return {k: float(ms[i]) for i, k in enumerate(self.PHASES)}
+
+    def time_run_phases(self, val, b, c, stream=None, warmup: int = 5, iters: int = 10):
+        """(mean milliseconds of a whole run, per-phase dict) from the same
+        `iters` runs: the run time between hipEvents before the first run and
+        after the last, each phase's kernel timed by its own dispatch."""
+        n = len(self.PHASES) + 1
+        ms = (ctypes.c_float * n)()
+        call("tca_spmm_time_phases", self._p, _addr(val), _addr(b), _addr(c),
+             _addr(stream) if stream is not None else None, warmup, iters, ms, n)
+        return float(ms[n - 1]), {k: float(ms[i]) for i, k in enumerate(self.PHASES)}
 
     def close(self) -> None:
         if self._p:

@@ -383,9 +383,11 @@ int tca_smtx_read_dense(const char* path, int32_t dtype, void** dense, int32_t* 
 int tca_smtx_write(const char* path, const tca_csr* a) {
     return api_guard("tca_smtx_write", [&]() -> int {
         if (!path || !a) return fail(TCA_ERR_INVALID, "tca_smtx_write: bad argument");
+        // The stream buffer is allocated before the file is opened: if the
+        // allocation throws (api_guard -> TCA_ERR_ALLOC), no FILE is left open.
+        std::vector<char> buf(1 << 22);
         FILE* f = std::fopen(path, "wb");
         if (!f) return fail(TCA_ERR_IO, "cannot create '%s'", path);
-        std::vector<char> buf(1 << 22);
         std::setvbuf(f, buf.data(), _IOFBF, buf.size());
         std::fprintf(f, "%d, %d, %d\n", a->nRow, a->nCol, a->nnz);
         char tmp[16];

@@ -69,7 +69,7 @@ struct ShortArgs {
     float* C;               // [M][N]
     const void* zeros;      // 16 zero bytes
     int M, K, N;
-    int nwin;               // ceil(M / 32)
+    int nwin;               // windows of 64 rows: ceil(M / 64)
     int col_blocks;         // ceil(N / 64)
     int steps;              // ceil(K / 32)
     int wstart_arg[kShArgWindows + 1];  // window starts, when nwin <= kShArgWindows

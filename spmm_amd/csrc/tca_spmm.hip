@@ -1,5 +1,6 @@
 // tca_spmm.hip -- plan / run / time entry points of libtcaspmm.so and the
 // host-pointer driver with the reference our_spmm_balanced contract.
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -213,6 +214,20 @@ int row_blocks(const tca_spmm_plan* p) {
     return ((slots + kRowWaves - 1) / kRowWaves) * p->rows.col_chunks;
 }
 
+// Kernel launch of one phase of a run.  While tca_spmm_time_phases has a
+// phase armed (g_phase_ev[0] set on this thread), the dispatch itself
+// carries that phase's start and stop timestamps (hipExtLaunchKernelGGL:
+// the same span a kernel trace reports, with no event packets between the
+// kernels); otherwise it is a plain launch.  Every phase launches one kernel.
+thread_local hipEvent_t g_phase_ev[2] = {nullptr, nullptr};
+#define TCA_PHASE_LAUNCH(kernel, grid, block, shm, stream, ...)                                                 \
+    do {                                                                                                        \
+        if (g_phase_ev[0])                                                                                      \
+            hipExtLaunchKernelGGL(kernel, grid, block, shm, stream, g_phase_ev[0], g_phase_ev[1], 0, __VA_ARGS__); \
+        else                                                                                                    \
+            hipLaunchKernelGGL(kernel, grid, block, shm, stream, __VA_ARGS__);                                  \
+    } while (0)
+
 template <typename T, int E>
 void launch_rows_t(const tca_spmm_plan* p, const void* val, const void* B, float* C, float* W, hipStream_t s) {
     RowArgs a;
@@ -234,14 +249,14 @@ void launch_rows_t(const tca_spmm_plan* p, const void* val, const void* B, float
     a.colidx_bytes = static_cast<uint32_t>(static_cast<uint64_t>(p->nnz) * 4);
     a.val_bytes = static_cast<uint32_t>(static_cast<uint64_t>(p->nnz) * sizeof(T));
     a.B_bytes = static_cast<uint32_t>(static_cast<uint64_t>(p->K) * p->N * sizeof(T));
-    hipLaunchKernelGGL((row_kernel<T, E>), dim3(row_blocks(p)), dim3(64 * kRowWaves), 0, s, a);
+    TCA_PHASE_LAUNCH((row_kernel<T, E>), dim3(row_blocks(p)), dim3(64 * kRowWaves), 0, s, a);
 }
 
 // Adds the segments of long rows (after the row kernel, same stream).
 void launch_finalize(const tca_spmm_plan* p, float* C, const float* W, hipStream_t s) {
     if (p->n_longrows == 0) return;
     const dim3 fgrid(static_cast<unsigned>(p->n_longrows), (p->N + 4 * fin_lanes(p->N) - 1) / (4 * fin_lanes(p->N)));
-    hipLaunchKernelGGL(seg_finalize_kernel, fgrid, dim3(256), 0, s, p->d_longrows, W, C, p->N);
+    TCA_PHASE_LAUNCH(seg_finalize_kernel, fgrid, dim3(256), 0, s, p->d_longrows, W, C, p->N);
 }
 
 template <typename T>
@@ -264,13 +279,13 @@ int launch_rows_e(const tca_spmm_plan* p, const void* val, const void* B, float*
 void launch_pack(const tca_spmm_plan* p, const void* val, hipStream_t s) {
     if (p->mfma_dense) {
         if (p->n_dn > 0)
-            hipLaunchKernelGGL(dense_pack_kernel, dim3((p->n_dn + 255) / 256), dim3(256), 0, s, p->d_dn_src,
+            TCA_PHASE_LAUNCH(dense_pack_kernel, dim3((p->n_dn + 255) / 256), dim3(256), 0, s, p->d_dn_src,
                                p->d_dn_pos, p->n_dn, static_cast<const uint16_t*>(val), p->d_adense);
         return;
     }
     const int n = p->n_pk_words;
     if (p->mfma.windows.empty() || n == 0) return;
-    hipLaunchKernelGGL(mfma_pack_kernel, dim3((n + 1023) / 1024), dim3(256), 0, s, p->d_pk_src, p->d_pk_cell, n,
+    TCA_PHASE_LAUNCH(mfma_pack_kernel, dim3((n + 1023) / 1024), dim3(256), 0, s, p->d_pk_src, p->d_pk_cell, n,
                        static_cast<const uint16_t*>(val), p->d_packed);
 }
 
@@ -302,8 +317,8 @@ int launch_short(const tca_spmm_plan* p, const void* val, const void* B, float* 
     if (a.nwin <= kShArgWindows)
         for (int w = 0; w <= a.nwin; w++) a.wstart_arg[w] = p->short_wstart[w];
     const dim3 grid(mfma_short_grid(a.nwin, a.col_blocks));
-    if (p->dtype == TCA_BF16) hipLaunchKernelGGL(mfma_short_kernel<true>, grid, dim3(kShThreads), 0, s, a);
-    else hipLaunchKernelGGL(mfma_short_kernel<false>, grid, dim3(kShThreads), 0, s, a);
+    if (p->dtype == TCA_BF16) TCA_PHASE_LAUNCH(mfma_short_kernel<true>, grid, dim3(kShThreads), 0, s, a);
+    else TCA_PHASE_LAUNCH(mfma_short_kernel<false>, grid, dim3(kShThreads), 0, s, a);
     return TCA_OK;
 }
 
@@ -338,35 +353,35 @@ int launch_mfma(const tca_spmm_plan* p, const void* val, const void* B, float* C
         if (p->mfma_compact) {
             const int v = (bf ? 1 : 0) | (p->mfma_natural ? 2 : 0) | (p->mfma_compact_lb == 3 ? 4 : 0);
             switch (v) {
-                case 0: hipLaunchKernelGGL((mfma_compact_kernel<false, false, 4>), dgrid, dim3(kDnThreads), 0, s, a); break;
-                case 1: hipLaunchKernelGGL((mfma_compact_kernel<true, false, 4>), dgrid, dim3(kDnThreads), 0, s, a); break;
-                case 2: hipLaunchKernelGGL((mfma_compact_kernel<false, true, 4>), dgrid, dim3(kDnThreads), 0, s, a); break;
-                case 3: hipLaunchKernelGGL((mfma_compact_kernel<true, true, 4>), dgrid, dim3(kDnThreads), 0, s, a); break;
-                case 4: hipLaunchKernelGGL((mfma_compact_kernel<false, false, 3>), dgrid, dim3(kDnThreads), 0, s, a); break;
-                case 5: hipLaunchKernelGGL((mfma_compact_kernel<true, false, 3>), dgrid, dim3(kDnThreads), 0, s, a); break;
-                case 6: hipLaunchKernelGGL((mfma_compact_kernel<false, true, 3>), dgrid, dim3(kDnThreads), 0, s, a); break;
-                default: hipLaunchKernelGGL((mfma_compact_kernel<true, true, 3>), dgrid, dim3(kDnThreads), 0, s, a); break;
+                case 0: TCA_PHASE_LAUNCH((mfma_compact_kernel<false, false, 4>), dgrid, dim3(kDnThreads), 0, s, a); break;
+                case 1: TCA_PHASE_LAUNCH((mfma_compact_kernel<true, false, 4>), dgrid, dim3(kDnThreads), 0, s, a); break;
+                case 2: TCA_PHASE_LAUNCH((mfma_compact_kernel<false, true, 4>), dgrid, dim3(kDnThreads), 0, s, a); break;
+                case 3: TCA_PHASE_LAUNCH((mfma_compact_kernel<true, true, 4>), dgrid, dim3(kDnThreads), 0, s, a); break;
+                case 4: TCA_PHASE_LAUNCH((mfma_compact_kernel<false, false, 3>), dgrid, dim3(kDnThreads), 0, s, a); break;
+                case 5: TCA_PHASE_LAUNCH((mfma_compact_kernel<true, false, 3>), dgrid, dim3(kDnThreads), 0, s, a); break;
+                case 6: TCA_PHASE_LAUNCH((mfma_compact_kernel<false, true, 3>), dgrid, dim3(kDnThreads), 0, s, a); break;
+                default: TCA_PHASE_LAUNCH((mfma_compact_kernel<true, true, 3>), dgrid, dim3(kDnThreads), 0, s, a); break;
             }
             return TCA_OK;
         }
         if (p->mfma_natural) {
-            if (bf) hipLaunchKernelGGL((mfma_dense_kernel<true, true>), dgrid, dim3(kDnThreads), 0, s, a);
-            else hipLaunchKernelGGL((mfma_dense_kernel<false, true>), dgrid, dim3(kDnThreads), 0, s, a);
+            if (bf) TCA_PHASE_LAUNCH((mfma_dense_kernel<true, true>), dgrid, dim3(kDnThreads), 0, s, a);
+            else TCA_PHASE_LAUNCH((mfma_dense_kernel<false, true>), dgrid, dim3(kDnThreads), 0, s, a);
         } else {
-            if (bf) hipLaunchKernelGGL((mfma_dense_kernel<true, false>), dgrid, dim3(kDnThreads), 0, s, a);
-            else hipLaunchKernelGGL((mfma_dense_kernel<false, false>), dgrid, dim3(kDnThreads), 0, s, a);
+            if (bf) TCA_PHASE_LAUNCH((mfma_dense_kernel<true, false>), dgrid, dim3(kDnThreads), 0, s, a);
+            else TCA_PHASE_LAUNCH((mfma_dense_kernel<false, false>), dgrid, dim3(kDnThreads), 0, s, a);
         }
         return TCA_OK;
     }
     if (p->mfma_pair) {
         switch (p->mfma_groups) {
             case 4:
-                if (bf) hipLaunchKernelGGL((mfma_pair_kernel<true, 4>), grid, dim3(kPairThreads), 0, s, a);
-                else hipLaunchKernelGGL((mfma_pair_kernel<false, 4>), grid, dim3(kPairThreads), 0, s, a);
+                if (bf) TCA_PHASE_LAUNCH((mfma_pair_kernel<true, 4>), grid, dim3(kPairThreads), 0, s, a);
+                else TCA_PHASE_LAUNCH((mfma_pair_kernel<false, 4>), grid, dim3(kPairThreads), 0, s, a);
                 return TCA_OK;
             case 8:
-                if (bf) hipLaunchKernelGGL((mfma_pair_kernel<true, 8>), grid, dim3(kPairThreads), 0, s, a);
-                else hipLaunchKernelGGL((mfma_pair_kernel<false, 8>), grid, dim3(kPairThreads), 0, s, a);
+                if (bf) TCA_PHASE_LAUNCH((mfma_pair_kernel<true, 8>), grid, dim3(kPairThreads), 0, s, a);
+                else TCA_PHASE_LAUNCH((mfma_pair_kernel<false, 8>), grid, dim3(kPairThreads), 0, s, a);
                 return TCA_OK;
             default: return fail(TCA_ERR_INVALID, "bad MFMA entry group count %d", p->mfma_groups);
         }
@@ -402,7 +417,7 @@ void launch_panels_t(const tca_spmm_plan* p, const void* val, const void* B, flo
     a.chunks = p->panels.chunks;
     a.pos_bytes = static_cast<uint32_t>(p->n_pos_bytes);
     a.val_bytes = static_cast<uint32_t>(static_cast<uint64_t>(p->nnz) * sizeof(T));
-    hipLaunchKernelGGL((panel_kernel<T, E>), dim3(p->n_pblocks * p->panels.chunks), dim3(kPnThreads), 0, s, a);
+    TCA_PHASE_LAUNCH((panel_kernel<T, E>), dim3(p->n_pblocks * p->panels.chunks), dim3(kPnThreads), 0, s, a);
 }
 
 int launch_panels(const tca_spmm_plan* p, const void* val, const void* B, float* C, float* W, hipStream_t s) {
@@ -1587,53 +1602,84 @@ int tca_gather_values(const int32_t* d_perm, int32_t n, const void* d_val, int32
 }
 
 int tca_spmm_time_phases(const tca_spmm_plan* p, const void* d_val, const void* d_B, float* d_C, void* stream,
-                         int32_t warmup, int32_t iters, float* phase_ms) {
-    if (!p || !phase_ms || iters < 1 || warmup < 0) return fail(TCA_ERR_INVALID, "tca_spmm_time_phases: bad argument");
-    for (int k = 0; k < TCA_PHASES; k++) phase_ms[k] = 0.f;
-    // Full runs first: every phase's inputs (packed entries, segment partial
-    // sums) then exist, and each phase is idempotent, so a phase can be timed
-    // alone as `iters` back-to-back launches between two events.
-    for (int i = 0; i < warmup + 1; i++) {
+                         int32_t warmup, int32_t iters, float* phase_ms, int32_t n_phase_ms) {
+    if (!p || !phase_ms || n_phase_ms < 1 || iters < 1 || iters > 100000 || warmup < 0)
+        return fail(TCA_ERR_INVALID, "tca_spmm_time_phases: bad argument");
+    const int n_out = n_phase_ms < TCA_PHASES ? n_phase_ms : TCA_PHASES;
+    for (int k = 0; k < n_out; k++) phase_ms[k] = 0.f;
+    if (n_phase_ms > TCA_PHASE_RUN) phase_ms[TCA_PHASE_RUN] = 0.f;
+    for (int i = 0; i < warmup; i++) {
         int st = tca_spmm_run(p, d_val, d_B, d_C, stream);
         if (st) return st;
     }
     if (p->M == 0) return TCA_OK;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    hipEvent_t e0 = nullptr, e1 = nullptr;
-    TCA_HIP_TRY(hipEventCreate(&e0));
-    if (hipEventCreate(&e1) != hipSuccess) {
-        (void)hipEventDestroy(e0);
-        return fail(TCA_ERR_HIP, "hipEventCreate failed");
-    }
+    bool used[TCA_PHASES];
+    used[TCA_PHASE_PACK] = !p->mfma.windows.empty() && (!p->mfma.entries.empty() || p->n_dn > 0);
+    used[TCA_PHASE_TILES] = !p->mfma.windows.empty() || p->mfma_short;
+    used[TCA_PHASE_ROWS] = p->ntasks > 0;
+    used[TCA_PHASE_SEGMENTS] = p->n_longrows > 0;
+    used[TCA_PHASE_PANELS] = p->n_units > 0;
+    // `iters` whole runs back to back, in run_phases' launch order; each
+    // phase's one kernel is dispatched with a start and a stop event of its
+    // own (TCA_PHASE_LAUNCH), so nothing is inserted between the kernels and
+    // a phase's time is the mean over the runs of its kernel's span.  All
+    // runs are queued before the first event is read.
+    std::vector<hipEvent_t> ev(static_cast<size_t>(iters) * TCA_PHASES * 2, nullptr);
     int st = TCA_OK;
-    const bool used[TCA_PHASES] = {!p->mfma.windows.empty() && (!p->mfma.entries.empty() || p->n_dn > 0),
-                                   !p->mfma.windows.empty() || p->mfma_short,
-                                   p->ntasks > 0, p->n_longrows > 0, p->n_units > 0};
-    for (int k = 0; k < TCA_PHASES && st == TCA_OK; k++) {
-        if (!used[k]) continue;
-        (void)hipEventRecord(e0, s);
-        for (int i = 0; i < iters && st == TCA_OK; i++) {
-            switch (k) {
-                case TCA_PHASE_PACK: launch_pack(p, d_val, s); break;
-                case TCA_PHASE_TILES: st = launch_mfma(p, d_val, d_B, d_C, s); break;
-                case TCA_PHASE_ROWS: st = launch_rows(p, d_val, d_B, d_C, p->d_partials, s); break;
-                case TCA_PHASE_PANELS: st = launch_panels(p, d_val, d_B, d_C, p->d_partials, s); break;
-                default: launch_finalize(p, d_C, p->d_partials, s); break;
-            }
+    for (auto& e : ev)
+        if (hipEventCreate(&e) != hipSuccess) {
+            e = nullptr;
+            st = fail(TCA_ERR_HIP, "hipEventCreate failed");
+            break;
         }
-        (void)hipEventRecord(e1, s);
-        float ms = 0.f;
-        if (st == TCA_OK && (hipEventSynchronize(e1) != hipSuccess || hipEventElapsedTime(&ms, e0, e1) != hipSuccess))
-            st = fail(TCA_ERR_HIP, "event timing failed");
-        phase_ms[k] = ms / static_cast<float>(iters);
+    hipEvent_t r0 = nullptr, r1 = nullptr;  // around all the runs
+    if (st == TCA_OK && (hipEventCreate(&r0) != hipSuccess || hipEventCreate(&r1) != hipSuccess))
+        st = fail(TCA_ERR_HIP, "hipEventCreate failed");
+    if (st == TCA_OK && hipEventRecord(r0, s) != hipSuccess) st = fail(TCA_ERR_HIP, "hipEventRecord failed");
+    auto arm = [&](int i, int k) {
+        g_phase_ev[0] = ev[(static_cast<size_t>(i) * TCA_PHASES + k) * 2];
+        g_phase_ev[1] = ev[(static_cast<size_t>(i) * TCA_PHASES + k) * 2 + 1];
+    };
+    for (int i = 0; i < iters && st == TCA_OK; i++) {
+        arm(i, TCA_PHASE_PACK);
+        launch_pack(p, d_val, s);
+        arm(i, TCA_PHASE_TILES);
+        st = launch_mfma(p, d_val, d_B, d_C, s);
+        arm(i, TCA_PHASE_PANELS);
+        if (st == TCA_OK) st = launch_panels(p, d_val, d_B, d_C, p->d_partials, s);
+        arm(i, TCA_PHASE_ROWS);
+        if (st == TCA_OK) st = launch_rows(p, d_val, d_B, d_C, p->d_partials, s);
+        arm(i, TCA_PHASE_SEGMENTS);
+        if (st == TCA_OK) launch_finalize(p, d_C, p->d_partials, s);
+        g_phase_ev[0] = g_phase_ev[1] = nullptr;
     }
-    (void)hipEventDestroy(e0);
-    (void)hipEventDestroy(e1);
+    g_phase_ev[0] = g_phase_ev[1] = nullptr;
+    if (st == TCA_OK && hipEventRecord(r1, s) != hipSuccess) st = fail(TCA_ERR_HIP, "hipEventRecord failed");
     if (st == TCA_OK) {
         hipError_t e = hipGetLastError();
-        if (e != hipSuccess) return fail(TCA_ERR_HIP, "kernel launch: %s", hipGetErrorString(e));
+        if (e != hipSuccess) st = fail(TCA_ERR_HIP, "kernel launch: %s", hipGetErrorString(e));
     }
-    return st;
+    if (st == TCA_OK && hipStreamSynchronize(s) != hipSuccess) st = fail(TCA_ERR_HIP, "stream synchronisation failed");
+    double sum[TCA_PHASES] = {0, 0, 0, 0, 0};
+    for (int i = 0; i < iters && st == TCA_OK; i++)
+        for (int k = 0; k < TCA_PHASES && st == TCA_OK; k++) {
+            if (!used[k]) continue;
+            float ms = 0.f;
+            const size_t at = (static_cast<size_t>(i) * TCA_PHASES + k) * 2;
+            if (hipEventElapsedTime(&ms, ev[at], ev[at + 1]) != hipSuccess) st = fail(TCA_ERR_HIP, "event timing failed");
+            sum[k] += ms;
+        }
+    float run_ms = 0.f;
+    if (st == TCA_OK && hipEventElapsedTime(&run_ms, r0, r1) != hipSuccess) st = fail(TCA_ERR_HIP, "event timing failed");
+    for (auto e : ev)
+        if (e) (void)hipEventDestroy(e);
+    if (r0) (void)hipEventDestroy(r0);
+    if (r1) (void)hipEventDestroy(r1);
+    if (st != TCA_OK) return st;
+    for (int k = 0; k < n_out; k++) phase_ms[k] = used[k] ? static_cast<float>(sum[k] / iters) : 0.f;
+    if (n_phase_ms > TCA_PHASE_RUN) phase_ms[TCA_PHASE_RUN] = run_ms / static_cast<float>(iters);
+    return TCA_OK;
 }
 
 int tca_spmm_host(const int32_t* rowptr, const int32_t* colidx, const void* val, int32_t M, int32_t K, int32_t nnz,
