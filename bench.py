@@ -118,8 +118,8 @@ def main():
                     help="time the Blocked-ELL kernel (tca_bell_spmm) on A converted to blocks of BS x BS "
                          "instead of the CSR plan (fp16 / bf16 configurations)")
     ap.add_argument("--device-plan", action="store_true",
-                    help="build the plan on the GPU from device-resident CSR arrays (tca_spmm_plan_create_device; "
-                         "row-kernel plans) instead of the host planner")
+                    help="build the plan on the GPU from device-resident CSR arrays (tca_spmm_plan_create_device: "
+                         "row tasks, row panels, dense MFMA tiles) instead of the host planner")
     ap.add_argument("--sparse24", action="store_true",
                     help="time the 2:4 sparse-MFMA kernel (tca_spmm_24) on A pruned to 2:4 (fp16 / bf16 configurations)")
     args = ap.parse_args()

@@ -276,6 +276,22 @@ int tca_spmm_plan_export_order(const tca_spmm_plan* plan, int32_t* n_slots, int3
 int tca_spmm_plan_export_tiles(const tca_spmm_plan* plan, int32_t* n_windows, int32_t* n_entries, int32_t* n_ucols,
                                int32_t* windows, uint32_t* pos, int32_t* src, uint32_t* ucols);
 
+/* The plan's row panels as the panel kernel reads them (so tests can check a
+ * GPU-built plan against the host planner's, entry for entry).  sizes[8] in:
+ * capacities, out: {panels, tiles, units, launch-order entries, the panels'
+ * long rows, R (rows per panel), P (tile columns), pos bytes}.  With rows ==
+ * NULL only the sizes are written.  Arrays: rows [panels * R] (-1: empty
+ * slot), boff [tiles * P] (staged B rows as byte offsets), cnt [tiles *
+ * waves * 8] (count dwords), pos [pos bytes] (1-based tile position per
+ * nonzero, 0 outside panels), units [units * 4], order [launch-order entries]
+ * (-1: idle workgroup), panel_units [panels], ustart [units * R], longrows
+ * [panel long rows * 4] (segment slots after the row kernel's).  No
+ * counterpart in the reference (its task split, src/our_spmm.cu:353-477, has
+ * no panels). */
+int tca_spmm_plan_export_panels(const tca_spmm_plan* plan, int64_t* sizes, int32_t* rows, uint32_t* boff, uint32_t* cnt,
+                                uint8_t* pos, int32_t* units, int32_t* order, int32_t* panel_units, int32_t* ustart,
+                                int32_t* longrows);
+
 int tca_spmm_plan_info(const tca_spmm_plan* plan, tca_plan_info* info);
 
 int tca_spmm_plan_destroy(tca_spmm_plan* plan);

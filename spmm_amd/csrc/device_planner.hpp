@@ -55,12 +55,14 @@ __global__ void dp_check_cols_kernel(const int* __restrict__ colidx, int nnz, in
     }
 }
 
-// keys = row lengths + 1 (0 for rows of routed windows: wmap[r / 128] >= 0),
-// vals = row ids (the radix sort's input).  wmap may be NULL.
+// keys = row lengths + 1 (0 for rows of routed windows: wmap[r / 128] >= 0,
+// and for rows of taken panels: in_panel[r] != 0), vals = row ids (the radix
+// sort's input).  wmap and in_panel may be NULL.
 __global__ void dp_lengths_kernel(const int* __restrict__ rowptr, int M, const int* __restrict__ wmap,
-                                  uint32_t* __restrict__ keys, int* __restrict__ rows) {
+                                  const uint8_t* __restrict__ in_panel, uint32_t* __restrict__ keys,
+                                  int* __restrict__ rows) {
     for (int r = blockIdx.x * blockDim.x + threadIdx.x; r < M; r += gridDim.x * blockDim.x) {
-        const bool tiles = wmap && wmap[r / kDmaWinRows] >= 0;
+        const bool tiles = (wmap && wmap[r / kDmaWinRows] >= 0) || (in_panel && in_panel[r]);
         keys[r] = tiles ? 0u : static_cast<uint32_t>(rowptr[r + 1] - rowptr[r]) + 1u;
         rows[r] = r;
     }

@@ -287,22 +287,43 @@ bool panel_default_ok(int32_t N, int32_t es) {
 
 int32_t panel_tile_cols(int32_t chunk_bytes) { return std::min<int32_t>(255, 77824 / chunk_bytes); }
 
+bool panel_route(int32_t N, int32_t dtype, uint32_t flags, PanelRoute* r) {
+    *r = PanelRoute{};
+    if ((flags & TCA_PLAN_NO_PANELS) ||
+        (!(flags & TCA_PLAN_FORCE_PANELS) && !panel_default_ok(N, static_cast<int32_t>(dtype_size(dtype)))))
+        return false;
+    r->force = (flags & TCA_PLAN_FORCE_PANELS) != 0;
+    r->min_reuse = kPanelMinReuse;
+    r->min_nnz = kPanelMinNnz;
+    r->unit_nnz = 0;
+    // Tuning overrides (not part of the interface).
+    if (const char* e = std::getenv("TCA_PANEL_MIN_REUSE")) r->min_reuse = std::atof(e);
+    if (const char* e = std::getenv("TCA_PANEL_MIN_NNZ")) r->min_nnz = std::atoll(e);
+    if (const char* e = std::getenv("TCA_PANEL_UNIT")) r->unit_nnz = std::atoll(e);
+    return true;
+}
+
+int64_t panel_unit_nnz(int64_t unit_nnz, int64_t tot) {
+    // Units of ~1/320 of the panels' nonzeros: about one per CU, so each CU
+    // works through one contiguous column range of a panel and the partial
+    // rows stay few (measured on MI355X, per SpMM, config 2 / config 3:
+    // tot / 2048 1.87 / 3.34 ms, / 1024 1.69 / 3.23, / 512 1.65 / 3.24,
+    // / 256 1.63 / 3.07, / 128 - / 3.67, one box; then on another, config 3:
+    // / 256 3.15, / 320 3.03-3.04, / 192 3.08-3.13, config 2 level within
+    // the box's 5 % noise).
+    return unit_nnz > 0 ? unit_nnz : std::max<int64_t>(8192, tot / 320);
+}
+
 void plan_panels_routed(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_t K, int32_t N,
                         int32_t dtype, uint32_t flags, const std::vector<uint8_t>& skip, PanelPlan* p) {
-    if ((flags & TCA_PLAN_NO_PANELS) ||
-        (!(flags & TCA_PLAN_FORCE_PANELS) && !panel_default_ok(N, static_cast<int32_t>(dtype_size(dtype))))) {
+    PanelRoute r;
+    if (!panel_route(N, dtype, flags, &r)) {
         *p = PanelPlan{};
         p->row_panel.assign(M, 0);
         return;
     }
-    double min_reuse = kPanelMinReuse;
-    int64_t unit = 0, min_nnz = kPanelMinNnz;
-    // Tuning overrides (not part of the interface).
-    if (const char* e = std::getenv("TCA_PANEL_MIN_REUSE")) min_reuse = std::atof(e);
-    if (const char* e = std::getenv("TCA_PANEL_MIN_NNZ")) min_nnz = std::atoll(e);
-    if (const char* e = std::getenv("TCA_PANEL_UNIT")) unit = std::atoll(e);
-    plan_panels(rowptr, colidx, M, K, N, static_cast<int32_t>(dtype_size(dtype)), skip,
-                (flags & TCA_PLAN_FORCE_PANELS) != 0, min_reuse, min_nnz, unit, p);
+    plan_panels(rowptr, colidx, M, K, N, static_cast<int32_t>(dtype_size(dtype)), skip, r.force, r.min_reuse,
+                r.min_nnz, r.unit_nnz, p);
 }
 
 void plan_panels(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_t K, int32_t N, int32_t es,
@@ -420,14 +441,7 @@ void plan_panels(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_
         p->pos.clear();
         return;
     }
-    // Units of ~1/320 of the panels' nonzeros: about one per CU, so each CU
-    // works through one contiguous column range of a panel and the partial
-    // rows stay few (measured on MI355X, per SpMM, config 2 / config 3:
-    // tot / 2048 1.87 / 3.34 ms, / 1024 1.69 / 3.23, / 512 1.65 / 3.24,
-    // / 256 1.63 / 3.07, / 128 - / 3.67, one box; then on another, config 3:
-    // / 256 3.15, / 320 3.03-3.04, / 192 3.08-3.13, config 2 level within
-    // the box's 5 % noise).
-    if (unit_nnz <= 0) unit_nnz = std::max<int64_t>(8192, tot / 320);
+    unit_nnz = panel_unit_nnz(unit_nnz, tot);
     std::vector<int32_t> panel_of(n_cand, -1), tile0(n_cand, 0);
     int32_t n_tiles = 0;
     for (int32_t q = 0; q < n_cand; q++) {
@@ -542,11 +556,23 @@ void plan_panels(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_
 }
 
 void order_units(int32_t K, PanelPlan* p) {
-    const int32_t nu = static_cast<int32_t>(p->units.size());
-    p->order.clear();
+    const size_t nu = p->units.size();
+    std::vector<int64_t> lo(nu), hi(nu);
+    for (size_t u = 0; u < nu; u++) {
+        const Int4& t = p->units[u];
+        lo[u] = p->cols[static_cast<size_t>(t.y) * p->P];
+        hi[u] = p->cols[static_cast<size_t>(t.y + t.z) * p->P - 1];  // padding repeats the last column
+    }
+    order_unit_spans(K, p->chunks, p->units, lo, hi, &p->order);
+}
+
+void order_unit_spans(int32_t K, int32_t chunks, const std::vector<Int4>& units, const std::vector<int64_t>& lo,
+                      const std::vector<int64_t>& hi, std::vector<int32_t>* order) {
+    const int32_t nu = static_cast<int32_t>(units.size());
+    order->clear();
     const char* e = std::getenv("TCA_PANEL_ORDER");  // tuning override: 0 = natural order
-    if (p->chunks != 1 || (e && std::atoi(e) == 0)) {
-        for (int32_t u = 0; u < nu; u++) p->order.push_back(u);
+    if (chunks != 1 || (e && std::atoi(e) == 0)) {
+        for (int32_t u = 0; u < nu; u++) order->push_back(u);
         return;
     }
     // The hardware deals workgroups to the XCDs round robin (workgroup b on
@@ -557,17 +583,13 @@ void order_units(int32_t K, PanelPlan* p) {
     // together on one XCD stage nearby B rows and meet them in its L2.  Wider
     // units follow, each on the XCD with the fewest tiles so far; shorter
     // queues end in idle workgroups.
-    const int32_t P = p->P;
     std::vector<std::pair<int64_t, int32_t>> local;
     std::vector<int32_t> wide;
     int64_t local_tiles = 0;
     for (int32_t u = 0; u < nu; u++) {
-        const Int4& t = p->units[u];
-        const int64_t lo = p->cols[static_cast<size_t>(t.y) * P];
-        const int64_t hi = p->cols[static_cast<size_t>(t.y + t.z) * P - 1];  // padding repeats the last column
-        if ((hi - lo) * (kXcds / 2) <= K) {
-            local.push_back({lo + hi, u});
-            local_tiles += t.z;
+        if ((hi[u] - lo[u]) * (kXcds / 2) <= K) {
+            local.push_back({lo[u] + hi[u], u});
+            local_tiles += units[u].z;
         } else {
             wide.push_back(u);
         }
@@ -577,7 +599,7 @@ void order_units(int32_t K, PanelPlan* p) {
     std::vector<int64_t> load(kXcds, 0);
     int64_t cum = 0;
     for (const auto& l : local) {
-        const int32_t z = p->units[l.second].z;
+        const int32_t z = units[l.second].z;
         const int32_t x = static_cast<int32_t>(std::min<int64_t>(kXcds - 1, (2 * cum + z) * kXcds / (2 * local_tiles)));
         q[x].push_back(l.second);
         load[x] += z;
@@ -586,13 +608,13 @@ void order_units(int32_t K, PanelPlan* p) {
     for (int32_t u : wide) {
         const int32_t x = static_cast<int32_t>(std::min_element(load.begin(), load.end()) - load.begin());
         q[x].push_back(u);
-        load[x] += p->units[u].z;
+        load[x] += units[u].z;
     }
     size_t len = 0;
     for (const auto& v : q) len = std::max(len, v.size());
-    p->order.assign(len * kXcds, -1);
+    order->assign(len * kXcds, -1);
     for (int32_t x = 0; x < kXcds; x++)
-        for (size_t k = 0; k < q[x].size(); k++) p->order[k * kXcds + x] = q[x][k];
+        for (size_t k = 0; k < q[x].size(); k++) (*order)[k * kXcds + x] = q[x][k];
 }
 
 bool row_order_on(const RowPlan& p) {

@@ -192,6 +192,23 @@ constexpr double kPanelMinReuse = 1.02;
 constexpr int64_t kPanelMinNnz = int64_t(1) << 21;  // fewer nonzeros in panels: none (unless forced)
 // Launch order of the units (PanelPlan::order).
 void order_units(int32_t K, PanelPlan* p);
+// The same from each unit's first and last staged column (the GPU planner
+// builds those and runs this order on the host).
+void order_unit_spans(int32_t K, int32_t chunks, const std::vector<Int4>& units, const std::vector<int64_t>& lo,
+                      const std::vector<int64_t>& hi, std::vector<int32_t>* order);
+// Routing parameters of the panels (shared by the host and the GPU planner):
+// false when the plan takes no panels (TCA_PLAN_NO_PANELS, or by default B
+// rows under 256 bytes); else force / min_reuse / min_nnz / unit_nnz for
+// plan_panels (TCA_PANEL_MIN_REUSE, TCA_PANEL_MIN_NNZ, TCA_PANEL_UNIT: tuning
+// overrides).
+struct PanelRoute {
+    bool force = false;
+    double min_reuse = 0.0;
+    int64_t min_nnz = 0, unit_nnz = 0;
+};
+bool panel_route(int32_t N, int32_t dtype, uint32_t flags, PanelRoute* r);
+// Nonzeros per unit for panels holding `tot` nonzeros (unit_nnz > 0: forced).
+int64_t panel_unit_nnz(int64_t unit_nnz, int64_t tot);
 // Launch order of the row kernel's tasks (RowPlan::order): segments of long
 // rows by column range, one range per XCD.  row_order_on: whether a plan
 // gets one (one column chunk, at least 32 segments; TCA_ROW_ORDER=0 turns it

@@ -21,6 +21,7 @@
 #include "bell_kernel.hpp"
 #include "sparse24_kernel.hpp"
 #include "device_planner.hpp"
+#include "device_panel_planner.hpp"
 #include "panel_kernel.hpp"
 #include "sddmm_kernel.hpp"
 
@@ -98,6 +99,8 @@ struct tca_spmm_plan {
     uint8_t* d_ppos = nullptr;
     int* d_ustart = nullptr;
     size_t n_pos_bytes = 0;  // d_ppos, whole dwords
+    int64_t n_ptiles = 0;    // panel tiles (d_pcols: n_ptiles * P entries)
+    int32_t n_plongrows = 0; // the panels' long rows: the last entries of d_longrows
     tca_plan_info info{};
 };
 
@@ -733,6 +736,8 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
         }
         const size_t n_seg_total = n_seg_rows + static_cast<size_t>(p->panels.n_segments);
         p->n_units = static_cast<int32_t>(p->panels.units.size());
+        p->n_ptiles = p->panels.n_tiles();
+        p->n_plongrows = static_cast<int32_t>(p->panels.longrows.size());
         p->n_longrows = static_cast<int32_t>(p->rows.longrows.size());
         p->n_seg_total = n_seg_total;
         p->n_perm = static_cast<int32_t>(p->rows.perm.size());
@@ -939,6 +944,278 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
     });
 }
 
+// Row panels planned on the GPU (device_panel_planner.hpp), in two phases
+// around the row kernel's plan: phase_a picks the panels and their rows (the
+// row kernel then plans the other rows), phase_b writes the plan's panel
+// arrays once the row kernel's segments are known (the panels' partial rows
+// follow them, as in tca_spmm_plan_create).  The decisions that need all
+// panels at once -- which candidates are taken, the exclusive sums over
+// panels, the XCD launch order -- run on the host over per-panel arrays,
+// with the host planner's own rules.
+struct DevPanelPlanner {
+    hipStream_t s = nullptr;
+    int *lenv = nullptr, *lenpre = nullptr, *ucols = nullptr, *upos = nullptr, *ucount = nullptr, *pnnz = nullptr;
+    int *take_q = nullptr, *ubase = nullptr, *tbase = nullptr, *tile0 = nullptr, *m = nullptr, *cuts = nullptr;
+    int *ntiles = nullptr, *tile_of = nullptr, *tn = nullptr, *ucut = nullptr, *nunits = nullptr;
+    int4* poff = nullptr;
+    int64_t *ulo = nullptr, *uhi = nullptr;
+    uint8_t* in_panel = nullptr;
+    void* tmp = nullptr;
+    const int* rows_s = nullptr;  // the panels' row order (phase_b: a copy kept past the second sort)
+    std::vector<int> h_take, h_nt, h_nu, h_rows_in;
+    int n_nz = 0, n_take = 0, n_panel_rows = 0, n_plongrows = 0;
+    int64_t n_tiles = 0, n_units = 0, n_segments = 0, nnz = 0, staged = 0, unit_nnz = 0;
+    int E = 0, P = 0;
+
+    ~DevPanelPlanner() {
+        (void)hipStreamSynchronize(s);
+        for (void* q : {(void*)lenv, (void*)lenpre, (void*)ucols, (void*)upos, (void*)ucount, (void*)pnnz, (void*)take_q,
+                        (void*)ubase, (void*)tbase, (void*)tile0, (void*)m, (void*)cuts, (void*)ntiles, (void*)tile_of,
+                        (void*)tn, (void*)ucut, (void*)nunits, (void*)poff, (void*)ulo, (void*)uhi, (void*)in_panel, tmp})
+            (void)hipFree(q);
+    }
+
+    DppPanelArgs args(const tca_spmm_plan* p) const {
+        DppPanelArgs a{};
+        a.rowptr = p->d_rowptr;
+        a.rows = rows_s;
+        a.lenpre = lenpre;
+        a.ucols = ucols;
+        a.upos = upos;
+        a.ucount = ucount;
+        a.take_q = take_q;
+        a.ubase = ubase;
+        a.tbase = tbase;
+        a.tile0 = tile0;
+        a.n_nz = n_nz;
+        a.P = P;
+        a.n_take = n_take;
+        a.row_bytes = static_cast<uint32_t>(p->N) * static_cast<uint32_t>(dtype_size(p->dtype));
+        a.m = m;
+        a.cuts = cuts;
+        a.ntiles = ntiles;
+        a.tile_of = tile_of;
+        a.tn = tn;
+        a.cntb = reinterpret_cast<uint8_t*>(p->d_pcnt);
+        a.boff = reinterpret_cast<uint32_t*>(p->d_pcols);
+        a.pos = p->d_ppos;
+        a.ucut = ucut;
+        a.nunits = nunits;
+        a.poff = poff;
+        a.prows = p->d_prows;
+        a.units = p->d_units;
+        a.ustart = p->d_ustart;
+        a.panel_units = p->d_panel_units;
+        a.longrows = p->d_longrows;
+        a.ulo = ulo;
+        a.uhi = uhi;
+        return a;
+    }
+
+    // keys_s / order: the longest-first order (keys = length + 1, 0 for
+    // rows of MFMA windows); n_nz_rows: rows with nonzeros outside windows.
+    // On return n_take > 0 when panels are taken, in_panel flags their rows,
+    // and the plan's tile arrays (staged rows, counts, positions) are written.
+    int phase_a(tca_spmm_plan* p, const uint32_t* keys_s, const int* order, int n_nz_rows) {
+        PanelRoute route;
+        const int32_t es = static_cast<int32_t>(dtype_size(p->dtype));
+        E = panel_elems(p->N, es);
+        if (!panel_route(p->N, p->dtype, p->flags, &route) || E == 0 || p->M == 0 || n_nz_rows == 0) return TCA_OK;
+        // (the union kernel's column chunks end below c0 + 2^19: K leaves room for them in an int)
+        if (p->K > INT_MAX - 32 * kDppChunkWords) return fail(TCA_ERR_UNSUPPORTED, "K too large for panels planned on the GPU");
+        P = panel_tile_cols(16 * E * es);
+        n_nz = n_nz_rows;
+        rows_s = order;
+        const int n_cand = (n_nz + kDppR - 1) / kDppR;
+        int st;
+        if ((st = dev_upload(&lenv, nullptr, static_cast<size_t>(n_nz) + 1)) ||
+            (st = dev_upload(&lenpre, nullptr, static_cast<size_t>(n_nz) + 1)) ||
+            (st = dev_upload(&upos, nullptr, static_cast<size_t>(p->nnz))) ||
+            (st = dev_upload(&ucount, nullptr, n_cand)) || (st = dev_upload(&pnnz, nullptr, n_cand)))
+            return st;
+        const dim3 blk(256);
+        auto grid_for = [](int64_t n) { return dim3(static_cast<unsigned>(std::min<int64_t>((n + 255) / 256, 65536))); };
+        hipLaunchKernelGGL(dpp_len_kernel, grid_for(n_nz), blk, 0, s, keys_s, n_nz, lenv);
+        if (hipMemsetAsync(lenv + n_nz, 0, sizeof(int), s) != hipSuccess) return fail(TCA_ERR_HIP, "hipMemsetAsync failed");
+        size_t tmp_bytes = 0;
+        int total = 0;
+        if (rocprim::exclusive_scan(nullptr, tmp_bytes, lenv, lenpre, 0, static_cast<size_t>(n_nz) + 1,
+                                    rocprim::plus<int>(), s) != hipSuccess ||
+            dev_malloc(&tmp, std::max<size_t>(tmp_bytes, 4)) != hipSuccess ||
+            rocprim::exclusive_scan(tmp, tmp_bytes, lenv, lenpre, 0, static_cast<size_t>(n_nz) + 1, rocprim::plus<int>(),
+                                    s) != hipSuccess ||
+            hipMemcpyAsync(&total, lenpre + n_nz, sizeof(int), hipMemcpyDeviceToHost, s) != hipSuccess ||
+            hipStreamSynchronize(s) != hipSuccess)
+            return fail(TCA_ERR_HIP, "panel length scan failed");
+        if ((st = dev_upload(&ucols, nullptr, std::max(total, 1)))) return st;
+        DppUnionArgs ua;
+        ua.rowptr = p->d_rowptr;
+        ua.colidx = p->d_colidx;
+        ua.rows = rows_s;
+        ua.lenpre = lenpre;
+        ua.n_nz = n_nz;
+        ua.ucols = ucols;
+        ua.upos = upos;
+        ua.ucount = ucount;
+        ua.pnnz = pnnz;
+        hipLaunchKernelGGL(dpp_union_kernel, dim3(n_cand), dim3(kDppThreads), 0, s, ua);
+        std::vector<int> h_ucount(n_cand), h_pnnz(n_cand);
+        if (hipMemcpyAsync(h_ucount.data(), ucount, sizeof(int) * n_cand, hipMemcpyDeviceToHost, s) != hipSuccess ||
+            hipMemcpyAsync(h_pnnz.data(), pnnz, sizeof(int) * n_cand, hipMemcpyDeviceToHost, s) != hipSuccess ||
+            hipStreamSynchronize(s) != hipSuccess)
+            return fail(TCA_ERR_HIP, "panel unions failed");
+        // which candidates are taken: plan_panels' rule
+        int64_t tot = 0;
+        for (int q = 0; q < n_cand; q++) {
+            const bool take = h_ucount[q] > 0 &&
+                              (route.force || static_cast<double>(h_pnnz[q]) >= route.min_reuse * h_ucount[q]);
+            if (!take) continue;
+            h_take.push_back(q);
+            tot += h_pnnz[q];
+        }
+        if (tot == 0 || (!route.force && tot < route.min_nnz)) {
+            h_take.clear();
+            return TCA_OK;
+        }
+        n_take = static_cast<int>(h_take.size());
+        unit_nnz = panel_unit_nnz(route.unit_nnz, tot);
+        std::vector<int> h_ubase(n_take), h_tbase(n_take);
+        int64_t usum = 0, tsum = 0;
+        for (int t = 0; t < n_take; t++) {
+            const int q = h_take[t];
+            h_ubase[t] = static_cast<int>(usum);
+            h_tbase[t] = static_cast<int>(tsum);
+            usum += h_ucount[q];
+            tsum += static_cast<int64_t>(h_ucount[q]) + 1;
+            h_rows_in.push_back(std::min(kDppR, n_nz - q * kDppR));
+            n_panel_rows += h_rows_in.back();
+            nnz += h_pnnz[q];
+            staged += h_ucount[q];
+        }
+        if (tsum >= (int64_t(1) << 31)) return fail(TCA_ERR_UNSUPPORTED, "panel tile scratch past 2^31 entries");
+        if ((st = dev_upload(&take_q, h_take.data(), n_take)) || (st = dev_upload(&ubase, h_ubase.data(), n_take)) ||
+            (st = dev_upload(&tbase, h_tbase.data(), n_take)) || (st = dev_upload(&ntiles, nullptr, n_take)) ||
+            (st = dev_upload(&nunits, nullptr, n_take)) || (st = dev_upload(&m, nullptr, static_cast<size_t>(usum))) ||
+            (st = dev_upload(&tile_of, nullptr, static_cast<size_t>(usum))) ||
+            (st = dev_upload(&cuts, nullptr, static_cast<size_t>(tsum))) ||
+            (st = dev_upload(&tn, nullptr, static_cast<size_t>(tsum))) ||
+            (st = dev_upload(&ucut, nullptr, static_cast<size_t>(tsum))) ||
+            (st = dev_upload(&in_panel, nullptr, static_cast<size_t>(p->M))))
+            return st;
+        if (hipMemsetAsync(in_panel, 0, static_cast<size_t>(p->M), s) != hipSuccess ||
+            hipMemsetAsync(m, 0x7f, sizeof(int) * static_cast<size_t>(usum), s) != hipSuccess ||
+            hipMemsetAsync(tn, 0, sizeof(int) * static_cast<size_t>(tsum), s) != hipSuccess)
+            return fail(TCA_ERR_HIP, "hipMemsetAsync failed");
+        hipLaunchKernelGGL(dpp_mark_kernel, dim3(n_take), blk, 0, s, rows_s, n_nz, take_q, n_take, in_panel);
+        // tile cuts: m, then suffix minimum and walk
+        DppPanelArgs a = args(p);
+        const dim3 rgrid(static_cast<unsigned>(n_take) * (kDppR / 4));  // one wavefront per panel row
+        hipLaunchKernelGGL(dpp_m_kernel, rgrid, blk, 0, s, a);
+        hipLaunchKernelGGL(dpp_walk_kernel, dim3(n_take), dim3(1024), 0, s, a);
+        h_nt.resize(n_take);
+        if (hipMemcpyAsync(h_nt.data(), ntiles, sizeof(int) * n_take, hipMemcpyDeviceToHost, s) != hipSuccess ||
+            hipStreamSynchronize(s) != hipSuccess)
+            return fail(TCA_ERR_HIP, "panel tile cuts failed");
+        std::vector<int> h_tile0(n_take);
+        for (int t = 0; t < n_take; t++) {
+            h_tile0[t] = static_cast<int>(n_tiles);
+            n_tiles += h_nt[t];
+        }
+        if (n_tiles * P >= (int64_t(1) << 31)) return fail(TCA_ERR_UNSUPPORTED, "panel plan past 2^31 entries");
+        p->n_pos_bytes = (static_cast<size_t>(p->nnz) + 3) & ~size_t(3);
+        if ((st = dev_upload(&tile0, h_tile0.data(), n_take)) ||
+            (st = dev_upload(&p->d_pcols, nullptr, static_cast<size_t>(n_tiles) * P)) ||
+            (st = dev_upload(&p->d_pcnt, nullptr, static_cast<size_t>(n_tiles) * kDppCntDwords)) ||
+            (st = dev_upload(&p->d_ppos, nullptr, p->n_pos_bytes)))
+            return st;
+        if (hipMemsetAsync(p->d_ppos, 0, p->n_pos_bytes, s) != hipSuccess ||
+            hipMemsetAsync(p->d_pcnt, 0, sizeof(uint32_t) * static_cast<size_t>(n_tiles) * kDppCntDwords, s) != hipSuccess)
+            return fail(TCA_ERR_HIP, "hipMemsetAsync failed");
+        a = args(p);
+        hipLaunchKernelGGL(dpp_tile_fill_kernel, dim3(static_cast<unsigned>(n_tiles)), blk, 0, s, a);
+        hipLaunchKernelGGL(dpp_runs_kernel<false>, rgrid, blk, 0, s, a);
+        const int64_t nme = n_tiles * kPanelWaves * kPanelRpg;
+        hipLaunchKernelGGL(dpp_cnt_max_kernel, dim3(static_cast<unsigned>((nme + 255) / 256)), blk, 0, s,
+                           reinterpret_cast<uint8_t*>(p->d_pcnt), n_tiles);
+        hipLaunchKernelGGL(dpp_units_kernel, dim3((n_take + 3) / 4), blk, 0, s, take_q, n_take, pnnz, tbase, ntiles, tn,
+                           unit_nnz, ucut, nunits);
+        h_nu.resize(n_take);
+        if (hipMemcpyAsync(h_nu.data(), nunits, sizeof(int) * n_take, hipMemcpyDeviceToHost, s) != hipSuccess ||
+            hipStreamSynchronize(s) != hipSuccess)
+            return fail(TCA_ERR_HIP, "panel tiles failed");
+        for (int t = 0; t < n_take; t++) {
+            n_units += h_nu[t];
+            if (h_nu[t] > 1) {
+                n_plongrows += h_rows_in[t];
+                n_segments += static_cast<int64_t>(kDppR) * h_nu[t];
+            }
+        }
+        if (n_units * kDppR >= (int64_t(1) << 31)) return fail(TCA_ERR_UNSUPPORTED, "panel plan past 2^31 entries");
+        return TCA_OK;
+    }
+
+    // seg_off: the row kernel's segments (the panels' follow them);
+    // lr_off: its long rows (the panels' follow them in p->d_longrows).
+    // order: the panels' row order (a copy that outlived the second sort).
+    int phase_b(tca_spmm_plan* p, const int* order, int64_t seg_off, int lr_off) {
+        if (n_take == 0) return TCA_OK;
+        rows_s = order;
+        std::vector<int4> h_poff(n_take);
+        int64_t t0 = 0, unit0 = 0, seg = seg_off, lr = lr_off;
+        for (int t = 0; t < n_take; t++) {
+            h_poff[t] = make_int4(static_cast<int>(t0), static_cast<int>(unit0), h_nu[t] > 1 ? static_cast<int>(seg) : -1,
+                                  static_cast<int>(lr));
+            t0 += h_nt[t];
+            unit0 += h_nu[t];
+            if (h_nu[t] > 1) {
+                seg += static_cast<int64_t>(kDppR) * h_nu[t];
+                lr += h_rows_in[t];
+            }
+        }
+        int st;
+        if ((st = dev_upload(&poff, h_poff.data(), n_take)) ||
+            (st = dev_upload(&p->d_prows, nullptr, static_cast<size_t>(n_take) * kDppR)) ||
+            (st = dev_upload(&p->d_units, nullptr, static_cast<size_t>(n_units))) ||
+            (st = dev_upload(&p->d_ustart, nullptr, static_cast<size_t>(n_units) * kDppR)) ||
+            (st = dev_upload(&p->d_panel_units, nullptr, n_take)) ||
+            (st = dev_upload(&ulo, nullptr, static_cast<size_t>(n_units))) ||
+            (st = dev_upload(&uhi, nullptr, static_cast<size_t>(n_units))))
+            return st;
+        const DppPanelArgs a = args(p);
+        hipLaunchKernelGGL(dpp_emit_units_kernel, dim3(n_take), dim3(256), 0, s, a);
+        hipLaunchKernelGGL(dpp_runs_kernel<true>, dim3(static_cast<unsigned>(n_take) * (kDppR / 4)), dim3(256), 0, s, a);
+        // XCD launch order of the units (host rule, from each unit's column span)
+        std::vector<Int4> units(n_units);
+        std::vector<int64_t> lo(n_units), hi(n_units);
+        if (hipMemcpyAsync(units.data(), p->d_units, sizeof(int4) * n_units, hipMemcpyDeviceToHost, s) != hipSuccess ||
+            hipMemcpyAsync(lo.data(), ulo, sizeof(int64_t) * n_units, hipMemcpyDeviceToHost, s) != hipSuccess ||
+            hipMemcpyAsync(hi.data(), uhi, sizeof(int64_t) * n_units, hipMemcpyDeviceToHost, s) != hipSuccess ||
+            hipStreamSynchronize(s) != hipSuccess)
+            return fail(TCA_ERR_HIP, "panel emission failed");
+        std::vector<int32_t> uorder;
+        const int32_t chunks = p->N / (16 * E);
+        order_unit_spans(p->K, chunks, units, lo, hi, &uorder);
+        if ((st = dev_upload(&p->d_porder, uorder.data(), uorder.size()))) return st;
+        PanelPlan& pp = p->panels;
+        pp.waves = kPanelWaves;
+        pp.rpg = kPanelRpg;
+        pp.R = kDppR;
+        pp.P = P;
+        pp.elems = E;
+        pp.chunks = chunks;
+        pp.n_panels = n_take;
+        pp.nnz = nnz;
+        pp.staged = staged;
+        pp.n_rows = n_panel_rows;
+        pp.n_segments = n_segments;
+        p->n_units = static_cast<int32_t>(n_units);
+        p->n_pblocks = static_cast<int32_t>(uorder.size());
+        p->n_ptiles = n_tiles;
+        p->n_plongrows = n_plongrows;
+        return TCA_OK;
+    }
+};
+
 int tca_spmm_plan_create_device(const int32_t* d_rowptr, const int32_t* d_colidx, int32_t M, int32_t K, int32_t nnz,
                                 int32_t N, int32_t dtype, uint32_t flags, void* stream, tca_spmm_plan** plan) {
     return api_guard("tca_spmm_plan_create_device", [&]() -> int {
@@ -981,12 +1258,13 @@ int tca_spmm_plan_create_device(const int32_t* d_rowptr, const int32_t* d_colidx
         void* tmp = nullptr;
         uint32_t *skey = nullptr, *skey_s = nullptr;  // segment launch order
         int *sidx = nullptr, *sidx_s = nullptr;
+        int* dpp_rows = nullptr;  // the panels' row order (phase_b reads it after the second sort)
         auto bail = [&](int st) {
             (void)hipStreamSynchronize(s);
             for (void* q : {(void*)keys, (void*)keys_s, (void*)rows, (void*)rows_s, (void*)cnt, (void*)nseg, (void*)segoff,
                             (void*)start, tmp, (void*)bm, (void*)ekeys, (void*)ekeys_s, (void*)wordpre, (void*)scnt,
                             (void*)wstat, (void*)wmap, (void*)wgbase, (void*)evals, (void*)evals_s, (void*)skey,
-                            (void*)skey_s, (void*)sidx, (void*)sidx_s})
+                            (void*)skey_s, (void*)sidx, (void*)sidx_s, (void*)dpp_rows})
                 (void)hipFree(q);
             return st;  // on failure `hold` frees the plan
         };
@@ -1206,34 +1484,66 @@ int tca_spmm_plan_create_device(const int32_t* d_rowptr, const int32_t* d_colidx
             }
         }
         if (p->mfma.windows.empty()) p->flags |= TCA_PLAN_NO_MFMA;
-        const int Mp = M - rows_mfma;  // rows of the row kernel
+        int Mp = M - rows_mfma;  // rows outside MFMA windows: panels and the row kernel
 
         // rows longest first (stable descending radix sort of length + 1; rows of
-        // the routed windows have key 0 and sort last)
+        // the routed windows have key 0 and sort last); with panels, those rows
+        // leave too (key 0) and the order is sorted again for the row kernel
+        DevPanelPlanner dpp;
+        dpp.s = s;
+        size_t sort_bytes = 0;
+        auto sort_rows = [&](const uint8_t* in_panel) -> int {
+            hipLaunchKernelGGL(dp_lengths_kernel, grid_for(M), blk, 0, s, p->d_rowptr, M,
+                               p->mfma.windows.empty() ? nullptr : wmap, in_panel, keys, rows);
+            size_t tmp_bytes = 0;
+            if (rocprim::radix_sort_pairs_desc(nullptr, tmp_bytes, keys, keys_s, rows, rows_s, static_cast<size_t>(M), 0, 32,
+                                               s) != hipSuccess)
+                return fail(TCA_ERR_HIP, "radix sort sizing failed");
+            if (tmp_bytes > sort_bytes) {
+                (void)hipStreamSynchronize(s);
+                (void)hipFree(tmp);
+                tmp = nullptr;
+                if (dev_malloc(reinterpret_cast<void**>(&tmp), tmp_bytes) != hipSuccess)
+                    return fail(TCA_ERR_ALLOC, "radix sort workspace");
+                sort_bytes = tmp_bytes;
+            }
+            if (rocprim::radix_sort_pairs_desc(tmp, tmp_bytes, keys, keys_s, rows, rows_s, static_cast<size_t>(M), 0, 32, s) !=
+                hipSuccess)
+                return fail(TCA_ERR_HIP, "radix sort failed");
+            if (Mp > 0)
+                hipLaunchKernelGGL(dp_bounds_kernel, dim3(1), dim3(64), 0, s, keys_s, Mp, p->rows.wide_len, p->rows.row_len,
+                                   p->rows.multi_max, cnt);
+            if (hipMemcpyAsync(h_cnt, cnt, sizeof h_cnt, hipMemcpyDeviceToHost, s) != hipSuccess ||
+                hipStreamSynchronize(s) != hipSuccess)
+                return fail(TCA_ERR_HIP, "planning kernels failed");
+            // (cnt[3] held flags before the bounds kernel wrote it; with Mp == 0 it did not run)
+            if (Mp == 0) h_cnt[0] = h_cnt[1] = h_cnt[2] = h_cnt[3] = 0;
+            return TCA_OK;
+        };
         if (M > 0) {
             if ((st = dev_upload(&keys, nullptr, M)) || (st = dev_upload(&keys_s, nullptr, M)) ||
                 (st = dev_upload(&rows, nullptr, M)) || (st = dev_upload(&rows_s, nullptr, M)))
                 return bail(st);
-            hipLaunchKernelGGL(dp_lengths_kernel, grid_for(M), blk, 0, s, p->d_rowptr, M,
-                               p->mfma.windows.empty() ? nullptr : wmap, keys, rows);
-            size_t tmp_bytes = 0;
-            if (rocprim::radix_sort_pairs_desc(nullptr, tmp_bytes, keys, keys_s, rows, rows_s, static_cast<size_t>(M), 0, 32,
-                                               s) != hipSuccess)
-                return bail(fail(TCA_ERR_HIP, "radix sort sizing failed"));
-            if (dev_malloc(reinterpret_cast<void**>(&tmp), tmp_bytes) != hipSuccess)
-            return bail(fail(TCA_ERR_ALLOC, "radix sort workspace"));
-            if (rocprim::radix_sort_pairs_desc(tmp, tmp_bytes, keys, keys_s, rows, rows_s, static_cast<size_t>(M), 0, 32, s) !=
-                hipSuccess)
-                return bail(fail(TCA_ERR_HIP, "radix sort failed"));
-            if (Mp > 0)
-                hipLaunchKernelGGL(dp_bounds_kernel, dim3(1), dim3(64), 0, s, keys_s, Mp, p->rows.wide_len, p->rows.row_len,
-                                   p->rows.multi_max, cnt);
-        }
-        if (hipMemcpyAsync(h_cnt, cnt, sizeof h_cnt, hipMemcpyDeviceToHost, s) != hipSuccess ||
-            hipStreamSynchronize(s) != hipSuccess)
+            if ((st = sort_rows(nullptr))) return bail(st);
+            // Row panels from the first h_cnt[3] rows of the order (rows with
+            // nonzeros outside MFMA windows), as plan_panels takes them.
+            if (!p->mfma_short && (st = dpp.phase_a(p, keys_s, rows_s, h_cnt[3]))) return bail(st);
+            if (dpp.n_take > 0) {
+                Mp -= dpp.n_panel_rows;
+                // the panels keep their order (rows_s) until phase_b: sort a copy
+                int* prow_order = nullptr;
+                if ((st = dev_upload(&prow_order, nullptr, static_cast<size_t>(dpp.n_nz)))) return bail(st);
+                if (hipMemcpyAsync(prow_order, rows_s, sizeof(int) * static_cast<size_t>(dpp.n_nz), hipMemcpyDeviceToDevice,
+                                   s) != hipSuccess) {
+                    (void)hipFree(prow_order);
+                    return bail(fail(TCA_ERR_HIP, "panel order copy failed"));
+                }
+                dpp_rows = prow_order;
+                if ((st = sort_rows(dpp.in_panel))) return bail(st);
+            }
+        } else if (hipStreamSynchronize(s) != hipSuccess) {
             return bail(fail(TCA_ERR_HIP, "planning kernels failed"));
-        // (cnt[3] held flags before the bounds kernel wrote it; with Mp == 0 it did not run)
-        if (Mp == 0) h_cnt[0] = h_cnt[1] = h_cnt[2] = h_cnt[3] = 0;
+        }
         const int n_long = h_cnt[0], end_wide = h_cnt[1], end_row = h_cnt[2], end_nz = h_cnt[3];
         // segment slots of the long rows: exclusive sum of their segment counts
         int seg_total = 0;
@@ -1263,11 +1573,11 @@ int tca_spmm_plan_create_device(const int32_t* d_rowptr, const int32_t* d_colidx
         p->rows.n_seg = seg_total;
         p->rows.n_rowtasks = n_row;
         p->rows.n_multi = n_multi;
-        p->n_longrows = n_long;
-        p->n_seg_total = static_cast<size_t>(seg_total);
+        p->n_longrows = n_long + dpp.n_plongrows;  // the panels' long rows follow the row kernel's
+        p->n_seg_total = static_cast<size_t>(seg_total) + static_cast<size_t>(dpp.n_segments);
         p->n_perm = n_short;
         if ((st = dev_upload(&p->d_tasks, nullptr, p->ntasks)) || (st = dev_upload(&p->d_perm, nullptr, n_short)) ||
-            (st = dev_upload(&p->d_longrows, nullptr, n_long)) ||
+            (st = dev_upload(&p->d_longrows, nullptr, p->n_longrows)) ||
             (!(flags & TCA_PLAN_NO_SCRATCH) && (st = dev_upload(&p->d_partials, nullptr, p->n_seg_total * N))))
             return bail(st);
         if (Mp > 0) {
@@ -1320,6 +1630,7 @@ int tca_spmm_plan_create_device(const int32_t* d_rowptr, const int32_t* d_colidx
             hipLaunchKernelGGL(dp_order_seg_kernel, grid_for(ns), blk, 0, s, sidx_s, ns, b0, p->d_torder);
             p->n_torder = n_slots;
         }
+        if ((st = dpp.phase_b(p, dpp_rows, seg_total, n_long))) return bail(st);
         if (hipGetLastError() != hipSuccess || hipStreamSynchronize(s) != hipSuccess)
             return bail(fail(TCA_ERR_HIP, "task emission failed"));
         st = bail(TCA_OK);  // frees the temporaries only
@@ -1378,6 +1689,37 @@ int tca_spmm_plan_export_tiles(const tca_spmm_plan* p, int32_t* n_windows, int32
     *n_windows = nw;
     *n_entries = ne;
     *n_ucols = nu;
+    return TCA_OK;
+}
+
+int tca_spmm_plan_export_panels(const tca_spmm_plan* p, int64_t* sizes, int32_t* rows, uint32_t* boff, uint32_t* cnt,
+                                uint8_t* pos, int32_t* units, int32_t* order, int32_t* panel_units, int32_t* ustart,
+                                int32_t* longrows) {
+    if (!p || !sizes) return fail(TCA_ERR_INVALID, "tca_spmm_plan_export_panels: bad argument");
+    const bool on = p->n_units > 0;
+    const int64_t R = on ? p->panels.R : 0, P = on ? p->panels.P : 0;
+    const int64_t want[8] = {on ? p->panels.n_panels : 0, on ? p->n_ptiles : 0, on ? p->n_units : 0,
+                             on ? p->n_pblocks : 0, on ? p->n_plongrows : 0, R, P,
+                             on ? static_cast<int64_t>(p->n_pos_bytes) : 0};
+    if (rows) {
+        for (int k = 0; k < 5; k++)
+            if (sizes[k] < want[k]) return fail(TCA_ERR_INVALID, "tca_spmm_plan_export_panels: output buffers too small");
+        if (sizes[7] < want[7] || !boff || !cnt || !pos || !units || !order || !panel_units || !ustart || !longrows)
+            return fail(TCA_ERR_INVALID, "tca_spmm_plan_export_panels: output buffers too small");
+        auto get = [](void* dst, const void* src, size_t bytes) {
+            return bytes == 0 || hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost) == hipSuccess;
+        };
+        const size_t lr0 = static_cast<size_t>(p->n_longrows - p->n_plongrows);
+        if (!get(rows, p->d_prows, sizeof(int32_t) * want[0] * R) || !get(boff, p->d_pcols, sizeof(uint32_t) * want[1] * P) ||
+            !get(cnt, p->d_pcnt, sizeof(uint32_t) * want[1] * kPanelWaves * kPanelCntRows) ||
+            !get(pos, p->d_ppos, want[7]) || !get(units, p->d_units, sizeof(int4) * want[2]) ||
+            !get(order, p->d_porder, sizeof(int32_t) * want[3]) ||
+            !get(panel_units, p->d_panel_units, sizeof(int32_t) * want[0]) ||
+            !get(ustart, p->d_ustart, sizeof(int32_t) * want[2] * R) ||
+            !get(longrows, p->d_longrows + lr0, sizeof(int4) * want[4]))
+            return fail(TCA_ERR_HIP, "tca_spmm_plan_export_panels: copy failed");
+    }
+    for (int k = 0; k < 8; k++) sizes[k] = want[k];
     return TCA_OK;
 }
 

@@ -1,6 +1,7 @@
 """Planning on the GPU (tca_spmm_plan_create_device): the task list built by
 device kernels from a device-resident CSR equals the host planner's
-(TCA_PLAN_NO_MFMA) entry for entry, the matrix-core windows and their dense
+(TCA_PLAN_NO_MFMA | TCA_PLAN_NO_PANELS; panels: test_gpu_device_panels.py)
+entry for entry, the matrix-core windows and their dense
 tiles (natural and condensed) equal the host planner's for the same flags,
 and the plans give bit-identical products; invalid structures are rejected
 on the device."""
@@ -32,7 +33,7 @@ def test_device_plan_equals_host_plan(torch_cuda, name, a, n):
     print(f"device plan {name}: M={a.nrow} K={a.ncol} nnz={a.nnz} N={n}", flush=True)
     drp, dci = _dev(torch, a.rowptr), _dev(torch, a.colidx)
     with S.Plan(a, n, S.TCA_PLAN_NO_MFMA | S.TCA_PLAN_NO_PANELS) as hp:
-        dp = S.Plan.from_device(drp, dci, a.nrow, a.ncol, a.nnz, n, a.dtype, S.TCA_PLAN_NO_MFMA)
+        dp = S.Plan.from_device(drp, dci, a.nrow, a.ncol, a.nnz, n, a.dtype, S.TCA_PLAN_NO_MFMA | S.TCA_PLAN_NO_PANELS)
         try:
             ht, hperm, hl = hp.export_rows()
             dt, dperm, dl = dp.export_rows()
