@@ -236,15 +236,21 @@ int tca_spmm_24(const void* d_vals, const uint16_t* d_meta, int32_t M, int32_t K
  * for the routed windows, the dense tiles are laid out on the device: in
  * natural column order when the windows cover most of K (the host default,
  * TCA_TILES_DENSE_K), else condensed (TCA_TILES_DENSE; the host default
- * there is the paired kernel, whose layout only the host builds).  The
- * row-kernel task list of the other rows is built by device kernels (row
- * lengths, a stable descending radix sort, category bounds, a segment scan,
- * task emission).  With TCA_PLAN_NO_MFMA, TCA_PLAN_MFMA_DENSE (optionally
- * with TCA_PLAN_FORCE_MFMA), or by default when the windows cover most of K,
- * the plan equals the host planner's for the same flags, entry for entry.
- * TCA_PLAN_MFMA_PAIR gives TCA_ERR_UNSUPPORTED; panels are host-planned only;
- * window tables above 2^25 words (windows x ceil(K / 32)) leave every row on
- * the row kernel.  The structure is validated on the device
+ * there is the paired kernel, whose layout only the host builds).  The row
+ * panels of the other rows (the panel kernel) are planned on the device
+ * too: column unions of 192-row candidates in LDS bitmaps, the host's reuse
+ * rule on a few integers per candidate, tile cuts by a suffix minimum over
+ * union positions, counts, positions, units and their cursors per nonzero,
+ * the XCD launch order on the host from each unit's column span
+ * (tca_spmm_plan_export_panels reads them back).  The row-kernel task list
+ * of the remaining rows is built by device kernels (row lengths, a stable
+ * descending radix sort, category bounds, a segment scan, task emission).
+ * With TCA_PLAN_NO_MFMA, TCA_PLAN_MFMA_DENSE (optionally with
+ * TCA_PLAN_FORCE_MFMA), or by default when the windows cover most of K, the
+ * plan equals the host planner's for the same flags, entry for entry.
+ * TCA_PLAN_MFMA_PAIR gives TCA_ERR_UNSUPPORTED; window tables above 2^25
+ * words (windows x ceil(K / 32)) leave every row outside MFMA windows; K
+ * above 2^31 - 2^19 with panels gives TCA_ERR_UNSUPPORTED.  The structure is validated on the device
  * (TCA_ERR_INVALID as the host planner).  The plan copies the structure;
  * the caller's buffers may be freed after the call, which synchronises
  * `stream`.  Replaces reference workload_manager (src/our_spmm.cu:353-477),
