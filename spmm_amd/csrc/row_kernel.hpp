@@ -98,6 +98,45 @@ __device__ __forceinline__ void store_row(float* dst, const float (&v)[E]) {
     }
 }
 
+// C stores of lanes holding 32 bytes (E = 8: fp16 / bf16 B): lane g of a
+// slot holds 16-byte pieces 2g and 2g + 1 of the slot's chunk row, so two
+// plain store instructions would each fill half of every 128-byte line.
+// Instead the pieces are exchanged inside the slot (every lane active):
+// lane g receives piece g (from lane g / 2) for the first store and piece
+// g + cl (from lane (g + cl) / 2) for the second, so each store instruction
+// writes whole lines.  cl: lanes of the slot holding data.
+struct LinePieces {
+    f32x4 p0, p1;  // pieces g and g + cl of the chunk row
+};
+template <int E>
+__device__ __forceinline__ LinePieces line_pieces(const float (&v)[E], int lane, int g, int cl) {
+    static_assert(E == 8, "32-byte lanes");
+    const int base = lane - g;  // first lane of the slot
+    const int s1 = base + g / 2, s2 = base + (g + cl) / 2;
+    const bool odd1 = (g & 1) != 0, odd2 = ((g + cl) & 1) != 0;
+    LinePieces r;
+    float a[4], b[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const float lo1 = __shfl(v[e], s1), hi1 = __shfl(v[e + 4], s1);
+        const float lo2 = __shfl(v[e], s2), hi2 = __shfl(v[e + 4], s2);
+        a[e] = odd1 ? hi1 : lo1;
+        b[e] = odd2 ? hi2 : lo2;
+    }
+    r.p0 = f32x4{a[0], a[1], a[2], a[3]};
+    r.p1 = f32x4{b[0], b[1], b[2], b[3]};
+    return r;
+}
+// Stores pieces g and g + cl of a chunk row starting at `row` (column
+// chunk_col of the row); pieces past n_cols are not written.
+__device__ __forceinline__ void store_line_pieces(float* row, int chunk_col, int n_cols, int g, int cl,
+                                                  const LinePieces& p) {
+    if (chunk_col + 4 * g < n_cols)
+        __builtin_nontemporal_store(p.p0, reinterpret_cast<f32x4*>(row + chunk_col + 4 * g));
+    if (chunk_col + 4 * (g + cl) < n_cols)
+        __builtin_nontemporal_store(p.p1, reinterpret_cast<f32x4*>(row + chunk_col + 4 * (g + cl)));
+}
+
 template <typename T, int E>
 __device__ __forceinline__ void fma_pack(float (&acc)[E], float a, const Pack<T, E>& b) {
 #pragma unroll
@@ -244,7 +283,14 @@ __global__ __launch_bounds__(256) void row_kernel(RowArgs a) {
 #pragma unroll
             for (int u = 0; u < kRowUnroll; u++) fma_pack<T, E>(acc, av[u], bv[u]);
         }
-        if (row >= 0 && colok) store_row<E>(a.C + static_cast<size_t>(row) * a.N + col, acc);
+        if constexpr (E == 8) {
+            const LinePieces lp = line_pieces<E>(acc, lane, g, a.chunk_lanes);
+            if (row >= 0 && g < a.chunk_lanes)
+                store_line_pieces(a.C + static_cast<size_t>(row) * a.N, chunk * a.chunk_lanes * 8, a.N, g, a.chunk_lanes,
+                                  lp);
+        } else {
+            if (row >= 0 && colok) store_row<E>(a.C + static_cast<size_t>(row) * a.N + col, acc);
+        }
         return;
     }
 
@@ -265,18 +311,28 @@ __global__ __launch_bounds__(256) void row_kernel(RowArgs a) {
 #pragma unroll
             for (int e = 0; e < E; e++) red[wave][g * E + e] = acc[e];
         __syncthreads();
-        if (wave != 0 || slot != 0 || !colok) return;
+        if (wave != 0) return;
 #pragma unroll
         for (int e = 0; e < E; e++)
             acc[e] = ((red[0][g * E + e] + red[1][g * E + e]) + red[2][g * E + e]) + red[3][g * E + e];
-        store_row<E>(a.C + static_cast<size_t>(t.x) * a.N + col, acc);
+        if constexpr (E == 8) {
+            const LinePieces lp = line_pieces<E>(acc, lane, g, a.chunk_lanes);
+            if (slot == 0 && g < a.chunk_lanes)
+                store_line_pieces(a.C + static_cast<size_t>(t.x) * a.N, chunk * a.chunk_lanes * 8, a.N, g, a.chunk_lanes,
+                                  lp);
+        } else {
+            if (slot == 0 && colok) store_row<E>(a.C + static_cast<size_t>(t.x) * a.N + col, acc);
+        }
         return;
     }
-    if (slot != 0 || !colok) return;
-    if (t.w == 0)
-        store_row<E>(a.C + static_cast<size_t>(t.x) * a.N + col, acc);
-    else  // seg: partial row of segment slot t.w >> 2
-        store_row<E>(a.partials + static_cast<size_t>(t.w >> 2) * a.N + col, acc);
+    float* const dst_row = t.w == 0 ? a.C + static_cast<size_t>(t.x) * a.N
+                                    : a.partials + static_cast<size_t>(t.w >> 2) * a.N;  // seg: partial row of slot t.w >> 2
+    if constexpr (E == 8) {
+        const LinePieces lp = line_pieces<E>(acc, lane, g, a.chunk_lanes);
+        if (slot == 0 && g < a.chunk_lanes) store_line_pieces(dst_row, chunk * a.chunk_lanes * 8, a.N, g, a.chunk_lanes, lp);
+    } else {
+        if (slot == 0 && colok) store_row<E>(dst_row + col, acc);
+    }
 }
 
 // Lanes of seg_finalize_kernel per partial row: four columns each, a power
