@@ -187,7 +187,10 @@ enum { TCA_PHASE_PACK = 0, TCA_PHASE_TILES = 1, TCA_PHASE_ROWS = 2, TCA_PHASE_SE
  * shorter buffer in bounds), and when n_phase_ms > TCA_PHASE_RUN also
  * phase_ms[TCA_PHASE_RUN] = mean milliseconds of one whole run of the same
  * runs (hipEvents before the first and after the last, as tca_spmm_time), so
- * every phase of the output lies within its run time.  iters <= 100000.  No counterpart in the
+ * every phase of the output lies within its run time.  Dispatches that carry
+ * timestamps leave gaps of several microseconds between kernels (measured on
+ * MI355X: a 5.6 us single-kernel run takes 17.5 us), so that run time is not
+ * the SpMM's: tca_spmm_time gives it.  iters <= 100000.  No counterpart in the
  * reference, which times whole runs only (src/our_spmm.cu:553-576); this is
  * the per-kernel figure a roofline needs. */
 int tca_spmm_time_phases(const tca_spmm_plan* plan, const void* d_val, const void* d_B, float* d_C, void* stream,
