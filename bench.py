@@ -209,7 +209,13 @@ def measure(cfg: int, args, sha: str, headline: bool) -> dict:
         del src, dst
     torch.cuda.synchronize()
 
-    # Per-kernel durations first: K steps back to back on the launch stream,
+    # Clocks settle first: untimed steps for at least 0.15 s (a fresh GPU
+    # ramps its clocks over the first tens of milliseconds of load, which
+    # would otherwise slow whichever block below runs first).
+    est_ms = plan.time(val, bd, c, stream=stream.cuda_stream, warmup=1, iters=2)
+    plan.time(val, bd, c, stream=stream.cuda_stream, warmup=0, iters=max(args.warmup, min(20000, int(150.0 / max(est_ms, 1e-3)))))
+    torch.cuda.synchronize()
+    # Per-kernel durations: K steps back to back on the launch stream,
     # each kernel dispatched with start / stop timestamps of its own
     # (tca_spmm_time_phases), the roofline's kernel time.  Timestamped
     # dispatches add a gap of several microseconds between kernels (measured:
