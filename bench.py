@@ -215,15 +215,18 @@ def measure(cfg: int, args, sha: str, headline: bool) -> dict:
     est_ms = plan.time(val, bd, c, stream=stream.cuda_stream, warmup=1, iters=2)
     plan.time(val, bd, c, stream=stream.cuda_stream, warmup=0, iters=max(args.warmup, min(20000, int(150.0 / max(est_ms, 1e-3)))))
     torch.cuda.synchronize()
-    # Per-kernel durations: K steps back to back on the launch stream,
-    # each kernel dispatched with start / stop timestamps of its own
-    # (tca_spmm_time_phases), the roofline's kernel time.  Timestamped
+    # Per-kernel spans: K steps back to back on the launch stream, each
+    # kernel dispatched with start / stop timestamps of its own
+    # (tca_spmm_time_phases); they name the dominant kernel.  Timestamped
     # dispatches add a gap of several microseconds between kernels (measured:
-    # config 0 runs 17.5 us per step with them, 5.6 us without), so the step
-    # time does not come from those runs.
+    # config 0 runs 17.5 us per step with them, 5.6 us without), and a span
+    # of a few microseconds can hold the dispatch's own start-up, so neither
+    # the step time nor the roofline's kernel time comes from those runs.
     phase_run_ms, phases = plan.time_run_phases(val, bd, c, stream=stream.cuda_stream, warmup=args.warmup,
                                                 iters=args.steps)
     torch.cuda.synchronize()
+    dominant = max(phases, key=phases.get)
+    rest = [k for k in plan.phases() if k != dominant]
     # Timed region: W warm-up steps, then K steps between hipEvents recorded on
     # the launch stream (tca_spmm_time; the reference's protocol,
     # src/our_spmm.cu:553-576); wall clock around it as a cross-check.
@@ -231,10 +234,21 @@ def measure(cfg: int, args, sha: str, headline: bool) -> dict:
     ms_per_step = plan.time(val, bd, c, stream=stream.cuda_stream, warmup=args.warmup, iters=args.steps)
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - wall0) * 1e3
+    # The dominant kernel's share of the timed step: the step minus K steps
+    # of the plan's other phases alone, with the same plain launches
+    # (tca_spmm_time_subset); the whole step when it is the only phase.
+    rest_ms = plan.time_subset(val, bd, c, rest, stream=stream.cuda_stream, warmup=args.warmup,
+                               iters=args.steps) if rest else 0.0
+    torch.cuda.synchronize()
+    # C again holds the full product (the subset runs leave the dominant
+    # kernel's rows stale)
+    plan.run(val, bd, c, stream=stream.cuda_stream)
+    torch.cuda.synchronize()
     if not torch.isfinite(c).all().item():
         sys.exit(f"config {cfg}: non-finite output")
-    log("phases (ms):", json.dumps(phases), "timestamped run", phase_run_ms, "step", ms_per_step)
-    dominant = max(phases, key=phases.get)
+    dom_ms = ms_per_step - rest_ms
+    log("phases (ms):", json.dumps(phases), "timestamped run", phase_run_ms, "step", ms_per_step,
+        "other phases alone", rest_ms, "->", dominant, dom_ms)
 
     s_a = 4 if a.dtype == S.TCA_F32 else 2
     m, k, nnz = a.nrow, a.ncol, a.nnz
@@ -253,13 +267,14 @@ def measure(cfg: int, args, sha: str, headline: bool) -> dict:
         rows_k = m - info["rows_mfma"] - info["rows_panels"]
         nnz_k = nnz - info["nnz_mfma"] - info["nnz_panels"]
     bytes_dom = 4 * (rows_k + 1) + nnz_k * (4 + s_a) + k * n * s_a + rows_k * n * 4
-    dom_ms = phases[dominant]
     achieved = bytes_dom / (dom_ms * 1e-3) / 1e9
     kernel_name = phase_kernel(dominant, info["tile_kernel"])
     traffic, traffic_src = measured_traffic(cfg, kernel_name, sha)
     log(f"config {cfg}: {ms_per_step * 1e3:.2f} us/step, wall {wall_ms:.2f} ms for {args.warmup}+{args.steps} steps")
     roofline = {"bound": "hbm", "kernel": kernel_name, "bytes_alg": bytes_dom,
                 "kernel_us": round(dom_ms * 1e3, 3), "step_us": round(ms_per_step * 1e3, 3),
+                "other_phases_us": round(rest_ms * 1e3, 3),
+                "kernel_us_timestamped": round(phases[dominant] * 1e3, 3),
                 "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": traffic,
                 # measured L2 <-> fabric bytes of the same launch over its time (HBM or MALL)
@@ -272,7 +287,7 @@ def measure(cfg: int, args, sha: str, headline: bool) -> dict:
                 "ms_per_step": round(ms_per_step, 6), "ms_per_step_timestamped": round(phase_run_ms, 6),
                 "gflops": round(gflops, 3), "bytes_alg": bytes_alg,
                 "hbm_gbs_whole_step": round(hbm_gbs, 2),
-                "phases_us": {kk: round(v * 1e3, 3) for kk, v in phases.items()},
+                "phases_us_timestamped": {kk: round(v * 1e3, 3) for kk, v in phases.items()},
                 "tile_kernel": TILE_KERNELS.get(info["tile_kernel"], "none"), "roofline": roofline}
 
     # Cold-cache SpMM: L2s and MALL flushed by writing a 512 MiB buffer
@@ -347,7 +362,7 @@ def measure(cfg: int, args, sha: str, headline: bool) -> dict:
                    "plan_ms": round(info["plan_ms"], 3),
                    **({"plan_on_gpu": True, "plan_first_ms": round(plan_first_ms, 3)} if plan_first_ms is not None
                       else {}),
-                   "phases_us": {kk: round(v * 1e3, 3) for kk, v in phases.items()},
+                   "phases_us_timestamped": {kk: round(v * 1e3, 3) for kk, v in phases.items()},
                    "cold_cache_us": round(cold_ms * 1e3, 3), "launch_floor_us": round(floor_ms * 1e3, 3),
                    "mfma_windows": info["n_windows_mfma"], "rows_mfma": info["rows_mfma"],
                    "panels": info["n_panels"], "panel_units": info["n_panel_units"],

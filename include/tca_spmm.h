@@ -196,6 +196,19 @@ enum { TCA_PHASE_PACK = 0, TCA_PHASE_TILES = 1, TCA_PHASE_ROWS = 2, TCA_PHASE_SE
 int tca_spmm_time_phases(const tca_spmm_plan* plan, const void* d_val, const void* d_B, float* d_C, void* stream,
                          int32_t warmup, int32_t iters, float* phase_ms, int32_t n_phase_ms);
 
+/* Timing of a subset of a run's phases: `warmup`, then `iters` runs of only
+ * the phases whose bit (1 << TCA_PHASE_*) is set in phase_mask, in run
+ * order, back to back between two hipEvents on `stream`; *avg_ms = mean
+ * milliseconds per run.  C holds a full product only when every phase the
+ * plan uses is in the mask.  With the full mask it is tca_spmm_time; without
+ * one phase, the difference to the full time is that phase's share of the
+ * timed step (how bench.py times the roofline's kernel).  No counterpart in
+ * the reference (src/our_spmm.cu:553-576 times whole runs). */
+int tca_spmm_time_subset(const tca_spmm_plan* plan, const void* d_val, const void* d_B, float* d_C, void* stream,
+                         uint32_t phase_mask, int32_t warmup, int32_t iters, float* avg_ms);
+/* The phases the plan runs: bit 1 << TCA_PHASE_* set for each. */
+int tca_spmm_plan_phases(const tca_spmm_plan* plan, uint32_t* phase_mask);
+
 /* Backward-pass kernels of the PyTorch op (no counterpart in the reference,
  * which has no backward pass).
  *

@@ -584,8 +584,8 @@ class Plan:
     def time_phases(self, val, b, c, stream=None, warmup: int = 5, iters: int = 10) -> dict:
         """Mean milliseconds of each phase (MFMA value pack, MFMA tiles, row
         kernel, segment sums of split rows, panel kernel) inside whole runs:
-        `iters` runs back to back on the stream, hipEvents recorded between
-        their kernels."""
+        `iters` runs back to back on the stream, each phase's kernel
+        dispatched with start / stop timestamps of its own."""
         ms = (ctypes.c_float * (len(self.PHASES) + 1))()
         call("tca_spmm_time_phases", self._p, _addr(val), _addr(b), _addr(c),
              _addr(stream) if stream is not None else None, warmup, iters, ms, len(self.PHASES))
@@ -600,6 +600,25 @@ class Plan:
         call("tca_spmm_time_phases", self._p, _addr(val), _addr(b), _addr(c),
              _addr(stream) if stream is not None else None, warmup, iters, ms, n)
         return float(ms[n - 1]), {k: float(ms[i]) for i, k in enumerate(self.PHASES)}
+
+    def phases(self) -> tuple:
+        """Names of the phases in which the plan launches a kernel, in run order."""
+        m = ctypes.c_uint32()
+        call("tca_spmm_plan_phases", self._p, ctypes.byref(m))
+        return tuple(k for k in ("pack", "tiles", "panels", "rows", "segments")
+                     if m.value & (1 << self.PHASES.index(k)))
+
+    def time_subset(self, val, b, c, phases, stream=None, warmup: int = 5, iters: int = 10) -> float:
+        """Mean milliseconds of runs that launch only the named phases, back to
+        back between two hipEvents (tca_spmm_time_subset); C holds a full
+        product only when every phase the plan uses is named."""
+        mask = 0
+        for k in phases:
+            mask |= 1 << self.PHASES.index(k)
+        ms = ctypes.c_float()
+        call("tca_spmm_time_subset", self._p, _addr(val), _addr(b), _addr(c),
+             _addr(stream) if stream is not None else None, mask, warmup, iters, ctypes.byref(ms))
+        return ms.value
 
     def close(self) -> None:
         if self._p:

@@ -89,6 +89,8 @@ SIGNATURES = {
     "tca_spmm_run": (i32, [vp, vp, vp, vp, vp]),
     "tca_spmm_time": (i32, [vp, vp, vp, vp, vp, i32, i32, f32p]),
     "tca_spmm_time_phases": (i32, [vp, vp, vp, vp, vp, i32, i32, f32p, i32]),
+    "tca_spmm_time_subset": (i32, [vp, vp, vp, vp, vp, u32, i32, i32, f32p]),
+    "tca_spmm_plan_phases": (i32, [vp, u32p]),
     "tca_spmm_run_static": (i32, [vp, vp, vp, vp, vp]),
     "tca_sddmm": (i32, [vp, vp, vp, vp, vp]),
     "tca_launch_floor": (i32, [vp, i32, f32p]),

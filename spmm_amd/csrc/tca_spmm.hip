@@ -446,17 +446,31 @@ int launch_panels(const tca_spmm_plan* p, const void* val, const void* B, float*
     }
 }
 
+// Bit 1 << TCA_PHASE_* for each phase in which the plan launches a kernel.
+uint32_t phases_used(const tca_spmm_plan* p) {
+    uint32_t m = 0;
+    if (!p->mfma.windows.empty() && (!p->mfma.entries.empty() || p->n_dn > 0)) m |= 1u << TCA_PHASE_PACK;
+    if (!p->mfma.windows.empty() || p->mfma_short) m |= 1u << TCA_PHASE_TILES;
+    if (p->ntasks > 0) m |= 1u << TCA_PHASE_ROWS;
+    if (p->n_longrows > 0) m |= 1u << TCA_PHASE_SEGMENTS;
+    if (p->n_units > 0) m |= 1u << TCA_PHASE_PANELS;
+    return m;
+}
+
 // One SpMM in stream order: pack, tile kernel, panel kernel, row kernel, segment sums.
 // W: the partial rows of split rows (plan-owned, or the static scratch).
-int run_phases(const tca_spmm_plan* p, const void* val, const void* B, float* C, float* W, hipStream_t s) {
-    launch_pack(p, val, s);
-    int st = launch_mfma(p, val, B, C, s);
+// mask: the phases to launch (bit 1 << TCA_PHASE_*); all of them for a product.
+int run_phases(const tca_spmm_plan* p, const void* val, const void* B, float* C, float* W, hipStream_t s,
+               uint32_t mask = ~0u) {
+    if (mask & (1u << TCA_PHASE_PACK)) launch_pack(p, val, s);
+    int st = TCA_OK;
+    if (mask & (1u << TCA_PHASE_TILES)) st = launch_mfma(p, val, B, C, s);
     if (st) return st;
-    st = launch_panels(p, val, B, C, W, s);
+    if (mask & (1u << TCA_PHASE_PANELS)) st = launch_panels(p, val, B, C, W, s);
     if (st) return st;
-    st = launch_rows(p, val, B, C, W, s);
+    if (mask & (1u << TCA_PHASE_ROWS)) st = launch_rows(p, val, B, C, W, s);
     if (st) return st;
-    launch_finalize(p, C, W, s);
+    if (mask & (1u << TCA_PHASE_SEGMENTS)) launch_finalize(p, C, W, s);
     return TCA_OK;
 }
 
@@ -1736,9 +1750,8 @@ int tca_spmm_plan_destroy(tca_spmm_plan* plan) {
     return TCA_OK;
 }
 
-int tca_spmm_run(const tca_spmm_plan* p, const void* d_val, const void* d_B, float* d_C, void* stream) {
-    if (!p) return fail(TCA_ERR_INVALID, "plan is NULL");
-    if (p->M == 0) return TCA_OK;
+// Operand checks of tca_spmm_run (p non-NULL, M > 0).
+static int check_run_operands(const tca_spmm_plan* p, const void* d_val, const void* d_B, const float* d_C) {
     if ((p->nnz > 0 && (!d_val || !d_B)) || !d_C) return fail(TCA_ERR_INVALID, "NULL device pointer");
     const size_t vb = static_cast<size_t>(p->rows.elems_per_lane) * dtype_size(p->dtype);
     if (reinterpret_cast<uintptr_t>(d_B) % vb != 0)
@@ -1748,8 +1761,16 @@ int tca_spmm_run(const tca_spmm_plan* p, const void* d_val, const void* d_B, flo
         return fail(TCA_ERR_INVALID, "values misaligned");
     if (p->n_seg_total > 0 && !p->d_partials)
         return fail(TCA_ERR_INVALID, "plan was created with TCA_PLAN_NO_SCRATCH: run it with tca_spmm_run_static");
+    return TCA_OK;
+}
+
+int tca_spmm_run(const tca_spmm_plan* p, const void* d_val, const void* d_B, float* d_C, void* stream) {
+    if (!p) return fail(TCA_ERR_INVALID, "plan is NULL");
+    if (p->M == 0) return TCA_OK;
+    int st = check_run_operands(p, d_val, d_B, d_C);
+    if (st) return st;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    const int st = run_phases(p, d_val, d_B, d_C, p->d_partials, s);
+    st = run_phases(p, d_val, d_B, d_C, p->d_partials, s);
     if (st) return st;
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(TCA_ERR_HIP, "kernel launch: %s", hipGetErrorString(e));
@@ -1943,6 +1964,44 @@ int tca_gather_values(const int32_t* d_perm, int32_t n, const void* d_val, int32
     return TCA_OK;
 }
 
+int tca_spmm_time_subset(const tca_spmm_plan* p, const void* d_val, const void* d_B, float* d_C, void* stream,
+                         uint32_t phase_mask, int32_t warmup, int32_t iters, float* avg_ms) {
+    if (!p || !avg_ms || iters < 1 || warmup < 0 || (phase_mask & ~((1u << TCA_PHASES) - 1u)))
+        return fail(TCA_ERR_INVALID, "tca_spmm_time_subset: bad argument");
+    *avg_ms = 0.f;
+    if (p->M == 0) return TCA_OK;
+    int st = check_run_operands(p, d_val, d_B, d_C);
+    if (st) return st;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    for (int i = 0; i < warmup && st == TCA_OK; i++) st = run_phases(p, d_val, d_B, d_C, p->d_partials, s, phase_mask);
+    if (st) return st;
+    hipEvent_t e0, e1;
+    TCA_HIP_TRY(hipEventCreate(&e0));
+    if (hipEventCreate(&e1) != hipSuccess) {
+        (void)hipEventDestroy(e0);
+        return fail(TCA_ERR_HIP, "hipEventCreate failed");
+    }
+    if (hipEventRecord(e0, s) != hipSuccess) st = fail(TCA_ERR_HIP, "hipEventRecord failed");
+    for (int i = 0; i < iters && st == TCA_OK; i++) st = run_phases(p, d_val, d_B, d_C, p->d_partials, s, phase_mask);
+    float ms = 0.f;
+    if (st == TCA_OK && (hipEventRecord(e1, s) != hipSuccess || hipEventSynchronize(e1) != hipSuccess ||
+                         hipEventElapsedTime(&ms, e0, e1) != hipSuccess))
+        st = fail(TCA_ERR_HIP, "event timing failed");
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    if (st) return st;
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(TCA_ERR_HIP, "kernel launch: %s", hipGetErrorString(e));
+    *avg_ms = ms / static_cast<float>(iters);
+    return TCA_OK;
+}
+
+int tca_spmm_plan_phases(const tca_spmm_plan* p, uint32_t* phase_mask) {
+    if (!p || !phase_mask) return fail(TCA_ERR_INVALID, "tca_spmm_plan_phases: bad argument");
+    *phase_mask = phases_used(p);
+    return TCA_OK;
+}
+
 int tca_spmm_time_phases(const tca_spmm_plan* p, const void* d_val, const void* d_B, float* d_C, void* stream,
                          int32_t warmup, int32_t iters, float* phase_ms, int32_t n_phase_ms) {
     if (!p || !phase_ms || n_phase_ms < 1 || iters < 1 || iters > 100000 || warmup < 0)
@@ -1956,12 +2015,7 @@ int tca_spmm_time_phases(const tca_spmm_plan* p, const void* d_val, const void* 
     }
     if (p->M == 0) return TCA_OK;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    bool used[TCA_PHASES];
-    used[TCA_PHASE_PACK] = !p->mfma.windows.empty() && (!p->mfma.entries.empty() || p->n_dn > 0);
-    used[TCA_PHASE_TILES] = !p->mfma.windows.empty() || p->mfma_short;
-    used[TCA_PHASE_ROWS] = p->ntasks > 0;
-    used[TCA_PHASE_SEGMENTS] = p->n_longrows > 0;
-    used[TCA_PHASE_PANELS] = p->n_units > 0;
+    const uint32_t used = phases_used(p);
     // `iters` whole runs back to back, in run_phases' launch order; each
     // phase's one kernel is dispatched with a start and a stop event of its
     // own (TCA_PHASE_LAUNCH), so nothing is inserted between the kernels and
@@ -2006,7 +2060,7 @@ int tca_spmm_time_phases(const tca_spmm_plan* p, const void* d_val, const void* 
     double sum[TCA_PHASES] = {0, 0, 0, 0, 0};
     for (int i = 0; i < iters && st == TCA_OK; i++)
         for (int k = 0; k < TCA_PHASES && st == TCA_OK; k++) {
-            if (!used[k]) continue;
+            if (!(used & (1u << k))) continue;
             float ms = 0.f;
             const size_t at = (static_cast<size_t>(i) * TCA_PHASES + k) * 2;
             if (hipEventElapsedTime(&ms, ev[at], ev[at + 1]) != hipSuccess) st = fail(TCA_ERR_HIP, "event timing failed");
@@ -2019,7 +2073,7 @@ int tca_spmm_time_phases(const tca_spmm_plan* p, const void* d_val, const void* 
     if (r0) (void)hipEventDestroy(r0);
     if (r1) (void)hipEventDestroy(r1);
     if (st != TCA_OK) return st;
-    for (int k = 0; k < n_out; k++) phase_ms[k] = used[k] ? static_cast<float>(sum[k] / iters) : 0.f;
+    for (int k = 0; k < n_out; k++) phase_ms[k] = (used & (1u << k)) ? static_cast<float>(sum[k] / iters) : 0.f;
     if (n_phase_ms > TCA_PHASE_RUN) phase_ms[TCA_PHASE_RUN] = run_ms / static_cast<float>(iters);
     return TCA_OK;
 }

@@ -11,6 +11,7 @@ Bars:
   be <= 1e-3 for every element, where S = sum_j |a_j * b_j| of that element
   (the floor makes outputs that cancel to ~0 compare on the scale of their
   terms; any wrong or missing term of ordinary size still fails it)."""
+import ctypes
 import os
 
 import numpy as np
@@ -423,6 +424,49 @@ def test_phase_timing_reports_the_kernels_a_plan_uses(torch_cuda):
             ph = pl.time_phases(val, bd, c, warmup=1, iters=3)
             if pl.info()["n_long_rows"] > 0:  # rows split over several units or segments
                 used = used | {"segments"}
+            named = pl.phases()
         torch.cuda.synchronize()
         assert {k for k, v in ph.items() if v > 0} == used, (flags, ph)
+        assert set(named) == used and list(named) == [k for k in ("pack", "tiles", "panels", "rows", "segments")
+                                                      if k in used], (flags, named)
         assert np.array_equal(c.cpu().numpy(), oracle_c(a, b))
+
+
+def test_subset_timing_runs_only_the_named_phases(torch_cuda):
+    """tca_spmm_time_subset: with every phase of the plan C holds the exact
+    product; with all but the first phase the rows of that phase stay as they
+    were (NaN here) while the other rows are exact; an empty subset launches
+    nothing; a mask bit beyond the phases is rejected."""
+    torch = torch_cuda
+    rng = np.random.default_rng(98)
+    a, _ = S.gen_bernoulli(256, 512, 0.08, seed=10, dtype=S.TCA_F16)
+    a = S.CSR(a.nrow, a.ncol, a.rowptr, a.colidx, S.to_storage(exact_values(rng, a.nnz), S.TCA_F16), S.TCA_F16)
+    b = S.to_storage(exact_dense(rng, (512, 256)), S.TCA_F16)
+    dev = torch.device("cuda:0")
+    val = torch.from_numpy(a.values.view(np.int16)).to(dev)
+    bd = torch.from_numpy(b.view(np.int16)).to(dev)
+    want = oracle_c(a, b)
+    # MFMA windows on the leading rows, the row kernel on the rest
+    flags = S.TCA_PLAN_FORCE_MFMA | S.TCA_PLAN_MFMA_DENSE
+    with S.Plan(a, 256, flags) as pl:
+        phases = pl.phases()
+        assert phases[:2] == ("pack", "tiles"), phases
+        c = torch.full((a.nrow, 256), float("nan"), dtype=torch.float32, device=dev)
+        assert pl.time_subset(val, bd, c, phases, warmup=1, iters=3) > 0
+        torch.cuda.synchronize()
+        assert np.array_equal(c.cpu().numpy(), want)
+        c.fill_(float("nan"))
+        assert pl.time_subset(val, bd, c, (), warmup=1, iters=2) >= 0
+        torch.cuda.synchronize()
+        assert torch.isnan(c).all().item()
+        if "rows" in phases:
+            pl.time_subset(val, bd, c, ("rows",) + (("segments",) if "segments" in phases else ()), warmup=0, iters=1)
+            torch.cuda.synchronize()
+            got = c.cpu().numpy()
+            done = ~np.isnan(got).any(axis=1)
+            assert done.any() and not done.all()
+            assert np.array_equal(got[done], want[done])
+        with pytest.raises(S.TcaError) as ei:
+            S._lib.call("tca_spmm_time_subset", pl._p, val.data_ptr(), bd.data_ptr(), c.data_ptr(), None,
+                        1 << len(S.Plan.PHASES), 0, 1, ctypes.byref(ctypes.c_float()))
+        assert ei.value.status == 1
