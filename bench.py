@@ -67,17 +67,21 @@ def source_sha() -> str:
 
 
 def measured_traffic(config: int, kernel: str, sha: str):
-    """(bytes per launch, profile file) for this config and kernel at these sources, else (None, None)."""
+    """The profile entry for this config and kernel at these sources:
+    {"bytes": L2<->fabric bytes per launch, "dram_read" / "dram_write":
+    DRAM-destined bytes per launch (MALL hits included), "profile": file},
+    or None."""
     try:
         with open(TRAFFIC_JSON) as fh:
             entries = json.load(fh)["entries"]
     except (OSError, ValueError, KeyError):
-        return None, None
+        return None
     for e in entries:
         if e["config"] == config and e["kernel"] == kernel and e["source_sha"] == sha:
             kib = e["fetch_kib"] * e["fetch_scale"] + e["write_kib"] * e["write_scale"]
-            return int(round(kib * 1024)), e["profile"]
-    return None, None
+            return {"bytes": int(round(kib * 1024)), "dram_read": e.get("dram_read_bytes"),
+                    "dram_write": e.get("dram_write_bytes"), "profile": e["profile"]}
+    return None
 
 
 def log(*a):
@@ -269,7 +273,8 @@ def measure(cfg: int, args, sha: str, headline: bool) -> dict:
     bytes_dom = 4 * (rows_k + 1) + nnz_k * (4 + s_a) + k * n * s_a + rows_k * n * 4
     achieved = bytes_dom / (dom_ms * 1e-3) / 1e9
     kernel_name = phase_kernel(dominant, info["tile_kernel"])
-    traffic, traffic_src = measured_traffic(cfg, kernel_name, sha)
+    tr = measured_traffic(cfg, kernel_name, sha) or {}
+    traffic = tr.get("bytes")
     log(f"config {cfg}: {ms_per_step * 1e3:.2f} us/step, wall {wall_ms:.2f} ms for {args.warmup}+{args.steps} steps")
     roofline = {"bound": "hbm", "kernel": kernel_name, "bytes_alg": bytes_dom,
                 "kernel_us": round(dom_ms * 1e3, 3), "step_us": round(ms_per_step * 1e3, 3),
@@ -279,7 +284,10 @@ def measure(cfg: int, args, sha: str, headline: bool) -> dict:
                 "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": traffic,
                 # measured L2 <-> fabric bytes of the same launch over its time (HBM or MALL)
                 "traffic_gbs": round(traffic / (dom_ms * 1e-3) / 1e9, 2) if traffic else None,
-                "traffic_profile": traffic_src, "source_sha": sha}
+                # requests addressed to HBM from the same profile (TCC_EA0_RDREQ_DRAM x 128 B,
+                # TCC_EA0_WRREQ_DRAM x 64 B): MALL hits are among them, so an upper bound on HBM bytes
+                "dram_read_bytes": tr.get("dram_read"), "dram_write_bytes": tr.get("dram_write"),
+                "traffic_profile": tr.get("profile"), "source_sha": sha}
     dtype = "f32" if a.dtype == S.TCA_F32 else ("f16" if a.dtype == S.TCA_F16 else "bf16") + "->f32acc"
     if not headline:
         plan.close()
