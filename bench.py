@@ -5,14 +5,17 @@ and C resident in HBM before the timed region starts.  Headline workload:
 benchmark configuration 2, the largest one that fits one GPU (GCN
 aggregation: symmetric R-MAT graph with 232,965 nodes and ~114.8M nonzeros
 including self-loops, D^-1/2 (A+I) D^-1/2 in fp32, B 232,965 x 128 fp32).
-The other four configurations are timed in the same run and reported under
-config.other_configs.  Prints ONE JSON line.
+The other four configurations are timed in the same run, each in a child
+process of its own (as `--config c --no-others` would time it: a fresh
+device allocator, so no configuration runs on memory another one left
+behind), and reported under config.other_configs.  Prints ONE JSON line.
 
     python bench.py [--steps K] [--warmup W] [--config 0..4] [--gpus 1] [--no-others] [--no-cpu]
 """
 import argparse
 import json
 import os
+import subprocess
 import sys
 import time
 
@@ -126,11 +129,35 @@ def main():
                          "row tasks, row panels, dense MFMA tiles) instead of the host planner")
     ap.add_argument("--sparse24", action="store_true",
                     help="time the 2:4 sparse-MFMA kernel (tca_spmm_24) on A pruned to 2:4 (fp16 / bf16 configurations)")
+    ap.add_argument("--short-record", action="store_true",
+                    help="print the short record of --config (what config.other_configs holds) instead of the bench line")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
               file=sys.stderr)
         sys.exit(2)
+
+    # The other configurations first, each in a child process of its own
+    # (a fresh device allocator: measured in one process after other
+    # configurations, a configuration's buffers land on blocks the earlier
+    # ones left in torch's cache, which made config 3 5 % faster and config 4
+    # 5 % slower than after an emptied cache), started before this process
+    # touches the GPU.
+    others = {}
+    if not (args.no_others or args.short_record or args.bell or args.sparse24):
+        base = [sys.executable, os.path.abspath(__file__), "--short-record", "--steps", str(args.steps),
+                "--warmup", str(args.warmup), "--seed", str(args.seed), "--flags", str(args.flags)]
+        if args.device_plan:
+            base.append("--device-plan")
+        for cfg in range(5):
+            if cfg == args.config:
+                continue
+            out = subprocess.run(base + ["--config", str(cfg)], stdout=subprocess.PIPE, text=True)
+            if out.returncode != 0:
+                sys.exit(f"config {cfg}: child run failed with status {out.returncode}")
+            r = json.loads([ln for ln in out.stdout.splitlines() if ln.startswith("{")][-1])
+            others[str(cfg)] = r
+            log(f"config {cfg}:", json.dumps(r))
 
     import torch
 
@@ -143,15 +170,11 @@ def main():
         return
 
     sha = source_sha()
+    if args.short_record:
+        print(json.dumps(measure(args.config, args, sha, headline=False)), flush=True)
+        return
     head = measure(args.config, args, sha, headline=True)
-    others = {}
-    if not args.no_others:
-        for cfg in range(5):
-            if cfg != args.config:
-                r = measure(cfg, args, sha, headline=False)
-                others[str(cfg)] = r
-                log(f"config {cfg}:", json.dumps(r))
-    head["config"]["other_configs"] = others
+    head["config"]["other_configs"] = {k: others[k] for k in sorted(others)}
     print(json.dumps(head), flush=True)
 
 
