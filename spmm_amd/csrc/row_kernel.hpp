@@ -237,6 +237,21 @@ __global__ __launch_bounds__(256) void row_kernel(RowArgs a) {
     for (int e = 0; e < E; e++) acc[e] = 0.f;
 
     if (t.w == 1 && t.z == 0) {  // zero task: clear the C rows of up to kZeroRows empty rows
+        // A task's rows ascend (the planners keep the empty rows of the
+        // longest-first order in row order), so when its first and last
+        // differ by its count less one they are consecutive and, with one
+        // column chunk, their C rows are one contiguous range: cleared 16
+        // bytes per lane, 1 KiB per store instruction.
+        if (a.col_chunks == 1 && (a.N & 3) == 0) {
+            const int r0 = a.perm[t.x];
+            if (a.perm[t.x + t.y - 1] - r0 == t.y - 1) {
+                f32x4* const base = reinterpret_cast<f32x4*>(a.C + static_cast<size_t>(r0) * a.N);
+                const int n4 = t.y * (a.N >> 2);
+                const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+                for (int o = lane; o < n4; o += 64) __builtin_nontemporal_store(z, base + o);
+                return;
+            }
+        }
         const int step = 1 << logS;
         if constexpr (E == 8) {
             // 32 bytes per lane: lane g clears 16-byte pieces g and g + chunk

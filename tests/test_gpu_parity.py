@@ -329,6 +329,26 @@ def test_empty_and_degenerate(torch_cuda):
     assert np.array_equal(run_gpu(torch_cuda, a, b), oracle_c(a, b))
 
 
+@pytest.mark.parametrize("dtype,n", [(S.TCA_F16, 64), (S.TCA_F32, 128), (S.TCA_F32, 7), (S.TCA_BF16, 1000)],
+                         ids=["f16-n64", "f32-n128", "f32-n7", "bf16-n1000-chunks"])
+def test_runs_of_empty_rows(torch_cuda, dtype, n):
+    """Empty rows in long consecutive runs (zero tasks whose rows are one
+    contiguous range of C, cleared as one range) and scattered ones (the
+    row-by-row clear), between rows with nonzeros; N not a multiple of 4 and
+    several column chunks keep the row-by-row clear.  C starts as NaN, so
+    every row must be written."""
+    rng = np.random.default_rng(61 + n)
+    lens = np.zeros(6000, np.int64)
+    lens[::97] = rng.integers(1, 40, len(lens[::97]))   # long runs of empty rows between them
+    lens[3000:3300:2] = rng.integers(1, 5, 150)          # a stretch of alternating rows
+    lens[5999] = 3
+    k = 500
+    a = make_csr(rng, lens, k, dtype)
+    b = S.to_storage(exact_dense(rng, (k, n)), dtype)
+    got = run_gpu(torch_cuda, a, b, S.TCA_PLAN_NO_MFMA | S.TCA_PLAN_NO_PANELS)
+    assert np.array_equal(got, oracle_c(a, b))
+
+
 def test_misaligned_b_is_rejected(torch_cuda):
     torch = torch_cuda
     rng = np.random.default_rng(51)

@@ -377,8 +377,9 @@ def test_plan_covers_every_row_once(n, dtype):
             covered[x] += 1
         elif w == 1:
             rows = perm[x:x + y]
-            if z == 0:  # zero task: empty rows only
+            if z == 0:  # zero task: empty rows only, ascending (the kernel clears consecutive ones as one range)
                 assert 1 <= y <= 64 and np.all(lens[rows] == 0)
+                assert np.all(np.diff(rows) > 0)
             else:
                 assert 1 <= y <= 64 // g and np.all(lens[rows] > 0)
                 assert z == lens[rows].max() and z <= geo["multi_max"]
