@@ -6,7 +6,8 @@
 //   [0, 4 W)              the 4 quarters of the W wide rows,
 //   [4 W, 4 W + S)        the segments of the long rows (S in all),
 //   [4 W + S, .. + R)     one task per medium row,
-//   then                  groups of `slots` consecutive short rows.
+//   then                  groups of multi_group_rows(slots) consecutive short
+//                         rows, and groups of kZeroRows empty rows.
 // Long rows come first in the order, then wide, medium and short rows, so
 // the category boundaries are three positions in the sorted lengths.  The
 // sort keys are length + 1, and 0 for the rows of the windows routed to the
@@ -99,7 +100,7 @@ struct DpEmitArgs {
     int4* tasks;
     int* perm;
     int4* longrows;
-    int M, n_long, end_wide, end_row, end_nz, slots, seg_total;  // M: the rows planned (Mp)
+    int M, n_long, end_wide, end_row, end_nz, group, seg_total;  // M: the rows planned (Mp); group: rows per multi task
 };
 
 // Every row of the order writes its own tasks (see the file comment).
@@ -126,17 +127,17 @@ __global__ void dp_emit_kernel(DpEmitArgs a) {
         } else if (i < a.end_row) {
             a.tasks[4 * n_wide + a.seg_total + (i - a.end_wide)] = make_int4(r, beg, beg + static_cast<int>(L), kTaskRow);
         } else {
-            // short rows in groups of `slots`, then empty rows in groups of kZeroRows
+            // short rows in groups of `group`, then empty rows in groups of kZeroRows
             const int k = i - a.end_row;
             a.perm[k] = r;
             const int base = 4 * n_wide + a.seg_total + (a.end_row - a.end_wide);
             if (i < a.end_nz) {
-                if (k % a.slots == 0)
-                    a.tasks[base + k / a.slots] = make_int4(k, min(a.slots, a.end_nz - i), static_cast<int>(L), kTaskMulti);
+                if (k % a.group == 0)
+                    a.tasks[base + k / a.group] = make_int4(k, min(a.group, a.end_nz - i), static_cast<int>(L), kTaskMulti);
             } else {
                 const int k0 = i - a.end_nz;
                 if (k0 % kZeroRows == 0)
-                    a.tasks[base + (a.end_nz - a.end_row + a.slots - 1) / a.slots + k0 / kZeroRows] =
+                    a.tasks[base + (a.end_nz - a.end_row + a.group - 1) / a.group + k0 / kZeroRows] =
                         make_int4(k, min(kZeroRows, a.M - i), 0, kTaskMulti);
             }
         }

@@ -130,13 +130,15 @@ void plan_rows(const int32_t* rowptr, int32_t M, int32_t N, int32_t es, const st
         p->tasks.push_back({r, rowptr[r], rowptr[r + 1], kTaskRow});
     }
     p->n_rowtasks = static_cast<int32_t>(p->tasks.size()) - p->n_seg - p->n_wide;
-    // Short rows: groups of `slots` rows of similar length; empty rows (the
-    // tail of the order) in groups of kZeroRows, which only clear their C rows.
+    // Short rows: groups of multi_group_rows(slots) rows of similar length;
+    // empty rows (the tail of the order) in groups of kZeroRows, which only
+    // clear their C rows.
     const size_t first_multi = p->tasks.size();
     size_t end_nz = i;
     while (end_nz < rows.size() && len(rows[end_nz]) > 0) end_nz++;
     for (size_t k = i; k < rows.size();) {
-        const size_t lim = k < end_nz ? std::min<size_t>(k + slots, end_nz) : std::min<size_t>(k + kZeroRows, rows.size());
+        const size_t lim = k < end_nz ? std::min<size_t>(k + multi_group_rows(slots), end_nz)
+                                      : std::min<size_t>(k + kZeroRows, rows.size());
         p->tasks.push_back({static_cast<int32_t>(p->perm.size()), static_cast<int32_t>(lim - k), len(rows[k]), kTaskMulti});
         for (; k < lim; k++) p->perm.push_back(rows[k]);
     }

@@ -273,7 +273,11 @@ __global__ __launch_bounds__(256) void row_kernel(RowArgs a) {
         }
         return;
     }
-    if (t.w == 1) {  // multi: slot s walks row perm[t.x + s]
+    if (t.w == 1) {  // multi: in pass p0 (of S rows), slot s walks row perm[t.x + p0 + s]
+        // The next pass's row and CSR range are loaded before this pass's
+        // gathers, so they arrive during them.  Every pass runs t.z steps
+        // (the group's first and longest row).
+        const int S = 1 << logS;
         int row = -1, beg = 0, len = 0;
         if (slot < t.y) {
             row = a.perm[t.x + slot];
@@ -282,29 +286,42 @@ __global__ __launch_bounds__(256) void row_kernel(RowArgs a) {
         }
         const uint32_t rowbytes = static_cast<uint32_t>(a.N) * sizeof(T);
         const uint32_t colbytes = static_cast<uint32_t>(col) * sizeof(T);
-        for (int j = 0; j < t.z; j += kRowUnroll) {
-            Pack<T, E> bv[kRowUnroll];
-            float av[kRowUnroll];
-            int c[kRowUnroll];
-#pragma unroll
-            for (int u = 0; u < kRowUnroll; u++) {
-                c[u] = load_idx(rcol, beg + j + u, j + u < len);
-                av[u] = load_val<T>(rval, beg + j + u, j + u < len);
+        for (int p0 = 0; p0 < t.y; p0 += S) {
+            int nrow = -1, nbeg = 0, nlen = 0;
+            if (p0 + S + slot < t.y) {
+                nrow = a.perm[t.x + p0 + S + slot];
+                nbeg = a.rowptr[nrow];
+                nlen = a.rowptr[nrow + 1] - nbeg;
             }
 #pragma unroll
-            for (int u = 0; u < kRowUnroll; u++)
-                bv[u] = load_pack<T, E>(rB, j + u < len && colok ? static_cast<uint32_t>(c[u]) * rowbytes + colbytes
-                                                                 : kOob);
+            for (int e = 0; e < E; e++) acc[e] = 0.f;
+            for (int j = 0; j < t.z; j += kRowUnroll) {
+                Pack<T, E> bv[kRowUnroll];
+                float av[kRowUnroll];
+                int c[kRowUnroll];
 #pragma unroll
-            for (int u = 0; u < kRowUnroll; u++) fma_pack<T, E>(acc, av[u], bv[u]);
-        }
-        if constexpr (E == 8) {
-            const LinePieces lp = line_pieces<E>(acc, lane, g, a.chunk_lanes);
-            if (row >= 0 && g < a.chunk_lanes)
-                store_line_pieces(a.C + static_cast<size_t>(row) * a.N, chunk * a.chunk_lanes * 8, a.N, g, a.chunk_lanes,
-                                  lp);
-        } else {
-            if (row >= 0 && colok) store_row<E>(a.C + static_cast<size_t>(row) * a.N + col, acc);
+                for (int u = 0; u < kRowUnroll; u++) {
+                    c[u] = load_idx(rcol, beg + j + u, j + u < len);
+                    av[u] = load_val<T>(rval, beg + j + u, j + u < len);
+                }
+#pragma unroll
+                for (int u = 0; u < kRowUnroll; u++)
+                    bv[u] = load_pack<T, E>(rB, j + u < len && colok ? static_cast<uint32_t>(c[u]) * rowbytes + colbytes
+                                                                     : kOob);
+#pragma unroll
+                for (int u = 0; u < kRowUnroll; u++) fma_pack<T, E>(acc, av[u], bv[u]);
+            }
+            if constexpr (E == 8) {
+                const LinePieces lp = line_pieces<E>(acc, lane, g, a.chunk_lanes);
+                if (row >= 0 && g < a.chunk_lanes)
+                    store_line_pieces(a.C + static_cast<size_t>(row) * a.N, chunk * a.chunk_lanes * 8, a.N, g,
+                                      a.chunk_lanes, lp);
+            } else {
+                if (row >= 0 && colok) store_row<E>(a.C + static_cast<size_t>(row) * a.N + col, acc);
+            }
+            row = nrow;
+            beg = nbeg;
+            len = nlen;
         }
         return;
     }

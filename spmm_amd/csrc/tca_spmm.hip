@@ -1260,7 +1260,7 @@ int tca_spmm_plan_create_device(const int32_t* d_rowptr, const int32_t* d_colidx
         p->mfma.row_mfma.clear();
         if (hipGetDevice(&p->device) != hipSuccess) return fail(TCA_ERR_HIP, "no HIP device");
         plan_row_params(nnz, N, static_cast<int32_t>(dtype_size(dtype)), default_slices(K, N, dtype), &p->rows);
-        const int slots = 64 >> p->rows.log_lanes;
+        const int group = multi_group_rows(64 >> p->rows.log_lanes);  // rows per multi task
         hipStream_t s = static_cast<hipStream_t>(stream);
 
         // temporaries of the planning, freed on every exit
@@ -1581,7 +1581,7 @@ int tca_spmm_plan_create_device(const int32_t* d_rowptr, const int32_t* d_colidx
                 return bail(fail(TCA_ERR_HIP, "segment scan failed"));
         }
         const int n_wide = end_wide - n_long, n_row = end_row - end_wide, n_short = Mp - end_row;
-        const int n_multi = (end_nz - end_row + slots - 1) / slots + (Mp - end_nz + kZeroRows - 1) / kZeroRows;
+        const int n_multi = (end_nz - end_row + group - 1) / group + (Mp - end_nz + kZeroRows - 1) / kZeroRows;
         p->ntasks = 4 * n_wide + seg_total + n_row + n_multi;
         p->rows.n_wide = 4 * n_wide;
         p->rows.n_seg = seg_total;
@@ -1608,7 +1608,7 @@ int tca_spmm_plan_create_device(const int32_t* d_rowptr, const int32_t* d_colidx
             ea.end_wide = end_wide;
             ea.end_row = end_row;
             ea.end_nz = end_nz;
-            ea.slots = slots;
+            ea.group = group;
             ea.seg_total = seg_total;
             hipLaunchKernelGGL(dp_emit_kernel, grid_for(Mp), blk, 0, s, ea);
         }

@@ -381,7 +381,7 @@ def test_plan_covers_every_row_once(n, dtype):
                 assert 1 <= y <= 64 and np.all(lens[rows] == 0)
                 assert np.all(np.diff(rows) > 0)
             else:
-                assert 1 <= y <= 64 // g and np.all(lens[rows] > 0)
+                assert 1 <= y <= min(64, 4 * (64 // g)) and np.all(lens[rows] > 0)  # up to 4 passes of 64 / g rows
                 assert z == lens[rows].max() and z <= geo["multi_max"]
             covered[rows] += 1
         elif w & 3 == 2:
