@@ -119,6 +119,7 @@ typedef struct tca_plan_info {
     int64_t staged_panels;    /* B rows staged per run (column unions summed over panels) */
     int32_t panel_blockdim;   /* threads per workgroup of the panel kernel */
     int32_t panel_lds_bytes;  /* LDS per panel workgroup */
+    int32_t panel_window;     /* 1: the panel kernel takes its run data through per-row windows (low-reuse panels) */
 } tca_plan_info;
 
 /* tca_plan_info.tile_kernel */

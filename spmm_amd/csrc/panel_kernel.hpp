@@ -263,7 +263,7 @@ __device__ __forceinline__ void pn_static_for(F&& f) {
     }
 }
 
-template <typename T, int E>
+template <typename T, int E, bool kWin>
 __global__ __launch_bounds__(kPnThreads, 1) void panel_kernel(PanelArgs a) {
     using G = PanelGeom<T, E>;
     constexpr int R = kPnWaves * 4 * kPnRpg;
@@ -415,29 +415,60 @@ __global__ __launch_bounds__(kPnThreads, 1) void panel_kernel(PanelArgs a) {
             c[b] = v.x; c[b + 1] = v.y; c[b + 2] = v.z;
         }
     };
-    // Entry i's run of tile t + 1 is fetched right after entry i is done with
-    // tile t, so its latency hides behind the rest of the tile: lane g loads
-    // the run's nonzero g (its 1-based position byte and its value; masked
-    // loads give 0 and 0 past the run).  Tile 0's runs are fetched before
-    // the loop, with the same instructions in the same order as every later
-    // fetch: the compiler's vmcnt waits then count exactly the loads issued
-    // after the one they wait for.  The fetch after the last tile has n = 0.
-    // cn: counts of tile t (cursor advance, longest runs); cnx: of tile t + 1
-    // (masks of the fetches for t + 1).
+    // Run data: right after entry i is done with tile t, the run of tile
+    // t + 1 ([cur, cur + nn) of its group's row: 1-based position bytes and
+    // values, lane g holding nonzero cur + g) is fetched, so its latency hides
+    // behind the rest of the tile; lanes past the run take position 0 and
+    // value 0 (the zero row, times 0).  Tile 0's runs are fetched before the
+    // loop with the same instructions as every later fetch (the compiler's
+    // vmcnt waits then count exactly the loads issued after the one they wait
+    // for); the fetch after the last tile has nn = 0.
+    //   kWin = false: each run is loaded where it lies (masked loads).
+    //   kWin = true: through a window per entry, lane g holding nonzero
+    //     w0 + g, 16 nonzeros ahead: a run inside the window is taken from it
+    //     (ds_bpermute by cur - w0), else a new window is loaded at cur (its
+    //     lanes 0 .. nn - 1 are then the run).  A row's runs in consecutive
+    //     tiles are consecutive nonzeros, so one window serves several tiles
+    //     and each line of the position and value arrays is fetched about
+    //     once instead of once per tile (between tiles the B-row staging
+    //     pushes those lines out of the L2).  Lanes that keep their window
+    //     load out of range (no memory access), so every fetch issues the
+    //     same instructions.  Worth its ~10 VALU per entry when runs are short
+    //     and the kernel waits on memory (panel_window in planner.cpp).
+    // cn: counts of tile t (cursor advance, longest runs); cnx: of tile t + 1.
     uint32_t cn[kPnCntUsed], cnx[kPnCntUsed];
-    uint32_t q[kPnRpg];
-    float vvq[kPnRpg];
+    uint32_t wq[kPnRpg], lq[kPnRpg], rq[kPnRpg];
+    float wv[kPnRpg], lv[kPnRpg], rv[kPnRpg];
+    int w0[kPnRpg], nnx[kPnRpg];
+    bool nd[kPnRpg];
+    auto fetch = [&](int i, int nn) {
+        const uint32_t k = static_cast<uint32_t>(cur[i] + g);
+        if constexpr (kWin) {
+            const bool need = nn > 0 && cur[i] + nn > w0[i] + 16;
+            const int src = (lane + cur[i] - w0[i]) << 2;
+            rq[i] = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(src, static_cast<int>(wq[i])));
+            rv[i] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src, __builtin_bit_cast(int, wv[i])));
+            lq[i] = __builtin_amdgcn_raw_buffer_load_b8(rpos, need ? k : kOob, 0, 0);
+            lv[i] = load_val<T>(rval, k, need);
+            w0[i] = need ? cur[i] : w0[i];
+            nd[i] = need;
+            nnx[i] = nn;
+        } else {
+            const bool ok = g < nn;
+            lq[i] = __builtin_amdgcn_raw_buffer_load_b8(rpos, ok ? k : kOob, 0, 0);
+            lv[i] = load_val<T>(rval, k, ok);
+        }
+        // loads in the loop's order (no reordering across entries)
+        asm volatile("" ::: "memory");
+    };
     read_counts(reinterpret_cast<const char*>(a.cnt) + (static_cast<size_t>(u.y) * kPnWaves + wave) * (kPnCntRows * 4),
                 cn);
 #pragma unroll
     for (int i = 0; i < kPnRpg; i++) {
-        const int nn = static_cast<int>((cn[i] >> shift) & 255);
-        const bool ok = g < nn;
-        const uint32_t k = static_cast<uint32_t>(cur[i] + g);
-        q[i] = __builtin_amdgcn_raw_buffer_load_b8(rpos, ok ? k : kOob, 0, 0);
-        vvq[i] = load_val<T>(rval, k, ok);
-        // loads in the loop's order (no reordering across entries)
-        asm volatile("" ::: "memory");
+        wq[i] = 0u;
+        wv[i] = 0.f;
+        w0[i] = -64;  // empty: the first run with nonzeros loads a window
+        fetch(i, static_cast<int>((cn[i] >> shift) & 255));
     }
     for (int t = 0; t < u.z; t++) {
         pn_barrier();
@@ -454,14 +485,22 @@ __global__ __launch_bounds__(kPnThreads, 1) void panel_kernel(PanelArgs a) {
         pn_static_for<0, kPnRpg>([&](auto ic) {
             constexpr int i = decltype(ic)::value;
             const int nmax = static_cast<int>((mxw[i / 4] >> (8 * (i % 4))) & 255);
-            if (nmax > 0) pn_run<T, E>(acc[i], q[i], vvq[i], nmax, zb, lanepart);
+            uint32_t qq;
+            float vv;
+            if constexpr (kWin) {
+                // this tile's run: the new window, or the one taken from the old
+                wq[i] = nd[i] ? lq[i] : wq[i];
+                wv[i] = nd[i] ? lv[i] : wv[i];
+                const bool in = g < nnx[i];
+                qq = in ? (nd[i] ? lq[i] : rq[i]) : 0u;
+                vv = in ? (nd[i] ? lv[i] : rv[i]) : 0.f;
+            } else {
+                qq = lq[i];
+                vv = lv[i];
+            }
+            if (nmax > 0) pn_run<T, E>(acc[i], qq, vv, nmax, zb, lanepart);
             cur[i] += static_cast<int>((cn[i] >> shift) & 255);
-            const int nn = more ? static_cast<int>((cnx[i] >> shift) & 255) : 0;
-            const bool ok = g < nn;
-            const uint32_t k = static_cast<uint32_t>(cur[i] + g);
-            q[i] = __builtin_amdgcn_raw_buffer_load_b8(rpos, ok ? k : kOob, 0, 0);
-            vvq[i] = load_val<T>(rval, k, ok);
-            asm volatile("" ::: "memory");
+            fetch(i, more ? static_cast<int>((cnx[i] >> shift) & 255) : 0);
         });
 #pragma unroll
         for (int j = 0; j < kPnCntUsed; j++) cn[j] = cnx[j];

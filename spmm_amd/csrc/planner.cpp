@@ -554,7 +554,13 @@ void plan_panels(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_
         for (int32_t s = 0; s < R; s++) p->n_rows += c.slots[s] >= 0;
     }
     p->n_segments = seg;
+    p->window = panel_window(p->nnz, p->staged);
     order_units(K, p);
+}
+
+bool panel_window(int64_t nnz, int64_t staged) {
+    if (const char* e = std::getenv("TCA_PANEL_WINDOW")) return std::atoi(e) != 0;
+    return static_cast<double>(nnz) < kPanelWindowReuse * static_cast<double>(staged);
 }
 
 void order_units(int32_t K, PanelPlan* p) {

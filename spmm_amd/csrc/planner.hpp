@@ -183,6 +183,7 @@ struct PanelPlan {
     int64_t nnz = 0;           // nonzeros in panels
     int64_t staged = 0;        // union columns summed over panels
     int32_t n_rows = 0;        // rows in panels
+    bool window = false;       // run data through per-entry windows (panel_window)
     int32_t n_tiles() const { return P ? static_cast<int32_t>(cols.size() / P) : 0; }
 };
 constexpr int kPanelWaves = 12;   // consumer wavefronts per workgroup (plus four producers: 1024 threads)
@@ -197,6 +198,15 @@ constexpr int kPanelMaxRun = 16;  // nonzeros of one row in one tile (one 16-lan
 // cost less than the row kernel's gathers; rows that share none stay there.
 constexpr double kPanelMinReuse = 1.02;
 constexpr int64_t kPanelMinNnz = int64_t(1) << 21;  // fewer nonzeros in panels: none (unless forced)
+// Whether the panel kernel takes its run data through windows (a window of
+// 16 nonzeros per row serves several tiles): when the panels' reuse
+// nnz / staged is below kPanelWindowReuse their rows hold few nonzeros per
+// tile, and the kernel waits on memory more than on issue.  Measured on
+// MI355X (panel phase, windows against direct run loads): config 3 (reuse
+// 1.67) 2.34 against 2.82 ms, config 2 (5.74) 1.57 against 1.53 ms.
+// TCA_PANEL_WINDOW=0 / 1 forces it (tests).
+constexpr double kPanelWindowReuse = 3.0;
+bool panel_window(int64_t nnz, int64_t staged);
 // Launch order of the units (PanelPlan::order).
 void order_units(int32_t K, PanelPlan* p);
 // The same from each unit's first and last staged column (the GPU planner

@@ -420,7 +420,10 @@ void launch_panels_t(const tca_spmm_plan* p, const void* val, const void* B, flo
     a.chunks = p->panels.chunks;
     a.pos_bytes = static_cast<uint32_t>(p->n_pos_bytes);
     a.val_bytes = static_cast<uint32_t>(static_cast<uint64_t>(p->nnz) * sizeof(T));
-    TCA_PHASE_LAUNCH((panel_kernel<T, E>), dim3(p->n_pblocks * p->panels.chunks), dim3(kPnThreads), 0, s, a);
+    if (p->panels.window)
+        TCA_PHASE_LAUNCH((panel_kernel<T, E, true>), dim3(p->n_pblocks * p->panels.chunks), dim3(kPnThreads), 0, s, a);
+    else
+        TCA_PHASE_LAUNCH((panel_kernel<T, E, false>), dim3(p->n_pblocks * p->panels.chunks), dim3(kPnThreads), 0, s, a);
 }
 
 int launch_panels(const tca_spmm_plan* p, const void* val, const void* B, float* C, float* W, hipStream_t s) {
@@ -519,6 +522,7 @@ void fill_info(tca_spmm_plan* p) {
     in.panel_blockdim = kPnThreads;
     in.panel_lds_bytes =
         p->n_units ? panel_lds_bytes(16 * p->panels.elems * static_cast<int>(dtype_size(p->dtype))) : 0;
+    in.panel_window = p->n_units && p->panels.window ? 1 : 0;
     if (p->mfma_short) {
         in.n_windows_mfma = p->short_nwin;
         in.rows_mfma = p->M;
@@ -1220,6 +1224,7 @@ struct DevPanelPlanner {
         pp.n_panels = n_take;
         pp.nnz = nnz;
         pp.staged = staged;
+        pp.window = panel_window(nnz, staged);
         pp.n_rows = n_panel_rows;
         pp.n_segments = n_segments;
         p->n_units = static_cast<int32_t>(n_units);

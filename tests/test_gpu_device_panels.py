@@ -89,7 +89,7 @@ def test_device_panels_equal_host_panels(torch_cuda, name, a, n, flags, env):
             assert np.array_equal(hx[k], dx[k]), (name, k)
         hi, di = hp.info(), dp.info()
         for key in ("n_panels", "n_panel_units", "rows_panels", "nnz_panels", "staged_panels", "panel_blocks",
-                    "n_row_tasks", "n_multi_tasks", "n_seg_tasks", "n_long_rows", "scratch_bytes", "row_blocks"):
+                    "panel_window", "n_row_tasks", "n_multi_tasks", "n_seg_tasks", "n_long_rows", "scratch_bytes", "row_blocks"):
             assert hi[key] == di[key], (name, key, hi[key], di[key])
         if name == "no-panel-rows":
             assert hx["panels"] == 0

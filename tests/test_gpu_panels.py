@@ -3,7 +3,8 @@ bit-exact against the oracle on exact-arithmetic inputs for every lane
 geometry (fp32 E = 8/4/2, fp16 and bf16 E = 8/4, several column chunks),
 split panels (partial rows summed in a fixed order), panels beside MFMA windows
 and the row kernel, determinism, and exactness of the masked steps with
-non-finite B rows."""
+non-finite B rows; each with the run data loaded where it lies and through
+per-row windows."""
 import numpy as np
 import pytest
 
@@ -16,6 +17,13 @@ from test_gpu_parity import _dev, assert_parity, make_csr, oracle_c, run_gpu
 pytestmark = pytest.mark.gpu
 
 
+@pytest.fixture(autouse=True, params=["0", "1"], ids=["direct", "window"])
+def window_mode(request, monkeypatch):
+    """Every test with the run data loaded where it lies and through per-row windows."""
+    monkeypatch.setenv("TCA_PANEL_WINDOW", request.param)
+    return int(request.param)
+
+
 def exact(a: S.CSR, dtype, seed=7):
     rng = np.random.default_rng(seed)
     v = exact_values(rng, a.nnz)
@@ -25,7 +33,7 @@ def exact(a: S.CSR, dtype, seed=7):
 
 @pytest.mark.parametrize("dtype,widths", [(S.TCA_F32, (32, 64, 128, 256)), (S.TCA_F16, (64, 128, 256)),
                                           (S.TCA_BF16, (64, 128))])
-def test_panels_exact_all_geometries(torch_cuda, dtype, widths):
+def test_panels_exact_all_geometries(torch_cuda, window_mode, dtype, widths):
     rng = np.random.default_rng(3 + dtype)
     base, _ = S.gen_rmat(12, 3000, 60000, seed=4)
     a = exact(base, dtype)
@@ -37,6 +45,7 @@ def test_panels_exact_all_geometries(torch_cuda, dtype, widths):
         print(f"dtype {dtype} N={n}: {info['n_panels']} panels, {info['n_panel_units']} units, "
               f"{info['rows_panels']} rows", flush=True)
         assert info["n_panels"] > 0 and info["rows_panels"] == int((np.diff(a.rowptr) > 0).sum())
+        assert info["panel_window"] == window_mode
         want = oracle_c(a, b)
         assert np.array_equal(got, want), (dtype, n, np.abs(got - want).max())
 
