@@ -119,7 +119,7 @@ typedef struct tca_plan_info {
     int64_t staged_panels;    /* B rows staged per run (column unions summed over panels) */
     int32_t panel_blockdim;   /* threads per workgroup of the panel kernel */
     int32_t panel_lds_bytes;  /* LDS per panel workgroup */
-    int32_t panel_window;     /* 1: the panel kernel takes its run data through per-row windows (low-reuse panels) */
+    int32_t panel_window;     /* panels whose run data go through per-row windows (low reuse) */
 } tca_plan_info;
 
 /* tca_plan_info.tile_kernel */
@@ -308,12 +308,13 @@ int tca_spmm_plan_export_tiles(const tca_spmm_plan* plan, int32_t* n_windows, in
  * waves * 8] (count dwords), pos [pos bytes] (1-based tile position per
  * nonzero, 0 outside panels), units [units * 4], order [launch-order entries]
  * (-1: idle workgroup), panel_units [panels], ustart [units * R], longrows
- * [panel long rows * 4] (segment slots after the row kernel's).  No
+ * [panel long rows * 4] (segment slots after the row kernel's), window
+ * [panels] (1: the panel's run data go through per-row windows).  No
  * counterpart in the reference (its task split, src/our_spmm.cu:353-477, has
  * no panels). */
 int tca_spmm_plan_export_panels(const tca_spmm_plan* plan, int64_t* sizes, int32_t* rows, uint32_t* boff, uint32_t* cnt,
                                 uint8_t* pos, int32_t* units, int32_t* order, int32_t* panel_units, int32_t* ustart,
-                                int32_t* longrows);
+                                int32_t* longrows, uint8_t* window);
 
 int tca_spmm_plan_info(const tca_spmm_plan* plan, tca_plan_info* info);
 

@@ -536,23 +536,24 @@ class Plan:
         (tca_spmm_plan_export_panels) as numpy arrays."""
         sizes = np.zeros(8, np.int64)
         call("tca_spmm_plan_export_panels", self._p, np_ptr(sizes, ctypes.c_int64), None, None, None, None, None,
-             None, None, None, None)
+             None, None, None, None, None)
         n_p, n_t, n_u, n_o, n_lr, R, P, n_pos = (int(x) for x in sizes)
         out = dict(panels=n_p, tiles=n_t, n_units=n_u, R=R, P=P,
                    rows=np.zeros(max(n_p * R, 1), np.int32), boff=np.zeros(max(n_t * P, 1), np.uint32),
                    cnt=np.zeros(max(n_t * 96, 1), np.uint32), pos=np.zeros(max(n_pos, 1), np.uint8),
                    units=np.zeros((max(n_u, 1), 4), np.int32), order=np.zeros(max(n_o, 1), np.int32),
                    panel_units=np.zeros(max(n_p, 1), np.int32), ustart=np.zeros(max(n_u * R, 1), np.int32),
-                   longrows=np.zeros((max(n_lr, 1), 4), np.int32))
+                   longrows=np.zeros((max(n_lr, 1), 4), np.int32), window=np.zeros(max(n_p, 1), np.uint8))
         cnt_words = self.PANEL_CNT_DWORDS
         out["cnt"] = np.zeros(max(n_t * cnt_words, 1), np.uint32)
         call("tca_spmm_plan_export_panels", self._p, np_ptr(sizes, ctypes.c_int64), np_ptr(out["rows"], ctypes.c_int32),
              np_ptr(out["boff"], ctypes.c_uint32), np_ptr(out["cnt"], ctypes.c_uint32), out["pos"].ctypes.data,
              np_ptr(out["units"], ctypes.c_int32), np_ptr(out["order"], ctypes.c_int32),
              np_ptr(out["panel_units"], ctypes.c_int32), np_ptr(out["ustart"], ctypes.c_int32),
-             np_ptr(out["longrows"], ctypes.c_int32))
+             np_ptr(out["longrows"], ctypes.c_int32), out["window"].ctypes.data)
         for k, n in (("rows", n_p * R), ("boff", n_t * P), ("cnt", n_t * cnt_words), ("pos", n_pos), ("units", n_u),
-                     ("order", n_o), ("panel_units", n_p), ("ustart", n_u * R), ("longrows", n_lr)):
+                     ("order", n_o), ("panel_units", n_p), ("ustart", n_u * R), ("longrows", n_lr),
+                     ("window", n_p)):
             out[k] = out[k][:n]
         return out
 

@@ -102,7 +102,7 @@ SIGNATURES = {
     "tca_spmm_plan_export_order": (i32, [vp, i32p, i32p]),
     "tca_plan_launch_orders": (i32, [i32p, i32p, i32, i32, i32, i32, u32, i32p, i32p, i32p, i32p, i32p, i32p]),
     "tca_spmm_plan_export_tiles": (i32, [vp, i32p, i32p, i32p, i32p, u32p, i32p, u32p]),
-    "tca_spmm_plan_export_panels": (i32, [vp, i64p, i32p, u32p, u32p, vp, i32p, i32p, i32p, i32p, i32p]),
+    "tca_spmm_plan_export_panels": (i32, [vp, i64p, i32p, u32p, u32p, vp, i32p, i32p, i32p, i32p, i32p, vp]),
     "tca_spmm_plan_info": (i32, [vp, ctypes.POINTER(TcaPlanInfo)]),
     "tca_spmm_plan_destroy": (i32, [vp]),
     "tca_spmm_host": (i32, [i32p, i32p, vp, i32, i32, i32, vp, f32p, i32, i32, i32, i32,

@@ -65,6 +65,7 @@ struct PanelArgs {
     const uint32_t* cnt;     // [tile][wave][16 entries] dwords: byte g = group g's count
     const void* pos;         // [nnz] bytes, padded to whole dwords (pos_bytes)
     const int* ustart;       // [unit * R + slot]
+    const uint8_t* win;      // [panel]: 1 = run data through per-row windows
     const void* val;
     const void* B;
     float* C;
@@ -263,7 +264,7 @@ __device__ __forceinline__ void pn_static_for(F&& f) {
     }
 }
 
-template <typename T, int E, bool kWin>
+template <typename T, int E>
 __global__ __launch_bounds__(kPnThreads, 1) void panel_kernel(PanelArgs a) {
     using G = PanelGeom<T, E>;
     constexpr int R = kPnWaves * 4 * kPnRpg;
@@ -365,158 +366,165 @@ __global__ __launch_bounds__(kPnThreads, 1) void panel_kernel(PanelArgs a) {
     }
 
     // ---- consumers
-    const int group = lane >> 4;
-    const int g = lane & 15;
-    const __amdgpu_buffer_rsrc_t rpos = make_rsrc(a.pos, a.pos_bytes);
-    const __amdgpu_buffer_rsrc_t rval = make_rsrc(a.val, a.val_bytes);
-    float acc[kPnRpg][E];
-    int cur[kPnRpg];
+    // The panel's choice (PanelPlan::win): run data loaded where it lies, or
+    // through per-row windows; one branch per workgroup.
+    auto consume = [&](auto win_tag) {
+        constexpr bool kWin = decltype(win_tag)::value != 0;
+        const int group = lane >> 4;
+        const int g = lane & 15;
+        const __amdgpu_buffer_rsrc_t rpos = make_rsrc(a.pos, a.pos_bytes);
+        const __amdgpu_buffer_rsrc_t rval = make_rsrc(a.val, a.val_bytes);
+        float acc[kPnRpg][E];
+        int cur[kPnRpg];
 #pragma unroll
-    for (int i = 0; i < kPnRpg; i++) {
-        cur[i] = a.ustart[static_cast<size_t>(unit) * R + (wave * kPnRpg + i) * 4 + group];
+        for (int i = 0; i < kPnRpg; i++) {
+            cur[i] = a.ustart[static_cast<size_t>(unit) * R + (wave * kPnRpg + i) * 4 + group];
 #pragma unroll
-        for (int e = 0; e < E; e++) acc[i][e] = 0.f;
-    }
-    if (wave == 0)
-        for (int o = 16 * lane; o < G::kRowBytes; o += 1024) {
-            *reinterpret_cast<f32x4*>(smem + pn_zrow_off<T, E>(0) + o) = f32x4{0.f, 0.f, 0.f, 0.f};
-            *reinterpret_cast<f32x4*>(smem + pn_zrow_off<T, E>(1) + o) = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int e = 0; e < E; e++) acc[i][e] = 0.f;
         }
-    const int shift = 8 * group;
-    const uint32_t lds0 = pn_lds_addr(smem);
-    const uint32_t lanepart = static_cast<uint32_t>((G::kLaneBytes == 32 ? 16 : G::kLaneBytes) * g);
-    // Counts: per tile and wavefront kPnCntRows dwords; dword i (i < rpg)
-    // holds entry i's four group counts, byte i % 4 of dword kPnMaxDword + i / 4
-    // entry i's longest.  Tile 0's come through one vector load before the loop;
-    // tile t + 1's are read from the count slot the producer staged with tile
-    // t (LDS reads, ordered with the B-row reads: no scalar loads, which
-    // share lgkmcnt with the LDS reads and return out of order, and no
-    // loop-carried vector loads, whose copies between iterations would wait
-    // for every load in flight).
-    // Only the kPnCntUsed dwords in use are read (16-byte reads, then one of
-    // 4, 8 or 12 bytes): a register loaded and never used would be reused by
-    // the compiler while its read is in flight, which costs a wait.
-    auto read_counts = [&](const char* p, uint32_t (&c)[kPnCntUsed]) {
-        pn_static_for<0, kPnCntUsed / 4>([&](auto jc) {
-            constexpr int j = decltype(jc)::value;
-            const i32x4v v = *reinterpret_cast<const i32x4v*>(p + 16 * j);
-            c[4 * j] = v.x; c[4 * j + 1] = v.y; c[4 * j + 2] = v.z; c[4 * j + 3] = v.w;
-        });
-        constexpr int b = kPnCntUsed / 4 * 4, rem = kPnCntUsed % 4;
-        if constexpr (rem == 1) {
-            c[b] = *reinterpret_cast<const uint32_t*>(p + 4 * b);
-        } else if constexpr (rem == 2) {
-            typedef int i32x2t __attribute__((ext_vector_type(2)));
-            const i32x2t v = *reinterpret_cast<const i32x2t*>(p + 4 * b);
-            c[b] = v.x; c[b + 1] = v.y;
-        } else if constexpr (rem == 3) {
-            typedef int i32x3t __attribute__((ext_vector_type(3)));
-            const i32x3t v = *reinterpret_cast<const i32x3t*>(p + 4 * b);
-            c[b] = v.x; c[b + 1] = v.y; c[b + 2] = v.z;
-        }
-    };
-    // Run data: right after entry i is done with tile t, the run of tile
-    // t + 1 ([cur, cur + nn) of its group's row: 1-based position bytes and
-    // values, lane g holding nonzero cur + g) is fetched, so its latency hides
-    // behind the rest of the tile; lanes past the run take position 0 and
-    // value 0 (the zero row, times 0).  Tile 0's runs are fetched before the
-    // loop with the same instructions as every later fetch (the compiler's
-    // vmcnt waits then count exactly the loads issued after the one they wait
-    // for); the fetch after the last tile has nn = 0.
-    //   kWin = false: each run is loaded where it lies (masked loads).
-    //   kWin = true: through a window per entry, lane g holding nonzero
-    //     w0 + g, 16 nonzeros ahead: a run inside the window is taken from it
-    //     (ds_bpermute by cur - w0), else a new window is loaded at cur (its
-    //     lanes 0 .. nn - 1 are then the run).  A row's runs in consecutive
-    //     tiles are consecutive nonzeros, so one window serves several tiles
-    //     and each line of the position and value arrays is fetched about
-    //     once instead of once per tile (between tiles the B-row staging
-    //     pushes those lines out of the L2).  Lanes that keep their window
-    //     load out of range (no memory access), so every fetch issues the
-    //     same instructions.  Worth its ~10 VALU per entry when runs are short
-    //     and the kernel waits on memory (panel_window in planner.cpp).
-    // cn: counts of tile t (cursor advance, longest runs); cnx: of tile t + 1.
-    uint32_t cn[kPnCntUsed], cnx[kPnCntUsed];
-    uint32_t wq[kPnRpg], lq[kPnRpg], rq[kPnRpg];
-    float wv[kPnRpg], lv[kPnRpg], rv[kPnRpg];
-    int w0[kPnRpg], nnx[kPnRpg];
-    bool nd[kPnRpg];
-    auto fetch = [&](int i, int nn) {
-        const uint32_t k = static_cast<uint32_t>(cur[i] + g);
-        if constexpr (kWin) {
-            const bool need = nn > 0 && cur[i] + nn > w0[i] + 16;
-            const int src = (lane + cur[i] - w0[i]) << 2;
-            rq[i] = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(src, static_cast<int>(wq[i])));
-            rv[i] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src, __builtin_bit_cast(int, wv[i])));
-            lq[i] = __builtin_amdgcn_raw_buffer_load_b8(rpos, need ? k : kOob, 0, 0);
-            lv[i] = load_val<T>(rval, k, need);
-            w0[i] = need ? cur[i] : w0[i];
-            nd[i] = need;
-            nnx[i] = nn;
-        } else {
-            const bool ok = g < nn;
-            lq[i] = __builtin_amdgcn_raw_buffer_load_b8(rpos, ok ? k : kOob, 0, 0);
-            lv[i] = load_val<T>(rval, k, ok);
-        }
-        // loads in the loop's order (no reordering across entries)
-        asm volatile("" ::: "memory");
-    };
-    read_counts(reinterpret_cast<const char*>(a.cnt) + (static_cast<size_t>(u.y) * kPnWaves + wave) * (kPnCntRows * 4),
-                cn);
-#pragma unroll
-    for (int i = 0; i < kPnRpg; i++) {
-        wq[i] = 0u;
-        wv[i] = 0.f;
-        w0[i] = -64;  // empty: the first run with nonzeros loads a window
-        fetch(i, static_cast<int>((cn[i] >> shift) & 255));
-    }
-    for (int t = 0; t < u.z; t++) {
-        pn_barrier();
-        const bool more = t + 1 < u.z;
-        const uint32_t zb = lds0 + pn_zrow_off<T, E>(t & 1);
-        {
-            read_counts(smem + pn_cnt_off<T, E>(t & 1) + wave * (kPnCntRows * 4), cnx);
-        }
-        // entries' longest runs (uniform)
-        uint32_t mxw[(kPnRpg + 3) / 4];
-#pragma unroll
-        for (int w = 0; w < (kPnRpg + 3) / 4; w++)
-            mxw[w] = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(cn[kPnMaxDword + w])));
-        pn_static_for<0, kPnRpg>([&](auto ic) {
-            constexpr int i = decltype(ic)::value;
-            const int nmax = static_cast<int>((mxw[i / 4] >> (8 * (i % 4))) & 255);
-            uint32_t qq;
-            float vv;
-            if constexpr (kWin) {
-                // this tile's run: the new window, or the one taken from the old
-                wq[i] = nd[i] ? lq[i] : wq[i];
-                wv[i] = nd[i] ? lv[i] : wv[i];
-                const bool in = g < nnx[i];
-                qq = in ? (nd[i] ? lq[i] : rq[i]) : 0u;
-                vv = in ? (nd[i] ? lv[i] : rv[i]) : 0.f;
-            } else {
-                qq = lq[i];
-                vv = lv[i];
+        if (wave == 0)
+            for (int o = 16 * lane; o < G::kRowBytes; o += 1024) {
+                *reinterpret_cast<f32x4*>(smem + pn_zrow_off<T, E>(0) + o) = f32x4{0.f, 0.f, 0.f, 0.f};
+                *reinterpret_cast<f32x4*>(smem + pn_zrow_off<T, E>(1) + o) = f32x4{0.f, 0.f, 0.f, 0.f};
             }
-            if (nmax > 0) pn_run<T, E>(acc[i], qq, vv, nmax, zb, lanepart);
-            cur[i] += static_cast<int>((cn[i] >> shift) & 255);
-            fetch(i, more ? static_cast<int>((cnx[i] >> shift) & 255) : 0);
-        });
+        const int shift = 8 * group;
+        const uint32_t lds0 = pn_lds_addr(smem);
+        const uint32_t lanepart = static_cast<uint32_t>((G::kLaneBytes == 32 ? 16 : G::kLaneBytes) * g);
+        // Counts: per tile and wavefront kPnCntRows dwords; dword i (i < rpg)
+        // holds entry i's four group counts, byte i % 4 of dword kPnMaxDword + i / 4
+        // entry i's longest.  Tile 0's come through one vector load before the loop;
+        // tile t + 1's are read from the count slot the producer staged with tile
+        // t (LDS reads, ordered with the B-row reads: no scalar loads, which
+        // share lgkmcnt with the LDS reads and return out of order, and no
+        // loop-carried vector loads, whose copies between iterations would wait
+        // for every load in flight).
+        // Only the kPnCntUsed dwords in use are read (16-byte reads, then one of
+        // 4, 8 or 12 bytes): a register loaded and never used would be reused by
+        // the compiler while its read is in flight, which costs a wait.
+        auto read_counts = [&](const char* p, uint32_t (&c)[kPnCntUsed]) {
+            pn_static_for<0, kPnCntUsed / 4>([&](auto jc) {
+                constexpr int j = decltype(jc)::value;
+                const i32x4v v = *reinterpret_cast<const i32x4v*>(p + 16 * j);
+                c[4 * j] = v.x; c[4 * j + 1] = v.y; c[4 * j + 2] = v.z; c[4 * j + 3] = v.w;
+            });
+            constexpr int b = kPnCntUsed / 4 * 4, rem = kPnCntUsed % 4;
+            if constexpr (rem == 1) {
+                c[b] = *reinterpret_cast<const uint32_t*>(p + 4 * b);
+            } else if constexpr (rem == 2) {
+                typedef int i32x2t __attribute__((ext_vector_type(2)));
+                const i32x2t v = *reinterpret_cast<const i32x2t*>(p + 4 * b);
+                c[b] = v.x; c[b + 1] = v.y;
+            } else if constexpr (rem == 3) {
+                typedef int i32x3t __attribute__((ext_vector_type(3)));
+                const i32x3t v = *reinterpret_cast<const i32x3t*>(p + 4 * b);
+                c[b] = v.x; c[b + 1] = v.y; c[b + 2] = v.z;
+            }
+        };
+        // Run data: right after entry i is done with tile t, the run of tile
+        // t + 1 ([cur, cur + nn) of its group's row: 1-based position bytes and
+        // values, lane g holding nonzero cur + g) is fetched, so its latency hides
+        // behind the rest of the tile; lanes past the run take position 0 and
+        // value 0 (the zero row, times 0).  Tile 0's runs are fetched before the
+        // loop with the same instructions as every later fetch (the compiler's
+        // vmcnt waits then count exactly the loads issued after the one they wait
+        // for); the fetch after the last tile has nn = 0.
+        //   kWin = false: each run is loaded where it lies (masked loads).
+        //   kWin = true: through a window per entry, lane g holding nonzero
+        //     w0 + g, 16 nonzeros ahead: a run inside the window is taken from it
+        //     (ds_bpermute by cur - w0), else a new window is loaded at cur (its
+        //     lanes 0 .. nn - 1 are then the run).  A row's runs in consecutive
+        //     tiles are consecutive nonzeros, so one window serves several tiles
+        //     and each line of the position and value arrays is fetched about
+        //     once instead of once per tile (between tiles the B-row staging
+        //     pushes those lines out of the L2).  Lanes that keep their window
+        //     load out of range (no memory access), so every fetch issues the
+        //     same instructions.  Worth its ~10 VALU per entry when runs are short
+        //     and the kernel waits on memory (panel_window in planner.cpp).
+        // cn: counts of tile t (cursor advance, longest runs); cnx: of tile t + 1.
+        uint32_t cn[kPnCntUsed], cnx[kPnCntUsed];
+        uint32_t wq[kPnRpg], lq[kPnRpg], rq[kPnRpg];
+        float wv[kPnRpg], lv[kPnRpg], rv[kPnRpg];
+        int w0[kPnRpg], nnx[kPnRpg];
+        bool nd[kPnRpg];
+        auto fetch = [&](int i, int nn) {
+            const uint32_t k = static_cast<uint32_t>(cur[i] + g);
+            if constexpr (kWin) {
+                const bool need = nn > 0 && cur[i] + nn > w0[i] + 16;
+                const int src = (lane + cur[i] - w0[i]) << 2;
+                rq[i] = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(src, static_cast<int>(wq[i])));
+                rv[i] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src, __builtin_bit_cast(int, wv[i])));
+                lq[i] = __builtin_amdgcn_raw_buffer_load_b8(rpos, need ? k : kOob, 0, 0);
+                lv[i] = load_val<T>(rval, k, need);
+                w0[i] = need ? cur[i] : w0[i];
+                nd[i] = need;
+                nnx[i] = nn;
+            } else {
+                const bool ok = g < nn;
+                lq[i] = __builtin_amdgcn_raw_buffer_load_b8(rpos, ok ? k : kOob, 0, 0);
+                lv[i] = load_val<T>(rval, k, ok);
+            }
+            // loads in the loop's order (no reordering across entries)
+            asm volatile("" ::: "memory");
+        };
+        read_counts(reinterpret_cast<const char*>(a.cnt) + (static_cast<size_t>(u.y) * kPnWaves + wave) * (kPnCntRows * 4),
+                    cn);
 #pragma unroll
-        for (int j = 0; j < kPnCntUsed; j++) cn[j] = cnx[j];
-    }
-    // ---- results: C rows, or this unit's partial rows of a split panel
-    const int nu = u.w >= 0 ? a.panel_units[u.x] : 0;
-    const int col0 = chunk * 16 * E;
+        for (int i = 0; i < kPnRpg; i++) {
+            wq[i] = 0u;
+            wv[i] = 0.f;
+            w0[i] = -64;  // empty: the first run with nonzeros loads a window
+            fetch(i, static_cast<int>((cn[i] >> shift) & 255));
+        }
+        for (int t = 0; t < u.z; t++) {
+            pn_barrier();
+            const bool more = t + 1 < u.z;
+            const uint32_t zb = lds0 + pn_zrow_off<T, E>(t & 1);
+            {
+                read_counts(smem + pn_cnt_off<T, E>(t & 1) + wave * (kPnCntRows * 4), cnx);
+            }
+            // entries' longest runs (uniform)
+            uint32_t mxw[(kPnRpg + 3) / 4];
 #pragma unroll
-    for (int i = 0; i < kPnRpg; i++) {
-        const int s = (wave * kPnRpg + i) * 4 + group;
-        const int row = a.rows[static_cast<size_t>(u.x) * R + s];
-        if (row < 0) continue;
-        float* dst = u.w < 0 ? a.C + static_cast<size_t>(row) * a.N + col0
-                             : a.partials + static_cast<size_t>(u.w + s * nu) * a.N + col0;
-        panel_store<T, E>(dst, g, acc[i]);
-    }
+            for (int w = 0; w < (kPnRpg + 3) / 4; w++)
+                mxw[w] = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(cn[kPnMaxDword + w])));
+            pn_static_for<0, kPnRpg>([&](auto ic) {
+                constexpr int i = decltype(ic)::value;
+                const int nmax = static_cast<int>((mxw[i / 4] >> (8 * (i % 4))) & 255);
+                uint32_t qq;
+                float vv;
+                if constexpr (kWin) {
+                    // this tile's run: the new window, or the one taken from the old
+                    wq[i] = nd[i] ? lq[i] : wq[i];
+                    wv[i] = nd[i] ? lv[i] : wv[i];
+                    const bool in = g < nnx[i];
+                    qq = in ? (nd[i] ? lq[i] : rq[i]) : 0u;
+                    vv = in ? (nd[i] ? lv[i] : rv[i]) : 0.f;
+                } else {
+                    qq = lq[i];
+                    vv = lv[i];
+                }
+                if (nmax > 0) pn_run<T, E>(acc[i], qq, vv, nmax, zb, lanepart);
+                cur[i] += static_cast<int>((cn[i] >> shift) & 255);
+                fetch(i, more ? static_cast<int>((cnx[i] >> shift) & 255) : 0);
+            });
+#pragma unroll
+            for (int j = 0; j < kPnCntUsed; j++) cn[j] = cnx[j];
+        }
+        // ---- results: C rows, or this unit's partial rows of a split panel
+        const int nu = u.w >= 0 ? a.panel_units[u.x] : 0;
+        const int col0 = chunk * 16 * E;
+#pragma unroll
+        for (int i = 0; i < kPnRpg; i++) {
+            const int s = (wave * kPnRpg + i) * 4 + group;
+            const int row = a.rows[static_cast<size_t>(u.x) * R + s];
+            if (row < 0) continue;
+            float* dst = u.w < 0 ? a.C + static_cast<size_t>(row) * a.N + col0
+                                 : a.partials + static_cast<size_t>(u.w + s * nu) * a.N + col0;
+            panel_store<T, E>(dst, g, acc[i]);
+        }
+    };
+    if (a.win[u.x]) consume(PnIndex<1>{});
+    else consume(PnIndex<0>{});
 }
 
 }  // namespace tca

@@ -551,16 +551,18 @@ void plan_panels(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_
         }
         p->nnz += c.nnz;
         p->staged += static_cast<int64_t>(c.uni.size());
+        p->win.push_back(panel_window(c.nnz, static_cast<int64_t>(c.uni.size())) ? 1 : 0);
         for (int32_t s = 0; s < R; s++) p->n_rows += c.slots[s] >= 0;
     }
     p->n_segments = seg;
-    p->window = panel_window(p->nnz, p->staged);
     order_units(K, p);
 }
 
 bool panel_window(int64_t nnz, int64_t staged) {
     if (const char* e = std::getenv("TCA_PANEL_WINDOW")) return std::atoi(e) != 0;
-    return static_cast<double>(nnz) < kPanelWindowReuse * static_cast<double>(staged);
+    double reuse = kPanelWindowReuse;
+    if (const char* e = std::getenv("TCA_PANEL_WINDOW_REUSE")) reuse = std::atof(e);  // tuning override
+    return static_cast<double>(nnz) < reuse * static_cast<double>(staged);
 }
 
 void order_units(int32_t K, PanelPlan* p) {

@@ -183,7 +183,7 @@ struct PanelPlan {
     int64_t nnz = 0;           // nonzeros in panels
     int64_t staged = 0;        // union columns summed over panels
     int32_t n_rows = 0;        // rows in panels
-    bool window = false;       // run data through per-entry windows (panel_window)
+    std::vector<uint8_t> win;  // [panel]: 1 = the kernel takes its run data through per-row windows (panel_window)
     int32_t n_tiles() const { return P ? static_cast<int32_t>(cols.size() / P) : 0; }
 };
 constexpr int kPanelWaves = 12;   // consumer wavefronts per workgroup (plus four producers: 1024 threads)
@@ -198,14 +198,19 @@ constexpr int kPanelMaxRun = 16;  // nonzeros of one row in one tile (one 16-lan
 // cost less than the row kernel's gathers; rows that share none stay there.
 constexpr double kPanelMinReuse = 1.02;
 constexpr int64_t kPanelMinNnz = int64_t(1) << 21;  // fewer nonzeros in panels: none (unless forced)
-// Whether the panel kernel takes its run data through windows (a window of
-// 16 nonzeros per row serves several tiles): when the panels' reuse
-// nnz / staged is below kPanelWindowReuse their rows hold few nonzeros per
-// tile, and the kernel waits on memory more than on issue.  Measured on
-// MI355X (panel phase, windows against direct run loads): config 3 (reuse
-// 1.67) 2.34 against 2.82 ms, config 2 (5.74) 1.57 against 1.53 ms.
-// TCA_PANEL_WINDOW=0 / 1 forces it (tests).
-constexpr double kPanelWindowReuse = 3.0;
+// Whether the panel kernel takes a panel's run data through windows (a
+// window of 16 nonzeros per row serves several tiles): when the panel's
+// reuse nnz / |union| is below kPanelWindowReuse its rows hold few nonzeros
+// per tile, and the kernel waits on memory more than on issue.  Measured on
+// MI355X (panel phase; one box, alternating runs): every panel direct /
+// every panel windowed: config 3 (reuse 1.67) 2.82 / 2.34 ms, config 2
+// (5.74) 1.53 / 1.57 ms; per panel, config 2 / config 3 whole SpMM:
+// threshold 3 1.527-1.534 / 2.672-2.679 ms (config 3's nine hub panels
+// direct), 6 1.520-1.544 / 2.620-2.632, every panel windowed 1.575-1.591 /
+// 2.626-2.631, none 1.546-1.555 / -.  TCA_PANEL_WINDOW=0 / 1 forces it for
+// every panel (tests); TCA_PANEL_WINDOW_REUSE overrides the threshold
+// (tuning).
+constexpr double kPanelWindowReuse = 6.0;
 bool panel_window(int64_t nnz, int64_t staged);
 // Launch order of the units (PanelPlan::order).
 void order_units(int32_t K, PanelPlan* p);

@@ -93,6 +93,7 @@ struct tca_spmm_plan {
     int4* d_units = nullptr;
     int32_t* d_porder = nullptr;
     int* d_panel_units = nullptr;
+    uint8_t* d_pwin = nullptr;  // [panel]: run data through per-row windows (PanelPlan::win)
     int* d_prows = nullptr;
     int* d_pcols = nullptr;  // panel tiles' staged B rows, as byte offsets into B
     uint32_t* d_pcnt = nullptr;
@@ -185,6 +186,7 @@ void free_plan_device(tca_spmm_plan* p) {
     (void)hipFree(p->d_units);
     (void)hipFree(p->d_porder);
     (void)hipFree(p->d_panel_units);
+    (void)hipFree(p->d_pwin);
     (void)hipFree(p->d_prows);
     (void)hipFree(p->d_pcols);
     (void)hipFree(p->d_pcnt);
@@ -407,6 +409,7 @@ void launch_panels_t(const tca_spmm_plan* p, const void* val, const void* B, flo
     a.units = p->d_units;
     a.order = p->d_porder;
     a.panel_units = p->d_panel_units;
+    a.win = p->d_pwin;
     a.rows = p->d_prows;
     a.boff = reinterpret_cast<const uint32_t*>(p->d_pcols);
     a.cnt = p->d_pcnt;
@@ -420,10 +423,7 @@ void launch_panels_t(const tca_spmm_plan* p, const void* val, const void* B, flo
     a.chunks = p->panels.chunks;
     a.pos_bytes = static_cast<uint32_t>(p->n_pos_bytes);
     a.val_bytes = static_cast<uint32_t>(static_cast<uint64_t>(p->nnz) * sizeof(T));
-    if (p->panels.window)
-        TCA_PHASE_LAUNCH((panel_kernel<T, E, true>), dim3(p->n_pblocks * p->panels.chunks), dim3(kPnThreads), 0, s, a);
-    else
-        TCA_PHASE_LAUNCH((panel_kernel<T, E, false>), dim3(p->n_pblocks * p->panels.chunks), dim3(kPnThreads), 0, s, a);
+    TCA_PHASE_LAUNCH((panel_kernel<T, E>), dim3(p->n_pblocks * p->panels.chunks), dim3(kPnThreads), 0, s, a);
 }
 
 int launch_panels(const tca_spmm_plan* p, const void* val, const void* B, float* C, float* W, hipStream_t s) {
@@ -522,7 +522,9 @@ void fill_info(tca_spmm_plan* p) {
     in.panel_blockdim = kPnThreads;
     in.panel_lds_bytes =
         p->n_units ? panel_lds_bytes(16 * p->panels.elems * static_cast<int>(dtype_size(p->dtype))) : 0;
-    in.panel_window = p->n_units && p->panels.window ? 1 : 0;
+    in.panel_window = 0;
+    if (p->n_units)
+        for (uint8_t w : p->panels.win) in.panel_window += w;
     if (p->mfma_short) {
         in.n_windows_mfma = p->short_nwin;
         in.rows_mfma = p->M;
@@ -777,6 +779,7 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
             if ((st = dev_upload(&p->d_porder, pp.order.data(), pp.order.size()))) return bail(st);
             p->n_pblocks = static_cast<int32_t>(pp.order.size());
             if ((st = dev_upload(&p->d_panel_units, pp.panel_units.data(), pp.panel_units.size()))) return bail(st);
+            if ((st = dev_upload(&p->d_pwin, pp.win.data(), pp.win.size()))) return bail(st);
             if ((st = dev_upload(&p->d_prows, pp.rows.data(), pp.rows.size()))) return bail(st);
             {
                 // staged rows as byte offsets into B (B < 4 GiB, checked above)
@@ -981,6 +984,7 @@ struct DevPanelPlanner {
     void* tmp = nullptr;
     const int* rows_s = nullptr;  // the panels' row order (phase_b: a copy kept past the second sort)
     std::vector<int> h_take, h_nt, h_nu, h_rows_in;
+    std::vector<uint8_t> h_win;  // [taken panel]: panel_window
     int n_nz = 0, n_take = 0, n_panel_rows = 0, n_plongrows = 0;
     int64_t n_tiles = 0, n_units = 0, n_segments = 0, nnz = 0, staged = 0, unit_nnz = 0;
     int E = 0, P = 0;
@@ -1109,6 +1113,7 @@ struct DevPanelPlanner {
             n_panel_rows += h_rows_in.back();
             nnz += h_pnnz[q];
             staged += h_ucount[q];
+            h_win.push_back(panel_window(h_pnnz[q], h_ucount[q]) ? 1 : 0);
         }
         if (tsum >= (int64_t(1) << 31)) return fail(TCA_ERR_UNSUPPORTED, "panel tile scratch past 2^31 entries");
         if ((st = dev_upload(&take_q, h_take.data(), n_take)) || (st = dev_upload(&ubase, h_ubase.data(), n_take)) ||
@@ -1196,6 +1201,7 @@ struct DevPanelPlanner {
             (st = dev_upload(&p->d_units, nullptr, static_cast<size_t>(n_units))) ||
             (st = dev_upload(&p->d_ustart, nullptr, static_cast<size_t>(n_units) * kDppR)) ||
             (st = dev_upload(&p->d_panel_units, nullptr, n_take)) ||
+            (st = dev_upload(&p->d_pwin, h_win.data(), h_win.size())) ||
             (st = dev_upload(&ulo, nullptr, static_cast<size_t>(n_units))) ||
             (st = dev_upload(&uhi, nullptr, static_cast<size_t>(n_units))))
             return st;
@@ -1224,7 +1230,7 @@ struct DevPanelPlanner {
         pp.n_panels = n_take;
         pp.nnz = nnz;
         pp.staged = staged;
-        pp.window = panel_window(nnz, staged);
+        pp.win = h_win;
         pp.n_rows = n_panel_rows;
         pp.n_segments = n_segments;
         p->n_units = static_cast<int32_t>(n_units);
@@ -1713,7 +1719,7 @@ int tca_spmm_plan_export_tiles(const tca_spmm_plan* p, int32_t* n_windows, int32
 
 int tca_spmm_plan_export_panels(const tca_spmm_plan* p, int64_t* sizes, int32_t* rows, uint32_t* boff, uint32_t* cnt,
                                 uint8_t* pos, int32_t* units, int32_t* order, int32_t* panel_units, int32_t* ustart,
-                                int32_t* longrows) {
+                                int32_t* longrows, uint8_t* window) {
     if (!p || !sizes) return fail(TCA_ERR_INVALID, "tca_spmm_plan_export_panels: bad argument");
     const bool on = p->n_units > 0;
     const int64_t R = on ? p->panels.R : 0, P = on ? p->panels.P : 0;
@@ -1723,7 +1729,8 @@ int tca_spmm_plan_export_panels(const tca_spmm_plan* p, int64_t* sizes, int32_t*
     if (rows) {
         for (int k = 0; k < 5; k++)
             if (sizes[k] < want[k]) return fail(TCA_ERR_INVALID, "tca_spmm_plan_export_panels: output buffers too small");
-        if (sizes[7] < want[7] || !boff || !cnt || !pos || !units || !order || !panel_units || !ustart || !longrows)
+        if (sizes[7] < want[7] || !boff || !cnt || !pos || !units || !order || !panel_units || !ustart || !longrows ||
+            !window)
             return fail(TCA_ERR_INVALID, "tca_spmm_plan_export_panels: output buffers too small");
         auto get = [](void* dst, const void* src, size_t bytes) {
             return bytes == 0 || hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost) == hipSuccess;
@@ -1735,7 +1742,7 @@ int tca_spmm_plan_export_panels(const tca_spmm_plan* p, int64_t* sizes, int32_t*
             !get(order, p->d_porder, sizeof(int32_t) * want[3]) ||
             !get(panel_units, p->d_panel_units, sizeof(int32_t) * want[0]) ||
             !get(ustart, p->d_ustart, sizeof(int32_t) * want[2] * R) ||
-            !get(longrows, p->d_longrows + lr0, sizeof(int4) * want[4]))
+            !get(longrows, p->d_longrows + lr0, sizeof(int4) * want[4]) || !get(window, p->d_pwin, want[0]))
             return fail(TCA_ERR_HIP, "tca_spmm_plan_export_panels: copy failed");
     }
     for (int k = 0; k < 8; k++) sizes[k] = want[k];

@@ -22,7 +22,7 @@ import spmm_amd as S
 
 pytestmark = pytest.mark.gpu
 
-PANEL_KEYS = ("rows", "boff", "cnt", "pos", "units", "order", "panel_units", "ustart", "longrows")
+PANEL_KEYS = ("rows", "boff", "cnt", "pos", "units", "order", "panel_units", "ustart", "longrows", "window")
 
 
 def _exact(a, seed):
