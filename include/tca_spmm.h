@@ -60,8 +60,9 @@ typedef enum tca_status {
                                       fragment cells, at most 255 per step; else plain dense tiles) */
 /* Row panels with B staged in LDS (the panel kernel): by default rows not in
  * MFMA windows are grouped longest first into panels of 192 rows, and those
- * whose nonzeros reuse their column union at least 1.02 times on average run
- * on the panel kernel, other rows on the row kernel.  Needs N % (16 E) == 0 for an
+ * whose nonzeros reuse their column union at least 1.02 times on average
+ * (every panel when B is larger than the 256 MB MALL) run on the panel
+ * kernel, other rows on the row kernel.  Needs N % (16 E) == 0 for an
  * E in {8, 4, 2} with E * element size in 8..32 bytes; by default also B
  * rows of at least 256 bytes and at least 2^21 nonzeros in panels. */
 #define TCA_PLAN_NO_PANELS 256u    /* no panels: rows outside MFMA windows go to the row kernel */

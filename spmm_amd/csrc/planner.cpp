@@ -289,13 +289,19 @@ bool panel_default_ok(int32_t N, int32_t es) {
 
 int32_t panel_tile_cols(int32_t chunk_bytes) { return std::min<int32_t>(255, 77824 / chunk_bytes); }
 
-bool panel_route(int32_t N, int32_t dtype, uint32_t flags, PanelRoute* r) {
+bool panel_route(int32_t K, int32_t N, int32_t dtype, uint32_t flags, PanelRoute* r) {
     *r = PanelRoute{};
     if ((flags & TCA_PLAN_NO_PANELS) ||
         (!(flags & TCA_PLAN_FORCE_PANELS) && !panel_default_ok(N, static_cast<int32_t>(dtype_size(dtype)))))
         return false;
     r->force = (flags & TCA_PLAN_FORCE_PANELS) != 0;
-    r->min_reuse = kPanelMinReuse;
+    // With B past the MALL the row kernel's per-nonzero gathers come from
+    // HBM, and even rows that share no columns cost less staged (measured
+    // on MI355X, config 3, B 1.25 GB: every row with nonzeros in panels
+    // 2.564-2.573 ms against 2.600-2.608 at reuse 1.02, one box; config 2,
+    // B 119 MB: 1.66-1.72 against 1.54-1.57 ms).
+    const bool b_past_mall = static_cast<int64_t>(K) * N * static_cast<int64_t>(dtype_size(dtype)) > kMallBytes;
+    r->min_reuse = b_past_mall ? 0.0 : kPanelMinReuse;
     r->min_nnz = kPanelMinNnz;
     r->unit_nnz = 0;
     // Tuning overrides (not part of the interface).
@@ -319,7 +325,7 @@ int64_t panel_unit_nnz(int64_t unit_nnz, int64_t tot) {
 void plan_panels_routed(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_t K, int32_t N,
                         int32_t dtype, uint32_t flags, const std::vector<uint8_t>& skip, PanelPlan* p) {
     PanelRoute r;
-    if (!panel_route(N, dtype, flags, &r)) {
+    if (!panel_route(K, N, dtype, flags, &r)) {
         *p = PanelPlan{};
         p->row_panel.assign(M, 0);
         return;

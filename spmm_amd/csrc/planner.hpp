@@ -19,6 +19,7 @@
 namespace tca {
 
 constexpr int kXcds = 8;  // XCDs of the MI355X: the hardware deals workgroup b to XCD b % 8
+constexpr int64_t kMallBytes = int64_t(256) << 20;  // MI355X Infinity Cache (MALL), shared by the XCDs
 
 // Task kinds of the row kernel (int4 {x, y, z, w}).  Multi tasks hold at most
 // multi_group_rows(slots) rows, walked `slots` at a time, except zero tasks
@@ -228,7 +229,7 @@ struct PanelRoute {
     double min_reuse = 0.0;
     int64_t min_nnz = 0, unit_nnz = 0;
 };
-bool panel_route(int32_t N, int32_t dtype, uint32_t flags, PanelRoute* r);
+bool panel_route(int32_t K, int32_t N, int32_t dtype, uint32_t flags, PanelRoute* r);
 // Nonzeros per unit for panels holding `tot` nonzeros (unit_nnz > 0: forced).
 int64_t panel_unit_nnz(int64_t unit_nnz, int64_t tot);
 // Launch order of the row kernel's tasks (RowPlan::order): segments of long
@@ -248,7 +249,8 @@ bool panel_default_ok(int32_t N, int32_t es);
 int32_t panel_tile_cols(int32_t chunk_bytes);
 // plan_panels with the routing of a plan: none with TCA_PLAN_NO_PANELS, every
 // eligible row with TCA_PLAN_FORCE_PANELS, else (B rows of >= 256 bytes)
-// panels of reuse >= kPanelMinReuse when they hold at least kPanelMinNnz nonzeros in all.
+// panels of reuse >= kPanelMinReuse (every panel when B is larger than the
+// MALL) when they hold at least kPanelMinNnz nonzeros in all.
 void plan_panels_routed(const int32_t* rowptr, const int32_t* colidx, int32_t M, int32_t K, int32_t N,
                         int32_t dtype, uint32_t flags, const std::vector<uint8_t>& skip, PanelPlan* p);
 // Builds the panel plan over the rows with skip[r] == 0 (skip may be empty).

@@ -1042,7 +1042,7 @@ struct DevPanelPlanner {
         PanelRoute route;
         const int32_t es = static_cast<int32_t>(dtype_size(p->dtype));
         E = panel_elems(p->N, es);
-        if (!panel_route(p->N, p->dtype, p->flags, &route) || E == 0 || p->M == 0 || n_nz_rows == 0) return TCA_OK;
+        if (!panel_route(p->K, p->N, p->dtype, p->flags, &route) || E == 0 || p->M == 0 || n_nz_rows == 0) return TCA_OK;
         // (the union kernel's column chunks end below c0 + 2^19: K leaves room for them in an int)
         if (p->K > INT_MAX - 32 * kDppChunkWords) return fail(TCA_ERR_UNSUPPORTED, "K too large for panels planned on the GPU");
         P = panel_tile_cols(16 * E * es);
