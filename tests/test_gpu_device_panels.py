@@ -59,6 +59,8 @@ def _cases():
     yield "beside-mfma", _mixed_f16(9), 128, S.TCA_PLAN_FORCE_PANELS | S.TCA_PLAN_MFMA_DENSE, {}
     yield "no-panel-rows", S.gen_bernoulli(700, 900, 0.002, seed=10, dtype=S.TCA_F32)[0], 128, \
         S.TCA_PLAN_DEFAULT, {}
+    # B of 512 MB, past the MALL: by default every row with nonzeros in panels
+    yield "past-mall", S.gen_rmat(20, 1 << 20, 1500000, seed=11, dtype=S.TCA_F32)[0], 128, S.TCA_PLAN_DEFAULT, {}
 
 
 CASES = list(_cases())
@@ -99,6 +101,8 @@ def test_device_panels_equal_host_panels(torch_cuda, name, a, n, flags, env):
             assert len(hx["longrows"]) > 0 and hx["n_units"] > hx["panels"], name
         if name == "wide-k":
             assert a.ncol > 2 * (1 << 19)
+        if name == "past-mall":
+            assert hi["rows_panels"] == int((np.diff(a.rowptr) > 0).sum()), hi
         # the other rows: the same row-kernel plan
         ht, hperm, hl = hp.export_rows()
         dt, dperm, dl = dp.export_rows()
