@@ -121,6 +121,9 @@ typedef struct tca_plan_info {
     int32_t panel_blockdim;   /* threads per workgroup of the panel kernel */
     int32_t panel_lds_bytes;  /* LDS per panel workgroup */
     int32_t panel_window;     /* panels whose run data go through per-row windows (low reuse) */
+    int32_t rows_beside_panels; /* 1: the row phase only clears empty rows and runs on a second
+                                   stream of the plan beside the panel kernel (forked and joined
+                                   by events on the run's stream; TCA_ROWS_BESIDE=0 turns it off) */
 } tca_plan_info;
 
 /* tca_plan_info.tile_kernel */
@@ -146,7 +149,12 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
  * d_B[K*N] (plan dtype) and d_C[M*N] (fp32) are DEVICE pointers; d_B and d_C
  * must be aligned to 16 bytes.  Stream-ordered on `stream` (a hipStream_t,
  * NULL = default stream); does not synchronise.  One plan must not run on two
- * streams at once: long-row partial sums live in plan-owned scratch. */
+ * streams at once: long-row partial sums live in plan-owned scratch.  A plan
+ * whose row phase only clears empty rows (tca_plan_info.rows_beside_panels)
+ * runs it on a second stream it owns, beside the panel kernel: that stream
+ * waits for the work queued on `stream` before the call, and `stream` waits
+ * for it before the call's last kernel, so the run stays ordered on `stream`
+ * (under graph capture the two become a fork and a join of the graph). */
 int tca_spmm_run(const tca_spmm_plan* plan, const void* d_val, const void* d_B, float* d_C,
                  void* stream);
 

@@ -63,7 +63,7 @@ class TcaPlanInfo(ctypes.Structure):
                 ("n_wide_tasks", i32), ("chunk_lanes", i32), ("row_len", i32), ("wide_len", i32),
                 ("tile_kernel", i32), ("n_panels", i32), ("n_panel_units", i32), ("rows_panels", i32),
                 ("panel_blocks", i32), ("nnz_panels", i64), ("staged_panels", i64), ("panel_blockdim", i32),
-                ("panel_lds_bytes", i32), ("panel_window", i32)]
+                ("panel_lds_bytes", i32), ("panel_window", i32), ("rows_beside_panels", i32)]
 
     def as_dict(self):
         return {name: getattr(self, name) for name, _ in self._fields_}

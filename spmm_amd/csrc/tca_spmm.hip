@@ -102,6 +102,12 @@ struct tca_spmm_plan {
     size_t n_pos_bytes = 0;  // d_ppos, whole dwords
     int64_t n_ptiles = 0;    // panel tiles (d_pcols: n_ptiles * P entries)
     int32_t n_plongrows = 0; // the panels' long rows: the last entries of d_longrows
+    // A row phase that only clears empty rows (every nonzero is in panels or
+    // tiles) runs on this second stream of the plan, beside the panel kernel:
+    // forked after the phases before the panels, joined before the segment
+    // sums (null: the phases run in order on the caller's stream).
+    hipStream_t side = nullptr;
+    hipEvent_t fork = nullptr, join = nullptr;
     tca_plan_info info{};
 };
 
@@ -192,6 +198,9 @@ void free_plan_device(tca_spmm_plan* p) {
     (void)hipFree(p->d_pcnt);
     (void)hipFree(p->d_ppos);
     (void)hipFree(p->d_ustart);
+    if (p->fork) (void)hipEventDestroy(p->fork);
+    if (p->join) (void)hipEventDestroy(p->join);
+    if (p->side) (void)hipStreamDestroy(p->side);
 }
 
 // Owns a plan under construction: frees it (device buffers included) unless
@@ -469,11 +478,43 @@ int run_phases(const tca_spmm_plan* p, const void* val, const void* B, float* C,
     int st = TCA_OK;
     if (mask & (1u << TCA_PHASE_TILES)) st = launch_mfma(p, val, B, C, s);
     if (st) return st;
+    const uint32_t both = (1u << TCA_PHASE_PANELS) | (1u << TCA_PHASE_ROWS);
+    const bool beside = p->side && (mask & both) == both;
+    if (beside && (hipEventRecord(p->fork, s) != hipSuccess || hipStreamWaitEvent(p->side, p->fork, 0) != hipSuccess))
+        return fail(TCA_ERR_HIP, "fork to the plan's second stream failed");
     if (mask & (1u << TCA_PHASE_PANELS)) st = launch_panels(p, val, B, C, W, s);
     if (st) return st;
-    if (mask & (1u << TCA_PHASE_ROWS)) st = launch_rows(p, val, B, C, W, s);
+    if (mask & (1u << TCA_PHASE_ROWS)) st = launch_rows(p, val, B, C, W, beside ? p->side : s);
     if (st) return st;
+    if (beside && (hipEventRecord(p->join, p->side) != hipSuccess || hipStreamWaitEvent(s, p->join, 0) != hipSuccess))
+        return fail(TCA_ERR_HIP, "join of the plan's second stream failed");
     if (mask & (1u << TCA_PHASE_SEGMENTS)) launch_finalize(p, C, W, s);
+    return TCA_OK;
+}
+
+// The second stream of a plan whose row phase only clears empty rows: those
+// stores then run beside the panel kernel instead of after it (an R-MAT graph
+// with every row in panels: 2.606-2.611 -> 2.552-2.556 ms per step; with
+// gathering row tasks beside the panels the step was slower).
+// TCA_ROWS_BESIDE=0 keeps every phase on the caller's stream (tuning override).
+int setup_side_stream(tca_spmm_plan* p) {
+    if (p->n_units == 0 || p->ntasks == 0) return TCA_OK;
+    if (static_cast<int64_t>(p->nnz) - p->panels.nnz - p->mfma.nnz != 0) return TCA_OK;
+    if (const char* e = std::getenv("TCA_ROWS_BESIDE"))
+        if (std::atoi(e) == 0) return TCA_OK;
+    if (hipStreamCreateWithFlags(&p->side, hipStreamNonBlocking) != hipSuccess) {
+        p->side = nullptr;
+        return fail(TCA_ERR_HIP, "hipStreamCreateWithFlags failed");
+    }
+    if (hipEventCreateWithFlags(&p->fork, hipEventDisableTiming) != hipSuccess) {
+        p->fork = nullptr;
+        return fail(TCA_ERR_HIP, "hipEventCreateWithFlags failed");
+    }
+    if (hipEventCreateWithFlags(&p->join, hipEventDisableTiming) != hipSuccess) {
+        p->join = nullptr;
+        return fail(TCA_ERR_HIP, "hipEventCreateWithFlags failed");
+    }
+    p->info.rows_beside_panels = 1;
     return TCA_OK;
 }
 
@@ -959,6 +1000,7 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
         if (hipDeviceSynchronize() != hipSuccess) return bail(fail(TCA_ERR_HIP, "hipDeviceSynchronize failed"));
 
         fill_info(p);
+        if ((st = setup_side_stream(p))) return st;
         p->info.plan_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
         *plan = hold.release();
         return TCA_OK;
@@ -1660,6 +1702,7 @@ int tca_spmm_plan_create_device(const int32_t* d_rowptr, const int32_t* d_colidx
             return bail(fail(TCA_ERR_HIP, "task emission failed"));
         st = bail(TCA_OK);  // frees the temporaries only
         fill_info(p);
+        if ((st = setup_side_stream(p))) return st;  // on failure `hold` frees the plan
         p->info.plan_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
         *plan = hold.release();
         return TCA_OK;

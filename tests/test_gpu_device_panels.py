@@ -91,7 +91,7 @@ def test_device_panels_equal_host_panels(torch_cuda, name, a, n, flags, env):
             assert np.array_equal(hx[k], dx[k]), (name, k)
         hi, di = hp.info(), dp.info()
         for key in ("n_panels", "n_panel_units", "rows_panels", "nnz_panels", "staged_panels", "panel_blocks",
-                    "panel_window", "n_row_tasks", "n_multi_tasks", "n_seg_tasks", "n_long_rows", "scratch_bytes", "row_blocks"):
+                    "panel_window", "rows_beside_panels", "n_row_tasks", "n_multi_tasks", "n_seg_tasks", "n_long_rows", "scratch_bytes", "row_blocks"):
             assert hi[key] == di[key], (name, key, hi[key], di[key])
         if name == "no-panel-rows":
             assert hx["panels"] == 0
@@ -103,6 +103,7 @@ def test_device_panels_equal_host_panels(torch_cuda, name, a, n, flags, env):
             assert a.ncol > 2 * (1 << 19)
         if name == "past-mall":
             assert hi["rows_panels"] == int((np.diff(a.rowptr) > 0).sum()), hi
+            assert hi["rows_beside_panels"] == int(hi["n_row_tasks"] > 0), hi
         # the other rows: the same row-kernel plan
         ht, hperm, hl = hp.export_rows()
         dt, dperm, dl = dp.export_rows()

@@ -148,3 +148,43 @@ def test_panels_nonfinite_b_stays_in_its_rows(torch_cuda):
     want = oracle_c(a, b)
     fin = np.isfinite(want)
     assert np.array_equal(got[fin], want[fin])
+
+
+def test_rows_beside_panels_follow_the_run_stream(torch_cuda, monkeypatch):
+    """A row phase that only clears empty rows (every row with nonzeros in panels)
+    runs on the plan's second stream beside the panel kernel.  Its clears start
+    after the work queued before the run on the run's stream (a NaN fill behind a
+    sleep: clearing early would leave NaN rows), the segment sums and the work
+    queued after the run wait for them, and the product equals the oracle and the
+    one-stream run (TCA_ROWS_BESIDE=0) bit for bit."""
+    torch = torch_cuda
+    monkeypatch.setenv("TCA_PANEL_MIN_REUSE", "0")
+    monkeypatch.setenv("TCA_PANEL_MIN_NNZ", "0")
+    base, _ = S.gen_rmat(16, 65536, 100000, norm=1, seed=21)
+    a = exact(base, S.TCA_F32, seed=22)
+    n = 128
+    nonempty = int((np.diff(a.rowptr) > 0).sum())
+    b = S.to_storage(exact_dense(np.random.default_rng(23), (a.ncol, n)), S.TCA_F32)
+    want = oracle_c(a, b)
+    val, bd = _dev(torch, a.values), _dev(torch, b)
+    outs = {}
+    for beside in ("1", "0"):
+        monkeypatch.setenv("TCA_ROWS_BESIDE", beside)
+        with S.Plan(a, n) as pl:
+            info = pl.info()
+            print(f"rows beside panels={beside}: {info['rows_panels']} panel rows of {a.nrow}, "
+                  f"{info['n_row_tasks']} row tasks, {info['n_long_rows']} long rows", flush=True)
+            assert info["rows_panels"] == nonempty and info["n_row_tasks"] > 0 and info["n_long_rows"] > 0
+            assert info["rows_beside_panels"] == int(beside)
+            s = torch.cuda.Stream()
+            c = torch.zeros((a.nrow, n), dtype=torch.float32, device="cuda:0")
+            torch.cuda.synchronize()
+            with torch.cuda.stream(s):
+                torch.cuda._sleep(50_000_000)
+                c.fill_(float("nan"))
+                pl.run(val, bd, c, stream=s.cuda_stream)
+                copy = c.clone()
+            s.synchronize()
+            outs[beside] = copy.cpu().numpy()
+        assert np.array_equal(outs[beside], want), (beside, int(np.isnan(outs[beside]).any(axis=1).sum()))
+    assert np.array_equal(outs["1"], outs["0"])
