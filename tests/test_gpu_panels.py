@@ -188,3 +188,43 @@ def test_rows_beside_panels_follow_the_run_stream(torch_cuda, monkeypatch):
             outs[beside] = copy.cpu().numpy()
         assert np.array_equal(outs[beside], want), (beside, int(np.isnan(outs[beside]).any(axis=1).sum()))
     assert np.array_equal(outs["1"], outs["0"])
+
+
+def test_rows_beside_panels_under_graph_capture(torch_cuda, monkeypatch):
+    """The second stream's fork and join are captured into a HIP graph with the
+    run (torch.cuda.graph on the plan's allocation-free run): every replay,
+    with eager work and synchronisations between replays, gives the eager
+    product bit for bit."""
+    torch = torch_cuda
+    monkeypatch.setenv("TCA_PANEL_MIN_REUSE", "0")
+    monkeypatch.setenv("TCA_PANEL_MIN_NNZ", "0")
+    base, _ = S.gen_rmat(15, 32768, 60000, norm=1, seed=31)
+    a = exact(base, S.TCA_F32, seed=32)
+    n = 64
+    b = S.to_storage(exact_dense(np.random.default_rng(33), (a.ncol, n)), S.TCA_F32)
+    want = oracle_c(a, b)
+    val, bd = _dev(torch, a.values), _dev(torch, b)
+    with S.Plan(a, n, S.TCA_PLAN_NO_SCRATCH) as pl:
+        info = pl.info()
+        print(f"graph capture: {info['rows_panels']} panel rows of {a.nrow}, {info['n_row_tasks']} row tasks, "
+              f"rows beside panels {info['rows_beside_panels']}", flush=True)
+        assert info["rows_beside_panels"] == 1
+        c = torch.zeros((a.nrow, n), dtype=torch.float32, device="cuda:0")
+        pl.run_static(val, bd, c)
+        torch.cuda.synchronize()
+        assert np.array_equal(c.cpu().numpy(), want)
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            with torch.cuda.graph(g, stream=s):
+                pl.run_static(val, bd, c, stream=s.cuda_stream)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        for rep in range(3):
+            c.fill_(float("nan"))
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            assert np.array_equal(c.cpu().numpy(), want), rep
+        del g
