@@ -85,7 +85,10 @@ typedef enum tca_status {
 typedef struct tca_spmm_plan tca_spmm_plan;
 
 /* Plan statistics, for the harness's "num_block / blockdim / shm" line
- * (reference src/our_spmm.cu:552) and for the measurement scripts. */
+ * (reference src/our_spmm.cu:552) and for the measurement scripts.  New
+ * fields are only ever appended, so the struct grows: compile callers against
+ * the header of the library they load (tca_spmm_plan_info writes the whole
+ * struct). */
 typedef struct tca_plan_info {
     int32_t M, K, N, nnz, dtype;
     int32_t elems_per_lane;   /* B columns per lane per load (16-byte vectors when possible) */
