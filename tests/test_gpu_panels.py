@@ -186,6 +186,14 @@ def test_rows_beside_panels_follow_the_run_stream(torch_cuda, monkeypatch):
                 copy = c.clone()
             s.synchronize()
             outs[beside] = copy.cpu().numpy()
+            # the timing entry points on the same plan: phase subsets with and
+            # without the fork, the per-phase spans (one stream), whole runs
+            for phases in (("rows",), ("panels", "rows", "segments"), pl.phases()):
+                assert pl.time_subset(val, bd, c, phases, warmup=1, iters=2) > 0.0, phases
+            pl.time_phases(val, bd, c, warmup=1, iters=2)
+            assert pl.time(val, bd, c, warmup=1, iters=2) > 0.0
+            torch.cuda.synchronize()
+            assert np.array_equal(c.cpu().numpy(), want), beside
         assert np.array_equal(outs[beside], want), (beside, int(np.isnan(outs[beside]).any(axis=1).sum()))
     assert np.array_equal(outs["1"], outs["0"])
 
