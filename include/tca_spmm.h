@@ -126,7 +126,8 @@ typedef struct tca_plan_info {
     int32_t panel_window;     /* panels whose run data go through per-row windows (low reuse) */
     int32_t rows_beside_panels; /* 1: the row phase only clears empty rows and runs on a second
                                    stream of the plan beside the panel kernel (forked and joined
-                                   by events on the run's stream; TCA_ROWS_BESIDE=0 turns it off) */
+                                   by events on the run's stream; TCA_ROWS_BESIDE=0 turns it off;
+                                   0 also when the runtime could not create that stream) */
 } tca_plan_info;
 
 /* tca_plan_info.tile_kernel */

@@ -497,25 +497,25 @@ int run_phases(const tca_spmm_plan* p, const void* val, const void* B, float* C,
 // with every row in panels: 2.606-2.611 -> 2.552-2.556 ms per step; with
 // gathering row tasks beside the panels the step was slower).
 // TCA_ROWS_BESIDE=0 keeps every phase on the caller's stream (tuning override).
-int setup_side_stream(tca_spmm_plan* p) {
-    if (p->n_units == 0 || p->ntasks == 0) return TCA_OK;
-    if (static_cast<int64_t>(p->nnz) - p->panels.nnz - p->mfma.nnz != 0) return TCA_OK;
+// The stream and its events are an optimisation: when the runtime cannot
+// create them the plan keeps one stream (rows_beside_panels = 0), no error.
+void setup_side_stream(tca_spmm_plan* p) {
+    if (p->n_units == 0 || p->ntasks == 0) return;
+    if (static_cast<int64_t>(p->nnz) - p->panels.nnz - p->mfma.nnz != 0) return;
     if (const char* e = std::getenv("TCA_ROWS_BESIDE"))
-        if (std::atoi(e) == 0) return TCA_OK;
-    if (hipStreamCreateWithFlags(&p->side, hipStreamNonBlocking) != hipSuccess) {
+        if (std::atoi(e) == 0) return;
+    if (hipStreamCreateWithFlags(&p->side, hipStreamNonBlocking) != hipSuccess) p->side = nullptr;
+    if (p->side && hipEventCreateWithFlags(&p->fork, hipEventDisableTiming) != hipSuccess) p->fork = nullptr;
+    if (p->fork && hipEventCreateWithFlags(&p->join, hipEventDisableTiming) != hipSuccess) p->join = nullptr;
+    if (!p->join) {
+        if (p->fork) (void)hipEventDestroy(p->fork);
+        if (p->side) (void)hipStreamDestroy(p->side);
         p->side = nullptr;
-        return fail(TCA_ERR_HIP, "hipStreamCreateWithFlags failed");
-    }
-    if (hipEventCreateWithFlags(&p->fork, hipEventDisableTiming) != hipSuccess) {
         p->fork = nullptr;
-        return fail(TCA_ERR_HIP, "hipEventCreateWithFlags failed");
-    }
-    if (hipEventCreateWithFlags(&p->join, hipEventDisableTiming) != hipSuccess) {
-        p->join = nullptr;
-        return fail(TCA_ERR_HIP, "hipEventCreateWithFlags failed");
+        (void)hipGetLastError();  // the failed creation is not the next call's error
+        return;
     }
     p->info.rows_beside_panels = 1;
-    return TCA_OK;
 }
 
 // Plan statistics (tca_plan_info) from a built plan.
@@ -1000,7 +1000,7 @@ int tca_spmm_plan_create(const int32_t* rowptr, const int32_t* colidx, int32_t M
         if (hipDeviceSynchronize() != hipSuccess) return bail(fail(TCA_ERR_HIP, "hipDeviceSynchronize failed"));
 
         fill_info(p);
-        if ((st = setup_side_stream(p))) return st;
+        setup_side_stream(p);
         p->info.plan_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
         *plan = hold.release();
         return TCA_OK;
@@ -1702,7 +1702,7 @@ int tca_spmm_plan_create_device(const int32_t* d_rowptr, const int32_t* d_colidx
             return bail(fail(TCA_ERR_HIP, "task emission failed"));
         st = bail(TCA_OK);  // frees the temporaries only
         fill_info(p);
-        if ((st = setup_side_stream(p))) return st;  // on failure `hold` frees the plan
+        setup_side_stream(p);
         p->info.plan_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
         *plan = hold.release();
         return TCA_OK;
